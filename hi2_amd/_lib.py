@@ -1,0 +1,145 @@
+"""ctypes binding of ``libhi2x.so`` (the C ABI declared in ``include/hi2x.h``).
+
+The library is the only compute path of this package: if it is missing or fails to
+load, every entry point raises ``RuntimeError`` naming the problem — there is no CPU
+or torch fallback.  Tensors are passed as raw device pointers with the caller's
+current HIP stream, and the library never keeps them beyond the call.
+"""
+
+import ctypes
+import os
+import threading
+
+import torch
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libhi2x.so")
+
+OK, EINVAL, ENOTPD, ELAUNCH, ERANGE = 0, -1, -2, -3, -4
+
+_lock = threading.Lock()
+_lib = None
+_failed: str | None = None
+
+_P = ctypes.c_void_p
+_I64 = ctypes.c_int64
+_I = ctypes.c_int
+_F = ctypes.c_float
+
+# name -> argtypes (all return int status except the two identity calls)
+SIGNATURES = {
+    "hi2x_gptq_block": [_P, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _I64, _P, _P, _P, _P, _P, _P],
+    "hi2x_gptq_trailing": [_P, _I64, _I64, _I64, _I64, _P, _I64, _I64, _I64, _P, _P, _P],
+    "hi2x_gptq_run": [_P, _I64, _I64, _P, _P, _P, _I64, _P, _P, _P, _P, _P, _P, _I64, _P],
+    "hi2x_ladder_fit": [_P, _P, _I64, _I64, _I64, _I, _P, _I, _I, _P, _P, _P, _P],
+    "hi2x_params": [_P, _P, _I64, _I64, _P, _P, _P, _P, _P, _I64, _P],
+    "hi2x_decode_params": [_P, _P, _P, _I64, _I64, _P, _P, _P],
+    "hi2x_finish": [_P, _P, _P, _I64, _I64, _I64, _P, _P, _I64, _P, _P, _P, _P, _P, _P],
+    "hi2x_ladder_dequantize": [_P, _P, _P, _I64, _I64, _I64, _I, _P, _P],
+    "hi2x_fwht16": [_P, _P, _I, _I64, _I64, _P, _P],
+    "hi2x_pack_codes": [_P, _I64, _I64, _I, _P, _P, _P],
+    "hi2x_assemble_piece": [_P, _I64, _P, _P, _P, _I64, _I, _I64, _P, _P, _P, _P, _P, _P, _P],
+    "hi2x_hessian_syrk": [_P, _I, _I64, _I64, _P, _P],
+    "hi2x_hessian_syrk_varlen": [_P, _I, _P, _I64, _I64, _P, _P],
+    "hi2x_sigma_transform": [_P, _P, _P, _I64, _P, _P],
+    "hi2x_chol_inv_upper": [_P, _I64, _F, _I, _P, _P],
+}
+
+
+def _bind(lib):
+    lib.hi2x_version.restype = ctypes.c_int
+    lib.hi2x_version.argtypes = []
+    lib.hi2x_last_error.restype = ctypes.c_char_p
+    lib.hi2x_last_error.argtypes = []
+    for name, args in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = ctypes.c_int
+        fn.argtypes = args
+    return lib
+
+
+def load():
+    """The loaded library, or None with :func:`failure` set (thread-safe, idempotent)."""
+    global _lib, _failed
+    if _lib is not None or _failed is not None:
+        return _lib
+    with _lock:
+        if _lib is not None or _failed is not None:
+            return _lib
+        try:
+            if not os.path.exists(LIB_PATH):
+                raise FileNotFoundError(
+                    f"{LIB_PATH} is not built (run `python -m hi2_amd.build`)"
+                )
+            _lib = _bind(ctypes.CDLL(LIB_PATH))
+        except (OSError, AttributeError) as e:
+            _failed = f"{type(e).__name__}: {e}"
+        return _lib
+
+
+def failure() -> str | None:
+    return _failed
+
+
+def lib():
+    """The library; raises RuntimeError if it cannot be loaded (no fallback exists)."""
+    handle = load()
+    if handle is None:
+        raise RuntimeError(f"hi2x HIP library unavailable: {_failed}")
+    return handle
+
+
+def last_error() -> str:
+    return lib().hi2x_last_error().decode(errors="replace")
+
+
+class NotPositiveDefinite(RuntimeError):
+    pass
+
+
+def check(rc: int, what: str) -> None:
+    """Map a status to the reference's exception types."""
+    if rc == OK:
+        return
+    msg = f"{what}: {last_error()}"
+    if rc == ERANGE:
+        raise ValueError(msg)
+    if rc == ENOTPD:
+        raise NotPositiveDefinite(msg)
+    raise RuntimeError(msg)
+
+
+def require_gpu(*tensors: torch.Tensor) -> torch.device:
+    """All tensors on one HIP device; returns it."""
+    dev = None
+    for t in tensors:
+        if t is None:
+            continue
+        if t.device.type != "cuda":
+            raise RuntimeError(
+                f"hi2_amd runs on the MI355X only: got a tensor on {t.device} "
+                "(move inputs to a 'cuda' device)"
+            )
+        if dev is None:
+            dev = t.device
+        elif t.device != dev:
+            raise RuntimeError(f"tensors on different devices: {dev} and {t.device}")
+    if dev is None:
+        raise RuntimeError("no device tensor given")
+    return dev
+
+
+def ptr(t: torch.Tensor | None):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def stream(dev: torch.device):
+    return ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+
+
+def call(name: str, dev: torch.device, *args) -> None:
+    """Call ``name`` with ``args`` + the current stream of ``dev`` (device made current)."""
+    fn = getattr(lib(), name)
+    with torch.cuda.device(dev):
+        rc = fn(*args, stream(dev))
+    check(rc, name)

@@ -1,0 +1,91 @@
+// Shared helpers of the hi2x HIP library (gfx950 only).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/hi2x.h"
+
+namespace hi2x {
+
+// Thread-local last-error text (hi2x_last_error).
+void set_error(const char* fmt, ...);
+void clear_error();
+
+// Status of the last launch on this thread: HI2X_OK or HI2X_ELAUNCH (message set).
+int launch_status(const char* what);
+
+inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+}  // namespace hi2x
+
+#define HI2X_REQUIRE(cond, ...)          \
+  do {                                   \
+    if (!(cond)) {                       \
+      hi2x::set_error(__VA_ARGS__);      \
+      return HI2X_EINVAL;                \
+    }                                    \
+  } while (0)
+
+#define HI2X_HIP(call)                                                        \
+  do {                                                                        \
+    hipError_t e_ = (call);                                                   \
+    if (e_ != hipSuccess) {                                                   \
+      hi2x::set_error("%s: %s", #call, hipGetErrorString(e_));                \
+      return HI2X_ELAUNCH;                                                    \
+    }                                                                         \
+  } while (0)
+
+// ---- device helpers ------------------------------------------------------------------
+
+// fp32 -> fp16 -> fp32 with round-to-nearest-even (torch's .to(float16).float()).
+__device__ __forceinline__ float f16_round(float x) { return (float)(_Float16)x; }
+
+__device__ __forceinline__ uint16_t f16_bits(float x) {
+  _Float16 h = (_Float16)x;
+  return __builtin_bit_cast(uint16_t, h);
+}
+
+__device__ __forceinline__ float f16_from_bits(uint16_t b) {
+  return (float)__builtin_bit_cast(_Float16, b);
+}
+
+// torch.clamp(q, 0, n - 1): NaN propagates through both compares.
+__device__ __forceinline__ float clamp_code(float q, float nm) {
+  q = (q < 0.0f) ? 0.0f : q;
+  q = (q > nm) ? nm : q;
+  return q;
+}
+
+// Sum of x[0..B) in torch's CPU order for a contiguous inner reduction of B <= 64
+// floats (8 vector lanes, 4 vector accumulators; the cascade needs >= 16 rows of 4
+// vectors, i.e. B >= 512, so it never triggers here).  fn(t) yields x[t].
+template <int B, class F>
+__device__ __forceinline__ float torch_sum_small(F fn) {
+  static_assert(B % 8 == 0 && B <= 64, "block size");
+  constexpr int VS = B / 8;   // vectors
+  constexpr int SI = VS / 4;  // rows of 4 vectors
+  float p[4][8];
+#pragma unroll
+  for (int k = 0; k < 4; ++k)
+#pragma unroll
+    for (int v = 0; v < 8; ++v) p[k][v] = 0.0f;
+#pragma unroll
+  for (int i = 0; i < SI; ++i)
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+#pragma unroll
+      for (int v = 0; v < 8; ++v) p[k][v] += fn((i * 4 + k) * 8 + v);
+#pragma unroll
+  for (int i = SI * 4; i < VS; ++i)
+#pragma unroll
+    for (int v = 0; v < 8; ++v) p[0][v] += fn(i * 8 + v);
+#pragma unroll
+  for (int k = 1; k < 4; ++k)
+#pragma unroll
+    for (int v = 0; v < 8; ++v) p[0][v] += p[k][v];
+  float out = 0.0f;
+#pragma unroll
+  for (int v = 0; v < 8; ++v) out += p[0][v];
+  return out;
+}
+

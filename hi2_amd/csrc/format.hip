@@ -1,0 +1,165 @@
+// Order-16 Hadamard rotation and rdna_hint_flex packing (HBM-bound kernels).
+//
+// Reference: hi2/format.py:22-41 (hadamard16, fwht_groups), hi2/format.py:73-85
+// (pack_codes) and hi2/format.py:155-171 (the scatters of assemble).
+#include "common.h"
+
+namespace hi2x {
+namespace {
+
+// Sylvester sign of H16[i][j]: (-1)^popcount(i & j); the entries are +-1/4.
+__device__ __forceinline__ bool hneg(int i, int j) { return __builtin_popcount(i & j) & 1; }
+
+// One thread per 16-column group of a row.  y_j = sum_i x_i * H[i][j] as the
+// reference's matmul evaluates it: a sequential FMA chain over i from zero (the
+// products by +-1/4 are exact).  Unflagged groups are copied.
+template <typename T>
+__global__ __launch_bounds__(256) void fwht16_kernel(const T* __restrict__ x, T* __restrict__ y,
+                                                     int64_t rows, int64_t k,
+                                                     const uint8_t* __restrict__ flags) {
+  const int64_t ng = k / 16;
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= rows * ng) return;
+  const int64_t g = i % ng;
+  const T* xi = x + i * 16;
+  T* yo = y + i * 16;
+  T v[16];
+#pragma unroll
+  for (int t = 0; t < 16; ++t) v[t] = xi[t];
+  if (!flags[g]) {
+#pragma unroll
+    for (int t = 0; t < 16; ++t) yo[t] = v[t];
+    return;
+  }
+  const T q = (T)0.25;
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {
+    T acc = (T)0;
+#pragma unroll
+    for (int t = 0; t < 16; ++t) acc = __builtin_fma(v[t], hneg(t, j) ? -q : q, acc);
+    yo[j] = acc;
+  }
+}
+
+__device__ __forceinline__ void note_bad(int32_t* bad, int n) {
+  if (n && bad) atomicAdd(bad, n);
+}
+
+// One thread per output word: 32/nbits codes, LSB first.
+__global__ __launch_bounds__(256) void pack_kernel(const uint8_t* __restrict__ codes,
+                                                   int64_t rows, int64_t k, int nbits,
+                                                   int32_t* __restrict__ words,
+                                                   int32_t* __restrict__ bad) {
+  const int per = 32 / nbits;
+  const int64_t nw = k / per;
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= rows * nw) return;
+  const uint8_t* c = codes + i * per;
+  const uint32_t lim = 1u << nbits;
+  uint32_t v = 0;
+  int nbad = 0;
+  for (int t = 0; t < per; ++t) {
+    const uint32_t cv = c[t];
+    nbad += cv >= lim;
+    v |= (cv & (lim - 1u)) << (nbits * t);
+  }
+  words[i] = (int32_t)v;
+  note_bad(bad, nbad);
+}
+
+// assemble, one piece: thread (i, wi) packs word wi of piece row i into the flat
+// buffer at code_off[rows[i]] + wi; threads (i, b) with b < nblk copy the two bytes
+// of block b to param_off[rows[i]] + b; thread (i, 0) copies the row constants.
+__global__ __launch_bounds__(256) void assemble_kernel(
+    const int64_t* __restrict__ rows, int64_t r, const uint8_t* __restrict__ codes,
+    const uint8_t* __restrict__ params, const uint16_t* __restrict__ consts, int64_t k,
+    int nbits, int64_t nblk, const int64_t* __restrict__ code_off,
+    const int64_t* __restrict__ param_off, int32_t* __restrict__ out_codes,
+    uint8_t* __restrict__ out_params, uint16_t* __restrict__ out_consts,
+    int32_t* __restrict__ bad) {
+  const int per = 32 / nbits;
+  const int64_t nw = k / per;
+  const int64_t span = nw > nblk ? nw : nblk;
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= r * span) return;
+  const int64_t i = t / span, j = t % span;
+  const int64_t row = rows[i];
+  if (j < nw) {
+    const uint8_t* c = codes + i * k + j * per;
+    const uint32_t lim = 1u << nbits;
+    uint32_t v = 0;
+    int nbad = 0;
+    for (int q = 0; q < per; ++q) {
+      const uint32_t cv = c[q];
+      nbad += cv >= lim;
+      v |= (cv & (lim - 1u)) << (nbits * q);
+    }
+    out_codes[code_off[row] + j] = (int32_t)v;
+    note_bad(bad, nbad);
+  }
+  if (j < nblk) {
+    const int64_t dst = (param_off[row] + j) * 2;
+    out_params[dst] = params[(i * nblk + j) * 2];
+    out_params[dst + 1] = params[(i * nblk + j) * 2 + 1];
+  }
+  if (j == 0) {
+    out_consts[row * 3 + 0] = consts[i * 3 + 0];
+    out_consts[row * 3 + 1] = consts[i * 3 + 1];
+    out_consts[row * 3 + 2] = consts[i * 3 + 2];
+  }
+}
+
+}  // namespace
+}  // namespace hi2x
+
+using namespace hi2x;
+
+extern "C" int hi2x_fwht16(const void* x, void* y, int dtype, int64_t rows, int64_t k,
+                           const uint8_t* flags, void* stream) {
+  clear_error();
+  HI2X_REQUIRE(k > 0 && k % 16 == 0, "fwht16: K=%lld must be a multiple of 16", (long long)k);
+  HI2X_REQUIRE(dtype == 0 || dtype == 1, "fwht16: dtype %d (0 = f32, 1 = f64)", dtype);
+  if (rows == 0) return HI2X_OK;
+  const int64_t total = rows * (k / 16);
+  const dim3 grid((unsigned)((total + 255) / 256));
+  hipStream_t s = as_stream(stream);
+  if (dtype == 0)
+    hipLaunchKernelGGL(fwht16_kernel<float>, grid, dim3(256), 0, s, (const float*)x, (float*)y,
+                       rows, k, flags);
+  else
+    hipLaunchKernelGGL(fwht16_kernel<double>, grid, dim3(256), 0, s, (const double*)x,
+                       (double*)y, rows, k, flags);
+  return launch_status("fwht16_kernel");
+}
+
+extern "C" int hi2x_pack_codes(const uint8_t* codes, int64_t rows, int64_t k, int nbits,
+                               int32_t* words, int32_t* bad, void* stream) {
+  clear_error();
+  HI2X_REQUIRE(nbits == 2 || nbits == 4 || nbits == 8, "pack_codes: nbits=%d", nbits);
+  HI2X_REQUIRE(k > 0 && k % (32 / nbits) == 0, "pack_codes: %lld codes is not a multiple of %d",
+               (long long)k, 32 / nbits);
+  if (rows == 0) return HI2X_OK;
+  const int64_t total = rows * (k / (32 / nbits));
+  hipLaunchKernelGGL(pack_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0,
+                     as_stream(stream), codes, rows, k, nbits, words, bad);
+  return launch_status("pack_kernel");
+}
+
+extern "C" int hi2x_assemble_piece(const int64_t* rows, int64_t r, const uint8_t* codes,
+                                   const uint8_t* params, const uint16_t* consts, int64_t k,
+                                   int nbits, int64_t block, const int64_t* code_off,
+                                   const int64_t* param_off, int32_t* out_codes,
+                                   uint8_t* out_params, uint16_t* out_consts, int32_t* bad,
+                                   void* stream) {
+  clear_error();
+  HI2X_REQUIRE(nbits == 2 || nbits == 4 || nbits == 8, "assemble: nbits=%d", nbits);
+  HI2X_REQUIRE(block > 0 && k % block == 0 && k % (32 / nbits) == 0, "assemble: K/block");
+  if (r == 0) return HI2X_OK;
+  const int64_t nw = k / (32 / nbits), nblk = k / block;
+  const int64_t span = nw > nblk ? nw : nblk;
+  const int64_t total = r * span;
+  hipLaunchKernelGGL(assemble_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0,
+                     as_stream(stream), rows, r, codes, params, consts, k, nbits, nblk, code_off,
+                     param_off, out_codes, out_params, out_consts, bad);
+  return launch_status("assemble_kernel");
+}

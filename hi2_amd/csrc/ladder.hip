@@ -1,0 +1,365 @@
+// Ladder fit, 8-bit block parameters, decode, and the GPTQ finish (un-permute + SSE).
+//
+// Reference: hi2/encode.py:18-119 (EFFORT, _recon, _lsq, fit_ladder, quantize_params),
+// hi2/ladder_kernel.py:44-86 (the grid search), hi2/format.py:45-69 (decode_params,
+// ladder_dequantize), hi2/hessian.py:318-345 (_finish).
+#include "common.h"
+
+namespace hi2x {
+namespace {
+
+struct Grid {
+  float v[8];
+};
+
+// One thread per (row, block).  Grid search then `ls` weighted least-squares refits,
+// every elementwise op rounded as the reference's torch ops and every block sum in
+// torch's CPU order (torch_sum_small), so lo/step are bit-identical to fit_ladder.
+template <int B>
+__global__ __launch_bounds__(256) void ladder_fit_kernel(
+    const float* __restrict__ w, const float* __restrict__ d, int64_t rows, int64_t k,
+    int nlev, Grid grid, int G, int ls, float* __restrict__ out_lo,
+    float* __restrict__ out_st, float* __restrict__ out_err) {
+  const int64_t nb = k / B;
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= rows * nb) return;
+  const int64_t r = i / nb, b = i % nb;
+  const float* wp = w + r * k + b * B;
+  const float* dp = d + b * B;
+  float x[B], dd[B];
+#pragma unroll
+  for (int t = 0; t < B; t += 4) {
+    const float4 v = *reinterpret_cast<const float4*>(wp + t);
+    x[t] = v.x;
+    x[t + 1] = v.y;
+    x[t + 2] = v.z;
+    x[t + 3] = v.w;
+    const float4 e = *reinterpret_cast<const float4*>(dp + t);
+    dd[t] = e.x;
+    dd[t + 1] = e.y;
+    dd[t + 2] = e.z;
+    dd[t + 3] = e.w;
+  }
+  const float nm = (float)(nlev - 1);
+  float mn = x[0], mx = x[0];
+#pragma unroll
+  for (int t = 1; t < B; ++t) {
+    mn = (x[t] < mn) ? x[t] : mn;
+    mx = (x[t] > mx) ? x[t] : mx;
+  }
+  const float span = mx - mn;
+
+  auto err_of = [&](float lo, float step) {
+    const float safe = (step == 0.0f) ? 1.0f : step;
+    return torch_sum_small<B>([&](int t) {
+      const float c = clamp_code(__builtin_rintf((x[t] - lo) / safe), nm);
+      const float rec = lo + c * step;
+      const float df = rec - x[t];
+      return dd[t] * (df * df);
+    });
+  };
+
+  float best_lo = 0.0f, best_st = 0.0f, best_err = 0.0f;
+  bool first = true;
+  for (int a = 0; a < G; ++a) {
+    const float lo = mn + grid.v[a] * span;
+    for (int bb = 0; bb < G; ++bb) {
+      const float step = ((mx - grid.v[bb] * span) - lo) / nm;
+      const float err = err_of(lo, step);
+      if (first || err < best_err) {
+        best_lo = lo;
+        best_st = step;
+        best_err = err;
+        first = false;
+      }
+    }
+  }
+  for (int it = 0; it < ls; ++it) {
+    const float safe = (best_st == 0.0f) ? 1.0f : best_st;
+    float c[B];
+#pragma unroll
+    for (int t = 0; t < B; ++t) c[t] = clamp_code(__builtin_rintf((x[t] - best_lo) / safe), nm);
+    const float sd = torch_sum_small<B>([&](int t) { return dd[t]; });
+    const float sc = torch_sum_small<B>([&](int t) { return dd[t] * c[t]; });
+    const float scc = torch_sum_small<B>([&](int t) { return (dd[t] * c[t]) * c[t]; });
+    const float sw = torch_sum_small<B>([&](int t) { return dd[t] * x[t]; });
+    const float scw = torch_sum_small<B>([&](int t) { return (dd[t] * c[t]) * x[t]; });
+    const float det = sd * scc - sc * sc;
+    const bool ok = __builtin_fabsf(det) > 1e-20f;
+    const float step = ok ? (sd * scw - sc * sw) / det : 0.0f;
+    const float sdc = (sd < 1e-20f) ? 1e-20f : sd;
+    const float lo =
+        ok ? (sw - step * sc) / sdc : torch_sum_small<B>([&](int t) { return x[t]; }) / (float)B;
+    const float err = err_of(lo, step);
+    if (err < best_err && step > 0.0f) {
+      best_lo = lo;
+      best_st = step;
+      best_err = err;
+    }
+  }
+  out_lo[i] = best_lo;
+  out_st[i] = best_st;
+  if (out_err) out_err[i] = best_err;
+}
+
+// quantize_params + decode_params, one wave per row (max/min reductions are exact).
+__global__ __launch_bounds__(256) void params_kernel(
+    const float* __restrict__ lo, const float* __restrict__ step, int64_t rows, int64_t nb,
+    uint8_t* __restrict__ lo_u8, uint8_t* __restrict__ st_u8, uint16_t* __restrict__ consts,
+    float* __restrict__ lo_d, float* __restrict__ st_d, int64_t ldd) {
+  const int lane = threadIdx.x & 63;
+  const int64_t r = (int64_t)blockIdx.x * (blockDim.x / 64) + (threadIdx.x >> 6);
+  if (r >= rows) return;
+  const float* l = lo + r * nb;
+  const float* s = step + r * nb;
+  float smax = 0.0f, lmin = __builtin_inff(), lmax = -__builtin_inff();
+  bool any = false;
+  for (int64_t b = lane; b < nb; b += 64) {
+    const float sv = s[b] < 0.0f ? 0.0f : s[b];
+    smax = (!any || sv > smax) ? sv : smax;
+    lmin = (l[b] < lmin) ? l[b] : lmin;
+    lmax = (l[b] > lmax) ? l[b] : lmax;
+    any = true;
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) {
+    const float so = __shfl_xor(smax, off);
+    const float no = __shfl_xor(lmin, off);
+    const float xo = __shfl_xor(lmax, off);
+    const int ao = __shfl_xor((int)any, off);
+    smax = (ao && (!any || so > smax)) ? so : smax;
+    lmin = (no < lmin) ? no : lmin;
+    lmax = (xo > lmax) ? xo : lmax;
+    any = any || ao;
+  }
+  const uint16_t ss_h = f16_bits(smax / 255.0f);
+  const float ss = f16_from_bits(ss_h);
+  const uint16_t lm_h = f16_bits(lmin);
+  const float lmf = f16_from_bits(lm_h);
+  float span = lmax - lmf;
+  span = span < 0.0f ? 0.0f : span;
+  const uint16_t ls_h = f16_bits(span / 255.0f);
+  const float lsf = f16_from_bits(ls_h);
+  if (lane == 0) {
+    consts[r * 3 + 0] = lm_h;
+    consts[r * 3 + 1] = ls_h;
+    consts[r * 3 + 2] = ss_h;
+  }
+  for (int64_t b = lane; b < nb; b += 64) {
+    const float sv = s[b] < 0.0f ? 0.0f : s[b];
+    float su = 0.0f;
+    if (ss > 0.0f) su = __builtin_rintf(sv / (ss < 1e-30f ? 1e-30f : ss));
+    su = su < 0.0f ? 0.0f : (su > 255.0f ? 255.0f : su);
+    float lu = 0.0f;
+    if (lsf > 0.0f) lu = __builtin_rintf((l[b] - lmf) / (lsf < 1e-30f ? 1e-30f : lsf));
+    lu = lu < 0.0f ? 0.0f : (lu > 255.0f ? 255.0f : lu);
+    const uint8_t lub = (uint8_t)lu, sub = (uint8_t)su;
+    lo_u8[r * nb + b] = lub;
+    st_u8[r * nb + b] = sub;
+    if (lo_d) {
+      const double v = (double)lub * (double)lsf + (double)lmf;
+      lo_d[r * ldd + b] = f16_round((float)v);
+      st_d[r * ldd + b] = f16_round((float)sub * ss);
+    }
+  }
+}
+
+__global__ void decode_kernel(const uint8_t* __restrict__ lo_u8, const uint8_t* __restrict__ st_u8,
+                              const uint16_t* __restrict__ consts, int64_t rows, int64_t nb,
+                              uint16_t* __restrict__ lo_h, uint16_t* __restrict__ st_h) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= rows * nb) return;
+  const int64_t r = i / nb;
+  const float lm = f16_from_bits(consts[r * 3 + 0]);
+  const float ls = f16_from_bits(consts[r * 3 + 1]);
+  const float ss = f16_from_bits(consts[r * 3 + 2]);
+  const double v = (double)lo_u8[i] * (double)ls + (double)lm;
+  lo_h[i] = f16_bits((float)v);
+  st_h[i] = f16_bits((float)st_u8[i] * ss);
+}
+
+__global__ void dequant_kernel(const uint8_t* __restrict__ codes, const float* __restrict__ lo,
+                               const float* __restrict__ st, int64_t rows, int64_t nb, int64_t B,
+                               int exact, uint16_t* __restrict__ out) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= rows * nb * B) return;
+  const int64_t rb = i / B;
+  const float c = (float)codes[i];
+  if (exact) {
+    const double v = (double)lo[rb] + (double)c * (double)st[rb];
+    out[i] = __builtin_bit_cast(uint16_t, (_Float16)v);
+  } else {
+    out[i] = f16_bits(lo[rb] + c * st[rb]);
+  }
+}
+
+// Un-permute codes / comp: out[r, perm[j]] = in[r, j].
+__global__ void unpermute_kernel(const uint8_t* __restrict__ codes_ro, const float* __restrict__ comp_ro,
+                                 const int64_t* __restrict__ perm, int64_t n, int64_t k,
+                                 uint8_t* __restrict__ codes, float* __restrict__ comp) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n * k) return;
+  const int64_t r = i / k, j = i % k;
+  const int64_t c = perm ? perm[j] : j;
+  codes[r * k + c] = codes_ro[i];
+  if (comp && comp_ro) comp[r * k + c] = comp_ro[i];
+}
+
+// sse[r] = sum_c d_c (fp16(lo + code*step) - w)^2 in torch's CPU sum order for a
+// contiguous row of k floats: 8 vector lanes x 4 vector accumulators, the 4-level
+// cascade over rows of 32 floats (base 2^max(4, ceil_log2(rows)/4)), the extra vectors
+// into accumulator 0, the accumulators folded, then the 8 lanes in order.  Two rows per
+// wave; lane (kq, v) = (l/8 % 4, l%8) of a 32-lane half holds p[kq][v].
+__device__ __forceinline__ int64_t ceil_log2_dev(int64_t x) {
+  if (x <= 2) return 1;
+  return 64 - __builtin_clzll((unsigned long long)(x - 1));
+}
+
+__global__ __launch_bounds__(256) void sse_kernel(const uint8_t* __restrict__ codes,
+                                                  int64_t n, int64_t k, int64_t B,
+                                                  const float* __restrict__ lo_d,
+                                                  const float* __restrict__ st_d, int64_t ldd,
+                                                  const float* __restrict__ w,
+                                                  const float* __restrict__ d,
+                                                  float* __restrict__ sse) {
+  const int lane = threadIdx.x & 63;
+  const int half = lane >> 5, hl = lane & 31;
+  const int kq = hl >> 3, v = hl & 7;
+  const int64_t r = ((int64_t)blockIdx.x * (blockDim.x / 64) + (threadIdx.x >> 6)) * 2 + half;
+  const bool live = r < n;
+  const int64_t rr = live ? r : 0;
+  auto term = [&](int64_t c) -> float {
+    const int64_t b = c / B;
+    const float rec = f16_round(lo_d[rr * ldd + b] + (float)codes[rr * k + c] * st_d[rr * ldd + b]);
+    const float df = rec - w[rr * k + c];
+    return d[c] * (df * df);
+  };
+  const int64_t vec_size = k / 8;
+  const int64_t size_ilp = vec_size / 4;
+  float p = 0.0f;
+  if (size_ilp > 0) {
+    int64_t lp = ceil_log2_dev(size_ilp) / 4;
+    if (lp < 4) lp = 4;
+    const int64_t step = (int64_t)1 << lp, lmask = step - 1;
+    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    int64_t i = 0;
+    while (i + step <= size_ilp) {
+      for (int64_t j = 0; j < step; ++j) acc[0] += term(((i + j) * 4 + kq) * 8 + v);
+      i += step;
+      for (int lev = 1; lev < 4; ++lev) {
+        acc[lev] += acc[lev - 1];
+        acc[lev - 1] = 0.0f;
+        if (i & (lmask << (lev * lp))) break;
+      }
+    }
+    for (; i < size_ilp; ++i) acc[0] += term((i * 4 + kq) * 8 + v);
+    p = ((acc[0] + acc[1]) + acc[2]) + acc[3];
+  }
+  if (kq == 0)
+    for (int64_t i = size_ilp * 4; i < vec_size; ++i) p += term(i * 8 + v);
+  // fold the 4 accumulators of lane v: ((p0 + p1) + p2) + p3
+  const int base = half * 32;
+  const float p1 = __shfl(p, base + 8 + v);
+  const float p2 = __shfl(p, base + 16 + v);
+  const float p3 = __shfl(p, base + 24 + v);
+  const float p0 = ((p + p1) + p2) + p3;  // valid on kq == 0
+  float out = 0.0f;
+  for (int64_t i = vec_size * 8; i < k; ++i) out += term(i);
+#pragma unroll
+  for (int vv = 0; vv < 8; ++vv) out += __shfl(p0, base + vv);
+  if (live && hl == 0) sse[r] = out;
+}
+
+template <int B>
+int launch_fit(const float* w, const float* d, int64_t rows, int64_t k, int nlev,
+               const Grid& grid, int g, int ls, float* lo, float* step, float* err,
+               hipStream_t s) {
+  const int64_t total = rows * (k / B);
+  const dim3 blocks((unsigned)((total + 255) / 256));
+  hipLaunchKernelGGL(ladder_fit_kernel<B>, blocks, dim3(256), 0, s, w, d, rows, k, nlev, grid,
+                     g, ls, lo, step, err);
+  return launch_status("ladder_fit_kernel");
+}
+
+}  // namespace
+}  // namespace hi2x
+
+using namespace hi2x;
+
+extern "C" int hi2x_ladder_fit(const float* w, const float* d, int64_t rows, int64_t k,
+                               int64_t block, int nlev, const float* grid, int g, int ls,
+                               float* lo, float* step, float* err, void* stream) {
+  clear_error();
+  HI2X_REQUIRE(block == 16 || block == 32 || block == 64, "ladder_fit: block %lld",
+               (long long)block);
+  HI2X_REQUIRE(k > 0 && k % block == 0, "ladder_fit: K=%lld not a multiple of %lld",
+               (long long)k, (long long)block);
+  HI2X_REQUIRE(g >= 1 && g <= 8 && grid, "ladder_fit: grid of %d points", g);
+  HI2X_REQUIRE(nlev >= 2 && nlev <= 256 && ls >= 0, "ladder_fit: nlev=%d ls=%d", nlev, ls);
+  if (rows == 0) return HI2X_OK;
+  Grid gr{};
+  for (int i = 0; i < g; ++i) gr.v[i] = grid[i];
+  hipStream_t s = as_stream(stream);
+  switch (block) {
+    case 16: return launch_fit<16>(w, d, rows, k, nlev, gr, g, ls, lo, step, err, s);
+    case 32: return launch_fit<32>(w, d, rows, k, nlev, gr, g, ls, lo, step, err, s);
+    default: return launch_fit<64>(w, d, rows, k, nlev, gr, g, ls, lo, step, err, s);
+  }
+}
+
+extern "C" int hi2x_params(const float* lo, const float* step, int64_t rows, int64_t nb,
+                           uint8_t* lo_u8, uint8_t* step_u8, uint16_t* consts, float* lo_d,
+                           float* step_d, int64_t ldd, void* stream) {
+  clear_error();
+  HI2X_REQUIRE(nb > 0 && rows >= 0, "params: bad shape");
+  HI2X_REQUIRE(!lo_d || ldd >= nb, "params: ldd < nb");
+  HI2X_REQUIRE((lo_d == nullptr) == (step_d == nullptr), "params: lo_d/step_d pairing");
+  if (rows == 0) return HI2X_OK;
+  const dim3 blocks((unsigned)((rows + 3) / 4));
+  hipLaunchKernelGGL(params_kernel, blocks, dim3(256), 0, as_stream(stream), lo, step, rows, nb,
+                     lo_u8, step_u8, consts, lo_d, step_d, ldd);
+  return launch_status("params_kernel");
+}
+
+extern "C" int hi2x_decode_params(const uint8_t* lo_u8, const uint8_t* step_u8,
+                                  const uint16_t* consts, int64_t rows, int64_t nb,
+                                  uint16_t* lo_h, uint16_t* step_h, void* stream) {
+  clear_error();
+  HI2X_REQUIRE(rows >= 0 && nb > 0, "decode_params: bad shape");
+  if (rows == 0) return HI2X_OK;
+  const int64_t total = rows * nb;
+  hipLaunchKernelGGL(decode_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0,
+                     as_stream(stream), lo_u8, step_u8, consts, rows, nb, lo_h, step_h);
+  return launch_status("decode_kernel");
+}
+
+extern "C" int hi2x_ladder_dequantize(const uint8_t* codes, const float* lo, const float* step,
+                                      int64_t rows, int64_t nb, int64_t block, int exact,
+                                      uint16_t* out_h, void* stream) {
+  clear_error();
+  HI2X_REQUIRE(rows >= 0 && nb > 0 && block > 0, "ladder_dequantize: bad shape");
+  if (rows == 0) return HI2X_OK;
+  const int64_t total = rows * nb * block;
+  hipLaunchKernelGGL(dequant_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0,
+                     as_stream(stream), codes, lo, step, rows, nb, block, exact, out_h);
+  return launch_status("dequant_kernel");
+}
+
+extern "C" int hi2x_finish(const uint8_t* codes_ro, const float* comp_ro, const int64_t* perm,
+                           int64_t n, int64_t k, int64_t block, const float* lo_d,
+                           const float* step_d, int64_t ldd, const float* w, const float* d,
+                           uint8_t* codes, float* comp, float* sse, void* stream) {
+  clear_error();
+  HI2X_REQUIRE(n >= 0 && k > 0 && block > 0 && k % block == 0, "finish: bad shape");
+  HI2X_REQUIRE(ldd >= k / block, "finish: ldd < nb");
+  if (n == 0) return HI2X_OK;
+  hipStream_t s = as_stream(stream);
+  const int64_t total = n * k;
+  hipLaunchKernelGGL(unpermute_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s,
+                     codes_ro, comp_ro, perm, n, k, codes, comp);
+  int rc = launch_status("unpermute_kernel");
+  if (rc) return rc;
+  hipLaunchKernelGGL(sse_kernel, dim3((unsigned)((n + 7) / 8)), dim3(256), 0, s, codes, n, k,
+                     block, lo_d, step_d, ldd, w, d, sse);
+  return launch_status("sse_kernel");
+}

@@ -1,0 +1,215 @@
+"""HadamardINT2-FP16 v3.2 format helpers on the encode path (MI355X).
+
+Mirror of the hot-path part of the reference's ``hi2/format.py`` (same names, argument
+meaning and errors): ``GROUP``, ``hadamard16`` (22-27), ``fwht_groups`` (30-41),
+``decode_params`` (45-60), ``ladder_dequantize`` (63-69), ``pack_codes`` (73-85),
+``HI2Tensor`` / ``FIELDS`` (97-124) and ``assemble`` (127-184).  The arithmetic runs in
+the hi2x HIP kernels; inputs must be device tensors (``assemble`` returns the flat
+buffers on the host, as the reference does).  Decode/verification helpers
+(``dequantize``, accounting) are not part of the encode path and are not provided.
+"""
+
+import math
+from dataclasses import dataclass
+
+import torch
+
+from . import _lib
+
+GROUP = 16
+
+
+def hadamard16(dtype: torch.dtype = torch.float64, device="cpu") -> torch.Tensor:
+    """Normalised order-16 Walsh-Hadamard matrix (Sylvester, entries +-1/4):
+    symmetric, ``H @ H = I``.  A constant, built on the host."""
+    i = torch.arange(GROUP)
+    bits = torch.bitwise_and(i[:, None], i[None, :])
+    parity = torch.zeros_like(bits)
+    for b in range(4):
+        parity ^= (bits >> b) & 1
+    h = torch.where(parity.bool(), -1.0, 1.0).to(torch.float64) / math.sqrt(GROUP)
+    return h.to(dtype=dtype, device=device)
+
+
+def fwht_groups(x: torch.Tensor, flags: torch.Tensor) -> torch.Tensor:
+    """Transform the flagged 16-column groups of ``x[..., K]`` (an involution).
+
+    float32/float64 inputs are transformed in their own precision, other dtypes in
+    float64 and cast back, as the reference does."""
+    k = x.shape[-1]
+    if k % GROUP:
+        raise ValueError(f"K={k} must be a multiple of {GROUP}")
+    if flags.numel() != k // GROUP:
+        raise ValueError(f"flags has {flags.numel()} entries, expected {k // GROUP}")
+    dev = _lib.require_gpu(x)
+    work = x.dtype if x.dtype in (torch.float32, torch.float64) else torch.float64
+    xi = x.to(work).contiguous()
+    fl = flags.to(dev, torch.uint8).reshape(-1).contiguous()
+    out = torch.empty_like(xi)
+    rows = xi.numel() // k if k else 0
+    _lib.call("hi2x_fwht16", dev, _lib.ptr(xi), _lib.ptr(out), 0 if work == torch.float32 else 1,
+              rows, k, _lib.ptr(fl))
+    return out.to(x.dtype)
+
+
+# ---- block parameters (spec 2.2) --------------------------------------------------------
+def decode_params(
+    lo_u8: torch.Tensor,
+    step_u8: torch.Tensor,
+    lo_min: torch.Tensor,
+    lo_scale: torch.Tensor,
+    step_scale: torch.Tensor,
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """fp16 ``lo``/``step`` of each block from its two bytes and the row constants
+    (broadcast): ``lo = fp16(f32(f64(u) * f64(lo_scale) + f64(lo_min)))``,
+    ``step = fp16(f32(u) * f32(step_scale))``."""
+    dev = _lib.require_gpu(lo_u8, step_u8)
+    shape = torch.broadcast_shapes(lo_u8.shape, step_u8.shape, lo_min.shape, lo_scale.shape,
+                                   step_scale.shape)
+    lu = lo_u8.to(dev, torch.uint8).expand(shape).contiguous().reshape(-1)
+    su = step_u8.to(dev, torch.uint8).expand(shape).contiguous().reshape(-1)
+    consts = torch.stack(
+        [c.to(dev, torch.float16).expand(shape).reshape(-1) for c in (lo_min, lo_scale, step_scale)],
+        dim=-1,
+    ).contiguous()
+    n = lu.numel()
+    lo = torch.empty(n, dtype=torch.float16, device=dev)
+    st = torch.empty(n, dtype=torch.float16, device=dev)
+    if n:
+        _lib.call("hi2x_decode_params", dev, _lib.ptr(lu), _lib.ptr(su), _lib.ptr(consts), n, 1,
+                  _lib.ptr(lo), _lib.ptr(st))
+    return lo.reshape(shape), st.reshape(shape)
+
+
+def ladder_dequantize(
+    codes: torch.Tensor, lo: torch.Tensor, step: torch.Tensor, dtype=torch.float64
+) -> torch.Tensor:
+    """``lo + code * step`` (codes ``[..., nb, B]``, lo/step ``[..., nb]``) with one
+    rounding to fp16; evaluated in float64 (exact) or float32 (candidate search)."""
+    if dtype not in (torch.float32, torch.float64):
+        raise ValueError(f"dtype {dtype} (float32 or float64)")
+    dev = _lib.require_gpu(codes)
+    b = codes.shape[-1]
+    lo_b = lo.to(dev, torch.float32).expand(codes.shape[:-1]).contiguous()
+    st_b = step.to(dev, torch.float32).expand(codes.shape[:-1]).contiguous()
+    c8 = codes.to(dev, torch.uint8).contiguous()
+    out = torch.empty(codes.shape, dtype=torch.float16, device=dev)
+    rows = lo_b.numel()
+    if rows:
+        _lib.call("hi2x_ladder_dequantize", dev, _lib.ptr(c8), _lib.ptr(lo_b), _lib.ptr(st_b),
+                  rows, 1, b, int(dtype == torch.float64), _lib.ptr(out))
+    return out
+
+
+# ---- code packing (v3.1 6.2) --------------------------------------------------------------
+def pack_codes(codes: torch.Tensor, nbits: int) -> torch.Tensor:
+    """``[..., n]`` codes -> ``[..., n * nbits / 32]`` int32, LSB-first."""
+    per_word = 32 // nbits
+    n = codes.shape[-1]
+    if n % per_word:
+        raise ValueError(f"{n} codes is not a multiple of {per_word}")
+    dev = _lib.require_gpu(codes)
+    if codes.dtype != torch.uint8:
+        if codes.numel() and (int(codes.max()) >= 2**nbits or int(codes.min()) < 0):
+            raise ValueError("code outside the ladder")
+        codes = codes.to(torch.uint8)
+    c = codes.contiguous()
+    rows = c.numel() // n if n else 0
+    out = torch.empty(*codes.shape[:-1], n // per_word, dtype=torch.int32, device=dev)
+    bad = torch.zeros(1, dtype=torch.int32, device=dev)
+    _lib.call("hi2x_pack_codes", dev, _lib.ptr(c), rows, n, int(nbits), _lib.ptr(out),
+              _lib.ptr(bad))
+    if int(bad.item()):
+        raise ValueError("code outside the ladder")
+    return out
+
+
+# ---- tensor container (2.4) ---------------------------------------------------------------
+@dataclass
+class HI2Tensor:
+    """Flat per-tensor buffers of spec 2.4 (CPU tensors)."""
+
+    codes: torch.Tensor  # int32 [sum words_per_row]
+    code_off: torch.Tensor  # int32 [R+1]
+    blk_params: torch.Tensor  # uint8 [2 * sum K/B_r]: (lo_u8, step_u8) per block
+    param_off: torch.Tensor  # int32 [R+1], offsets in blocks
+    row_consts: torch.Tensor  # fp16 [R, 3]: lo_min, lo_scale, step_scale
+    row_nbits: torch.Tensor  # uint8 [R]
+    row_block: torch.Tensor  # uint8 [R]
+    had: torch.Tensor  # uint8 [K/16]
+    shape: tuple[int, int]
+    col_scale: torch.Tensor | None = None
+
+
+FIELDS = (
+    "codes",
+    "code_off",
+    "blk_params",
+    "param_off",
+    "row_consts",
+    "row_nbits",
+    "row_block",
+    "had",
+)
+
+
+def assemble(
+    pieces: list[tuple[torch.Tensor, ...]],
+    row_nbits: torch.Tensor,
+    row_block: torch.Tensor,
+    had: torch.Tensor,
+    k: int,
+    col_scale: torch.Tensor | None = None,
+    stager=None,
+) -> HI2Tensor:
+    """Flat buffers from per-config row groups ``(rows, codes[r, K] uint8,
+    params[r, nb, 2] uint8, consts[r, 3] fp16)``: packing and scatters run on the
+    device of the first piece's codes, the result is returned on the host (through
+    ``stager.to_host`` when given)."""
+    if not pieces:
+        raise ValueError("assemble needs at least one piece on the device")
+    dev = _lib.require_gpu(pieces[0][1])
+    r = row_nbits.numel()
+    nb = row_nbits.to(torch.int64).cpu()
+    words = (k * nb) // 32
+    blocks = k // row_block.to(torch.int64).cpu()
+    code_off = torch.zeros(r + 1, dtype=torch.int64)
+    code_off[1:] = torch.cumsum(words, 0)
+    param_off = torch.zeros(r + 1, dtype=torch.int64)
+    param_off[1:] = torch.cumsum(blocks, 0)
+    code_off_d, param_off_d = code_off.to(dev), param_off.to(dev)
+    codes = torch.zeros(int(code_off[-1]), dtype=torch.int32, device=dev)
+    params = torch.zeros(int(param_off[-1]) * 2, dtype=torch.uint8, device=dev)
+    consts = torch.zeros(r, 3, dtype=torch.float16, device=dev)
+    bad = torch.zeros(1, dtype=torch.int32, device=dev)
+    keep = []
+    for rows, c, p, rc in pieces:
+        rows_c = rows.cpu()
+        if rows_c.numel() == 0:
+            continue
+        nbits = int(nb[rows_c[0]])
+        blk = k // int(blocks[rows_c[0]])
+        rows_d = rows.to(dev, torch.int64).contiguous()
+        c_d = c.to(dev, torch.uint8).contiguous()
+        p_d = p.to(dev, torch.uint8).contiguous()
+        rc_d = rc.to(dev, torch.float16).contiguous()
+        keep += [rows_d, c_d, p_d, rc_d]
+        _lib.call("hi2x_assemble_piece", dev, _lib.ptr(rows_d), rows_d.numel(), _lib.ptr(c_d),
+                  _lib.ptr(p_d), _lib.ptr(rc_d), k, nbits, blk, _lib.ptr(code_off_d),
+                  _lib.ptr(param_off_d), _lib.ptr(codes), _lib.ptr(params), _lib.ptr(consts),
+                  _lib.ptr(bad))
+    if int(bad.item()):
+        raise ValueError("code outside the ladder")
+    to_host = stager.to_host if stager is not None else (lambda t: t.cpu())
+    return HI2Tensor(
+        codes=to_host(codes),
+        code_off=code_off.to(torch.int32),
+        blk_params=to_host(params),
+        param_off=param_off.to(torch.int32),
+        row_consts=to_host(consts),
+        row_nbits=row_nbits.to(torch.uint8).cpu(),
+        row_block=row_block.to(torch.uint8).cpu(),
+        had=had.to(torch.uint8).reshape(-1).cpu(),
+        shape=(r, k),
+        col_scale=col_scale,
+    )

@@ -1,0 +1,357 @@
+"""Hessian-aware (error-compensated) rounding on MI355X, spec 8.3.
+
+Mirror of the reference's ``hi2/hessian.py`` (same names, argument meaning, module
+globals and errors): ``HessianStats`` (26-47), ``transform_sigma`` (50-68),
+``inverse_factor`` (71-86), ``encode_rows_gptq_reference`` (89-175), ``GptqJob``
+(178-188), ``_Unit`` / ``_prepare`` / ``_round_kernel`` / ``_finish`` (191-345),
+``encode_jobs_gptq`` (359-416), ``encode_rows_gptq`` (419-443).
+
+Every arithmetic step runs in the hi2x HIP kernels (``libhi2x.so``):
+
+* ``HessianStats.update``: ``hi2x_hessian_syrk`` (bf16 / f32 MFMA, exactly symmetric);
+* ``transform_sigma``: ``hi2x_sigma_transform`` (bit-identical to the reference einsums);
+* ``inverse_factor``: ``hi2x_chol_inv_upper`` (reversed blocked Cholesky + triangular
+  inverse on f32 MFMA), the damping retry driven here as in the reference;
+* the ladder fit / 8-bit params (``hi2x_ladder_fit``, ``hi2x_params``), the column loop
+  with its cross-block updates (``hi2x_gptq_run``) and ``_finish`` (``hi2x_finish``),
+  all bit-identical to the reference's torch CPU path for the same ``(w, d, u)``.
+
+Inputs must be HIP device tensors; there is no CPU or torch fallback
+(``backend="torch"`` raises).
+"""
+
+import os
+from dataclasses import dataclass
+
+import torch
+
+from . import _lib
+from .encode import EFFORT, Encoded, _fit, params_decoded
+from .format import GROUP
+
+BLOCK_COLUMNS = 128  # lazy-update block of GPTQ
+ROW_ELEMS = 1 << 26  # rows per chunk are bounded so the working copies fit
+# chunks of several jobs batched through one kernel launch sequence (weights per batch)
+BATCH_ELEMS = int(os.environ.get("HI2_BATCH_ELEMS", 1 << 27))
+# 128-column blocks whose far-column updates share one pass over the working copy
+SUPER_BLOCKS = int(os.environ.get("HI2_SUPER_BLOCKS", 4))
+
+__all__ = [
+    "EFFORT",
+    "GptqJob",
+    "HessianStats",
+    "encode_jobs_gptq",
+    "encode_rows_gptq",
+    "encode_rows_gptq_reference",
+    "inverse_factor",
+    "transform_sigma",
+]
+
+
+class HessianStats:
+    """Full second moment ``sum x x^T`` of a Linear's input (fp32, ``[K, K]``) on a HIP
+    device; ``update`` accumulates on MFMA (bf16 inputs exactly, fp32 inputs on f32
+    MFMA, other dtypes converted to fp32 first as the reference does)."""
+
+    def __init__(self, k: int, device="cuda"):
+        self.k = k
+        dev = torch.device(device)
+        if dev.type != "cuda":
+            raise RuntimeError(
+                f"hi2_amd.HessianStats accumulates on the MI355X; got device {dev}"
+            )
+        self.S = torch.zeros(k, k, dtype=torch.float32, device=dev)
+        self.n = 0
+
+    @torch.no_grad()
+    def update(self, x: torch.Tensor, chunk: int = 4096) -> None:
+        """``S += x^T x`` over all rows of ``x[..., K]`` (``chunk`` is accepted for
+        interface compatibility; the kernel streams the rows itself)."""
+        x = x.reshape(-1, self.k)
+        dev = self.S.device
+        if x.dtype not in (torch.bfloat16, torch.float32):
+            x = x.to(torch.float32)
+        x = x.to(dev).contiguous()
+        t = x.shape[0]
+        if t:
+            dtype = 2 if x.dtype == torch.bfloat16 else 0
+            _lib.call("hi2x_hessian_syrk", dev, _lib.ptr(x), dtype, t, self.k,
+                      _lib.ptr(self.S))
+        self.n += t
+
+    def merge(self, other: "HessianStats") -> None:
+        self.S += other.S.to(self.S.device)
+        self.n += other.n
+
+    def mean(self) -> torch.Tensor:
+        return self.S / max(self.n, 1)
+
+
+def transform_sigma(
+    sigma: torch.Tensor, col_scale: torch.Tensor | None, had: torch.Tensor
+) -> torch.Tensor:
+    """``Hs = T Sigma T^T`` with ``T = R diag(1/s)`` (R block-diagonal, flagged groups),
+    symmetrised."""
+    k = sigma.shape[0]
+    if k % GROUP:
+        raise ValueError(f"K={k} must be a multiple of {GROUP}")
+    dev = _lib.require_gpu(sigma)
+    s = sigma.to(torch.float32).contiguous()
+    fl = had.to(dev, torch.uint8).reshape(-1).contiguous()
+    if fl.numel() != k // GROUP:
+        raise ValueError(f"had has {fl.numel()} entries, expected {k // GROUP}")
+    cs = None
+    if col_scale is not None:
+        cs = col_scale.to(dev, torch.float16).reshape(-1).contiguous()
+    out = torch.empty_like(s)
+    _lib.call("hi2x_sigma_transform", dev, _lib.ptr(s), _lib.ptr(cs), _lib.ptr(fl), k,
+              _lib.ptr(out))
+    return out
+
+
+def inverse_factor(hs: torch.Tensor, damp: float = 0.01) -> torch.Tensor:
+    """Upper Cholesky factor ``U`` of ``(Hs + damp * mean(diag) I)^-1``; the damping is
+    raised tenfold (up to five times) if the factorisation fails."""
+    dev = _lib.require_gpu(hs)
+    k = hs.shape[0]
+    h = hs.to(torch.float32).contiguous()
+    u = torch.empty_like(h)
+    last = None
+    for attempt in range(6):
+        try:
+            _lib.call("hi2x_chol_inv_upper", dev, _lib.ptr(h), k, float(damp), attempt,
+                      _lib.ptr(u))
+            return u
+        except _lib.NotPositiveDefinite as e:
+            last = e
+    raise RuntimeError(f"Hessian is not factorisable even with heavy damping: {last}")
+
+
+@dataclass
+class GptqJob:
+    """One call of :func:`encode_rows_gptq`: rows ``w[N, K]`` (stored basis), ladder
+    weights ``d[K]``, factor ``u[K, K]`` (of the permuted Hessian when ``perm`` is set)."""
+
+    w: torch.Tensor
+    d: torch.Tensor
+    u: torch.Tensor
+    nbits: int
+    block: int
+    perm: torch.Tensor | None = None
+
+
+@dataclass
+class _Unit:
+    """A row chunk of a job, exactly the unit the reference processes in one pass."""
+
+    job: int
+    s: int
+    wc: torch.Tensor | None  # [n, K] fp32 working copy, columns in rounding order
+    lo_u8: torch.Tensor
+    step_u8: torch.Tensor
+    consts: torch.Tensor
+    lo_d: torch.Tensor  # [n, nb] fp32 decoded
+    step_d: torch.Tensor
+    blk_of: torch.Tensor  # [K] block of each column in rounding order
+    codes: torch.Tensor | None = None  # uint8 [n, K] in rounding order
+    comp: torch.Tensor | None = None  # fp32 [n, K] value each code was rounded from
+
+
+def _prepare(ji: int, job: GptqJob, s: int, step_rows: int, effort: str) -> _Unit:
+    w, k = job.w, job.w.shape[1]
+    if k % job.block:
+        raise ValueError(f"K={k} is not a multiple of the block {job.block}")
+    dev = w.device
+    nb = k // job.block
+    wc = w[s : s + step_rows].to(torch.float32).contiguous()
+    if wc.data_ptr() == w.data_ptr() and wc.dtype == w.dtype:
+        wc = wc.clone()
+    cfg = EFFORT[effort]
+    lo, step, _ = _fit(wc.reshape(-1, nb, job.block), job.d, 2**job.nbits, cfg["grid"],
+                       cfg["ls"], False)
+    lo_u8, step_u8, consts, lo_d, step_d = params_decoded(lo, step)
+    cols = torch.arange(k, device=dev)
+    if job.perm is not None:
+        p = job.perm.to(dev)
+        wc = wc.index_select(1, p)
+        cols = p
+    return _Unit(ji, s, wc, lo_u8, step_u8, consts, lo_d, step_d, cols // job.block)
+
+
+def _round_kernel(
+    units: list[_Unit], jobs: list[GptqJob], want_comp: bool = False, super_blocks=None
+) -> None:
+    """All ``units`` (same K, same device) through ``hi2x_gptq_run``: one intra-block
+    launch per 128 columns for every row, the cross-block updates on MFMA with the
+    reference's rounding."""
+    dev, k = units[0].wc.device, units[0].wc.shape[1]
+    sizes = [x.wc.shape[0] for x in units]
+    total = sum(sizes)
+    wc = torch.cat([x.wc for x in units]) if len(units) > 1 else units[0].wc
+    ldp = k // 16
+    lo = torch.zeros(total, ldp, dtype=torch.float32, device=dev)
+    st = torch.zeros(total, ldp, dtype=torch.float32, device=dev)
+    views, off = [], 0
+    for x, n in zip(units, sizes):
+        nb = x.lo_d.shape[1]
+        lo[off : off + n, :nb] = x.lo_d
+        st[off : off + n, :nb] = x.step_d
+        views.append((off, n))
+        off += n
+    row_grp = torch.repeat_interleave(
+        torch.arange(len(units), dtype=torch.int32), torch.tensor(sizes)
+    ).to(dev)
+    uk = [jobs[x.job].u.to(dev, torch.float32).contiguous() for x in units]
+    for u in uk:
+        if u.shape != (k, k):
+            raise ValueError(f"factor has shape {tuple(u.shape)}, expected ({k}, {k})")
+    u_ptrs = torch.tensor([u.data_ptr() for u in uk], dtype=torch.int64).to(dev)
+    blk = torch.stack([x.blk_of for x in units]).to(dev, torch.int32).contiguous()
+    nmax = torch.tensor(
+        [2 ** jobs[x.job].nbits - 1 for x in units], dtype=torch.float32
+    ).to(dev)
+    codes = torch.zeros(total, k, dtype=torch.uint8, device=dev)
+    comp = torch.zeros(total, k, dtype=torch.float32, device=dev) if want_comp else None
+    sb = SUPER_BLOCKS if super_blocks is None else super_blocks
+    sb = max(1, min(int(sb), (k + BLOCK_COLUMNS - 1) // BLOCK_COLUMNS))
+    err_ws = torch.empty(total, BLOCK_COLUMNS * sb, dtype=torch.float32, device=dev)
+    _lib.call("hi2x_gptq_run", dev, _lib.ptr(wc), total, k, _lib.ptr(codes), _lib.ptr(lo),
+              _lib.ptr(st), ldp, _lib.ptr(row_grp), _lib.ptr(u_ptrs), _lib.ptr(blk),
+              _lib.ptr(nmax), _lib.ptr(comp), _lib.ptr(err_ws), sb)
+    for x, (o, n) in zip(units, views):
+        x.codes = codes[o : o + n]
+        x.comp = None if comp is None else comp[o : o + n]
+    # Temporaries freed here (factor copies, index tensors, workspace) return to
+    # torch's caching allocator, which reuses them only in order on this stream.
+
+
+def _finish(unit: _Unit, job: GptqJob) -> Encoded:
+    k = job.w.shape[1]
+    dev = unit.codes.device
+    n_rows = unit.codes.shape[0]
+    w = job.w[unit.s : unit.s + n_rows].to(dev, torch.float32).contiguous()
+    d = job.d.to(dev, torch.float32).reshape(-1).contiguous()
+    perm = None if job.perm is None else job.perm.to(dev, torch.int64).contiguous()
+    codes_ro = unit.codes.contiguous()
+    comp_ro = None if unit.comp is None else unit.comp.contiguous()
+    codes = torch.empty(n_rows, k, dtype=torch.uint8, device=dev)
+    comp = None if comp_ro is None else torch.empty(n_rows, k, dtype=torch.float32, device=dev)
+    sse = torch.empty(n_rows, dtype=torch.float32, device=dev)
+    lo_d, st_d = unit.lo_d.contiguous(), unit.step_d.contiguous()
+    _lib.call("hi2x_finish", dev, _lib.ptr(codes_ro), _lib.ptr(comp_ro), _lib.ptr(perm), n_rows,
+              k, job.block, _lib.ptr(lo_d), _lib.ptr(st_d), lo_d.shape[1], _lib.ptr(w),
+              _lib.ptr(d), _lib.ptr(codes), _lib.ptr(comp), _lib.ptr(sse))
+    return Encoded(
+        codes,
+        torch.stack([unit.lo_u8, unit.step_u8], dim=-1),
+        unit.consts,
+        sse,
+        comp,
+    )
+
+
+def _use_kernel(dev: torch.device, backend: str) -> bool:
+    from . import gptq_kernel
+
+    if backend == "torch":
+        raise RuntimeError(
+            "hi2_amd has no torch backend: the encode path runs in the hi2x HIP kernels"
+        )
+    if not gptq_kernel.available(dev):
+        raise RuntimeError(
+            f"gptq kernel unavailable on {dev}: "
+            f"{gptq_kernel.failure() or 'not a gfx950 HIP device'}"
+        )
+    return True
+
+
+@torch.no_grad()
+def encode_jobs_gptq(
+    jobs: list[GptqJob],
+    effort: str = "normal",
+    backend: str | None = None,
+    comp: bool = False,
+    super_blocks: int | None = None,
+) -> list[Encoded]:
+    """:func:`encode_rows_gptq` for several jobs (tensors, experts, candidate groups)
+    at once, bit-identical to calling it on each.  Jobs are cut into the reference's
+    row chunks (``ROW_ELEMS``); chunks with the same K on the same device are batched
+    (up to ``BATCH_ELEMS`` weights) through one ``hi2x_gptq_run``.  With ``comp`` every
+    result carries ``Encoded.comp``."""
+    backend = backend or os.environ.get("HI2_GPTQ_BACKEND", "auto")
+    for job in jobs:
+        _lib.require_gpu(job.w)
+    units: list[_Unit] = []
+    for ji, job in enumerate(jobs):
+        n_rows, k = job.w.shape
+        step_rows = max(1, ROW_ELEMS // k)
+        for s in range(0, n_rows, step_rows):
+            units.append(_prepare(ji, job, s, step_rows, effort))
+    batches: dict[tuple, list[list[_Unit]]] = {}
+    for x in units:
+        key = (x.wc.device, x.wc.shape[1])
+        bl = batches.setdefault(key, [[]])
+        if bl[-1] and sum(y.wc.numel() for y in bl[-1]) + x.wc.numel() > BATCH_ELEMS:
+            bl.append([])
+        bl[-1].append(x)
+    for (dev, _k), bl in batches.items():
+        _use_kernel(dev, backend)
+        for batch in bl:
+            _round_kernel(batch, jobs, comp, super_blocks)
+            for x in batch:
+                x.wc = None  # free the working copy early
+    per_job: list[list[Encoded]] = [[] for _ in jobs]
+    for x in units:
+        per_job[x.job].append(_finish(x, jobs[x.job]))
+    out = []
+    for encs in per_job:
+        if len(encs) == 1:
+            out.append(encs[0])
+        else:
+            out.append(
+                Encoded(
+                    *(
+                        torch.cat([getattr(o, f) for o in encs])
+                        for f in ("codes", "params", "consts", "sse")
+                    ),
+                    torch.cat([o.comp for o in encs]) if comp else None,
+                )
+            )
+    return out
+
+
+def encode_rows_gptq(
+    w: torch.Tensor,
+    d: torch.Tensor,
+    u: torch.Tensor,
+    nbits: int,
+    block: int,
+    effort: str = "normal",
+    perm: torch.Tensor | None = None,
+    backend: str | None = None,
+    comp: bool = True,
+) -> Encoded:
+    """Quantise ``w[N, K]`` (stored basis) with error compensation; with ``perm`` the
+    columns are rounded in that order (``u`` is then the factor of the permuted
+    Hessian) and the blocks and stored codes keep their original positions.  ``d`` are
+    the ladder-fit weights (``diag(Hs)``), ``u`` the factor from :func:`inverse_factor`."""
+    return encode_jobs_gptq(
+        [GptqJob(w, d, u, nbits, block, perm)], effort, backend, comp
+    )[0]
+
+
+def encode_rows_gptq_reference(
+    w: torch.Tensor,
+    d: torch.Tensor,
+    u: torch.Tensor,
+    nbits: int,
+    block: int,
+    effort: str = "normal",
+    perm: torch.Tensor | None = None,
+) -> Encoded:
+    """The reference's per-block schedule (one cross-block update per 128 columns,
+    ``hi2/hessian.py:132-150``) on the same kernels; bit-identical to
+    :func:`encode_rows_gptq`, which batches the far-column updates."""
+    return encode_jobs_gptq(
+        [GptqJob(w, d, u, nbits, block, perm)], effort, comp=True, super_blocks=1
+    )[0]

@@ -1,0 +1,179 @@
+/*
+ * hi2x — MI355X (gfx950) encode path of the hi2 / rdna_hint_flex quantizer.
+ *
+ * C ABI of libhi2x.so.  Every buffer argument is a raw device pointer (the library
+ * borrows it for the duration of the call and never frees it); sizes are int64;
+ * `stream` is a hipStream_t passed as void*.  Calls are asynchronous on `stream`
+ * unless stated otherwise.  Every entry returns an int status:
+ *
+ *   HI2X_OK (0), HI2X_EINVAL (bad argument), HI2X_ENOTPD (matrix not positive
+ *   definite), HI2X_ELAUNCH (a HIP call failed), HI2X_ERANGE (a code outside the
+ *   ladder).  hi2x_last_error() returns the calling thread's last message.
+ *
+ * The library keeps no mutable global state (the last-error text is thread-local),
+ * so one host thread per device may call it concurrently.
+ *
+ * Reference interfaces are cited as path:line of BlivionIaG/hi2.
+ */
+#ifndef HI2X_H
+#define HI2X_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define HI2X_OK 0
+#define HI2X_EINVAL (-1)
+#define HI2X_ENOTPD (-2)
+#define HI2X_ELAUNCH (-3)
+#define HI2X_ERANGE (-4)
+
+#define HI2X_BLOCK_COLUMNS 128 /* GPTQ lazy block (hi2/hessian.py:20) */
+
+/* Library version (major*10000 + minor*100 + patch). */
+int hi2x_version(void);
+
+/* Last error message of the calling thread ("" if none). */
+const char* hi2x_last_error(void);
+
+/* ---- GPTQ ------------------------------------------------------------------------ */
+
+/* One lazy block of the GPTQ column loop for every row of a batch.
+ * Replaces the fused kernel launched by hi2/gptq_kernel.py:103-127 (`gptq_block`,
+ * Python entry hi2/gptq_kernel.py:187-196), same arguments and meaning:
+ *   wc [n, k] f32 (read only; columns in rounding order), err1 [n, len] f32 out,
+ *   codes [n, k] u8 out (rounding-order positions i1..i1+len), lo/st [n, ldp] f32
+ *   decoded block params, row_grp [n] i32 (sorted ascending), u_ptrs [G] i64 device
+ *   addresses of contiguous [k, k] f32 factors, blk [G, k] i32 block of each column,
+ *   nmax [G] f32 (codes - 1), comp [n, k] f32 out or NULL.
+ * Bit-exact to the reference column loop (hi2/hessian.py:248-261). */
+int hi2x_gptq_block(const float* wc, int64_t n, int64_t k, int64_t i1, int64_t len,
+                    float* err1, uint8_t* codes, const float* lo, const float* st,
+                    int64_t ldp, const int32_t* row_grp, const int64_t* u_ptrs,
+                    const int32_t* blk, const float* nmax, float* comp, void* stream);
+
+/* Cross-block update of hi2/hessian.py:310-312 for every row r (group g):
+ *   wc[r, c] -= err1[r, :len] @ U_g[i1:i1+len, c]   for c in [c0, c1)
+ * err1 [n, lde] f32.  Each product is a sequential fp32 FMA chain over the rank in
+ * order, then one subtraction: the rounding of the reference's BLAS call. */
+int hi2x_gptq_trailing(float* wc, int64_t n, int64_t k, int64_t i1, int64_t len,
+                       const float* err1, int64_t lde, int64_t c0, int64_t c1,
+                       const int32_t* row_grp, const int64_t* u_ptrs, void* stream);
+
+/* The whole column loop of _round_kernel (hi2/hessian.py:267-315): for every
+ * 128-column block, hi2x_gptq_block then the cross-block update, with the updates
+ * of `super_blocks` consecutive blocks applied to the far columns in one pass
+ * (each block's product still subtracted separately, in block order, so the result
+ * is bit-identical to the per-block schedule).  wc is modified in place.
+ * err_ws: device workspace of n * 128 * super_blocks floats. */
+int hi2x_gptq_run(float* wc, int64_t n, int64_t k, uint8_t* codes, const float* lo,
+                  const float* st, int64_t ldp, const int32_t* row_grp,
+                  const int64_t* u_ptrs, const int32_t* blk, const float* nmax,
+                  float* comp, float* err_ws, int64_t super_blocks, void* stream);
+
+/* ---- ladder fit and block parameters ---------------------------------------------- */
+
+/* fit_ladder (hi2/encode.py:53-92; grid part = ladder_grid_k, hi2/ladder_kernel.py:44-86):
+ * w [rows, k] f32 (stored basis, rows contiguous), d [k] f32 = diag(Hs), block B in
+ * {16,32,64}, nlev = 2^nbits, grid [g] f32, ls refits.  Outputs lo, step [rows, k/B].
+ * err (optional, [rows, k/B]) receives the best weighted error.  Sums follow the
+ * reference's torch CPU order, so results are bit-identical to hi2.encode.fit_ladder. */
+int hi2x_ladder_fit(const float* w, const float* d, int64_t rows, int64_t k, int64_t block,
+                    int nlev, const float* grid, int g, int ls, float* lo, float* step,
+                    float* err, void* stream);
+
+/* quantize_params + decode_params (hi2/encode.py:95-119, hi2/format.py:45-60):
+ * lo, step [rows, nb] -> lo_u8, step_u8 [rows, nb], consts [rows, 3] fp16 bits
+ * (lo_min, lo_scale, step_scale), lo_d, step_d [rows, ldd] f32 decoded values
+ * (ldd >= nb; padding untouched).  lo_d/step_d may be NULL. */
+int hi2x_params(const float* lo, const float* step, int64_t rows, int64_t nb,
+                uint8_t* lo_u8, uint8_t* step_u8, uint16_t* consts, float* lo_d,
+                float* step_d, int64_t ldd, void* stream);
+
+/* decode_params alone (hi2/format.py:45-60) on [rows, nb] bytes with per-row constants
+ * consts [rows, 3] fp16 bits; outputs fp16 bits lo_h, step_h [rows, nb]. */
+int hi2x_decode_params(const uint8_t* lo_u8, const uint8_t* step_u8, const uint16_t* consts,
+                       int64_t rows, int64_t nb, uint16_t* lo_h, uint16_t* step_h,
+                       void* stream);
+
+/* _finish (hi2/hessian.py:318-345): codes_ro/comp_ro [n, k] in rounding order ->
+ * codes/comp in column order (perm [k] i64 or NULL), sse [n] = sum_c d_c (rec - w)^2
+ * with rec = fp16(lo + code*step) in f32 and the sum in torch's CPU order.
+ * lo_d/step_d [n, ldd] f32, w [n, k] f32 original rows, d [k] f32. */
+int hi2x_finish(const uint8_t* codes_ro, const float* comp_ro, const int64_t* perm,
+                int64_t n, int64_t k, int64_t block, const float* lo_d, const float* step_d,
+                int64_t ldd, const float* w, const float* d, uint8_t* codes, float* comp,
+                float* sse, void* stream);
+
+/* ladder_dequantize (hi2/format.py:63-69): out_h [rows, nb*B] fp16 bits of
+ * lo + code*step evaluated in f32 (f64 when exact != 0), one rounding to fp16.
+ * lo/step [rows, nb] f32. */
+int hi2x_ladder_dequantize(const uint8_t* codes, const float* lo, const float* step,
+                           int64_t rows, int64_t nb, int64_t block, int exact,
+                           uint16_t* out_h, void* stream);
+
+/* ---- format ------------------------------------------------------------------------ */
+
+/* fwht_groups (hi2/format.py:30-41): flagged 16-column groups of x [rows, k] times
+ * the normalised order-16 Hadamard (an involution).  dtype: 0 = f32, 1 = f64 (in and
+ * out share the dtype; sums in the reference matmul's sequential order). */
+int hi2x_fwht16(const void* x, void* y, int dtype, int64_t rows, int64_t k,
+                const uint8_t* flags, void* stream);
+
+/* pack_codes (hi2/format.py:73-85): codes [rows, k] u8 -> words [rows, k*nbits/32]
+ * i32, LSB first.  bad: device i32 counter incremented per code >= 2^nbits (the
+ * caller raises ValueError when nonzero). */
+int hi2x_pack_codes(const uint8_t* codes, int64_t rows, int64_t k, int nbits,
+                    int32_t* words, int32_t* bad, void* stream);
+
+/* One piece of assemble (hi2/format.py:155-171): rows [r] i64 tensor-row indices,
+ * codes [r, k] u8, params [r, k/block, 2] u8, consts [r, 3] fp16 bits scattered into
+ * the flat buffers out_codes (i32 words at code_off[row]), out_params (2 bytes per
+ * block at param_off[row]), out_consts [R, 3].  code_off/param_off are i64 device
+ * arrays.  bad as in hi2x_pack_codes. */
+int hi2x_assemble_piece(const int64_t* rows, int64_t r, const uint8_t* codes,
+                        const uint8_t* params, const uint16_t* consts, int64_t k, int nbits,
+                        int64_t block, const int64_t* code_off, const int64_t* param_off,
+                        int32_t* out_codes, uint8_t* out_params, uint16_t* out_consts,
+                        int32_t* bad, void* stream);
+
+/* ---- Hessian ------------------------------------------------------------------------ */
+
+/* HessianStats.update (hi2/hessian.py:35-40): s [k, k] f32 += x^T x over t rows of
+ * x [t, k] (dtype 0 = f32, 2 = bf16).  bf16 runs on bf16 MFMA with f32 accumulation
+ * (products exact); f32 on f32 MFMA.  The result is exactly symmetric. */
+int hi2x_hessian_syrk(const void* x, int dtype, int64_t t, int64_t k, float* s,
+                      void* stream);
+
+/* Variable-length batch of the above (routed MoE tokens, hi2/moe.py:83-100):
+ * group e accumulates rows [offs[e], offs[e+1]) of x into s_ptrs[e] ([k, k] f32).
+ * offs is a host array of n_groups + 1 row offsets; s_ptrs a host array. */
+int hi2x_hessian_syrk_varlen(const void* x, int dtype, const int64_t* offs,
+                             int64_t n_groups, int64_t k, float* const* s_ptrs,
+                             void* stream);
+
+/* transform_sigma (hi2/hessian.py:50-68): hs [k, k] f32 = sym(M diag(1/s) sigma
+ * diag(1/s) M^T) with M block-diagonal (H16/4 on flagged groups, I elsewhere).
+ * col_scale: fp16 bits [k] or NULL; had [k/16] u8.  Bit-identical to the reference's
+ * fp32 einsum order. */
+int hi2x_sigma_transform(const float* sigma, const uint16_t* col_scale, const uint8_t* had,
+                         int64_t k, float* hs, void* stream);
+
+/* ---- Cholesky chain ------------------------------------------------------------------ */
+
+/* One attempt of inverse_factor (hi2/hessian.py:71-86): with lam = damp * mean(diag hs)
+ * (clamped at 1e-12) * 10^attempt, writes u [k, k] f32 = the upper Cholesky factor of
+ * (hs + lam I)^-1 (lower triangle zero).  Computed as U = (J chol(J (hs + lam I) J) J)^-1
+ * (J = reversal), the same matrix as the reference's chol -> cholesky_inverse ->
+ * chol(upper) chain.  Synchronises `stream`; returns HI2X_ENOTPD when the damped matrix
+ * is not numerically positive definite (the caller retries with attempt + 1). */
+int hi2x_chol_inv_upper(const float* hs, int64_t k, float damp, int attempt, float* u,
+                        void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* HI2X_H */

@@ -1,0 +1,286 @@
+"""CPU oracle of the hi2 encode path — TEST INFRASTRUCTURE ONLY.
+
+Only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s ``cpu_baseline`` leg
+import this package, and only as the checker / CPU baseline.  The product package
+(``hi2_amd``) never imports, links or calls it.
+
+``libhi2_oracle.so`` is the plain-C restatement in ``hi2_oracle.c`` (each function
+cites the reference lines it follows); this module wraps it with numpy and composes
+the per-tensor flow of the reference's ``encode_rows_gptq_reference``
+(``hi2/hessian.py:89-175``): ladder fit -> 8-bit params -> decode -> GPTQ column loop
+-> finish.
+
+Pinning (what holds each function to the reference):
+
+* ``f32_to_f16``: numpy's IEEE round-to-nearest-even ``astype(float16)``.
+* ``fwht16``: closed form (Sylvester H16 / 4, involution, float64 matmul).
+* ``fit_ladder``: golden vectors of the reference (``tests/golden/fit_ladder.npz``).
+* ``params`` (quantize/decode): closed forms of ``hi2/encode.py:95-119`` and
+  ``hi2/format.py:45-60`` evaluated independently with numpy, plus the reference's
+  constant/zero-block KAT, plus the params inside the GPTQ golden vectors.
+* ``gptq_rows`` / ``gptq_block`` / ``finish``: GPTQ golden vectors
+  (``tests/golden/gptq_int*.npz``), the diagonal-Hessian special case (nearest
+  rounding) and H-error decrease.
+* ``hessian_update``: float64 brute force ``X^T X``.
+* ``transform_sigma``: covariance of the transformed activation.
+* ``inverse_factor``: golden vectors (``tests/golden/inverse_factor.npz``) and
+  ``U^T U (Hs + lam I) = I``.
+* ``pack_codes`` / ``assemble_piece``: LSB-first KATs and the mixed-row offsets KAT.
+"""
+
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB = os.path.join(_HERE, "libhi2_oracle.so")
+_lib = None
+
+EFFORT = {
+    "fast": dict(grid=(0.0, 0.06, 0.12), ls=1),
+    "normal": dict(grid=(0.0, 0.04, 0.08, 0.12, 0.16, 0.20), ls=2),
+    "max": dict(grid=(0.0, 0.025, 0.05, 0.075, 0.10, 0.125, 0.15, 0.20), ls=4),
+}
+
+
+def build(force: bool = False) -> str:
+    if force or not os.path.exists(_LIB) or (
+        os.path.getmtime(_LIB) < os.path.getmtime(os.path.join(_HERE, "hi2_oracle.c"))
+    ):
+        subprocess.run(["make", "-s", "-C", _HERE, "-B" if force else "-s"], check=True)
+    return _LIB
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(_LIB):
+            build()
+        _lib = ctypes.CDLL(_LIB)
+        P = ctypes.c_void_p
+        I64 = ctypes.c_int64
+        I = ctypes.c_int
+        F = ctypes.c_float
+        sig = {
+            "or_f32_to_f16": (ctypes.c_uint16, [F]),
+            "or_f16_to_f32": (F, [ctypes.c_uint16]),
+            "or_fwht16": (None, [P, P, I64, I64, P]),
+            "or_fit_ladder": (None, [P, P, I64, I64, I, I, P, I, I, P, P]),
+            "or_params": (None, [P, P, I64, I64, P, P, P, P, P]),
+            "or_gptq_rows": (None, [P, I64, I64, P, P, P, I64, P, I, P, P]),
+            "or_gptq_block": (None, [P, I64, I64, I64, I, P, P, P, P, I64, P, P, P, P, P]),
+            "or_finish": (None, [P, P, P, I64, I64, I64, P, P, P, P, P, P, P]),
+            "or_hessian_update": (None, [P, I, I64, I64, P]),
+            "or_transform_sigma": (None, [P, P, P, I64, P]),
+            "or_inverse_factor": (I, [P, I64, F, P]),
+            "or_pack_codes": (I64, [P, I64, I64, I, P]),
+            "or_assemble_piece": (I64, [P, I64, P, P, P, I64, I, I64, P, P, P, P, P]),
+        }
+        for name, (res, args) in sig.items():
+            fn = getattr(_lib, name)
+            fn.restype = res
+            fn.argtypes = args
+    return _lib
+
+
+def _p(a):
+    return None if a is None else a.ctypes.data_as(ctypes.c_void_p)
+
+
+def _c(a, dtype):
+    return np.ascontiguousarray(a, dtype=dtype)
+
+
+def f32_to_f16_bits(x):
+    x = np.atleast_1d(_c(x, np.float32))
+    return np.array([lib().or_f32_to_f16(float(v)) for v in x.ravel()], np.uint16).reshape(x.shape)
+
+
+def fwht16(x, flags):
+    x = _c(x, np.float32)
+    k = x.shape[-1]
+    if k % 16:
+        raise ValueError(f"K={k} must be a multiple of 16")
+    flags = _c(flags, np.uint8).reshape(-1)
+    if flags.size != k // 16:
+        raise ValueError("flag count")
+    y = np.empty_like(x)
+    lib().or_fwht16(_p(x), _p(y), x.size // k, k, _p(flags))
+    return y
+
+
+def fit_ladder(wb, db, n, effort="normal"):
+    """``hi2/encode.py:53-92``: wb [N, nb, B], db broadcastable to [nb, B]."""
+    wb = _c(wb, np.float32)
+    rows, nb, b = wb.shape
+    db = _c(np.broadcast_to(np.asarray(db, np.float32).reshape(-1, nb, b)[0], (nb, b)), np.float32)
+    cfg = EFFORT[effort]
+    grid = np.array(cfg["grid"], np.float32)
+    lo = np.empty((rows, nb), np.float32)
+    st = np.empty((rows, nb), np.float32)
+    lib().or_fit_ladder(_p(wb), _p(db), rows, nb, b, int(n), _p(grid), grid.size,
+                        cfg["ls"], _p(lo), _p(st))
+    return lo, st
+
+
+def params(lo, step):
+    """quantize_params + decode_params: returns lo_u8, step_u8, consts (fp16 bits
+    [N, 3]), lo_d, step_d (fp32)."""
+    lo = _c(lo, np.float32)
+    step = _c(step, np.float32)
+    rows, nb = lo.shape
+    lo_u8 = np.empty((rows, nb), np.uint8)
+    st_u8 = np.empty((rows, nb), np.uint8)
+    consts = np.empty((rows, 3), np.uint16)
+    lo_d = np.empty((rows, nb), np.float32)
+    st_d = np.empty((rows, nb), np.float32)
+    lib().or_params(_p(lo), _p(step), rows, nb, _p(lo_u8), _p(st_u8), _p(consts),
+                    _p(lo_d), _p(st_d))
+    return lo_u8, st_u8, consts, lo_d, st_d
+
+
+def gptq_rows(wc, u, lo_d, step_d, blk_of, nbits, want_comp=True):
+    wc = _c(wc, np.float32).copy()
+    n, k = wc.shape
+    u = _c(u, np.float32)
+    lo_d = _c(lo_d, np.float32)
+    step_d = _c(step_d, np.float32)
+    blk_of = _c(blk_of, np.int64)
+    codes = np.zeros((n, k), np.uint8)
+    comp = np.zeros((n, k), np.float32) if want_comp else None
+    lib().or_gptq_rows(_p(wc), n, k, _p(u), _p(lo_d), _p(step_d), lo_d.shape[1],
+                       _p(blk_of), 2 ** int(nbits), _p(codes), _p(comp))
+    return codes, comp
+
+
+def gptq_block(wc, i1, length, lo, st, row_grp, us, blk, nmax, want_comp=True):
+    """The one-block contract of ``hi2/gptq_kernel.py:59-101``."""
+    wc = _c(wc, np.float32)
+    n, k = wc.shape
+    lo = _c(lo, np.float32)
+    st = _c(st, np.float32)
+    row_grp = _c(row_grp, np.int32)
+    us = [_c(u, np.float32) for u in us]
+    ptrs = (ctypes.c_void_p * len(us))(*[u.ctypes.data for u in us])
+    blk = _c(blk, np.int32)
+    nmax = _c(nmax, np.float32)
+    err1 = np.zeros((n, length), np.float32)
+    codes = np.zeros((n, k), np.uint8)
+    comp = np.zeros((n, k), np.float32) if want_comp else None
+    lib().or_gptq_block(_p(wc), n, k, int(i1), int(length), _p(err1), _p(codes), _p(lo),
+                        _p(st), lo.shape[1], _p(row_grp), ctypes.cast(ptrs, ctypes.c_void_p),
+                        _p(blk), _p(nmax), _p(comp))
+    return err1, codes, comp
+
+
+def finish(codes_ro, comp_ro, perm, block, lo_d, step_d, w, d):
+    codes_ro = _c(codes_ro, np.uint8)
+    n, k = codes_ro.shape
+    comp_ro = None if comp_ro is None else _c(comp_ro, np.float32)
+    perm = None if perm is None else _c(perm, np.int64)
+    codes = np.zeros((n, k), np.uint8)
+    comp = None if comp_ro is None else np.zeros((n, k), np.float32)
+    sse = np.zeros(n, np.float32)
+    lib().or_finish(_p(codes_ro), _p(comp_ro), _p(perm), n, k, int(block),
+                    _p(_c(lo_d, np.float32)), _p(_c(step_d, np.float32)),
+                    _p(_c(w, np.float32)), _p(_c(d, np.float32)), _p(codes), _p(comp), _p(sse))
+    return codes, comp, sse
+
+
+def encode_rows_gptq(w, d, u, nbits, block, effort="normal", perm=None, comp=True):
+    """The reference flow of ``encode_rows_gptq_reference`` (``hi2/hessian.py:89-175``)
+    on numpy arrays.  Returns dict(codes, params, consts (fp16 bits), sse, comp)."""
+    w = _c(w, np.float32)
+    n, k = w.shape
+    d = _c(d, np.float32).reshape(-1)
+    nb = k // block
+    lo, st = fit_ladder(w.reshape(n, nb, block), d.reshape(1, nb, block), 2 ** nbits, effort)
+    lo_u8, st_u8, consts, lo_d, st_d = params(lo, st)
+    if perm is not None:
+        perm = _c(perm, np.int64)
+        wc = w[:, perm]
+        blk_of = perm // block
+    else:
+        wc = w
+        blk_of = np.arange(k, dtype=np.int64) // block
+    codes_ro, comp_ro = gptq_rows(wc, u, lo_d, st_d, blk_of, nbits, comp)
+    codes, compo, sse = finish(codes_ro, comp_ro, perm, block, lo_d, st_d, w, d)
+    return dict(codes=codes, params=np.stack([lo_u8, st_u8], -1), consts=consts, sse=sse,
+                comp=compo, lo_d=lo_d, step_d=st_d)
+
+
+def hessian_update(s, x):
+    """S += X^T X; x is float32 or bf16 given as uint16 bits."""
+    s = _c(s, np.float32)
+    x = np.ascontiguousarray(x)
+    is_bf16 = x.dtype == np.uint16
+    if not is_bf16:
+        x = _c(x, np.float32)
+    t, k = x.shape
+    lib().or_hessian_update(_p(x), int(is_bf16), t, k, _p(s))
+    return s
+
+
+def transform_sigma(sigma, col_scale_bits, had):
+    sigma = _c(sigma, np.float32)
+    k = sigma.shape[0]
+    out = np.empty_like(sigma)
+    cs = None if col_scale_bits is None else _c(col_scale_bits, np.uint16)
+    lib().or_transform_sigma(_p(sigma), _p(cs), _p(_c(had, np.uint8)), k, _p(out))
+    return out
+
+
+def inverse_factor(hs, damp=0.01):
+    """Returns (U, attempt); raises RuntimeError when every attempt fails."""
+    hs = _c(hs, np.float32)
+    k = hs.shape[0]
+    u = np.zeros_like(hs)
+    att = lib().or_inverse_factor(_p(hs), k, float(damp), _p(u))
+    if att < 0:
+        raise RuntimeError("Hessian is not factorisable even with heavy damping")
+    return u, att
+
+
+def pack_codes(codes, nbits):
+    codes = _c(codes, np.uint8)
+    k = codes.shape[-1]
+    per = 32 // nbits
+    if k % per:
+        raise ValueError(f"{k} codes is not a multiple of {per}")
+    rows = codes.size // k
+    out = np.empty((rows, k // per), np.int32)
+    bad = lib().or_pack_codes(_p(codes), rows, k, int(nbits), _p(out))
+    if bad:
+        raise ValueError("code outside the ladder")
+    return out.reshape(*codes.shape[:-1], k // per)
+
+
+def assemble(pieces, row_nbits, row_block, k):
+    """Flat buffers of ``hi2/format.py:127-184`` from (rows, codes, params, consts
+    fp16 bits) pieces."""
+    row_nbits = np.asarray(row_nbits, np.int64)
+    row_block = np.asarray(row_block, np.int64)
+    r = row_nbits.size
+    words = (k * row_nbits) // 32
+    blocks = k // row_block
+    code_off = np.zeros(r + 1, np.int64)
+    code_off[1:] = np.cumsum(words)
+    param_off = np.zeros(r + 1, np.int64)
+    param_off[1:] = np.cumsum(blocks)
+    codes = np.zeros(int(code_off[-1]), np.int32)
+    params_ = np.zeros(int(param_off[-1]) * 2, np.uint8)
+    consts = np.zeros((r, 3), np.uint16)
+    for rows, c, p, rc in pieces:
+        rows = _c(rows, np.int64)
+        nbits = int(row_nbits[rows[0]])
+        blk = int(row_block[rows[0]])
+        bad = lib().or_assemble_piece(_p(rows), rows.size, _p(_c(c, np.uint8)),
+                                      _p(_c(p, np.uint8)), _p(_c(rc, np.uint16)), k, nbits,
+                                      blk, _p(code_off), _p(param_off), _p(codes), _p(params_),
+                                      _p(consts))
+        if bad:
+            raise ValueError("code outside the ladder")
+    return dict(codes=codes, code_off=code_off.astype(np.int32), blk_params=params_,
+                param_off=param_off.astype(np.int32), row_consts=consts)

@@ -1,0 +1,142 @@
+"""Write the golden vectors that pin the oracle where closed forms cannot.
+
+This script imports the reference package from ``/root/reference`` (read-only) in the
+build container and records inputs and outputs of the three functions whose exact bits
+depend on the reference's own torch-CPU arithmetic:
+
+* ``hi2.hessian.inverse_factor`` (LAPACK ``cholesky`` -> ``cholesky_inverse`` ->
+  ``cholesky(upper)`` with the damping retry, ``hi2/hessian.py:71-86``);
+* ``hi2.encode.fit_ladder`` (grid search + weighted LSQ refits on torch reductions,
+  ``hi2/encode.py:53-92``);
+* ``hi2.hessian.encode_rows_gptq_reference`` (the verbatim column loop with the BLAS
+  trailing update, ``hi2/hessian.py:89-175``), on the inputs of the reference's own
+  ``tests/test_gptq_fast.py:19-36`` ``_layer`` recipe.
+
+The fixtures are plain ``.npz`` data (inputs and expected outputs); nothing of the
+reference is stored.  Run from the repository root:
+
+    python tests/golden/make_golden.py
+"""
+
+import os
+import sys
+
+import numpy as np
+import torch
+
+REF = os.environ.get("HI2_REFERENCE", "/root/reference")
+OUT = os.path.dirname(os.path.abspath(__file__))
+
+CASES = [(2, 16), (2, 32), (2, 64), (4, 16), (4, 32), (4, 64), (8, 32), (8, 64)]
+
+
+def _layer(rows, k, seed, act_order, inverse_factor):
+    # same recipe as the reference's tests/test_gptq_fast.py:19-36
+    g = torch.Generator().manual_seed(seed)
+    mix = torch.randn(k, k, generator=g) * 0.1 + torch.eye(k)
+    x = torch.randn(4 * k, k, generator=g) @ mix
+    x *= torch.exp(0.5 * torch.randn(1, k, generator=g))
+    hs = x.T @ x / x.shape[0]
+    w = torch.randn(rows, k, generator=g) * torch.exp(
+        0.4 * torch.randn(rows, 1, generator=g)
+    )
+    w[:, :: max(1, k // 5)] *= 8
+    d = hs.diagonal().clone()
+    perm = None
+    if act_order:
+        perm = torch.argsort(d, descending=True)
+        hs = hs[perm][:, perm]
+    u = inverse_factor(hs, 0.01)
+    return w, d, u, perm, hs
+
+
+def _correlated(t, k, seed):
+    # reference tests/test_hessian.py:18-23
+    g = torch.Generator().manual_seed(seed)
+    mix = torch.randn(k, k, generator=g) * 0.15 + torch.eye(k)
+    x = torch.randn(t, k, generator=g) @ mix
+    x *= torch.exp(0.5 * torch.randn(1, k, generator=g))
+    return x
+
+
+def main():
+    sys.path.insert(0, REF)
+    from hi2.encode import EFFORT, fit_ladder
+    from hi2.hessian import encode_rows_gptq_reference, inverse_factor
+
+    torch.set_num_threads(1)
+    meta = dict(torch=torch.__version__, threads=1)
+
+    # ---- GPTQ end to end (codes/params/consts/sse/comp) ------------------------
+    for nbits in (2, 4, 8):
+        arrs = {}
+        for (nb, b) in CASES:
+            if nb != nbits:
+                continue
+            for ao in (False, True):
+                for effort in ("fast", "normal"):
+                    if effort == "normal" and ao:
+                        continue
+                    seed = nb * 100 + b + (7 if effort == "normal" else 0)
+                    w, d, u, perm, _ = _layer(24, 192, seed, ao, inverse_factor)
+                    enc = encode_rows_gptq_reference(w, d, u, nb, b, effort, perm)
+                    tag = f"b{b}_ao{int(ao)}_{effort}"
+                    arrs[f"{tag}_w"] = w.numpy()
+                    arrs[f"{tag}_d"] = d.numpy()
+                    arrs[f"{tag}_u"] = u.numpy()
+                    arrs[f"{tag}_perm"] = (
+                        perm.numpy().astype(np.int64)
+                        if perm is not None
+                        else np.zeros(0, np.int64)
+                    )
+                    arrs[f"{tag}_codes"] = enc.codes.numpy()
+                    arrs[f"{tag}_params"] = enc.params.numpy()
+                    arrs[f"{tag}_consts"] = enc.consts.view(torch.int16).numpy()
+                    arrs[f"{tag}_sse"] = enc.sse.numpy()
+                    arrs[f"{tag}_comp"] = enc.comp.numpy()
+        np.savez_compressed(os.path.join(OUT, f"gptq_int{nbits}.npz"), **arrs)
+
+    # ---- inverse_factor ---------------------------------------------------------
+    arrs = {}
+    for k, t, seed in ((32, 500, 0), (64, 1000, 1), (200, 4000, 2)):
+        x = _correlated(t, k, seed)
+        hs = x.T @ x / t
+        arrs[f"k{k}_hs"] = hs.numpy()
+        arrs[f"k{k}_u"] = inverse_factor(hs, 0.01).numpy()
+    sing = torch.zeros(16, 16)
+    sing[0, 0] = 1.0
+    arrs["singular_hs"] = sing.numpy()
+    arrs["singular_u"] = inverse_factor(sing, 0.01).numpy()
+    # indefinite: the first attempts fail, a later damping succeeds
+    ind = torch.eye(16)
+    ind[15, 15] = -0.2
+    arrs["indef_hs"] = ind.numpy()
+    arrs["indef_u"] = inverse_factor(ind, 0.01).numpy()
+    np.savez_compressed(os.path.join(OUT, "inverse_factor.npz"), **arrs)
+
+    # ---- fit_ladder -----------------------------------------------------------------
+    arrs = {}
+    g = torch.Generator().manual_seed(11)
+    for n, b, effort in ((4, 16, "normal"), (16, 64, "normal"), (4, 32, "fast"),
+                         (16, 32, "max"), (256, 64, "normal")):
+        wb = torch.randn(48, 6, b, generator=g) * torch.exp(
+            0.5 * torch.randn(48, 6, 1, generator=g)
+        )
+        wb[:, :, :: max(1, b // 5)] *= 4
+        db = torch.rand(1, 6, b, generator=g) + 0.25
+        lo, step = fit_ladder(wb, db, n, effort)
+        tag = f"n{n}_b{b}_{effort}"
+        arrs[f"{tag}_wb"] = wb.numpy()
+        arrs[f"{tag}_db"] = db.numpy()
+        arrs[f"{tag}_lo"] = lo.numpy()
+        arrs[f"{tag}_step"] = step.numpy()
+    arrs["effort_normal_grid"] = np.array(EFFORT["normal"]["grid"], np.float64)
+    np.savez_compressed(os.path.join(OUT, "fit_ladder.npz"), **arrs)
+
+    with open(os.path.join(OUT, "golden_meta.txt"), "w") as f:
+        for k, v in meta.items():
+            f.write(f"{k}={v}\n")
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,38 @@
+"""Loaders for the reference's golden vectors in tests/golden (written by
+tests/golden/make_golden.py from the reference's own functions)."""
+
+import os
+
+import numpy as np
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+CASES = [(2, 16), (2, 32), (2, 64), (4, 16), (4, 32), (4, 64), (8, 32), (8, 64)]
+
+
+def gptq_cases():
+    """Yields (nbits, block, effort, act_order, dict of arrays)."""
+    for nbits in (2, 4, 8):
+        g = np.load(os.path.join(GOLDEN, f"gptq_int{nbits}.npz"))
+        tags = sorted({k.rsplit("_", 1)[0] for k in g.files})
+        for tag in tags:
+            b, ao, effort = tag.split("_")
+            arr = {f: g[f"{tag}_{f}"] for f in ("w", "d", "u", "perm", "codes", "params",
+                                                "consts", "sse", "comp")}
+            if arr["perm"].size == 0:
+                arr["perm"] = None
+            yield nbits, int(b[1:]), effort, ao == "ao1", arr
+
+
+def fit_cases():
+    g = np.load(os.path.join(GOLDEN, "fit_ladder.npz"))
+    tags = sorted({k.rsplit("_", 1)[0] for k in g.files if not k.startswith("effort")})
+    for tag in tags:
+        n, b, effort = tag.split("_")
+        yield int(n[1:]), int(b[1:]), effort, {f: g[f"{tag}_{f}"] for f in ("wb", "db", "lo", "step")}
+
+
+def inverse_cases():
+    g = np.load(os.path.join(GOLDEN, "inverse_factor.npz"))
+    tags = sorted({k.rsplit("_", 1)[0] for k in g.files})
+    for tag in tags:
+        yield tag, g[f"{tag}_hs"], g[f"{tag}_u"]

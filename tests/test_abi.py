@@ -1,0 +1,103 @@
+"""The C ABI library loads and exports every entry point include/hi2x.h declares, and
+the Python mirror keeps the reference's call surface — CPU only (no compute calls)."""
+
+import ctypes
+import os
+import re
+
+import pytest
+import torch
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def _declared():
+    src = open(os.path.join(ROOT, "include", "hi2x.h")).read()
+    src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
+    return sorted(set(re.findall(r"\b(hi2x_\w+)\s*\(", src)))
+
+
+def test_library_exports_every_declared_symbol():
+    from hi2_amd import _lib
+
+    lib = _lib.lib()
+    names = _declared()
+    assert len(names) >= 15
+    for name in names:
+        assert hasattr(lib, name), name
+    assert lib.hi2x_version() >= 100
+    assert set(_lib.SIGNATURES) | {"hi2x_version", "hi2x_last_error"} == set(names)
+
+
+def test_raw_symbols_resolve_without_ctypes_wrappers():
+    from hi2_amd import _lib
+
+    raw = ctypes.CDLL(_lib.LIB_PATH)
+    for name in _declared():
+        assert ctypes.cast(getattr(raw, name), ctypes.c_void_p).value
+
+
+def test_argument_errors_come_back_as_status_without_a_gpu():
+    # argument checks run before any HIP call, so they work on a host without a GPU
+    from hi2_amd import _lib
+
+    lib = _lib.lib()
+    rc = lib.hi2x_gptq_block(None, 4, 64, 0, 200, None, None, None, None, 4, None, None,
+                             None, None, None, None)
+    assert rc == _lib.EINVAL and "block length" in _lib.last_error()
+    rc = lib.hi2x_fwht16(None, None, 0, 1, 24, None, None)
+    assert rc == _lib.EINVAL and "multiple of 16" in _lib.last_error()
+    rc = lib.hi2x_pack_codes(None, 1, 30, 4, None, None, None)
+    assert rc == _lib.EINVAL
+    with pytest.raises(ValueError):
+        _lib.check(_lib.ERANGE, "x")
+    with pytest.raises(_lib.NotPositiveDefinite):
+        _lib.check(_lib.ENOTPD, "x")
+
+
+def test_python_surface_matches_the_reference_modules():
+    import hi2_amd.encode as enc
+    import hi2_amd.format as fmt
+    import hi2_amd.gptq_kernel as gk
+    import hi2_amd.hessian as hs
+    import hi2_amd.ladder_kernel as lk
+
+    for name in ("BLOCK_COLUMNS", "kernel_dir", "supported", "load", "available", "failure",
+                 "gptq_block"):
+        assert hasattr(gk, name), name
+    for name in ("BLOCK_COLUMNS", "ROW_ELEMS", "BATCH_ELEMS", "HessianStats", "transform_sigma",
+                 "inverse_factor", "GptqJob", "encode_jobs_gptq", "encode_rows_gptq",
+                 "encode_rows_gptq_reference", "EFFORT", "Encoded"):
+        assert hasattr(hs, name), name
+    for name in ("EFFORT", "CHUNK_ELEMS", "_safe", "fit_ladder", "quantize_params", "Encoded",
+                 "encode_rows"):
+        assert hasattr(enc, name), name
+    for name in ("ladder_grid", "available", "load", "failure", "supported"):
+        assert hasattr(lk, name), name
+    for name in ("GROUP", "hadamard16", "fwht_groups", "decode_params", "ladder_dequantize",
+                 "pack_codes", "HI2Tensor", "FIELDS", "assemble"):
+        assert hasattr(fmt, name), name
+    assert hs.BLOCK_COLUMNS == gk.BLOCK_COLUMNS == 128
+    assert enc.EFFORT["normal"]["grid"] == (0.0, 0.04, 0.08, 0.12, 0.16, 0.20)
+
+
+def test_cpu_tensors_are_refused_not_computed():
+    import hi2_amd.format as fmt
+    import hi2_amd.hessian as hs
+
+    with pytest.raises(RuntimeError, match="MI355X"):
+        fmt.fwht_groups(torch.zeros(2, 32), torch.ones(2, dtype=torch.uint8))
+    with pytest.raises(RuntimeError):
+        hs.HessianStats(16, "cpu")
+    with pytest.raises(RuntimeError, match="MI355X"):
+        hs.encode_rows_gptq(torch.zeros(4, 32), torch.ones(32), torch.eye(32), 2, 16)
+    with pytest.raises(ValueError):
+        fmt.fwht_groups(torch.zeros(2, 24), torch.ones(1))
+
+
+def test_hadamard16_constant():
+    import hi2_amd.format as fmt
+
+    h = fmt.hadamard16()
+    assert torch.allclose(h @ h, torch.eye(16, dtype=torch.float64))
+    assert torch.equal(h, h.T)

@@ -1,0 +1,382 @@
+"""The HIP path against the oracle and the reference's golden vectors (MI355X).
+
+Bit-exact wherever the reference's arithmetic is a fixed sequence of IEEE operations
+(ladder fit, params, column loop and its MFMA cross-block update, finish, Hadamard,
+transform_sigma, packing); tolerance for the Hessian GEMM and the Cholesky chain,
+whose reference rounding comes from BLAS/LAPACK blocking (rtol stated per test)."""
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from golden_data import CASES, fit_cases, gptq_cases, inverse_cases
+
+pytestmark = pytest.mark.gpu
+
+
+def T(a, dev, dtype=None):
+    t = torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+    return t if dtype is None else t.to(dtype)
+
+
+def N(t):
+    return t.detach().cpu().numpy()
+
+
+def _same(got, want: dict):
+    assert np.array_equal(N(got.codes), want["codes"]), "codes"
+    assert np.array_equal(N(got.params), want["params"]), "params"
+    assert np.array_equal(N(got.consts).view(np.int16), want["consts"].view(np.int16)), "consts"
+    assert np.array_equal(N(got.sse), want["sse"]), "sse"
+    if want.get("comp") is not None:
+        assert got.comp is not None
+        assert np.array_equal(N(got.comp), want["comp"]), "comp"
+
+
+def _layer(rows, k, seed, act_order=False):
+    """Seeded layer like the reference's tests/test_gptq_fast.py:19-36 (numpy RNG),
+    with the factor from the oracle (the same U goes to both sides)."""
+    rng = np.random.default_rng(seed)
+    mix = rng.standard_normal((k, k)) * 0.1 + np.eye(k)
+    x = rng.standard_normal((4 * k, k)) @ mix
+    x *= np.exp(0.5 * rng.standard_normal((1, k)))
+    hs = (x.T @ x / x.shape[0]).astype(np.float32)
+    w = (rng.standard_normal((rows, k)) * np.exp(0.4 * rng.standard_normal((rows, 1)))).astype(np.float32)
+    w[:, :: max(1, k // 5)] *= 8
+    d = np.diag(hs).copy()
+    perm = None
+    if act_order:
+        perm = np.argsort(-d, kind="stable")
+        hs = hs[perm][:, perm]
+    u, _ = oracle.inverse_factor(hs, 0.01)
+    return w, d, u, perm, hs
+
+
+# ---- the reference's golden vectors ---------------------------------------------------
+@pytest.mark.parametrize(
+    "case", list(gptq_cases()), ids=lambda c: f"int{c[0]}_b{c[1]}_{c[2]}_ao{int(c[3])}"
+)
+@pytest.mark.parametrize("schedule", ["batched", "per_block"])
+def test_gptq_equals_reference_golden(dev, case, schedule):
+    from hi2_amd.hessian import encode_rows_gptq, encode_rows_gptq_reference
+
+    nbits, block, effort, _, a = case
+    perm = None if a["perm"] is None else T(a["perm"], dev)
+    fn = encode_rows_gptq if schedule == "batched" else encode_rows_gptq_reference
+    got = fn(T(a["w"], dev), T(a["d"], dev), T(a["u"], dev), nbits, block, effort, perm)
+    _same(got, a)
+
+
+@pytest.mark.parametrize("case", list(fit_cases()), ids=lambda c: f"n{c[0]}_b{c[1]}_{c[2]}")
+def test_fit_ladder_equals_reference_golden(dev, case):
+    from hi2_amd.encode import fit_ladder
+
+    n, b, effort, a = case
+    lo, st = fit_ladder(T(a["wb"], dev), T(a["db"], dev), n, effort)
+    assert np.array_equal(N(lo), a["lo"]) and np.array_equal(N(st), a["step"])
+
+
+@pytest.mark.parametrize("case", list(inverse_cases()), ids=lambda c: c[0])
+def test_inverse_factor_matches_reference_golden(dev, case):
+    from hi2_amd.hessian import inverse_factor
+
+    _, hs, u_ref = case
+    u = N(inverse_factor(T(hs, dev), 0.01))
+    assert np.array_equal(np.tril(u, -1), np.zeros_like(u))
+    scale = np.abs(u_ref).max()
+    # fp32 factorisations in different orders: agreement to the conditioning allows
+    assert np.allclose(u, u_ref, rtol=1e-3, atol=1e-4 * scale), np.abs(u - u_ref).max() / scale
+
+
+# ---- the column loop ------------------------------------------------------------------
+@pytest.mark.parametrize("nbits,block", CASES)
+@pytest.mark.parametrize("act_order", [False, True])
+@pytest.mark.parametrize("k", [192, 448])  # last block shorter than 128
+def test_gptq_equals_oracle(dev, nbits, block, act_order, k):
+    from hi2_amd.hessian import encode_rows_gptq
+
+    w, d, u, perm, _ = _layer(200, k, nbits * 7 + block + k, act_order)
+    want = oracle.encode_rows_gptq(w, d, u, nbits, block, "fast", perm)
+    got = encode_rows_gptq(T(w, dev), T(d, dev), T(u, dev), nbits, block, "fast",
+                           None if perm is None else T(perm, dev))
+    _same(got, want)
+
+
+def test_gptq_block_one_launch_equals_oracle(dev):
+    """hi2x_gptq_block alone (the gptq_kernel.gptq_block contract), three row groups
+    with different factors, column maps and code counts, a 96-column last block."""
+    from hi2_amd import gptq_kernel
+
+    rng = np.random.default_rng(7)
+    k, i1, length = 224, 128, 96
+    sizes = [37, 64, 70]
+    n = sum(sizes)
+    us, blks, nmax = [], [], []
+    for g, nb in enumerate((4, 16, 256)):
+        _, _, u, perm, _ = _layer(4, k, 100 + g, act_order=g == 1)
+        us.append(u)
+        blks.append((np.arange(k) if perm is None else perm) // 32)
+        nmax.append(nb - 1)
+    wc = (rng.standard_normal((n, k)) * 0.3).astype(np.float32)
+    ldp = k // 16
+    lo = (rng.standard_normal((n, ldp)) * 0.2 - 0.5).astype(np.float32)
+    st = (rng.random((n, ldp)) * 0.1).astype(np.float32)
+    st[5, 4] = 0.0
+    row_grp = np.repeat(np.arange(3), sizes).astype(np.int32)
+    blk = np.stack(blks).astype(np.int32)
+    nm = np.array(nmax, np.float32)
+    err_w, codes_w, comp_w = oracle.gptq_block(wc, i1, length, lo, st, row_grp, us, blk, nm)
+    ut = [T(u, dev) for u in us]
+    u_ptrs = torch.tensor([u.data_ptr() for u in ut], dtype=torch.int64, device=dev)
+    err1 = torch.empty(n, length, dtype=torch.float32, device=dev)
+    codes = torch.zeros(n, k, dtype=torch.uint8, device=dev)
+    comp = torch.zeros(n, k, dtype=torch.float32, device=dev)
+    gptq_kernel.gptq_block(T(wc, dev), i1, length, err1, codes, T(lo, dev), T(st, dev),
+                           T(row_grp, dev), u_ptrs, T(blk, dev), T(nm, dev), comp)
+    assert np.array_equal(N(err1), err_w)
+    assert np.array_equal(N(codes), codes_w)
+    assert np.array_equal(N(comp), comp_w)
+
+
+@pytest.mark.parametrize("sb", [1, 2, 3, 8])
+def test_super_block_schedule_is_bit_identical(dev, sb):
+    from hi2_amd.hessian import GptqJob, encode_jobs_gptq
+
+    w, d, u, perm, _ = _layer(150, 1024, 5, act_order=True)
+    job = GptqJob(T(w, dev), T(d, dev), T(u, dev), 4, 64, T(perm, dev))
+    ref = encode_jobs_gptq([job], "normal", comp=True, super_blocks=1)[0]
+    got = encode_jobs_gptq([job], "normal", comp=True, super_blocks=sb)[0]
+    for f in ("codes", "params", "consts", "sse", "comp"):
+        assert torch.equal(getattr(got, f), getattr(ref, f)), f
+
+
+def test_batched_jobs_match_one_call_each(dev, monkeypatch):
+    # reference tests/test_gptq_fast.py:58-72: several row chunks and batches, two widths
+    import hi2_amd.hessian as hm
+
+    monkeypatch.setattr(hm, "ROW_ELEMS", 256 * 5)
+    monkeypatch.setattr(hm, "BATCH_ELEMS", 256 * 23)
+    jobs, refs = [], []
+    for i, (nb, b) in enumerate(CASES):
+        k = 256 if i % 3 else 128
+        w, d, u, perm, _ = _layer(13 + i, k, i, act_order=i % 2 == 1)
+        jobs.append(hm.GptqJob(T(w, dev), T(d, dev), T(u, dev), nb, b,
+                               None if perm is None else T(perm, dev)))
+        refs.append(oracle.encode_rows_gptq(w, d, u, nb, b, "fast", perm))
+    for got, ref in zip(hm.encode_jobs_gptq(jobs, "fast", comp=True), refs):
+        _same(got, ref)
+
+
+def test_nearest_encode_rows_equals_oracle(dev):
+    from hi2_amd.encode import encode_rows
+
+    rng = np.random.default_rng(3)
+    w = (rng.standard_normal((40, 256)) * np.exp(rng.standard_normal((1, 256)))).astype(np.float32)
+    d = (rng.random(256) + 0.1).astype(np.float32)
+    eye = np.eye(256, dtype=np.float32)
+    want = oracle.encode_rows_gptq(w, d, eye, 2, 32, "fast")
+    got = encode_rows(T(w, dev), T(d, dev), 2, 32, "fast")
+    _same(got, {**want, "comp": None})
+
+
+# ---- ladder, params, finish -------------------------------------------------------------
+@pytest.mark.parametrize("n,b,effort", [(4, 16, "normal"), (16, 32, "max"), (256, 64, "fast"),
+                                        (4, 64, "normal")])
+def test_fit_ladder_equals_oracle(dev, n, b, effort):
+    from hi2_amd.encode import fit_ladder
+
+    rng = np.random.default_rng(n + b)
+    wb = (rng.standard_normal((101, 640 // b * 4, b)) * np.exp(rng.standard_normal((101, 1, 1)))).astype(np.float32)
+    db = (rng.random((1, wb.shape[1], b)) + 0.5).astype(np.float32)
+    lo_w, st_w = oracle.fit_ladder(wb, db, n, effort)
+    lo, st = fit_ladder(T(wb, dev), T(db, dev), n, effort)
+    assert np.array_equal(N(lo), lo_w) and np.array_equal(N(st), st_w)
+
+
+def test_params_equal_oracle(dev):
+    from hi2_amd.encode import params_decoded, quantize_params
+    from hi2_amd.format import decode_params
+
+    rng = np.random.default_rng(4)
+    lo = (rng.standard_normal((300, 70)) * 0.4).astype(np.float32)
+    st = (rng.random((300, 70)) * 0.05).astype(np.float32)
+    st[10] = 0
+    st[11, ::2] = -0.01
+    lo[12] = -0.125
+    want = oracle.params(lo, st)
+    got = params_decoded(T(lo, dev), T(st, dev))
+    for g, w in zip(got, want):
+        g = N(g)
+        assert np.array_equal(g.view(w.dtype) if g.dtype == np.float16 else g, w)
+    lo_u8, st_u8, consts = quantize_params(T(lo, dev), T(st, dev))
+    dl, ds = decode_params(lo_u8, st_u8, consts[:, 0:1], consts[:, 1:2], consts[:, 2:3])
+    assert np.array_equal(N(dl).astype(np.float32), want[3])
+    assert np.array_equal(N(ds).astype(np.float32), want[4])
+
+
+# ---- format ------------------------------------------------------------------------------
+def test_fwht_equals_oracle_and_is_an_involution(dev):
+    from hi2_amd.format import fwht_groups
+
+    rng = np.random.default_rng(1)
+    x = (rng.standard_normal((333, 512)) * np.exp(rng.standard_normal((333, 512)))).astype(np.float32)
+    fl = rng.integers(0, 2, 32).astype(np.uint8)
+    y = fwht_groups(T(x, dev), T(fl, dev))
+    assert np.array_equal(N(y), oracle.fwht16(x, fl))
+    back = fwht_groups(y.double(), T(fl, dev))
+    assert torch.allclose(back, T(x, dev).double(), rtol=1e-6, atol=1e-6)
+    xb = T(x, dev).to(torch.bfloat16)  # non-fp32 input: float64 work, cast back
+    yb = fwht_groups(xb, T(fl, dev))
+    assert yb.dtype == torch.bfloat16
+    with pytest.raises(ValueError):
+        fwht_groups(T(x[:, :24], dev), T(fl[:1], dev))
+
+
+@pytest.mark.parametrize("nbits", [2, 4, 8])
+def test_pack_and_assemble_equal_oracle(dev, nbits):
+    from hi2_amd.format import assemble, pack_codes
+
+    rng = np.random.default_rng(nbits)
+    codes = rng.integers(0, 2**nbits, (37, 256)).astype(np.uint8)
+    assert np.array_equal(N(pack_codes(T(codes, dev), nbits)), oracle.pack_codes(codes, nbits))
+    if nbits < 8:
+        bad = codes.copy()
+        bad[3, 7] = 2**nbits
+        with pytest.raises(ValueError):
+            pack_codes(T(bad, dev), nbits)
+    k, r = 128, 9
+    row_nbits = rng.choice([2, 4, 8], r)
+    row_block = rng.choice([16, 32, 64], r)
+    pieces_np, pieces = [], []
+    for nb in (2, 4, 8):
+        for b in (16, 32, 64):
+            rows = np.nonzero((row_nbits == nb) & (row_block == b))[0]
+            if not rows.size:
+                continue
+            c = rng.integers(0, 2**nb, (rows.size, k)).astype(np.uint8)
+            p = rng.integers(0, 256, (rows.size, k // b, 2)).astype(np.uint8)
+            rc = rng.standard_normal((rows.size, 3)).astype(np.float16)
+            pieces_np.append((rows, c, p, rc.view(np.uint16)))
+            pieces.append((T(rows, dev), T(c, dev), T(p, dev), T(rc, dev)))
+    want = oracle.assemble(pieces_np, row_nbits, row_block, k)
+    got = assemble(pieces, torch.from_numpy(row_nbits), torch.from_numpy(row_block),
+                   torch.zeros(k // 16, dtype=torch.uint8), k)
+    assert np.array_equal(got.codes.numpy(), want["codes"])
+    assert np.array_equal(got.blk_params.numpy(), want["blk_params"])
+    assert np.array_equal(got.row_consts.numpy().view(np.uint16), want["row_consts"])
+    assert np.array_equal(got.code_off.numpy(), want["code_off"])
+    assert np.array_equal(got.param_off.numpy(), want["param_off"])
+
+
+# ---- Hessian, transform, factor --------------------------------------------------------------
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("t,k", [(700, 320), (4096, 256)])
+def test_hessian_stats_equal_xtx(dev, dtype, t, k):
+    from hi2_amd.hessian import HessianStats
+
+    rng = np.random.default_rng(t + k)
+    x = (rng.standard_normal((t, k)) * np.exp(rng.standard_normal((1, k)))).astype(np.float32)
+    x[:, 3] *= 20  # outlier channel
+    xt = T(x, dev).to(dtype)
+    st = HessianStats(k, dev)
+    st.update(xt[: t // 3])
+    other = HessianStats(k, dev)
+    other.update(xt[t // 3:])
+    st.merge(other)
+    assert st.n == t
+    xd = xt.double().cpu().numpy()
+    want = xd.T @ xd
+    got = N(st.S).astype(np.float64)
+    assert np.array_equal(N(st.S), N(st.S).T)  # exactly symmetric
+    # f32 accumulation of exact products over t terms
+    assert np.allclose(got, want, rtol=1e-4, atol=1e-4 * np.abs(want).max())
+    assert torch.allclose(st.mean(), st.S / t)
+
+
+@pytest.mark.parametrize("smooth", [False, True])
+def test_transform_sigma_equals_oracle(dev, smooth):
+    from hi2_amd.hessian import transform_sigma
+
+    rng = np.random.default_rng(2)
+    k = 320
+    a = rng.standard_normal((k, k)).astype(np.float32)
+    sigma = (a @ a.T / k).astype(np.float32)
+    sigma = (sigma + sigma.T) / 2
+    had = rng.integers(0, 2, k // 16).astype(np.uint8)
+    cs = (rng.random(k) * 2 + 0.3).astype(np.float16) if smooth else None
+    want = oracle.transform_sigma(sigma, None if cs is None else cs.view(np.uint16), had)
+    got = transform_sigma(T(sigma, dev), None if cs is None else T(cs, dev), T(had, dev))
+    assert np.array_equal(N(got), want)
+
+
+@pytest.mark.parametrize("k", [96, 320, 1000 - 1000 % 16])
+def test_inverse_factor_inverts(dev, k):
+    from hi2_amd.hessian import inverse_factor
+
+    rng = np.random.default_rng(k)
+    mix = rng.standard_normal((k, k)) * 0.15 + np.eye(k)
+    x = rng.standard_normal((3 * k, k)) @ mix
+    x *= np.exp(0.5 * rng.standard_normal((1, k)))
+    hs = (x.T @ x / x.shape[0]).astype(np.float32)
+    u = N(inverse_factor(T(hs, dev), 0.01)).astype(np.float64)
+    assert np.array_equal(np.tril(u, -1), np.zeros_like(u))
+    assert (np.diag(u) > 0).all()
+    damped = hs.astype(np.float64) + 0.01 * np.diag(hs).mean() * np.eye(k)
+    assert np.allclose(u.T @ u @ damped, np.eye(k), atol=2e-3)
+    u_o, _ = oracle.inverse_factor(hs, 0.01)
+    scale = np.abs(u_o).max()
+    assert np.allclose(u, u_o, rtol=1e-3, atol=2e-4 * scale)
+
+
+def test_inverse_factor_retries_and_survives_singular(dev):
+    from hi2_amd.hessian import inverse_factor
+
+    sing = torch.zeros(16, 16, device=dev)
+    sing[0, 0] = 1.0
+    assert torch.isfinite(inverse_factor(sing, 0.01)).all()
+    ind = torch.eye(16, device=dev)
+    ind[15, 15] = -0.2
+    u = N(inverse_factor(ind, 0.01))
+    u_o, att = oracle.inverse_factor(N(ind), 0.01)
+    assert att == 2
+    assert np.allclose(u, u_o, rtol=1e-5, atol=1e-6)
+
+
+# ---- end to end: Hessian -> transform -> factor -> GPTQ -> pack ---------------------------
+def test_small_config_end_to_end_against_oracle(dev):
+    """cfg1 scaled down (512 x 512, 256 tokens): the GPU pipeline against the oracle
+    pipeline.  The factor differs in rounding (LAPACK-free fp32 vs float64), so codes are
+    compared at the north-star tolerance: >= 99.9 % equal."""
+    from hi2_amd.format import assemble, fwht_groups
+    from hi2_amd.hessian import HessianStats, encode_rows_gptq, inverse_factor, transform_sigma
+
+    rng = np.random.default_rng(0)
+    k, n, t = 512, 512, 256
+    x = rng.standard_normal((t, k)).astype(np.float32)
+    x[:, rng.permutation(k)[: k // 100 + 1]] *= 20
+    xb = T(x, dev).to(torch.bfloat16)
+    w = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
+    had = np.ones(k // 16, np.uint8)
+    st = HessianStats(k, dev)
+    st.update(xb)
+    hs = transform_sigma(st.mean(), None, T(had, dev))
+    d = hs.diagonal().clone()
+    u = inverse_factor(hs, 0.01)
+    wt = fwht_groups(T(w, dev), T(had, dev))
+    enc = encode_rows_gptq(wt, d, u, 4, 64, "normal")
+    # oracle pipeline
+    s = np.zeros((k, k), np.float32)
+    oracle.hessian_update(s, N(xb.view(torch.int16)).view(np.uint16))
+    hs_o = oracle.transform_sigma(s / np.float32(t), None, had)
+    u_o, _ = oracle.inverse_factor(hs_o, 0.01)
+    wt_o = oracle.fwht16(w, had)
+    assert np.array_equal(N(wt), wt_o)
+    want = oracle.encode_rows_gptq(wt_o, np.diag(hs_o).copy(), u_o, 4, 64, "normal")
+    match = (N(enc.codes) == want["codes"]).mean()
+    assert match >= 0.999, match
+    sse_rel = np.abs(N(enc.sse) / want["sse"] - 1).max()
+    assert sse_rel < 1e-2, sse_rel
+    t_ = assemble([(torch.arange(n), enc.codes, enc.params, enc.consts)],
+                  torch.full((n,), 4), torch.full((n,), 64), torch.from_numpy(had), k)
+    assert t_.codes.numel() == n * k * 4 // 32
