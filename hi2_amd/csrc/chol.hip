@@ -65,7 +65,9 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g) {
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
         const int64_t kk = k0 + h * 8 + j;
-        As[h * 8 + j][m] = (rr < g.M && kk < kend) ? g.A[rr * g.lda + kk] : 0.0f;
+        // ALOW: the strict upper triangle of A is structurally zero (not read)
+        const bool ok = rr < g.M && kk < kend && (!ALOW || kk <= rr);
+        As[h * 8 + j][m] = ok ? g.A[rr * g.lda + kk] : 0.0f;
       }
     }
     if (TB) {  // Bs[k][n] = B[c0+n, k0+k]
@@ -74,14 +76,17 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g) {
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
         const int64_t kk = k0 + h * 8 + j;
-        Bs[h * 8 + j][n] = (cc < g.N && kk < kend) ? g.B[cc * g.ldb + kk] : 0.0f;
+        const bool ok = cc < g.N && kk < kend && (!BLOW || kk >= cc);
+        Bs[h * 8 + j][n] = ok ? g.B[cc * g.ldb + kk] : 0.0f;
       }
     } else {  // Bs[k][n] = B[k0+k, c0+n]
       const int k = tid >> 4, nb = (tid & 15) * 8;
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
         const int64_t cc = c0 + nb + j, kk = k0 + k;
-        Bs[k][nb + j] = (cc < g.N && kk < kend) ? g.B[kk * g.ldb + cc] : 0.0f;
+        // BLOW: op(B)[k][j] = 0 for k < j (not read)
+        const bool ok = cc < g.N && kk < kend && (!BLOW || kk >= cc);
+        Bs[k][nb + j] = ok ? g.B[kk * g.ldb + cc] : 0.0f;
       }
     }
     __syncthreads();

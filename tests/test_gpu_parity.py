@@ -224,8 +224,9 @@ def test_fwht_equals_oracle_and_is_an_involution(dev):
     fl = rng.integers(0, 2, 32).astype(np.uint8)
     y = fwht_groups(T(x, dev), T(fl, dev))
     assert np.array_equal(N(y), oracle.fwht16(x, fl))
-    back = fwht_groups(y.double(), T(fl, dev))
-    assert torch.allclose(back, T(x, dev).double(), rtol=1e-6, atol=1e-6)
+    back = fwht_groups(y.double(), T(fl, dev))  # y carries fp32 rounding
+    xd = T(x, dev).double()
+    assert torch.allclose(back, xd, rtol=1e-5, atol=1e-6 * float(xd.abs().max()))
     xb = T(x, dev).to(torch.bfloat16)  # non-fp32 input: float64 work, cast back
     yb = fwht_groups(xb, T(fl, dev))
     assert yb.dtype == torch.bfloat16
