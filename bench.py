@@ -72,11 +72,11 @@ def encode_block(xs, ws, masks, timer=None):
     import torch
 
     from hi2_amd.format import assemble, fwht_groups
-    from hi2_amd.hessian import GptqJob, HessianStats, encode_jobs_gptq, inverse_factor
+    from hi2_amd.hessian import GptqJob, HessianStats, encode_jobs_gptq, inverse_factors
     from hi2_amd.hessian import transform_sigma
 
     dev = next(iter(xs.values())).device
-    factors = {}
+    hss, meta = [], []
     for name, k in INPUTS.items():
         had = torch.ones(k // 16, dtype=torch.uint8, device=dev)
         if timer:
@@ -86,11 +86,12 @@ def encode_block(xs, ws, masks, timer=None):
         if timer:
             timer.mark(f"transform_{name}")
         hs = transform_sigma(st.mean(), None, had)
-        d = hs.diagonal().clone()
-        if timer:
-            timer.mark(f"factor_{name}")
-        u = inverse_factor(hs, DAMP)
-        factors[name] = (d, u, had)
+        hss.append(hs)
+        meta.append((name, hs.diagonal().clone(), had))
+    if timer:
+        timer.mark("factor")
+    us = inverse_factors(hss, DAMP)  # the four factors run concurrently
+    factors = {name: (d, u, had) for (name, d, had), u in zip(meta, us)}
     if timer:
         timer.mark("rotate")
     jobs, where = [], []

@@ -43,6 +43,7 @@ SIGNATURES = {
     "hi2x_hessian_syrk_varlen": [_P, _I, _P, _I64, _I64, _P, _P],
     "hi2x_sigma_transform": [_P, _P, _P, _I64, _P, _P],
     "hi2x_chol_inv_upper": [_P, _I64, _F, _I, _P, _P],
+    "hi2x_chol_inv_upper_async": [_P, _I64, _F, _I, _P, _P, _P],
 }
 
 

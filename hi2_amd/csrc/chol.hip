@@ -4,33 +4,33 @@
 // H = Hs + lam I: three O(K^3) passes (4K^3/3 flops).  The same matrix is
 //   U = (J L J)^-1 = J L^-1 J,   L = chol(J H J),   J = the reversal permutation,
 // because J L J is upper triangular with H = (J L J)(J L J)^T, so (J L J)^-1 is the
-// upper triangular factor of H^-1 with positive diagonal, which is unique.  That is
-// one Cholesky and one triangular inverse: 2K^3/3 flops.
+// upper triangular factor of H^-1 with positive diagonal, which is unique.  Only L^-1
+// is needed, never L: 2K^3/3 flops.
 //
-// Blocked, right-looking, NB = 128:
-//   potrf: per block column, a one-workgroup LDS factorisation (+ inverse) of the
-//          diagonal block, the panel solve as a GEMM with that inverse, and the
-//          trailing SYRK update on fp32 MFMA;
-//   trtri: recursive, inv([A 0; B C]) = [A^-1 0; -C^-1 B A^-1  C^-1], leaves from the
-//          diagonal inverses, the two products per node as triangular GEMMs.
+// L^-1 is built recursively on P = J H J, in place in its lower triangle:
+//   leaf (n <= 128): one workgroup factors the block and inverts the factor in
+//     registers (fused right-looking sweeps, one barrier per column);
+//   node [A11 0; A21 A22], n1 + n2 = n, after inv_chol(A11) left A11 = L11^-1:
+//     T1  = A21 A11^T               (= L21)
+//     A22 = A22 - T1 T1^T           (lower triangle)
+//     inv_chol(A22)                 (A22 = L22^-1)
+//     T2  = T1 A11                  (= L21 L11^-1)
+//     A21 = -A22 T2                 (= -L22^-1 L21 L11^-1, the lower-left block of L^-1)
+//   every product on the fp32 MFMA GEMM of mfma_gemm.h with triangular operands masked.
+#include <type_traits>
 #include <vector>
 
-#include "common.h"
+#include "mfma_gemm.h"
 
 namespace hi2x {
 namespace {
 
-typedef float f32x16 __attribute__((ext_vector_type(16)));
+constexpr int NB = 128;  // leaf size
 
-constexpr int NB = 128;
-constexpr int GT = 128, GK = 16;
-
-// ---- generic fp32 MFMA GEMM ----------------------------------------------------------
-// C[M, N] = alpha * A[M, Kd] * op(B) + beta * C, op(B) = B [Kd, N] (TB = false) or
-// B^T with B [N, Kd] (TB = true).  Flags skip structural zeros at tile granularity:
-//   ALOW: A lower triangular (A[i][k] = 0 for k > i)  -> k < row tile end
-//   BLOW: op(B) lower triangular (op(B)[k][j] = 0 for k < j) -> k >= col tile start
-//   CLOW: only the lower triangle of C (incl. diagonal) is computed and written.
+// ---- triangular GEMM ----------------------------------------------------------------
+// C[M, N] = alpha * A[M, Kd] * op(B) + beta * C (beta 0 or 1).
+// AMODE 1: A lower triangular.  BMODE 1 / 2: op(B) lower / upper triangular.
+// TB: B is given as [N, Kd] (op(B) = B^T).  CLOW: only the lower triangle of C.
 struct GemmArgs {
   const float* A;
   const float* B;
@@ -39,71 +39,40 @@ struct GemmArgs {
   float alpha, beta;
 };
 
-template <bool TB, bool ALOW, bool BLOW, bool CLOW>
-__global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g) {
-  __shared__ float As[GK][GT + 4];
-  __shared__ float Bs[GK][GT + 4];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wr = wave >> 1, wcn = wave & 1;
-  const int64_t r0 = (int64_t)blockIdx.y * GT, c0 = (int64_t)blockIdx.x * GT;
-  if (CLOW && c0 > r0 + GT - 1) return;
+struct MaskLower {  // keep (r, k) with k <= r
+  __device__ __forceinline__ bool operator()(int64_t r, int64_t k) const { return k <= r; }
+};
+struct MaskUpper {  // keep (r, k) with k >= r
+  __device__ __forceinline__ bool operator()(int64_t r, int64_t k) const { return k >= r; }
+};
+
+template <int AMODE, int BMODE, bool TB, bool CLOW>
+__global__ __launch_bounds__(256) void tri_gemm_kernel(GemmArgs g, int64_t tn, int64_t ntiles) {
+  __shared__ MgSmem sm;
+  const int64_t t = xcd_tile(blockIdx.x, ntiles);
+  if (t < 0) return;
+  const int64_t r0 = (t / tn) * MG_T, c0 = (t % tn) * MG_T;
+  if (CLOW && c0 > r0 + MG_T - 1) return;
   int64_t kbeg = 0, kend = g.Kd;
-  if (ALOW) kend = (r0 + GT < kend) ? r0 + GT : kend;
-  if (BLOW) kbeg = c0 - (c0 % GK);
+  if (AMODE == 1) kend = (r0 + MG_T < kend) ? r0 + MG_T : kend;
+  if (BMODE == 1) kbeg = c0;
+  if (BMODE == 2) kend = (c0 + MG_T < kend) ? c0 + MG_T : kend;
   f32x16 acc[2][2];
-#pragma unroll
-  for (int a = 0; a < 2; ++a)
-#pragma unroll
-    for (int b = 0; b < 2; ++b)
-#pragma unroll
-      for (int j = 0; j < 16; ++j) acc[a][b][j] = 0.0f;
-  for (int64_t k0 = kbeg; k0 < kend; k0 += GK) {
-    __syncthreads();
-    {  // A chunk: As[k][m] = A[r0+m, k0+k]
-      const int m = tid >> 1, h = tid & 1;
-      const int64_t rr = r0 + m;
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const int64_t kk = k0 + h * 8 + j;
-        // ALOW: the strict upper triangle of A is structurally zero (not read)
-        const bool ok = rr < g.M && kk < kend && (!ALOW || kk <= rr);
-        As[h * 8 + j][m] = ok ? g.A[rr * g.lda + kk] : 0.0f;
-      }
-    }
-    if (TB) {  // Bs[k][n] = B[c0+n, k0+k]
-      const int n = tid >> 1, h = tid & 1;
-      const int64_t cc = c0 + n;
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const int64_t kk = k0 + h * 8 + j;
-        const bool ok = cc < g.N && kk < kend && (!BLOW || kk >= cc);
-        Bs[h * 8 + j][n] = ok ? g.B[cc * g.ldb + kk] : 0.0f;
-      }
-    } else {  // Bs[k][n] = B[k0+k, c0+n]
-      const int k = tid >> 4, nb = (tid & 15) * 8;
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const int64_t cc = c0 + nb + j, kk = k0 + k;
-        // BLOW: op(B)[k][j] = 0 for k < j (not read)
-        const bool ok = cc < g.N && kk < kend && (!BLOW || kk >= cc);
-        Bs[k][nb + j] = ok ? g.B[kk * g.ldb + cc] : 0.0f;
-      }
-    }
-    __syncthreads();
-#pragma unroll
-    for (int k2 = 0; k2 < GK; k2 += 2) {
-      const int kr = k2 + (lane >> 5);
-      float av[2], bv[2];
-#pragma unroll
-      for (int a = 0; a < 2; ++a) av[a] = As[kr][wr * 64 + a * 32 + (lane & 31)];
-#pragma unroll
-      for (int b = 0; b < 2; ++b) bv[b] = Bs[kr][wcn * 64 + b * 32 + (lane & 31)];
-#pragma unroll
-      for (int a = 0; a < 2; ++a)
-#pragma unroll
-        for (int b = 0; b < 2; ++b)
-          acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[a], bv[b], acc[a][b], 0, 0, 0);
-    }
+  mg_zero(acc);
+  using AMask = typename std::conditional<AMODE == 1, MaskLower, NoMask>::type;
+  RowsLoader<AMask> al{g.A, g.lda, g.M, kend, AMask{}};
+  if (TB) {
+    // op(B)[k][j] = B[j][k]: lower op(B) keeps k >= j, upper keeps k <= j
+    using BMask = typename std::conditional<
+        BMODE == 1, MaskUpper, typename std::conditional<BMODE == 2, MaskLower, NoMask>::type>::type;
+    RowsLoader<BMask> bl{g.B, g.ldb, g.N, kend, BMask{}};
+    mg_mainloop(acc, sm, al, bl, r0, c0, kbeg, kend);
+  } else {
+    // op(B)[k][c] = B[k][c]: lower keeps c <= k (mask(k, c)), upper keeps c >= k
+    using BMask = typename std::conditional<
+        BMODE == 1, MaskLower, typename std::conditional<BMODE == 2, MaskUpper, NoMask>::type>::type;
+    ColsLoader<BMask> bl{g.B, g.ldb, g.N, kend, BMask{}};
+    mg_mainloop(acc, sm, al, bl, r0, c0, kbeg, kend);
   }
 #pragma unroll
   for (int a = 0; a < 2; ++a)
@@ -111,149 +80,192 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g) {
     for (int b = 0; b < 2; ++b)
 #pragma unroll
       for (int j = 0; j < 16; ++j) {
-        const int64_t row = r0 + wr * 64 + a * 32 + 8 * (j >> 2) + 4 * (lane >> 5) + (j & 3);
-        const int64_t col = c0 + wcn * 64 + b * 32 + (lane & 31);
+        const int64_t row = r0 + mg_row(a, j), col = c0 + mg_col(b);
         if (row >= g.M || col >= g.N) continue;
         if (CLOW && col > row) continue;
         float* cp = g.C + row * g.ldc + col;
         const float v = g.alpha * acc[a][b][j];
-        *cp = (g.beta != 0.0f) ? g.beta * *cp + v : v;
+        *cp = (g.beta != 0.0f) ? *cp + v : v;
       }
 }
 
-template <bool TB, bool ALOW, bool BLOW, bool CLOW>
-int gemm(const GemmArgs& a, hipStream_t s) {
+template <int AMODE, int BMODE, bool TB, bool CLOW>
+int tri_gemm(const GemmArgs& a, hipStream_t s) {
   if (a.M <= 0 || a.N <= 0) return HI2X_OK;
-  const dim3 grid((unsigned)((a.N + GT - 1) / GT), (unsigned)((a.M + GT - 1) / GT));
-  hipLaunchKernelGGL((gemm_kernel<TB, ALOW, BLOW, CLOW>), grid, dim3(256), 0, s, a);
-  return launch_status("gemm_kernel");
+  const int64_t tm = (a.M + MG_T - 1) / MG_T, tn = (a.N + MG_T - 1) / MG_T;
+  const int64_t ntiles = tm * tn;
+  const int64_t grid = (ntiles + 7) / 8 * 8;
+  hipLaunchKernelGGL((tri_gemm_kernel<AMODE, BMODE, TB, CLOW>), dim3((unsigned)grid), dim3(256),
+                     0, s, a, tn, ntiles);
+  return launch_status("tri_gemm_kernel");
 }
 
-// ---- prep: P = J (hs + lam I) J, lam = damp * max(mean(diag hs), 1e-12) * 10^attempt ---
+// ---- lam = damp * max(mean(diag hs), 1e-12) * 10^attempt ---------------------------------
 // mean(diag) as the reference's torch CPU reduction of the strided diagonal: 4 scalar
-// accumulators over rows of 4, the 4-level cascade, the tail into accumulator 0, the
-// accumulators folded, then divided by K.
-__global__ void diag_mean_kernel(const float* __restrict__ hs, int64_t K, float damp,
-                                 float p10, float* __restrict__ lam_out) {
-  if (threadIdx.x != 0 || blockIdx.x != 0) return;
-  auto x = [&](int64_t i) { return hs[i * K + i]; };
+// accumulators over rows of 4 elements, the 4-level cascade (base 2^max(4,
+// ceil_log2(rows)/4)), the tail into accumulator 0, the accumulators folded, / K.
+// Thread q < 4 runs accumulator q; the diagonal is staged through LDS in chunks.
+__global__ __launch_bounds__(256) void diag_mean_kernel(const float* __restrict__ hs, int64_t K,
+                                                        float damp, float p10,
+                                                        float* __restrict__ lam_out) {
+  constexpr int CH = 4096;  // diagonal elements per LDS chunk (multiple of 4)
+  __shared__ float dg[CH];
+  __shared__ float part[4];
+  const int tid = threadIdx.x;
   const int64_t size_ilp = K / 4;
-  float acc[4][4];
-  for (int a = 0; a < 4; ++a)
-    for (int b = 0; b < 4; ++b) acc[a][b] = 0.0f;
-  if (size_ilp > 0) {
-    int64_t lp = 1;
-    if (size_ilp > 2) lp = 64 - __builtin_clzll((unsigned long long)(size_ilp - 1));
-    lp /= 4;
-    if (lp < 4) lp = 4;
-    const int64_t step = (int64_t)1 << lp, lmask = step - 1;
-    int64_t i = 0;
-    while (i + step <= size_ilp) {
-      for (int64_t j = 0; j < step; ++j)
-        for (int q = 0; q < 4; ++q) acc[0][q] += x((i + j) * 4 + q);
-      i += step;
-      for (int lev = 1; lev < 4; ++lev) {
-        for (int q = 0; q < 4; ++q) {
-          acc[lev][q] += acc[lev - 1][q];
-          acc[lev - 1][q] = 0.0f;
+  int64_t lp = 1;
+  if (size_ilp > 2) lp = 64 - __builtin_clzll((unsigned long long)(size_ilp - 1));
+  lp /= 4;
+  if (lp < 4) lp = 4;
+  const int64_t step = (int64_t)1 << lp, lmask = step - 1;
+  float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  int64_t j = 0;  // rows of 4 consumed into the current step
+  int64_t i = 0;  // row index of the cascade (rows of 4)
+  for (int64_t base = 0; base < K; base += CH) {
+    const int64_t cnt = (K - base < CH) ? K - base : CH;
+    __syncthreads();
+    for (int64_t e = tid; e < cnt; e += 256) dg[e] = hs[(base + e) * K + (base + e)];
+    __syncthreads();
+    if (tid < 4) {
+      for (int64_t e = 0; e + 4 <= cnt; e += 4) {
+        const int64_t row = (base + e) / 4;
+        if (row >= size_ilp) break;
+        const int64_t full = (size_ilp / step) * step;  // rows handled by the cascade loop
+        if (row < full) {
+          acc[0] += dg[e + tid];
+          if (++j == step) {  // a full step of rows done: propagate as the reference does
+            j = 0;
+            i += step;
+            for (int lev = 1; lev < 4; ++lev) {
+              acc[lev] += acc[lev - 1];
+              acc[lev - 1] = 0.0f;
+              if (i & (lmask << (lev * lp))) break;
+            }
+          }
+        } else {
+          acc[0] += dg[e + tid];  // the remaining rows after the last full step
         }
-        if (i & (lmask << (lev * lp))) break;
       }
     }
-    for (; i < size_ilp; ++i)
-      for (int q = 0; q < 4; ++q) acc[0][q] += x(i * 4 + q);
-    for (int lev = 1; lev < 4; ++lev)
-      for (int q = 0; q < 4; ++q) acc[0][q] += acc[lev][q];
   }
-  float p[4] = {acc[0][0], acc[0][1], acc[0][2], acc[0][3]};
-  for (int64_t i = size_ilp * 4; i < K; ++i) p[0] += x(i);
-  const float sum = ((p[0] + p[1]) + p[2]) + p[3];
-  float mean = sum / (float)K;
-  mean = mean < 1e-12f ? 1e-12f : mean;
-  *lam_out = (damp * mean) * p10;
+  if (tid < 4) part[tid] = ((acc[0] + acc[1]) + acc[2]) + acc[3];
+  __syncthreads();
+  if (tid == 0) {
+    float p0 = part[0];
+    for (int64_t e = size_ilp * 4; e < K; ++e) p0 += hs[e * K + e];  // tail, in order
+    const float sum = ((p0 + part[1]) + part[2]) + part[3];
+    float mean = sum / (float)K;
+    mean = mean < 1e-12f ? 1e-12f : mean;
+    *lam_out = (damp * mean) * p10;
+  }
 }
 
+// P[i][j] = hs[K-1-i][K-1-j] (+ lam on the diagonal), lower triangle only.
 __global__ __launch_bounds__(256) void reverse_damp_kernel(const float* __restrict__ hs,
                                                            int64_t K,
                                                            const float* __restrict__ lam,
                                                            float* __restrict__ P) {
   const int64_t i = (int64_t)blockIdx.y;
   const float l = *lam;
-  for (int64_t j = threadIdx.x + (int64_t)blockIdx.x * blockDim.x; j <= i; j += (int64_t)gridDim.x * blockDim.x) {
+  for (int64_t j = threadIdx.x + (int64_t)blockIdx.x * blockDim.x; j <= i;
+       j += (int64_t)gridDim.x * blockDim.x) {
     const float v = hs[(K - 1 - i) * K + (K - 1 - j)];
     P[i * K + j] = (i == j) ? v + l : v;
   }
 }
 
-// ---- diagonal block: factor in LDS, write L_jj, write inv(L_jj) to inv_out ----------
-// status: first failing global pivot index + 1 (atomicMin over failures), 0 if none.
-__global__ __launch_bounds__(256) void potrf_diag_kernel(float* __restrict__ P, int64_t K,
-                                                         int64_t j0, int nb,
-                                                         float* __restrict__ inv_out,
-                                                         int* __restrict__ status) {
-  __shared__ float T[NB][NB + 1];
-  __shared__ float V[NB][NB + 1];
-  const int tid = threadIdx.x;
-  for (int idx = tid; idx < nb * nb; idx += 256) {
-    const int i = idx / nb, j = idx % nb;
-    T[i][j] = (j <= i) ? P[(j0 + i) * K + j0 + j] : 0.0f;
-  }
+// ---- leaf: L^-1 of chol(P[r0:r0+n, r0:r0+n]) in place (lower triangle) ---------------------
+// 1024 threads as 32 x 32; thread (ty, tx) holds slots (i, j) = (ty + 32a, tx + 32b),
+// b <= a < 4, of the lower triangle in registers.  Sweep c = 0..n-1, one barrier each:
+//   piv = sqrt(T[c][c]), rp = 1/piv; l_i = T[i][c] rp (column c of L); for column c the
+//   multiplier is rp, for j < c it is x_j = B[c][j] rp (row c of L^-1), for j > c l_j.
+//   Slots with i > c:  j > c: T[i][j] -= l_i l_j   (Cholesky update)
+//                      j = c: B[i][c]  = -l_i rp   (start of column c of L^-1)
+//                      j < c: B[i][j] -= l_i x_j   (forward substitution)
+//   Row c is final: X[c][j] = B[c][j] rp, X[c][c] = rp.
+// Column c+1 of T and row c+1 of B go through LDS to the next sweep.  The reciprocal
+// and square root are the hardware approximations (the factor is compared to a
+// tolerance, not bit for bit).
+constexpr int LT = 32;           // thread grid edge
+constexpr int LB = NB / LT;      // slots per thread edge
+
+__global__ __launch_bounds__(1024) void leaf_kernel(float* __restrict__ P, int64_t K, int64_t r0,
+                                                    int n, int* __restrict__ status) {
+  __shared__ float colb[2][NB];
+  __shared__ float rowb[2][NB];
+  const int tid = threadIdx.x, ty = tid / LT, tx = tid % LT;
+  float v[LB][LB];
+#pragma unroll
+  for (int a = 0; a < LB; ++a)
+#pragma unroll
+    for (int b = 0; b <= a; ++b) {
+      const int i = ty + LT * a, j = tx + LT * b;
+      v[a][b] = (i < n && j <= i) ? P[(r0 + i) * K + r0 + j] : 0.0f;
+    }
+  if (tx == 0)
+#pragma unroll
+    for (int a = 0; a < LB; ++a) colb[0][ty + LT * a] = v[a][0];
   __syncthreads();
-  for (int c = 0; c < nb; ++c) {
-    if (tid == 0) {
-      const float d = T[c][c];
-      if (!(d > 0.0f)) {
-        atomicMin(status, (int)(j0 + c + 1));
-        T[c][c] = __builtin_nanf("");
-      } else {
-        T[c][c] = __builtin_sqrtf(d);
+  bool bad = false;
+  for (int c = 0; c < n; ++c) {
+    const int p = c & 1;
+    const float d = colb[p][c];
+    bad = bad || !(d > 0.0f);
+    const float piv = __builtin_amdgcn_sqrtf(d);
+    const float rp = __builtin_amdgcn_rcpf(piv);
+    float li[LB], mj[LB];
+#pragma unroll
+    for (int a = 0; a < LB; ++a) li[a] = colb[p][ty + LT * a] * rp;
+#pragma unroll
+    for (int b = 0; b < LB; ++b) {
+      const int j = tx + LT * b;
+      mj[b] = (j > c) ? colb[p][j] * rp : (j == c ? rp : rowb[p][j] * rp);
+    }
+    const int ac = c / LT;  // band of row c (uniform)
+#pragma unroll
+    for (int a = 0; a < LB; ++a) {
+      if (a < ac) continue;  // rows all above c: final already
+      const int i = ty + LT * a;
+      const bool below = i > c;
+#pragma unroll
+      for (int b = 0; b <= a; ++b) {
+        const int j = tx + LT * b;
+        const float cur = (j == c) ? 0.0f : v[a][b];
+        v[a][b] = below ? __builtin_fmaf(-li[a], mj[b], cur) : v[a][b];
+      }
+      if (a == ac && i == c) {  // finalise row c of L^-1
+#pragma unroll
+        for (int b = 0; b <= a; ++b) {
+          const int j = tx + LT * b;
+          v[a][b] = (j < c) ? v[a][b] * rp : (j == c ? rp : v[a][b]);
+        }
       }
     }
-    __syncthreads();
-    const float piv = T[c][c];
-    for (int i = c + 1 + tid; i < nb; i += 256) T[i][c] = T[i][c] / piv;
-    __syncthreads();
-    const int m = nb - c - 1;
-    for (int idx = tid; idx < m * m; idx += 256) {
-      const int i = c + 1 + idx / m, j = c + 1 + idx % m;
-      if (j <= i) T[i][j] = T[i][j] - T[i][c] * T[j][c];
+    const int cn = c + 1;
+    if (cn < n) {
+      const int bn = cn / LT;  // band of column / row c+1 (uniform)
+#pragma unroll
+      for (int a = 0; a < LB; ++a)
+#pragma unroll
+        for (int b = 0; b <= a; ++b) {
+          if (b == bn && tx == cn - LT * b && ty + LT * a >= cn) colb[p ^ 1][ty + LT * a] = v[a][b];
+          if (a == bn && ty == cn - LT * a && tx + LT * b < cn) rowb[p ^ 1][tx + LT * b] = v[a][b];
+        }
     }
     __syncthreads();
   }
-  for (int idx = tid; idx < nb * nb; idx += 256) {
-    const int i = idx / nb, j = idx % nb;
-    if (j <= i) P[(j0 + i) * K + j0 + j] = T[i][j];
-  }
-  // inverse of the lower triangular T, one column per thread (forward substitution)
-  if (tid < nb) {
-    const int j = tid;
-    for (int i = 0; i < j; ++i) V[i][j] = 0.0f;
-    V[j][j] = 1.0f / T[j][j];
-    for (int i = j + 1; i < nb; ++i) {
-      float s = 0.0f;
-      for (int p = j; p < i; ++p) s = s + T[i][p] * V[p][j];
-      V[i][j] = -s / T[i][i];
+  if (bad && tid == 0) atomicMin(status, (int)(r0 + 1));
+#pragma unroll
+  for (int a = 0; a < LB; ++a)
+#pragma unroll
+    for (int b = 0; b <= a; ++b) {
+      const int i = ty + LT * a, j = tx + LT * b;
+      if (i < n && j <= i) P[(r0 + i) * K + r0 + j] = v[a][b];
     }
-  }
-  __syncthreads();
-  if (inv_out)
-    for (int idx = tid; idx < nb * nb; idx += 256) {
-      const int i = idx / nb, j = idx % nb;
-      inv_out[(int64_t)i * NB + j] = V[i][j];
-    }
-}
-
-// Copy an NB x NB inverse (ld NB) into the lower diagonal block of P at j0.
-__global__ void put_diag_kernel(float* __restrict__ P, int64_t K, int64_t j0, int nb,
-                                const float* __restrict__ inv) {
-  for (int idx = threadIdx.x; idx < nb * nb; idx += blockDim.x) {
-    const int i = idx / nb, j = idx % nb;
-    if (j <= i) P[(j0 + i) * K + j0 + j] = inv[(int64_t)i * NB + j];
-  }
 }
 
 // U[i][j] = Linv[K-1-i][K-1-j] for j >= i, 0 below: in place over pairs
-// {(i, j), (K-1-i, K-1-j)}, thread per element of the upper triangle.
+// {(i, j), (K-1-i, K-1-j)}, one thread per element of the upper triangle.
 __global__ __launch_bounds__(256) void reverse_out_kernel(float* __restrict__ P, int64_t K) {
   const int64_t i = (int64_t)blockIdx.y;
   for (int64_t j = i + threadIdx.x + (int64_t)blockIdx.x * blockDim.x; j < K;
@@ -272,64 +284,62 @@ __global__ __launch_bounds__(256) void reverse_out_kernel(float* __restrict__ P,
   }
 }
 
-// ---- host driver --------------------------------------------------------------------
-struct Chol {
+__global__ void status_init_kernel(int* __restrict__ status, int v) { *status = v; }
+
+// ---- host recursion -------------------------------------------------------------------
+struct Plan {
+  std::vector<int64_t> t1_off;  // per depth offset into the workspace
+  int64_t t2_off = 0, total = 0;
+};
+
+void plan_sizes(int64_t m, int depth, std::vector<int64_t>& t1, int64_t& t2) {
+  if (m <= NB) return;
+  const int64_t nbk = (m + NB - 1) / NB;
+  const int64_t m1 = ((nbk + 1) / 2) * NB, m2 = m - m1;
+  if ((int)t1.size() <= depth) t1.resize(depth + 1, 0);
+  t1[depth] = std::max(t1[depth], m1 * m2);
+  t2 = std::max(t2, m1 * m2);
+  plan_sizes(m1, depth + 1, t1, t2);
+  plan_sizes(m2, depth + 1, t1, t2);
+}
+
+struct Ctx {
   float* P;
   int64_t K;
-  float* inv;   // [nblk, NB, NB] diagonal-block inverses
-  float* tmp;   // [K/2 + NB, K/2 + NB] trtri temporary
+  float* ws;
+  const Plan* plan;
+  int* status;
   hipStream_t s;
 };
 
-int potrf(const Chol& c, int* status) {
-  const int64_t K = c.K;
-  for (int64_t j0 = 0; j0 < K; j0 += NB) {
-    const int nb = (int)((K - j0 < NB) ? K - j0 : NB);
-    float* inv = c.inv + (j0 / NB) * NB * NB;
-    hipLaunchKernelGGL(potrf_diag_kernel, dim3(1), dim3(256), 0, c.s, c.P, K, j0, nb, inv,
-                       status);
-    int rc = launch_status("potrf_diag_kernel");
-    if (rc) return rc;
-    const int64_t m = K - j0 - nb;
-    if (m <= 0) break;
-    float* panel = c.P + (j0 + nb) * K + j0;
-    // panel <- panel * inv(L_jj)^T   (in place: one column tile, rows read before written)
-    GemmArgs a{panel, inv, panel, m, nb, nb, K, NB, K, 1.0f, 0.0f};
-    rc = gemm<true, false, false, false>(a, c.s);
-    if (rc) return rc;
-    // trailing lower triangle: A22 -= panel * panel^T
-    float* a22 = c.P + (j0 + nb) * K + (j0 + nb);
-    GemmArgs b{panel, panel, a22, m, m, nb, K, K, K, -1.0f, 1.0f};
-    rc = gemm<true, false, false, true>(b, c.s);
-    if (rc) return rc;
-  }
-  return HI2X_OK;
-}
-
-// Lower triangular inverse of the diagonal region [r0, r0 + m) in place.
-int trtri(const Chol& c, int64_t r0, int64_t m) {
+int inv_chol(const Ctx& c, int64_t r0, int64_t m, int depth) {
   const int64_t K = c.K;
   if (m <= NB) {
-    hipLaunchKernelGGL(put_diag_kernel, dim3(1), dim3(256), 0, c.s, c.P, K, r0, (int)m,
-                       c.inv + (r0 / NB) * NB * NB);
-    return launch_status("put_diag_kernel");
+    hipLaunchKernelGGL(leaf_kernel, dim3(1), dim3(1024), 0, c.s, c.P, K, r0, (int)m, c.status);
+    return launch_status("leaf_kernel");
   }
   const int64_t nbk = (m + NB - 1) / NB;
   const int64_t m1 = ((nbk + 1) / 2) * NB, m2 = m - m1;
-  int rc = trtri(c, r0, m1);
+  float* A11 = c.P + r0 * K + r0;
+  float* A21 = c.P + (r0 + m1) * K + r0;
+  float* A22 = c.P + (r0 + m1) * K + (r0 + m1);
+  float* T1 = c.ws + c.plan->t1_off[depth];
+  float* T2 = c.ws + c.plan->t2_off;
+  int rc = inv_chol(c, r0, m1, depth + 1);
   if (rc) return rc;
-  rc = trtri(c, r0 + m1, m2);
+  // T1 = A21 A11^T  (op(B) = A11^T upper)
+  rc = tri_gemm<0, 2, true, false>(GemmArgs{A21, A11, T1, m2, m1, m1, K, K, m1, 1.0f, 0.0f}, c.s);
   if (rc) return rc;
-  float* Ainv = c.P + r0 * K + r0;               // m1 x m1, lower
-  float* Bblk = c.P + (r0 + m1) * K + r0;        // m2 x m1, full (original L)
-  float* Cinv = c.P + (r0 + m1) * K + (r0 + m1); // m2 x m2, lower
-  // tmp = B * A^-1   (op(B) = A^-1 lower: k >= j)
-  GemmArgs g1{Bblk, Ainv, c.tmp, m2, m1, m1, K, K, m1, 1.0f, 0.0f};
-  rc = gemm<false, false, true, false>(g1, c.s);
+  // A22 -= T1 T1^T  (lower triangle)
+  rc = tri_gemm<0, 0, true, true>(GemmArgs{T1, T1, A22, m2, m2, m1, m1, m1, K, -1.0f, 1.0f}, c.s);
   if (rc) return rc;
-  // B <- -C^-1 * tmp  (A = C^-1 lower: k <= i)
-  GemmArgs g2{Cinv, c.tmp, Bblk, m2, m1, m2, K, m1, K, -1.0f, 0.0f};
-  return gemm<false, true, false, false>(g2, c.s);
+  rc = inv_chol(c, r0 + m1, m2, depth + 1);
+  if (rc) return rc;
+  // T2 = T1 A11  (op(B) = A11 lower)
+  rc = tri_gemm<0, 1, false, false>(GemmArgs{T1, A11, T2, m2, m1, m1, m1, K, m1, 1.0f, 0.0f}, c.s);
+  if (rc) return rc;
+  // A21 = -A22 T2  (A = A22 lower)
+  return tri_gemm<1, 0, false, false>(GemmArgs{A22, T2, A21, m2, m1, m2, K, m1, K, -1.0f, 0.0f}, c.s);
 }
 
 }  // namespace
@@ -337,38 +347,70 @@ int trtri(const Chol& c, int64_t r0, int64_t m) {
 
 using namespace hi2x;
 
+static int chol_launch(const float* hs, int64_t k, float damp, int attempt, float* u,
+                       int* status_out, hipStream_t s) {
+  Plan plan;
+  {
+    std::vector<int64_t> t1;
+    int64_t t2 = 0;
+    plan_sizes(k, 0, t1, t2);
+    int64_t off = 0;
+    for (int64_t sz : t1) {
+      plan.t1_off.push_back(off);
+      off += (sz + 63) / 64 * 64;
+    }
+    plan.t2_off = off;
+    plan.total = off + (t2 + 63) / 64 * 64;
+  }
+  float* ws = nullptr;
+  float* lam = nullptr;
+  if (plan.total) HI2X_HIP(hipMallocAsync((void**)&ws, (size_t)plan.total * sizeof(float), s));
+  HI2X_HIP(hipMallocAsync((void**)&lam, sizeof(float), s));
+  const int big = 0x7fffffff;
+  int rc = HI2X_OK;
+  hipLaunchKernelGGL(status_init_kernel, dim3(1), dim3(1), 0, s, status_out, big);
+  rc = launch_status("status_init_kernel");
+  float p10 = 1.0f;
+  for (int a = 0; a < attempt; ++a) p10 *= 10.0f;
+  if (!rc) {
+    hipLaunchKernelGGL(diag_mean_kernel, dim3(1), dim3(256), 0, s, hs, k, damp, p10, lam);
+    rc = launch_status("diag_mean_kernel");
+  }
+  if (!rc) {
+    const dim3 g((unsigned)((k + 255) / 256 < 16 ? (k + 255) / 256 : 16), (unsigned)k);
+    hipLaunchKernelGGL(reverse_damp_kernel, g, dim3(256), 0, s, hs, k, lam, u);
+    rc = launch_status("reverse_damp_kernel");
+  }
+  Ctx c{u, k, ws, &plan, status_out, s};
+  if (!rc) rc = inv_chol(c, 0, k, 0);
+  if (!rc) {  // U = J L^-1 J (garbage if the factorisation failed; the status says so)
+    const dim3 g((unsigned)((k + 255) / 256 < 16 ? (k + 255) / 256 : 16), (unsigned)k);
+    hipLaunchKernelGGL(reverse_out_kernel, g, dim3(256), 0, s, u, k);
+    rc = launch_status("reverse_out_kernel");
+  }
+  if (ws) (void)hipFreeAsync(ws, s);
+  (void)hipFreeAsync(lam, s);
+  return rc;
+}
+
+extern "C" int hi2x_chol_inv_upper_async(const float* hs, int64_t k, float damp, int attempt,
+                                         float* u, int32_t* status, void* stream) {
+  clear_error();
+  HI2X_REQUIRE(k > 0 && hs && u && hs != u && status, "chol_inv_upper_async: bad arguments");
+  HI2X_REQUIRE(attempt >= 0 && attempt < 10, "chol_inv_upper_async: attempt %d", attempt);
+  return chol_launch(hs, k, damp, attempt, u, status, as_stream(stream));
+}
+
 extern "C" int hi2x_chol_inv_upper(const float* hs, int64_t k, float damp, int attempt,
                                    float* u, void* stream) {
   clear_error();
   HI2X_REQUIRE(k > 0 && hs && u && hs != u, "chol_inv_upper: bad arguments");
   HI2X_REQUIRE(attempt >= 0 && attempt < 10, "chol_inv_upper: attempt %d", attempt);
   hipStream_t s = as_stream(stream);
-  const int64_t nblk = (k + NB - 1) / NB;
-  const int64_t half = (nblk + 1) / 2 * NB;
-  float* inv = nullptr;
-  float* tmp = nullptr;
   int* status = nullptr;
-  float* lam = nullptr;
-  const size_t inv_bytes = (size_t)nblk * NB * NB * sizeof(float);
-  const size_t tmp_bytes = (size_t)half * (size_t)half * sizeof(float);
-  HI2X_HIP(hipMallocAsync((void**)&inv, inv_bytes, s));
-  HI2X_HIP(hipMallocAsync((void**)&tmp, tmp_bytes, s));
-  HI2X_HIP(hipMallocAsync((void**)&status, 2 * sizeof(int) + sizeof(float), s));
-  lam = reinterpret_cast<float*>(status + 2);
-  const int big = 0x7fffffff;
-  HI2X_HIP(hipMemcpyAsync(status, &big, sizeof(int), hipMemcpyHostToDevice, s));
-  float p10 = 1.0f;
-  for (int a = 0; a < attempt; ++a) p10 *= 10.0f;
-  hipLaunchKernelGGL(diag_mean_kernel, dim3(1), dim3(64), 0, s, hs, k, damp, p10, lam);
-  int rc = launch_status("diag_mean_kernel");
-  if (!rc) {
-    const dim3 g((unsigned)((k + 255) / 256 < 16 ? (k + 255) / 256 : 16), (unsigned)k);
-    hipLaunchKernelGGL(reverse_damp_kernel, g, dim3(256), 0, s, hs, k, lam, u);
-    rc = launch_status("reverse_damp_kernel");
-  }
-  Chol c{u, k, inv, tmp, s};
-  if (!rc) rc = potrf(c, status);
-  int st = big;
+  HI2X_HIP(hipMallocAsync((void**)&status, sizeof(int), s));
+  int rc = chol_launch(hs, k, damp, attempt, u, status, s);
+  int st = 0x7fffffff;
   if (!rc) {
     hipError_t e = hipMemcpyAsync(&st, status, sizeof(int), hipMemcpyDeviceToHost, s);
     if (e == hipSuccess) e = hipStreamSynchronize(s);
@@ -377,18 +419,11 @@ extern "C" int hi2x_chol_inv_upper(const float* hs, int64_t k, float damp, int a
       rc = HI2X_ELAUNCH;
     }
   }
-  if (!rc && st != big) {
-    set_error("chol_inv_upper: not positive definite at pivot %d (attempt %d)", st - 1, attempt);
+  (void)hipFreeAsync(status, s);
+  if (!rc && st != 0x7fffffff) {
+    set_error("chol_inv_upper: not positive definite in the block at %d (attempt %d)", st - 1,
+              attempt);
     rc = HI2X_ENOTPD;
   }
-  if (!rc) rc = trtri(c, 0, k);
-  if (!rc) {
-    const dim3 g((unsigned)((k + 255) / 256 < 16 ? (k + 255) / 256 : 16), (unsigned)k);
-    hipLaunchKernelGGL(reverse_out_kernel, g, dim3(256), 0, s, u, k);
-    rc = launch_status("reverse_out_kernel");
-  }
-  (void)hipFreeAsync(inv, s);
-  (void)hipFreeAsync(tmp, s);
-  (void)hipFreeAsync(status, s);
   return rc;
 }

@@ -6,12 +6,13 @@
 #include <stdarg.h>
 #include <stdio.h>
 
+#include <utility>
+
 #include "common.h"
+#include "mfma_gemm.h"
 
 namespace hi2x {
 namespace {
-
-typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 // ---------------------------------------------------------------------------------
 // Intra-block kernel.
@@ -40,19 +41,50 @@ constexpr int QSTR = CPL + 4;         // per-lane stride in an LDS U row (bank s
 constexpr int USTR = QL * QSTR;       // LDS U row stride (floats)
 
 template <int S>
-__device__ __forceinline__ float quad_bcast_t(float v) {
+__device__ __forceinline__ float quad_bcast(float v) {
   constexpr int ctrl = S * 0x55;  // quad_perm(S, S, S, S)
   return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), ctrl,
                                                             0xf, 0xf, false));
 }
 
-__device__ __forceinline__ float quad_bcast(float v, int s) {
-  switch (s) {
-    case 0: return quad_bcast_t<0>(v);
-    case 1: return quad_bcast_t<1>(v);
-    case 2: return quad_bcast_t<2>(v);
-    default: return quad_bcast_t<3>(v);
+// Register state of one row (this lane's 32 columns).
+struct RowRegs {
+  float w[CPL], loc[CPL], stc[CPL], er[CPL];
+  uint32_t cq[CPL / 4];
+};
+
+// Step I of the column loop, I a compile-time constant so that every register index
+// below is static (no dynamic VGPR indexing).
+template <int I>
+__device__ __forceinline__ void gptq_step(RowRegs& R, int L, int q, float nm,
+                                          const float* __restrict__ su,
+                                          const float* __restrict__ qrow, float* compr) {
+  constexpr int m = I / QL, s = I % QL;
+  if (I >= L) return;
+  const float col = R.w[m];
+  const float lo_j = R.loc[m], st_j = R.stc[m];
+  const float safe = (st_j == 0.0f) ? 1.0f : st_j;
+  float qv = clamp_code(__builtin_rintf((col - lo_j) / safe), nm);
+  if (st_j == 0.0f) qv = 0.0f;
+  const float wq = f16_round(lo_j + qv * st_j);
+  const float ujj = su[I * USTR + s * QSTR + m];
+  const float e = (col - wq) / ujj;
+  const float eb = quad_bcast<s>(e);
+  if (q == s) {
+    R.er[m] = e;
+    R.cq[m >> 2] |= ((uint32_t)qv & 0xffu) << (8 * (m & 3));
+    if (compr) compr[I] = col;
   }
+  const float* urow = qrow + I * USTR;
+#pragma unroll
+  for (int mm = (I + 1) / QL; mm < CPL; ++mm) R.w[mm] = R.w[mm] - eb * urow[mm];
+}
+
+template <int... Is>
+__device__ __forceinline__ void gptq_steps(std::integer_sequence<int, Is...>, RowRegs& R, int L,
+                                           int q, float nm, const float* __restrict__ su,
+                                           const float* __restrict__ qrow, float* compr) {
+  (gptq_step<Is>(R, L, q, nm, su, qrow, compr), ...);
 }
 
 __global__ __launch_bounds__(RPG * QL) void gptq_block_kernel(
@@ -90,8 +122,7 @@ __global__ __launch_bounds__(RPG * QL) void gptq_block_kernel(
 
     const int32_t* bl = blk + (int64_t)g * K;
     const float nm = nmax[g];
-    float w[CPL], loc[CPL], stc[CPL], er[CPL];
-    uint32_t cq[CPL / 4];
+    RowRegs R;
 #pragma unroll
     for (int m = 0; m < CPL; ++m) {
       const int c = QL * m + q;
@@ -102,44 +133,23 @@ __global__ __launch_bounds__(RPG * QL) void gptq_block_kernel(
         lv = lo[r * ldp + b];
         sv = st[r * ldp + b];
       }
-      w[m] = wv;
-      loc[m] = lv;
-      stc[m] = sv;
-      er[m] = 0.0f;
+      R.w[m] = wv;
+      R.loc[m] = lv;
+      R.stc[m] = sv;
+      R.er[m] = 0.0f;
     }
 #pragma unroll
-    for (int m = 0; m < CPL / 4; ++m) cq[m] = 0u;
+    for (int m = 0; m < CPL / 4; ++m) R.cq[m] = 0u;
 
-    const float* qrow = su + q * QSTR;
-#pragma unroll
-    for (int i = 0; i < LMAX; ++i) {
-      if (i >= L) break;
-      const int m = i / QL, s = i % QL;
-      const float col = w[m];
-      const float lo_j = loc[m], st_j = stc[m];
-      const float safe = (st_j == 0.0f) ? 1.0f : st_j;
-      float qv = clamp_code(__builtin_rintf((col - lo_j) / safe), nm);
-      if (st_j == 0.0f) qv = 0.0f;
-      const float wq = f16_round(lo_j + qv * st_j);
-      const float ujj = su[i * USTR + s * QSTR + m];
-      const float e = (col - wq) / ujj;
-      const float eb = quad_bcast(e, s);
-      if (q == s) {
-        er[m] = e;
-        cq[m >> 2] |= ((uint32_t)qv & 0xffu) << (8 * (m & 3));
-        if (comp) comp[r * K + i1 + i] = col;
-      }
-      const float* urow = qrow + i * USTR;
-#pragma unroll
-      for (int mm = (i + 1) / QL; mm < CPL; ++mm) w[mm] = w[mm] - eb * urow[mm];
-    }
+    float* compr = comp ? comp + r * K + i1 : nullptr;
+    gptq_steps(std::make_integer_sequence<int, LMAX>{}, R, L, q, nm, su, su + q * QSTR, compr);
 
 #pragma unroll
     for (int m = 0; m < CPL; ++m) {
       const int c = QL * m + q;
       if (c < L) {
-        err1[r * lde + c] = er[m];
-        codes[r * K + i1 + c] = (uint8_t)((cq[m >> 2] >> (8 * (m & 3))) & 0xffu);
+        err1[r * lde + c] = R.er[m];
+        codes[r * K + i1 + c] = (uint8_t)((R.cq[m >> 2] >> (8 * (m & 3))) & 0xffu);
       }
     }
   }
@@ -159,37 +169,37 @@ __global__ __launch_bounds__(RPG * QL) void gptq_block_kernel(
 // 16 through LDS.  Rows of another group than the pass's are masked in A and left
 // untouched in the epilogue.
 // ---------------------------------------------------------------------------------
-constexpr int TM = 128, TN = 128, KC = 16;
+struct GroupMask {  // A rows of the current group pass (this thread's staged row)
+  bool mine;
+  __device__ __forceinline__ bool operator()(int64_t, int64_t) const { return mine; }
+};
 
 __global__ __launch_bounds__(256) void gptq_trailing_kernel(
     float* __restrict__ wc, int64_t N, int64_t K, int64_t i1, int nblk,
     const float* __restrict__ err1, int64_t lde, int64_t c0, int64_t c1,
-    const int32_t* __restrict__ row_grp, const int64_t* __restrict__ u_ptrs) {
-  __shared__ float As[KC][TM];
-  __shared__ float Bs[KC][TN];
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = tid >> 6;
-  const int wr = wave >> 1, wcn = wave & 1;
-  const int64_t r0 = (int64_t)blockIdx.y * TM;
-  const int64_t cc0 = c0 + (int64_t)blockIdx.x * TN;
-  const int64_t rlast = ((r0 + TM < N) ? r0 + TM : N) - 1;
+    const int32_t* __restrict__ row_grp, const int64_t* __restrict__ u_ptrs, int64_t tn,
+    int64_t ntiles) {
+  __shared__ MgSmem sm;
+  const int64_t tile = xcd_tile(blockIdx.x, ntiles);
+  if (tile < 0) return;
+  const int64_t r0 = (tile / tn) * MG_T;
+  const int64_t cc0 = c0 + (tile % tn) * MG_T;
+  const int64_t rlast = ((r0 + MG_T < N) ? r0 + MG_T : N) - 1;
   const int g0 = row_grp[r0], g1 = row_grp[rlast];
+  const int tid = threadIdx.x;
+  const int64_t my_row = r0 + (tid >> 1);  // row this thread stages for the A operand
+  const int my_grp = my_row < N ? row_grp[my_row] : -1;
 
-  // C tile in the MFMA accumulator layout: tile (a, b), register j, lane l ->
-  // row 8*(j/4) + 4*(l/32) + j%4 (+32a, +64wr), col l%32 (+32b, +64wcn).
+  // the working-copy tile stays in registers (accumulator layout) for all blocks
   f32x16 cv[2][2];
-  const int64_t row_base = r0 + wr * 64 + 4 * (lane >> 5);
-  const int64_t col_base = cc0 + wcn * 64 + (lane & 31);
-#define TROW(a, j) (row_base + (a) * 32 + 8 * ((j) >> 2) + ((j) & 3))
 #pragma unroll
   for (int a = 0; a < 2; ++a)
 #pragma unroll
     for (int b = 0; b < 2; ++b) {
-      const int64_t cc = col_base + b * 32;
+      const int64_t cc = cc0 + mg_col(b);
 #pragma unroll
       for (int j = 0; j < 16; ++j) {
-        const int64_t rr = TROW(a, j);
+        const int64_t rr = r0 + mg_row(a, j);
         cv[a][b][j] = (rr < N && cc < c1) ? wc[rr * K + cc] : 0.0f;
       }
     }
@@ -198,51 +208,12 @@ __global__ __launch_bounds__(256) void gptq_trailing_kernel(
     const float* U = reinterpret_cast<const float*>(u_ptrs[g]);
     for (int t = 0; t < nblk; ++t) {
       const int64_t ib = i1 + (int64_t)t * LMAX;
-      const int L = (int)((K - ib < LMAX) ? K - ib : LMAX);
+      const int64_t L = (K - ib < LMAX) ? K - ib : LMAX;
       f32x16 acc[2][2];
-#pragma unroll
-      for (int a = 0; a < 2; ++a)
-#pragma unroll
-        for (int b = 0; b < 2; ++b)
-#pragma unroll
-          for (int j = 0; j < 16; ++j) acc[a][b][j] = 0.0f;
-
-      for (int kk = 0; kk < L; kk += KC) {
-        __syncthreads();
-        {  // A chunk: As[k][m] = err1[r0+m, t*128 + kk + k] (rows of group g only)
-          const int m = tid >> 1, h = tid & 1;
-          const int64_t rr = r0 + m;
-          const bool ok = rr < N && row_grp[rr] == g;
-#pragma unroll
-          for (int j = 0; j < 8; ++j) {
-            const int k = h * 8 + j;
-            As[k][m] = (ok && kk + k < L) ? err1[rr * lde + t * LMAX + kk + k] : 0.0f;
-          }
-        }
-        {  // B chunk: Bs[k][n] = U[ib + kk + k, cc0 + n]
-          const int k = tid >> 4, nb = (tid & 15) * 8;
-#pragma unroll
-          for (int j = 0; j < 8; ++j) {
-            const int64_t cc = cc0 + nb + j;
-            Bs[k][nb + j] = (kk + k < L && cc < c1) ? U[(ib + kk + k) * K + cc] : 0.0f;
-          }
-        }
-        __syncthreads();
-#pragma unroll
-        for (int k2 = 0; k2 < KC; k2 += 2) {
-          const int kr = k2 + (lane >> 5);
-          float av[2], bv[2];
-#pragma unroll
-          for (int a = 0; a < 2; ++a) av[a] = As[kr][wr * 64 + a * 32 + (lane & 31)];
-#pragma unroll
-          for (int b = 0; b < 2; ++b) bv[b] = Bs[kr][wcn * 64 + b * 32 + (lane & 31)];
-#pragma unroll
-          for (int a = 0; a < 2; ++a)
-#pragma unroll
-            for (int b = 0; b < 2; ++b)
-              acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[a], bv[b], acc[a][b], 0, 0, 0);
-        }
-      }
+      mg_zero(acc);
+      RowsLoader<GroupMask> al{err1 + t * LMAX, lde, N, L, GroupMask{my_grp == g}};
+      ColsLoader<NoMask> bl{U + ib * K, K, c1, L, NoMask{}};
+      mg_mainloop(acc, sm, al, bl, r0, cc0, 0, L);
       if (g0 == g1) {
 #pragma unroll
         for (int a = 0; a < 2; ++a)
@@ -255,7 +226,7 @@ __global__ __launch_bounds__(256) void gptq_trailing_kernel(
         for (int a = 0; a < 2; ++a)
 #pragma unroll
           for (int j = 0; j < 16; ++j) {
-            const int64_t rr = TROW(a, j);
+            const int64_t rr = r0 + mg_row(a, j);
             const bool mine = rr < N && row_grp[rr] == g;
 #pragma unroll
             for (int b = 0; b < 2; ++b)
@@ -268,14 +239,13 @@ __global__ __launch_bounds__(256) void gptq_trailing_kernel(
   for (int a = 0; a < 2; ++a)
 #pragma unroll
     for (int b = 0; b < 2; ++b) {
-      const int64_t cc = col_base + b * 32;
+      const int64_t cc = cc0 + mg_col(b);
 #pragma unroll
       for (int j = 0; j < 16; ++j) {
-        const int64_t rr = TROW(a, j);
+        const int64_t rr = r0 + mg_row(a, j);
         if (rr < N && cc < c1) wc[rr * K + cc] = cv[a][b][j];
       }
     }
-#undef TROW
 }
 
 int launch_block(const float* wc, int64_t n, int64_t k, int64_t i1, int64_t len, float* err1,
@@ -292,9 +262,11 @@ int launch_trailing(float* wc, int64_t n, int64_t k, int64_t i1, int nblk, const
                     int64_t lde, int64_t c0, int64_t c1, const int32_t* row_grp,
                     const int64_t* u_ptrs, hipStream_t s) {
   if (c1 <= c0 || n == 0) return HI2X_OK;
-  const dim3 grid((unsigned)((c1 - c0 + TN - 1) / TN), (unsigned)((n + TM - 1) / TM));
+  const int64_t tn = (c1 - c0 + MG_T - 1) / MG_T, tm = (n + MG_T - 1) / MG_T;
+  const int64_t ntiles = tn * tm;
+  const dim3 grid((unsigned)((ntiles + 7) / 8 * 8));
   hipLaunchKernelGGL(gptq_trailing_kernel, grid, dim3(256), 0, s, wc, n, k, i1, nblk, err1,
-                     lde, c0, c1, row_grp, u_ptrs);
+                     lde, c0, c1, row_grp, u_ptrs, tn, ntiles);
   return launch_status("gptq_trailing_kernel");
 }
 

@@ -3,11 +3,11 @@
 // Reference: hi2/hessian.py:26-47 (HessianStats.update/merge/mean),
 // hi2/hessian.py:50-68 (transform_sigma), hi2/moe.py:83-100 (routed token subsets).
 #include "common.h"
+#include "mfma_gemm.h"
 
 namespace hi2x {
 namespace {
 
-typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef unsigned short u16x8 __attribute__((ext_vector_type(8)));
 
@@ -117,6 +117,161 @@ __global__ __launch_bounds__(256) void syrk_bf16_kernel(const uint16_t* __restri
   store_sym(s, K, a0, b0, diag, wr, wcn, lane, acc);
 }
 
+// ---- bf16 SYRK on the feature-major copy Xt [K, T] -----------------------------------
+// X [T, K] is first transposed once (one HBM pass) so that every MFMA operand (8
+// consecutive tokens of one feature) is a 16-byte vector in memory and in LDS.  A
+// workgroup (4 waves) computes a 256 x 256 upper tile of S; each wave owns 128 x 128 as
+// 4 x 4 accumulators of v_mfma_f32_32x32x16_bf16 (f32 accumulation, products of bf16
+// exact).  Tokens stream in stages of 32 through double-buffered LDS.  Workgroups may
+// split the token range (partials combined in a fixed order afterwards) so that small
+// K still fills the chip.
+constexpr int S2T = 256;          // workgroup tile edge
+constexpr int S2C = 32;           // tokens per stage
+constexpr int S2P = S2C + 8;      // LDS pitch (bf16) per feature row
+
+// xt [K, Tp] = x^T with the token range padded with zeros to Tp (a multiple of 64).
+__global__ __launch_bounds__(256) void transpose_bf16_kernel(const uint16_t* __restrict__ x,
+                                                             int64_t T, int64_t K, int64_t Tp,
+                                                             uint16_t* __restrict__ xt) {
+  __shared__ uint16_t tile[64][66];
+  const int64_t t0 = (int64_t)blockIdx.y * 64, k0 = (int64_t)blockIdx.x * 64;
+  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+  for (int y = ty; y < 64; y += 4) {
+    const int64_t t = t0 + y, k = k0 + tx;
+    tile[y][tx] = (t < T && k < K) ? x[t * K + k] : (uint16_t)0;
+  }
+  __syncthreads();
+  for (int y = ty; y < 64; y += 4) {
+    const int64_t k = k0 + y, t = t0 + tx;
+    if (k < K && t < Tp) xt[k * Tp + t] = tile[tx][y];
+  }
+}
+
+__global__ __launch_bounds__(256) void syrk2_bf16_kernel(const uint16_t* __restrict__ xt,
+                                                         int64_t T, int64_t K, int nT,
+                                                         int64_t ntiles, int splits,
+                                                         int64_t tchunk, float* __restrict__ out,
+                                                         int64_t out_stride) {
+  __shared__ __attribute__((aligned(16))) uint16_t Xa[2][S2T * S2P];
+  __shared__ __attribute__((aligned(16))) uint16_t Xb[2][S2T * S2P];
+  const int64_t id = (int64_t)blockIdx.x;
+  const int sp = (int)(id % splits);
+  const int64_t tile = xcd_tile(id / splits, ntiles);
+  if (tile < 0) return;
+  int ta, tb;
+  upper_tile(nT, (int)tile, ta, tb);
+  const bool diag = ta == tb;
+  const int64_t a0 = (int64_t)ta * S2T, b0 = (int64_t)tb * S2T;
+  const int64_t tbeg = (int64_t)sp * tchunk;
+  const int64_t tend = (tbeg + tchunk < T) ? tbeg + tchunk : T;
+  float* s = out + (int64_t)sp * out_stride;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wr = wave >> 1, wcn = wave & 1;
+  f32x16 acc[4][4];
+#pragma unroll
+  for (int a = 0; a < 4; ++a)
+#pragma unroll
+    for (int b = 0; b < 4; ++b)
+#pragma unroll
+      for (int j = 0; j < 16; ++j) acc[a][b][j] = 0.0f;
+
+  // staging (T is the padded token count: every stage is whole, pad tokens are zero)
+  uint4 ra[4], rb[4];
+  auto load = [&](int64_t t0) {
+    const int64_t fa = a0 + tid, fb = b0 + tid;
+    const bool okA = fa < K, okB = !diag && fb < K;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int64_t tt = t0 + 8 * q;
+      ra[q] = okA ? *reinterpret_cast<const uint4*>(xt + fa * T + tt) : make_uint4(0, 0, 0, 0);
+      rb[q] = okB ? *reinterpret_cast<const uint4*>(xt + fb * T + tt) : make_uint4(0, 0, 0, 0);
+    }
+  };
+  auto store = [&](int buf) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      *reinterpret_cast<uint4*>(&Xa[buf][tid * S2P + 8 * q]) = ra[q];
+      if (!diag) *reinterpret_cast<uint4*>(&Xb[buf][tid * S2P + 8 * q]) = rb[q];
+    }
+  };
+  const int nst = (int)((tend - tbeg + S2C - 1) / S2C);
+  if (nst > 0) {
+    load(tbeg);
+    store(0);
+    __syncthreads();
+  }
+  for (int st = 0; st < nst; ++st) {
+    const int buf = st & 1;
+    if (st + 1 < nst) load(tbeg + (int64_t)(st + 1) * S2C);
+    const uint16_t* XA = Xa[buf];
+    const uint16_t* XB = diag ? Xa[buf] : Xb[buf];
+#pragma unroll
+    for (int ks = 0; ks < S2C; ks += 16) {
+      const int ko = ks + 8 * (lane >> 5);
+      bf16x8 bv[4];
+#pragma unroll
+      for (int b = 0; b < 4; ++b)
+        bv[b] = __builtin_bit_cast(
+            bf16x8, *reinterpret_cast<const u16x8*>(&XB[(wcn * 128 + b * 32 + (lane & 31)) * S2P + ko]));
+#pragma unroll
+      for (int a = 0; a < 4; ++a) {
+        const bf16x8 av = __builtin_bit_cast(
+            bf16x8, *reinterpret_cast<const u16x8*>(&XA[(wr * 128 + a * 32 + (lane & 31)) * S2P + ko]));
+#pragma unroll
+        for (int b = 0; b < 4; ++b)
+          acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, bv[b], acc[a][b], 0, 0, 0);
+      }
+    }
+    if (st + 1 < nst) store(buf ^ 1);  // buffer buf ^ 1 was last read before the barrier
+    __syncthreads();
+  }
+  // upper part of the tile (i <= j on the diagonal tile); the lower triangle is mirrored
+  // from it afterwards
+#pragma unroll
+  for (int a = 0; a < 4; ++a)
+#pragma unroll
+    for (int b = 0; b < 4; ++b)
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        const int64_t row = a0 + wr * 128 + a * 32 + 8 * (j >> 2) + 4 * (lane >> 5) + (j & 3);
+        const int64_t col = b0 + wcn * 128 + b * 32 + (lane & 31);
+        if (row >= K || col >= K || (diag && row > col)) continue;
+        if (splits == 1) s[row * K + col] += acc[a][b][j];
+        else s[row * K + col] = acc[a][b][j];
+      }
+}
+
+// S (upper triangle) += partial_0 + partial_1 + ... in split order.
+__global__ __launch_bounds__(256) void split_sum_kernel(float* __restrict__ s,
+                                                        const float* __restrict__ parts,
+                                                        int splits, int64_t K) {
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= K * K) return;
+  const int64_t i = idx / K, j = idx % K;
+  if (j < i) return;
+  float v = s[idx];
+  for (int p = 0; p < splits; ++p) v = v + parts[(int64_t)p * K * K + idx];
+  s[idx] = v;
+}
+
+// S[j][i] = S[i][j] for i < j (32 x 32 tile pairs through LDS).
+__global__ __launch_bounds__(256) void mirror_kernel(float* __restrict__ s, int64_t K, int nT) {
+  __shared__ float A[32][33];
+  int ti, tj;
+  upper_tile(nT, blockIdx.x, ti, tj);
+  const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;
+  const int64_t i0 = (int64_t)ti * 32, j0 = (int64_t)tj * 32;
+  for (int y = ty; y < 32; y += 8) {
+    const int64_t r = i0 + y, c = j0 + tx;
+    A[y][tx] = (r < K && c < K) ? s[r * K + c] : 0.0f;
+  }
+  __syncthreads();
+  for (int y = ty; y < 32; y += 8) {
+    const int64_t r = j0 + y, c = i0 + tx;  // lower element (r, c) = upper (c, r)
+    if (r < K && c < K && r > c) s[r * K + c] = A[tx][y];
+  }
+}
+
 // f32 X [T, K]: same tiling on v_mfma_f32_32x32x2_f32.
 __global__ __launch_bounds__(256) void syrk_f32_kernel(const float* __restrict__ x, int64_t T,
                                                        int64_t K, int nT,
@@ -166,96 +321,154 @@ __global__ __launch_bounds__(256) void syrk_f32_kernel(const float* __restrict__
   store_sym(s, K, a0, b0, diag, wr, wcn, lane, acc);
 }
 
-// transform_sigma, one workgroup (16 x 16 threads) per upper pair of 16 x 16 blocks
-// (gi <= gh).  Evaluates, as the reference's fp32 einsums do:
-//   s = (sigma * inv_i) * inv_j                       (smoothing, when col_scale given)
-//   t1[i][k] = sum_j m_gi[i][j] s[j][k]                (sequential FMA chain from 0)
-//   t2[i][l] = sum_k t1[i][k] m_gh[l][k]               (sequential FMA chain from 0)
-//   out = 0.5 * (t2 + t2^T)
-// with m = H16/4 on flagged groups and I elsewhere; an identity product reduces to
-// x + 0 (the chain maps -0 to +0), so both orders give the reference's bits.
+// transform_sigma in three coalesced passes over HBM, evaluating what the reference's
+// fp32 ops evaluate (hi2/hessian.py:57-68):
+//   (a) t1[16g+i][c] = sum_j m_g[i][j] s[16g+j][c], s = (sigma * inv_r) * inv_c
+//   (b) t2[r][16h+l] = sum_k t1[r][16h+k] m_h[l][k]          (in place)
+//   (c) out = 0.5 * (t2 + t2^T)                              (in place, tile pairs)
+// with m = H16/4 on flagged groups (sequential FMA chains from zero, the products by
+// +-1/4 exact) and I elsewhere; an identity product reduces to x + 0 (the chain maps
+// -0 to +0), so the bits are the reference einsums'.
 __device__ __forceinline__ float hsgn(int i, int j) {
   return (__builtin_popcount(i & j) & 1) ? -0.25f : 0.25f;
 }
 
-__global__ __launch_bounds__(256) void sigma_transform_kernel(
-    const float* __restrict__ sigma, const uint16_t* __restrict__ col_scale,
-    const uint8_t* __restrict__ had, int64_t K, int G, float* __restrict__ hs) {
-  __shared__ float S1[16][17], S2[16][17], T1[16][17], T2[16][17];
-  int gi, gh;
-  upper_tile(G, blockIdx.x, gi, gh);
-  const int i = threadIdx.x >> 4, l = threadIdx.x & 15;
-  const bool same = gi == gh;
-  const int64_t ri = (int64_t)gi * 16, rh = (int64_t)gh * 16;
-  {
-    float a = sigma[(ri + i) * K + rh + l];
-    float b = sigma[(rh + i) * K + ri + l];
-    if (col_scale) {
-      const float ii = 1.0f / f16_from_bits(col_scale[ri + i]);
-      const float il = 1.0f / f16_from_bits(col_scale[rh + l]);
-      const float hi = 1.0f / f16_from_bits(col_scale[rh + i]);
-      const float hl = 1.0f / f16_from_bits(col_scale[ri + l]);
-      a = (a * ii) * il;
-      b = (b * hi) * hl;
-    }
-    S1[i][l] = a;  // block (gi, gh)
-    S2[i][l] = b;  // block (gh, gi)
+__global__ __launch_bounds__(256) void st_left_kernel(const float* __restrict__ sigma,
+                                                      const uint16_t* __restrict__ col_scale,
+                                                      const uint8_t* __restrict__ had, int64_t K,
+                                                      float* __restrict__ out) {
+  const int64_t c = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t g = blockIdx.y;
+  if (c >= K) return;
+  float x[16];
+  const float ic = col_scale ? 1.0f / f16_from_bits(col_scale[c]) : 1.0f;
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {
+    const int64_t r = g * 16 + j;
+    float v = sigma[r * K + c];
+    if (col_scale) v = (v * (1.0f / f16_from_bits(col_scale[r]))) * ic;
+    x[j] = v;
   }
-  __syncthreads();
-  const bool fi = had[gi] != 0, fh = had[gh] != 0;
-  // left products: rows of block (gi, gh) by m_gi, rows of block (gh, gi) by m_gh
-  {
-    float a = 0.0f, b = 0.0f;
-    if (fi) {
+  if (had[g]) {
 #pragma unroll
-      for (int j = 0; j < 16; ++j) a = __builtin_fmaf(hsgn(i, j), S1[j][l], a);
-    } else {
-      a = S1[i][l] + 0.0f;
+    for (int i = 0; i < 16; ++i) {
+      float a = 0.0f;
+#pragma unroll
+      for (int j = 0; j < 16; ++j) a = __builtin_fmaf(hsgn(i, j), x[j], a);
+      out[(g * 16 + i) * K + c] = a;
     }
-    if (fh) {
-#pragma unroll
-      for (int j = 0; j < 16; ++j) b = __builtin_fmaf(hsgn(i, j), S2[j][l], b);
-    } else {
-      b = S2[i][l] + 0.0f;
-    }
-    T1[i][l] = a;
-    T2[i][l] = b;
-  }
-  __syncthreads();
-  // right products: block (gi, gh) by m_gh^T, block (gh, gi) by m_gi^T
-  float u1 = 0.0f, u2 = 0.0f;
-  if (fh) {
-#pragma unroll
-    for (int k = 0; k < 16; ++k) u1 = __builtin_fmaf(T1[i][k], hsgn(l, k), u1);
   } else {
-    u1 = T1[i][l] + 0.0f;
-  }
-  if (fi) {
 #pragma unroll
-    for (int k = 0; k < 16; ++k) u2 = __builtin_fmaf(T2[i][k], hsgn(l, k), u2);
+    for (int i = 0; i < 16; ++i) out[(g * 16 + i) * K + c] = x[i] + 0.0f;
+  }
+}
+
+__global__ __launch_bounds__(256) void st_right_kernel(const uint8_t* __restrict__ had, int64_t K,
+                                                       float* __restrict__ t) {
+  const int64_t G = K / 16;
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= K * G) return;
+  const int64_t r = idx / G, h = idx % G;
+  float* p = t + r * K + h * 16;
+  float x[16];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const float4 v = *reinterpret_cast<const float4*>(p + 4 * q);
+    x[4 * q] = v.x;
+    x[4 * q + 1] = v.y;
+    x[4 * q + 2] = v.z;
+    x[4 * q + 3] = v.w;
+  }
+  float y[16];
+  if (had[h]) {
+#pragma unroll
+    for (int l = 0; l < 16; ++l) {
+      float a = 0.0f;
+#pragma unroll
+      for (int k = 0; k < 16; ++k) a = __builtin_fmaf(x[k], hsgn(l, k), a);
+      y[l] = a;
+    }
   } else {
-    u2 = T2[i][l] + 0.0f;
+#pragma unroll
+    for (int l = 0; l < 16; ++l) y[l] = x[l] + 0.0f;
+  }
+#pragma unroll
+  for (int q = 0; q < 4; ++q)
+    *reinterpret_cast<float4*>(p + 4 * q) =
+        make_float4(y[4 * q], y[4 * q + 1], y[4 * q + 2], y[4 * q + 3]);
+}
+
+// 32 x 32 tile pairs (I <= J): out[i][j] = out[j][i] = 0.5 * (t[i][j] + t[j][i]).
+__global__ __launch_bounds__(256) void st_sym_kernel(int64_t K, int nT, float* __restrict__ t) {
+  __shared__ float A[32][33], B[32][33];
+  int ti, tj;
+  upper_tile(nT, blockIdx.x, ti, tj);
+  const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;  // 32 x 8
+  const int64_t i0 = (int64_t)ti * 32, j0 = (int64_t)tj * 32;
+  for (int y = ty; y < 32; y += 8) {
+    const int64_t r1 = i0 + y, c1 = j0 + tx, r2 = j0 + y, c2 = i0 + tx;
+    A[y][tx] = (r1 < K && c1 < K) ? t[r1 * K + c1] : 0.0f;
+    B[y][tx] = (r2 < K && c2 < K) ? t[r2 * K + c2] : 0.0f;
   }
   __syncthreads();
-  S1[i][l] = u1;  // t2 of block (gi, gh)
-  S2[i][l] = u2;  // t2 of block (gh, gi)
-  __syncthreads();
-  // out(gi, gh)[i][l] = 0.5 * (t2(gi,gh)[i][l] + t2(gh,gi)[l][i]); out(gh, gi) is its transpose
-  const float o = 0.5f * (S1[i][l] + (same ? S1[l][i] : S2[l][i]));
-  hs[(ri + i) * K + rh + l] = o;
-  if (!same) hs[(rh + l) * K + ri + i] = o;
+  for (int y = ty; y < 32; y += 8) {
+    const int64_t r1 = i0 + y, c1 = j0 + tx, r2 = j0 + y, c2 = i0 + tx;
+    const float o1 = 0.5f * (A[y][tx] + B[tx][y]);
+    const float o2 = 0.5f * (B[y][tx] + A[tx][y]);
+    if (r1 < K && c1 < K) t[r1 * K + c1] = o1;
+    if (ti != tj && r2 < K && c2 < K) t[r2 * K + c2] = o2;
+  }
 }
 
 int launch_syrk(const void* x, int dtype, int64_t t, int64_t k, float* s, hipStream_t st) {
-  const int nT = (int)((k + HT - 1) / HT);
-  const int64_t tiles = (int64_t)nT * (nT + 1) / 2;
-  if (dtype == 2)
-    hipLaunchKernelGGL(syrk_bf16_kernel, dim3((unsigned)tiles), dim3(256), 0, st,
-                       (const uint16_t*)x, t, k, nT, s);
-  else
+  if (dtype != 2) {
+    const int nT = (int)((k + HT - 1) / HT);
+    const int64_t tiles = (int64_t)nT * (nT + 1) / 2;
     hipLaunchKernelGGL(syrk_f32_kernel, dim3((unsigned)tiles), dim3(256), 0, st,
                        (const float*)x, t, k, nT, s);
-  return launch_status("syrk_kernel");
+    return launch_status("syrk_f32_kernel");
+  }
+  // bf16: transpose, tiles of 256 (token range split when the tiles are few), mirror
+  uint16_t* xt = nullptr;
+  const int64_t tp = (t + 63) / 64 * 64;
+  HI2X_HIP(hipMallocAsync((void**)&xt, (size_t)tp * (size_t)k * 2, st));
+  hipLaunchKernelGGL(transpose_bf16_kernel, dim3((unsigned)((k + 63) / 64), (unsigned)(tp / 64)),
+                     dim3(256), 0, st, (const uint16_t*)x, t, k, tp, xt);
+  int rc = launch_status("transpose_bf16_kernel");
+  const int nT = (int)((k + S2T - 1) / S2T);
+  const int64_t ntiles = (int64_t)nT * (nT + 1) / 2;
+  int splits = (int)((256 + ntiles - 1) / ntiles);
+  int64_t tchunk = (tp + splits - 1) / splits;
+  tchunk = (tchunk + S2C - 1) / S2C * S2C;
+  splits = (int)((tp + tchunk - 1) / tchunk);
+  if (splits < 1) splits = 1;
+  float* parts = nullptr;
+  if (!rc && splits > 1) {
+    if (hipMallocAsync((void**)&parts, (size_t)splits * k * k * sizeof(float), st) != hipSuccess) {
+      set_error("hessian_syrk: workspace allocation failed");
+      rc = HI2X_ELAUNCH;
+    }
+  }
+  if (!rc) {
+    const int64_t grid = (ntiles + 7) / 8 * 8 * splits;
+    hipLaunchKernelGGL(syrk2_bf16_kernel, dim3((unsigned)grid), dim3(256), 0, st, xt, tp, k, nT,
+                       ntiles, splits, tchunk, splits > 1 ? parts : s, k * k);
+    rc = launch_status("syrk2_bf16_kernel");
+  }
+  if (!rc && splits > 1) {
+    hipLaunchKernelGGL(split_sum_kernel, dim3((unsigned)((k * k + 255) / 256)), dim3(256), 0, st,
+                       s, parts, splits, k);
+    rc = launch_status("split_sum_kernel");
+  }
+  if (!rc) {
+    const int nM = (int)((k + 31) / 32);
+    hipLaunchKernelGGL(mirror_kernel, dim3((unsigned)((int64_t)nM * (nM + 1) / 2)), dim3(256), 0,
+                       st, s, k, nM);
+    rc = launch_status("mirror_kernel");
+  }
+  if (parts) (void)hipFreeAsync(parts, st);
+  (void)hipFreeAsync(xt, st);
+  return rc;
 }
 
 }  // namespace
@@ -295,9 +508,18 @@ extern "C" int hi2x_sigma_transform(const float* sigma, const uint16_t* col_scal
   HI2X_REQUIRE(k > 0 && k % 16 == 0, "sigma_transform: K=%lld not a multiple of 16",
                (long long)k);
   HI2X_REQUIRE(sigma != hs, "sigma_transform: in-place not supported");
-  const int G = (int)(k / 16);
-  const int64_t pairs = (int64_t)G * (G + 1) / 2;
-  hipLaunchKernelGGL(sigma_transform_kernel, dim3((unsigned)pairs), dim3(256), 0,
-                     as_stream(stream), sigma, col_scale, had, k, G, hs);
-  return launch_status("sigma_transform_kernel");
+  hipStream_t s = as_stream(stream);
+  const int64_t G = k / 16;
+  hipLaunchKernelGGL(st_left_kernel, dim3((unsigned)((k + 255) / 256), (unsigned)G), dim3(256),
+                     0, s, sigma, col_scale, had, k, hs);
+  int rc = launch_status("st_left_kernel");
+  if (rc) return rc;
+  hipLaunchKernelGGL(st_right_kernel, dim3((unsigned)((k * G + 255) / 256)), dim3(256), 0, s,
+                     had, k, hs);
+  rc = launch_status("st_right_kernel");
+  if (rc) return rc;
+  const int nT = (int)((k + 31) / 32);
+  hipLaunchKernelGGL(st_sym_kernel, dim3((unsigned)((int64_t)nT * (nT + 1) / 2)), dim3(256), 0,
+                     s, k, nT, hs);
+  return launch_status("st_sym_kernel");
 }

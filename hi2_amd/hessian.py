@@ -44,6 +44,7 @@ __all__ = [
     "encode_rows_gptq",
     "encode_rows_gptq_reference",
     "inverse_factor",
+    "inverse_factors",
     "transform_sigma",
 ]
 
@@ -125,6 +126,48 @@ def inverse_factor(hs: torch.Tensor, damp: float = 0.01) -> torch.Tensor:
         except _lib.NotPositiveDefinite as e:
             last = e
     raise RuntimeError(f"Hessian is not factorisable even with heavy damping: {last}")
+
+
+def inverse_factors(hss: list[torch.Tensor], damp: float = 0.01) -> list[torch.Tensor]:
+    """:func:`inverse_factor` of several Hessians (distinct calibration inputs) at once:
+    the first attempt of every factor runs on its own stream, concurrently; the status
+    words are read after one synchronisation and any factor that needs more damping is
+    retried as :func:`inverse_factor` would.  Same results as calling it on each."""
+    if not hss:
+        return []
+    dev = _lib.require_gpu(*hss)
+    main = torch.cuda.current_stream(dev)
+    hs32 = [h.to(torch.float32).contiguous() for h in hss]
+    us = [torch.empty_like(h) for h in hs32]
+    status = torch.empty(len(hss), dtype=torch.int32, device=dev)
+    streams = [torch.cuda.Stream(device=dev) for _ in hss]
+    for i, (h, u, st) in enumerate(zip(hs32, us, streams)):
+        st.wait_stream(main)
+        with torch.cuda.stream(st):
+            _lib.call("hi2x_chol_inv_upper_async", dev, _lib.ptr(h), h.shape[0], float(damp), 0,
+                      _lib.ptr(u), _lib.ptr(status[i:i + 1]))
+        for t in (h, u, status):
+            t.record_stream(st)
+    for st in streams:
+        main.wait_stream(st)
+    ok = status.cpu().tolist()
+    out = []
+    for h, u, stv in zip(hs32, us, ok):
+        if stv == 0x7FFFFFFF:
+            out.append(u)
+            continue
+        last = None
+        for attempt in range(1, 6):
+            try:
+                _lib.call("hi2x_chol_inv_upper", dev, _lib.ptr(h), h.shape[0], float(damp),
+                          attempt, _lib.ptr(u))
+                break
+            except _lib.NotPositiveDefinite as e:
+                last = e
+        else:
+            raise RuntimeError(f"Hessian is not factorisable even with heavy damping: {last}")
+        out.append(u)
+    return out
 
 
 @dataclass
@@ -294,12 +337,30 @@ def encode_jobs_gptq(
         if bl[-1] and sum(y.wc.numel() for y in bl[-1]) + x.wc.numel() > BATCH_ELEMS:
             bl.append([])
         bl[-1].append(x)
+    # batches of different K are independent: each runs on its own stream
+    side = []
     for (dev, _k), bl in batches.items():
         _use_kernel(dev, backend)
-        for batch in bl:
-            _round_kernel(batch, jobs, comp, super_blocks)
-            for x in batch:
-                x.wc = None  # free the working copy early
+        main = torch.cuda.current_stream(dev)
+        st = torch.cuda.Stream(device=dev) if len(batches) > 1 else main
+        if st is not main:
+            st.wait_stream(main)
+            side.append((main, st))
+        with torch.cuda.stream(st):
+            for batch in bl:
+                if st is not main:
+                    for x in batch:
+                        for t in (x.wc, x.lo_d, x.step_d, x.blk_of, jobs[x.job].u):
+                            t.record_stream(st)
+                _round_kernel(batch, jobs, comp, super_blocks)
+                for x in batch:
+                    if st is not main:
+                        x.codes.record_stream(main)
+                        if x.comp is not None:
+                            x.comp.record_stream(main)
+                    x.wc = None  # free the working copy early
+    for main, st in side:
+        main.wait_stream(st)
     per_job: list[list[Encoded]] = [[] for _ in jobs]
     for x in units:
         per_job[x.job].append(_finish(x, jobs[x.job]))

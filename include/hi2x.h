@@ -172,6 +172,14 @@ int hi2x_sigma_transform(const float* sigma, const uint16_t* col_scale, const ui
 int hi2x_chol_inv_upper(const float* hs, int64_t k, float damp, int attempt, float* u,
                         void* stream);
 
+/* Asynchronous form of hi2x_chol_inv_upper (same computation, same reference
+ * interface hi2/hessian.py:71-86): nothing is synchronised; `status` (device i32)
+ * receives 0x7fffffff when the factorisation succeeded, else 1 + the first row of the
+ * failing 128-block, once `stream` reaches it.  Lets independent factors (one per
+ * calibration input) run concurrently on separate streams. */
+int hi2x_chol_inv_upper_async(const float* hs, int64_t k, float damp, int attempt, float* u,
+                              int32_t* status, void* stream);
+
 #ifdef __cplusplus
 }
 #endif
