@@ -140,33 +140,50 @@ class StageTimer:
         return out
 
 
-def hessian_roofline(xs, reps=3):
-    """Average duration of the bf16 SYRK kernel launches, timed with HIP events on the
-    stream the kernel runs on; algorithmic work 2*T*K^2 per launch."""
-    import torch
+# kernel families timed by the library (hi2x_timing_*), with the peak that bounds each
+KERNELS = {  # kind -> (kernel, bound, peak FLOP/s, work unit)
+    0: ("gptq_trailing_kernel", "mfma", PEAK_F32, "2*rows*rank*cols"),
+    1: ("syrk2_bf16_kernel", "mfma", PEAK_BF16, "2*T*K^2"),
+    2: ("tri_gemm_kernel", "mfma", PEAK_F32, "M*N*rank (one triangular operand)"),
+    3: ("leaf_kernel", "latency", PEAK_F32, "2*n^3/3"),
+    4: ("gptq_block_kernel", "latency", PEAK_F32, "rows*L*(L-1)"),
+}
+DOMINANT = 0  # the GPTQ trailing-update GEMM: the metric's MFMA kernel with the most time
 
+
+def traffic_per_launch(kernel):
+    """HBM bytes per launch of ``kernel`` from the committed PMC summary (FETCH_SIZE +
+    WRITE_SIZE, scaled by the copy-kernel calibration), or None when not measured."""
+    path = os.path.join(ROOT, "profiles", "traffic.json")
+    try:
+        with open(path) as f:
+            rec = json.load(f).get(kernel)
+    except (OSError, ValueError):
+        return None
+    return None if rec is None else rec.get("bytes_per_launch")
+
+
+def kernel_stats(kind):
+    """Event-timed launches of one kernel family since hi2x_timing_enable."""
     from hi2_amd import _lib
 
-    dev = next(iter(xs.values())).device
-    flops, ms = 0.0, 0.0
-    for name, k in INPUTS.items():
-        x = xs[name].contiguous()
-        s = torch.zeros(k, k, dtype=torch.float32, device=dev)
-        strm = torch.cuda.current_stream(dev)
-        for r in range(reps + 1):
-            e0 = torch.cuda.Event(enable_timing=True)
-            e1 = torch.cuda.Event(enable_timing=True)
-            e0.record(strm)
-            _lib.call("hi2x_hessian_syrk", dev, _lib.ptr(x), 2, TOKENS, k, _lib.ptr(s))
-            e1.record(strm)
-            e1.synchronize()
-            if r:  # first launch is a warm-up
-                ms += e0.elapsed_time(e1)
-                flops += 2.0 * TOKENS * k * k
-    achieved = flops / (ms / 1e3)
-    return {"bound": "mfma", "kernel": "syrk_bf16_kernel", "achieved": achieved / 1e12,
-            "peak": PEAK_BF16 / 1e12, "unit": "TFLOP/s", "frac": achieved / PEAK_BF16,
-            "traffic": None, "launches": reps * len(INPUTS), "avg_ms": ms / (reps * len(INPUTS))}
+    name, bound, peak, unit = KERNELS[kind]
+    n, ms, work = _lib.timing_query(kind)
+    if n == 0 or ms <= 0.0:
+        return None
+    rate = work / (ms / 1e3)
+    return {"kernel": name, "bound": bound, "launches": n, "avg_ms": ms / n,
+            "total_ms": ms, "work_per_launch": work / n, "work_unit": unit,
+            "tflops": rate / 1e12, "frac_of_peak": rate / peak}
+
+
+def roofline(kind):
+    st = kernel_stats(kind)
+    name, bound, peak, unit = KERNELS[kind]
+    return {"bound": bound, "achieved": st["tflops"], "peak": peak / 1e12, "unit": "TFLOP/s",
+            "frac": st["frac_of_peak"], "traffic": traffic_per_launch(name), "kernel": name,
+            "launches": st["launches"], "avg_ms": st["avg_ms"],
+            "flops_per_launch": st["work_per_launch"], "work": unit}
 
 
 def cpu_baseline(seed=0):
@@ -239,6 +256,9 @@ def main():
     ap.add_argument("--steps", type=int, default=3)
     ap.add_argument("--warmup", type=int, default=1)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
+                    help="first run 3 plain device copies of MIB MiB (f32), the known-size "
+                         "reference for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU only (--gpus 1); the "
@@ -248,12 +268,23 @@ def main():
 
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
+    if args.copy_probe:
+        src = torch.ones(args.copy_probe << 18, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     xs, ws, masks = make_inputs(dev)
     torch.cuda.synchronize()
     for _ in range(args.warmup):
         encode_block(xs, ws, masks)
     torch.cuda.synchronize()
+    from hi2_amd import _lib
+
     timer = StageTimer(torch)
+    _lib.timing_enable([DOMINANT])  # HIP events around each launch of the dominant kernel
+    torch.cuda.synchronize()
     t0 = time.perf_counter()
     for i in range(args.steps):
         encode_block(xs, ws, masks, timer if i == args.steps - 1 else None)
@@ -261,7 +292,13 @@ def main():
     wall = time.perf_counter() - t0
     ms_step = wall * 1e3 / args.steps
     stages = timer.summary()
-    roof = hessian_roofline(xs)
+    roof = roofline(DOMINANT)
+    # one more, untimed step with every kernel family event-timed: per-kernel breakdown
+    _lib.timing_enable(list(KERNELS))
+    encode_block(xs, ws, masks)
+    torch.cuda.synchronize()
+    kernels = {KERNELS[k][0]: kernel_stats(k) for k in KERNELS}
+    _lib.timing_enable([])
     res = {
         "metric": "encode ms per linear layer (Llama-3-8B-shaped block, 7 linears)",
         "value": ms_step / len(LINEARS),
@@ -273,13 +310,15 @@ def main():
         "higher_is_better": False,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "fp32 (bf16 MFMA for the Hessian)",
+        "dtype": "f32",
         "data": "synthetic (seeded normal X with 1% x20 outlier channels, W ~ N(0, 0.02^2))",
         "config": {"workload": "cfg3: Llama-3-8B-shaped decoder block, 8192 calibration "
                                "tokens, 30% INT2/B32 + 70% INT4/B64 rows, order-16 Hadamard, "
-                               "damp 0.01, effort normal", "linears": len(LINEARS)},
+                               "damp 0.01, effort normal", "linears": len(LINEARS),
+                   "hessian_input_dtype": "bf16 (f32 accumulation)"},
         "stages_ms": {k: round(v, 3) for k, v in stages.items()},
         "roofline": roof,
+        "kernels_one_step": kernels,
     }
     if not args.no_cpu:
         res["cpu_baseline"] = cpu_baseline()

@@ -50,6 +50,11 @@ SIGNATURES = {
 def _bind(lib):
     lib.hi2x_version.restype = ctypes.c_int
     lib.hi2x_version.argtypes = []
+    lib.hi2x_timing_enable.restype = ctypes.c_int
+    lib.hi2x_timing_enable.argtypes = [ctypes.c_uint]
+    lib.hi2x_timing_query.restype = ctypes.c_int
+    lib.hi2x_timing_query.argtypes = [_I, ctypes.POINTER(_I64), ctypes.POINTER(ctypes.c_double),
+                                      ctypes.POINTER(ctypes.c_double)]
     lib.hi2x_last_error.restype = ctypes.c_char_p
     lib.hi2x_last_error.argtypes = []
     for name, args in SIGNATURES.items():
@@ -88,6 +93,26 @@ def lib():
     if handle is None:
         raise RuntimeError(f"hi2x HIP library unavailable: {_failed}")
     return handle
+
+
+# launch-timing kinds (HI2X_TIME_* in include/hi2x.h)
+TIME_GPTQ_TRAILING, TIME_HESSIAN_SYRK, TIME_CHOL_GEMM, TIME_CHOL_LEAF, TIME_GPTQ_BLOCK = range(5)
+
+
+def timing_enable(kinds) -> None:
+    """Start recording event-timed launches of the given kinds (empty: stop)."""
+    mask = 0
+    for k in kinds:
+        mask |= 1 << k
+    check(lib().hi2x_timing_enable(mask), "hi2x_timing_enable")
+
+
+def timing_query(kind: int) -> tuple[int, float, float]:
+    """(launches, summed event milliseconds, summed algorithmic work) of ``kind``."""
+    n, ms, work = _I64(0), ctypes.c_double(0.0), ctypes.c_double(0.0)
+    check(lib().hi2x_timing_query(kind, ctypes.byref(n), ctypes.byref(ms), ctypes.byref(work)),
+          "hi2x_timing_query")
+    return n.value, ms.value, work.value
 
 
 def last_error() -> str:

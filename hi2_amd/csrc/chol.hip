@@ -95,6 +95,8 @@ int tri_gemm(const GemmArgs& a, hipStream_t s) {
   const int64_t tm = (a.M + MG_T - 1) / MG_T, tn = (a.N + MG_T - 1) / MG_T;
   const int64_t ntiles = tm * tn;
   const int64_t grid = (ntiles + 7) / 8 * 8;
+  // every product here has one triangular operand or output: M*N*rank useful flops
+  LaunchTimer timer(HI2X_TIME_CHOL_GEMM, (double)a.M * a.N * a.Kd, s);
   hipLaunchKernelGGL((tri_gemm_kernel<AMODE, BMODE, TB, CLOW>), dim3((unsigned)grid), dim3(256),
                      0, s, a, tn, ntiles);
   return launch_status("tri_gemm_kernel");
@@ -315,6 +317,7 @@ struct Ctx {
 int inv_chol(const Ctx& c, int64_t r0, int64_t m, int depth) {
   const int64_t K = c.K;
   if (m <= NB) {
+    LaunchTimer timer(HI2X_TIME_CHOL_LEAF, 2.0 * m * m * m / 3.0, c.s);
     hipLaunchKernelGGL(leaf_kernel, dim3(1), dim3(1024), 0, c.s, c.P, K, r0, (int)m, c.status);
     return launch_status("leaf_kernel");
   }

@@ -16,6 +16,23 @@ int launch_status(const char* what);
 
 inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 
+// Launch timing (hi2x_timing_enable): while the kind is enabled, a LaunchTimer brackets
+// the launch it scopes with HIP events on the launch's stream and records its algorithmic
+// work.  Construct it right before the launch, let it go out of scope right after.
+class LaunchTimer {
+ public:
+  LaunchTimer(int kind, double work, hipStream_t s);
+  ~LaunchTimer();
+  LaunchTimer(const LaunchTimer&) = delete;
+  LaunchTimer& operator=(const LaunchTimer&) = delete;
+
+ private:
+  int kind_;
+  double work_;
+  hipStream_t s_;
+  hipEvent_t e0_ = nullptr;
+};
+
 }  // namespace hi2x
 
 #define HI2X_REQUIRE(cond, ...)          \

@@ -8,6 +8,8 @@
 
 #include <utility>
 
+#include <algorithm>
+
 #include "common.h"
 #include "mfma_gemm.h"
 
@@ -253,6 +255,7 @@ int launch_block(const float* wc, int64_t n, int64_t k, int64_t i1, int64_t len,
                  const int32_t* row_grp, const int64_t* u_ptrs, const int32_t* blk,
                  const float* nmax, float* comp, hipStream_t s) {
   const dim3 grid((unsigned)((n + RPG - 1) / RPG));
+  LaunchTimer timer(HI2X_TIME_GPTQ_BLOCK, (double)n * len * (len - 1), s);
   hipLaunchKernelGGL(gptq_block_kernel, grid, dim3(RPG * QL), 0, s, wc, n, k, i1, (int)len,
                      err1, lde, codes, lo, st, ldp, row_grp, u_ptrs, blk, nmax, comp);
   return launch_status("gptq_block_kernel");
@@ -265,6 +268,9 @@ int launch_trailing(float* wc, int64_t n, int64_t k, int64_t i1, int nblk, const
   const int64_t tn = (c1 - c0 + MG_T - 1) / MG_T, tm = (n + MG_T - 1) / MG_T;
   const int64_t ntiles = tn * tm;
   const dim3 grid((unsigned)((ntiles + 7) / 8 * 8));
+  double rank = 0.0;
+  for (int t = 0; t < nblk; ++t) rank += (double)std::min<int64_t>(LMAX, k - (i1 + (int64_t)t * LMAX));
+  LaunchTimer timer(HI2X_TIME_GPTQ_TRAILING, 2.0 * n * rank * (c1 - c0), s);
   hipLaunchKernelGGL(gptq_trailing_kernel, grid, dim3(256), 0, s, wc, n, k, i1, nblk, err1,
                      lde, c0, c1, row_grp, u_ptrs, tn, ntiles);
   return launch_status("gptq_trailing_kernel");

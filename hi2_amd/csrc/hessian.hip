@@ -424,6 +424,7 @@ int launch_syrk(const void* x, int dtype, int64_t t, int64_t k, float* s, hipStr
   if (dtype != 2) {
     const int nT = (int)((k + HT - 1) / HT);
     const int64_t tiles = (int64_t)nT * (nT + 1) / 2;
+    LaunchTimer timer(HI2X_TIME_HESSIAN_SYRK, 2.0 * t * k * k, st);
     hipLaunchKernelGGL(syrk_f32_kernel, dim3((unsigned)tiles), dim3(256), 0, st,
                        (const float*)x, t, k, nT, s);
     return launch_status("syrk_f32_kernel");
@@ -451,6 +452,7 @@ int launch_syrk(const void* x, int dtype, int64_t t, int64_t k, float* s, hipStr
   }
   if (!rc) {
     const int64_t grid = (ntiles + 7) / 8 * 8 * splits;
+    LaunchTimer timer(HI2X_TIME_HESSIAN_SYRK, 2.0 * t * k * k, st);
     hipLaunchKernelGGL(syrk2_bf16_kernel, dim3((unsigned)grid), dim3(256), 0, st, xt, tp, k, nT,
                        ntiles, splits, tchunk, splits > 1 ? parts : s, k * k);
     rc = launch_status("syrk2_bf16_kernel");

@@ -180,6 +180,25 @@ int hi2x_chol_inv_upper(const float* hs, int64_t k, float damp, int attempt, flo
 int hi2x_chol_inv_upper_async(const float* hs, int64_t k, float damp, int attempt, float* u,
                               int32_t* status, void* stream);
 
+/* ---- measurement ------------------------------------------------------------------------ */
+
+/* Launch-timing hook.  No counterpart in the reference (whose profiling is host-side
+ * timers, hi2/hessian.py stage clocks); it exists so a benchmark can time the dominant
+ * kernels with HIP events on the streams they are launched on.  While bit `kind` of
+ * `mask` is set, every launch of that kernel family is bracketed by two events on its
+ * stream and its algorithmic work recorded.  hi2x_timing_enable clears earlier records
+ * (waiting for their events); mask 0 stops recording.  Process-wide, not meant to be
+ * switched while other threads launch. */
+#define HI2X_TIME_GPTQ_TRAILING 0 /* work = 2 * rows * rank * columns (flops) */
+#define HI2X_TIME_HESSIAN_SYRK 1  /* work = 2 * tokens * k^2 (flops, full X^T X) */
+#define HI2X_TIME_CHOL_GEMM 2     /* work = flops of the triangular product */
+#define HI2X_TIME_CHOL_LEAF 3     /* work = 2 * n^3 / 3 (factor + inverse of the leaf) */
+#define HI2X_TIME_GPTQ_BLOCK 4    /* work = rows * len * (len - 1) (intra-block flops) */
+int hi2x_timing_enable(unsigned mask);
+
+/* Sum over the recorded launches of `kind`: count, event-timed milliseconds, work. */
+int hi2x_timing_query(int kind, int64_t* launches, double* ms, double* work);
+
 #ifdef __cplusplus
 }
 #endif

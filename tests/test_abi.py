@@ -26,7 +26,8 @@ def test_library_exports_every_declared_symbol():
     for name in names:
         assert hasattr(lib, name), name
     assert lib.hi2x_version() >= 100
-    assert set(_lib.SIGNATURES) | {"hi2x_version", "hi2x_last_error"} == set(names)
+    assert set(_lib.SIGNATURES) | {"hi2x_version", "hi2x_last_error", "hi2x_timing_enable",
+                                   "hi2x_timing_query"} == set(names)
 
 
 def test_raw_symbols_resolve_without_ctypes_wrappers():
@@ -49,6 +50,10 @@ def test_argument_errors_come_back_as_status_without_a_gpu():
     assert rc == _lib.EINVAL and "multiple of 16" in _lib.last_error()
     rc = lib.hi2x_pack_codes(None, 1, 30, 4, None, None, None)
     assert rc == _lib.EINVAL
+    rc = lib.hi2x_timing_query(0, None, None, None)
+    assert rc == _lib.EINVAL and "null" in _lib.last_error()
+    _lib.timing_enable([])  # nothing recorded yet: no HIP call is made
+    assert _lib.timing_query(_lib.TIME_GPTQ_TRAILING) == (0, 0.0, 0.0)
     with pytest.raises(ValueError):
         _lib.check(_lib.ERANGE, "x")
     with pytest.raises(_lib.NotPositiveDefinite):
