@@ -40,10 +40,14 @@ struct GemmArgs {
 };
 
 struct MaskLower {  // keep (r, k) with k <= r
-  __device__ __forceinline__ bool operator()(int64_t r, int64_t k) const { return k <= r; }
+  static constexpr bool kElem = true;
+  __device__ __forceinline__ bool row(int64_t) const { return true; }
+  __device__ __forceinline__ bool elem(int64_t r, int64_t k) const { return k <= r; }
 };
 struct MaskUpper {  // keep (r, k) with k >= r
-  __device__ __forceinline__ bool operator()(int64_t r, int64_t k) const { return k >= r; }
+  static constexpr bool kElem = true;
+  __device__ __forceinline__ bool row(int64_t) const { return true; }
+  __device__ __forceinline__ bool elem(int64_t r, int64_t k) const { return k >= r; }
 };
 
 template <int AMODE, int BMODE, bool TB, bool CLOW>
@@ -74,19 +78,25 @@ __global__ __launch_bounds__(256) void tri_gemm_kernel(GemmArgs g, int64_t tn, i
     ColsLoader<BMask> bl{g.B, g.ldb, g.N, kend, BMask{}};
     mg_mainloop(acc, sm, al, bl, r0, c0, kbeg, kend);
   }
+  const CTile ct(g.C, g.ldc, g.M, g.N, r0, c0);
+  f32x16 cv[2][2];
+  if (g.beta != 0.0f) {
+    ct.load(cv);
 #pragma unroll
-  for (int a = 0; a < 2; ++a)
+    for (int a = 0; a < 2; ++a)
 #pragma unroll
-    for (int b = 0; b < 2; ++b)
+      for (int b = 0; b < 2; ++b)
 #pragma unroll
-      for (int j = 0; j < 16; ++j) {
-        const int64_t row = r0 + mg_row(a, j), col = c0 + mg_col(b);
-        if (row >= g.M || col >= g.N) continue;
-        if (CLOW && col > row) continue;
-        float* cp = g.C + row * g.ldc + col;
-        const float v = g.alpha * acc[a][b][j];
-        *cp = (g.beta != 0.0f) ? *cp + v : v;
-      }
+        for (int j = 0; j < 16; ++j) cv[a][b][j] = cv[a][b][j] + g.alpha * acc[a][b][j];
+  } else {
+#pragma unroll
+    for (int a = 0; a < 2; ++a)
+#pragma unroll
+      for (int b = 0; b < 2; ++b)
+#pragma unroll
+        for (int j = 0; j < 16; ++j) cv[a][b][j] = g.alpha * acc[a][b][j];
+  }
+  ct.store(cv, [&](int a, int j, int b) { return !CLOW || c0 + mg_col(b) <= r0 + mg_row(a, j); });
 }
 
 template <int AMODE, int BMODE, bool TB, bool CLOW>

@@ -164,19 +164,22 @@ __global__ __launch_bounds__(RPG * QL) void gptq_block_kernel(
 //
 // Each product is accumulated from zero with v_mfma_f32_32x32x2_f32, which evaluates
 // fma(a1, b1, fma(a0, b0, acc)) in k order: the same sequential fp32 FMA chain as the
-// reference's CPU GEMM, then one subtraction per block.  The wc tile stays in registers
-// across the nblk blocks (lazy batching of the far columns) and every block's product
-// is subtracted separately, so the result equals the per-block schedule bit for bit.
+// reference's CPU GEMM, then one subtraction per block.  One launch applies the nblk
+// blocks of a super-block to the far columns (lazy batching: the wc tile stays in L2
+// between them) and every block's product is subtracted separately, in block order, so
+// the result equals the per-block schedule bit for bit.
 // Workgroup tile 128 x 128 (4 waves as 2 x 2 of 64 x 64), rank streamed in chunks of
 // 16 through LDS.  Rows of another group than the pass's are masked in A and left
 // untouched in the epilogue.
 // ---------------------------------------------------------------------------------
 struct GroupMask {  // A rows of the current group pass (this thread's staged row)
+  static constexpr bool kElem = false;
   bool mine;
-  __device__ __forceinline__ bool operator()(int64_t, int64_t) const { return mine; }
+  __device__ __forceinline__ bool row(int64_t) const { return mine; }
+  __device__ __forceinline__ bool elem(int64_t, int64_t) const { return true; }
 };
 
-__global__ __launch_bounds__(256) void gptq_trailing_kernel(
+__global__ __launch_bounds__(256, 2) void gptq_trailing_kernel(
     float* __restrict__ wc, int64_t N, int64_t K, int64_t i1, int nblk,
     const float* __restrict__ err1, int64_t lde, int64_t c0, int64_t c1,
     const int32_t* __restrict__ row_grp, const int64_t* __restrict__ u_ptrs, int64_t tn,
@@ -191,20 +194,7 @@ __global__ __launch_bounds__(256) void gptq_trailing_kernel(
   const int tid = threadIdx.x;
   const int64_t my_row = r0 + (tid >> 1);  // row this thread stages for the A operand
   const int my_grp = my_row < N ? row_grp[my_row] : -1;
-
-  // the working-copy tile stays in registers (accumulator layout) for all blocks
-  f32x16 cv[2][2];
-#pragma unroll
-  for (int a = 0; a < 2; ++a)
-#pragma unroll
-    for (int b = 0; b < 2; ++b) {
-      const int64_t cc = cc0 + mg_col(b);
-#pragma unroll
-      for (int j = 0; j < 16; ++j) {
-        const int64_t rr = r0 + mg_row(a, j);
-        cv[a][b][j] = (rr < N && cc < c1) ? wc[rr * K + cc] : 0.0f;
-      }
-    }
+  const CTile ct(wc, K, N, c1, r0, cc0);
 
   for (int g = g0; g <= g1; ++g) {
     const float* U = reinterpret_cast<const float*>(u_ptrs[g]);
@@ -216,38 +206,31 @@ __global__ __launch_bounds__(256) void gptq_trailing_kernel(
       RowsLoader<GroupMask> al{err1 + t * LMAX, lde, N, L, GroupMask{my_grp == g}};
       ColsLoader<NoMask> bl{U + ib * K, K, c1, L, NoMask{}};
       mg_mainloop(acc, sm, al, bl, r0, cc0, 0, L);
+      // wc tile -= this block's product (read-modify-write: the tile is not held in
+      // registers across the rank loop, which keeps two workgroups per CU resident)
+      f32x16 cv[2][2];
+      ct.load(cv);
+#pragma unroll
+      for (int a = 0; a < 2; ++a)
+#pragma unroll
+        for (int b = 0; b < 2; ++b)
+#pragma unroll
+          for (int j = 0; j < 16; ++j) cv[a][b][j] = cv[a][b][j] - acc[a][b][j];
       if (g0 == g1) {
-#pragma unroll
-        for (int a = 0; a < 2; ++a)
-#pragma unroll
-          for (int b = 0; b < 2; ++b)
-#pragma unroll
-            for (int j = 0; j < 16; ++j) cv[a][b][j] = cv[a][b][j] - acc[a][b][j];
-      } else {
+        ct.store(cv, [](int, int, int) { return true; });
+      } else {  // a tile shared by two factors: bit a*16+j = row (a, j) is in group g
+        uint32_t in_g = 0;
 #pragma unroll
         for (int a = 0; a < 2; ++a)
 #pragma unroll
           for (int j = 0; j < 16; ++j) {
             const int64_t rr = r0 + mg_row(a, j);
-            const bool mine = rr < N && row_grp[rr] == g;
-#pragma unroll
-            for (int b = 0; b < 2; ++b)
-              cv[a][b][j] = mine ? cv[a][b][j] - acc[a][b][j] : cv[a][b][j];
+            in_g |= (uint32_t)(rr < N && row_grp[rr] == g) << (a * 16 + j);
           }
+        ct.store(cv, [&](int a, int j, int) { return (in_g >> (a * 16 + j)) & 1u; });
       }
     }
   }
-#pragma unroll
-  for (int a = 0; a < 2; ++a)
-#pragma unroll
-    for (int b = 0; b < 2; ++b) {
-      const int64_t cc = cc0 + mg_col(b);
-#pragma unroll
-      for (int j = 0; j < 16; ++j) {
-        const int64_t rr = r0 + mg_row(a, j);
-        if (rr < N && cc < c1) wc[rr * K + cc] = cv[a][b][j];
-      }
-    }
 }
 
 int launch_block(const float* wc, int64_t n, int64_t k, int64_t i1, int64_t len, float* err1,

@@ -9,8 +9,9 @@
 // fma(a1, b1, fma(a0, b0, acc)), so every element of the product is the sequential
 // fp32 FMA chain over k.
 //
-// Operand access is through small loader structs so that triangular operands can mask
-// their structural zeros (never reading the unused triangle) and edges can be guarded.
+// Operand access is through small loader structs: edges and masked rows read as zero
+// through the buffer-load range check, and triangular operands zero their structural
+// zeros when a chunk is staged, so the unused triangle never enters a product.
 #pragma once
 #include "common.h"
 
@@ -30,90 +31,99 @@ struct MgSmem {
   float B[2][MG_T][MG_RP];
 };
 
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+// Operand fetches go through buffer loads whose resource covers exactly the valid part
+// of the chunk's panel: an access past it returns zero without touching memory, so the
+// loads need no branches (a branch around a load makes the compiler wait for it right
+// there, before the MFMAs, instead of after them).  Offsets stay far below 2^31.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t mg_rsrc(const float* base, int64_t nfloats) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(base), (short)0,
+                                           (int)(nfloats * 4), 0x00020000);
+}
+__device__ __forceinline__ f32x4 mg_load4(__amdgpu_buffer_rsrc_t r, uint32_t byte_off) {
+  return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)byte_off, 0, 0));
+}
+constexpr uint32_t MG_OOB = 0x80000000u;  // byte offset past every panel: reads as zero
+
+// Masks: row(r) drops a whole staged row (applied through the load offset); elem(r, k)
+// drops single elements (applied when the chunk is written to LDS, after the MFMAs).
+struct NoMask {
+  static constexpr bool kElem = false;
+  __device__ __forceinline__ bool row(int64_t) const { return true; }
+  __device__ __forceinline__ bool elem(int64_t, int64_t) const { return true; }
+};
+
 // Row-major operand X[r][k] (k contiguous), read as "rows" of the tile: the A operand,
-// or the B operand of a transposed product (op(B) = X^T).  mask(r, k) -> keep.
-// Thread t stages row t/2, 16 consecutive k starting at 16*(t%2).
+// or the B operand of a transposed product (op(B) = X^T).  Rows >= nrows and k >= kend
+// read as zero.  Thread t stages row t/2, 16 consecutive k starting at 16*(t%2).
 template <class Mask>
 struct RowsLoader {
   const float* p;
   int64_t ld, nrows, kend;
   Mask mask;
-  __device__ __forceinline__ void load(int64_t r0, int64_t k0, int tid, float (&st)[16]) const {
-    const int64_t r = r0 + (tid >> 1);
-    const int64_t kb = k0 + 16 * (tid & 1);
-    const bool rok = r < nrows;
-    const float* src = p + r * ld + kb;
-    const bool vec = rok && kb + 16 <= kend && ((reinterpret_cast<uintptr_t>(src) & 15) == 0);
-    if (vec) {
+  __device__ __forceinline__ void load(int64_t r0, int64_t k0, int tid, f32x4 (&st)[4]) const {
+    const int64_t rows = (nrows - r0 < MG_T) ? nrows - r0 : MG_T;
+    const int64_t kv = kend - k0;
+    // last valid element of the panel: row rows-1, column kend-1
+    const __amdgpu_buffer_rsrc_t rs = mg_rsrc(p + r0 * ld + k0, (rows - 1) * ld + kv);
+    const int rr = tid >> 1;
+    uint32_t off = (uint32_t)((rr * ld + 16 * (tid & 1)) * 4);
+    off = (rr < rows && mask.row(r0 + rr)) ? off : MG_OOB;
 #pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        const float4 x = *reinterpret_cast<const float4*>(src + 4 * v);
-        st[4 * v] = x.x;
-        st[4 * v + 1] = x.y;
-        st[4 * v + 2] = x.z;
-        st[4 * v + 3] = x.w;
-      }
-#pragma unroll
-      for (int e = 0; e < 16; ++e) st[e] = mask(r, kb + e) ? st[e] : 0.0f;
-    } else {
-#pragma unroll
-      for (int e = 0; e < 16; ++e)
-        st[e] = (rok && kb + e < kend && mask(r, kb + e)) ? src[e] : 0.0f;
-    }
+    for (int v = 0; v < 4; ++v) st[v] = mg_load4(rs, off + 16 * v);
   }
-  // k = 16h + e -> parity e & 1, pair 8h + e / 2
-  __device__ __forceinline__ static void store(float (*S)[MG_RP], int tid, const float (&st)[16]) {
+  // k = 16h + e -> parity e & 1, pair 8h + e / 2.  Elements at k >= kend of rows before
+  // the last are real memory of the next columns: zeroed here.
+  __device__ __forceinline__ void store(float (*S)[MG_RP], int64_t r0, int64_t k0, int tid,
+                                        f32x4 (&st)[4]) const {
     const int m = tid >> 1, h = tid & 1;
+    const int64_t kb = k0 + 16 * h;
+    if (Mask::kElem || k0 + MG_KC > kend) {
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const bool keep = kb + e < kend && mask.elem(r0 + m, kb + e);
+        st[e >> 2][e & 3] = keep ? st[e >> 2][e & 3] : 0.0f;
+      }
+    }
 #pragma unroll
     for (int par = 0; par < 2; ++par) {
       float* d = &S[m][par * MG_KP + 8 * h];
-      *reinterpret_cast<float4*>(d) = make_float4(st[par], st[par + 2], st[par + 4], st[par + 6]);
+      *reinterpret_cast<float4*>(d) =
+          make_float4(st[0][par], st[0][par + 2], st[1][par], st[1][par + 2]);
       *reinterpret_cast<float4*>(d + 4) =
-          make_float4(st[par + 8], st[par + 10], st[par + 12], st[par + 14]);
+          make_float4(st[2][par], st[2][par + 2], st[3][par], st[3][par + 2]);
     }
   }
 };
 
 // Row-major operand X[k][c] (c contiguous) read as the B operand of a plain product.
-// Thread t stages k = t%32 and 16 consecutive columns starting at 16*(t/32).
+// k >= kend reads as zero; columns >= ncols feed only output columns that are never
+// stored.  Thread t stages k = t%32 and 16 consecutive columns starting at 16*(t/32).
 template <class Mask>
 struct ColsLoader {
   const float* p;
   int64_t ld, ncols, kend;
   Mask mask;
-  __device__ __forceinline__ void load(int64_t c0, int64_t k0, int tid, float (&st)[16]) const {
-    const int64_t k = k0 + (tid & 31);
-    const int64_t cb = c0 + 16 * (tid >> 5);
-    const bool kok = k < kend;
-    const float* src = p + k * ld + cb;
-    const bool vec = kok && cb + 16 <= ncols && ((reinterpret_cast<uintptr_t>(src) & 15) == 0);
-    if (vec) {
+  __device__ __forceinline__ void load(int64_t c0, int64_t k0, int tid, f32x4 (&st)[4]) const {
+    const int64_t kv = (kend - k0 < MG_KC) ? kend - k0 : MG_KC;
+    const __amdgpu_buffer_rsrc_t rs = mg_rsrc(p + k0 * ld + c0, (kv - 1) * ld + (ncols - c0));
+    const uint32_t off = (uint32_t)(((tid & 31) * ld + 16 * (tid >> 5)) * 4);
 #pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        const float4 x = *reinterpret_cast<const float4*>(src + 4 * v);
-        st[4 * v] = x.x;
-        st[4 * v + 1] = x.y;
-        st[4 * v + 2] = x.z;
-        st[4 * v + 3] = x.w;
-      }
-#pragma unroll
-      for (int e = 0; e < 16; ++e) st[e] = mask(k, cb + e) ? st[e] : 0.0f;
-    } else {
+    for (int v = 0; v < 4; ++v) st[v] = mg_load4(rs, off + 16 * v);
+  }
+  __device__ __forceinline__ void store(float (*S)[MG_RP], int64_t c0, int64_t k0, int tid,
+                                        f32x4 (&st)[4]) const {
+    const int kk = tid & 31, cb = 16 * (tid >> 5);
+    if (Mask::kElem) {
 #pragma unroll
       for (int e = 0; e < 16; ++e)
-        st[e] = (kok && cb + e < ncols && mask(k, cb + e)) ? src[e] : 0.0f;
+        st[e >> 2][e & 3] = mask.elem(k0 + kk, c0 + cb + e) ? st[e >> 2][e & 3] : 0.0f;
     }
-  }
-  __device__ __forceinline__ static void store(float (*S)[MG_RP], int tid, const float (&st)[16]) {
-    const int kk = tid & 31, cb = 16 * (tid >> 5);
     const int off = (kk & 1) * MG_KP + (kk >> 1);
 #pragma unroll
-    for (int e = 0; e < 16; ++e) S[cb + e][off] = st[e];
+    for (int e = 0; e < 16; ++e) S[cb + e][off] = st[e >> 2][e & 3];
   }
-};
-
-struct NoMask {
-  __device__ __forceinline__ bool operator()(int64_t, int64_t) const { return true; }
 };
 
 __device__ __forceinline__ void mg_zero(f32x16 (&acc)[2][2]) {
@@ -125,8 +135,45 @@ __device__ __forceinline__ void mg_zero(f32x16 (&acc)[2][2]) {
       for (int j = 0; j < 16; ++j) acc[a][b][j] = 0.0f;
 }
 
+// The 64 MFMAs of one LDS chunk (16 k-pairs x 2 x 2 tiles), in k order.  Operands are
+// read in 4 groups of 4 k-pairs (one ds_read_b128 per operand and group) with the next
+// group's reads issued before the current group's MFMAs.
+__device__ __forceinline__ void mg_chunk(f32x16 (&acc)[2][2], const float (*A)[MG_RP],
+                                         const float (*B)[MG_RP], int wr, int wcn, int par,
+                                         int lr) {
+  const float* pa[2] = {&A[wr * 64 + lr][par * MG_KP], &A[wr * 64 + 32 + lr][par * MG_KP]};
+  const float* pb[2] = {&B[wcn * 64 + lr][par * MG_KP], &B[wcn * 64 + 32 + lr][par * MG_KP]};
+  f32x4 av[2][2], bv[2][2];  // [set][tile]
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    av[0][t] = *reinterpret_cast<const f32x4*>(pa[t]);
+    bv[0][t] = *reinterpret_cast<const f32x4*>(pb[t]);
+  }
+#pragma unroll
+  for (int g = 0; g < MG_KP / 4; ++g) {
+    const int cur = g & 1;
+    if (g + 1 < MG_KP / 4) {
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        av[cur ^ 1][t] = *reinterpret_cast<const f32x4*>(pa[t] + 4 * (g + 1));
+        bv[cur ^ 1][t] = *reinterpret_cast<const f32x4*>(pb[t] + 4 * (g + 1));
+      }
+    }
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+#pragma unroll
+      for (int a = 0; a < 2; ++a)
+#pragma unroll
+        for (int b = 0; b < 2; ++b)
+          acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[cur][a][q], bv[cur][b][q],
+                                                          acc[a][b], 0, 0, 0);
+  }
+}
+
 // acc += A[r0:r0+128, kbeg:kend] * op(B)[kbeg:kend, c0:c0+128], rank chunks in order.
-// kbeg must be a multiple of 2 (MFMA k-pairs); loaders mask everything beyond kend.
+// kbeg must be a multiple of 2 (MFMA k-pairs); loaders zero everything beyond kend.
+// Per chunk: the next chunk's global loads are issued first, the chunk's MFMAs run from
+// LDS, and only then are the loaded values masked and written to the other LDS buffer.
 template <class AL, class BL>
 __device__ __forceinline__ void mg_mainloop(f32x16 (&acc)[2][2], MgSmem& sm, const AL& al,
                                             const BL& bl, int64_t r0, int64_t c0,
@@ -135,56 +182,27 @@ __device__ __forceinline__ void mg_mainloop(f32x16 (&acc)[2][2], MgSmem& sm, con
   const int wr = wave >> 1, wcn = wave & 1;
   if (kend <= kbeg) return;
   const int nch = (int)((kend - kbeg + MG_KC - 1) / MG_KC);
-  float sa[16], sb[16];
+  f32x4 sa[4], sb[4];
   al.load(r0, kbeg, tid, sa);
   bl.load(c0, kbeg, tid, sb);
   __syncthreads();  // the previous use of the LDS buffers is over
-  AL::store(sm.A[0], tid, sa);
-  BL::store(sm.B[0], tid, sb);
+  al.store(sm.A[0], r0, kbeg, tid, sa);
+  bl.store(sm.B[0], c0, kbeg, tid, sb);
   __syncthreads();
   const int par = lane >> 5, lr = lane & 31;
   for (int ch = 0; ch < nch; ++ch) {
     const int buf = ch & 1;
-    if (ch + 1 < nch) {
-      al.load(r0, kbeg + (int64_t)(ch + 1) * MG_KC, tid, sa);
-      bl.load(c0, kbeg + (int64_t)(ch + 1) * MG_KC, tid, sb);
+    const int64_t kn = kbeg + (int64_t)(ch + 1) * MG_KC;
+    const bool more = ch + 1 < nch;
+    if (more) {
+      al.load(r0, kn, tid, sa);
+      bl.load(c0, kn, tid, sb);
     }
-    // this lane's operands for all 16 k-pairs of the chunk
-    float av[2][MG_KP], bv[2][MG_KP];
-#pragma unroll
-    for (int a = 0; a < 2; ++a) {
-      const float* src = &sm.A[buf][wr * 64 + a * 32 + lr][par * MG_KP];
-#pragma unroll
-      for (int q = 0; q < MG_KP / 4; ++q) {
-        const float4 x = *reinterpret_cast<const float4*>(src + 4 * q);
-        av[a][4 * q] = x.x;
-        av[a][4 * q + 1] = x.y;
-        av[a][4 * q + 2] = x.z;
-        av[a][4 * q + 3] = x.w;
-      }
-    }
-#pragma unroll
-    for (int b = 0; b < 2; ++b) {
-      const float* src = &sm.B[buf][wcn * 64 + b * 32 + lr][par * MG_KP];
-#pragma unroll
-      for (int q = 0; q < MG_KP / 4; ++q) {
-        const float4 x = *reinterpret_cast<const float4*>(src + 4 * q);
-        bv[b][4 * q] = x.x;
-        bv[b][4 * q + 1] = x.y;
-        bv[b][4 * q + 2] = x.z;
-        bv[b][4 * q + 3] = x.w;
-      }
-    }
-#pragma unroll
-    for (int kp = 0; kp < MG_KP; ++kp)
-#pragma unroll
-      for (int a = 0; a < 2; ++a)
-#pragma unroll
-        for (int b = 0; b < 2; ++b)
-          acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[a][kp], bv[b][kp], acc[a][b], 0, 0, 0);
-    if (ch + 1 < nch) {  // buffer buf ^ 1 was last read before the previous barrier
-      AL::store(sm.A[buf ^ 1], tid, sa);
-      BL::store(sm.B[buf ^ 1], tid, sb);
+    mg_chunk(acc, sm.A[buf], sm.B[buf], wr, wcn, par, lr);
+    __builtin_amdgcn_sched_barrier(0);
+    if (more) {  // buffer buf ^ 1 was last read before the previous barrier
+      al.store(sm.A[buf ^ 1], r0, kn, tid, sa);
+      bl.store(sm.B[buf ^ 1], c0, kn, tid, sb);
     }
     __syncthreads();
   }
@@ -200,6 +218,70 @@ __device__ __forceinline__ int mg_col(int b) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   return (wave & 1) * 64 + b * 32 + (lane & 31);
 }
+
+// The 128 x 128 tile of a row-major [nrows, ncols] matrix at (r0, c0), accessed in the
+// accumulator layout through a buffer resource that ends at the tile's last valid element:
+// loads are branch-free (rows past the end read zero, columns past the end of rows before
+// the last read real memory that is never stored back), stores drop every element the
+// predicate rejects or that lies outside [nrows, ncols).
+//
+// Offsets are one per-lane base plus a uniform term per register; the base passes
+// through an empty asm so the 64 offsets are rebuilt at each access instead of being
+// hoisted out of the caller's loops and held in registers across them.
+struct CTile {
+  __amdgpu_buffer_rsrc_t rs;
+  int64_t ld;
+  uint32_t vbase;  // byte offset of this lane's (row 0, column 0) element
+  int rows, cols;
+  __device__ __forceinline__ CTile(float* p, int64_t ld_, int64_t nrows, int64_t ncols,
+                                   int64_t r0, int64_t c0)
+      : ld(ld_) {
+    rows = (int)((nrows - r0 < MG_T) ? nrows - r0 : MG_T);
+    cols = (int)((ncols - c0 < MG_T) ? ncols - c0 : MG_T);
+    rs = mg_rsrc(p + r0 * ld + c0, (int64_t)(rows - 1) * ld + cols);
+    vbase = (uint32_t)(((int64_t)mg_row(0, 0) * ld + mg_col(0)) * 4);
+  }
+  // byte offset of register j of tile (a, b) relative to vbase (uniform)
+  __device__ __forceinline__ uint32_t uoff(int a, int b, int j) const {
+    return (uint32_t)(((int64_t)(a * 32 + 8 * (j >> 2) + (j & 3)) * ld + b * 32) * 4);
+  }
+  __device__ __forceinline__ uint32_t base() const {
+    uint32_t v = vbase;
+    asm volatile("" : "+v"(v));
+    return v;
+  }
+  __device__ __forceinline__ void load(f32x16 (&v)[2][2]) const {
+    const uint32_t vb = base();
+#pragma unroll
+    for (int a = 0; a < 2; ++a)
+#pragma unroll
+      for (int b = 0; b < 2; ++b)
+#pragma unroll
+        for (int j = 0; j < 16; ++j)
+          v[a][b][j] = __builtin_bit_cast(
+              float, __builtin_amdgcn_raw_buffer_load_b32(rs, (int)(vb + uoff(a, b, j)), 0, 0));
+  }
+  // keep(a, j, b): predicate for register j of tile (a, b) (rows and columns outside the
+  // matrix are dropped regardless)
+  template <class Keep>
+  __device__ __forceinline__ void store(const f32x16 (&v)[2][2], Keep keep) const {
+    const uint32_t vb = base();
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+      const bool cok = mg_col(b) < cols;
+#pragma unroll
+      for (int a = 0; a < 2; ++a)
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+          const uint32_t o = (cok && keep(a, j, b)) ? vb + uoff(a, b, j) : MG_OOB;
+          // copy the element to a scalar first: this compiler's __builtin_bit_cast of a
+          // vector-element lvalue reads element 0
+          const float x = v[a][b][j];
+          __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(x), rs, (int)o, 0, 0);
+        }
+    }
+  }
+};
 
 // Workgroup -> tile mapping that keeps neighbouring tiles on one XCD: workgroups are
 // dispatched round-robin over the 8 XCDs, so linear id i runs on XCD i % 8; give XCD x
