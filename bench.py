@@ -64,79 +64,110 @@ def make_inputs(dev, seed=0):
         perm = torch.randperm(n, generator=g, device=dev)
         m = torch.zeros(n, dtype=torch.bool, device=dev)
         m[perm[: int(round(INT2_FRAC * n))]] = True
-        masks[name] = m  # True = INT2 row
+        # the allocation (fixed input of the encode): INT2 rows, INT4 rows, per-row tables
+        masks[name] = {
+            "r2": m.nonzero().flatten(),
+            "r4": (~m).nonzero().flatten(),
+            "nbits": torch.where(m, 2, 4).cpu(),
+            "block": torch.where(m, 32, 64).cpu(),
+        }
     return xs, ws, masks
 
 
+ORDER = ["down", "mlp", "attn", "o"]  # calibration inputs, longest chain first
+_CHAIN_STREAMS = {}
+
+
+def _chain_stream(dev, i):
+    """One persistent stream per chain (reused every step, so each keeps its cached
+    device blocks; the library's own side streams are separate)."""
+    import torch
+
+    key = (dev.index, i)
+    if key not in _CHAIN_STREAMS:
+        _CHAIN_STREAMS[key] = torch.cuda.Stream(device=dev)
+    return _CHAIN_STREAMS[key]
+
+
 def encode_block(xs, ws, masks, timer=None):
+    """Encode the whole block.  Each calibration input runs its own chain on its own
+    stream (Hessian -> transform -> factor -> rotation -> GPTQ -> packing of the linears
+    it feeds); the chains are independent, so they overlap on the GPU.  The host waits
+    only after every chain has been enqueued (factor status, packing's range check)."""
     import torch
 
     from hi2_amd.format import assemble, fwht_groups
-    from hi2_amd.hessian import GptqJob, HessianStats, encode_jobs_gptq, inverse_factors
-    from hi2_amd.hessian import transform_sigma
+    from hi2_amd.hessian import GptqJob, HessianStats, encode_jobs_gptq
+    from hi2_amd.hessian import finish_factor, inverse_factor_async, transform_sigma
 
     dev = next(iter(xs.values())).device
-    hss, meta = [], []
-    for name, k in INPUTS.items():
-        had = torch.ones(k // 16, dtype=torch.uint8, device=dev)
-        if timer:
-            timer.mark(f"hessian_{name}")
-        st = HessianStats(k, dev)
-        st.update(xs[name])
-        if timer:
-            timer.mark(f"transform_{name}")
-        hs = transform_sigma(st.mean(), None, had)
-        hss.append(hs)
-        meta.append((name, hs.diagonal().clone(), had))
-    if timer:
-        timer.mark("factor")
-    us = inverse_factors(hss, DAMP)  # the four factors run concurrently
-    factors = {name: (d, u, had) for (name, d, had), u in zip(meta, us)}
-    if timer:
-        timer.mark("rotate")
-    jobs, where = [], []
-    for name, n, k, inp in LINEARS:
-        d, u, had = factors[inp]
-        wt = fwht_groups(ws[name].float(), had)
-        r2 = masks[name].nonzero().flatten()
-        r4 = (~masks[name]).nonzero().flatten()
-        jobs.append(GptqJob(wt.index_select(0, r2), d, u, 2, 32))
-        where.append((name, r2))
-        jobs.append(GptqJob(wt.index_select(0, r4), d, u, 4, 64))
-        where.append((name, r4))
-    if timer:
-        timer.mark("gptq")
-    encs = encode_jobs_gptq(jobs, EFFORT)
-    if timer:
-        timer.mark("pack")
+    main = torch.cuda.current_stream(dev)
+    chains = {}
+    for ci, inp in enumerate(ORDER):
+        k = INPUTS[inp]
+        st = _chain_stream(dev, ci)
+        st.wait_stream(main)
+        mark = (lambda stage, inp=inp: timer.mark(inp, stage)) if timer else (lambda stage: None)
+        with torch.cuda.stream(st):
+            had = torch.ones(k // 16, dtype=torch.uint8, device=dev)
+            mark("hessian")
+            hst = HessianStats(k, dev)
+            hst.update(xs[inp])
+            mark("transform")
+            hs = transform_sigma(hst.mean(), None, had)
+            d = hs.diagonal().clone()
+            mark("factor")
+            u, status = inverse_factor_async(hs, DAMP)
+            mark("rotate")
+            jobs, where = [], []
+            for name, n, kk, i in LINEARS:
+                if i != inp:
+                    continue
+                wt = fwht_groups(ws[name].float(), had)
+                r2, r4 = masks[name]["r2"], masks[name]["r4"]
+                jobs.append(GptqJob(wt.index_select(0, r2), d, u, 2, 32))
+                where.append((name, r2))
+                jobs.append(GptqJob(wt.index_select(0, r4), d, u, 4, 64))
+                where.append((name, r4))
+            mark("gptq")
+            encs = encode_jobs_gptq(jobs, EFFORT)
+            mark("end")
+        chains[inp] = (st, hs, u, status, had, jobs, where, encs)
     out = {}
-    for name, n, k, inp in LINEARS:
-        pieces = [(rows, e.codes, e.params, e.consts)
-                  for (nm, rows), e in zip(where, encs) if nm == name]
-        nbits = torch.where(masks[name], 2, 4).cpu()
-        block = torch.where(masks[name], 32, 64).cpu()
-        out[name] = assemble(pieces, nbits, block, factors[inp][2], k, stager=_DeviceStager)
-    if timer:
-        timer.mark("end")
+    for inp in reversed(ORDER):  # shortest chains finish first: pack them meanwhile
+        st, hs, u, status, had, jobs, where, encs = chains[inp]
+        with torch.cuda.stream(st):
+            if finish_factor(hs, u, status, DAMP):  # more damping was needed: redo the rounding
+                encs = encode_jobs_gptq(jobs, EFFORT)
+            for name, n, k, i in LINEARS:
+                if i != inp:
+                    continue
+                pieces = [(rows, e.codes, e.params, e.consts)
+                          for (nm, rows), e in zip(where, encs) if nm == name]
+                out[name] = assemble(pieces, masks[name]["nbits"], masks[name]["block"], had, k,
+                                     stager=_DeviceStager)
+        main.wait_stream(st)
     return out
 
 
 class StageTimer:
+    """Events on each chain's stream at its stage boundaries."""
+
     def __init__(self, torch):
         self.torch = torch
-        self.events = []
+        self.events = {}
 
-    def mark(self, name):
+    def mark(self, chain, stage):
         e = self.torch.cuda.Event(enable_timing=True)
         e.record()
-        self.events.append((name, e))
+        self.events.setdefault(chain, []).append((stage, e))
 
     def summary(self):
         self.torch.cuda.synchronize()
         out = {}
-        for (n0, e0), (_, e1) in zip(self.events, self.events[1:]):
-            key = n0.split("_")[0]
-            out[key] = out.get(key, 0.0) + e0.elapsed_time(e1)
+        for chain, evs in self.events.items():
+            out[chain] = {n0: round(e0.elapsed_time(e1), 3)
+                          for (n0, e0), (_, e1) in zip(evs, evs[1:])}
         return out
 
 
@@ -316,7 +347,7 @@ def main():
                                "tokens, 30% INT2/B32 + 70% INT4/B64 rows, order-16 Hadamard, "
                                "damp 0.01, effort normal", "linears": len(LINEARS),
                    "hessian_input_dtype": "bf16 (f32 accumulation)"},
-        "stages_ms": {k: round(v, 3) for k, v in stages.items()},
+        "chain_stages_ms": stages,
         "roofline": roof,
         "kernels_one_step": kernels,
     }

@@ -39,11 +39,16 @@ SIGNATURES = {
     "hi2x_fwht16": [_P, _P, _I, _I64, _I64, _P, _P],
     "hi2x_pack_codes": [_P, _I64, _I64, _I, _P, _P, _P],
     "hi2x_assemble_piece": [_P, _I64, _P, _P, _P, _I64, _I, _I64, _P, _P, _P, _P, _P, _P, _P],
-    "hi2x_hessian_syrk": [_P, _I, _I64, _I64, _P, _P],
-    "hi2x_hessian_syrk_varlen": [_P, _I, _P, _I64, _I64, _P, _P],
+    "hi2x_hessian_syrk": [_P, _I, _I64, _I64, _P, _P, _I64, _P],
+    "hi2x_hessian_syrk_varlen": [_P, _I, _P, _I64, _I64, _P, _P, _I64, _P],
     "hi2x_sigma_transform": [_P, _P, _P, _I64, _P, _P],
-    "hi2x_chol_inv_upper": [_P, _I64, _F, _I, _P, _P],
-    "hi2x_chol_inv_upper_async": [_P, _I64, _F, _I, _P, _P, _P],
+    "hi2x_chol_inv_upper": [_P, _I64, _F, _I, _P, _P, _I64, _P],
+    "hi2x_chol_inv_upper_async": [_P, _I64, _F, _I, _P, _P, _P, _I64, _P],
+}
+# workspace sizes (int64 bytes, -1 for bad arguments): name -> argtypes
+SIZES = {
+    "hi2x_hessian_workspace_bytes": [_I, _I64, _I64],
+    "hi2x_chol_workspace_bytes": [_I64],
 }
 
 
@@ -60,6 +65,10 @@ def _bind(lib):
     for name, args in SIGNATURES.items():
         fn = getattr(lib, name)
         fn.restype = ctypes.c_int
+        fn.argtypes = args
+    for name, args in SIZES.items():
+        fn = getattr(lib, name)
+        fn.restype = ctypes.c_int64
         fn.argtypes = args
     return lib
 
@@ -161,6 +170,40 @@ def ptr(t: torch.Tensor | None):
 
 def stream(dev: torch.device):
     return ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+
+
+_streams: dict = {}
+
+
+def side_stream(dev: torch.device, i: int) -> torch.cuda.Stream:
+    """The i-th persistent side stream of ``dev`` (default priority).  Reusing the same
+    streams keeps torch's per-stream cached blocks warm: a fresh stream per call would
+    make the caching allocator go back to the driver, which can synchronise the device."""
+    key = (torch.device(dev).index, i)
+    st = _streams.get(key)
+    if st is None:
+        with _lock:
+            st = _streams.get(key)
+            if st is None:
+                st = torch.cuda.Stream(device=dev)
+                _streams[key] = st
+    return st
+
+
+def h2d(t: torch.Tensor, dev: torch.device) -> torch.Tensor:
+    """Host tensor to the device without blocking the host: staged through pinned
+    memory (torch's pinned allocator keeps the buffer until the copy has run)."""
+    return t.contiguous().pin_memory().to(dev, non_blocking=True)
+
+
+def workspace(dev: torch.device, size_fn: str, *args) -> torch.Tensor:
+    """A device workspace for an entry point, from torch's caching allocator on the
+    current stream (so concurrent streams never share a block): ``size_fn`` is the
+    library's size query for that entry point."""
+    n = getattr(lib(), size_fn)(*args)
+    if n < 0:
+        raise RuntimeError(f"{size_fn}{args}: bad arguments")
+    return torch.empty(max(int(n), 1), dtype=torch.uint8, device=dev)
 
 
 def call(name: str, dev: torch.device, *args) -> None:

@@ -360,25 +360,27 @@ int inv_chol(const Ctx& c, int64_t r0, int64_t m, int depth) {
 
 using namespace hi2x;
 
-static int chol_launch(const float* hs, int64_t k, float damp, int attempt, float* u,
-                       int* status_out, hipStream_t s) {
+// Workspace layout (floats): the recursion's T1 (one per depth) and T2, then lam and the
+// status word of the synchronous entry.
+static Plan make_plan(int64_t k) {
   Plan plan;
-  {
-    std::vector<int64_t> t1;
-    int64_t t2 = 0;
-    plan_sizes(k, 0, t1, t2);
-    int64_t off = 0;
-    for (int64_t sz : t1) {
-      plan.t1_off.push_back(off);
-      off += (sz + 63) / 64 * 64;
-    }
-    plan.t2_off = off;
-    plan.total = off + (t2 + 63) / 64 * 64;
+  std::vector<int64_t> t1;
+  int64_t t2 = 0;
+  plan_sizes(k, 0, t1, t2);
+  int64_t off = 0;
+  for (int64_t sz : t1) {
+    plan.t1_off.push_back(off);
+    off += (sz + 63) / 64 * 64;
   }
-  float* ws = nullptr;
-  float* lam = nullptr;
-  if (plan.total) HI2X_HIP(hipMallocAsync((void**)&ws, (size_t)plan.total * sizeof(float), s));
-  HI2X_HIP(hipMallocAsync((void**)&lam, sizeof(float), s));
+  plan.t2_off = off;
+  plan.total = off + (t2 + 63) / 64 * 64;
+  return plan;
+}
+static int64_t ws_floats(const Plan& p) { return p.total + 64; }
+
+static int chol_launch(const float* hs, int64_t k, float damp, int attempt, float* u,
+                       int* status_out, float* ws, const Plan& plan, hipStream_t s) {
+  float* lam = ws + plan.total;
   const int big = 0x7fffffff;
   int rc = HI2X_OK;
   hipLaunchKernelGGL(status_init_kernel, dim3(1), dim3(1), 0, s, status_out, big);
@@ -401,28 +403,43 @@ static int chol_launch(const float* hs, int64_t k, float damp, int attempt, floa
     hipLaunchKernelGGL(reverse_out_kernel, g, dim3(256), 0, s, u, k);
     rc = launch_status("reverse_out_kernel");
   }
-  if (ws) (void)hipFreeAsync(ws, s);
-  (void)hipFreeAsync(lam, s);
   return rc;
 }
 
+extern "C" int64_t hi2x_chol_workspace_bytes(int64_t k) {
+  if (k <= 0) return -1;
+  return ws_floats(make_plan(k)) * (int64_t)sizeof(float);
+}
+
 extern "C" int hi2x_chol_inv_upper_async(const float* hs, int64_t k, float damp, int attempt,
-                                         float* u, int32_t* status, void* stream) {
+                                         float* u, int32_t* status, void* ws, int64_t ws_bytes,
+                                         void* stream) {
   clear_error();
   HI2X_REQUIRE(k > 0 && hs && u && hs != u && status, "chol_inv_upper_async: bad arguments");
   HI2X_REQUIRE(attempt >= 0 && attempt < 10, "chol_inv_upper_async: attempt %d", attempt);
-  return chol_launch(hs, k, damp, attempt, u, status, as_stream(stream));
+  hipStream_t s = as_stream(stream);
+  const Plan plan = make_plan(k);
+  Workspace w;
+  const int rc = take_workspace(w, ws, ws_bytes, (size_t)ws_floats(plan) * sizeof(float), s,
+                                "chol_inv_upper_async");
+  if (rc) return rc;
+  return chol_launch(hs, k, damp, attempt, u, status, reinterpret_cast<float*>(w.p), plan, s);
 }
 
 extern "C" int hi2x_chol_inv_upper(const float* hs, int64_t k, float damp, int attempt,
-                                   float* u, void* stream) {
+                                   float* u, void* ws, int64_t ws_bytes, void* stream) {
   clear_error();
   HI2X_REQUIRE(k > 0 && hs && u && hs != u, "chol_inv_upper: bad arguments");
   HI2X_REQUIRE(attempt >= 0 && attempt < 10, "chol_inv_upper: attempt %d", attempt);
   hipStream_t s = as_stream(stream);
-  int* status = nullptr;
-  HI2X_HIP(hipMallocAsync((void**)&status, sizeof(int), s));
-  int rc = chol_launch(hs, k, damp, attempt, u, status, s);
+  const Plan plan = make_plan(k);
+  Workspace w;
+  int rc = take_workspace(w, ws, ws_bytes, (size_t)ws_floats(plan) * sizeof(float), s,
+                          "chol_inv_upper");
+  if (rc) return rc;
+  float* wsf = reinterpret_cast<float*>(w.p);
+  int* status = reinterpret_cast<int*>(wsf + plan.total + 1);
+  rc = chol_launch(hs, k, damp, attempt, u, status, wsf, plan, s);
   int st = 0x7fffffff;
   if (!rc) {
     hipError_t e = hipMemcpyAsync(&st, status, sizeof(int), hipMemcpyDeviceToHost, s);
@@ -432,7 +449,6 @@ extern "C" int hi2x_chol_inv_upper(const float* hs, int64_t k, float damp, int a
       rc = HI2X_ELAUNCH;
     }
   }
-  (void)hipFreeAsync(status, s);
   if (!rc && st != 0x7fffffff) {
     set_error("chol_inv_upper: not positive definite in the block at %d (attempt %d)", st - 1,
               attempt);

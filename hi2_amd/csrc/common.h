@@ -52,6 +52,40 @@ class LaunchTimer {
     }                                                                         \
   } while (0)
 
+namespace hi2x {
+
+// The caller's device workspace (checked for size and 256-byte alignment), or else a
+// stream-ordered allocation of the library's own, released in stream order when the
+// Workspace goes out of scope.  Callers that run work on several streams at once pass
+// their own workspaces: blocks freed on one stream and reused on another make the
+// allocator order the two streams.
+struct Workspace {
+  char* p = nullptr;
+  bool owned = false;
+  hipStream_t s = nullptr;
+  ~Workspace() {
+    if (owned && p) (void)hipFreeAsync(p, s);
+  }
+};
+
+inline int take_workspace(Workspace& w, void* given, int64_t given_bytes, size_t need,
+                          hipStream_t s, const char* what) {
+  w.s = s;
+  if (need == 0) return HI2X_OK;
+  if (given) {
+    HI2X_REQUIRE(given_bytes >= (int64_t)need, "%s: workspace of %lld bytes, %lld needed", what,
+                 (long long)given_bytes, (long long)need);
+    HI2X_REQUIRE(((uintptr_t)given & 255) == 0, "%s: workspace not 256-byte aligned", what);
+    w.p = static_cast<char*>(given);
+    return HI2X_OK;
+  }
+  HI2X_HIP(hipMallocAsync((void**)&w.p, need, s));
+  w.owned = true;
+  return HI2X_OK;
+}
+
+}  // namespace hi2x
+
 // ---- device helpers ------------------------------------------------------------------
 
 // fp32 -> fp16 -> fp32 with round-to-nearest-even (torch's .to(float16).float()).

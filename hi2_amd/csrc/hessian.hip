@@ -420,7 +420,36 @@ __global__ __launch_bounds__(256) void st_sym_kernel(int64_t K, int nT, float* _
   }
 }
 
-int launch_syrk(const void* x, int dtype, int64_t t, int64_t k, float* s, hipStream_t st) {
+// Work split of the bf16 SYRK and the workspace it needs: the transposed X (tokens
+// padded to 64) and, when the 256-tiles are fewer than the CUs, one partial [k, k] per
+// token split.
+struct SyrkPlan {
+  int64_t tp = 0, tchunk = 0, ntiles = 0;
+  int nT = 0, splits = 1;
+  size_t xt_bytes = 0, parts_bytes = 0;
+  size_t total() const { return xt_bytes + parts_bytes; }
+};
+
+SyrkPlan syrk_plan(int dtype, int64_t t, int64_t k) {
+  SyrkPlan p;
+  if (dtype != 2 || t == 0) return p;
+  p.tp = (t + 63) / 64 * 64;
+  p.nT = (int)((k + S2T - 1) / S2T);
+  p.ntiles = (int64_t)p.nT * (p.nT + 1) / 2;
+  int splits = (int)((256 + p.ntiles - 1) / p.ntiles);
+  int64_t tchunk = (p.tp + splits - 1) / splits;
+  tchunk = (tchunk + S2C - 1) / S2C * S2C;
+  splits = (int)((p.tp + tchunk - 1) / tchunk);
+  p.splits = splits < 1 ? 1 : splits;
+  p.tchunk = tchunk;
+  p.xt_bytes = ((size_t)p.tp * (size_t)k * 2 + 255) / 256 * 256;
+  p.parts_bytes = p.splits > 1 ? (size_t)p.splits * k * k * sizeof(float) : 0;
+  return p;
+}
+
+// ws: device workspace of at least syrk_plan(...).total() bytes, 256-byte aligned
+int launch_syrk(const void* x, int dtype, int64_t t, int64_t k, float* s, char* ws,
+                hipStream_t st) {
   if (dtype != 2) {
     const int nT = (int)((k + HT - 1) / HT);
     const int64_t tiles = (int64_t)nT * (nT + 1) / 2;
@@ -430,36 +459,22 @@ int launch_syrk(const void* x, int dtype, int64_t t, int64_t k, float* s, hipStr
     return launch_status("syrk_f32_kernel");
   }
   // bf16: transpose, tiles of 256 (token range split when the tiles are few), mirror
-  uint16_t* xt = nullptr;
-  const int64_t tp = (t + 63) / 64 * 64;
-  HI2X_HIP(hipMallocAsync((void**)&xt, (size_t)tp * (size_t)k * 2, st));
-  hipLaunchKernelGGL(transpose_bf16_kernel, dim3((unsigned)((k + 63) / 64), (unsigned)(tp / 64)),
-                     dim3(256), 0, st, (const uint16_t*)x, t, k, tp, xt);
+  const SyrkPlan p = syrk_plan(dtype, t, k);
+  uint16_t* xt = reinterpret_cast<uint16_t*>(ws);
+  float* parts = p.splits > 1 ? reinterpret_cast<float*>(ws + p.xt_bytes) : nullptr;
+  hipLaunchKernelGGL(transpose_bf16_kernel, dim3((unsigned)((k + 63) / 64), (unsigned)(p.tp / 64)),
+                     dim3(256), 0, st, (const uint16_t*)x, t, k, p.tp, xt);
   int rc = launch_status("transpose_bf16_kernel");
-  const int nT = (int)((k + S2T - 1) / S2T);
-  const int64_t ntiles = (int64_t)nT * (nT + 1) / 2;
-  int splits = (int)((256 + ntiles - 1) / ntiles);
-  int64_t tchunk = (tp + splits - 1) / splits;
-  tchunk = (tchunk + S2C - 1) / S2C * S2C;
-  splits = (int)((tp + tchunk - 1) / tchunk);
-  if (splits < 1) splits = 1;
-  float* parts = nullptr;
-  if (!rc && splits > 1) {
-    if (hipMallocAsync((void**)&parts, (size_t)splits * k * k * sizeof(float), st) != hipSuccess) {
-      set_error("hessian_syrk: workspace allocation failed");
-      rc = HI2X_ELAUNCH;
-    }
-  }
   if (!rc) {
-    const int64_t grid = (ntiles + 7) / 8 * 8 * splits;
+    const int64_t grid = (p.ntiles + 7) / 8 * 8 * p.splits;
     LaunchTimer timer(HI2X_TIME_HESSIAN_SYRK, 2.0 * t * k * k, st);
-    hipLaunchKernelGGL(syrk2_bf16_kernel, dim3((unsigned)grid), dim3(256), 0, st, xt, tp, k, nT,
-                       ntiles, splits, tchunk, splits > 1 ? parts : s, k * k);
+    hipLaunchKernelGGL(syrk2_bf16_kernel, dim3((unsigned)grid), dim3(256), 0, st, xt, p.tp, k,
+                       p.nT, p.ntiles, p.splits, p.tchunk, parts ? parts : s, k * k);
     rc = launch_status("syrk2_bf16_kernel");
   }
-  if (!rc && splits > 1) {
+  if (!rc && parts) {
     hipLaunchKernelGGL(split_sum_kernel, dim3((unsigned)((k * k + 255) / 256)), dim3(256), 0, st,
-                       s, parts, splits, k);
+                       s, parts, p.splits, k);
     rc = launch_status("split_sum_kernel");
   }
   if (!rc) {
@@ -468,8 +483,6 @@ int launch_syrk(const void* x, int dtype, int64_t t, int64_t k, float* s, hipStr
                        st, s, k, nM);
     rc = launch_status("mirror_kernel");
   }
-  if (parts) (void)hipFreeAsync(parts, st);
-  (void)hipFreeAsync(xt, st);
   return rc;
 }
 
@@ -478,27 +491,50 @@ int launch_syrk(const void* x, int dtype, int64_t t, int64_t k, float* s, hipStr
 
 using namespace hi2x;
 
+extern "C" int64_t hi2x_hessian_workspace_bytes(int dtype, int64_t t, int64_t k) {
+  if ((dtype != 0 && dtype != 2) || k <= 0 || t < 0) return -1;
+  return (int64_t)syrk_plan(dtype, t, k).total();
+}
+
 extern "C" int hi2x_hessian_syrk(const void* x, int dtype, int64_t t, int64_t k, float* s,
-                                 void* stream) {
+                                 void* ws, int64_t ws_bytes, void* stream) {
   clear_error();
   HI2X_REQUIRE(dtype == 0 || dtype == 2, "hessian_syrk: dtype %d (0 = f32, 2 = bf16)", dtype);
   HI2X_REQUIRE(k > 0 && t >= 0, "hessian_syrk: bad shape");
   if (t == 0) return HI2X_OK;
-  return launch_syrk(x, dtype, t, k, s, as_stream(stream));
+  hipStream_t st = as_stream(stream);
+  Workspace w;
+  const int rc = take_workspace(w, ws, ws_bytes, syrk_plan(dtype, t, k).total(), st,
+                                "hessian_syrk");
+  if (rc) return rc;
+  return launch_syrk(x, dtype, t, k, s, w.p, st);
 }
 
 extern "C" int hi2x_hessian_syrk_varlen(const void* x, int dtype, const int64_t* offs,
                                         int64_t n_groups, int64_t k, float* const* s_ptrs,
-                                        void* stream) {
+                                        void* ws, int64_t ws_bytes, void* stream) {
   clear_error();
   HI2X_REQUIRE(dtype == 0 || dtype == 2, "hessian_syrk_varlen: dtype %d", dtype);
+  HI2X_REQUIRE(k > 0 && n_groups >= 0 && offs && (n_groups == 0 || s_ptrs),
+               "hessian_syrk_varlen: bad arguments");
   const size_t esz = dtype == 2 ? 2 : 4;
+  int64_t tmax = 0;
   for (int64_t e = 0; e < n_groups; ++e) {
     const int64_t t = offs[e + 1] - offs[e];
     HI2X_REQUIRE(t >= 0, "hessian_syrk_varlen: offsets not ascending");
+    tmax = t > tmax ? t : tmax;
+  }
+  if (tmax == 0) return HI2X_OK;
+  hipStream_t st = as_stream(stream);
+  Workspace w;  // sized for the longest group, reused by every group in stream order
+  int rc = take_workspace(w, ws, ws_bytes, syrk_plan(dtype, tmax, k).total(), st,
+                          "hessian_syrk_varlen");
+  if (rc) return rc;
+  for (int64_t e = 0; e < n_groups; ++e) {
+    const int64_t t = offs[e + 1] - offs[e];
     if (t == 0) continue;
     const char* xe = static_cast<const char*>(x) + (size_t)offs[e] * (size_t)k * esz;
-    const int rc = launch_syrk(xe, dtype, t, k, s_ptrs[e], as_stream(stream));
+    rc = launch_syrk(xe, dtype, t, k, s_ptrs[e], w.p, st);
     if (rc) return rc;
   }
   return HI2X_OK;

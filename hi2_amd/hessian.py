@@ -43,7 +43,9 @@ __all__ = [
     "encode_jobs_gptq",
     "encode_rows_gptq",
     "encode_rows_gptq_reference",
+    "finish_factor",
     "inverse_factor",
+    "inverse_factor_async",
     "inverse_factors",
     "transform_sigma",
 ]
@@ -76,8 +78,9 @@ class HessianStats:
         t = x.shape[0]
         if t:
             dtype = 2 if x.dtype == torch.bfloat16 else 0
+            ws = _lib.workspace(dev, "hi2x_hessian_workspace_bytes", dtype, t, self.k)
             _lib.call("hi2x_hessian_syrk", dev, _lib.ptr(x), dtype, t, self.k,
-                      _lib.ptr(self.S))
+                      _lib.ptr(self.S), _lib.ptr(ws), ws.numel())
         self.n += t
 
     def merge(self, other: "HessianStats") -> None:
@@ -117,12 +120,52 @@ def inverse_factor(hs: torch.Tensor, damp: float = 0.01) -> torch.Tensor:
     k = hs.shape[0]
     h = hs.to(torch.float32).contiguous()
     u = torch.empty_like(h)
+    ws = _lib.workspace(dev, "hi2x_chol_workspace_bytes", k)
     last = None
     for attempt in range(6):
         try:
             _lib.call("hi2x_chol_inv_upper", dev, _lib.ptr(h), k, float(damp), attempt,
-                      _lib.ptr(u))
+                      _lib.ptr(u), _lib.ptr(ws), ws.numel())
             return u
+        except _lib.NotPositiveDefinite as e:
+            last = e
+    raise RuntimeError(f"Hessian is not factorisable even with heavy damping: {last}")
+
+
+_OK = 0x7FFFFFFF  # status word of a successful factorisation
+
+
+def inverse_factor_async(hs: torch.Tensor, damp: float = 0.01):
+    """First attempt of :func:`inverse_factor`, enqueued on the current stream without
+    waiting for it: returns ``(u, status)`` with ``status`` a device int32 that reads
+    0x7FFFFFFF once the factorisation has succeeded.  :func:`finish_factor` checks it
+    (and retries with more damping) when the caller is ready to wait."""
+    dev = _lib.require_gpu(hs)
+    h = hs.to(torch.float32).contiguous()
+    u = torch.empty_like(h)
+    status = torch.empty(1, dtype=torch.int32, device=dev)
+    ws = _lib.workspace(dev, "hi2x_chol_workspace_bytes", h.shape[0])
+    _lib.call("hi2x_chol_inv_upper_async", dev, _lib.ptr(h), h.shape[0], float(damp), 0,
+              _lib.ptr(u), _lib.ptr(status), _lib.ptr(ws), ws.numel())
+    return u, status
+
+
+def finish_factor(hs: torch.Tensor, u: torch.Tensor, status: torch.Tensor,
+                  damp: float = 0.01) -> bool:
+    """Wait for an :func:`inverse_factor_async` result; if that attempt failed, redo the
+    reference's damping retries into ``u``.  Returns True when ``u`` was recomputed
+    (work that consumed it must then be redone)."""
+    if int(status.item()) == _OK:
+        return False
+    dev = u.device
+    h = hs.to(torch.float32).contiguous()
+    ws = _lib.workspace(dev, "hi2x_chol_workspace_bytes", h.shape[0])
+    last = None
+    for attempt in range(1, 6):
+        try:
+            _lib.call("hi2x_chol_inv_upper", dev, _lib.ptr(h), h.shape[0], float(damp),
+                      attempt, _lib.ptr(u), _lib.ptr(ws), ws.numel())
+            return True
         except _lib.NotPositiveDefinite as e:
             last = e
     raise RuntimeError(f"Hessian is not factorisable even with heavy damping: {last}")
@@ -140,12 +183,13 @@ def inverse_factors(hss: list[torch.Tensor], damp: float = 0.01) -> list[torch.T
     hs32 = [h.to(torch.float32).contiguous() for h in hss]
     us = [torch.empty_like(h) for h in hs32]
     status = torch.empty(len(hss), dtype=torch.int32, device=dev)
-    streams = [torch.cuda.Stream(device=dev) for _ in hss]
+    streams = [_lib.side_stream(dev, i) for i in range(len(hss))]
     for i, (h, u, st) in enumerate(zip(hs32, us, streams)):
         st.wait_stream(main)
         with torch.cuda.stream(st):
+            ws = _lib.workspace(dev, "hi2x_chol_workspace_bytes", h.shape[0])
             _lib.call("hi2x_chol_inv_upper_async", dev, _lib.ptr(h), h.shape[0], float(damp), 0,
-                      _lib.ptr(u), _lib.ptr(status[i:i + 1]))
+                      _lib.ptr(u), _lib.ptr(status[i:i + 1]), _lib.ptr(ws), ws.numel())
         for t in (h, u, status):
             t.record_stream(st)
     for st in streams:
@@ -153,14 +197,15 @@ def inverse_factors(hss: list[torch.Tensor], damp: float = 0.01) -> list[torch.T
     ok = status.cpu().tolist()
     out = []
     for h, u, stv in zip(hs32, us, ok):
-        if stv == 0x7FFFFFFF:
+        if stv == _OK:
             out.append(u)
             continue
         last = None
+        ws = _lib.workspace(dev, "hi2x_chol_workspace_bytes", h.shape[0])
         for attempt in range(1, 6):
             try:
                 _lib.call("hi2x_chol_inv_upper", dev, _lib.ptr(h), h.shape[0], float(damp),
-                          attempt, _lib.ptr(u))
+                          attempt, _lib.ptr(u), _lib.ptr(ws), ws.numel())
                 break
             except _lib.NotPositiveDefinite as e:
                 last = e
@@ -241,18 +286,18 @@ def _round_kernel(
         st[off : off + n, :nb] = x.step_d
         views.append((off, n))
         off += n
-    row_grp = torch.repeat_interleave(
-        torch.arange(len(units), dtype=torch.int32), torch.tensor(sizes)
-    ).to(dev)
+    # small index arrays: built on the host, copied without blocking the host (other
+    # streams keep being fed while this batch waits for its inputs)
+    row_grp = _lib.h2d(torch.repeat_interleave(
+        torch.arange(len(units), dtype=torch.int32), torch.tensor(sizes)), dev)
     uk = [jobs[x.job].u.to(dev, torch.float32).contiguous() for x in units]
     for u in uk:
         if u.shape != (k, k):
             raise ValueError(f"factor has shape {tuple(u.shape)}, expected ({k}, {k})")
-    u_ptrs = torch.tensor([u.data_ptr() for u in uk], dtype=torch.int64).to(dev)
-    blk = torch.stack([x.blk_of for x in units]).to(dev, torch.int32).contiguous()
-    nmax = torch.tensor(
-        [2 ** jobs[x.job].nbits - 1 for x in units], dtype=torch.float32
-    ).to(dev)
+    u_ptrs = _lib.h2d(torch.tensor([u.data_ptr() for u in uk], dtype=torch.int64), dev)
+    blk = torch.stack([x.blk_of.to(dev, torch.int32) for x in units]).contiguous()
+    nmax = _lib.h2d(torch.tensor(
+        [2 ** jobs[x.job].nbits - 1 for x in units], dtype=torch.float32), dev)
     codes = torch.zeros(total, k, dtype=torch.uint8, device=dev)
     comp = torch.zeros(total, k, dtype=torch.float32, device=dev) if want_comp else None
     sb = SUPER_BLOCKS if super_blocks is None else super_blocks
@@ -339,10 +384,10 @@ def encode_jobs_gptq(
         bl[-1].append(x)
     # batches of different K are independent: each runs on its own stream
     side = []
-    for (dev, _k), bl in batches.items():
+    for bi, ((dev, _k), bl) in enumerate(batches.items()):
         _use_kernel(dev, backend)
         main = torch.cuda.current_stream(dev)
-        st = torch.cuda.Stream(device=dev) if len(batches) > 1 else main
+        st = _lib.side_stream(dev, bi) if len(batches) > 1 else main
         if st is not main:
             st.wait_stream(main)
             side.append((main, st))

@@ -141,18 +141,29 @@ int hi2x_assemble_piece(const int64_t* rows, int64_t r, const uint8_t* codes,
 
 /* ---- Hessian ------------------------------------------------------------------------ */
 
+/* Workspaces.  Entry points that need device scratch take (ws, ws_bytes): a 256-byte
+ * aligned device buffer of at least the size the matching *_workspace_bytes query
+ * returns (-1 for bad arguments).  ws = NULL makes the library allocate it stream-ordered
+ * (hipMallocAsync) and release it after the call's work; callers that run several
+ * streams at once should pass their own, since a block the allocator hands from one
+ * stream to another orders the two streams. */
+
+/* Workspace of hi2x_hessian_syrk for t rows of width k (0 for f32 input). */
+int64_t hi2x_hessian_workspace_bytes(int dtype, int64_t t, int64_t k);
+
 /* HessianStats.update (hi2/hessian.py:35-40): s [k, k] f32 += x^T x over t rows of
  * x [t, k] (dtype 0 = f32, 2 = bf16).  bf16 runs on bf16 MFMA with f32 accumulation
  * (products exact); f32 on f32 MFMA.  The result is exactly symmetric. */
-int hi2x_hessian_syrk(const void* x, int dtype, int64_t t, int64_t k, float* s,
-                      void* stream);
+int hi2x_hessian_syrk(const void* x, int dtype, int64_t t, int64_t k, float* s, void* ws,
+                      int64_t ws_bytes, void* stream);
 
 /* Variable-length batch of the above (routed MoE tokens, hi2/moe.py:83-100):
  * group e accumulates rows [offs[e], offs[e+1]) of x into s_ptrs[e] ([k, k] f32).
- * offs is a host array of n_groups + 1 row offsets; s_ptrs a host array. */
+ * offs is a host array of n_groups + 1 row offsets; s_ptrs a host array.  The workspace
+ * is sized for the longest group (hi2x_hessian_workspace_bytes with its row count). */
 int hi2x_hessian_syrk_varlen(const void* x, int dtype, const int64_t* offs,
-                             int64_t n_groups, int64_t k, float* const* s_ptrs,
-                             void* stream);
+                             int64_t n_groups, int64_t k, float* const* s_ptrs, void* ws,
+                             int64_t ws_bytes, void* stream);
 
 /* transform_sigma (hi2/hessian.py:50-68): hs [k, k] f32 = sym(M diag(1/s) sigma
  * diag(1/s) M^T) with M block-diagonal (H16/4 on flagged groups, I elsewhere).
@@ -163,6 +174,9 @@ int hi2x_sigma_transform(const float* sigma, const uint16_t* col_scale, const ui
 
 /* ---- Cholesky chain ------------------------------------------------------------------ */
 
+/* Workspace of the two entry points below for a k x k matrix. */
+int64_t hi2x_chol_workspace_bytes(int64_t k);
+
 /* One attempt of inverse_factor (hi2/hessian.py:71-86): with lam = damp * mean(diag hs)
  * (clamped at 1e-12) * 10^attempt, writes u [k, k] f32 = the upper Cholesky factor of
  * (hs + lam I)^-1 (lower triangle zero).  Computed as U = (J chol(J (hs + lam I) J) J)^-1
@@ -170,7 +184,7 @@ int hi2x_sigma_transform(const float* sigma, const uint16_t* col_scale, const ui
  * chol(upper) chain.  Synchronises `stream`; returns HI2X_ENOTPD when the damped matrix
  * is not numerically positive definite (the caller retries with attempt + 1). */
 int hi2x_chol_inv_upper(const float* hs, int64_t k, float damp, int attempt, float* u,
-                        void* stream);
+                        void* ws, int64_t ws_bytes, void* stream);
 
 /* Asynchronous form of hi2x_chol_inv_upper (same computation, same reference
  * interface hi2/hessian.py:71-86): nothing is synchronised; `status` (device i32)
@@ -178,7 +192,7 @@ int hi2x_chol_inv_upper(const float* hs, int64_t k, float damp, int attempt, flo
  * failing 128-block, once `stream` reaches it.  Lets independent factors (one per
  * calibration input) run concurrently on separate streams. */
 int hi2x_chol_inv_upper_async(const float* hs, int64_t k, float damp, int attempt, float* u,
-                              int32_t* status, void* stream);
+                              int32_t* status, void* ws, int64_t ws_bytes, void* stream);
 
 /* ---- measurement ------------------------------------------------------------------------ */
 

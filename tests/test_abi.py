@@ -26,8 +26,9 @@ def test_library_exports_every_declared_symbol():
     for name in names:
         assert hasattr(lib, name), name
     assert lib.hi2x_version() >= 100
-    assert set(_lib.SIGNATURES) | {"hi2x_version", "hi2x_last_error", "hi2x_timing_enable",
-                                   "hi2x_timing_query"} == set(names)
+    assert set(_lib.SIGNATURES) | set(_lib.SIZES) | {
+        "hi2x_version", "hi2x_last_error", "hi2x_timing_enable", "hi2x_timing_query"
+    } == set(names)
 
 
 def test_raw_symbols_resolve_without_ctypes_wrappers():
