@@ -18,6 +18,7 @@
 //     A21 = -A22 T2                 (= -L22^-1 L21 L11^-1, the lower-left block of L^-1)
 //   every product on the fp32 MFMA GEMM of mfma_gemm.h with triangular operands masked.
 #include <type_traits>
+#include <utility>
 #include <vector>
 
 #include "mfma_gemm.h"
@@ -187,93 +188,200 @@ __global__ __launch_bounds__(256) void reverse_damp_kernel(const float* __restri
 }
 
 // ---- leaf: L^-1 of chol(P[r0:r0+n, r0:r0+n]) in place (lower triangle) ---------------------
-// 1024 threads as 32 x 32; thread (ty, tx) holds slots (i, j) = (ty + 32a, tx + 32b),
-// b <= a < 4, of the lower triangle in registers.  Sweep c = 0..n-1, one barrier each:
-//   piv = sqrt(T[c][c]), rp = 1/piv; l_i = T[i][c] rp (column c of L); for column c the
-//   multiplier is rp, for j < c it is x_j = B[c][j] rp (row c of L^-1), for j > c l_j.
-//   Slots with i > c:  j > c: T[i][j] -= l_i l_j   (Cholesky update)
-//                      j = c: B[i][c]  = -l_i rp   (start of column c of L^-1)
-//                      j < c: B[i][j] -= l_i x_j   (forward substitution)
+// One workgroup of 4 waves holds the 128 x 128 block in LDS (identity beyond n, zeros
+// above the diagonal) and runs the same recursion as the host on it, down to 16 x 16:
+//   node [A11 0; A21 A22]: leaf(A11); T1 = A21 A11^T; A22 -= T1 T1^T (lower);
+//                          leaf(A22); T2 = T1 A11; A21 = -A22 T2
+// with the products on v_mfma_f32_16x16x4f32 (each product is read into registers,
+// then written back in place after a barrier).
+//
+// The 16 x 16 base is one wave's fused factor-and-invert sweep, lane l holding row
+// i = l/4, columns j = 4(l%4) + e, e < 4.  For c = 0..15:
+//   piv = sqrt(T[c][c]), rp = 1/piv; l_i = T[i][c] rp; the multiplier of column j is
+//   l_j = T[j][c] rp for j > c, rp for j = c, x_j = B[c][j] rp for j < c (row c of L^-1).
+//   Rows i > c, j <= i:  T[i][j] -= l_i m_j  (j > c: Cholesky update; j = c: starts
+//   column c of L^-1 as -l_i rp; j < c: forward substitution)
 //   Row c is final: X[c][j] = B[c][j] rp, X[c][c] = rp.
-// Column c+1 of T and row c+1 of B go through LDS to the next sweep.  The reciprocal
-// and square root are the hardware approximations (the factor is compared to a
-// tolerance, not bit for bit).
-constexpr int LT = 32;           // thread grid edge
-constexpr int LB = NB / LT;      // slots per thread edge
+// Column c comes from the row's own quad (DPP), T[j][c] and B[c][j] from other quads
+// (ds_bpermute), the pivot by readlane: no barrier and no LDS traffic in the sweep.  The
+// reciprocal and square root are the hardware approximations (the factor is compared to
+// a tolerance, not bit for bit).
+constexpr int LP = NB + 4;  // LDS pitch of the leaf block (floats)
 
-__global__ __launch_bounds__(1024) void leaf_kernel(float* __restrict__ P, int64_t K, int64_t r0,
-                                                    int n, int* __restrict__ status) {
-  __shared__ float colb[2][NB];
-  __shared__ float rowb[2][NB];
-  const int tid = threadIdx.x, ty = tid / LT, tx = tid % LT;
-  float v[LB][LB];
+typedef float f32x4v __attribute__((ext_vector_type(4)));
+
+template <int Q>
+__device__ __forceinline__ float quad_pick(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), Q * 0x55,
+                                                            0xf, 0xf, false));
+}
+
+__device__ __forceinline__ float lane_fetch(float v, int src_lane) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(src_lane * 4,
+                                                                __builtin_bit_cast(int, v)));
+}
+
+template <int C>
+__device__ __forceinline__ void base_step(float (&v)[4], int l, bool& bad) {
+  constexpr int QC = C / 4, EC = C % 4;
+  const int i = l >> 2, q = l & 3;
+  const float d = __builtin_bit_cast(
+      float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v[EC]), 4 * C + QC));
+  bad = bad || !(d > 0.0f);
+  const float rp = __builtin_amdgcn_rcpf(__builtin_amdgcn_sqrtf(d));
+  const float li = quad_pick<QC>(v[EC]) * rp;
+  float colv[4], rowv[4];
 #pragma unroll
-  for (int a = 0; a < LB; ++a)
-#pragma unroll
-    for (int b = 0; b <= a; ++b) {
-      const int i = ty + LT * a, j = tx + LT * b;
-      v[a][b] = (i < n && j <= i) ? P[(r0 + i) * K + r0 + j] : 0.0f;
-    }
-  if (tx == 0)
-#pragma unroll
-    for (int a = 0; a < LB; ++a) colb[0][ty + LT * a] = v[a][0];
-  __syncthreads();
-  bool bad = false;
-  for (int c = 0; c < n; ++c) {
-    const int p = c & 1;
-    const float d = colb[p][c];
-    bad = bad || !(d > 0.0f);
-    const float piv = __builtin_amdgcn_sqrtf(d);
-    const float rp = __builtin_amdgcn_rcpf(piv);
-    float li[LB], mj[LB];
-#pragma unroll
-    for (int a = 0; a < LB; ++a) li[a] = colb[p][ty + LT * a] * rp;
-#pragma unroll
-    for (int b = 0; b < LB; ++b) {
-      const int j = tx + LT * b;
-      mj[b] = (j > c) ? colb[p][j] * rp : (j == c ? rp : rowb[p][j] * rp);
-    }
-    const int ac = c / LT;  // band of row c (uniform)
-#pragma unroll
-    for (int a = 0; a < LB; ++a) {
-      if (a < ac) continue;  // rows all above c: final already
-      const int i = ty + LT * a;
-      const bool below = i > c;
-#pragma unroll
-      for (int b = 0; b <= a; ++b) {
-        const int j = tx + LT * b;
-        const float cur = (j == c) ? 0.0f : v[a][b];
-        v[a][b] = below ? __builtin_fmaf(-li[a], mj[b], cur) : v[a][b];
-      }
-      if (a == ac && i == c) {  // finalise row c of L^-1
-#pragma unroll
-        for (int b = 0; b <= a; ++b) {
-          const int j = tx + LT * b;
-          v[a][b] = (j < c) ? v[a][b] * rp : (j == c ? rp : v[a][b]);
-        }
-      }
-    }
-    const int cn = c + 1;
-    if (cn < n) {
-      const int bn = cn / LT;  // band of column / row c+1 (uniform)
-#pragma unroll
-      for (int a = 0; a < LB; ++a)
-#pragma unroll
-        for (int b = 0; b <= a; ++b) {
-          if (b == bn && tx == cn - LT * b && ty + LT * a >= cn) colb[p ^ 1][ty + LT * a] = v[a][b];
-          if (a == bn && ty == cn - LT * a && tx + LT * b < cn) rowb[p ^ 1][tx + LT * b] = v[a][b];
-        }
-    }
-    __syncthreads();
+  for (int e = 0; e < 4; ++e) {
+    colv[e] = lane_fetch(v[EC], 16 * q + 4 * e + QC);  // T[j][c], j = 4q + e
+    rowv[e] = lane_fetch(v[e], 4 * C + q);             // B[c][j]
   }
-  if (bad && tid == 0) atomicMin(status, (int)(r0 + 1));
 #pragma unroll
-  for (int a = 0; a < LB; ++a)
-#pragma unroll
-    for (int b = 0; b <= a; ++b) {
-      const int i = ty + LT * a, j = tx + LT * b;
-      if (i < n && j <= i) P[(r0 + i) * K + r0 + j] = v[a][b];
+  for (int e = 0; e < 4; ++e) {
+    const int j = 4 * q + e;
+    const float m = (j > C) ? colv[e] * rp : (j == C ? rp : rowv[e] * rp);
+    if (i > C && j <= i) {
+      const float cur = (j == C) ? 0.0f : v[e];
+      v[e] = __builtin_fmaf(-li, m, cur);
+    } else if (i == C) {
+      v[e] = (j < C) ? v[e] * rp : (j == C ? rp : v[e]);
     }
+  }
+}
+
+template <int... Cs>
+__device__ __forceinline__ void base_steps(float (&v)[4], int l, bool& bad,
+                                           std::integer_sequence<int, Cs...>) {
+  (base_step<Cs>(v, l, bad), ...);
+}
+
+// 16 x 16 block at (o, o): one wave (the caller's wave 0)
+__device__ __forceinline__ void leaf_base16(float* S, int o, bool& bad) {
+  const int l = threadIdx.x & 63;
+  float* row = &S[(o + (l >> 2)) * LP + o + 4 * (l & 3)];
+  const float4 x = *reinterpret_cast<const float4*>(row);
+  float v[4] = {x.x, x.y, x.z, x.w};
+  base_steps(v, l, bad, std::make_integer_sequence<int, 16>{});
+  *reinterpret_cast<float4*>(row) = make_float4(v[0], v[1], v[2], v[3]);
+}
+
+// C[H x H] at (cr, cc) = alpha * A (at (ar, ac)) * op(B) (at (br, bc)), op(B) = B^T when
+// TB; with LOWER, C += alpha * A op(B) on the lower triangle of C only.  Every block is in
+// the leaf's LDS; the result is written after all inputs have been read (C may alias).
+// For each 16 k: lane group g = l/16 supplies k = 16 kb + 4 g + s at MFMA step s, so a
+// lane reads its 4 k of A (and of B^T) as one 16-byte vector.
+template <int H, bool TB, bool LOWER>
+__device__ __forceinline__ void leaf_prod(float* S, int ar, int ac, int br, int bc, int cr,
+                                          int cc, float alpha) {
+  constexpr int NT = H / 16, TILES = NT * NT, PER = (TILES + 3) / 4;
+  const int wave = threadIdx.x >> 6, l = threadIdx.x & 63;
+  const int lr = l & 15, lg = l >> 4;
+  f32x4v acc[PER];
+#pragma unroll
+  for (int p = 0; p < PER; ++p) {
+    const int t = wave + 4 * p;
+    acc[p] = (f32x4v){0.0f, 0.0f, 0.0f, 0.0f};
+    if (t < TILES) {
+      const int tr = t / NT, tc = t % NT;
+#pragma unroll
+      for (int kb = 0; kb < H; kb += 16) {
+        const int k = kb + 4 * lg;
+        const float4 a = *reinterpret_cast<const float4*>(&S[(ar + tr * 16 + lr) * LP + ac + k]);
+        float4 b;
+        if (TB) {
+          b = *reinterpret_cast<const float4*>(&S[(br + tc * 16 + lr) * LP + bc + k]);
+        } else {
+          const float* bp = &S[(br + k) * LP + bc + tc * 16 + lr];
+          b = make_float4(bp[0], bp[LP], bp[2 * LP], bp[3 * LP]);
+        }
+        acc[p] = __builtin_amdgcn_mfma_f32_16x16x4f32(a.x, b.x, acc[p], 0, 0, 0);
+        acc[p] = __builtin_amdgcn_mfma_f32_16x16x4f32(a.y, b.y, acc[p], 0, 0, 0);
+        acc[p] = __builtin_amdgcn_mfma_f32_16x16x4f32(a.z, b.z, acc[p], 0, 0, 0);
+        acc[p] = __builtin_amdgcn_mfma_f32_16x16x4f32(a.w, b.w, acc[p], 0, 0, 0);
+      }
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int p = 0; p < PER; ++p) {
+    const int t = wave + 4 * p;
+    if (t < TILES) {
+      const int tr = t / NT, tc = t % NT;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int r = tr * 16 + 4 * lg + j, c = tc * 16 + lr;
+        const float x = acc[p][j];
+        float* d = &S[(cr + r) * LP + cc + c];
+        if (LOWER) {
+          if (c <= r) *d = *d + alpha * x;
+        } else {
+          *d = alpha * x;
+        }
+      }
+    }
+  }
+  __syncthreads();
+}
+
+// returns true when a pivot of this block was not positive (wave 0's view)
+template <int N>
+__device__ __forceinline__ bool leaf_rec(float* S, int o) {
+  if constexpr (N == 16) {
+    bool bad = false;
+    if ((threadIdx.x >> 6) == 0) leaf_base16(S, o, bad);
+    __syncthreads();
+    return bad;
+  } else {
+    constexpr int H = N / 2;
+    bool bad = leaf_rec<H>(S, o);
+    leaf_prod<H, true, false>(S, o + H, o, o, o, o + H, o, 1.0f);             // T1
+    leaf_prod<H, true, true>(S, o + H, o, o + H, o, o + H, o + H, -1.0f);      // A22 -= T1 T1^T
+    bad = leaf_rec<H>(S, o + H) || bad;
+    leaf_prod<H, false, false>(S, o + H, o, o, o, o + H, o, 1.0f);            // T2 = T1 A11
+    leaf_prod<H, false, false>(S, o + H, o + H, o + H, o, o + H, o, -1.0f);   // -A22 T2
+    return bad;
+  }
+}
+
+__global__ __launch_bounds__(256) void leaf_kernel(float* __restrict__ P, int64_t K, int64_t r0,
+                                                   int n, int* __restrict__ status) {
+  __shared__ float S[NB * LP];
+  const int tid = threadIdx.x;
+  // the block's rows as one buffer ending at its last element: rows past n read zero;
+  // n and K are multiples of 16, so every 16-byte vector is all in or all out
+  const __amdgpu_buffer_rsrc_t rs = mg_rsrc(P + r0 * K + r0, (int64_t)(n - 1) * K + n);
+  constexpr int V = NB / 4;  // float4 per row
+  float4 x[NB * V / 256];
+#pragma unroll
+  for (int q = 0; q < NB * V / 256; ++q) {
+    const int idx = tid + 256 * q, i = idx / V, j = 4 * (idx % V);
+    const uint32_t off = (i < n && j < n) ? (uint32_t)(((int64_t)i * K + j) * 4) : MG_OOB;
+    x[q] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rs, (int)off, 0, 0));
+  }
+#pragma unroll
+  for (int q = 0; q < NB * V / 256; ++q) {
+    const int idx = tid + 256 * q, i = idx / V, j = 4 * (idx % V);
+    float e[4] = {x[q].x, x[q].y, x[q].z, x[q].w};
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {  // lower triangle of the block, identity beyond n
+      const int jj = j + t;
+      e[t] = (i < n && jj < n) ? (jj <= i ? e[t] : 0.0f) : (i == jj ? 1.0f : 0.0f);
+    }
+    *reinterpret_cast<float4*>(&S[i * LP + j]) = make_float4(e[0], e[1], e[2], e[3]);
+  }
+  __syncthreads();
+  const bool bad = leaf_rec<NB>(S, 0);
+  if (tid == 0 && bad) atomicMin(status, (int)(r0 + 1));
+  // rows < n back in full vectors: the zeros above the diagonal land in P's upper
+  // triangle, which nothing reads before the final reflection overwrites it
+#pragma unroll
+  for (int q = 0; q < NB * V / 256; ++q) {
+    const int idx = tid + 256 * q, i = idx / V, j = 4 * (idx % V);
+    const uint32_t off = (i < n && j < n) ? (uint32_t)(((int64_t)i * K + j) * 4) : MG_OOB;
+    const float4 v = *reinterpret_cast<const float4*>(&S[i * LP + j]);
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(__attribute__((ext_vector_type(4))) unsigned, v),
+                                           rs, (int)off, 0, 0);
+  }
 }
 
 // U[i][j] = Linv[K-1-i][K-1-j] for j >= i, 0 below: in place over pairs
@@ -328,7 +436,7 @@ int inv_chol(const Ctx& c, int64_t r0, int64_t m, int depth) {
   const int64_t K = c.K;
   if (m <= NB) {
     LaunchTimer timer(HI2X_TIME_CHOL_LEAF, 2.0 * m * m * m / 3.0, c.s);
-    hipLaunchKernelGGL(leaf_kernel, dim3(1), dim3(1024), 0, c.s, c.P, K, r0, (int)m, c.status);
+    hipLaunchKernelGGL(leaf_kernel, dim3(1), dim3(256), 0, c.s, c.P, K, r0, (int)m, c.status);
     return launch_status("leaf_kernel");
   }
   const int64_t nbk = (m + NB - 1) / NB;
