@@ -51,12 +51,26 @@ struct MaskUpper {  // keep (r, k) with k >= r
   __device__ __forceinline__ bool elem(int64_t r, int64_t k) const { return k >= r; }
 };
 
+// where the heavy tiles of each product are (its rank grows along rows or columns)
+template <int AMODE, int BMODE>
+constexpr int tri_order() {
+  return AMODE == 1 ? 1 : (BMODE == 2 ? 2 : (BMODE == 1 ? 3 : 0));
+}
+
 template <int AMODE, int BMODE, bool TB, bool CLOW>
-__global__ __launch_bounds__(256) void tri_gemm_kernel(GemmArgs g, int64_t tn, int64_t ntiles) {
+__global__ __launch_bounds__(256) void tri_gemm_kernel(GemmArgs g, int64_t tm, int64_t tn,
+                                                       int super) {
   __shared__ MgSmem sm;
-  const int64_t t = xcd_tile(blockIdx.x, ntiles);
-  if (t < 0) return;
-  const int64_t r0 = (t / tn) * MG_T, c0 = (t % tn) * MG_T;
+  int64_t tr, tc;
+  if (super) {
+    if (!mg_super_tile<tri_order<AMODE, BMODE>(), CLOW>(blockIdx.x, tm, tn, tr, tc)) return;
+  } else {
+    const int64_t t = xcd_tile(blockIdx.x, tm * tn);
+    if (t < 0) return;
+    tr = t / tn;
+    tc = t % tn;
+  }
+  const int64_t r0 = tr * MG_T, c0 = tc * MG_T;
   if (CLOW && c0 > r0 + MG_T - 1) return;
   int64_t kbeg = 0, kend = g.Kd;
   if (AMODE == 1) kend = (r0 + MG_T < kend) ? r0 + MG_T : kend;
@@ -105,11 +119,13 @@ int tri_gemm(const GemmArgs& a, hipStream_t s) {
   if (a.M <= 0 || a.N <= 0) return HI2X_OK;
   const int64_t tm = (a.M + MG_T - 1) / MG_T, tn = (a.N + MG_T - 1) / MG_T;
   const int64_t ntiles = tm * tn;
-  const int64_t grid = (ntiles + 7) / 8 * 8;
+  // big grids (several rounds of the 512 workgroup slots): super-tile schedule
+  const int super = (CLOW ? ntiles / 2 : ntiles) >= 1024 ? 1 : 0;
+  const int64_t grid = super ? mg_super_grid(tm, tn, CLOW) : (ntiles + 7) / 8 * 8;
   // every product here has one triangular operand or output: M*N*rank useful flops
   LaunchTimer timer(HI2X_TIME_CHOL_GEMM, (double)a.M * a.N * a.Kd, s);
   hipLaunchKernelGGL((tri_gemm_kernel<AMODE, BMODE, TB, CLOW>), dim3((unsigned)grid), dim3(256),
-                     0, s, a, tn, ntiles);
+                     0, s, a, tm, tn, super);
   return launch_status("tri_gemm_kernel");
 }
 

@@ -292,4 +292,61 @@ __device__ __forceinline__ int64_t xcd_tile(int64_t id, int64_t ntiles) {
   return t < ntiles ? t : -1;
 }
 
+// Super-tile schedule for large grids: groups of 8 x 8 tiles (64 tiles, one per
+// workgroup slot of an XCD at two workgroups per CU) go whole to one XCD, so the 8 row
+// panels and 8 column panels they read are shared in that XCD's L2; groups are dealt to
+// the 8 XCDs in turn, heaviest first.  ORDER says where the heavy tiles are (the rank
+// of a triangular product grows along rows or columns):
+//   0 uniform, 1 heaviest at the bottom rows, 2 at the right columns, 3 at the left.
+// TRI enumerates only the lower triangle of a square grid (uniform work).
+constexpr int MG_SUP = 8;  // super-tile edge (tiles)
+
+__host__ __device__ inline int64_t mg_super_count(int64_t tm, int64_t tn, bool tri) {
+  const int64_t nsr = (tm + MG_SUP - 1) / MG_SUP, nsc = (tn + MG_SUP - 1) / MG_SUP;
+  return tri ? nsr * (nsr + 1) / 2 : nsr * nsc;
+}
+
+// workgroups to launch for the super-tile schedule (8 XCDs x 64 slots per group round)
+__host__ inline int64_t mg_super_grid(int64_t tm, int64_t tn, bool tri) {
+  const int64_t nsup = mg_super_count(tm, tn, tri);
+  return (nsup + 7) / 8 * 8 * MG_SUP * MG_SUP;
+}
+
+template <int ORDER, bool TRI>
+__device__ __forceinline__ bool mg_super_tile(int64_t bid, int64_t tm, int64_t tn, int64_t& tr,
+                                              int64_t& tc) {
+  const int64_t x = bid & 7, slot = bid >> 3;
+  const int64_t u = (slot / (MG_SUP * MG_SUP)) * 8 + x;  // super-tile, dealt round-robin
+  const int w = (int)(slot % (MG_SUP * MG_SUP));
+  const int64_t nsr = (tm + MG_SUP - 1) / MG_SUP, nsc = (tn + MG_SUP - 1) / MG_SUP;
+  int64_t sr, sc;
+  if (TRI) {
+    if (u >= nsr * (nsr + 1) / 2) return false;
+    sr = (int64_t)((sqrtf(8.0f * (float)u + 1.0f) - 1.0f) * 0.5f);
+    while (sr * (sr + 1) / 2 > u) --sr;
+    while ((sr + 1) * (sr + 2) / 2 <= u) ++sr;
+    sc = u - sr * (sr + 1) / 2;
+  } else {
+    if (u >= nsr * nsc) return false;
+    if (ORDER == 1) {
+      sr = nsr - 1 - u / nsc;
+      sc = u % nsc;
+    } else if (ORDER == 2) {
+      sc = nsc - 1 - u / nsr;
+      sr = u % nsr;
+    } else if (ORDER == 3) {
+      sc = u / nsr;
+      sr = u % nsr;
+    } else {
+      sr = u / nsc;
+      sc = u % nsc;
+    }
+  }
+  tr = sr * MG_SUP + w / MG_SUP;
+  tc = sc * MG_SUP + w % MG_SUP;
+  if (tr >= tm || tc >= tn) return false;
+  if (TRI && tc > tr) return false;
+  return true;
+}
+
 }  // namespace hi2x

@@ -330,6 +330,27 @@ def test_inverse_factor_inverts(dev, k):
     assert np.allclose(u, u_o, rtol=1e-3, atol=2e-4 * scale)
 
 
+def test_inverse_factor_inverts_large(dev):
+    """K = 8448: every product of the top recursion levels runs the super-tile schedule
+    of the large-grid path (4356 tiles); checked by U^T U (Hs + lam I) = I in float64 on
+    the device (the CPU oracle would take minutes at this size)."""
+    from hi2_amd.hessian import inverse_factor
+
+    k = 8448
+    g = torch.Generator(device=dev).manual_seed(11)
+    x = torch.randn(2 * k, k, device=dev, generator=g)
+    x = x * torch.exp(0.5 * torch.randn(1, k, device=dev, generator=g))
+    hs = (x.T.double() @ x.double() / x.shape[0]).float().contiguous()
+    u = inverse_factor(hs, 0.01).double()
+    assert torch.equal(torch.tril(u, -1), torch.zeros_like(u))
+    assert bool((torch.diagonal(u) > 0).all())
+    h = hs.double()
+    damped = h + 0.01 * torch.diagonal(h).mean() * torch.eye(k, device=dev, dtype=torch.float64)
+    r = u.T @ (u @ damped)
+    err = (r - torch.eye(k, device=dev, dtype=torch.float64)).abs().max().item()
+    assert err < 5e-3, err
+
+
 def test_inverse_factor_retries_and_survives_singular(dev):
     from hi2_amd.hessian import inverse_factor
 
