@@ -75,6 +75,9 @@ def make_inputs(dev, seed=0):
 
 
 ORDER = ["down", "mlp", "attn", "o"]  # calibration inputs, longest chain first
+# streams and the inputs each one encodes in turn (one stream per input measured best:
+# the short chains fill the GPU around the long chain's latency-bound steps)
+LANES = [["down"], ["mlp"], ["attn"], ["o"]]
 _CHAIN_STREAMS = {}
 
 
@@ -89,7 +92,7 @@ def _chain_stream(dev, i):
     return _CHAIN_STREAMS[key]
 
 
-def encode_block(xs, ws, masks, timer=None):
+def encode_block(xs, ws, masks, timer=None, lanes=None):
     """Encode the whole block.  Each calibration input runs its own chain on its own
     stream (Hessian -> transform -> factor -> rotation -> GPTQ -> packing of the linears
     it feeds); the chains are independent, so they overlap on the GPU.  The host waits
@@ -102,11 +105,16 @@ def encode_block(xs, ws, masks, timer=None):
 
     dev = next(iter(xs.values())).device
     main = torch.cuda.current_stream(dev)
+    lanes = LANES if lanes is None else lanes
+    lane_of = {inp: li for li, lane in enumerate(lanes) for inp in lane}
+    order = [inp for lane in zip(*[l + [None] * (4 - len(l)) for l in lanes]) for inp in lane
+             if inp is not None]
     chains = {}
-    for ci, inp in enumerate(ORDER):
+    for li in range(len(lanes)):
+        _chain_stream(dev, li).wait_stream(main)
+    for inp in order:
         k = INPUTS[inp]
-        st = _chain_stream(dev, ci)
-        st.wait_stream(main)
+        st = _chain_stream(dev, lane_of[inp])
         mark = (lambda stage, inp=inp: timer.mark(inp, stage)) if timer else (lambda stage: None)
         with torch.cuda.stream(st):
             had = torch.ones(k // 16, dtype=torch.uint8, device=dev)
@@ -134,7 +142,7 @@ def encode_block(xs, ws, masks, timer=None):
             mark("end")
         chains[inp] = (st, hs, u, status, had, jobs, where, encs)
     out = {}
-    for inp in reversed(ORDER):  # shortest chains finish first: pack them meanwhile
+    for inp in reversed(order):  # the long chain last: the others are packed meanwhile
         st, hs, u, status, had, jobs, where, encs = chains[inp]
         with torch.cuda.stream(st):
             if finish_factor(hs, u, status, DAMP):  # more damping was needed: redo the rounding

@@ -120,7 +120,7 @@ int tri_gemm(const GemmArgs& a, hipStream_t s) {
   const int64_t tm = (a.M + MG_T - 1) / MG_T, tn = (a.N + MG_T - 1) / MG_T;
   const int64_t ntiles = tm * tn;
   // big grids (several rounds of the 512 workgroup slots): super-tile schedule
-  const int super = (CLOW ? ntiles / 2 : ntiles) >= 1024 ? 1 : 0;
+  const int super = (CLOW ? ntiles / 2 : ntiles) >= 256 ? 1 : 0;
   const int64_t grid = super ? mg_super_grid(tm, tn, CLOW) : (ntiles + 7) / 8 * 8;
   // every product here has one triangular operand or output: M*N*rank useful flops
   LaunchTimer timer(HI2X_TIME_CHOL_GEMM, (double)a.M * a.N * a.Kd, s);

@@ -16,77 +16,84 @@
 namespace hi2x {
 namespace {
 
-// ---------------------------------------------------------------------------------
 // Intra-block kernel.
 //
-// One row is owned by a quad of lanes (16 rows per wave, 64 per workgroup).  Lane q of
-// the quad holds the row's columns c = 4m + q (m = 0..31) of the 128-column block in
-// registers, together with the decoded (lo, step) of each column's ladder block.  The
-// factor block U[i1:i1+128, i1:i1+128] of the row's group sits in LDS, laid out so that
-// lane q reads its 32 columns of a U row contiguously: su[i][q][m] = U[i1+i][i1+4m+q].
+// One row is owned by 16 lanes (a DPP row: 4 rows per wave, 16 per workgroup).  Lane q
+// holds the row's columns c = 16m + q (m = 0..7) of the 128-column block in registers,
+// with the decoded (lo, step) of each column's ladder block.  The factor block
+// U[i1:i1+128, i1:i1+128] of the row's group sits in LDS, laid out so that lane q reads
+// its 8 columns of a U row as two 16-byte vectors (U[i1+i][i1+16m+q], m = 0..7, from
+// lane_off(q)).  The U row of step i+1 is read during step i.
 //
-// Step i (fully unrolled): every lane runs the rounding chain on its own column m=i/4;
-// only lane q = i%4 owns column i, so its error e is broadcast to the quad with a DPP
-// quad_perm, recorded by the owner, and the quad applies w[c] -= e * U[i][c] to the
-// columns it holds.  Columns <= i of the other lanes are dead (already rounded), so
-// updating them is harmless.  Every product and difference is rounded separately
-// (-ffp-contract=off), division is IEEE, rounding to an integer is half-to-even: the
+// Step i (fully unrolled): every lane runs the rounding chain on its own column m=i/16;
+// only lane q = i%16 owns column i (its U value of row i is then U[i][i]), so its error e
+// is broadcast to the row with DPP row_newbcast, recorded by the owner, and the row
+// applies w[c] -= e * U[i][c] to the columns it holds.  Columns <= i of the other lanes
+// are dead (already rounded), so updating them is harmless.  Every product and
+// difference is rounded separately (-ffp-contract=off), division is IEEE, rounding to an
+// integer is half-to-even, and every column receives its updates in step order: the
 // codes, errors and compensated values are bit-identical to the reference loop.
 // ---------------------------------------------------------------------------------
 constexpr int LMAX = 128;
-constexpr int QL = 4;                 // lanes per row
+constexpr int QL = 16;                // lanes per row
 constexpr int CPL = LMAX / QL;        // columns per lane
 constexpr int RPW = 64 / QL;          // rows per wave
 constexpr int WPG = 4;                // waves per workgroup
 constexpr int RPG = RPW * WPG;        // rows per workgroup
-constexpr int QSTR = CPL + 4;         // per-lane stride in an LDS U row (bank spread)
-constexpr int USTR = QL * QSTR;       // LDS U row stride (floats)
+constexpr int USTR = QL * CPL + 4;    // LDS U row stride (floats)
+
+// Start of lane q's 8 columns in an LDS U row: lanes 8..15 are shifted by 4 floats so
+// that the 16 lanes' 16-byte reads fall on distinct banks.
+__device__ __forceinline__ int lane_off(int q) { return q * CPL + ((q >> 3) << 2); }
 
 template <int S>
-__device__ __forceinline__ float quad_bcast(float v) {
-  constexpr int ctrl = S * 0x55;  // quad_perm(S, S, S, S)
-  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), ctrl,
-                                                            0xf, 0xf, false));
+__device__ __forceinline__ float row_bcast(float v) {  // lane S of each 16-lane row
+  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v),
+                                                            0x150 + S, 0xf, 0xf, false));
 }
 
-// Register state of one row (this lane's 32 columns).
+// Register state of one row (this lane's 8 columns).
 struct RowRegs {
   float w[CPL], loc[CPL], stc[CPL], er[CPL];
   uint32_t cq[CPL / 4];
 };
 
 // Step I of the column loop, I a compile-time constant so that every register index
-// below is static (no dynamic VGPR indexing).
+// below is static (no dynamic VGPR indexing).  ub[I & 1] holds this lane's U row I;
+// the step fills ub[(I + 1) & 1] with row I + 1.
 template <int I>
 __device__ __forceinline__ void gptq_step(RowRegs& R, int L, int q, float nm,
-                                          const float* __restrict__ su,
-                                          const float* __restrict__ qrow, float* compr) {
-  constexpr int m = I / QL, s = I % QL;
+                                          const float* __restrict__ suq, f32x4 (&ub)[2][2],
+                                          float* compr) {
+  constexpr int m = I / QL, s = I % QL, cur = I & 1;
   if (I >= L) return;
+  if (I + 1 < LMAX) {
+    ub[cur ^ 1][0] = *reinterpret_cast<const f32x4*>(suq + (I + 1) * USTR);
+    ub[cur ^ 1][1] = *reinterpret_cast<const f32x4*>(suq + (I + 1) * USTR + 4);
+  }
   const float col = R.w[m];
   const float lo_j = R.loc[m], st_j = R.stc[m];
   const float safe = (st_j == 0.0f) ? 1.0f : st_j;
   float qv = clamp_code(__builtin_rintf((col - lo_j) / safe), nm);
   if (st_j == 0.0f) qv = 0.0f;
   const float wq = f16_round(lo_j + qv * st_j);
-  const float ujj = su[I * USTR + s * QSTR + m];
+  const float ujj = ub[cur][m >> 2][m & 3];  // U[I][I] in the owner lane
   const float e = (col - wq) / ujj;
-  const float eb = quad_bcast<s>(e);
+  const float eb = row_bcast<s>(e);
   if (q == s) {
     R.er[m] = e;
     R.cq[m >> 2] |= ((uint32_t)qv & 0xffu) << (8 * (m & 3));
     if (compr) compr[I] = col;
   }
-  const float* urow = qrow + I * USTR;
 #pragma unroll
-  for (int mm = (I + 1) / QL; mm < CPL; ++mm) R.w[mm] = R.w[mm] - eb * urow[mm];
+  for (int mm = (I + 1) / QL; mm < CPL; ++mm) R.w[mm] = R.w[mm] - eb * ub[cur][mm >> 2][mm & 3];
 }
 
 template <int... Is>
 __device__ __forceinline__ void gptq_steps(std::integer_sequence<int, Is...>, RowRegs& R, int L,
-                                           int q, float nm, const float* __restrict__ su,
-                                           const float* __restrict__ qrow, float* compr) {
-  (gptq_step<Is>(R, L, q, nm, su, qrow, compr), ...);
+                                           int q, float nm, const float* __restrict__ suq,
+                                           f32x4 (&ub)[2][2], float* compr) {
+  (gptq_step<Is>(R, L, q, nm, suq, ub, compr), ...);
 }
 
 __global__ __launch_bounds__(RPG * QL) void gptq_block_kernel(
@@ -100,51 +107,84 @@ __global__ __launch_bounds__(RPG * QL) void gptq_block_kernel(
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  const int q = lane & 3;
+  const int q = lane & (QL - 1);
   const int64_t rbase = (int64_t)blockIdx.x * RPG;
-  const int64_t r = rbase + wave * RPW + (lane >> 2);
+  const int lr = wave * RPW + lane / QL;  // row within the workgroup
+  const int64_t r = rbase + lr;
   const bool live = r < N;
   const int64_t rend = ((rbase + RPG < N) ? rbase + RPG : N) - 1;
+  const int nrows = (int)(rend - rbase + 1);
   const int g0 = row_grp[rbase];
   const int g1 = row_grp[rend];
   const int gr = live ? row_grp[r] : -1;
 
+  // Global reads go through buffer resources that end at the last valid element, so
+  // they need no branches (a branch around a load makes the compiler wait for each load
+  // in turn): all loads of a phase are issued before the first is used.
   for (int g = g0; g <= g1; ++g) {
     __syncthreads();  // LDS of the previous group is no longer read
     {
+      // U[i1:i1+L, i1:i1+L]: rows >= L read zero, columns >= L are zeroed here
       const float* U = reinterpret_cast<const float*>(u_ptrs[g]);
-      for (int idx = tid; idx < LMAX * LMAX; idx += RPG * QL) {
-        const int i = idx / LMAX, c = idx % LMAX;
-        const float v = (i < L && c < L) ? U[(i1 + i) * K + i1 + c] : 0.0f;
-        su[i * USTR + (c & 3) * QSTR + (c >> 2)] = v;
+      const __amdgpu_buffer_rsrc_t ur = mg_rsrc(U + i1 * K + i1, (int64_t)(L - 1) * K + L);
+      constexpr int NV = LMAX * LMAX / 4 / (RPG * QL);  // 16-byte vectors per thread
+      f32x4 uv[NV];
+#pragma unroll
+      for (int t = 0; t < NV; ++t) {
+        const int idx = tid + RPG * QL * t, i = idx / (LMAX / 4), c = 4 * (idx % (LMAX / 4));
+        const uint32_t off = i < L ? (uint32_t)(((int64_t)i * K + c) * 4) : MG_OOB;
+        uv[t] = mg_load4(ur, off);
+      }
+#pragma unroll
+      for (int t = 0; t < NV; ++t) {
+        const int idx = tid + RPG * QL * t, i = idx / (LMAX / 4), c = 4 * (idx % (LMAX / 4));
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int cc = c + e;
+          const float v = uv[t][e];
+          su[i * USTR + lane_off(cc % QL) + cc / QL] = (cc < L) ? v : 0.0f;
+        }
       }
     }
     __syncthreads();
-    if (gr != g) continue;  // uniform over the quad (one row)
+    if (gr != g) continue;  // uniform over the row's 16 lanes
 
-    const int32_t* bl = blk + (int64_t)g * K;
     const float nm = nmax[g];
     RowRegs R;
+    {
+      // this row's columns c = 16m + q: the working copy and each column's ladder block
+      const __amdgpu_buffer_rsrc_t wrs =
+          mg_rsrc(wc + rbase * K + i1, (int64_t)(nrows - 1) * K + L);
+      const __amdgpu_buffer_rsrc_t brs = __builtin_amdgcn_make_buffer_rsrc(
+          const_cast<int32_t*>(blk + (int64_t)g * K + i1), (short)0, L * 4, 0x00020000);
+      int bix[CPL];
 #pragma unroll
-    for (int m = 0; m < CPL; ++m) {
-      const int c = QL * m + q;
-      float wv = 0.0f, lv = 0.0f, sv = 0.0f;
-      if (c < L) {
-        wv = wc[r * K + i1 + c];
-        const int b = bl[i1 + c];
-        lv = lo[r * ldp + b];
-        sv = st[r * ldp + b];
+      for (int m = 0; m < CPL; ++m) {
+        const int c = QL * m + q;
+        const uint32_t wo = c < L ? (uint32_t)(((int64_t)lr * K + c) * 4) : MG_OOB;
+        R.w[m] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(wrs, (int)wo, 0, 0));
+        bix[m] = (int)__builtin_amdgcn_raw_buffer_load_b32(brs, (int)(c < L ? c * 4 : MG_OOB), 0, 0);
       }
-      R.w[m] = wv;
-      R.loc[m] = lv;
-      R.stc[m] = sv;
-      R.er[m] = 0.0f;
+      // decoded (lo, step) of those blocks (block 0 for the dead columns c >= L)
+      const __amdgpu_buffer_rsrc_t lrs = mg_rsrc(lo + rbase * ldp, (int64_t)nrows * ldp);
+      const __amdgpu_buffer_rsrc_t srs = mg_rsrc(st + rbase * ldp, (int64_t)nrows * ldp);
+#pragma unroll
+      for (int m = 0; m < CPL; ++m) {
+        const uint32_t po = (uint32_t)(((int64_t)lr * ldp + bix[m]) * 4);
+        R.loc[m] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(lrs, (int)po, 0, 0));
+        R.stc[m] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(srs, (int)po, 0, 0));
+        R.er[m] = 0.0f;
+      }
     }
 #pragma unroll
     for (int m = 0; m < CPL / 4; ++m) R.cq[m] = 0u;
 
+    const float* suq = su + lane_off(q);
+    f32x4 ub[2][2];
+    ub[0][0] = *reinterpret_cast<const f32x4*>(suq);
+    ub[0][1] = *reinterpret_cast<const f32x4*>(suq + 4);
     float* compr = comp ? comp + r * K + i1 : nullptr;
-    gptq_steps(std::make_integer_sequence<int, LMAX>{}, R, L, q, nm, su, su + q * QSTR, compr);
+    gptq_steps(std::make_integer_sequence<int, LMAX>{}, R, L, q, nm, suq, ub, compr);
 
 #pragma unroll
     for (int m = 0; m < CPL; ++m) {
