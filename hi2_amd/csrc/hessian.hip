@@ -122,12 +122,54 @@ __global__ __launch_bounds__(256) void syrk_bf16_kernel(const uint16_t* __restri
 // consecutive tokens of one feature) is a 16-byte vector in memory and in LDS.  A
 // workgroup (4 waves) computes a 256 x 256 upper tile of S; each wave owns 128 x 128 as
 // 4 x 4 accumulators of v_mfma_f32_32x32x16_bf16 (f32 accumulation, products of bf16
-// exact).  Tokens stream in stages of 32 through double-buffered LDS.  Workgroups may
-// split the token range (partials combined in a fixed order afterwards) so that small
-// K still fills the chip.
+// exact).  Tokens stream in stages of 64 through double-buffered LDS, loaded with
+// branch-free buffer loads (features past K read zero) one stage ahead.  Big grids run
+// the super-tile schedule: 4 x 8 tiles of the upper triangle per XCD round, so the 32
+// workgroups of an XCD read 12 feature panels instead of up to 33.  Workgroups may split
+// the token range (partials combined in a fixed order afterwards) so that small K still
+// fills the chip.
 constexpr int S2T = 256;          // workgroup tile edge
-constexpr int S2C = 32;           // tokens per stage
+constexpr int S2C = 64;           // tokens per stage
 constexpr int S2P = S2C + 8;      // LDS pitch (bf16) per feature row
+constexpr int S2R = 4, S2S = 8;   // super-tile: tile rows x tile columns per XCD round
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc_bytes(const void* base, int64_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,
+                                           0x00020000);
+}
+
+// Upper-triangular grid of nT x nT tiles (tb >= ta) cut into super-tiles of S2R x S2S
+// tiles; super-tile (sr, sc) holds upper tiles when sc >= floor(sr * S2R / S2S).  The
+// valid super-tiles are numbered row by row and dealt to the 8 XCDs in turn.
+__host__ __device__ inline int syrk_first_sc(int sr) { return (sr * S2R) / S2S; }
+
+__host__ inline int64_t syrk_super_count(int nT) {
+  const int nsr = (nT + S2R - 1) / S2R, nsc = (nT + S2S - 1) / S2S;
+  int64_t n = 0;
+  for (int sr = 0; sr < nsr; ++sr) n += nsc - syrk_first_sc(sr) > 0 ? nsc - syrk_first_sc(sr) : 0;
+  return n;
+}
+
+__device__ __forceinline__ bool syrk_super_tile(int64_t bid, int nT, int& ta, int& tb) {
+  const int64_t x = bid & 7, slot = bid >> 3;
+  int64_t rem = (slot / (S2R * S2S)) * 8 + x;
+  const int w = (int)(slot % (S2R * S2S));
+  const int nsr = (nT + S2R - 1) / S2R, nsc = (nT + S2S - 1) / S2S;
+  int sr = 0, sc = -1;
+  for (; sr < nsr; ++sr) {
+    const int first = syrk_first_sc(sr);
+    const int cnt = nsc - first > 0 ? nsc - first : 0;
+    if (rem < cnt) {
+      sc = first + (int)rem;
+      break;
+    }
+    rem -= cnt;
+  }
+  if (sc < 0) return false;
+  ta = sr * S2R + w / S2S;
+  tb = sc * S2S + w % S2S;
+  return ta < nT && tb < nT && tb >= ta;
+}
 
 // xt [K, Tp] = x^T with the token range padded with zeros to Tp (a multiple of 64).
 __global__ __launch_bounds__(256) void transpose_bf16_kernel(const uint16_t* __restrict__ x,
@@ -151,15 +193,19 @@ __global__ __launch_bounds__(256) void syrk2_bf16_kernel(const uint16_t* __restr
                                                          int64_t T, int64_t K, int nT,
                                                          int64_t ntiles, int splits,
                                                          int64_t tchunk, float* __restrict__ out,
-                                                         int64_t out_stride) {
+                                                         int64_t out_stride, int super) {
   __shared__ __attribute__((aligned(16))) uint16_t Xa[2][S2T * S2P];
   __shared__ __attribute__((aligned(16))) uint16_t Xb[2][S2T * S2P];
   const int64_t id = (int64_t)blockIdx.x;
-  const int sp = (int)(id % splits);
-  const int64_t tile = xcd_tile(id / splits, ntiles);
-  if (tile < 0) return;
-  int ta, tb;
-  upper_tile(nT, (int)tile, ta, tb);
+  int ta, tb, sp = 0;
+  if (super) {
+    if (!syrk_super_tile(id, nT, ta, tb)) return;
+  } else {
+    sp = (int)(id % splits);
+    const int64_t tile = xcd_tile(id / splits, ntiles);
+    if (tile < 0) return;
+    upper_tile(nT, (int)tile, ta, tb);
+  }
   const bool diag = ta == tb;
   const int64_t a0 = (int64_t)ta * S2T, b0 = (int64_t)tb * S2T;
   const int64_t tbeg = (int64_t)sp * tchunk;
@@ -175,21 +221,28 @@ __global__ __launch_bounds__(256) void syrk2_bf16_kernel(const uint16_t* __restr
 #pragma unroll
       for (int j = 0; j < 16; ++j) acc[a][b][j] = 0.0f;
 
-  // staging (T is the padded token count: every stage is whole, pad tokens are zero)
-  uint4 ra[4], rb[4];
+  // feature panels [a0, a0 + 256) and [b0, b0 + 256) of xt: features past K read zero
+  // (T is the padded token count: every stage is whole, pad tokens are zero)
+  const int rowsA = (int)((K - a0 < S2T) ? K - a0 : S2T);
+  const int rowsB = (int)((K - b0 < S2T) ? K - b0 : S2T);
+  const __amdgpu_buffer_rsrc_t rsa = rsrc_bytes(xt + a0 * T, (int64_t)rowsA * T * 2);
+  const __amdgpu_buffer_rsrc_t rsb = rsrc_bytes(xt + b0 * T, (int64_t)rowsB * T * 2);
+  const uint32_t rowoff = (uint32_t)((int64_t)tid * T * 2);
+  const uint32_t offA = tid < rowsA ? rowoff : MG_OOB;
+  const uint32_t offB = (!diag && tid < rowsB) ? rowoff : MG_OOB;
+  constexpr int NQ = S2C / 8;  // 16-byte vectors per feature row and stage
+  uint4 ra[NQ], rb[NQ];
   auto load = [&](int64_t t0) {
-    const int64_t fa = a0 + tid, fb = b0 + tid;
-    const bool okA = fa < K, okB = !diag && fb < K;
+    const uint32_t tb8 = (uint32_t)(t0 * 2);
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const int64_t tt = t0 + 8 * q;
-      ra[q] = okA ? *reinterpret_cast<const uint4*>(xt + fa * T + tt) : make_uint4(0, 0, 0, 0);
-      rb[q] = okB ? *reinterpret_cast<const uint4*>(xt + fb * T + tt) : make_uint4(0, 0, 0, 0);
+    for (int q = 0; q < NQ; ++q) {
+      ra[q] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rsa, (int)(offA + tb8 + 16 * q), 0, 0));
+      rb[q] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rsb, (int)(offB + tb8 + 16 * q), 0, 0));
     }
   };
   auto store = [&](int buf) {
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
+    for (int q = 0; q < NQ; ++q) {
       *reinterpret_cast<uint4*>(&Xa[buf][tid * S2P + 8 * q]) = ra[q];
       if (!diag) *reinterpret_cast<uint4*>(&Xb[buf][tid * S2P + 8 * q]) = rb[q];
     }
@@ -202,7 +255,8 @@ __global__ __launch_bounds__(256) void syrk2_bf16_kernel(const uint16_t* __restr
   }
   for (int st = 0; st < nst; ++st) {
     const int buf = st & 1;
-    if (st + 1 < nst) load(tbeg + (int64_t)(st + 1) * S2C);
+    const bool more = st + 1 < nst;
+    if (more) load(tbeg + (int64_t)(st + 1) * S2C);
     const uint16_t* XA = Xa[buf];
     const uint16_t* XB = diag ? Xa[buf] : Xb[buf];
 #pragma unroll
@@ -222,23 +276,42 @@ __global__ __launch_bounds__(256) void syrk2_bf16_kernel(const uint16_t* __restr
           acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, bv[b], acc[a][b], 0, 0, 0);
       }
     }
-    if (st + 1 < nst) store(buf ^ 1);  // buffer buf ^ 1 was last read before the barrier
+    __builtin_amdgcn_sched_barrier(0);
+    if (more) store(buf ^ 1);  // buffer buf ^ 1 was last read before the barrier
     __syncthreads();
   }
   // upper part of the tile (i <= j on the diagonal tile); the lower triangle is mirrored
-  // from it afterwards
+  // from it afterwards.  Branch-free: one buffer over the tile, rejected elements get an
+  // offset past it.
+  const __amdgpu_buffer_rsrc_t rss = mg_rsrc(s + a0 * K + b0, (int64_t)(rowsA - 1) * K + rowsB);
+  uint32_t base = (uint32_t)((((int64_t)wr * 128 + 4 * (lane >> 5)) * K + wcn * 128 + (lane & 31)) * 4);
+  asm volatile("" : "+v"(base));
 #pragma unroll
   for (int a = 0; a < 4; ++a)
 #pragma unroll
-    for (int b = 0; b < 4; ++b)
+    for (int b = 0; b < 4; ++b) {
+      uint32_t offs[16];
+      float cur[16];
 #pragma unroll
       for (int j = 0; j < 16; ++j) {
-        const int64_t row = a0 + wr * 128 + a * 32 + 8 * (j >> 2) + 4 * (lane >> 5) + (j & 3);
-        const int64_t col = b0 + wcn * 128 + b * 32 + (lane & 31);
-        if (row >= K || col >= K || (diag && row > col)) continue;
-        if (splits == 1) s[row * K + col] += acc[a][b][j];
-        else s[row * K + col] = acc[a][b][j];
+        const int r = wr * 128 + a * 32 + 8 * (j >> 2) + 4 * (lane >> 5) + (j & 3);
+        const int c = wcn * 128 + b * 32 + (lane & 31);
+        const bool ok = r < rowsA && c < rowsB && !(diag && r > c);
+        offs[j] = ok ? base + (uint32_t)((((int64_t)(a * 32 + 8 * (j >> 2) + (j & 3))) * K + b * 32) * 4)
+                     : MG_OOB;
+        cur[j] = 0.0f;
       }
+      if (splits == 1) {
+#pragma unroll
+        for (int j = 0; j < 16; ++j)
+          cur[j] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rss, (int)offs[j], 0, 0));
+      }
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        const float v = cur[j] + acc[a][b][j];
+        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), rss, (int)offs[j], 0, 0);
+      }
+    }
 }
 
 // S (upper triangle) += partial_0 + partial_1 + ... in split order.
@@ -466,10 +539,13 @@ int launch_syrk(const void* x, int dtype, int64_t t, int64_t k, float* s, char* 
                      dim3(256), 0, st, (const uint16_t*)x, t, k, p.tp, xt);
   int rc = launch_status("transpose_bf16_kernel");
   if (!rc) {
-    const int64_t grid = (p.ntiles + 7) / 8 * 8 * p.splits;
+    // one workgroup per CU: super-tile rounds once the tiles fill several rounds
+    const int super = (p.splits == 1 && p.ntiles >= 512) ? 1 : 0;
+    const int64_t grid = super ? (syrk_super_count(p.nT) + 7) / 8 * 8 * S2R * S2S
+                               : (p.ntiles + 7) / 8 * 8 * p.splits;
     LaunchTimer timer(HI2X_TIME_HESSIAN_SYRK, 2.0 * t * k * k, st);
     hipLaunchKernelGGL(syrk2_bf16_kernel, dim3((unsigned)grid), dim3(256), 0, st, xt, p.tp, k,
-                       p.nT, p.ntiles, p.splits, p.tchunk, parts ? parts : s, k * k);
+                       p.nT, p.ntiles, p.splits, p.tchunk, parts ? parts : s, k * k, super);
     rc = launch_status("syrk2_bf16_kernel");
   }
   if (!rc && parts) {

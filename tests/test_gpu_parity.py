@@ -295,6 +295,30 @@ def test_hessian_stats_equal_xtx(dev, dtype, t, k):
     assert torch.allclose(st.mean(), st.S / t)
 
 
+def test_hessian_stats_large_k_super_schedule(dev):
+    """K = 8448 (33 tiles of 256, 561 upper tiles): the bf16 SYRK runs its super-tile
+    schedule and accumulates into a nonzero S (two updates); checked against X^T X in
+    float64 on the device (bf16 products are exact, the sums are f32)."""
+    from hi2_amd.hessian import HessianStats
+
+    k, t = 8448, 640
+    g = torch.Generator(device=dev).manual_seed(5)
+    x = (torch.randn(t, k, device=dev, generator=g)
+         * torch.exp(torch.randn(1, k, device=dev, generator=g))).to(torch.bfloat16)
+    st = HessianStats(k, dev)
+    st.update(x[:256])
+    st.update(x[256:])
+    xd = x.double()
+    want = xd.T @ xd
+    got = st.S.double()
+    assert torch.equal(st.S, st.S.T)
+    # the tolerance of the other Hessian tests (f32 sums of exact products over t terms)
+    assert torch.allclose(got, want, rtol=1e-4, atol=1e-4 * want.abs().max().item())
+    # the diagonal sums positive terms only: relative agreement entry by entry
+    dg = torch.diagonal(got), torch.diagonal(want)
+    assert ((dg[0] - dg[1]).abs() / dg[1]).max().item() < 1e-5
+
+
 @pytest.mark.parametrize("smooth", [False, True])
 def test_transform_sigma_equals_oracle(dev, smooth):
     from hi2_amd.hessian import transform_sigma
