@@ -274,22 +274,34 @@ def _round_kernel(
     reference's rounding."""
     dev, k = units[0].wc.device, units[0].wc.shape[1]
     sizes = [x.wc.shape[0] for x in units]
-    total = sum(sizes)
-    wc = torch.cat([x.wc for x in units]) if len(units) > 1 else units[0].wc
+    # Every unit starts on a 128-row boundary: no workgroup or tile of the kernels then
+    # holds rows of two factors (it would run once per factor).  Padding rows have
+    # w = lo = step = 0: they round to code 0 with zero error and change nothing.
+    if len(units) > 1:
+        padded = [-(-n // BLOCK_COLUMNS) * BLOCK_COLUMNS for n in sizes]
+    else:
+        padded = sizes
+    total = sum(padded)
+    if len(units) > 1:
+        wc = torch.zeros(total, k, dtype=torch.float32, device=dev)
+    else:
+        wc = units[0].wc
     ldp = k // 16
     lo = torch.zeros(total, ldp, dtype=torch.float32, device=dev)
     st = torch.zeros(total, ldp, dtype=torch.float32, device=dev)
     views, off = [], 0
-    for x, n in zip(units, sizes):
+    for x, n, pn in zip(units, sizes, padded):
         nb = x.lo_d.shape[1]
+        if len(units) > 1:
+            wc[off : off + n] = x.wc
         lo[off : off + n, :nb] = x.lo_d
         st[off : off + n, :nb] = x.step_d
         views.append((off, n))
-        off += n
+        off += pn
     # small index arrays: built on the host, copied without blocking the host (other
     # streams keep being fed while this batch waits for its inputs)
     row_grp = _lib.h2d(torch.repeat_interleave(
-        torch.arange(len(units), dtype=torch.int32), torch.tensor(sizes)), dev)
+        torch.arange(len(units), dtype=torch.int32), torch.tensor(padded)), dev)
     uk = [jobs[x.job].u.to(dev, torch.float32).contiguous() for x in units]
     for u in uk:
         if u.shape != (k, k):
