@@ -332,11 +332,13 @@ def main():
     ms_step = wall * 1e3 / args.steps
     stages = timer.summary()
     roof = roofline(DOMINANT)
-    # one more, untimed step with every kernel family event-timed: per-kernel breakdown
+    # one more, untimed step with every kernel family event-timed and the chains run one
+    # after another on one stream: per-kernel rates without other chains sharing the GPU
     _lib.timing_enable(list(KERNELS))
-    encode_block(xs, ws, masks)
+    encode_block(xs, ws, masks, lanes=[ORDER])
     torch.cuda.synchronize()
     kernels = {KERNELS[k][0]: kernel_stats(k) for k in KERNELS}
+    roof_iso = roofline(DOMINANT)
     _lib.timing_enable([])
     res = {
         "metric": "encode ms per linear layer (Llama-3-8B-shaped block, 7 linears)",
@@ -357,6 +359,7 @@ def main():
                    "hessian_input_dtype": "bf16 (f32 accumulation)"},
         "chain_stages_ms": stages,
         "roofline": roof,
+        "roofline_isolated": roof_iso,
         "kernels_one_step": kernels,
     }
     if not args.no_cpu:
