@@ -211,74 +211,76 @@ __global__ __launch_bounds__(256) void reverse_damp_kernel(const float* __restri
 // with the products on v_mfma_f32_16x16x4f32 (each product is read into registers,
 // then written back in place after a barrier).
 //
-// The 16 x 16 base is one wave's fused factor-and-invert sweep, lane l holding row
-// i = l/4, columns j = 4(l%4) + e, e < 4.  For c = 0..15:
+// The 16 x 16 base is one wave's fused factor-and-invert sweep, lane i (< 16) holding row
+// i in 16 registers.  For c = 0..15:
 //   piv = sqrt(T[c][c]), rp = 1/piv; l_i = T[i][c] rp; the multiplier of column j is
 //   l_j = T[j][c] rp for j > c, rp for j = c, x_j = B[c][j] rp for j < c (row c of L^-1).
 //   Rows i > c, j <= i:  T[i][j] -= l_i m_j  (j > c: Cholesky update; j = c: starts
 //   column c of L^-1 as -l_i rp; j < c: forward substitution)
 //   Row c is final: X[c][j] = B[c][j] rp, X[c][c] = rp.
-// Column c comes from the row's own quad (DPP), T[j][c] and B[c][j] from other quads
-// (ds_bpermute), the pivot by readlane: no barrier and no LDS traffic in the sweep.  The
-// reciprocal and square root are the hardware approximations (the factor is compared to
-// a tolerance, not bit for bit).
+// The pivot, column c (T[j][c] of every row j) and row c (B[c][j]) are read into scalar
+// registers with readlane, l_i is the lane's own register: no barrier and no LDS traffic
+// in the sweep.  The reciprocal and square root are the hardware approximations (the
+// factor is compared to a tolerance, not bit for bit).
 constexpr int LP = NB + 4;  // LDS pitch of the leaf block (floats)
 
 typedef float f32x4v __attribute__((ext_vector_type(4)));
 
-template <int Q>
-__device__ __forceinline__ float quad_pick(float v) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), Q * 0x55,
-                                                            0xf, 0xf, false));
+template <int C, int J>
+__device__ __forceinline__ float lane_read(const float (&v)[16]) {  // v[J] of lane C (uniform)
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v[J]), C));
 }
 
-__device__ __forceinline__ float lane_fetch(float v, int src_lane) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(src_lane * 4,
-                                                                __builtin_bit_cast(int, v)));
-}
-
-template <int C>
-__device__ __forceinline__ void base_step(float (&v)[4], int l, bool& bad) {
-  constexpr int QC = C / 4, EC = C % 4;
-  const int i = l >> 2, q = l & 3;
-  const float d = __builtin_bit_cast(
-      float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v[EC]), 4 * C + QC));
+template <int C, int... Js>
+__device__ __forceinline__ void base_step(float (&v)[16], int i, bool& bad,
+                                          std::integer_sequence<int, Js...>) {
+  const float d = lane_read<C, C>(v);  // pivot T[c][c]
   bad = bad || !(d > 0.0f);
   const float rp = __builtin_amdgcn_rcpf(__builtin_amdgcn_sqrtf(d));
-  const float li = quad_pick<QC>(v[EC]) * rp;
-  float colv[4], rowv[4];
-#pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    colv[e] = lane_fetch(v[EC], 16 * q + 4 * e + QC);  // T[j][c], j = 4q + e
-    rowv[e] = lane_fetch(v[e], 4 * C + q);             // B[c][j]
-  }
-#pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    const int j = 4 * q + e;
-    const float m = (j > C) ? colv[e] * rp : (j == C ? rp : rowv[e] * rp);
-    if (i > C && j <= i) {
-      const float cur = (j == C) ? 0.0f : v[e];
-      v[e] = __builtin_fmaf(-li, m, cur);
-    } else if (i == C) {
-      v[e] = (j < C) ? v[e] * rp : (j == C ? rp : v[e]);
-    }
-  }
+  const bool below = i > C, at = i == C;
+  const float li = v[C] * rp;  // l_i = T[i][c] rp (rows below c)
+  // row c is final first: X[c][j] = B[c][j] rp (j < c), X[c][c] = rp
+  const float sc = at ? rp : 1.0f;
+  ((v[Js] = Js < C ? v[Js] * sc : v[Js]), ...);
+  v[C] = at ? rp : v[C];
+  // multipliers, uniform over the wave: l_j from row j (j > c), row c's finals (j <= c)
+  const float m[16] = {(Js > C ? __builtin_bit_cast(float, __builtin_amdgcn_readlane(
+                                     __builtin_bit_cast(int, li), (Js > C ? Js : 0)))
+                               : lane_read<C, (Js <= C ? Js : 0)>(v))...};
+  // rows below c: T[i][j] -= l_i m_j (j > c), column c starts as -l_i rp, B[i][j] -= l_i x_j
+  const float lb = below ? li : 0.0f;
+  ((v[Js] = Js == C ? (below ? -lb * m[Js] : v[Js]) : __builtin_fmaf(-lb, m[Js], v[Js])), ...);
 }
 
 template <int... Cs>
-__device__ __forceinline__ void base_steps(float (&v)[4], int l, bool& bad,
+__device__ __forceinline__ void base_steps(float (&v)[16], int i, bool& bad,
                                            std::integer_sequence<int, Cs...>) {
-  (base_step<Cs>(v, l, bad), ...);
+  (base_step<Cs>(v, i, bad, std::make_integer_sequence<int, 16>{}), ...);
 }
 
-// 16 x 16 block at (o, o): one wave (the caller's wave 0)
+// 16 x 16 block at (o, o): one wave (the caller's wave 0), lane i holds row i % 16 (lanes
+// 16..63 repeat rows 0..15 and do not write back)
 __device__ __forceinline__ void leaf_base16(float* S, int o, bool& bad) {
-  const int l = threadIdx.x & 63;
-  float* row = &S[(o + (l >> 2)) * LP + o + 4 * (l & 3)];
-  const float4 x = *reinterpret_cast<const float4*>(row);
-  float v[4] = {x.x, x.y, x.z, x.w};
-  base_steps(v, l, bad, std::make_integer_sequence<int, 16>{});
-  *reinterpret_cast<float4*>(row) = make_float4(v[0], v[1], v[2], v[3]);
+  const int l = threadIdx.x & 63, i = l & 15;
+  float* row = &S[(o + i) * LP + o];
+  float v[16];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const float4 x = *reinterpret_cast<const float4*>(row + 4 * q);
+    v[4 * q] = x.x;
+    v[4 * q + 1] = x.y;
+    v[4 * q + 2] = x.z;
+    v[4 * q + 3] = x.w;
+  }
+  base_steps(v, i, bad, std::make_integer_sequence<int, 16>{});
+#pragma unroll
+  for (int j = 0; j < 16; ++j) v[j] = j <= i ? v[j] : 0.0f;  // the block stays lower
+  if (l < 16) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      *reinterpret_cast<float4*>(row + 4 * q) =
+          make_float4(v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]);
+  }
 }
 
 // C[H x H] at (cr, cc) = alpha * A (at (ar, ac)) * op(B) (at (br, bc)), op(B) = B^T when
