@@ -288,17 +288,25 @@ __device__ __forceinline__ void leaf_base16(float* S, int o, bool& bad) {
 // the leaf's LDS; the result is written after all inputs have been read (C may alias).
 // For each 16 k: lane group g = l/16 supplies k = 16 kb + 4 g + s at MFMA step s, so a
 // lane reads its 4 k of A (and of B^T) as one 16-byte vector.
-template <int H, bool TB, bool LOWER>
-__device__ __forceinline__ void leaf_prod(float* S, int ar, int ac, int br, int bc, int cr,
-                                          int cc, float alpha) {
-  constexpr int NT = H / 16, TILES = NT * NT, PER = (TILES + 3) / 4;
+template <int H>
+struct ProdAcc {  // this wave's tiles of an H x H product (tile t = wave + 4p, p < PER)
+  static constexpr int NT = H / 16, TILES = NT * NT, PER = (TILES + 3) / 4;
+  f32x4v acc[PER];
+};
+
+// acc = A (at (ar, ac)) * op(B) (at (br, bc)), H x H blocks of the leaf's LDS, op(B) = B^T
+// when TB.  For each 16 k: lane group g = l/16 supplies k = 16 kb + 4 g + s at MFMA step
+// s, so a lane reads its 4 k of A (and of B^T) as one 16-byte vector.
+template <int H, bool TB>
+__device__ __forceinline__ void leaf_mma(const float* S, int ar, int ac, int br, int bc,
+                                         ProdAcc<H>& P) {
+  constexpr int NT = ProdAcc<H>::NT, TILES = ProdAcc<H>::TILES, PER = ProdAcc<H>::PER;
   const int wave = threadIdx.x >> 6, l = threadIdx.x & 63;
   const int lr = l & 15, lg = l >> 4;
-  f32x4v acc[PER];
 #pragma unroll
   for (int p = 0; p < PER; ++p) {
     const int t = wave + 4 * p;
-    acc[p] = (f32x4v){0.0f, 0.0f, 0.0f, 0.0f};
+    P.acc[p] = (f32x4v){0.0f, 0.0f, 0.0f, 0.0f};
     if (t < TILES) {
       const int tr = t / NT, tc = t % NT;
 #pragma unroll
@@ -312,29 +320,52 @@ __device__ __forceinline__ void leaf_prod(float* S, int ar, int ac, int br, int 
           const float* bp = &S[(br + k) * LP + bc + tc * 16 + lr];
           b = make_float4(bp[0], bp[LP], bp[2 * LP], bp[3 * LP]);
         }
-        acc[p] = __builtin_amdgcn_mfma_f32_16x16x4f32(a.x, b.x, acc[p], 0, 0, 0);
-        acc[p] = __builtin_amdgcn_mfma_f32_16x16x4f32(a.y, b.y, acc[p], 0, 0, 0);
-        acc[p] = __builtin_amdgcn_mfma_f32_16x16x4f32(a.z, b.z, acc[p], 0, 0, 0);
-        acc[p] = __builtin_amdgcn_mfma_f32_16x16x4f32(a.w, b.w, acc[p], 0, 0, 0);
+        P.acc[p] = __builtin_amdgcn_mfma_f32_16x16x4f32(a.x, b.x, P.acc[p], 0, 0, 0);
+        P.acc[p] = __builtin_amdgcn_mfma_f32_16x16x4f32(a.y, b.y, P.acc[p], 0, 0, 0);
+        P.acc[p] = __builtin_amdgcn_mfma_f32_16x16x4f32(a.z, b.z, P.acc[p], 0, 0, 0);
+        P.acc[p] = __builtin_amdgcn_mfma_f32_16x16x4f32(a.w, b.w, P.acc[p], 0, 0, 0);
       }
     }
   }
+}
+
+// (row, col) within the H x H product of register j of tile p of this lane
+template <int H>
+__device__ __forceinline__ int prod_row(int p, int j) {
+  const int t = (threadIdx.x >> 6) + 4 * p;
+  return (t / ProdAcc<H>::NT) * 16 + 4 * ((threadIdx.x & 63) >> 4) + j;
+}
+template <int H>
+__device__ __forceinline__ int prod_col(int p) {
+  const int t = (threadIdx.x >> 6) + 4 * p;
+  return (t % ProdAcc<H>::NT) * 16 + (threadIdx.x & 15);
+}
+template <int H>
+__device__ __forceinline__ bool prod_live(int p) {
+  return (threadIdx.x >> 6) + 4 * p < ProdAcc<H>::TILES;
+}
+
+// C[H x H] at (cr, cc) = alpha * A op(B); with LOWER, C += alpha * A op(B) on the lower
+// triangle of C only.  The result is written after all inputs have been read (C may
+// alias an input).
+template <int H, bool TB, bool LOWER>
+__device__ __forceinline__ void leaf_prod(float* S, int ar, int ac, int br, int bc, int cr,
+                                          int cc, float alpha) {
+  ProdAcc<H> P;
+  leaf_mma<H, TB>(S, ar, ac, br, bc, P);
   __syncthreads();
 #pragma unroll
-  for (int p = 0; p < PER; ++p) {
-    const int t = wave + 4 * p;
-    if (t < TILES) {
-      const int tr = t / NT, tc = t % NT;
+  for (int p = 0; p < ProdAcc<H>::PER; ++p) {
+    if (!prod_live<H>(p)) continue;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int r = tr * 16 + 4 * lg + j, c = tc * 16 + lr;
-        const float x = acc[p][j];
-        float* d = &S[(cr + r) * LP + cc + c];
-        if (LOWER) {
-          if (c <= r) *d = *d + alpha * x;
-        } else {
-          *d = alpha * x;
-        }
+    for (int j = 0; j < 4; ++j) {
+      const int r = prod_row<H>(p, j), c = prod_col<H>(p);
+      const float x = P.acc[p][j];
+      float* d = &S[(cr + r) * LP + cc + c];
+      if (LOWER) {
+        if (c <= r) *d = *d + alpha * x;
+      } else {
+        *d = alpha * x;
       }
     }
   }
@@ -361,14 +392,14 @@ __device__ __forceinline__ bool leaf_rec(float* S, int o) {
   }
 }
 
-__global__ __launch_bounds__(256) void leaf_kernel(float* __restrict__ P, int64_t K, int64_t r0,
-                                                   int n, int* __restrict__ status) {
-  __shared__ float S[NB * LP];
-  const int tid = threadIdx.x;
-  // the block's rows as one buffer ending at its last element: rows past n read zero;
-  // n and K are multiples of 16, so every 16-byte vector is all in or all out
-  const __amdgpu_buffer_rsrc_t rs = mg_rsrc(P + r0 * K + r0, (int64_t)(n - 1) * K + n);
+// Rows [0, n) x columns [0, n) of the n x n diagonal block at P (row stride K) into the
+// LDS block at row offset so of S: lower triangle, zeros above, identity beyond n.  The
+// buffer ends at the block's last element: rows past n read zero; n and K are multiples
+// of 16, so every 16-byte vector is all in or all out.
+__device__ __forceinline__ void leaf_load(float* S, int so, const float* P, int64_t K, int n) {
+  const __amdgpu_buffer_rsrc_t rs = mg_rsrc(P, (int64_t)(n - 1) * K + n);
   constexpr int V = NB / 4;  // float4 per row
+  const int tid = threadIdx.x;
   float4 x[NB * V / 256];
 #pragma unroll
   for (int q = 0; q < NB * V / 256; ++q) {
@@ -381,24 +412,117 @@ __global__ __launch_bounds__(256) void leaf_kernel(float* __restrict__ P, int64_
     const int idx = tid + 256 * q, i = idx / V, j = 4 * (idx % V);
     float e[4] = {x[q].x, x[q].y, x[q].z, x[q].w};
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {  // lower triangle of the block, identity beyond n
+    for (int t = 0; t < 4; ++t) {
       const int jj = j + t;
       e[t] = (i < n && jj < n) ? (jj <= i ? e[t] : 0.0f) : (i == jj ? 1.0f : 0.0f);
     }
-    *reinterpret_cast<float4*>(&S[i * LP + j]) = make_float4(e[0], e[1], e[2], e[3]);
+    *reinterpret_cast<float4*>(&S[(so + i) * LP + j]) = make_float4(e[0], e[1], e[2], e[3]);
   }
-  __syncthreads();
-  const bool bad = leaf_rec<NB>(S, 0);
-  if (tid == 0 && bad) atomicMin(status, (int)(r0 + 1));
-  // rows < n back in full vectors: the zeros above the diagonal land in P's upper
-  // triangle, which nothing reads before the final reflection overwrites it
+}
+
+// The LDS block at row offset so back to rows [0, n) x columns [0, n) at P in full
+// vectors: the zeros above the diagonal land in P's upper triangle, which nothing reads
+// before the final reflection overwrites it.
+__device__ __forceinline__ void leaf_store(const float* S, int so, float* P, int64_t K, int n) {
+  const __amdgpu_buffer_rsrc_t rs = mg_rsrc(P, (int64_t)(n - 1) * K + n);
+  constexpr int V = NB / 4;
+  const int tid = threadIdx.x;
 #pragma unroll
   for (int q = 0; q < NB * V / 256; ++q) {
     const int idx = tid + 256 * q, i = idx / V, j = 4 * (idx % V);
     const uint32_t off = (i < n && j < n) ? (uint32_t)(((int64_t)i * K + j) * 4) : MG_OOB;
-    const float4 v = *reinterpret_cast<const float4*>(&S[i * LP + j]);
-    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(__attribute__((ext_vector_type(4))) unsigned, v),
-                                           rs, (int)off, 0, 0);
+    const float4 v = *reinterpret_cast<const float4*>(&S[(so + i) * LP + j]);
+    __builtin_amdgcn_raw_buffer_store_b128(
+        __builtin_bit_cast(__attribute__((ext_vector_type(4))) unsigned, v), rs, (int)off, 0, 0);
+  }
+}
+
+__global__ __launch_bounds__(256) void leaf_kernel(float* __restrict__ P, int64_t K, int64_t r0,
+                                                   int n, int* __restrict__ status) {
+  __shared__ float S[NB * LP];
+  float* blk = P + r0 * K + r0;
+  leaf_load(S, 0, blk, K, n);
+  __syncthreads();
+  const bool bad = leaf_rec<NB>(S, 0);
+  if (threadIdx.x == 0 && bad) atomicMin(status, (int)(r0 + 1));
+  leaf_store(S, 0, blk, K, n);
+}
+
+// A whole recursion node of m = 128 + m2 columns (0 < m2 <= 128) in one workgroup: both
+// diagonal blocks live in LDS (rows 0..127 and 128..255 of S), so the node's two leaves
+// and four 128 x 128 products run without a launch in between:
+//   S_A = leaf(A11) -> A11;  S_B = A21;  T1 = S_B S_A^T -> S_B;  T2 = T1 S_A -> S_A;
+//   S_B = A22 - T1 T1^T (lower);  S_B = leaf(S_B) -> A22;  A21 = -S_B T2.
+__global__ __launch_bounds__(256) void node_kernel(float* __restrict__ P, int64_t K, int64_t r0,
+                                                   int m2, int* __restrict__ status) {
+  __shared__ float S[2 * NB * LP];
+  float* a11 = P + r0 * K + r0;
+  float* a21 = P + (r0 + NB) * K + r0;
+  float* a22 = P + (r0 + NB) * K + (r0 + NB);
+  leaf_load(S, 0, a11, K, NB);
+  {  // A21 [m2 x 128] into S_B (rows past m2 zero)
+    const __amdgpu_buffer_rsrc_t rs = mg_rsrc(a21, (int64_t)(m2 - 1) * K + NB);
+    constexpr int V = NB / 4;
+    const int tid = threadIdx.x;
+    float4 x[NB * V / 256];
+#pragma unroll
+    for (int q = 0; q < NB * V / 256; ++q) {
+      const int idx = tid + 256 * q, i = idx / V, j = 4 * (idx % V);
+      const uint32_t off = i < m2 ? (uint32_t)(((int64_t)i * K + j) * 4) : MG_OOB;
+      x[q] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rs, (int)off, 0, 0));
+    }
+#pragma unroll
+    for (int q = 0; q < NB * V / 256; ++q) {
+      const int idx = tid + 256 * q, i = idx / V, j = 4 * (idx % V);
+      *reinterpret_cast<float4*>(&S[(NB + i) * LP + j]) = x[q];
+    }
+  }
+  __syncthreads();
+  bool bad1 = leaf_rec<NB>(S, 0);
+  leaf_store(S, 0, a11, K, NB);
+  leaf_prod<NB, true, false>(S, NB, 0, 0, 0, NB, 0, 1.0f);   // T1 = A21 A11^T
+  leaf_prod<NB, false, false>(S, NB, 0, 0, 0, 0, 0, 1.0f);   // T2 = T1 A11 (over S_A)
+  {  // S_B = A22 - T1 T1^T: lower triangle, zeros above, identity beyond m2
+    ProdAcc<NB> Q;
+    leaf_mma<NB, true>(S, NB, 0, NB, 0, Q);
+    const __amdgpu_buffer_rsrc_t rs = mg_rsrc(a22, (int64_t)(m2 - 1) * K + m2);
+    float g[ProdAcc<NB>::PER][4];
+#pragma unroll
+    for (int p = 0; p < ProdAcc<NB>::PER; ++p)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int r = prod_row<NB>(p, j), c = prod_col<NB>(p);
+        const uint32_t off = (r < m2 && c <= r) ? (uint32_t)(((int64_t)r * K + c) * 4) : MG_OOB;
+        g[p][j] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, (int)off, 0, 0));
+      }
+    __syncthreads();  // T1 has been read
+#pragma unroll
+    for (int p = 0; p < ProdAcc<NB>::PER; ++p)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int r = prod_row<NB>(p, j), c = prod_col<NB>(p);
+        const float x = Q.acc[p][j];
+        const float v = (r < m2 && c < m2) ? (c <= r ? g[p][j] - x : 0.0f) : (r == c ? 1.0f : 0.0f);
+        S[(NB + r) * LP + c] = v;
+      }
+    __syncthreads();
+  }
+  bool bad2 = leaf_rec<NB>(S + NB * LP, 0);
+  if (threadIdx.x == 0 && (bad1 || bad2)) atomicMin(status, (int)(r0 + (bad1 ? 1 : NB + 1)));
+  leaf_store(S, NB, a22, K, m2);
+  {  // A21 = -S_B T2 (rows < m2)
+    ProdAcc<NB> Q;
+    leaf_mma<NB, false>(S, NB, 0, 0, 0, Q);
+    const __amdgpu_buffer_rsrc_t rs = mg_rsrc(a21, (int64_t)(m2 - 1) * K + NB);
+#pragma unroll
+    for (int p = 0; p < ProdAcc<NB>::PER; ++p)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int r = prod_row<NB>(p, j), c = prod_col<NB>(p);
+        const uint32_t off = r < m2 ? (uint32_t)(((int64_t)r * K + c) * 4) : MG_OOB;
+        const float x = Q.acc[p][j];
+        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(-x), rs, (int)off, 0, 0);
+      }
   }
 }
 
@@ -456,6 +580,12 @@ int inv_chol(const Ctx& c, int64_t r0, int64_t m, int depth) {
     LaunchTimer timer(HI2X_TIME_CHOL_LEAF, 2.0 * m * m * m / 3.0, c.s);
     hipLaunchKernelGGL(leaf_kernel, dim3(1), dim3(256), 0, c.s, c.P, K, r0, (int)m, c.status);
     return launch_status("leaf_kernel");
+  }
+  if (m <= 2 * NB) {  // the node's split is 128 + (m - 128): one fused kernel
+    LaunchTimer timer(HI2X_TIME_CHOL_LEAF, 2.0 * m * m * m / 3.0, c.s);
+    hipLaunchKernelGGL(node_kernel, dim3(1), dim3(256), 0, c.s, c.P, K, r0, (int)(m - NB),
+                       c.status);
+    return launch_status("node_kernel");
   }
   const int64_t nbk = (m + NB - 1) / NB;
   const int64_t m1 = ((nbk + 1) / 2) * NB, m2 = m - m1;
