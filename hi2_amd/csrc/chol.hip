@@ -57,10 +57,11 @@ constexpr int tri_order() {
   return AMODE == 1 ? 1 : (BMODE == 2 ? 2 : (BMODE == 1 ? 3 : 0));
 }
 
-template <int AMODE, int BMODE, bool TB, bool CLOW>
+template <int AMODE, int BMODE, bool TB, bool CLOW, int T>
 __global__ __launch_bounds__(256) void tri_gemm_kernel(GemmArgs g, int64_t tm, int64_t tn,
                                                        int super) {
-  __shared__ MgSmem sm;
+  constexpr int NA = T / 64;
+  __shared__ MgSmemT<T> sm;
   int64_t tr, tc;
   if (super) {
     if (!mg_super_tile<tri_order<AMODE, BMODE>(), CLOW>(blockIdx.x, tm, tn, tr, tc)) return;
@@ -70,48 +71,50 @@ __global__ __launch_bounds__(256) void tri_gemm_kernel(GemmArgs g, int64_t tm, i
     tr = t / tn;
     tc = t % tn;
   }
-  const int64_t r0 = tr * MG_T, c0 = tc * MG_T;
-  if (CLOW && c0 > r0 + MG_T - 1) return;
+  const int64_t r0 = tr * T, c0 = tc * T;
+  if (CLOW && c0 > r0 + T - 1) return;
   int64_t kbeg = 0, kend = g.Kd;
-  if (AMODE == 1) kend = (r0 + MG_T < kend) ? r0 + MG_T : kend;
+  if (AMODE == 1) kend = (r0 + T < kend) ? r0 + T : kend;
   if (BMODE == 1) kbeg = c0;
-  if (BMODE == 2) kend = (c0 + MG_T < kend) ? c0 + MG_T : kend;
-  f32x16 acc[2][2];
-  mg_zero(acc);
+  if (BMODE == 2) kend = (c0 + T < kend) ? c0 + T : kend;
+  f32x16 acc[NA][NA];
+  mg_zero<NA>(acc);
   using AMask = typename std::conditional<AMODE == 1, MaskLower, NoMask>::type;
-  RowsLoader<AMask> al{g.A, g.lda, g.M, kend, AMask{}};
+  RowsLoader<AMask, T> al{g.A, g.lda, g.M, kend, AMask{}};
   if (TB) {
     // op(B)[k][j] = B[j][k]: lower op(B) keeps k >= j, upper keeps k <= j
     using BMask = typename std::conditional<
         BMODE == 1, MaskUpper, typename std::conditional<BMODE == 2, MaskLower, NoMask>::type>::type;
-    RowsLoader<BMask> bl{g.B, g.ldb, g.N, kend, BMask{}};
-    mg_mainloop(acc, sm, al, bl, r0, c0, kbeg, kend);
+    RowsLoader<BMask, T> bl{g.B, g.ldb, g.N, kend, BMask{}};
+    mg_mainloop<NA, T>(acc, sm, al, bl, r0, c0, kbeg, kend);
   } else {
     // op(B)[k][c] = B[k][c]: lower keeps c <= k (mask(k, c)), upper keeps c >= k
     using BMask = typename std::conditional<
         BMODE == 1, MaskLower, typename std::conditional<BMODE == 2, MaskUpper, NoMask>::type>::type;
-    ColsLoader<BMask> bl{g.B, g.ldb, g.N, kend, BMask{}};
-    mg_mainloop(acc, sm, al, bl, r0, c0, kbeg, kend);
+    ColsLoader<BMask, T> bl{g.B, g.ldb, g.N, kend, BMask{}};
+    mg_mainloop<NA, T>(acc, sm, al, bl, r0, c0, kbeg, kend);
   }
-  const CTile ct(g.C, g.ldc, g.M, g.N, r0, c0);
-  f32x16 cv[2][2];
+  const CTile<T> ct(g.C, g.ldc, g.M, g.N, r0, c0);
+  f32x16 cv[NA][NA];
   if (g.beta != 0.0f) {
     ct.load(cv);
 #pragma unroll
-    for (int a = 0; a < 2; ++a)
+    for (int a = 0; a < NA; ++a)
 #pragma unroll
-      for (int b = 0; b < 2; ++b)
+      for (int b = 0; b < NA; ++b)
 #pragma unroll
         for (int j = 0; j < 16; ++j) cv[a][b][j] = cv[a][b][j] + g.alpha * acc[a][b][j];
   } else {
 #pragma unroll
-    for (int a = 0; a < 2; ++a)
+    for (int a = 0; a < NA; ++a)
 #pragma unroll
-      for (int b = 0; b < 2; ++b)
+      for (int b = 0; b < NA; ++b)
 #pragma unroll
         for (int j = 0; j < 16; ++j) cv[a][b][j] = g.alpha * acc[a][b][j];
   }
-  ct.store(cv, [&](int a, int j, int b) { return !CLOW || c0 + mg_col(b) <= r0 + mg_row(a, j); });
+  ct.store(cv, [&](int a, int j, int b) {
+    return !CLOW || c0 + mg_col<T>(b) <= r0 + mg_row<T>(a, j);
+  });
 }
 
 template <int AMODE, int BMODE, bool TB, bool CLOW>
@@ -119,13 +122,21 @@ int tri_gemm(const GemmArgs& a, hipStream_t s) {
   if (a.M <= 0 || a.N <= 0) return HI2X_OK;
   const int64_t tm = (a.M + MG_T - 1) / MG_T, tn = (a.N + MG_T - 1) / MG_T;
   const int64_t ntiles = tm * tn;
+  // every product here has one triangular operand or output: M*N*rank useful flops
+  LaunchTimer timer(HI2X_TIME_CHOL_GEMM, (double)a.M * a.N * a.Kd, s);
+  if ((CLOW ? ntiles / 2 : ntiles) < 128) {
+    // a small grid: 64-tiles, four times the workgroups for a quarter of the work each
+    const int64_t tm6 = (a.M + 63) / 64, tn6 = (a.N + 63) / 64;
+    const int64_t grid = (tm6 * tn6 + 7) / 8 * 8;
+    hipLaunchKernelGGL((tri_gemm_kernel<AMODE, BMODE, TB, CLOW, 64>), dim3((unsigned)grid),
+                       dim3(256), 0, s, a, tm6, tn6, 0);
+    return launch_status("tri_gemm_kernel");
+  }
   // big grids (several rounds of the 512 workgroup slots): super-tile schedule
   const int super = (CLOW ? ntiles / 2 : ntiles) >= 256 ? 1 : 0;
   const int64_t grid = super ? mg_super_grid(tm, tn, CLOW) : (ntiles + 7) / 8 * 8;
-  // every product here has one triangular operand or output: M*N*rank useful flops
-  LaunchTimer timer(HI2X_TIME_CHOL_GEMM, (double)a.M * a.N * a.Kd, s);
-  hipLaunchKernelGGL((tri_gemm_kernel<AMODE, BMODE, TB, CLOW>), dim3((unsigned)grid), dim3(256),
-                     0, s, a, tm, tn, super);
+  hipLaunchKernelGGL((tri_gemm_kernel<AMODE, BMODE, TB, CLOW, MG_T>), dim3((unsigned)grid),
+                     dim3(256), 0, s, a, tm, tn, super);
   return launch_status("tri_gemm_kernel");
 }
 

@@ -234,7 +234,7 @@ __global__ __launch_bounds__(256, 2) void gptq_trailing_kernel(
   const int tid = threadIdx.x;
   const int64_t my_row = r0 + (tid >> 1);  // row this thread stages for the A operand
   const int my_grp = my_row < N ? row_grp[my_row] : -1;
-  const CTile ct(wc, K, N, c1, r0, cc0);
+  const CTile<> ct(wc, K, N, c1, r0, cc0);
 
   for (int g = g0; g <= g1; ++g) {
     const float* U = reinterpret_cast<const float*>(u_ptrs[g]);

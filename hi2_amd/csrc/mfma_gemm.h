@@ -3,7 +3,8 @@
 //
 // A workgroup of 256 threads computes a 128 x 128 tile of A * op(B) as 2 x 2 waves of
 // 64 x 64, each wave holding 2 x 2 accumulators of v_mfma_f32_32x32x2_f32 (16 VGPRs
-// each).  The rank is streamed in chunks of 32 through double-buffered LDS: while the
+// each); a 64 x 64 variant (one accumulator per wave) serves grids too small for the
+// chip.  The rank is streamed in chunks of 32 through double-buffered LDS: while the
 // MFMAs consume one chunk, the next is already in flight from global memory into
 // registers.  Accumulation runs from zero in k order, and each MFMA step evaluates
 // fma(a1, b1, fma(a0, b0, acc)), so every element of the product is the sequential
@@ -26,10 +27,14 @@ constexpr int MG_RP = MG_KC + 4;   // LDS pitch of one tile row (floats)
 
 // A chunk in LDS: row m of the tile holds [k parity][k pair] = 2 x 16 floats, so the
 // lane that feeds MFMA row m with parity h reads all 16 of its k-pairs as 4 x b128.
-struct MgSmem {
-  float A[2][MG_T][MG_RP];
-  float B[2][MG_T][MG_RP];
+// T is the workgroup tile edge: 128 (2 x 2 accumulators per wave) or 64 (one per wave,
+// for grids too small to fill the chip with 128-tiles).
+template <int T = MG_T>
+struct MgSmemT {
+  float A[2][T][MG_RP];
+  float B[2][T][MG_RP];
 };
+using MgSmem = MgSmemT<MG_T>;
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
@@ -56,96 +61,111 @@ struct NoMask {
 
 // Row-major operand X[r][k] (k contiguous), read as "rows" of the tile: the A operand,
 // or the B operand of a transposed product (op(B) = X^T).  Rows >= nrows and k >= kend
-// read as zero.  Thread t stages row t/2, 16 consecutive k starting at 16*(t%2).
-template <class Mask>
+// read as zero.  TPR threads stage one tile row, KPT consecutive k each.
+template <class Mask, int T = MG_T>
 struct RowsLoader {
+  static constexpr int TPR = 256 / T, KPT = MG_KC / TPR, NV = KPT / 4;
   const float* p;
   int64_t ld, nrows, kend;
   Mask mask;
-  __device__ __forceinline__ void load(int64_t r0, int64_t k0, int tid, f32x4 (&st)[4]) const {
-    const int64_t rows = (nrows - r0 < MG_T) ? nrows - r0 : MG_T;
+  __device__ __forceinline__ void load(int64_t r0, int64_t k0, int tid, f32x4 (&st)[NV]) const {
+    const int64_t rows = (nrows - r0 < T) ? nrows - r0 : T;
     const int64_t kv = kend - k0;
     // last valid element of the panel: row rows-1, column kend-1
     const __amdgpu_buffer_rsrc_t rs = mg_rsrc(p + r0 * ld + k0, (rows - 1) * ld + kv);
-    const int rr = tid >> 1;
-    uint32_t off = (uint32_t)((rr * ld + 16 * (tid & 1)) * 4);
+    const int rr = tid / TPR;
+    uint32_t off = (uint32_t)((rr * ld + KPT * (tid % TPR)) * 4);
     off = (rr < rows && mask.row(r0 + rr)) ? off : MG_OOB;
 #pragma unroll
-    for (int v = 0; v < 4; ++v) st[v] = mg_load4(rs, off + 16 * v);
+    for (int v = 0; v < NV; ++v) st[v] = mg_load4(rs, off + 16 * v);
   }
-  // k = 16h + e -> parity e & 1, pair 8h + e / 2.  Elements at k >= kend of rows before
-  // the last are real memory of the next columns: zeroed here.
+  // k = KPT h + e -> parity e & 1, pair (KPT/2) h + e / 2.  Elements at k >= kend of rows
+  // before the last are real memory of the next columns: zeroed here.
   __device__ __forceinline__ void store(float (*S)[MG_RP], int64_t r0, int64_t k0, int tid,
-                                        f32x4 (&st)[4]) const {
-    const int m = tid >> 1, h = tid & 1;
-    const int64_t kb = k0 + 16 * h;
+                                        f32x4 (&st)[NV]) const {
+    const int m = tid / TPR, h = tid % TPR;
+    const int64_t kb = k0 + KPT * h;
     if (Mask::kElem || k0 + MG_KC > kend) {
 #pragma unroll
-      for (int e = 0; e < 16; ++e) {
+      for (int e = 0; e < KPT; ++e) {
         const bool keep = kb + e < kend && mask.elem(r0 + m, kb + e);
         st[e >> 2][e & 3] = keep ? st[e >> 2][e & 3] : 0.0f;
       }
     }
 #pragma unroll
     for (int par = 0; par < 2; ++par) {
-      float* d = &S[m][par * MG_KP + 8 * h];
-      *reinterpret_cast<float4*>(d) =
-          make_float4(st[0][par], st[0][par + 2], st[1][par], st[1][par + 2]);
-      *reinterpret_cast<float4*>(d + 4) =
-          make_float4(st[2][par], st[2][par + 2], st[3][par], st[3][par + 2]);
+      float* d = &S[m][par * MG_KP + (KPT / 2) * h];
+#pragma unroll
+      for (int g = 0; g < KPT / 8; ++g) {
+        // elements e = par + 2 (4g + i), i < 4
+        *reinterpret_cast<float4*>(d + 4 * g) =
+            make_float4(st[(par + 8 * g) >> 2][(par + 8 * g) & 3],
+                        st[(par + 8 * g + 2) >> 2][(par + 8 * g + 2) & 3],
+                        st[(par + 8 * g + 4) >> 2][(par + 8 * g + 4) & 3],
+                        st[(par + 8 * g + 6) >> 2][(par + 8 * g + 6) & 3]);
+      }
     }
   }
 };
 
 // Row-major operand X[k][c] (c contiguous) read as the B operand of a plain product.
 // k >= kend reads as zero; columns >= ncols feed only output columns that are never
-// stored.  Thread t stages k = t%32 and 16 consecutive columns starting at 16*(t/32).
-template <class Mask>
+// stored.  Thread t stages k = t%32 and CPT consecutive columns starting at CPT*(t/32).
+template <class Mask, int T = MG_T>
 struct ColsLoader {
+  static constexpr int CPT = T / 8, NV = CPT / 4;
   const float* p;
   int64_t ld, ncols, kend;
   Mask mask;
-  __device__ __forceinline__ void load(int64_t c0, int64_t k0, int tid, f32x4 (&st)[4]) const {
+  __device__ __forceinline__ void load(int64_t c0, int64_t k0, int tid, f32x4 (&st)[NV]) const {
     const int64_t kv = (kend - k0 < MG_KC) ? kend - k0 : MG_KC;
     const __amdgpu_buffer_rsrc_t rs = mg_rsrc(p + k0 * ld + c0, (kv - 1) * ld + (ncols - c0));
-    const uint32_t off = (uint32_t)(((tid & 31) * ld + 16 * (tid >> 5)) * 4);
+    const uint32_t off = (uint32_t)(((tid & 31) * ld + CPT * (tid >> 5)) * 4);
 #pragma unroll
-    for (int v = 0; v < 4; ++v) st[v] = mg_load4(rs, off + 16 * v);
+    for (int v = 0; v < NV; ++v) st[v] = mg_load4(rs, off + 16 * v);
   }
   __device__ __forceinline__ void store(float (*S)[MG_RP], int64_t c0, int64_t k0, int tid,
-                                        f32x4 (&st)[4]) const {
-    const int kk = tid & 31, cb = 16 * (tid >> 5);
+                                        f32x4 (&st)[NV]) const {
+    const int kk = tid & 31, cb = CPT * (tid >> 5);
     if (Mask::kElem) {
 #pragma unroll
-      for (int e = 0; e < 16; ++e)
+      for (int e = 0; e < CPT; ++e)
         st[e >> 2][e & 3] = mask.elem(k0 + kk, c0 + cb + e) ? st[e >> 2][e & 3] : 0.0f;
     }
     const int off = (kk & 1) * MG_KP + (kk >> 1);
 #pragma unroll
-    for (int e = 0; e < 16; ++e) S[cb + e][off] = st[e >> 2][e & 3];
+    for (int e = 0; e < CPT; ++e) S[cb + e][off] = st[e >> 2][e & 3];
   }
 };
 
-__device__ __forceinline__ void mg_zero(f32x16 (&acc)[2][2]) {
+template <int NA>
+__device__ __forceinline__ void mg_zero(f32x16 (&acc)[NA][NA]) {
 #pragma unroll
-  for (int a = 0; a < 2; ++a)
+  for (int a = 0; a < NA; ++a)
 #pragma unroll
-    for (int b = 0; b < 2; ++b)
+    for (int b = 0; b < NA; ++b)
 #pragma unroll
       for (int j = 0; j < 16; ++j) acc[a][b][j] = 0.0f;
 }
 
-// The 64 MFMAs of one LDS chunk (16 k-pairs x 2 x 2 tiles), in k order.  Operands are
+// The MFMAs of one LDS chunk (16 k-pairs x NA x NA tiles), in k order.  Operands are
 // read in 4 groups of 4 k-pairs (one ds_read_b128 per operand and group) with the next
-// group's reads issued before the current group's MFMAs.
-__device__ __forceinline__ void mg_chunk(f32x16 (&acc)[2][2], const float (*A)[MG_RP],
+// group's reads issued before the current group's MFMAs.  The wave owns rows
+// wr*(32 NA) + 32a + ... and columns wcn*(32 NA) + 32b + ... of the workgroup tile.
+template <int NA>
+__device__ __forceinline__ void mg_chunk(f32x16 (&acc)[NA][NA], const float (*A)[MG_RP],
                                          const float (*B)[MG_RP], int wr, int wcn, int par,
                                          int lr) {
-  const float* pa[2] = {&A[wr * 64 + lr][par * MG_KP], &A[wr * 64 + 32 + lr][par * MG_KP]};
-  const float* pb[2] = {&B[wcn * 64 + lr][par * MG_KP], &B[wcn * 64 + 32 + lr][par * MG_KP]};
-  f32x4 av[2][2], bv[2][2];  // [set][tile]
+  const float* pa[NA];
+  const float* pb[NA];
 #pragma unroll
-  for (int t = 0; t < 2; ++t) {
+  for (int t = 0; t < NA; ++t) {
+    pa[t] = &A[wr * 32 * NA + 32 * t + lr][par * MG_KP];
+    pb[t] = &B[wcn * 32 * NA + 32 * t + lr][par * MG_KP];
+  }
+  f32x4 av[2][NA], bv[2][NA];  // [set][tile]
+#pragma unroll
+  for (int t = 0; t < NA; ++t) {
     av[0][t] = *reinterpret_cast<const f32x4*>(pa[t]);
     bv[0][t] = *reinterpret_cast<const f32x4*>(pb[t]);
   }
@@ -154,7 +174,7 @@ __device__ __forceinline__ void mg_chunk(f32x16 (&acc)[2][2], const float (*A)[M
     const int cur = g & 1;
     if (g + 1 < MG_KP / 4) {
 #pragma unroll
-      for (int t = 0; t < 2; ++t) {
+      for (int t = 0; t < NA; ++t) {
         av[cur ^ 1][t] = *reinterpret_cast<const f32x4*>(pa[t] + 4 * (g + 1));
         bv[cur ^ 1][t] = *reinterpret_cast<const f32x4*>(pb[t] + 4 * (g + 1));
       }
@@ -162,27 +182,28 @@ __device__ __forceinline__ void mg_chunk(f32x16 (&acc)[2][2], const float (*A)[M
 #pragma unroll
     for (int q = 0; q < 4; ++q)
 #pragma unroll
-      for (int a = 0; a < 2; ++a)
+      for (int a = 0; a < NA; ++a)
 #pragma unroll
-        for (int b = 0; b < 2; ++b)
+        for (int b = 0; b < NA; ++b)
           acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[cur][a][q], bv[cur][b][q],
                                                           acc[a][b], 0, 0, 0);
   }
 }
 
-// acc += A[r0:r0+128, kbeg:kend] * op(B)[kbeg:kend, c0:c0+128], rank chunks in order.
+// acc += A[r0:r0+T, kbeg:kend] * op(B)[kbeg:kend, c0:c0+T], rank chunks in order.
 // kbeg must be a multiple of 2 (MFMA k-pairs); loaders zero everything beyond kend.
 // Per chunk: the next chunk's global loads are issued first, the chunk's MFMAs run from
 // LDS, and only then are the loaded values masked and written to the other LDS buffer.
-template <class AL, class BL>
-__device__ __forceinline__ void mg_mainloop(f32x16 (&acc)[2][2], MgSmem& sm, const AL& al,
+template <int NA, int T, class AL, class BL>
+__device__ __forceinline__ void mg_mainloop(f32x16 (&acc)[NA][NA], MgSmemT<T>& sm, const AL& al,
                                             const BL& bl, int64_t r0, int64_t c0,
                                             int64_t kbeg, int64_t kend) {
+  static_assert(NA * 64 == T, "accumulators must cover the tile");
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wr = wave >> 1, wcn = wave & 1;
   if (kend <= kbeg) return;
   const int nch = (int)((kend - kbeg + MG_KC - 1) / MG_KC);
-  f32x4 sa[4], sb[4];
+  f32x4 sa[AL::NV], sb[BL::NV];
   al.load(r0, kbeg, tid, sa);
   bl.load(c0, kbeg, tid, sb);
   __syncthreads();  // the previous use of the LDS buffers is over
@@ -198,7 +219,7 @@ __device__ __forceinline__ void mg_mainloop(f32x16 (&acc)[2][2], MgSmem& sm, con
       al.load(r0, kn, tid, sa);
       bl.load(c0, kn, tid, sb);
     }
-    mg_chunk(acc, sm.A[buf], sm.B[buf], wr, wcn, par, lr);
+    mg_chunk<NA>(acc, sm.A[buf], sm.B[buf], wr, wcn, par, lr);
     __builtin_amdgcn_sched_barrier(0);
     if (more) {  // buffer buf ^ 1 was last read before the previous barrier
       al.store(sm.A[buf ^ 1], r0, kn, tid, sa);
@@ -210,25 +231,29 @@ __device__ __forceinline__ void mg_mainloop(f32x16 (&acc)[2][2], MgSmem& sm, con
 
 // Row / column of accumulator register j of tile (a, b) for this lane, relative to the
 // workgroup tile origin.
+template <int T = MG_T>
 __device__ __forceinline__ int mg_row(int a, int j) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  return (wave >> 1) * 64 + a * 32 + 8 * (j >> 2) + 4 * (lane >> 5) + (j & 3);
+  return (wave >> 1) * (T / 2) + a * 32 + 8 * (j >> 2) + 4 * (lane >> 5) + (j & 3);
 }
+template <int T = MG_T>
 __device__ __forceinline__ int mg_col(int b) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  return (wave & 1) * 64 + b * 32 + (lane & 31);
+  return (wave & 1) * (T / 2) + b * 32 + (lane & 31);
 }
 
-// The 128 x 128 tile of a row-major [nrows, ncols] matrix at (r0, c0), accessed in the
+// The T x T tile of a row-major [nrows, ncols] matrix at (r0, c0), accessed in the
 // accumulator layout through a buffer resource that ends at the tile's last valid element:
 // loads are branch-free (rows past the end read zero, columns past the end of rows before
 // the last read real memory that is never stored back), stores drop every element the
 // predicate rejects or that lies outside [nrows, ncols).
 //
 // Offsets are one per-lane base plus a uniform term per register; the base passes
-// through an empty asm so the 64 offsets are rebuilt at each access instead of being
+// through an empty asm so the offsets are rebuilt at each access instead of being
 // hoisted out of the caller's loops and held in registers across them.
+template <int T = MG_T>
 struct CTile {
+  static constexpr int NA = T / 64;
   __amdgpu_buffer_rsrc_t rs;
   int64_t ld;
   uint32_t vbase;  // byte offset of this lane's (row 0, column 0) element
@@ -236,10 +261,10 @@ struct CTile {
   __device__ __forceinline__ CTile(float* p, int64_t ld_, int64_t nrows, int64_t ncols,
                                    int64_t r0, int64_t c0)
       : ld(ld_) {
-    rows = (int)((nrows - r0 < MG_T) ? nrows - r0 : MG_T);
-    cols = (int)((ncols - c0 < MG_T) ? ncols - c0 : MG_T);
+    rows = (int)((nrows - r0 < T) ? nrows - r0 : T);
+    cols = (int)((ncols - c0 < T) ? ncols - c0 : T);
     rs = mg_rsrc(p + r0 * ld + c0, (int64_t)(rows - 1) * ld + cols);
-    vbase = (uint32_t)(((int64_t)mg_row(0, 0) * ld + mg_col(0)) * 4);
+    vbase = (uint32_t)(((int64_t)mg_row<T>(0, 0) * ld + mg_col<T>(0)) * 4);
   }
   // byte offset of register j of tile (a, b) relative to vbase (uniform)
   __device__ __forceinline__ uint32_t uoff(int a, int b, int j) const {
@@ -250,12 +275,12 @@ struct CTile {
     asm volatile("" : "+v"(v));
     return v;
   }
-  __device__ __forceinline__ void load(f32x16 (&v)[2][2]) const {
+  __device__ __forceinline__ void load(f32x16 (&v)[NA][NA]) const {
     const uint32_t vb = base();
 #pragma unroll
-    for (int a = 0; a < 2; ++a)
+    for (int a = 0; a < NA; ++a)
 #pragma unroll
-      for (int b = 0; b < 2; ++b)
+      for (int b = 0; b < NA; ++b)
 #pragma unroll
         for (int j = 0; j < 16; ++j)
           v[a][b][j] = __builtin_bit_cast(
@@ -264,13 +289,13 @@ struct CTile {
   // keep(a, j, b): predicate for register j of tile (a, b) (rows and columns outside the
   // matrix are dropped regardless)
   template <class Keep>
-  __device__ __forceinline__ void store(const f32x16 (&v)[2][2], Keep keep) const {
+  __device__ __forceinline__ void store(const f32x16 (&v)[NA][NA], Keep keep) const {
     const uint32_t vb = base();
 #pragma unroll
-    for (int b = 0; b < 2; ++b) {
-      const bool cok = mg_col(b) < cols;
+    for (int b = 0; b < NA; ++b) {
+      const bool cok = mg_col<T>(b) < cols;
 #pragma unroll
-      for (int a = 0; a < 2; ++a)
+      for (int a = 0; a < NA; ++a)
 #pragma unroll
         for (int j = 0; j < 16; ++j) {
           const uint32_t o = (cok && keep(a, j, b)) ? vb + uoff(a, b, j) : MG_OOB;
