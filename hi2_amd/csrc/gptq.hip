@@ -205,12 +205,15 @@ __global__ __launch_bounds__(RPG * QL) void gptq_block_kernel(
 // Each product is accumulated from zero with v_mfma_f32_32x32x2_f32, which evaluates
 // fma(a1, b1, fma(a0, b0, acc)) in k order: the same sequential fp32 FMA chain as the
 // reference's CPU GEMM, then one subtraction per block.  One launch applies the nblk
-// blocks of a super-block to the far columns (lazy batching: the wc tile stays in L2
-// between them) and every block's product is subtracted separately, in block order, so
-// the result equals the per-block schedule bit for bit.
+// blocks of a super-block to the far columns (lazy batching) and every block's product
+// is subtracted separately, in block order, so the result equals the per-block schedule
+// bit for bit.
 // Workgroup tile 128 x 128 (4 waves as 2 x 2 of 64 x 64), rank streamed in chunks of
-// 16 through LDS.  Rows of another group than the pass's are masked in A and left
-// untouched in the epilogue.
+// 32 through LDS.  When the whole tile belongs to one factor, the wc tile is read once,
+// held in registers while the blocks stream through as one pipelined rank (the next
+// chunk in flight across block boundaries), and written once.  A tile shared by two
+// factors runs one pass per factor: rows of another group are masked in A and left
+// untouched in that pass's epilogue.
 // ---------------------------------------------------------------------------------
 struct GroupMask {  // A rows of the current group pass (this thread's staged row)
   static constexpr bool kElem = false;
@@ -236,6 +239,30 @@ __global__ __launch_bounds__(256, 2) void gptq_trailing_kernel(
   const int my_grp = my_row < N ? row_grp[my_row] : -1;
   const CTile<> ct(wc, K, N, c1, r0, cc0);
 
+  if (g0 == g1) {  // one factor for the whole tile: the blocks as one pipelined rank stream
+    const float* U = reinterpret_cast<const float*>(u_ptrs[g0]);
+    const int64_t R = (K - i1 < (int64_t)nblk * LMAX) ? K - i1 : (int64_t)nblk * LMAX;
+    RowsLoader<GroupMask> al{err1, lde, N, R, GroupMask{my_grp == g0}};
+    ColsLoader<NoMask> bl{U + i1 * K, K, c1, R, NoMask{}};
+    f32x16 acc[2][2], cv[2][2];
+    mg_zero(acc);
+    ct.load(cv);  // the wc tile stays in registers across the blocks
+    mg_mainloop_seg<2, MG_T, LMAX>(
+        acc, sm, al, bl, r0, cc0, 0, R, []() {},
+        [&](f32x16(&a)[2][2]) {
+#pragma unroll
+          for (int x = 0; x < 2; ++x)
+#pragma unroll
+            for (int y = 0; y < 2; ++y)
+#pragma unroll
+              for (int j = 0; j < 16; ++j) {
+                cv[x][y][j] = cv[x][y][j] - a[x][y][j];
+                a[x][y][j] = 0.0f;
+              }
+        });
+    ct.store(cv, [](int, int, int) { return true; });
+    return;
+  }
   for (int g = g0; g <= g1; ++g) {
     const float* U = reinterpret_cast<const float*>(u_ptrs[g]);
     for (int t = 0; t < nblk; ++t) {

@@ -229,6 +229,54 @@ __device__ __forceinline__ void mg_mainloop(f32x16 (&acc)[NA][NA], MgSmemT<T>& s
   }
 }
 
+// The rank [kbeg, kend) as consecutive segments of SEG (a multiple of MG_KC), each
+// accumulated from zero: after the MFMAs of a segment's last chunk, end(acc) consumes the
+// segment's product and must leave acc zero again; pre() runs at the start of that last
+// chunk, before its MFMAs (the place to issue the epilogue's global loads, so that they
+// are in flight while the MFMAs run).  The next chunk's loads are issued before every
+// chunk's MFMAs, across segment boundaries too, so only the first chunk's load latency
+// is exposed.
+template <int NA, int T, int SEG, class AL, class BL, class Pre, class End>
+__device__ __forceinline__ void mg_mainloop_seg(f32x16 (&acc)[NA][NA], MgSmemT<T>& sm,
+                                                const AL& al, const BL& bl, int64_t r0,
+                                                int64_t c0, int64_t kbeg, int64_t kend,
+                                                Pre pre, End end) {
+  static_assert(NA * 64 == T, "accumulators must cover the tile");
+  static_assert(SEG % MG_KC == 0, "segments are whole chunks");
+  constexpr int CPS = SEG / MG_KC;  // chunks per segment
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wr = wave >> 1, wcn = wave & 1;
+  if (kend <= kbeg) return;
+  const int nch = (int)((kend - kbeg + MG_KC - 1) / MG_KC);
+  f32x4 sa[AL::NV], sb[BL::NV];
+  al.load(r0, kbeg, tid, sa);
+  bl.load(c0, kbeg, tid, sb);
+  __syncthreads();  // the previous use of the LDS buffers is over
+  al.store(sm.A[0], r0, kbeg, tid, sa);
+  bl.store(sm.B[0], c0, kbeg, tid, sb);
+  __syncthreads();
+  const int par = lane >> 5, lr = lane & 31;
+  for (int ch = 0; ch < nch; ++ch) {
+    const int buf = ch & 1;
+    const int64_t kn = kbeg + (int64_t)(ch + 1) * MG_KC;
+    const bool more = ch + 1 < nch;
+    const bool seg_last = !more || (ch + 1) % CPS == 0;
+    if (seg_last) pre();
+    if (more) {
+      al.load(r0, kn, tid, sa);
+      bl.load(c0, kn, tid, sb);
+    }
+    mg_chunk<NA>(acc, sm.A[buf], sm.B[buf], wr, wcn, par, lr);
+    __builtin_amdgcn_sched_barrier(0);
+    if (seg_last) end(acc);
+    if (more) {  // buffer buf ^ 1 was last read before the previous barrier
+      al.store(sm.A[buf ^ 1], r0, kn, tid, sa);
+      bl.store(sm.B[buf ^ 1], c0, kn, tid, sb);
+    }
+    __syncthreads();
+  }
+}
+
 // Row / column of accumulator register j of tile (a, b) for this lane, relative to the
 // workgroup tile origin.
 template <int T = MG_T>
