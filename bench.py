@@ -79,6 +79,7 @@ ORDER = ["down", "mlp", "attn", "o"]  # calibration inputs, longest chain first
 # the short chains fill the GPU around the long chain's latency-bound steps)
 LANES = [["down"], ["mlp"], ["attn"], ["o"]]
 _CHAIN_STREAMS = {}
+HEAD_START = os.environ.get("HI2_HEAD_START", "transform")
 
 
 def _chain_stream(dev, i):
@@ -112,18 +113,27 @@ def encode_block(xs, ws, masks, timer=None, lanes=None):
     chains = {}
     for li in range(len(lanes)):
         _chain_stream(dev, li).wait_stream(main)
+    lead = None  # the first chain's head start: the others wait for its Hessian stages
     for inp in order:
         k = INPUTS[inp]
         st = _chain_stream(dev, lane_of[inp])
         mark = (lambda stage, inp=inp: timer.mark(inp, stage)) if timer else (lambda stage: None)
         with torch.cuda.stream(st):
+            if lead is not None and lane_of[inp] != 0:
+                st.wait_event(lead)
             had = torch.ones(k // 16, dtype=torch.uint8, device=dev)
             mark("hessian")
             hst = HessianStats(k, dev)
             hst.update(xs[inp])
+            if HEAD_START == "hessian" and lane_of[inp] == 0 and lead is None:
+                lead = torch.cuda.Event()
+                lead.record(st)
             mark("transform")
-            hs = transform_sigma(hst.mean(), None, had)
+            hs = hst.transformed(None, had)  # == transform_sigma(hst.mean(), None, had)
             d = hs.diagonal().clone()
+            if HEAD_START == "transform" and lane_of[inp] == 0 and lead is None:
+                lead = torch.cuda.Event()
+                lead.record(st)
             mark("factor")
             u, status = inverse_factor_async(hs, DAMP)
             mark("rotate")
@@ -182,7 +192,7 @@ class StageTimer:
 # kernel families timed by the library (hi2x_timing_*), with the peak that bounds each
 KERNELS = {  # kind -> (kernel, bound, peak FLOP/s, work unit)
     0: ("gptq_trailing_kernel", "mfma", PEAK_F32, "2*rows*rank*cols"),
-    1: ("syrk2_bf16_kernel", "mfma", PEAK_BF16, "2*T*K^2"),
+    1: ("syrk2_bf16_kernel", "mfma", PEAK_BF16, "T*K*(K+1) (upper triangle, 2 flops per product)"),
     2: ("tri_gemm_kernel", "mfma", PEAK_F32, "M*N*rank (one triangular operand)"),
     3: ("leaf_kernel", "latency", PEAK_F32, "2*n^3/3"),
     4: ("gptq_block_kernel", "latency", PEAK_F32, "rows*L*(L-1)"),

@@ -41,7 +41,10 @@ SIGNATURES = {
     "hi2x_assemble_piece": [_P, _I64, _P, _P, _P, _I64, _I, _I64, _P, _P, _P, _P, _P, _P, _P],
     "hi2x_hessian_syrk": [_P, _I, _I64, _I64, _P, _P, _I64, _P],
     "hi2x_hessian_syrk_varlen": [_P, _I, _P, _I64, _I64, _P, _P, _I64, _P],
+    "hi2x_hessian_syrk_upper": [_P, _I, _I64, _I64, _P, _P, _I64, _P],
+    "hi2x_hessian_mirror": [_P, _I64, _P],
     "hi2x_sigma_transform": [_P, _P, _P, _I64, _P, _P],
+    "hi2x_sigma_transform_upper": [_P, _I64, _P, _P, _I64, _P, _P],
     "hi2x_chol_inv_upper": [_P, _I64, _F, _I, _P, _P, _I64, _P],
     "hi2x_chol_inv_upper_async": [_P, _I64, _F, _I, _P, _P, _P, _I64, _P],
 }

@@ -227,24 +227,34 @@ __global__ __launch_bounds__(256) void syrk2_bf16_kernel(const uint16_t* __restr
   const int rowsB = (int)((K - b0 < S2T) ? K - b0 : S2T);
   const __amdgpu_buffer_rsrc_t rsa = rsrc_bytes(xt + a0 * T, (int64_t)rowsA * T * 2);
   const __amdgpu_buffer_rsrc_t rsb = rsrc_bytes(xt + b0 * T, (int64_t)rowsB * T * 2);
-  const uint32_t rowoff = (uint32_t)((int64_t)tid * T * 2);
-  const uint32_t offA = tid < rowsA ? rowoff : MG_OOB;
-  const uint32_t offB = (!diag && tid < rowsB) ? rowoff : MG_OOB;
-  constexpr int NQ = S2C / 8;  // 16-byte vectors per feature row and stage
+  // A stage of a panel is 256 feature rows x 128 bytes: 8 consecutive threads read one
+  // row's 128 contiguous bytes (one cache line per 8 lanes), thread tid covers piece
+  // tid % 8 of rows tid / 8 + 32 i.
+  constexpr int NQ = S2C / 8;            // 16-byte pieces per feature row and stage
+  constexpr int RSTEP = 256 / NQ;        // rows between a thread's pieces
+  const int pq = tid % NQ, pr = tid / NQ;
+  const uint32_t rowoff = (uint32_t)((int64_t)pr * T * 2 + 16 * pq);
+  const uint32_t rstep = (uint32_t)((int64_t)RSTEP * T * 2);
   uint4 ra[NQ], rb[NQ];
   auto load = [&](int64_t t0) {
-    const uint32_t tb8 = (uint32_t)(t0 * 2);
+    uint32_t b = rowoff + (uint32_t)(t0 * 2);
+    asm volatile("" : "+v"(b));  // rebuilt per stage, not held across the loop
 #pragma unroll
-    for (int q = 0; q < NQ; ++q) {
-      ra[q] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rsa, (int)(offA + tb8 + 16 * q), 0, 0));
-      rb[q] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rsb, (int)(offB + tb8 + 16 * q), 0, 0));
+    for (int i = 0; i < NQ; ++i) {
+      const int row = pr + RSTEP * i;
+      const uint32_t o = b + rstep * i;
+      ra[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(
+                                            rsa, (int)(row < rowsA ? o : MG_OOB), 0, 0));
+      rb[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(
+                                            rsb, (int)((!diag && row < rowsB) ? o : MG_OOB), 0, 0));
     }
   };
   auto store = [&](int buf) {
 #pragma unroll
-    for (int q = 0; q < NQ; ++q) {
-      *reinterpret_cast<uint4*>(&Xa[buf][tid * S2P + 8 * q]) = ra[q];
-      if (!diag) *reinterpret_cast<uint4*>(&Xb[buf][tid * S2P + 8 * q]) = rb[q];
+    for (int i = 0; i < NQ; ++i) {
+      const int row = pr + RSTEP * i;
+      *reinterpret_cast<uint4*>(&Xa[buf][row * S2P + 8 * pq]) = ra[i];
+      if (!diag) *reinterpret_cast<uint4*>(&Xb[buf][row * S2P + 8 * pq]) = rb[i];
     }
   };
   const int nst = (int)((tend - tbeg + S2C - 1) / S2C);
@@ -257,24 +267,30 @@ __global__ __launch_bounds__(256) void syrk2_bf16_kernel(const uint16_t* __restr
     const int buf = st & 1;
     const bool more = st + 1 < nst;
     if (more) load(tbeg + (int64_t)(st + 1) * S2C);
-    const uint16_t* XA = Xa[buf];
-    const uint16_t* XB = diag ? Xa[buf] : Xb[buf];
+    const uint16_t* XA = Xa[buf] + (wr * 128 + (lane & 31)) * S2P + 8 * (lane >> 5);
+    const uint16_t* XB = (diag ? Xa[buf] : Xb[buf]) + (wcn * 128 + (lane & 31)) * S2P + 8 * (lane >> 5);
+    // operands of k-step ks + 16 are read while the MFMAs of ks run (one wave per SIMD:
+    // nothing else hides the LDS latency)
+    bf16x8 av[2][4], bv[2][4];
+    auto read = [&](int set, int ks) {
 #pragma unroll
-    for (int ks = 0; ks < S2C; ks += 16) {
-      const int ko = ks + 8 * (lane >> 5);
-      bf16x8 bv[4];
+      for (int t = 0; t < 4; ++t) {
+        av[set][t] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u16x8*>(&XA[t * 32 * S2P + ks]));
+        bv[set][t] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u16x8*>(&XB[t * 32 * S2P + ks]));
+      }
+    };
+    read(0, 0);
 #pragma unroll
-      for (int b = 0; b < 4; ++b)
-        bv[b] = __builtin_bit_cast(
-            bf16x8, *reinterpret_cast<const u16x8*>(&XB[(wcn * 128 + b * 32 + (lane & 31)) * S2P + ko]));
+    for (int kk = 0; kk < S2C / 16; ++kk) {
+      const int cur = kk & 1;
+      if (kk + 1 < S2C / 16) read(cur ^ 1, 16 * (kk + 1));
+      __builtin_amdgcn_sched_barrier(0);  // keep the reads ahead of this step's MFMAs
 #pragma unroll
-      for (int a = 0; a < 4; ++a) {
-        const bf16x8 av = __builtin_bit_cast(
-            bf16x8, *reinterpret_cast<const u16x8*>(&XA[(wr * 128 + a * 32 + (lane & 31)) * S2P + ko]));
+      for (int a = 0; a < 4; ++a)
 #pragma unroll
         for (int b = 0; b < 4; ++b)
-          acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, bv[b], acc[a][b], 0, 0, 0);
-      }
+          acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av[cur][a], bv[cur][b], acc[a][b], 0, 0, 0);
+      __builtin_amdgcn_sched_barrier(0);
     }
     __builtin_amdgcn_sched_barrier(0);
     if (more) store(buf ^ 1);  // buffer buf ^ 1 was last read before the barrier
@@ -327,21 +343,47 @@ __global__ __launch_bounds__(256) void split_sum_kernel(float* __restrict__ s,
   s[idx] = v;
 }
 
-// S[j][i] = S[i][j] for i < j (32 x 32 tile pairs through LDS).
-__global__ __launch_bounds__(256) void mirror_kernel(float* __restrict__ s, int64_t K, int nT) {
-  __shared__ float A[32][33];
-  int ti, tj;
-  upper_tile(nT, blockIdx.x, ti, tj);
-  const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;
-  const int64_t i0 = (int64_t)ti * 32, j0 = (int64_t)tj * 32;
-  for (int y = ty; y < 32; y += 8) {
-    const int64_t r = i0 + y, c = j0 + tx;
-    A[y][tx] = (r < K && c < K) ? s[r * K + c] : 0.0f;
+// Element access to the 64 x 64 tile at (r0, c0) of a row-major [K, K] matrix through a
+// buffer resource that ends at the tile's last valid element: loads and stores need no
+// branch (a branch around a load makes the compiler wait for it on the spot); elements
+// outside the matrix read zero and are not written.
+struct TileIO {
+  __amdgpu_buffer_rsrc_t rs;
+  int64_t ld;
+  int rows, cols;
+  __device__ __forceinline__ TileIO(const float* p, int64_t K, int64_t r0, int64_t c0) : ld(K) {
+    rows = (int)((K - r0 < 64) ? K - r0 : 64);
+    cols = (int)((K - c0 < 64) ? K - c0 : 64);
+    rs = mg_rsrc(p + r0 * K + c0, (int64_t)(rows - 1) * K + cols);
   }
+  __device__ __forceinline__ uint32_t off(int y, int x, bool keep) const {
+    return (keep && y < rows && x < cols) ? (uint32_t)(((int64_t)y * ld + x) * 4) : MG_OOB;
+  }
+  __device__ __forceinline__ float load(int y, int x) const {
+    return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, (int)off(y, x, true), 0, 0));
+  }
+  __device__ __forceinline__ void store(int y, int x, float v, bool keep = true) const {
+    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), rs, (int)off(y, x, keep), 0, 0);
+  }
+};
+
+// S[j][i] = S[i][j] for i < j: 64 x 64 tile pairs (ti <= tj) through LDS, rows of 256
+// bytes on both sides; grid (tj, ti), the workgroups below the diagonal exit at once.
+constexpr int MT = 64, MTP = MT + 1;
+__global__ __launch_bounds__(256) void mirror_kernel(float* __restrict__ s, int64_t K) {
+  __shared__ float A[MT][MTP];
+  const int ti = blockIdx.y, tj = blockIdx.x;
+  if (ti > tj) return;
+  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+  const int64_t i0 = (int64_t)ti * MT, j0 = (int64_t)tj * MT;
+  const TileIO up(s, K, i0, j0), lo(s, K, j0, i0);
+#pragma unroll
+  for (int q = 0; q < MT / 4; ++q) A[ty + 4 * q][tx] = up.load(ty + 4 * q, tx);
   __syncthreads();
-  for (int y = ty; y < 32; y += 8) {
-    const int64_t r = j0 + y, c = i0 + tx;  // lower element (r, c) = upper (c, r)
-    if (r < K && c < K && r > c) s[r * K + c] = A[tx][y];
+#pragma unroll
+  for (int q = 0; q < MT / 4; ++q) {
+    const int y = ty + 4 * q;  // lower element (j0 + y, i0 + tx) = upper (i0 + tx, j0 + y)
+    lo.store(y, tx, A[tx][y], j0 + y > i0 + tx);
   }
 }
 
@@ -493,6 +535,123 @@ __global__ __launch_bounds__(256) void st_sym_kernel(int64_t K, int nT, float* _
   }
 }
 
+// transform_sigma of the mean S / n straight from the upper triangle of the running sum
+// S, in one pass: each workgroup takes the 64 x 64 tile pair (I, J), I <= J, reads only
+// S's upper tile (I, J) (a diagonal tile's lower half from its upper half), and evaluates
+// the same fp32 ops in the same order as the unfused path:
+//   x = S / n (IEEE division), then (x * inv_r) * inv_c with the block's own (r, c),
+//   the left group products, the right group products (sequential FMA chains from zero;
+//   x + 0 on unflagged groups), and out[r][c] = out[c][r] = 0.5 * (t[r][c] + t[c][r]).
+// Block (J, I) is built from the transposed values with its own (r, c) order of the
+// column scaling, so both blocks are exactly what the full-matrix passes would compute.
+constexpr int FT = 64, FTP = FT + 1;
+
+__device__ __forceinline__ void group_left(float (*B)[FTP], int col, int lg, bool flag) {
+  float x[16];
+#pragma unroll
+  for (int j = 0; j < 16; ++j) x[j] = B[16 * lg + j][col];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    float a;
+    if (flag) {
+      a = 0.0f;
+#pragma unroll
+      for (int j = 0; j < 16; ++j) a = __builtin_fmaf(hsgn(i, j), x[j], a);
+    } else {
+      a = x[i] + 0.0f;
+    }
+    B[16 * lg + i][col] = a;
+  }
+}
+
+__device__ __forceinline__ void group_right(float (*B)[FTP], int row, int h, bool flag) {
+  float x[16];
+#pragma unroll
+  for (int k = 0; k < 16; ++k) x[k] = B[row][16 * h + k];
+#pragma unroll
+  for (int l = 0; l < 16; ++l) {
+    float a;
+    if (flag) {
+      a = 0.0f;
+#pragma unroll
+      for (int k = 0; k < 16; ++k) a = __builtin_fmaf(x[k], hsgn(l, k), a);
+    } else {
+      a = x[l] + 0.0f;
+    }
+    B[row][16 * h + l] = a;
+  }
+}
+
+__global__ __launch_bounds__(256) void st_upper_kernel(const float* __restrict__ s, float nf,
+                                                       const uint16_t* __restrict__ col_scale,
+                                                       const uint8_t* __restrict__ had,
+                                                       int64_t K, float* __restrict__ out) {
+  __shared__ float X[FT][FTP], Y[FT][FTP];
+  const int ti = blockIdx.y, tj = blockIdx.x;
+  if (ti > tj) return;
+  const bool diag = ti == tj;
+  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+  const int64_t R0 = (int64_t)ti * FT, C0 = (int64_t)tj * FT;
+  const int64_t G = K / 16;
+  // raw upper tile
+  const TileIO in(s, K, R0, C0);
+#pragma unroll
+  for (int q = 0; q < FT / 4; ++q) X[ty + 4 * q][tx] = in.load(ty + 4 * q, tx);
+  __syncthreads();
+  float v[FT / 4];
+#pragma unroll
+  for (int q = 0; q < FT / 4; ++q) {
+    const int y = ty + 4 * q;
+    v[q] = (diag && y > tx) ? X[tx][y] : X[y][tx];
+  }
+  __syncthreads();
+  // X block (rows R0.., cols C0..) and the transposed Y block (rows C0.., cols R0..)
+  const float ic = (col_scale && C0 + tx < K) ? 1.0f / f16_from_bits(col_scale[C0 + tx]) : 1.0f;
+#pragma unroll
+  for (int q = 0; q < FT / 4; ++q) {
+    const int y = ty + 4 * q;
+    const float m = v[q] / nf;
+    float xv = m, yv = m;
+    if (col_scale) {
+      const float ir = R0 + y < K ? 1.0f / f16_from_bits(col_scale[R0 + y]) : 1.0f;
+      xv = (m * ir) * ic;
+      yv = (m * ic) * ir;
+    }
+    X[y][tx] = xv;
+    Y[tx][y] = yv;
+  }
+  __syncthreads();
+  // left products: X over the row groups of I, Y over those of J
+  {
+    const int lg = ty;  // 4 groups of 16 rows, column tx
+    const int64_t gx = R0 / 16 + lg, gy = C0 / 16 + lg;
+    group_left(X, tx, lg, gx < G && had[gx]);
+    group_left(Y, tx, lg, gy < G && had[gy]);
+  }
+  __syncthreads();
+  // right products: X over the column groups of J, Y over those of I
+  {
+    const int h = ty;  // row tx, 4 groups of 16 columns
+    const int64_t gx = C0 / 16 + h, gy = R0 / 16 + h;
+    group_right(X, tx, h, gx < G && had[gx]);
+    group_right(Y, tx, h, gy < G && had[gy]);
+  }
+  __syncthreads();
+  const TileIO o1(out, K, R0, C0), o2(out, K, C0, R0);
+#pragma unroll
+  for (int q = 0; q < FT / 4; ++q) {
+    const int y = ty + 4 * q;
+    o1.store(y, tx, 0.5f * (X[y][tx] + Y[tx][y]));
+  }
+  if (!diag) {
+#pragma unroll
+    for (int q = 0; q < FT / 4; ++q) {
+      const int y = ty + 4 * q;
+      o2.store(y, tx, 0.5f * (Y[y][tx] + X[tx][y]));
+    }
+  }
+}
+
 // Work split of the bf16 SYRK and the workspace it needs: the transposed X (tokens
 // padded to 64) and, when the 256-tiles are fewer than the CUs, one partial [k, k] per
 // token split.
@@ -520,13 +679,21 @@ SyrkPlan syrk_plan(int dtype, int64_t t, int64_t k) {
   return p;
 }
 
-// ws: device workspace of at least syrk_plan(...).total() bytes, 256-byte aligned
+int launch_mirror(float* s, int64_t k, hipStream_t st) {
+  const unsigned nM = (unsigned)((k + MT - 1) / MT);
+  hipLaunchKernelGGL(mirror_kernel, dim3(nM, nM), dim3(256), 0, st, s, k);
+  return launch_status("mirror_kernel");
+}
+
+// ws: device workspace of at least syrk_plan(...).total() bytes, 256-byte aligned.
+// mirror = false leaves the lower triangle of a bf16 accumulation stale (the f32 path
+// always writes both triangles).
 int launch_syrk(const void* x, int dtype, int64_t t, int64_t k, float* s, char* ws,
-                hipStream_t st) {
+                hipStream_t st, bool mirror = true) {
   if (dtype != 2) {
     const int nT = (int)((k + HT - 1) / HT);
     const int64_t tiles = (int64_t)nT * (nT + 1) / 2;
-    LaunchTimer timer(HI2X_TIME_HESSIAN_SYRK, 2.0 * t * k * k, st);
+    LaunchTimer timer(HI2X_TIME_HESSIAN_SYRK, (double)t * k * (k + 1), st);  // upper triangle
     hipLaunchKernelGGL(syrk_f32_kernel, dim3((unsigned)tiles), dim3(256), 0, st,
                        (const float*)x, t, k, nT, s);
     return launch_status("syrk_f32_kernel");
@@ -543,7 +710,7 @@ int launch_syrk(const void* x, int dtype, int64_t t, int64_t k, float* s, char* 
     const int super = (p.splits == 1 && p.ntiles >= 512) ? 1 : 0;
     const int64_t grid = super ? (syrk_super_count(p.nT) + 7) / 8 * 8 * S2R * S2S
                                : (p.ntiles + 7) / 8 * 8 * p.splits;
-    LaunchTimer timer(HI2X_TIME_HESSIAN_SYRK, 2.0 * t * k * k, st);
+    LaunchTimer timer(HI2X_TIME_HESSIAN_SYRK, (double)t * k * (k + 1), st);  // upper triangle
     hipLaunchKernelGGL(syrk2_bf16_kernel, dim3((unsigned)grid), dim3(256), 0, st, xt, p.tp, k,
                        p.nT, p.ntiles, p.splits, p.tchunk, parts ? parts : s, k * k, super);
     rc = launch_status("syrk2_bf16_kernel");
@@ -553,12 +720,7 @@ int launch_syrk(const void* x, int dtype, int64_t t, int64_t k, float* s, char* 
                        s, parts, p.splits, k);
     rc = launch_status("split_sum_kernel");
   }
-  if (!rc) {
-    const int nM = (int)((k + 31) / 32);
-    hipLaunchKernelGGL(mirror_kernel, dim3((unsigned)((int64_t)nM * (nM + 1) / 2)), dim3(256), 0,
-                       st, s, k, nM);
-    rc = launch_status("mirror_kernel");
-  }
+  if (!rc && mirror) rc = launch_mirror(s, k, st);
   return rc;
 }
 
@@ -584,6 +746,27 @@ extern "C" int hi2x_hessian_syrk(const void* x, int dtype, int64_t t, int64_t k,
                                 "hessian_syrk");
   if (rc) return rc;
   return launch_syrk(x, dtype, t, k, s, w.p, st);
+}
+
+extern "C" int hi2x_hessian_syrk_upper(const void* x, int dtype, int64_t t, int64_t k,
+                                       float* s, void* ws, int64_t ws_bytes, void* stream) {
+  clear_error();
+  HI2X_REQUIRE(dtype == 0 || dtype == 2, "hessian_syrk_upper: dtype %d (0 = f32, 2 = bf16)",
+               dtype);
+  HI2X_REQUIRE(k > 0 && t >= 0, "hessian_syrk_upper: bad shape");
+  if (t == 0) return HI2X_OK;
+  hipStream_t st = as_stream(stream);
+  Workspace w;
+  const int rc = take_workspace(w, ws, ws_bytes, syrk_plan(dtype, t, k).total(), st,
+                                "hessian_syrk_upper");
+  if (rc) return rc;
+  return launch_syrk(x, dtype, t, k, s, w.p, st, false);
+}
+
+extern "C" int hi2x_hessian_mirror(float* s, int64_t k, void* stream) {
+  clear_error();
+  HI2X_REQUIRE(s && k > 0, "hessian_mirror: bad arguments");
+  return launch_mirror(s, k, as_stream(stream));
 }
 
 extern "C" int hi2x_hessian_syrk_varlen(const void* x, int dtype, const int64_t* offs,
@@ -636,4 +819,19 @@ extern "C" int hi2x_sigma_transform(const float* sigma, const uint16_t* col_scal
   hipLaunchKernelGGL(st_sym_kernel, dim3((unsigned)((int64_t)nT * (nT + 1) / 2)), dim3(256), 0,
                      s, k, nT, hs);
   return launch_status("st_sym_kernel");
+}
+
+extern "C" int hi2x_sigma_transform_upper(const float* s, int64_t n, const uint16_t* col_scale,
+                                          const uint8_t* had, int64_t k, float* hs,
+                                          void* stream) {
+  clear_error();
+  HI2X_REQUIRE(k > 0 && k % 16 == 0, "sigma_transform_upper: K=%lld not a multiple of 16",
+               (long long)k);
+  HI2X_REQUIRE(s && had && hs && s != hs, "sigma_transform_upper: bad buffers");
+  HI2X_REQUIRE(n >= 0, "sigma_transform_upper: n=%lld", (long long)n);
+  const unsigned nT = (unsigned)((k + FT - 1) / FT);
+  const float nf = (float)(n > 1 ? n : 1);
+  hipLaunchKernelGGL(st_upper_kernel, dim3(nT, nT), dim3(256), 0, as_stream(stream), s, nf,
+                     col_scale, had, k, hs);
+  return launch_status("st_upper_kernel");
 }

@@ -8,8 +8,11 @@ globals and errors): ``HessianStats`` (26-47), ``transform_sigma`` (50-68),
 
 Every arithmetic step runs in the hi2x HIP kernels (``libhi2x.so``):
 
-* ``HessianStats.update``: ``hi2x_hessian_syrk`` (bf16 / f32 MFMA, exactly symmetric);
+* ``HessianStats.update``: ``hi2x_hessian_syrk_upper`` (bf16 / f32 MFMA), with
+  ``hi2x_hessian_mirror`` when ``S`` is read (exactly symmetric);
 * ``transform_sigma``: ``hi2x_sigma_transform`` (bit-identical to the reference einsums);
+  ``HessianStats.transformed`` fuses the mean and the transform over the upper triangle
+  (``hi2x_sigma_transform_upper``, the same bits);
 * ``inverse_factor``: ``hi2x_chol_inv_upper`` (reversed blocked Cholesky + triangular
   inverse on f32 MFMA), the damping retry driven here as in the reference;
 * the ladder fit / 8-bit params (``hi2x_ladder_fit``, ``hi2x_params``), the column loop
@@ -54,7 +57,11 @@ __all__ = [
 class HessianStats:
     """Full second moment ``sum x x^T`` of a Linear's input (fp32, ``[K, K]``) on a HIP
     device; ``update`` accumulates on MFMA (bf16 inputs exactly, fp32 inputs on f32
-    MFMA, other dtypes converted to fp32 first as the reference does)."""
+    MFMA, other dtypes converted to fp32 first as the reference does).
+
+    ``update`` brings only the upper triangle up to date; the lower one is mirrored when
+    ``S`` is read (``S``, ``mean``, ``merge``), and ``transformed`` reads the upper
+    triangle directly, so the encode path never pays for the mirror."""
 
     def __init__(self, k: int, device="cuda"):
         self.k = k
@@ -63,24 +70,40 @@ class HessianStats:
             raise RuntimeError(
                 f"hi2_amd.HessianStats accumulates on the MI355X; got device {dev}"
             )
-        self.S = torch.zeros(k, k, dtype=torch.float32, device=dev)
+        self._S = torch.zeros(k, k, dtype=torch.float32, device=dev)
+        self._upper_only = False
         self.n = 0
+
+    @property
+    def S(self) -> torch.Tensor:
+        if self._upper_only:
+            _lib.call("hi2x_hessian_mirror", self._S.device, _lib.ptr(self._S), self.k)
+            self._upper_only = False
+        return self._S
+
+    @S.setter
+    def S(self, value: torch.Tensor) -> None:
+        self._S = value
+        self._upper_only = False
 
     @torch.no_grad()
     def update(self, x: torch.Tensor, chunk: int = 4096) -> None:
         """``S += x^T x`` over all rows of ``x[..., K]`` (``chunk`` is accepted for
         interface compatibility; the kernel streams the rows itself)."""
         x = x.reshape(-1, self.k)
-        dev = self.S.device
+        dev = self._S.device
         if x.dtype not in (torch.bfloat16, torch.float32):
             x = x.to(torch.float32)
         x = x.to(dev).contiguous()
         t = x.shape[0]
         if t:
+            if self._S.dtype != torch.float32 or not self._S.is_contiguous():
+                self._S = self.S.to(torch.float32).contiguous()
             dtype = 2 if x.dtype == torch.bfloat16 else 0
             ws = _lib.workspace(dev, "hi2x_hessian_workspace_bytes", dtype, t, self.k)
-            _lib.call("hi2x_hessian_syrk", dev, _lib.ptr(x), dtype, t, self.k,
-                      _lib.ptr(self.S), _lib.ptr(ws), ws.numel())
+            _lib.call("hi2x_hessian_syrk_upper", dev, _lib.ptr(x), dtype, t, self.k,
+                      _lib.ptr(self._S), _lib.ptr(ws), ws.numel())
+            self._upper_only = True
         self.n += t
 
     def merge(self, other: "HessianStats") -> None:
@@ -88,7 +111,31 @@ class HessianStats:
         self.n += other.n
 
     def mean(self) -> torch.Tensor:
-        return self.S / max(self.n, 1)
+        # a device tensor divisor keeps this an IEEE division per element (a Python
+        # scalar would turn into a multiplication by its reciprocal on the GPU)
+        s = self.S
+        return s / torch.tensor(float(max(self.n, 1)), dtype=s.dtype, device=s.device)
+
+    def transformed(self, col_scale: torch.Tensor | None, had: torch.Tensor) -> torch.Tensor:
+        """``transform_sigma(self.mean(), col_scale, had)`` in one pass over the upper
+        triangle of ``S``, bit for bit."""
+        k = self.k
+        if k % GROUP:
+            raise ValueError(f"K={k} must be a multiple of {GROUP}")
+        s = self._S
+        if s.dtype != torch.float32 or not s.is_contiguous():
+            return transform_sigma(self.mean(), col_scale, had)
+        dev = s.device
+        fl = had.to(dev, torch.uint8).reshape(-1).contiguous()
+        if fl.numel() != k // GROUP:
+            raise ValueError(f"had has {fl.numel()} entries, expected {k // GROUP}")
+        cs = None
+        if col_scale is not None:
+            cs = col_scale.to(dev, torch.float16).reshape(-1).contiguous()
+        out = torch.empty_like(s)
+        _lib.call("hi2x_sigma_transform_upper", dev, _lib.ptr(s), self.n, _lib.ptr(cs),
+                  _lib.ptr(fl), k, _lib.ptr(out))
+        return out
 
 
 def transform_sigma(

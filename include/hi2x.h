@@ -157,6 +157,17 @@ int64_t hi2x_hessian_workspace_bytes(int dtype, int64_t t, int64_t k);
 int hi2x_hessian_syrk(const void* x, int dtype, int64_t t, int64_t k, float* s, void* ws,
                       int64_t ws_bytes, void* stream);
 
+/* As hi2x_hessian_syrk, but only the upper triangle (i <= j) of s is brought up to date
+ * (bf16; f32 input still writes both): for callers that read the sum through
+ * hi2x_sigma_transform_upper, or mirror it later with hi2x_hessian_mirror.  The split of
+ * HessianStats.update's symmetric result into these two steps has no counterpart in the
+ * reference (hi2/hessian.py:35-40 keeps the full matrix). */
+int hi2x_hessian_syrk_upper(const void* x, int dtype, int64_t t, int64_t k, float* s,
+                            void* ws, int64_t ws_bytes, void* stream);
+
+/* s[j][i] = s[i][j] for i < j: the lower triangle from the upper. */
+int hi2x_hessian_mirror(float* s, int64_t k, void* stream);
+
 /* Variable-length batch of the above (routed MoE tokens, hi2/moe.py:83-100):
  * group e accumulates rows [offs[e], offs[e+1]) of x into s_ptrs[e] ([k, k] f32).
  * offs is a host array of n_groups + 1 row offsets; s_ptrs a host array.  The workspace
@@ -171,6 +182,13 @@ int hi2x_hessian_syrk_varlen(const void* x, int dtype, const int64_t* offs,
  * fp32 einsum order. */
 int hi2x_sigma_transform(const float* sigma, const uint16_t* col_scale, const uint8_t* had,
                          int64_t k, float* hs, void* stream);
+
+/* transform_sigma(HessianStats.mean()) (hi2/hessian.py:46-47 then 50-68) in one pass from
+ * the upper triangle of the running sum s [k, k] over n rows: sigma = s / max(n, 1) by
+ * IEEE division (the reference's CPU mean), then exactly the ops of
+ * hi2x_sigma_transform.  The lower triangle of s is not read. */
+int hi2x_sigma_transform_upper(const float* s, int64_t n, const uint16_t* col_scale,
+                               const uint8_t* had, int64_t k, float* hs, void* stream);
 
 /* ---- Cholesky chain ------------------------------------------------------------------ */
 
@@ -204,7 +222,7 @@ int hi2x_chol_inv_upper_async(const float* hs, int64_t k, float damp, int attemp
  * (waiting for their events); mask 0 stops recording.  Process-wide, not meant to be
  * switched while other threads launch. */
 #define HI2X_TIME_GPTQ_TRAILING 0 /* work = 2 * rows * rank * columns (flops) */
-#define HI2X_TIME_HESSIAN_SYRK 1  /* work = 2 * tokens * k^2 (flops, full X^T X) */
+#define HI2X_TIME_HESSIAN_SYRK 1  /* work = tokens * k * (k + 1) (flops, upper triangle) */
 #define HI2X_TIME_CHOL_GEMM 2     /* work = flops of the triangular product */
 #define HI2X_TIME_CHOL_LEAF 3     /* work = 2 * n^3 / 3 (factor + inverse of the leaf) */
 #define HI2X_TIME_GPTQ_BLOCK 4    /* work = rows * len * (len - 1) (intra-block flops) */

@@ -335,6 +335,52 @@ def test_transform_sigma_equals_oracle(dev, smooth):
     assert np.array_equal(N(got), want)
 
 
+@pytest.mark.parametrize("k", [48, 320, 1040])
+@pytest.mark.parametrize("smooth", [False, True])
+def test_transformed_equals_transform_of_mean(dev, k, smooth):
+    """HessianStats.transformed (one pass over the upper triangle of S, no mirror) equals
+    the oracle's transform of S / n and transform_sigma(mean()) bit for bit: K not a
+    multiple of the 64-wide tiles, n not a power of two, mixed Hadamard flags."""
+    from hi2_amd.hessian import HessianStats, transform_sigma
+
+    rng = np.random.default_rng(k + smooth)
+    t = 777
+    x = (rng.standard_normal((t, k)) * np.exp(rng.standard_normal((1, k)))).astype(np.float32)
+    xb = T(x, dev).to(torch.bfloat16)
+    had = rng.integers(0, 2, k // 16).astype(np.uint8)
+    cs = (rng.random(k) * 2 + 0.3).astype(np.float16) if smooth else None
+    cs_d = None if cs is None else T(cs, dev)
+    st = HessianStats(k, dev)
+    st.update(xb[:300])
+    st.update(xb[300:])
+    got = st.transformed(cs_d, T(had, dev))
+    assert st._upper_only  # S has not been mirrored for it
+    s_full = N(st.S)
+    assert np.array_equal(s_full, s_full.T)
+    mean = s_full / np.float32(t)
+    assert np.array_equal(N(st.mean()), mean)  # IEEE division, as the reference's CPU mean
+    want = oracle.transform_sigma(mean, None if cs is None else cs.view(np.uint16), had)
+    assert np.array_equal(N(got), want)
+    assert torch.equal(got, transform_sigma(st.mean(), cs_d, T(had, dev)))
+
+
+def test_upper_update_then_mirror_equals_full_update(dev):
+    """hi2x_hessian_syrk_upper + the mirror on first read of S == hi2x_hessian_syrk."""
+    from hi2_amd import _lib
+    from hi2_amd.hessian import HessianStats
+
+    k, t = 1040, 500
+    g = torch.Generator(device=dev).manual_seed(9)
+    x = torch.randn(t, k, device=dev, generator=g).to(torch.bfloat16)
+    st = HessianStats(k, dev)
+    st.update(x)
+    full = torch.zeros(k, k, device=dev)
+    ws = _lib.workspace(dev, "hi2x_hessian_workspace_bytes", 2, t, k)
+    _lib.call("hi2x_hessian_syrk", dev, _lib.ptr(x), 2, t, k, _lib.ptr(full), _lib.ptr(ws),
+              ws.numel())
+    assert torch.equal(st.S, full)
+
+
 @pytest.mark.parametrize("k", [96, 320, 1000 - 1000 % 16])
 def test_inverse_factor_inverts(dev, k):
     from hi2_amd.hessian import inverse_factor
