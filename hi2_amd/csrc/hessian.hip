@@ -129,8 +129,9 @@ __global__ __launch_bounds__(256) void syrk_bf16_kernel(const uint16_t* __restri
 // the token range (partials combined in a fixed order afterwards) so that small K still
 // fills the chip.
 constexpr int S2T = 256;          // workgroup tile edge
-constexpr int S2C = 64;           // tokens per stage
-constexpr int S2P = S2C + 8;      // LDS pitch (bf16) per feature row
+constexpr int S2C = 32;           // tokens per stage (64 bytes of a feature row)
+constexpr int S2NB = 4;           // LDS stage buffers (prefetch distance S2NB - 1)
+constexpr int S2Q = S2C / 8;      // 16-byte slots per feature row and stage
 constexpr int S2R = 4, S2S = 8;   // super-tile: tile rows x tile columns per XCD round
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc_bytes(const void* base, int64_t bytes) {
@@ -189,13 +190,56 @@ __global__ __launch_bounds__(256) void transpose_bf16_kernel(const uint16_t* __r
   }
 }
 
+// Operands of one k-step (16 tokens) of the current stage: XA / XB point at this lane's
+// operand row (tile t adds 32 rows), so its 16-byte slot.
+__device__ __forceinline__ void syrk_read(bf16x8 (&av)[4], bf16x8 (&bv)[4], const uint16_t* XA,
+                                          const uint16_t* XB, int so) {
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    av[t] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u16x8*>(&XA[32 * t * S2C + so]));
+    bv[t] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u16x8*>(&XB[32 * t * S2C + so]));
+  }
+}
+__device__ __forceinline__ void syrk_mma(f32x16 (&acc)[4][4], const bf16x8 (&av)[4],
+                                         const bf16x8 (&bv)[4]) {
+#pragma unroll
+  for (int a = 0; a < 4; ++a)
+#pragma unroll
+    for (int b = 0; b < 4; ++b)
+      acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av[a], bv[b], acc[a][b], 0, 0, 0);
+}
+
+// 16 bytes per lane from a buffer straight into LDS: lane L writes lds + 16 L (lds is
+// wave-uniform).  Issued as inline assembly so that the compiler does not treat the
+// asynchronous LDS write as aliasing every later LDS read (it would wait for all loads
+// in flight before the first one); the kernel orders the writes itself with vmcnt waits
+// and barriers.  m0 holds the LDS address only for this instruction.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void lds_dma16(__amdgpu_buffer_rsrc_t rs, uint32_t voff, void* lds) {
+  const uint32_t la = __builtin_amdgcn_readfirstlane(
+      (uint32_t)(size_t)(__attribute__((address_space(3))) void*)lds);
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+               :
+               : "s"(la), "v"(voff), "s"(rs)
+               : "m0");
+}
+#pragma clang diagnostic pop
+
+// s_waitcnt immediate: wait until at most vm vector memory and lgkm LDS operations of this
+// wave are outstanding (gfx9 encoding: vmcnt in bits 3:0 and 15:14, expcnt 6:4 left at
+// its maximum, lgkmcnt 11:8)
+constexpr int waitcnt_imm(int vm, int lgkm) {
+  return (vm & 15) | ((vm >> 4) << 14) | (7 << 4) | (lgkm << 8);
+}
+
 __global__ __launch_bounds__(256) void syrk2_bf16_kernel(const uint16_t* __restrict__ xt,
                                                          int64_t T, int64_t K, int nT,
                                                          int64_t ntiles, int splits,
                                                          int64_t tchunk, float* __restrict__ out,
                                                          int64_t out_stride, int super) {
-  __shared__ __attribute__((aligned(16))) uint16_t Xa[2][S2T * S2P];
-  __shared__ __attribute__((aligned(16))) uint16_t Xb[2][S2T * S2P];
+  __shared__ __attribute__((aligned(1024))) uint16_t Xa[S2NB][S2T * S2C];
+  __shared__ __attribute__((aligned(1024))) uint16_t Xb[S2NB][S2T * S2C];
   const int64_t id = (int64_t)blockIdx.x;
   int ta, tb, sp = 0;
   if (super) {
@@ -227,75 +271,96 @@ __global__ __launch_bounds__(256) void syrk2_bf16_kernel(const uint16_t* __restr
   const int rowsB = (int)((K - b0 < S2T) ? K - b0 : S2T);
   const __amdgpu_buffer_rsrc_t rsa = rsrc_bytes(xt + a0 * T, (int64_t)rowsA * T * 2);
   const __amdgpu_buffer_rsrc_t rsb = rsrc_bytes(xt + b0 * T, (int64_t)rowsB * T * 2);
-  // A stage of a panel is 256 feature rows x 128 bytes: 8 consecutive threads read one
-  // row's 128 contiguous bytes (one cache line per 8 lanes), thread tid covers piece
-  // tid % 8 of rows tid / 8 + 32 i.
-  constexpr int NQ = S2C / 8;            // 16-byte pieces per feature row and stage
-  constexpr int RSTEP = 256 / NQ;        // rows between a thread's pieces
-  const int pq = tid % NQ, pr = tid / NQ;
-  const uint32_t rowoff = (uint32_t)((int64_t)pr * T * 2 + 16 * pq);
-  const uint32_t rstep = (uint32_t)((int64_t)RSTEP * T * 2);
-  uint4 ra[NQ], rb[NQ];
-  auto load = [&](int64_t t0) {
-    uint32_t b = rowoff + (uint32_t)(t0 * 2);
-    asm volatile("" : "+v"(b));  // rebuilt per stage, not held across the loop
-#pragma unroll
-    for (int i = 0; i < NQ; ++i) {
-      const int row = pr + RSTEP * i;
-      const uint32_t o = b + rstep * i;
-      ra[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(
-                                            rsa, (int)(row < rowsA ? o : MG_OOB), 0, 0));
-      rb[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(
-                                            rsb, (int)((!diag && row < rowsB) ? o : MG_OOB), 0, 0));
+  // A stage of a panel (256 feature rows x 32 tokens = 64 bytes per row) goes from L2
+  // straight into LDS (no registers, no LDS store instructions): each load instruction
+  // of a wave writes 1 KB, 16 rows of 4 16-byte slots, lane L into slot L % 4 of row
+  // L / 4.  Rows carry no padding; slot q of row r holds the row's piece q ^ ((r / 4) % 4),
+  // so that the 16 consecutive rows an MFMA operand read touches (same piece) fall on 16
+  // different 16-byte bank groups.  S2NB stages are in flight: the stage S2NB - 1 ahead
+  // is requested while the current one is multiplied.
+  constexpr int NC = S2T * S2C * 2 / 1024 / 4;  // 1 KB chunks per wave and panel
+  const int prow = lane >> 2, piece = (lane & 3) ^ ((lane >> 4) & 3);
+  const int wv = __builtin_amdgcn_readfirstlane(wave);  // uniform: LDS addresses in SGPRs
+  // load instruction j of a stage (chunk j / 2 of panel A or B, j % 2); b is this lane's
+  // byte offset of the stage in its first row
+  // (live = false: a load that reads nothing and writes zeros, for stages past the end,
+  // so that every stage issues the same number of loads)
+  auto dma_one = [&](int j, uint32_t b, int buf, bool live) {
+    const int i = j >> 1, c = NC * wv + i, row = 16 * c + prow;
+    const uint32_t o = b + (uint32_t)((int64_t)16 * i * T * 2);
+    if ((j & 1) == 0) {
+      lds_dma16(rsa, (live && row < rowsA) ? o : MG_OOB, &Xa[buf][c * 512]);
+    } else {  // diagonal tiles load the A panel twice (uniform count of loads per stage)
+      lds_dma16(diag ? rsa : rsb, (live && row < (diag ? rowsA : rowsB)) ? o : MG_OOB,
+                &Xb[buf][c * 512]);
     }
   };
-  auto store = [&](int buf) {
-#pragma unroll
-    for (int i = 0; i < NQ; ++i) {
-      const int row = pr + RSTEP * i;
-      *reinterpret_cast<uint4*>(&Xa[buf][row * S2P + 8 * pq]) = ra[i];
-      if (!diag) *reinterpret_cast<uint4*>(&Xb[buf][row * S2P + 8 * pq]) = rb[i];
-    }
+  auto stage_off = [&](int64_t t0) {
+    uint32_t b = (uint32_t)(((int64_t)(16 * NC * wv + prow)) * T * 2 + t0 * 2 + 16 * piece);
+    asm volatile("" : "+v"(b));
+    return b;
   };
+  auto dma = [&](int64_t t0, int buf, bool live) {
+    const uint32_t b = stage_off(t0);
+#pragma unroll
+    for (int j = 0; j < 2 * NC; ++j) dma_one(j, b, buf, live);
+  };
+  constexpr int PER_STAGE = 2 * NC;  // load instructions per wave and stage
+  static_assert(S2C == 32 && S2NB == 4, "the loop below reads two k-steps per stage");
+  // operand rows of this lane (+ 32 t for tile t) and its slots of pieces h and 2 + h:
+  // rows within a 32-row tile start at a multiple of 16, so (row / 4) % 4 = (lane / 4) % 4
+  const int rowA = wr * 128 + (lane & 31), rowB = wcn * 128 + (lane & 31);
+  const int so0 = 8 * ((lane >> 5) ^ ((lane >> 2) & 3));
+  const int so1 = 8 * ((2 + (lane >> 5)) ^ ((lane >> 2) & 3));
   const int nst = (int)((tend - tbeg + S2C - 1) / S2C);
+  // Pipeline: stage st + 1's k-step 0 operands are read, and stage st + 4 requested,
+  // between the two k-steps of stage st, so that no LDS latency is exposed at the stage
+  // boundary.  The ring holds stages st .. st + 3; every stage issues PER_STAGE loads
+  // (stages past the end load nothing), so "stage j has landed" is always "at most the
+  // two later stages' loads outstanding".  The loop body has no branch: MFMA chains on
+  // one path only keep the accumulators in place.
+  auto sync = [&]() {
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);  // no LDS access moves across the barrier
+    __builtin_amdgcn_s_barrier();
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  };
+  bf16x8 oa0[4], ob0[4], oa1[4], ob1[4];
   if (nst > 0) {
-    load(tbeg);
-    store(0);
-    __syncthreads();
+#pragma unroll
+    for (int p = 0; p < S2NB; ++p) dma(tbeg + (int64_t)p * S2C, p, p < nst);
+    __builtin_amdgcn_s_waitcnt(waitcnt_imm(3 * PER_STAGE, 15));  // stage 0 landed
+    sync();
+    syrk_read(oa0, ob0, &Xa[0][rowA * S2C], &Xb[0][rowB * S2C], so0);
   }
   for (int st = 0; st < nst; ++st) {
-    const int buf = st & 1;
-    const bool more = st + 1 < nst;
-    if (more) load(tbeg + (int64_t)(st + 1) * S2C);
-    const uint16_t* XA = Xa[buf] + (wr * 128 + (lane & 31)) * S2P + 8 * (lane >> 5);
-    const uint16_t* XB = (diag ? Xa[buf] : Xb[buf]) + (wcn * 128 + (lane & 31)) * S2P + 8 * (lane >> 5);
-    // operands of k-step ks + 16 are read while the MFMAs of ks run (one wave per SIMD:
-    // nothing else hides the LDS latency)
-    bf16x8 av[2][4], bv[2][4];
-    auto read = [&](int set, int ks) {
-#pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        av[set][t] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u16x8*>(&XA[t * 32 * S2P + ks]));
-        bv[set][t] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u16x8*>(&XB[t * 32 * S2P + ks]));
-      }
-    };
-    read(0, 0);
-#pragma unroll
-    for (int kk = 0; kk < S2C / 16; ++kk) {
-      const int cur = kk & 1;
-      if (kk + 1 < S2C / 16) read(cur ^ 1, 16 * (kk + 1));
-      __builtin_amdgcn_sched_barrier(0);  // keep the reads ahead of this step's MFMAs
-#pragma unroll
-      for (int a = 0; a < 4; ++a)
-#pragma unroll
-        for (int b = 0; b < 4; ++b)
-          acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av[cur][a], bv[cur][b], acc[a][b], 0, 0, 0);
-      __builtin_amdgcn_sched_barrier(0);
-    }
+    const int cb = st % S2NB, nb = (st + 1) % S2NB;
+    syrk_read(oa1, ob1, &Xa[cb][rowA * S2C], &Xb[cb][rowB * S2C], so1);
     __builtin_amdgcn_sched_barrier(0);
-    if (more) store(buf ^ 1);  // buffer buf ^ 1 was last read before the barrier
-    __syncthreads();
+    syrk_mma(acc, oa0, ob0);
+    __builtin_amdgcn_sched_barrier(0);
+    // this wave's reads of stage st are done and stage st + 1 has landed; after the
+    // barrier no wave reads buffer cb any more (past the end: reads of unused zeros)
+    __builtin_amdgcn_s_waitcnt(waitcnt_imm(2 * PER_STAGE, 0));
+    sync();
+    syrk_read(oa0, ob0, &Xa[nb][rowA * S2C], &Xb[nb][rowB * S2C], so0);
+    __builtin_amdgcn_sched_barrier(0);
+    // stage st + 4 into buffer cb, one load after every second MFMA (a single wave per
+    // SIMD issues in order: a block of loads would leave the MFMA pipe idle)
+    const uint32_t b = stage_off(tbeg + (int64_t)(st + S2NB) * S2C);
+    const bool live = st + S2NB < nst;
+#pragma unroll
+    for (int a = 0; a < 4; ++a)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        acc[a][q] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(oa1[a], ob1[q], acc[a][q], 0, 0, 0);
+        if (q & 1) {
+          dma_one(2 * a + (q >> 1), b, cb, live);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      }
+    __builtin_amdgcn_sched_barrier(0);
   }
+  __syncthreads();
   // upper part of the tile (i <= j on the diagonal tile); the lower triangle is mirrored
   // from it afterwards.  Branch-free: one buffer over the tile, rejected elements get an
   // offset past it.
