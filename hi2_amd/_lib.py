@@ -45,6 +45,7 @@ SIGNATURES = {
     "hi2x_hessian_mirror": [_P, _I64, _P],
     "hi2x_sigma_transform": [_P, _P, _P, _I64, _P, _P],
     "hi2x_sigma_transform_upper": [_P, _I64, _P, _P, _I64, _P, _P],
+    "hi2x_chol_lambda": [_P, _I64, _F, _I, _P, _P],
     "hi2x_chol_inv_upper": [_P, _I64, _F, _I, _P, _P, _I64, _P],
     "hi2x_chol_inv_upper_async": [_P, _I64, _F, _I, _P, _P, _P, _I64, _P],
 }

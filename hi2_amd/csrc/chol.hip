@@ -57,13 +57,26 @@ constexpr int tri_order() {
   return AMODE == 1 ? 1 : (BMODE == 2 ? 2 : (BMODE == 1 ? 3 : 0));
 }
 
+// rank range [kbeg, kend) of output tile (r0, c0): the triangular operand's nonzeros
+template <int AMODE, int BMODE>
+__host__ __device__ inline void tri_krange(int64_t r0, int64_t c0, int64_t T, int64_t Kd,
+                                           int64_t& kbeg, int64_t& kend) {
+  kbeg = 0;
+  kend = Kd;
+  if (AMODE == 1) kend = (r0 + T < kend) ? r0 + T : kend;
+  if (BMODE == 1) kbeg = c0;
+  if (BMODE == 2) kend = (c0 + T < kend) ? c0 + T : kend;
+}
+
 template <int AMODE, int BMODE, bool TB, bool CLOW, int T>
 __global__ __launch_bounds__(256) void tri_gemm_kernel(GemmArgs g, int64_t tm, int64_t tn,
-                                                       int super) {
+                                                       int super, MgSched sched) {
   constexpr int NA = T / 64;
   __shared__ MgSmemT<T> sm;
   int64_t tr, tc;
-  if (super) {
+  if (sched.per_xcd > 0) {
+    if (!mg_sched_tile<CLOW>(blockIdx.x, sched, tm, tn, tr, tc)) return;
+  } else if (super) {
     if (!mg_super_tile<tri_order<AMODE, BMODE>(), CLOW>(blockIdx.x, tm, tn, tr, tc)) return;
   } else {
     const int64_t t = xcd_tile(blockIdx.x, tm * tn);
@@ -73,10 +86,8 @@ __global__ __launch_bounds__(256) void tri_gemm_kernel(GemmArgs g, int64_t tm, i
   }
   const int64_t r0 = tr * T, c0 = tc * T;
   if (CLOW && c0 > r0 + T - 1) return;
-  int64_t kbeg = 0, kend = g.Kd;
-  if (AMODE == 1) kend = (r0 + T < kend) ? r0 + T : kend;
-  if (BMODE == 1) kbeg = c0;
-  if (BMODE == 2) kend = (c0 + T < kend) ? c0 + T : kend;
+  int64_t kbeg, kend;
+  tri_krange<AMODE, BMODE>(r0, c0, T, g.Kd, kbeg, kend);
   f32x16 acc[NA][NA];
   mg_zero<NA>(acc);
   using AMask = typename std::conditional<AMODE == 1, MaskLower, NoMask>::type;
@@ -129,14 +140,32 @@ int tri_gemm(const GemmArgs& a, hipStream_t s) {
     const int64_t tm6 = (a.M + 63) / 64, tn6 = (a.N + 63) / 64;
     const int64_t grid = (tm6 * tn6 + 7) / 8 * 8;
     hipLaunchKernelGGL((tri_gemm_kernel<AMODE, BMODE, TB, CLOW, 64>), dim3((unsigned)grid),
-                       dim3(256), 0, s, a, tm6, tn6, 0);
+                       dim3(256), 0, s, a, tm6, tn6, 0, MgSched{});
     return launch_status("tri_gemm_kernel");
   }
-  // big grids (several rounds of the 512 workgroup slots): super-tile schedule
+  // big grids (several rounds of the 512 workgroup slots): super-tiles balanced over the
+  // XCDs by their rank (plus two chunks' worth of per-tile overhead)
   const int super = (CLOW ? ntiles / 2 : ntiles) >= 256 ? 1 : 0;
-  const int64_t grid = super ? mg_super_grid(tm, tn, CLOW) : (ntiles + 7) / 8 * 8;
+  MgSched sched;
+  if (super) {
+    sched = mg_balance(tm, tn, [&](int64_t sr, int64_t sc) {
+      double w = 0.0;
+      for (int64_t i = 0; i < MG_SUP; ++i)
+        for (int64_t j = 0; j < MG_SUP; ++j) {
+          const int64_t tr = sr * MG_SUP + i, tc = sc * MG_SUP + j;
+          if (tr >= tm || tc >= tn || (CLOW && tc > tr)) continue;
+          int64_t kb, ke;
+          tri_krange<AMODE, BMODE>(tr * MG_T, tc * MG_T, MG_T, a.Kd, kb, ke);
+          w += (double)std::max<int64_t>(0, ke - kb) + 2.0 * MG_KC;
+        }
+      return w;
+    });
+  }
+  const int64_t grid = sched.per_xcd > 0 ? mg_sched_grid(sched)
+                       : super            ? mg_super_grid(tm, tn, CLOW)
+                                          : (ntiles + 7) / 8 * 8;
   hipLaunchKernelGGL((tri_gemm_kernel<AMODE, BMODE, TB, CLOW, MG_T>), dim3((unsigned)grid),
-                     dim3(256), 0, s, a, tm, tn, super);
+                     dim3(256), 0, s, a, tm, tn, super, sched);
   return launch_status("tri_gemm_kernel");
 }
 
@@ -148,8 +177,12 @@ int tri_gemm(const GemmArgs& a, hipStream_t s) {
 __global__ __launch_bounds__(256) void diag_mean_kernel(const float* __restrict__ hs, int64_t K,
                                                         float damp, float p10,
                                                         float* __restrict__ lam_out) {
-  constexpr int CH = 4096;  // diagonal elements per LDS chunk (multiple of 4)
-  __shared__ float dg[CH];
+  // Accumulator q adds element q of every row of 4 in row order; within a step of
+  // `step` rows it starts from zero (the cascade moved it up at the previous step end),
+  // so the step sums are independent: all threads form them in parallel (each one the
+  // same sequential chain as the reference), then thread q runs the cascade over them.
+  constexpr int SC = 1024;  // steps per round
+  __shared__ float ssum[SC][4];
   __shared__ float part[4];
   const int tid = threadIdx.x;
   const int64_t size_ilp = K / 4;
@@ -158,37 +191,42 @@ __global__ __launch_bounds__(256) void diag_mean_kernel(const float* __restrict_
   lp /= 4;
   if (lp < 4) lp = 4;
   const int64_t step = (int64_t)1 << lp, lmask = step - 1;
+  const int64_t nsteps = size_ilp / step;  // full steps; rows past them are the remainder
   float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-  int64_t j = 0;  // rows of 4 consumed into the current step
-  int64_t i = 0;  // row index of the cascade (rows of 4)
-  for (int64_t base = 0; base < K; base += CH) {
-    const int64_t cnt = (K - base < CH) ? K - base : CH;
+  int64_t i = 0;  // rows of 4 consumed by full steps
+  for (int64_t s0 = 0; s0 < nsteps; s0 += SC) {
+    const int64_t ns = (nsteps - s0 < SC) ? nsteps - s0 : SC;
     __syncthreads();
-    for (int64_t e = tid; e < cnt; e += 256) dg[e] = hs[(base + e) * K + (base + e)];
+    for (int64_t task = tid; task < ns * 4; task += 256) {
+      const int64_t sidx = task >> 2, q = task & 3;
+      const int64_t row0 = (s0 + sidx) * step;
+      float a = 0.0f;
+      for (int64_t r = 0; r < step; ++r) {
+        const int64_t e = 4 * (row0 + r) + q;
+        a += hs[e * K + e];
+      }
+      ssum[sidx][q] = a;
+    }
     __syncthreads();
     if (tid < 4) {
-      for (int64_t e = 0; e + 4 <= cnt; e += 4) {
-        const int64_t row = (base + e) / 4;
-        if (row >= size_ilp) break;
-        const int64_t full = (size_ilp / step) * step;  // rows handled by the cascade loop
-        if (row < full) {
-          acc[0] += dg[e + tid];
-          if (++j == step) {  // a full step of rows done: propagate as the reference does
-            j = 0;
-            i += step;
-            for (int lev = 1; lev < 4; ++lev) {
-              acc[lev] += acc[lev - 1];
-              acc[lev - 1] = 0.0f;
-              if (i & (lmask << (lev * lp))) break;
-            }
-          }
-        } else {
-          acc[0] += dg[e + tid];  // the remaining rows after the last full step
+      for (int64_t sidx = 0; sidx < ns; ++sidx) {
+        acc[0] = ssum[sidx][tid];  // acc[0] is zero at a step start
+        i += step;
+        for (int lev = 1; lev < 4; ++lev) {
+          acc[lev] += acc[lev - 1];
+          acc[lev - 1] = 0.0f;
+          if (i & (lmask << (lev * lp))) break;
         }
       }
     }
   }
-  if (tid < 4) part[tid] = ((acc[0] + acc[1]) + acc[2]) + acc[3];
+  if (tid < 4) {  // the remaining rows after the last full step, in order
+    for (int64_t row = nsteps * step; row < size_ilp; ++row) {
+      const int64_t e = 4 * row + tid;
+      acc[0] += hs[e * K + e];
+    }
+    part[tid] = ((acc[0] + acc[1]) + acc[2]) + acc[3];
+  }
   __syncthreads();
   if (tid == 0) {
     float p0 = part[0];
@@ -671,6 +709,18 @@ static int chol_launch(const float* hs, int64_t k, float damp, int attempt, floa
     rc = launch_status("reverse_out_kernel");
   }
   return rc;
+}
+
+extern "C" int hi2x_chol_lambda(const float* hs, int64_t k, float damp, int attempt,
+                                float* lam, void* stream) {
+  clear_error();
+  HI2X_REQUIRE(hs && lam && k > 0, "chol_lambda: bad arguments");
+  HI2X_REQUIRE(attempt >= 0 && attempt <= 30, "chol_lambda: attempt %d", attempt);
+  float p10 = 1.0f;
+  for (int a = 0; a < attempt; ++a) p10 *= 10.0f;
+  hipLaunchKernelGGL(diag_mean_kernel, dim3(1), dim3(256), 0, as_stream(stream), hs, k, damp,
+                     p10, lam);
+  return launch_status("diag_mean_kernel");
 }
 
 extern "C" int64_t hi2x_chol_workspace_bytes(int64_t k) {

@@ -14,6 +14,10 @@
 // through the buffer-load range check, and triangular operands zero their structural
 // zeros when a chunk is staged, so the unused triangle never enters a product.
 #pragma once
+#include <algorithm>
+#include <utility>
+#include <vector>
+
 #include "common.h"
 
 namespace hi2x {
@@ -383,6 +387,73 @@ __host__ __device__ inline int64_t mg_super_count(int64_t tm, int64_t tn, bool t
 __host__ inline int64_t mg_super_grid(int64_t tm, int64_t tn, bool tri) {
   const int64_t nsup = mg_super_count(tm, tn, tri);
   return (nsup + 7) / 8 * 8 * MG_SUP * MG_SUP;
+}
+
+// Balanced schedule: the host weighs every super-tile (the summed rank of its tiles plus
+// a per-tile overhead) and deals them to the 8 XCDs longest-processing-time first (each
+// to the least loaded XCD so far), so that no XCD ends long after the others.  Workgroup
+// slot j * 64 + w of XCD x runs tile w of the XCD's j-th super-tile.
+constexpr int MG_SCHED_MAX = 448;  // super-tiles a table holds (else round-robin)
+struct MgSched {
+  int32_t per_xcd = 0;                 // super-tiles of the busiest XCD (0: no table)
+  int32_t nsc = 0;                     // super-tile columns
+  uint16_t st[MG_SCHED_MAX] = {};      // [x * per_xcd + j]: sr * nsc + sc, 0xffff: none
+};
+
+// weight(sr, sc) -> work of super-tile (sr, sc) (0: empty)
+template <class Weight>
+__host__ inline MgSched mg_balance(int64_t tm, int64_t tn, Weight weight) {
+  MgSched s;
+  const int64_t nsr = (tm + MG_SUP - 1) / MG_SUP, nsc = (tn + MG_SUP - 1) / MG_SUP;
+  std::vector<std::pair<double, int>> items;
+  for (int64_t sr = 0; sr < nsr; ++sr)
+    for (int64_t sc = 0; sc < nsc; ++sc) {
+      const double w = weight(sr, sc);
+      if (w > 0.0) items.push_back({w, (int)(sr * nsc + sc)});
+    }
+  if (items.empty() || (int64_t)items.size() > MG_SCHED_MAX || nsr * nsc > 0xffff) return s;
+  std::stable_sort(items.begin(), items.end(),
+                   [](const std::pair<double, int>& a, const std::pair<double, int>& b) {
+                     return a.first > b.first;
+                   });
+  double load[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  std::vector<int> lists[8];
+  for (const auto& it : items) {
+    int best = 0;
+    for (int x = 1; x < 8; ++x)
+      if (load[x] < load[best]) best = x;
+    load[best] += it.first;
+    lists[best].push_back(it.second);
+  }
+  int per = 0;
+  for (int x = 0; x < 8; ++x) per = std::max(per, (int)lists[x].size());
+  if ((int64_t)per * 8 > MG_SCHED_MAX) return s;
+  s.per_xcd = per;
+  s.nsc = (int)nsc;
+  for (int x = 0; x < 8; ++x)
+    for (int j = 0; j < per; ++j)
+      s.st[x * per + j] = j < (int)lists[x].size() ? (uint16_t)lists[x][j] : (uint16_t)0xffff;
+  return s;
+}
+
+__host__ inline int64_t mg_sched_grid(const MgSched& s) {
+  return (int64_t)8 * s.per_xcd * MG_SUP * MG_SUP;
+}
+
+template <bool TRI>
+__device__ __forceinline__ bool mg_sched_tile(int64_t bid, const MgSched& s, int64_t tm,
+                                              int64_t tn, int64_t& tr, int64_t& tc) {
+  const int x = (int)(bid & 7);
+  const int64_t slot = bid >> 3;
+  const int j = (int)(slot / (MG_SUP * MG_SUP)), w = (int)(slot % (MG_SUP * MG_SUP));
+  if (j >= s.per_xcd) return false;
+  const int u = s.st[x * s.per_xcd + j];
+  if (u == 0xffff) return false;
+  tr = (int64_t)(u / s.nsc) * MG_SUP + w / MG_SUP;
+  tc = (int64_t)(u % s.nsc) * MG_SUP + w % MG_SUP;
+  if (tr >= tm || tc >= tn) return false;
+  if (TRI && tc > tr) return false;
+  return true;
 }
 
 template <int ORDER, bool TRI>

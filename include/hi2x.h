@@ -192,6 +192,13 @@ int hi2x_sigma_transform_upper(const float* s, int64_t n, const uint16_t* col_sc
 
 /* ---- Cholesky chain ------------------------------------------------------------------ */
 
+/* The damping term of attempt `attempt` (hi2/hessian.py:75-79): *lam (device) =
+ * damp * max(mean(diag hs), 1e-12) * 10^attempt in fp32, the mean reduced in the order
+ * of torch's CPU sum of a strided vector.  The entry points below compute it the same
+ * way. */
+int hi2x_chol_lambda(const float* hs, int64_t k, float damp, int attempt, float* lam,
+                     void* stream);
+
 /* Workspace of the two entry points below for a k x k matrix. */
 int64_t hi2x_chol_workspace_bytes(int64_t k);
 

@@ -75,6 +75,7 @@ def lib():
             "or_hessian_update": (None, [P, I, I64, I64, P]),
             "or_transform_sigma": (None, [P, P, P, I64, P]),
             "or_inverse_factor": (I, [P, I64, F, P]),
+            "or_torch_sum_strided": (F, [P, I64, I64]),
             "or_pack_codes": (I64, [P, I64, I64, I, P]),
             "or_assemble_piece": (I64, [P, I64, P, P, P, I64, I, I64, P, P, P, P, P]),
         }
@@ -230,6 +231,29 @@ def transform_sigma(sigma, col_scale_bits, had):
     cs = None if col_scale_bits is None else _c(col_scale_bits, np.uint16)
     lib().or_transform_sigma(_p(sigma), _p(cs), _p(_c(had, np.uint8)), k, _p(out))
     return out
+
+
+def damp_lambda(hs, damp=0.01, attempt=0):
+    """The damping term of attempt ``attempt`` of inverse_factor (hi2/hessian.py:75-79):
+    damp * max(mean(diag hs), 1e-12) * 10^attempt in fp32, the mean as torch's CPU
+    reduction of the strided diagonal (hi2_oracle.c: or_torch_sum_strided)."""
+    hs = np.ascontiguousarray(hs, dtype=np.float32)
+    k = hs.shape[0]
+    s = np.float32(lib().or_torch_sum_strided(_p(hs), k, k + 1))
+    mean = np.float32(s / np.float32(k))
+    mean = max(mean, np.float32(1e-12))
+    p10 = np.float32(1.0)
+    for _ in range(attempt):
+        p10 = np.float32(p10 * np.float32(10.0))
+    return np.float32(np.float32(np.float32(damp) * mean) * p10)
+
+
+def torch_sum_strided(x, n, stride):
+    """sum of x[0], x[stride], ..., x[(n-1) stride] in torch's CPU reduction order."""
+    x = np.ascontiguousarray(x, dtype=np.float32).reshape(-1)
+    if n and (n - 1) * stride >= x.size:
+        raise ValueError("strided vector exceeds the array")
+    return np.float32(lib().or_torch_sum_strided(_p(x), n, stride))
 
 
 def inverse_factor(hs, damp=0.01):

@@ -381,6 +381,22 @@ def test_upper_update_then_mirror_equals_full_update(dev):
     assert torch.equal(st.S, full)
 
 
+@pytest.mark.parametrize("k", [16, 100, 1000, 4108, 8448])
+def test_damping_lambda_equals_oracle(dev, k):
+    """The damping term (hi2/hessian.py:75-79) bit for bit: torch's CPU reduction order
+    of the strided diagonal, reproduced by the parallel step sums of diag_mean_kernel."""
+    from hi2_amd import _lib
+
+    rng = np.random.default_rng(k)
+    d = ((rng.standard_normal(k) * np.exp(rng.standard_normal(k))) ** 2).astype(np.float32)
+    hs = torch.diag(T(d, dev))
+    lam = torch.zeros(1, dtype=torch.float32, device=dev)
+    for a in (0, 2, 5):
+        _lib.call("hi2x_chol_lambda", dev, _lib.ptr(hs), k, 0.01, a, _lib.ptr(lam))
+        want = oracle.damp_lambda(np.diag(d), 0.01, a)
+        assert N(lam)[0] == want, (a, N(lam)[0], want)
+
+
 @pytest.mark.parametrize("k", [96, 320, 1000 - 1000 % 16])
 def test_inverse_factor_inverts(dev, k):
     from hi2_amd.hessian import inverse_factor

@@ -48,6 +48,29 @@ def test_sum_order_is_torch_cpu_order(n):
     assert _tsum(x) == torch.from_numpy(x).sum().item()
 
 
+@pytest.mark.parametrize("n,stride", [(16, 17), (48, 49), (100, 101), (1000, 1001),
+                                      (4108, 4109), (14336, 2), (65540, 3)])
+def test_strided_sum_is_torch_cpu_order(n, stride):
+    """The diagonal reduction of inverse_factor's damping (hi2/hessian.py:75) is torch's
+    CPU sum of a strided vector: pinned against torch itself."""
+    rng = np.random.default_rng(n)
+    x = (rng.standard_normal((n - 1) * stride + 1) * np.exp(2 * rng.standard_normal(1))).astype(np.float32)
+    want = torch.as_strided(torch.from_numpy(x), (n,), (stride,)).sum().item()
+    assert oracle.torch_sum_strided(x, n, stride) == np.float32(want)
+
+
+@pytest.mark.parametrize("k", [16, 100, 1000, 4108])
+def test_damp_lambda_is_the_reference_expression(k):
+    # hi2/hessian.py:75-79: mean = hs.diagonal().mean().clamp_min(1e-12); damp*mean*10**a
+    rng = np.random.default_rng(k)
+    hs = (rng.standard_normal((k, k)) * 0.01).astype(np.float32)
+    hs[np.diag_indices(k)] = (rng.standard_normal(k) * np.exp(rng.standard_normal(k))) ** 2
+    mean = torch.from_numpy(hs).diagonal().mean().clamp_min(1e-12)
+    for a in (0, 1, 3, 5):
+        want = (0.01 * mean * 10**a).item()
+        assert oracle.damp_lambda(hs, 0.01, a) == np.float32(want), a
+
+
 # ---- fit_ladder / params ---------------------------------------------------------------
 @pytest.mark.parametrize("case", list(fit_cases()), ids=lambda c: f"n{c[0]}_b{c[1]}_{c[2]}")
 def test_fit_ladder_equals_reference_golden(case):
