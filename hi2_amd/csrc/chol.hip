@@ -128,6 +128,69 @@ __global__ __launch_bounds__(256) void tri_gemm_kernel(GemmArgs g, int64_t tm, i
   });
 }
 
+// The same product with 128-tiles on bf16 MFMA through the three-way split (fp32
+// accuracy, not bit-identical to the fp32 MFMA path).
+template <int AMODE, int BMODE, bool TB, bool CLOW>
+__global__ __launch_bounds__(256) void tri3_gemm_kernel(GemmArgs g, int64_t tm, int64_t tn,
+                                                        int super, MgSched sched) {
+  constexpr int T = MG_T, NA = 2;
+  __shared__ Mg3Smem sm;
+  int64_t tr, tc;
+  if (sched.per_xcd > 0) {
+    if (!mg_sched_tile<CLOW>(blockIdx.x, sched, tm, tn, tr, tc)) return;
+  } else if (super) {
+    if (!mg_super_tile<tri_order<AMODE, BMODE>(), CLOW>(blockIdx.x, tm, tn, tr, tc)) return;
+  } else {
+    const int64_t t = xcd_tile(blockIdx.x, tm * tn);
+    if (t < 0) return;
+    tr = t / tn;
+    tc = t % tn;
+  }
+  const int64_t r0 = tr * T, c0 = tc * T;
+  if (CLOW && c0 > r0 + T - 1) return;
+  int64_t kbeg, kend;
+  tri_krange<AMODE, BMODE>(r0, c0, T, g.Kd, kbeg, kend);
+  f32x16 acc[NA][NA];
+  mg_zero<NA>(acc);
+  using AMask = typename std::conditional<AMODE == 1, MaskLower, NoMask>::type;
+  Rows3Loader<AMask> al{RowsLoader<AMask, T>{g.A, g.lda, g.M, kend, AMask{}}};
+  if (TB) {
+    using BMask = typename std::conditional<
+        BMODE == 1, MaskUpper, typename std::conditional<BMODE == 2, MaskLower, NoMask>::type>::type;
+    Rows3Loader<BMask> bl{RowsLoader<BMask, T>{g.B, g.ldb, g.N, kend, BMask{}}};
+    mg3_mainloop(acc, sm, al, bl, r0, c0, kbeg, kend);
+  } else {
+    using BMask = typename std::conditional<
+        BMODE == 1, MaskLower, typename std::conditional<BMODE == 2, MaskUpper, NoMask>::type>::type;
+    Cols3Loader<BMask> bl{g.B, g.ldb, g.N, kend, BMask{}};
+    mg3_mainloop(acc, sm, al, bl, r0, c0, kbeg, kend);
+  }
+  const CTile<T> ct(g.C, g.ldc, g.M, g.N, r0, c0);
+  f32x16 cv[NA][NA];
+  if (g.beta != 0.0f) {
+    ct.load(cv);
+#pragma unroll
+    for (int a = 0; a < NA; ++a)
+#pragma unroll
+      for (int b = 0; b < NA; ++b)
+#pragma unroll
+        for (int j = 0; j < 16; ++j) cv[a][b][j] = cv[a][b][j] + g.alpha * acc[a][b][j];
+  } else {
+#pragma unroll
+    for (int a = 0; a < NA; ++a)
+#pragma unroll
+      for (int b = 0; b < NA; ++b)
+#pragma unroll
+        for (int j = 0; j < 16; ++j) cv[a][b][j] = g.alpha * acc[a][b][j];
+  }
+  ct.store(cv, [&](int a, int j, int b) {
+    return !CLOW || c0 + mg_col<T>(b) <= r0 + mg_row<T>(a, j);
+  });
+}
+
+// 0: fp32 MFMA; 1: bf16 MFMA through the three-way split (128-tile grids)
+static int g_tri_split = 1;
+
 template <int AMODE, int BMODE, bool TB, bool CLOW>
 int tri_gemm(const GemmArgs& a, hipStream_t s) {
   if (a.M <= 0 || a.N <= 0) return HI2X_OK;
@@ -164,6 +227,11 @@ int tri_gemm(const GemmArgs& a, hipStream_t s) {
   const int64_t grid = sched.per_xcd > 0 ? mg_sched_grid(sched)
                        : super            ? mg_super_grid(tm, tn, CLOW)
                                           : (ntiles + 7) / 8 * 8;
+  if (g_tri_split) {
+    hipLaunchKernelGGL((tri3_gemm_kernel<AMODE, BMODE, TB, CLOW>), dim3((unsigned)grid),
+                       dim3(256), 0, s, a, tm, tn, super, sched);
+    return launch_status("tri3_gemm_kernel");
+  }
   hipLaunchKernelGGL((tri_gemm_kernel<AMODE, BMODE, TB, CLOW, MG_T>), dim3((unsigned)grid),
                      dim3(256), 0, s, a, tm, tn, super, sched);
   return launch_status("tri_gemm_kernel");
