@@ -28,6 +28,11 @@ namespace {
 
 constexpr int NB = 128;  // leaf size
 
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc_u16(const uint16_t* base, int64_t n) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(base), (short)0, (int)(n * 2),
+                                           0x00020000);
+}
+
 // ---- triangular GEMM ----------------------------------------------------------------
 // C[M, N] = alpha * A[M, Kd] * op(B) + beta * C (beta 0 or 1).
 // AMODE 1: A lower triangular.  BMODE 1 / 2: op(B) lower / upper triangular.
@@ -186,6 +191,268 @@ __global__ __launch_bounds__(256) void tri3_gemm_kernel(GemmArgs g, int64_t tm, 
   ct.store(cv, [&](int a, int j, int b) {
     return !CLOW || c0 + mg_col<T>(b) <= r0 + mg_row<T>(a, j);
   });
+}
+
+// ---- products of the big levels on bf16 MFMA through a three-way split ---------------
+// Every fp32 operand x is written once, before the product, as three bf16 planes
+// x1 = bf16(x), x2 = bf16(x - x1), x3 = bf16(x - x1 - x2) (the differences are exact in
+// fp32; x = x1 + x2 + x3 to within 2^-27 |x|), laid out [row][k] with k contiguous
+// (a transposed copy where the product needs one) and the operand's structural zeros
+// written as zeros.  The product keeps the six terms x_i y_j with i + j <= 4 (the dropped
+// ones are below 2^-26 |x y|); bf16 products are exact and v_mfma_f32_32x32x16_bf16
+// accumulates in fp32: six MFMAs of 32 cycles cover 16 k where the fp32 MFMA needs
+// eight of 64, with the rounding of an fp32 GEMM (not bit-identical to one).
+
+// out[p][r][k] (planes of R x Kp bf16) from X: !trans: x = X[r][k] (X is R x Kk, ld ldx),
+// trans: x = X[k][r] (X is Kk x R).  mask 1 keeps k <= r, 2 keeps k >= r; k >= Kk and
+// masked elements are zero.  A workgroup converts a 64 x 64 block through LDS: 4 threads
+// per output row, 16 consecutive k each.
+__global__ __launch_bounds__(256) void split3_kernel(const float* __restrict__ X, int64_t ldx,
+                                                     int64_t R, int64_t Kk, int trans, int mask,
+                                                     uint16_t* __restrict__ out, int64_t Kp) {
+  __shared__ float t[64][65];
+  const int64_t r0 = (int64_t)blockIdx.y * 64, k0 = (int64_t)blockIdx.x * 64;
+  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+  // input block: rows of X are contiguous along k (!trans) or along r (trans)
+  const int64_t xr0 = trans ? k0 : r0, xc0 = trans ? r0 : k0;
+  const int64_t xrows = trans ? Kk : R, xcols = trans ? R : Kk;
+  const int rows = (int)((xrows - xr0 < 64) ? (xrows - xr0 > 0 ? xrows - xr0 : 0) : 64);
+  const int cols = (int)((xcols - xc0 < 64) ? (xcols - xc0 > 0 ? xcols - xc0 : 0) : 64);
+  const __amdgpu_buffer_rsrc_t rs =
+      mg_rsrc(X + xr0 * ldx + xc0, rows > 0 && cols > 0 ? (int64_t)(rows - 1) * ldx + cols : 0);
+#pragma unroll
+  for (int q = 0; q < 16; ++q) {
+    const int y = ty + 4 * q;
+    const uint32_t off = (y < rows && tx < cols) ? (uint32_t)(((int64_t)y * ldx + tx) * 4) : MG_OOB;
+    t[y][tx] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, (int)off, 0, 0));
+  }
+  __syncthreads();
+  const int orow = threadIdx.x >> 2, kq = threadIdx.x & 3;  // output row, 16-k quarter
+  const int64_t r = r0 + orow;
+  if (r >= R) return;
+  mg_u16x8 p1[2], p2[2], p3[2];
+#pragma unroll
+  for (int e = 0; e < 16; ++e) {
+    const int kk = 16 * kq + e;
+    const int64_t k = k0 + kk;
+    float x = trans ? t[kk][orow] : t[orow][kk];
+    const bool keep = mask == 1 ? k <= r : (mask == 2 ? k >= r : true);
+    x = keep ? x : 0.0f;
+    const __bf16 b1 = (__bf16)x;
+    const float e1 = x - (float)b1;
+    const __bf16 b2 = (__bf16)e1;
+    const float e2 = e1 - (float)b2;
+    const __bf16 b3 = (__bf16)e2;
+    p1[e >> 3][e & 7] = __builtin_bit_cast(unsigned short, b1);
+    p2[e >> 3][e & 7] = __builtin_bit_cast(unsigned short, b2);
+    p3[e >> 3][e & 7] = __builtin_bit_cast(unsigned short, b3);
+  }
+  const int64_t kb = k0 + 16 * kq;
+  if (kb >= Kp) return;
+  const int64_t plane = R * Kp;
+  uint16_t* o = out + r * Kp + kb;
+#pragma unroll
+  for (int g = 0; g < 2; ++g) {
+    *reinterpret_cast<mg_u16x8*>(o + 8 * g) = p1[g];
+    *reinterpret_cast<mg_u16x8*>(o + plane + 8 * g) = p2[g];
+    *reinterpret_cast<mg_u16x8*>(o + 2 * plane + 8 * g) = p3[g];
+  }
+}
+
+// C[M, N] = alpha * A B^T + beta * C over k in [kbeg, kend) of each 128 x 128 output tile
+// (tri_krange), A and B given as split planes [3][rows][Kp].  Workgroup: 4 waves of
+// 64 x 64 (2 x 2 accumulators).  Stages of 32 k go from L2 straight into LDS through a
+// ring of three (prefetch distance two): each load instruction of a wave writes 1 KB
+// = 16 rows x 4 16-byte slots of one plane, slot q of row r holding piece
+// q ^ ((r / 4) % 4) so that the MFMA operand reads are free of bank conflicts.
+struct G3Args {
+  const uint16_t* A;
+  const uint16_t* B;
+  float* C;
+  int64_t M, N, Kd, Kp, ldc;
+  float alpha, beta;
+};
+constexpr int G3_KC = 32;                 // k per stage
+constexpr int G3_NB = 3;                  // stages in the ring
+constexpr int G3_PL = MG_T * G3_KC;       // bf16 per plane per stage
+constexpr int G3_PER_STAGE = 12;          // load instructions per wave and stage (2 x 3 x 8 / 4)
+
+__device__ __forceinline__ void g3_dma16(__amdgpu_buffer_rsrc_t rs, uint32_t voff, void* lds) {
+  const uint32_t la = __builtin_amdgcn_readfirstlane(
+      (uint32_t)(size_t)(__attribute__((address_space(3))) void*)lds);
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+  // as inline assembly: the compiler would otherwise take the asynchronous LDS write for
+  // an alias of every later LDS read and wait for all loads in flight before each one
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+               :
+               : "s"(la), "v"(voff), "s"(rs)
+               : "m0");
+#pragma clang diagnostic pop
+}
+
+constexpr int g3_waitcnt(int vm, int lgkm) {
+  return (vm & 15) | ((vm >> 4) << 14) | (7 << 4) | (lgkm << 8);
+}
+
+template <int AMODE, int BMODE, bool CLOW>
+__global__ __launch_bounds__(256) void gemm3_kernel(G3Args g, int64_t tm, int64_t tn,
+                                                    MgSched sched) {
+  __shared__ __attribute__((aligned(1024))) uint16_t SA[G3_NB][3][G3_PL];
+  __shared__ __attribute__((aligned(1024))) uint16_t SB[G3_NB][3][G3_PL];
+  int64_t tr, tc;
+  if (sched.per_xcd > 0) {
+    if (!mg_sched_tile<CLOW>(blockIdx.x, sched, tm, tn, tr, tc)) return;
+  } else {
+    const int64_t t = xcd_tile(blockIdx.x, tm * tn);
+    if (t < 0) return;
+    tr = t / tn;
+    tc = t % tn;
+  }
+  const int64_t r0 = tr * MG_T, c0 = tc * MG_T;
+  if (CLOW && c0 > r0 + MG_T - 1) return;
+  int64_t kbeg, kend;
+  tri_krange<AMODE, BMODE>(r0, c0, MG_T, g.Kd, kbeg, kend);
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wr = wave >> 1, wcn = wave & 1;
+  const int wv = __builtin_amdgcn_readfirstlane(wave);
+  f32x16 acc[2][2];
+  mg_zero<2>(acc);
+  // plane p of the operand tile rows: a buffer per plane that ends at the last valid row
+  const int rowsA = (int)((g.M - r0 < MG_T) ? g.M - r0 : MG_T);
+  const int rowsB = (int)((g.N - c0 < MG_T) ? g.N - c0 : MG_T);
+  const int64_t plA = g.M * g.Kp, plB = g.N * g.Kp;
+  // load j (0..11) of a stage: operand j / 6, plane (j % 6) / 2, row group 2 wv + j % 2
+  const int prow = lane >> 2, piece = (lane & 3) ^ ((lane >> 4) & 3);
+  auto dma_one = [&](int j, int64_t k0, int buf, bool live) {
+    const int opd = j / 6, pl = (j % 6) >> 1, rg = 2 * wv + (j & 1);
+    const int row = 16 * rg + prow;
+    const uint16_t* base = opd == 0 ? g.A + pl * plA + r0 * g.Kp : g.B + pl * plB + c0 * g.Kp;
+    const int rows = opd == 0 ? rowsA : rowsB;
+    const __amdgpu_buffer_rsrc_t rs = rsrc_u16(base, (int64_t)rows * g.Kp);
+    const uint32_t o = (uint32_t)(((int64_t)row * g.Kp + k0) * 2 + 16 * piece);
+    uint16_t* dst = opd == 0 ? &SA[buf][pl][rg * 16 * G3_KC] : &SB[buf][pl][rg * 16 * G3_KC];
+    g3_dma16(rs, (live && row < rows) ? o : MG_OOB, dst);
+  };
+  auto dma = [&](int64_t k0, int buf, bool live) {
+#pragma unroll
+    for (int j = 0; j < G3_PER_STAGE; ++j) dma_one(j, k0, buf, live);
+  };
+  // operand reads: rows wr * 64 + 32 t + lane % 32 (A) / wcn * 64 + ... (B); piece 2 kk + h
+  const int rA = wr * 64 + (lane & 31), rB = wcn * 64 + (lane & 31);
+  const int sw = (lane >> 2) & 3, h = lane >> 5;
+  const int so0 = 8 * (h ^ sw), so1 = 8 * ((2 + h) ^ sw);
+  typedef mg_bf16x8 V;
+  V a0[3][2], b0[3][2], a1[3][2], b1[3][2];  // [plane][tile], k-step sets 0 and 1
+  auto read = [&](V (&av)[3][2], V (&bv)[3][2], int buf, int so) {
+#pragma unroll
+    for (int pl = 0; pl < 3; ++pl)
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        av[pl][t] = __builtin_bit_cast(V, *reinterpret_cast<const mg_u16x8*>(&SA[buf][pl][(rA + 32 * t) * G3_KC + so]));
+        bv[pl][t] = __builtin_bit_cast(V, *reinterpret_cast<const mg_u16x8*>(&SB[buf][pl][(rB + 32 * t) * G3_KC + so]));
+      }
+  };
+  // the six products of tile (a, b), small terms first
+#define G3_MMA(AV, BV, a, b)                                                                     \
+  acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(AV[2][a], BV[0][b], acc[a][b], 0, 0, 0);   \
+  acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(AV[1][a], BV[1][b], acc[a][b], 0, 0, 0);   \
+  acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(AV[0][a], BV[2][b], acc[a][b], 0, 0, 0);   \
+  acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(AV[1][a], BV[0][b], acc[a][b], 0, 0, 0);   \
+  acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(AV[0][a], BV[1][b], acc[a][b], 0, 0, 0);   \
+  acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(AV[0][a], BV[0][b], acc[a][b], 0, 0, 0);
+  auto sync = [&]() {
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_barrier();
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  };
+  const int nst = kend > kbeg ? (int)((kend - kbeg + G3_KC - 1) / G3_KC) : 0;
+  if (nst > 0) {
+#pragma unroll
+    for (int p = 0; p < G3_NB; ++p) dma(kbeg + (int64_t)p * G3_KC, p, p < nst);
+    __builtin_amdgcn_s_waitcnt(g3_waitcnt(2 * G3_PER_STAGE, 15));  // stage 0 landed
+    sync();
+    read(a0, b0, 0, so0);
+  }
+  // every stage issues G3_PER_STAGE loads (past the end they read nothing), so "stage
+  // st + 1 has landed" is "at most stage st + 2's loads outstanding"; the loop body has
+  // no branch around the MFMAs
+  for (int st = 0; st < nst; ++st) {
+    const int cb = st % G3_NB, nb = (st + 1) % G3_NB;
+    read(a1, b1, cb, so1);
+    __builtin_amdgcn_sched_barrier(0);
+    G3_MMA(a0, b0, 0, 0) G3_MMA(a0, b0, 0, 1) G3_MMA(a0, b0, 1, 0) G3_MMA(a0, b0, 1, 1)
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_waitcnt(g3_waitcnt(G3_PER_STAGE, 0));
+    sync();  // stage st + 1 landed everywhere; buffer cb is read by no wave any more
+    read(a0, b0, nb, so0);
+    __builtin_amdgcn_sched_barrier(0);
+    // stage st + 3 into buffer cb: two loads after each tile's six MFMAs
+    const int64_t kn = kbeg + (int64_t)(st + G3_NB) * G3_KC;
+    const bool live = st + G3_NB < nst;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int a = q >> 1, b = q & 1;
+      G3_MMA(a1, b1, a, b)
+      dma_one(3 * q, kn, cb, live);
+      dma_one(3 * q + 1, kn, cb, live);
+      dma_one(3 * q + 2, kn, cb, live);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+#undef G3_MMA
+  const CTile<MG_T> ct(g.C, g.ldc, g.M, g.N, r0, c0);
+  f32x16 cv[2][2];
+  if (g.beta != 0.0f) {
+    ct.load(cv);
+#pragma unroll
+    for (int a = 0; a < 2; ++a)
+#pragma unroll
+      for (int b = 0; b < 2; ++b)
+#pragma unroll
+        for (int j = 0; j < 16; ++j) cv[a][b][j] = cv[a][b][j] + g.alpha * acc[a][b][j];
+  } else {
+#pragma unroll
+    for (int a = 0; a < 2; ++a)
+#pragma unroll
+      for (int b = 0; b < 2; ++b)
+#pragma unroll
+        for (int j = 0; j < 16; ++j) cv[a][b][j] = g.alpha * acc[a][b][j];
+  }
+  ct.store(cv, [&](int a, int j, int b) {
+    return !CLOW || c0 + mg_col<MG_T>(b) <= r0 + mg_row<MG_T>(a, j);
+  });
+  __syncthreads();  // no wave leaves while loads it issued may still write LDS
+}
+
+int split3(const float* X, int64_t ldx, int64_t R, int64_t Kk, int trans, int mask,
+           uint16_t* out, int64_t Kp, hipStream_t s) {
+  const dim3 grid((unsigned)((Kp + 63) / 64), (unsigned)((R + 63) / 64));
+  hipLaunchKernelGGL(split3_kernel, grid, dim3(256), 0, s, X, ldx, R, Kk, trans, mask, out, Kp);
+  return launch_status("split3_kernel");
+}
+
+template <int AMODE, int BMODE, bool CLOW>
+int gemm3(const G3Args& a, hipStream_t s) {
+  if (a.M <= 0 || a.N <= 0) return HI2X_OK;
+  const int64_t tm = (a.M + MG_T - 1) / MG_T, tn = (a.N + MG_T - 1) / MG_T;
+  LaunchTimer timer(HI2X_TIME_CHOL_GEMM, (double)a.M * a.N * a.Kd, s);
+  MgSched sched = mg_balance(tm, tn, [&](int64_t sr, int64_t sc) {
+    double w = 0.0;
+    for (int64_t i = 0; i < MG_SUP; ++i)
+      for (int64_t j = 0; j < MG_SUP; ++j) {
+        const int64_t tr = sr * MG_SUP + i, tc = sc * MG_SUP + j;
+        if (tr >= tm || tc >= tn || (CLOW && tc > tr)) continue;
+        int64_t kb, ke;
+        tri_krange<AMODE, BMODE>(tr * MG_T, tc * MG_T, MG_T, a.Kd, kb, ke);
+        w += (double)std::max<int64_t>(0, ke - kb) + 2.0 * G3_KC;
+      }
+    return w;
+  });
+  const int64_t grid = sched.per_xcd > 0 ? mg_sched_grid(sched) : (tm * tn + 7) / 8 * 8;
+  hipLaunchKernelGGL((gemm3_kernel<AMODE, BMODE, CLOW>), dim3((unsigned)grid), dim3(256), 0, s,
+                     a, tm, tn, sched);
+  return launch_status("gemm3_kernel");
 }
 
 // 0: fp32 MFMA; 1: bf16 MFMA through the three-way split (128-tile grids)
@@ -669,6 +936,7 @@ __global__ void status_init_kernel(int* __restrict__ status, int v) { *status = 
 struct Plan {
   std::vector<int64_t> t1_off;  // per depth offset into the workspace
   int64_t t2_off = 0, total = 0;
+  int64_t pa_off = 0, pb_off = 0;  // the two split-plane buffers (offsets in floats)
 };
 
 void plan_sizes(int64_t m, int depth, std::vector<int64_t>& t1, int64_t& t2) {
@@ -690,6 +958,31 @@ struct Ctx {
   int* status;
   hipStream_t s;
 };
+
+// op(B) mask of a TB / !TB product in split coordinates (row = output column j, k)
+constexpr int split_mask_b(int bmode) { return bmode == 1 ? 2 : (bmode == 2 ? 1 : 0); }
+
+// One product of the recursion: the big grids through the split planes, the small ones
+// on the fp32 MFMA GEMM.
+template <int AMODE, int BMODE, bool TB, bool CLOW>
+int product(const Ctx& c, const GemmArgs& a) {
+  const int64_t tm = (a.M + MG_T - 1) / MG_T, tn = (a.N + MG_T - 1) / MG_T;
+  const int64_t ntiles = tm * tn;
+  if (!g_tri_split || (CLOW ? ntiles / 2 : ntiles) < 128) return tri_gemm<AMODE, BMODE, TB, CLOW>(a, c.s);
+  const int64_t Kp = (a.Kd + G3_KC - 1) / G3_KC * G3_KC;
+  uint16_t* pa = reinterpret_cast<uint16_t*>(c.ws + c.plan->pa_off);
+  uint16_t* pb = reinterpret_cast<uint16_t*>(c.ws + c.plan->pb_off);
+  int rc = split3(a.A, a.lda, a.M, a.Kd, 0, AMODE == 1 ? 1 : 0, pa, Kp, c.s);
+  if (rc) return rc;
+  const uint16_t* bp = pa;
+  if (!(TB && a.B == a.A && a.ldb == a.lda && a.N == a.M && AMODE == 0 && BMODE == 0)) {
+    rc = split3(a.B, a.ldb, a.N, a.Kd, TB ? 0 : 1, split_mask_b(BMODE), pb, Kp, c.s);
+    if (rc) return rc;
+    bp = pb;
+  }
+  return gemm3<AMODE, BMODE, CLOW>(G3Args{pa, bp, a.C, a.M, a.N, a.Kd, Kp, a.ldc, a.alpha, a.beta},
+                                   c.s);
+}
 
 int inv_chol(const Ctx& c, int64_t r0, int64_t m, int depth) {
   const int64_t K = c.K;
@@ -714,18 +1007,18 @@ int inv_chol(const Ctx& c, int64_t r0, int64_t m, int depth) {
   int rc = inv_chol(c, r0, m1, depth + 1);
   if (rc) return rc;
   // T1 = A21 A11^T  (op(B) = A11^T upper)
-  rc = tri_gemm<0, 2, true, false>(GemmArgs{A21, A11, T1, m2, m1, m1, K, K, m1, 1.0f, 0.0f}, c.s);
+  rc = product<0, 2, true, false>(c, GemmArgs{A21, A11, T1, m2, m1, m1, K, K, m1, 1.0f, 0.0f});
   if (rc) return rc;
   // A22 -= T1 T1^T  (lower triangle)
-  rc = tri_gemm<0, 0, true, true>(GemmArgs{T1, T1, A22, m2, m2, m1, m1, m1, K, -1.0f, 1.0f}, c.s);
+  rc = product<0, 0, true, true>(c, GemmArgs{T1, T1, A22, m2, m2, m1, m1, m1, K, -1.0f, 1.0f});
   if (rc) return rc;
   rc = inv_chol(c, r0 + m1, m2, depth + 1);
   if (rc) return rc;
   // T2 = T1 A11  (op(B) = A11 lower)
-  rc = tri_gemm<0, 1, false, false>(GemmArgs{T1, A11, T2, m2, m1, m1, m1, K, m1, 1.0f, 0.0f}, c.s);
+  rc = product<0, 1, false, false>(c, GemmArgs{T1, A11, T2, m2, m1, m1, m1, K, m1, 1.0f, 0.0f});
   if (rc) return rc;
   // A21 = -A22 T2  (A = A22 lower)
-  return tri_gemm<1, 0, false, false>(GemmArgs{A22, T2, A21, m2, m1, m2, K, m1, K, -1.0f, 0.0f}, c.s);
+  return product<1, 0, false, false>(c, GemmArgs{A22, T2, A21, m2, m1, m2, K, m1, K, -1.0f, 0.0f});
 }
 
 }  // namespace
@@ -746,7 +1039,20 @@ static Plan make_plan(int64_t k) {
     off += (sz + 63) / 64 * 64;
   }
   plan.t2_off = off;
-  plan.total = off + (t2 + 63) / 64 * 64;
+  off += (t2 + 63) / 64 * 64;
+  // split planes: 3 x rows x Kp bf16 for the largest operand of the top-level products
+  int64_t m1 = 0;
+  if (k > NB) {
+    const int64_t nbk = (k + NB - 1) / NB;
+    m1 = ((nbk + 1) / 2) * NB;
+  }
+  const int64_t kp = (m1 + G3_KC - 1) / G3_KC * G3_KC;
+  const int64_t plane_floats = (3 * m1 * kp * 2 + 255) / 256 * 64;  // bytes / 4, 256-aligned
+  plan.pa_off = off;
+  off += plane_floats;
+  plan.pb_off = off;
+  off += plane_floats;
+  plan.total = off;
   return plan;
 }
 static int64_t ws_floats(const Plan& p) { return p.total + 64; }
