@@ -17,6 +17,8 @@
 //     T2  = T1 A11                  (= L21 L11^-1)
 //     A21 = -A22 T2                 (= -L22^-1 L21 L11^-1, the lower-left block of L^-1)
 //   every product on the fp32 MFMA GEMM of mfma_gemm.h with triangular operands masked.
+#include <cstdlib>
+#include <cstring>
 #include <type_traits>
 #include <utility>
 #include <vector>
@@ -109,66 +111,6 @@ __global__ __launch_bounds__(256) void tri_gemm_kernel(GemmArgs g, int64_t tm, i
         BMODE == 1, MaskLower, typename std::conditional<BMODE == 2, MaskUpper, NoMask>::type>::type;
     ColsLoader<BMask, T> bl{g.B, g.ldb, g.N, kend, BMask{}};
     mg_mainloop<NA, T>(acc, sm, al, bl, r0, c0, kbeg, kend);
-  }
-  const CTile<T> ct(g.C, g.ldc, g.M, g.N, r0, c0);
-  f32x16 cv[NA][NA];
-  if (g.beta != 0.0f) {
-    ct.load(cv);
-#pragma unroll
-    for (int a = 0; a < NA; ++a)
-#pragma unroll
-      for (int b = 0; b < NA; ++b)
-#pragma unroll
-        for (int j = 0; j < 16; ++j) cv[a][b][j] = cv[a][b][j] + g.alpha * acc[a][b][j];
-  } else {
-#pragma unroll
-    for (int a = 0; a < NA; ++a)
-#pragma unroll
-      for (int b = 0; b < NA; ++b)
-#pragma unroll
-        for (int j = 0; j < 16; ++j) cv[a][b][j] = g.alpha * acc[a][b][j];
-  }
-  ct.store(cv, [&](int a, int j, int b) {
-    return !CLOW || c0 + mg_col<T>(b) <= r0 + mg_row<T>(a, j);
-  });
-}
-
-// The same product with 128-tiles on bf16 MFMA through the three-way split (fp32
-// accuracy, not bit-identical to the fp32 MFMA path).
-template <int AMODE, int BMODE, bool TB, bool CLOW>
-__global__ __launch_bounds__(256) void tri3_gemm_kernel(GemmArgs g, int64_t tm, int64_t tn,
-                                                        int super, MgSched sched) {
-  constexpr int T = MG_T, NA = 2;
-  __shared__ Mg3Smem sm;
-  int64_t tr, tc;
-  if (sched.per_xcd > 0) {
-    if (!mg_sched_tile<CLOW>(blockIdx.x, sched, tm, tn, tr, tc)) return;
-  } else if (super) {
-    if (!mg_super_tile<tri_order<AMODE, BMODE>(), CLOW>(blockIdx.x, tm, tn, tr, tc)) return;
-  } else {
-    const int64_t t = xcd_tile(blockIdx.x, tm * tn);
-    if (t < 0) return;
-    tr = t / tn;
-    tc = t % tn;
-  }
-  const int64_t r0 = tr * T, c0 = tc * T;
-  if (CLOW && c0 > r0 + T - 1) return;
-  int64_t kbeg, kend;
-  tri_krange<AMODE, BMODE>(r0, c0, T, g.Kd, kbeg, kend);
-  f32x16 acc[NA][NA];
-  mg_zero<NA>(acc);
-  using AMask = typename std::conditional<AMODE == 1, MaskLower, NoMask>::type;
-  Rows3Loader<AMask> al{RowsLoader<AMask, T>{g.A, g.lda, g.M, kend, AMask{}}};
-  if (TB) {
-    using BMask = typename std::conditional<
-        BMODE == 1, MaskUpper, typename std::conditional<BMODE == 2, MaskLower, NoMask>::type>::type;
-    Rows3Loader<BMask> bl{RowsLoader<BMask, T>{g.B, g.ldb, g.N, kend, BMask{}}};
-    mg3_mainloop(acc, sm, al, bl, r0, c0, kbeg, kend);
-  } else {
-    using BMask = typename std::conditional<
-        BMODE == 1, MaskLower, typename std::conditional<BMODE == 2, MaskUpper, NoMask>::type>::type;
-    Cols3Loader<BMask> bl{g.B, g.ldb, g.N, kend, BMask{}};
-    mg3_mainloop(acc, sm, al, bl, r0, c0, kbeg, kend);
   }
   const CTile<T> ct(g.C, g.ldc, g.M, g.N, r0, c0);
   f32x16 cv[NA][NA];
@@ -353,14 +295,14 @@ __global__ __launch_bounds__(256) void gemm3_kernel(G3Args g, int64_t tm, int64_
         bv[pl][t] = __builtin_bit_cast(V, *reinterpret_cast<const mg_u16x8*>(&SB[buf][pl][(rB + 32 * t) * G3_KC + so]));
       }
   };
-  // the six products of tile (a, b), small terms first
-#define G3_MMA(AV, BV, a, b)                                                                     \
-  acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(AV[2][a], BV[0][b], acc[a][b], 0, 0, 0);   \
-  acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(AV[1][a], BV[1][b], acc[a][b], 0, 0, 0);   \
-  acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(AV[0][a], BV[2][b], acc[a][b], 0, 0, 0);   \
-  acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(AV[1][a], BV[0][b], acc[a][b], 0, 0, 0);   \
-  acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(AV[0][a], BV[1][b], acc[a][b], 0, 0, 0);   \
-  acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(AV[0][a], BV[0][b], acc[a][b], 0, 0, 0);
+  // the six products of a k-step, small terms first (planes (2,0) (1,1) (0,2) (1,0) (0,1)
+  // (0,0)), each over the four tiles in turn so that consecutive MFMAs use different
+  // accumulators
+  constexpr int PA[6] = {2, 1, 0, 1, 0, 0}, PB[6] = {0, 1, 2, 0, 1, 0};
+#define G3_ONE(AV, BV, n)                                                                    \
+  acc[((n) & 3) >> 1][(n) & 1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(                     \
+      AV[PA[(n) >> 2]][((n) & 3) >> 1], BV[PB[(n) >> 2]][(n) & 1], acc[((n) & 3) >> 1][(n) & 1], \
+      0, 0, 0);
   auto sync = [&]() {
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
     __builtin_amdgcn_s_barrier();
@@ -381,26 +323,28 @@ __global__ __launch_bounds__(256) void gemm3_kernel(G3Args g, int64_t tm, int64_
     const int cb = st % G3_NB, nb = (st + 1) % G3_NB;
     read(a1, b1, cb, so1);
     __builtin_amdgcn_sched_barrier(0);
-    G3_MMA(a0, b0, 0, 0) G3_MMA(a0, b0, 0, 1) G3_MMA(a0, b0, 1, 0) G3_MMA(a0, b0, 1, 1)
+#pragma unroll
+    for (int n = 0; n < 24; ++n) {
+      G3_ONE(a0, b0, n)
+    }
     __builtin_amdgcn_sched_barrier(0);
     __builtin_amdgcn_s_waitcnt(g3_waitcnt(G3_PER_STAGE, 0));
     sync();  // stage st + 1 landed everywhere; buffer cb is read by no wave any more
     read(a0, b0, nb, so0);
     __builtin_amdgcn_sched_barrier(0);
-    // stage st + 3 into buffer cb: two loads after each tile's six MFMAs
+    // stage st + 3 into buffer cb: one load after every second MFMA
     const int64_t kn = kbeg + (int64_t)(st + G3_NB) * G3_KC;
     const bool live = st + G3_NB < nst;
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const int a = q >> 1, b = q & 1;
-      G3_MMA(a1, b1, a, b)
-      dma_one(3 * q, kn, cb, live);
-      dma_one(3 * q + 1, kn, cb, live);
-      dma_one(3 * q + 2, kn, cb, live);
-      __builtin_amdgcn_sched_barrier(0);
+    for (int n = 0; n < 24; ++n) {
+      G3_ONE(a1, b1, n)
+      if (n & 1) {
+        dma_one(n >> 1, kn, cb, live);
+        __builtin_amdgcn_sched_barrier(0);
+      }
     }
   }
-#undef G3_MMA
+#undef G3_ONE
   const CTile<MG_T> ct(g.C, g.ldc, g.M, g.N, r0, c0);
   f32x16 cv[2][2];
   if (g.beta != 0.0f) {
@@ -455,8 +399,15 @@ int gemm3(const G3Args& a, hipStream_t s) {
   return launch_status("gemm3_kernel");
 }
 
-// 0: fp32 MFMA; 1: bf16 MFMA through the three-way split (128-tile grids)
-static int g_tri_split = 1;
+// Products of the big grids: bf16 MFMA on split planes (default), or the fp32 MFMA GEMM
+// when HI2X_CHOL_FP32 is set to a nonzero value (read once per process).
+static bool chol_split() {
+  static const bool split = [] {
+    const char* e = getenv("HI2X_CHOL_FP32");
+    return !(e && *e && strcmp(e, "0") != 0);
+  }();
+  return split;
+}
 
 template <int AMODE, int BMODE, bool TB, bool CLOW>
 int tri_gemm(const GemmArgs& a, hipStream_t s) {
@@ -494,11 +445,6 @@ int tri_gemm(const GemmArgs& a, hipStream_t s) {
   const int64_t grid = sched.per_xcd > 0 ? mg_sched_grid(sched)
                        : super            ? mg_super_grid(tm, tn, CLOW)
                                           : (ntiles + 7) / 8 * 8;
-  if (g_tri_split) {
-    hipLaunchKernelGGL((tri3_gemm_kernel<AMODE, BMODE, TB, CLOW>), dim3((unsigned)grid),
-                       dim3(256), 0, s, a, tm, tn, super, sched);
-    return launch_status("tri3_gemm_kernel");
-  }
   hipLaunchKernelGGL((tri_gemm_kernel<AMODE, BMODE, TB, CLOW, MG_T>), dim3((unsigned)grid),
                      dim3(256), 0, s, a, tm, tn, super, sched);
   return launch_status("tri_gemm_kernel");
@@ -968,7 +914,8 @@ template <int AMODE, int BMODE, bool TB, bool CLOW>
 int product(const Ctx& c, const GemmArgs& a) {
   const int64_t tm = (a.M + MG_T - 1) / MG_T, tn = (a.N + MG_T - 1) / MG_T;
   const int64_t ntiles = tm * tn;
-  if (!g_tri_split || (CLOW ? ntiles / 2 : ntiles) < 128) return tri_gemm<AMODE, BMODE, TB, CLOW>(a, c.s);
+  if (!chol_split() || (CLOW ? ntiles / 2 : ntiles) < 128)
+    return tri_gemm<AMODE, BMODE, TB, CLOW>(a, c.s);
   const int64_t Kp = (a.Kd + G3_KC - 1) / G3_KC * G3_KC;
   uint16_t* pa = reinterpret_cast<uint16_t*>(c.ws + c.plan->pa_off);
   uint16_t* pb = reinterpret_cast<uint16_t*>(c.ws + c.plan->pb_off);

@@ -281,184 +281,8 @@ __device__ __forceinline__ void mg_mainloop_seg(f32x16 (&acc)[NA][NA], MgSmemT<T
   }
 }
 
-// ---- fp32 products on bf16 MFMA: three-way split ------------------------------------
-// Every fp32 operand x is staged as three bf16 pieces x1 = bf16(x), x2 = bf16(x - x1),
-// x3 = bf16(x - x1 - x2) (the differences are exact in fp32), so x = x1 + x2 + x3 to
-// within 2^-27 |x|.  A product keeps the six terms x_i y_j with i + j <= 4 (the dropped
-// ones are below 2^-26 |x y|); bf16 products are exact and v_mfma_f32_32x32x16_bf16
-// accumulates them in fp32.  Six 32x32x16 bf16 MFMAs cover 16 k in 192 cycles where the
-// fp32 MFMA needs 512: the rounding is that of an fp32 GEMM (not bit-identical to it).
-//
-// LDS per stage: 3 planes x 128 rows x 32 k of bf16 for each operand, rows of 64 bytes as
-// 4 slots of 8 k; slot q of row r holds the row's piece q ^ ((r / 4) % 4), so the 16
-// consecutive rows an MFMA operand read touches (same piece) hit 16 different 16-byte
-// bank groups.
 typedef __bf16 mg_bf16x8 __attribute__((ext_vector_type(8)));
 typedef unsigned short mg_u16x8 __attribute__((ext_vector_type(8)));
-constexpr int M3_KC = 32;                  // k per stage
-constexpr int M3_PLANE = MG_T * M3_KC;     // bf16 per plane and operand
-
-struct Mg3Smem {
-  uint16_t A[2][3][M3_PLANE];
-  uint16_t B[2][3][M3_PLANE];
-};
-
-__device__ __forceinline__ int m3_slot(int row, int piece) { return piece ^ ((row >> 2) & 3); }
-
-// 16 fp32 at k = 16 h .. 16 h + 15 of LDS row `row`: split and written to the 3 planes
-__device__ __forceinline__ void m3_put(uint16_t (*P)[M3_PLANE], int row, int h,
-                                       const float (&v)[16]) {
-  mg_u16x8 p1[2], p2[2], p3[2];
-#pragma unroll
-  for (int e = 0; e < 16; ++e) {
-    const float x = v[e];
-    const __bf16 b1 = (__bf16)x;
-    const float r1 = x - (float)b1;
-    const __bf16 b2 = (__bf16)r1;
-    const float r2 = r1 - (float)b2;
-    const __bf16 b3 = (__bf16)r2;
-    p1[e >> 3][e & 7] = __builtin_bit_cast(unsigned short, b1);
-    p2[e >> 3][e & 7] = __builtin_bit_cast(unsigned short, b2);
-    p3[e >> 3][e & 7] = __builtin_bit_cast(unsigned short, b3);
-  }
-#pragma unroll
-  for (int g = 0; g < 2; ++g) {
-    const int off = row * M3_KC + 8 * m3_slot(row, 2 * h + g);
-    *reinterpret_cast<mg_u16x8*>(&P[0][off]) = p1[g];
-    *reinterpret_cast<mg_u16x8*>(&P[1][off]) = p2[g];
-    *reinterpret_cast<mg_u16x8*>(&P[2][off]) = p3[g];
-  }
-}
-
-// Row-major operand X[r][k] as rows of the tile (A, or B of a transposed product):
-// thread t stages row t / 2, k = 16 (t % 2) .. + 15 (RowsLoader's 128-tile mapping).
-template <class Mask>
-struct Rows3Loader {
-  RowsLoader<Mask, MG_T> rl;
-  __device__ __forceinline__ void load(int64_t r0, int64_t k0, int tid, f32x4 (&st)[4]) const {
-    rl.load(r0, k0, tid, st);
-  }
-  __device__ __forceinline__ void put(uint16_t (*P)[M3_PLANE], int64_t r0, int64_t k0, int tid,
-                                      f32x4 (&st)[4]) const {
-    const int m = tid >> 1, h = tid & 1;
-    const int64_t kb = k0 + 16 * h;
-    float v[16];
-#pragma unroll
-    for (int e = 0; e < 16; ++e) {
-      const bool keep = kb + e < rl.kend && rl.mask.elem(r0 + m, kb + e);
-      v[e] = (Mask::kElem || k0 + M3_KC > rl.kend) ? (keep ? st[e >> 2][e & 3] : 0.0f)
-                                                   : st[e >> 2][e & 3];
-    }
-    m3_put(P, m, h, v);
-  }
-};
-
-// Row-major operand X[k][c] (c contiguous) as the B operand of a plain product: thread t
-// stages column t % 128, k = 16 (t / 128) .. + 15, one dword per k (a wave reads 64
-// consecutive columns of a row).  k >= kend reads zero; columns >= ncols feed only
-// output columns that are never stored.
-template <class Mask>
-struct Cols3Loader {
-  const float* p;
-  int64_t ld, ncols, kend;
-  Mask mask;
-  __device__ __forceinline__ void load(int64_t c0, int64_t k0, int tid, f32x4 (&st)[4]) const {
-    const int64_t kv = (kend - k0 < M3_KC) ? kend - k0 : M3_KC;
-    const __amdgpu_buffer_rsrc_t rs = mg_rsrc(p + k0 * ld + c0, (kv - 1) * ld + (ncols - c0));
-    const int c = tid & 127, h = tid >> 7;
-    uint32_t base = (uint32_t)(((int64_t)16 * h * ld + c) * 4);
-    asm volatile("" : "+v"(base));
-#pragma unroll
-    for (int e = 0; e < 16; ++e)
-      st[e >> 2][e & 3] = __builtin_bit_cast(
-          float, __builtin_amdgcn_raw_buffer_load_b32(rs, (int)(base + (uint32_t)(e * ld * 4)), 0, 0));
-  }
-  __device__ __forceinline__ void put(uint16_t (*P)[M3_PLANE], int64_t c0, int64_t k0, int tid,
-                                      f32x4 (&st)[4]) const {
-    const int c = tid & 127, h = tid >> 7;
-    const int64_t kb = k0 + 16 * h;
-    float v[16];
-#pragma unroll
-    for (int e = 0; e < 16; ++e) {
-      const bool keep = kb + e < kend && mask.elem(kb + e, c0 + c);
-      v[e] = keep ? st[e >> 2][e & 3] : 0.0f;
-    }
-    m3_put(P, c, h, v);
-  }
-};
-
-// the MFMAs of one stage (2 k-steps x 2 x 2 tiles x 6 products); the operands of k-step
-// 1 are read while those of k-step 0 are multiplied
-__device__ __forceinline__ void m3_stage(f32x16 (&acc)[2][2], const uint16_t (*A)[M3_PLANE],
-                                         const uint16_t (*B)[M3_PLANE], int wr, int wcn,
-                                         int lane) {
-  const int lr = lane & 31, h = lane >> 5, sw = (lane >> 2) & 3;
-  mg_bf16x8 av[2][3][2], bv[2][3][2];  // [set][plane][tile]
-  auto read = [&](int set, int kk) {
-    const int so = 8 * ((2 * kk + h) ^ sw);
-#pragma unroll
-    for (int pl = 0; pl < 3; ++pl)
-#pragma unroll
-      for (int t = 0; t < 2; ++t) {
-        av[set][pl][t] = __builtin_bit_cast(
-            mg_bf16x8, *reinterpret_cast<const mg_u16x8*>(&A[pl][(wr * 64 + 32 * t + lr) * M3_KC + so]));
-        bv[set][pl][t] = __builtin_bit_cast(
-            mg_bf16x8, *reinterpret_cast<const mg_u16x8*>(&B[pl][(wcn * 64 + 32 * t + lr) * M3_KC + so]));
-      }
-  };
-  read(0, 0);
-  read(1, 1);
-#pragma unroll
-  for (int kk = 0; kk < 2; ++kk) {
-#pragma unroll
-    for (int a = 0; a < 2; ++a)
-#pragma unroll
-      for (int b = 0; b < 2; ++b) {
-        // small terms first: (3,1) (2,2) (1,3) (2,1) (1,2) (1,1)
-        acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av[kk][2][a], bv[kk][0][b], acc[a][b], 0, 0, 0);
-        acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av[kk][1][a], bv[kk][1][b], acc[a][b], 0, 0, 0);
-        acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av[kk][0][a], bv[kk][2][b], acc[a][b], 0, 0, 0);
-        acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av[kk][1][a], bv[kk][0][b], acc[a][b], 0, 0, 0);
-        acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av[kk][0][a], bv[kk][1][b], acc[a][b], 0, 0, 0);
-        acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av[kk][0][a], bv[kk][0][b], acc[a][b], 0, 0, 0);
-      }
-  }
-}
-
-// acc += A[r0:r0+128, kbeg:kend] * op(B)[kbeg:kend, c0:c0+128] through the split; stages
-// of 32 k, the next one's global loads in flight while the current one is multiplied.
-template <class AL, class BL>
-__device__ __forceinline__ void mg3_mainloop(f32x16 (&acc)[2][2], Mg3Smem& sm, const AL& al,
-                                             const BL& bl, int64_t r0, int64_t c0,
-                                             int64_t kbeg, int64_t kend) {
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wr = wave >> 1, wcn = wave & 1;
-  if (kend <= kbeg) return;
-  const int nch = (int)((kend - kbeg + M3_KC - 1) / M3_KC);
-  f32x4 sa[4], sb[4];
-  al.load(r0, kbeg, tid, sa);
-  bl.load(c0, kbeg, tid, sb);
-  __syncthreads();  // the previous use of the LDS buffers is over
-  al.put(sm.A[0], r0, kbeg, tid, sa);
-  bl.put(sm.B[0], c0, kbeg, tid, sb);
-  __syncthreads();
-  for (int ch = 0; ch < nch; ++ch) {
-    const int buf = ch & 1;
-    const int64_t kn = kbeg + (int64_t)(ch + 1) * M3_KC;
-    const bool more = ch + 1 < nch;
-    if (more) {
-      al.load(r0, kn, tid, sa);
-      bl.load(c0, kn, tid, sb);
-    }
-    m3_stage(acc, sm.A[buf], sm.B[buf], wr, wcn, lane);
-    __builtin_amdgcn_sched_barrier(0);
-    if (more) {  // buffer buf ^ 1 was last read before the previous barrier
-      al.put(sm.A[buf ^ 1], r0, kn, tid, sa);
-      bl.put(sm.B[buf ^ 1], c0, kn, tid, sb);
-    }
-    __syncthreads();
-  }
-}
 
 // Row / column of accumulator register j of tile (a, b) for this lane, relative to the
 // workgroup tile origin.

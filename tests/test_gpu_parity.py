@@ -194,6 +194,29 @@ def test_fit_ladder_equals_oracle(dev, n, b, effort):
     assert np.array_equal(N(lo), lo_w) and np.array_equal(N(st), st_w)
 
 
+@pytest.mark.parametrize("n,b", [(4, 64), (16, 32), (256, 64)])
+def test_fit_ladder_ties_equal_oracle(dev, n, b):
+    """Weights on the midpoints between ladder levels: (w - lo) / step lands on (or next to)
+    half-integers for the first grid candidates, where rounding the quotient to a code
+    must follow the IEEE division exactly (the kernel's reciprocal shortcut falls back to
+    the division there)."""
+    from hi2_amd.encode import fit_ladder
+
+    rng = np.random.default_rng(n * b)
+    rows, nb = 64, 640 // b
+    h = np.float32(2.0) ** rng.integers(-8, 3, (rows, nb, 1)).astype(np.float32)
+    k = rng.integers(0, n - 1, (rows, nb, b)).astype(np.float32)
+    wb = ((k + np.float32(0.5)) * h).astype(np.float32)
+    wb[:, :, 0] = 0.0                        # lo = 0 on the first candidate
+    wb[:, :, 1] = np.float32(n - 1) * h[:, :, 0]  # span = (n - 1) h: step = h
+    wb[::3] += rng.standard_normal(wb[::3].shape).astype(np.float32) * np.float32(1e-6)
+    db = (rng.random((1, nb, b)) + 0.5).astype(np.float32)
+    for effort in ("fast", "normal"):
+        lo_w, st_w = oracle.fit_ladder(wb, db, n, effort)
+        lo, st = fit_ladder(T(wb, dev), T(db, dev), n, effort)
+        assert np.array_equal(N(lo), lo_w) and np.array_equal(N(st), st_w), effort
+
+
 def test_params_equal_oracle(dev):
     from hi2_amd.encode import params_decoded, quantize_params
     from hi2_amd.format import decode_params
