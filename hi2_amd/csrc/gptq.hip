@@ -27,12 +27,14 @@ namespace {
 //
 // Step i (fully unrolled): every lane runs the rounding chain on its own column m=i/16;
 // only lane q = i%16 owns column i (its U value of row i is then U[i][i]), so its error e
-// is broadcast to the row with DPP row_newbcast, recorded by the owner, and the row
-// applies w[c] -= e * U[i][c] to the columns it holds.  Columns <= i of the other lanes
-// are dead (already rounded), so updating them is harmless.  Every product and
-// difference is rounded separately (-ffp-contract=off), division is IEEE, rounding to an
-// integer is half-to-even, and every column receives its updates in step order: the
-// codes, errors and compensated values are bit-identical to the reference loop.
+// is broadcast to the row with DPP row_newbcast, and the row applies
+// w[c] -= e * U[i][c] to the columns it holds.  Columns <= i of the other lanes are dead
+// (already rounded), so updating them is harmless.  The owner keeps e, the code and the
+// rounded-from value of its column in registers (selects, no branch); they are written
+// after the loop.  Every product and difference is rounded separately
+// (-ffp-contract=off), division is IEEE, rounding to an integer is half-to-even, and
+// every column receives its updates in step order: the codes, errors and compensated
+// values are bit-identical to the reference loop.
 // ---------------------------------------------------------------------------------
 constexpr int LMAX = 128;
 constexpr int QL = 16;                // lanes per row
@@ -53,20 +55,21 @@ __device__ __forceinline__ float row_bcast(float v) {  // lane S of each 16-lane
 }
 
 // Register state of one row (this lane's 8 columns).
+template <bool COMP>
 struct RowRegs {
-  float w[CPL], loc[CPL], stc[CPL], er[CPL];
-  uint32_t cq[CPL / 4];
+  float w[CPL], loc[CPL], stc[CPL], er[CPL], qc[CPL];
+  float cm[COMP ? CPL : 1];  // value each owned column was rounded from
 };
 
 // Step I of the column loop, I a compile-time constant so that every register index
 // below is static (no dynamic VGPR indexing).  ub[I & 1] holds this lane's U row I;
-// the step fills ub[(I + 1) & 1] with row I + 1.
-template <int I>
-__device__ __forceinline__ void gptq_step(RowRegs& R, int L, int q, float nm,
-                                          const float* __restrict__ suq, f32x4 (&ub)[2][2],
-                                          float* compr) {
+// the step fills ub[(I + 1) & 1] with row I + 1.  With FULL the block has LMAX columns
+// (no length test per step).
+template <int I, bool FULL, bool COMP>
+__device__ __forceinline__ void gptq_step(RowRegs<COMP>& R, int L, int q, float nm,
+                                          const float* __restrict__ suq, f32x4 (&ub)[2][2]) {
   constexpr int m = I / QL, s = I % QL, cur = I & 1;
-  if (I >= L) return;
+  if (!FULL && I >= L) return;
   if (I + 1 < LMAX) {
     ub[cur ^ 1][0] = *reinterpret_cast<const f32x4*>(suq + (I + 1) * USTR);
     ub[cur ^ 1][1] = *reinterpret_cast<const f32x4*>(suq + (I + 1) * USTR + 4);
@@ -80,22 +83,28 @@ __device__ __forceinline__ void gptq_step(RowRegs& R, int L, int q, float nm,
   const float ujj = ub[cur][m >> 2][m & 3];  // U[I][I] in the owner lane
   const float e = (col - wq) / ujj;
   const float eb = row_bcast<s>(e);
-  if (q == s) {
-    R.er[m] = e;
-    R.cq[m >> 2] |= ((uint32_t)qv & 0xffu) << (8 * (m & 3));
-    if (compr) compr[I] = col;
+  const bool own = q == s;
+  // the selects are pinned here (empty asm): left free, the compiler keeps every step's
+  // e and code in its own register until the end of the loop, which costs occupancy
+  R.er[m] = own ? e : R.er[m];
+  R.qc[m] = own ? qv : R.qc[m];
+  asm volatile("" : "+v"(R.er[m]), "+v"(R.qc[m]));
+  if constexpr (COMP) {
+    R.cm[m] = own ? col : R.cm[m];
+    asm volatile("" : "+v"(R.cm[m]));
   }
 #pragma unroll
   for (int mm = (I + 1) / QL; mm < CPL; ++mm) R.w[mm] = R.w[mm] - eb * ub[cur][mm >> 2][mm & 3];
 }
 
-template <int... Is>
-__device__ __forceinline__ void gptq_steps(std::integer_sequence<int, Is...>, RowRegs& R, int L,
-                                           int q, float nm, const float* __restrict__ suq,
-                                           f32x4 (&ub)[2][2], float* compr) {
-  (gptq_step<Is>(R, L, q, nm, suq, ub, compr), ...);
+template <bool FULL, bool COMP, int... Is>
+__device__ __forceinline__ void gptq_steps(std::integer_sequence<int, Is...>, RowRegs<COMP>& R,
+                                           int L, int q, float nm, const float* __restrict__ suq,
+                                           f32x4 (&ub)[2][2]) {
+  (gptq_step<Is, FULL, COMP>(R, L, q, nm, suq, ub), ...);
 }
 
+template <bool FULL, bool COMP>
 __global__ __launch_bounds__(RPG * QL) void gptq_block_kernel(
     const float* __restrict__ wc, int64_t N, int64_t K, int64_t i1, int L,
     float* __restrict__ err1, int64_t lde, uint8_t* __restrict__ codes,
@@ -150,7 +159,7 @@ __global__ __launch_bounds__(RPG * QL) void gptq_block_kernel(
     if (gr != g) continue;  // uniform over the row's 16 lanes
 
     const float nm = nmax[g];
-    RowRegs R;
+    RowRegs<COMP> R;
     {
       // this row's columns c = 16m + q: the working copy and each column's ladder block
       const __amdgpu_buffer_rsrc_t wrs =
@@ -174,24 +183,24 @@ __global__ __launch_bounds__(RPG * QL) void gptq_block_kernel(
         R.loc[m] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(lrs, (int)po, 0, 0));
         R.stc[m] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(srs, (int)po, 0, 0));
         R.er[m] = 0.0f;
+        R.qc[m] = 0.0f;
+        if constexpr (COMP) R.cm[m] = 0.0f;
       }
     }
-#pragma unroll
-    for (int m = 0; m < CPL / 4; ++m) R.cq[m] = 0u;
 
     const float* suq = su + lane_off(q);
     f32x4 ub[2][2];
     ub[0][0] = *reinterpret_cast<const f32x4*>(suq);
     ub[0][1] = *reinterpret_cast<const f32x4*>(suq + 4);
-    float* compr = comp ? comp + r * K + i1 : nullptr;
-    gptq_steps(std::make_integer_sequence<int, LMAX>{}, R, L, q, nm, suq, ub, compr);
+    gptq_steps<FULL, COMP>(std::make_integer_sequence<int, LMAX>{}, R, L, q, nm, suq, ub);
 
 #pragma unroll
     for (int m = 0; m < CPL; ++m) {
       const int c = QL * m + q;
       if (c < L) {
         err1[r * lde + c] = R.er[m];
-        codes[r * K + i1 + c] = (uint8_t)((R.cq[m >> 2] >> (8 * (m & 3))) & 0xffu);
+        codes[r * K + i1 + c] = (uint8_t)R.qc[m];
+        if constexpr (COMP) comp[r * K + i1 + c] = R.cm[m];
       }
     }
   }
@@ -306,8 +315,18 @@ int launch_block(const float* wc, int64_t n, int64_t k, int64_t i1, int64_t len,
                  const float* nmax, float* comp, hipStream_t s) {
   const dim3 grid((unsigned)((n + RPG - 1) / RPG));
   LaunchTimer timer(HI2X_TIME_GPTQ_BLOCK, (double)n * len * (len - 1), s);
-  hipLaunchKernelGGL(gptq_block_kernel, grid, dim3(RPG * QL), 0, s, wc, n, k, i1, (int)len,
-                     err1, lde, codes, lo, st, ldp, row_grp, u_ptrs, blk, nmax, comp);
+#define HI2X_BLOCK_LAUNCH(F, C)                                                            \
+  hipLaunchKernelGGL((gptq_block_kernel<F, C>), grid, dim3(RPG * QL), 0, s, wc, n, k, i1,   \
+                     (int)len, err1, lde, codes, lo, st, ldp, row_grp, u_ptrs, blk, nmax, comp)
+  const bool full = len == LMAX;
+  if (comp) {
+    if (full) HI2X_BLOCK_LAUNCH(true, true);
+    else HI2X_BLOCK_LAUNCH(false, true);
+  } else {
+    if (full) HI2X_BLOCK_LAUNCH(true, false);
+    else HI2X_BLOCK_LAUNCH(false, false);
+  }
+#undef HI2X_BLOCK_LAUNCH
   return launch_status("gptq_block_kernel");
 }
 
