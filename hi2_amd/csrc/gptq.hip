@@ -25,7 +25,8 @@ namespace {
 // its 8 columns of a U row as two 16-byte vectors (U[i1+i][i1+16m+q], m = 0..7, from
 // lane_off(q)).  The U row of step i+1 is read during step i.
 //
-// Step i (fully unrolled): every lane runs the rounding chain on its own column m=i/16;
+// Step i (fully unrolled): every lane runs the rounding chain on its own column m=i/16
+// (the two divisions through div_rcp with the lane's precomputed reciprocals);
 // only lane q = i%16 owns column i (its U value of row i is then U[i][i]), so its error e
 // is broadcast to the row with DPP row_newbcast, and the row applies
 // w[c] -= e * U[i][c] to the columns it holds.  Columns <= i of the other lanes are dead
@@ -54,10 +55,25 @@ __device__ __forceinline__ float row_bcast(float v) {  // lane S of each 16-lane
                                                             0x150 + S, 0xf, 0xf, false));
 }
 
-// Register state of one row (this lane's 8 columns).
+// a / b correctly rounded, given y = a correctly rounded 1 / b (Markstein's iteration:
+// q0 = a y is within 2 ulp of a / b, the first fma correction makes it faithful and the
+// second, from a faithful quotient, is the correctly rounded one; the remainders
+// a - b q are exact in an fma).  Five dependent operations instead of the ten of the
+// scaled IEEE division sequence, for operands that are normal with a normal quotient
+// (the rounding chain's values: weights, fp16 steps and factor diagonals).
+__device__ __forceinline__ float div_rcp(float a, float b, float y) {
+  const float q0 = a * y;
+  const float r0 = __builtin_fmaf(-b, q0, a);
+  const float q1 = __builtin_fmaf(r0, y, q0);
+  const float r1 = __builtin_fmaf(-b, q1, a);
+  return __builtin_fmaf(r1, y, q1);
+}
+
+// Register state of one row (this lane's 8 columns): working values, ladder (lo, step)
+// and the reciprocals of the step (ys) and of the factor diagonal U[c][c] (yu) of each.
 template <bool COMP>
 struct RowRegs {
-  float w[CPL], loc[CPL], stc[CPL], er[CPL], qc[CPL];
+  float w[CPL], loc[CPL], stc[CPL], ys[CPL], yu[CPL], er[CPL], qc[CPL];
   float cm[COMP ? CPL : 1];  // value each owned column was rounded from
 };
 
@@ -77,11 +93,11 @@ __device__ __forceinline__ void gptq_step(RowRegs<COMP>& R, int L, int q, float 
   const float col = R.w[m];
   const float lo_j = R.loc[m], st_j = R.stc[m];
   const float safe = (st_j == 0.0f) ? 1.0f : st_j;
-  float qv = clamp_code(__builtin_rintf((col - lo_j) / safe), nm);
+  float qv = clamp_code(__builtin_rintf(div_rcp(col - lo_j, safe, R.ys[m])), nm);
   if (st_j == 0.0f) qv = 0.0f;
   const float wq = f16_round(lo_j + qv * st_j);
   const float ujj = ub[cur][m >> 2][m & 3];  // U[I][I] in the owner lane
-  const float e = (col - wq) / ujj;
+  const float e = div_rcp(col - wq, ujj, R.yu[m]);
   const float eb = row_bcast<s>(e);
   const bool own = q == s;
   // the selects are pinned here (empty asm): left free, the compiler keeps every step's
@@ -185,6 +201,16 @@ __global__ __launch_bounds__(RPG * QL) void gptq_block_kernel(
         R.er[m] = 0.0f;
         R.qc[m] = 0.0f;
         if constexpr (COMP) R.cm[m] = 0.0f;
+      }
+      // IEEE reciprocals (correctly rounded) of each column's step and factor diagonal;
+      // dead columns (c >= L) get 1
+#pragma unroll
+      for (int m = 0; m < CPL; ++m) {
+        const int c = QL * m + q;
+        const float sc = R.stc[m] == 0.0f ? 1.0f : R.stc[m];
+        const float ud = c < L ? su[c * USTR + lane_off(q) + m] : 1.0f;
+        R.ys[m] = 1.0f / sc;
+        R.yu[m] = 1.0f / ud;
       }
     }
 
