@@ -139,16 +139,19 @@ __global__ __launch_bounds__(256) void tri_gemm_kernel(GemmArgs g, int64_t tm, i
 // Every fp32 operand x is written once, before the product, as three bf16 planes
 // x1 = bf16(x), x2 = bf16(x - x1), x3 = bf16(x - x1 - x2) (the differences are exact in
 // fp32; x = x1 + x2 + x3 to within 2^-27 |x|), laid out [row][k] with k contiguous
-// (a transposed copy where the product needs one) and the operand's structural zeros
+// (a transposed copy where the product needs one; stored in chunks of 16 k) and the
+// operand's structural zeros
 // written as zeros.  The product keeps the six terms x_i y_j with i + j <= 4 (the dropped
 // ones are below 2^-26 |x y|); bf16 products are exact and v_mfma_f32_32x32x16_bf16
 // accumulates in fp32: six MFMAs of 32 cycles cover 16 k where the fp32 MFMA needs
 // eight of 64, with the rounding of an fp32 GEMM (not bit-identical to one).
 
-// out[p][r][k] (planes of R x Kp bf16) from X: !trans: x = X[r][k] (X is R x Kk, ld ldx),
-// trans: x = X[k][r] (X is Kk x R).  mask 1 keeps k <= r, 2 keeps k >= r; k >= Kk and
-// masked elements are zero.  A workgroup converts a 64 x 64 block through LDS: 4 threads
-// per output row, 16 consecutive k each.
+// Planes of R x Kp bf16 from X, each stored in chunks of 16 k: element (r, k) of plane p
+// at out[p][k / 16][r][k % 16] (a chunk of a tile's rows is contiguous, so the product
+// reads whole cache lines).  !trans: x = X[r][k] (X is R x Kk, ld ldx), trans: x = X[k][r]
+// (X is Kk x R).  mask 1 keeps k <= r, 2 keeps k >= r; k >= Kk and masked elements are
+// zero.  A workgroup converts a 64 x 64 block through LDS: 4 threads per output row, 16
+// consecutive k (one chunk row) each.
 __global__ __launch_bounds__(256) void split3_kernel(const float* __restrict__ X, int64_t ldx,
                                                      int64_t R, int64_t Kk, int trans, int mask,
                                                      uint16_t* __restrict__ out, int64_t Kp) {
@@ -192,7 +195,7 @@ __global__ __launch_bounds__(256) void split3_kernel(const float* __restrict__ X
   const int64_t kb = k0 + 16 * kq;
   if (kb >= Kp) return;
   const int64_t plane = R * Kp;
-  uint16_t* o = out + r * Kp + kb;
+  uint16_t* o = out + ((kb >> 4) * R + r) * 16;
 #pragma unroll
   for (int g = 0; g < 2; ++g) {
     *reinterpret_cast<mg_u16x8*>(o + 8 * g) = p1[g];
@@ -202,11 +205,13 @@ __global__ __launch_bounds__(256) void split3_kernel(const float* __restrict__ X
 }
 
 // C[M, N] = alpha * A B^T + beta * C over k in [kbeg, kend) of each 128 x 128 output tile
-// (tri_krange), A and B given as split planes [3][rows][Kp].  Workgroup: 4 waves of
-// 64 x 64 (2 x 2 accumulators).  Stages of 32 k go from L2 straight into LDS through a
-// ring of three (prefetch distance two): each load instruction of a wave writes 1 KB
-// = 16 rows x 4 16-byte slots of one plane, slot q of row r holding piece
-// q ^ ((r / 4) % 4) so that the MFMA operand reads are free of bank conflicts.
+// (tri_krange), A and B given as split planes (16-k chunks).  Workgroup: 4 waves of
+// 64 x 64 (2 x 2 accumulators), two workgroups per CU (72 KB of LDS each), so each SIMD
+// has a second wave to issue MFMAs while one waits at a stage barrier.  Stages of 16 k
+// go from L2 straight into LDS through a ring of three (prefetch distance two): each load
+// instruction of a wave writes 1 KB = 32 rows x 2 16-byte slots of one plane, slot q of
+// row r holding piece q ^ ((r / 8) % 2) so that the MFMA operand reads are free of bank
+// conflicts.
 struct G3Args {
   const uint16_t* A;
   const uint16_t* B;
@@ -214,10 +219,11 @@ struct G3Args {
   int64_t M, N, Kd, Kp, ldc;
   float alpha, beta;
 };
-constexpr int G3_KC = 32;                 // k per stage
+constexpr int G3_KC = 16;                 // k per stage (one MFMA k-step)
+constexpr int G3_KA = 32;                 // k alignment of the planes (Kp)
 constexpr int G3_NB = 3;                  // stages in the ring
 constexpr int G3_PL = MG_T * G3_KC;       // bf16 per plane per stage
-constexpr int G3_PER_STAGE = 12;          // load instructions per wave and stage (2 x 3 x 8 / 4)
+constexpr int G3_PER_STAGE = 6;           // load instructions per wave and stage (2 x 3 x 4 / 4)
 
 __device__ __forceinline__ void g3_dma16(__amdgpu_buffer_rsrc_t rs, uint32_t voff, void* lds) {
   const uint32_t la = __builtin_amdgcn_readfirstlane(
@@ -238,8 +244,8 @@ constexpr int g3_waitcnt(int vm, int lgkm) {
 }
 
 template <int AMODE, int BMODE, bool CLOW>
-__global__ __launch_bounds__(256) void gemm3_kernel(G3Args g, int64_t tm, int64_t tn,
-                                                    MgSched sched) {
+__global__ __launch_bounds__(256, 2) void gemm3_kernel(G3Args g, int64_t tm, int64_t tn,
+                                                       MgSched sched) {
   __shared__ __attribute__((aligned(1024))) uint16_t SA[G3_NB][3][G3_PL];
   __shared__ __attribute__((aligned(1024))) uint16_t SB[G3_NB][3][G3_PL];
   int64_t tr, tc;
@@ -264,29 +270,31 @@ __global__ __launch_bounds__(256) void gemm3_kernel(G3Args g, int64_t tm, int64_
   const int rowsA = (int)((g.M - r0 < MG_T) ? g.M - r0 : MG_T);
   const int rowsB = (int)((g.N - c0 < MG_T) ? g.N - c0 : MG_T);
   const int64_t plA = g.M * g.Kp, plB = g.N * g.Kp;
-  // load j (0..11) of a stage: operand j / 6, plane (j % 6) / 2, row group 2 wv + j % 2
-  const int prow = lane >> 2, piece = (lane & 3) ^ ((lane >> 4) & 3);
+  // load j (0..5) of a stage: operand j / 3, plane j % 3, rows 32 wv .. 32 wv + 31
+  const int prow = lane >> 1, piece = (lane & 1) ^ ((lane >> 4) & 1);
   auto dma_one = [&](int j, int64_t k0, int buf, bool live) {
-    const int opd = j / 6, pl = (j % 6) >> 1, rg = 2 * wv + (j & 1);
-    const int row = 16 * rg + prow;
-    const uint16_t* base = opd == 0 ? g.A + pl * plA + r0 * g.Kp : g.B + pl * plB + c0 * g.Kp;
+    const int opd = j / 3, pl = j % 3;
+    const int row = 32 * wv + prow;
+    // chunk k0 / 16 of the tile's rows: rows x 16 contiguous bf16
+    const uint16_t* base = opd == 0 ? g.A + pl * plA + ((k0 >> 4) * g.M + r0) * G3_KC
+                                    : g.B + pl * plB + ((k0 >> 4) * g.N + c0) * G3_KC;
     const int rows = opd == 0 ? rowsA : rowsB;
-    const __amdgpu_buffer_rsrc_t rs = rsrc_u16(base, (int64_t)rows * g.Kp);
-    const uint32_t o = (uint32_t)(((int64_t)row * g.Kp + k0) * 2 + 16 * piece);
-    uint16_t* dst = opd == 0 ? &SA[buf][pl][rg * 16 * G3_KC] : &SB[buf][pl][rg * 16 * G3_KC];
+    const __amdgpu_buffer_rsrc_t rs = rsrc_u16(base, (int64_t)rows * G3_KC);
+    const uint32_t o = (uint32_t)(row * G3_KC * 2 + 16 * piece);
+    uint16_t* dst = opd == 0 ? &SA[buf][pl][wv * 32 * G3_KC] : &SB[buf][pl][wv * 32 * G3_KC];
     g3_dma16(rs, (live && row < rows) ? o : MG_OOB, dst);
   };
   auto dma = [&](int64_t k0, int buf, bool live) {
 #pragma unroll
     for (int j = 0; j < G3_PER_STAGE; ++j) dma_one(j, k0, buf, live);
   };
-  // operand reads: rows wr * 64 + 32 t + lane % 32 (A) / wcn * 64 + ... (B); piece 2 kk + h
+  // operand reads: rows wr * 64 + 32 t + lane % 32 (A) / wcn * 64 + ... (B), piece
+  // lane / 32 (k 8 h .. 8 h + 7 of the stage) in slot h ^ ((row / 8) % 2)
   const int rA = wr * 64 + (lane & 31), rB = wcn * 64 + (lane & 31);
-  const int sw = (lane >> 2) & 3, h = lane >> 5;
-  const int so0 = 8 * (h ^ sw), so1 = 8 * ((2 + h) ^ sw);
+  const int so = 8 * ((lane >> 5) ^ ((lane >> 3) & 1));
   typedef mg_bf16x8 V;
-  V a0[3][2], b0[3][2], a1[3][2], b1[3][2];  // [plane][tile], k-step sets 0 and 1
-  auto read = [&](V (&av)[3][2], V (&bv)[3][2], int buf, int so) {
+  V a0[3][2], b0[3][2], a1[3][2], b1[3][2];  // [plane][tile], stage sets 0 and 1
+  auto read = [&](V (&av)[3][2], V (&bv)[3][2], int buf) {
 #pragma unroll
     for (int pl = 0; pl < 3; ++pl)
 #pragma unroll
@@ -308,42 +316,45 @@ __global__ __launch_bounds__(256) void gemm3_kernel(G3Args g, int64_t tm, int64_
     __builtin_amdgcn_s_barrier();
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
   };
+  // nst stages carry data; the loop runs an even count (a last stage of zeros, loaded
+  // from past the end, when nst is odd) so that its body has no branch around the MFMAs
   const int nst = kend > kbeg ? (int)((kend - kbeg + G3_KC - 1) / G3_KC) : 0;
+  const int nst2 = (nst + 1) & ~1;
   if (nst > 0) {
 #pragma unroll
     for (int p = 0; p < G3_NB; ++p) dma(kbeg + (int64_t)p * G3_KC, p, p < nst);
     __builtin_amdgcn_s_waitcnt(g3_waitcnt(2 * G3_PER_STAGE, 15));  // stage 0 landed
     sync();
-    read(a0, b0, 0, so0);
+    read(a0, b0, 0);
   }
-  // every stage issues G3_PER_STAGE loads (past the end they read nothing), so "stage
-  // st + 1 has landed" is "at most stage st + 2's loads outstanding"; the loop body has
-  // no branch around the MFMAs
-  for (int st = 0; st < nst; ++st) {
-    const int cb = st % G3_NB, nb = (st + 1) % G3_NB;
-    read(a1, b1, cb, so1);
-    __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int n = 0; n < 24; ++n) {
-      G3_ONE(a0, b0, n)
-    }
-    __builtin_amdgcn_sched_barrier(0);
-    __builtin_amdgcn_s_waitcnt(g3_waitcnt(G3_PER_STAGE, 0));
-    sync();  // stage st + 1 landed everywhere; buffer cb is read by no wave any more
-    read(a0, b0, nb, so0);
-    __builtin_amdgcn_sched_barrier(0);
-    // stage st + 3 into buffer cb: one load after every second MFMA
-    const int64_t kn = kbeg + (int64_t)(st + G3_NB) * G3_KC;
-    const bool live = st + G3_NB < nst;
-#pragma unroll
-    for (int n = 0; n < 24; ++n) {
-      G3_ONE(a1, b1, n)
-      if (n & 1) {
-        dma_one(n >> 1, kn, cb, live);
-        __builtin_amdgcn_sched_barrier(0);
-      }
-    }
+  // Stage st: wait until stage st + 1 has landed (every stage issues G3_PER_STAGE loads,
+  // so that is "at most stage st + 2's loads outstanding") and this wave's reads of stage
+  // st are done; after the barrier no wave reads buffer st % 3 any more.  Then the reads
+  // of stage st + 1 are issued, and stage st's MFMAs run with the loads of stage st + 3
+  // into buffer st % 3 in between (one after every fourth MFMA).
+#define G3_STAGE(XA, XB, YA, YB, ST)                                                       \
+  {                                                                                        \
+    const int st_ = (ST);                                                                  \
+    const int cb = st_ % G3_NB, nb = (st_ + 1) % G3_NB;                                    \
+    __builtin_amdgcn_s_waitcnt(g3_waitcnt(G3_PER_STAGE, 0));                               \
+    sync();                                                                                \
+    read(YA, YB, nb);                                                                      \
+    __builtin_amdgcn_sched_barrier(0);                                                     \
+    const int64_t kn = kbeg + (int64_t)(st_ + G3_NB) * G3_KC;                              \
+    const bool live = st_ + G3_NB < nst;                                                   \
+    _Pragma("unroll") for (int n = 0; n < 24; ++n) {                                       \
+      G3_ONE(XA, XB, n)                                                                    \
+      if ((n & 3) == 3) {                                                                  \
+        dma_one(n >> 2, kn, cb, live);                                                     \
+        __builtin_amdgcn_sched_barrier(0);                                                 \
+      }                                                                                    \
+    }                                                                                      \
   }
+  for (int st = 0; st < nst2; st += 2) {
+    G3_STAGE(a0, b0, a1, b1, st)
+    G3_STAGE(a1, b1, a0, b0, st + 1)
+  }
+#undef G3_STAGE
 #undef G3_ONE
   const CTile<MG_T> ct(g.C, g.ldc, g.M, g.N, r0, c0);
   f32x16 cv[2][2];
@@ -916,7 +927,7 @@ int product(const Ctx& c, const GemmArgs& a) {
   const int64_t ntiles = tm * tn;
   if (!chol_split() || (CLOW ? ntiles / 2 : ntiles) < 128)
     return tri_gemm<AMODE, BMODE, TB, CLOW>(a, c.s);
-  const int64_t Kp = (a.Kd + G3_KC - 1) / G3_KC * G3_KC;
+  const int64_t Kp = (a.Kd + G3_KA - 1) / G3_KA * G3_KA;
   uint16_t* pa = reinterpret_cast<uint16_t*>(c.ws + c.plan->pa_off);
   uint16_t* pb = reinterpret_cast<uint16_t*>(c.ws + c.plan->pb_off);
   int rc = split3(a.A, a.lda, a.M, a.Kd, 0, AMODE == 1 ? 1 : 0, pa, Kp, c.s);
@@ -993,7 +1004,7 @@ static Plan make_plan(int64_t k) {
     const int64_t nbk = (k + NB - 1) / NB;
     m1 = ((nbk + 1) / 2) * NB;
   }
-  const int64_t kp = (m1 + G3_KC - 1) / G3_KC * G3_KC;
+  const int64_t kp = (m1 + G3_KA - 1) / G3_KA * G3_KA;
   const int64_t plane_floats = (3 * m1 * kp * 2 + 255) / 256 * 64;  // bytes / 4, 256-aligned
   plan.pa_off = off;
   off += plane_floats;
