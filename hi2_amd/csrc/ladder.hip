@@ -249,7 +249,15 @@ __global__ __launch_bounds__(256) void sse_kernel(const uint8_t* __restrict__ co
     float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
     int64_t i = 0;
     while (i + step <= size_ilp) {
-      for (int64_t j = 0; j < step; ++j) acc[0] += term(((i + j) * 4 + kq) * 8 + v);
+      // step is a power of two >= 16: the terms of 16 consecutive vectors are loaded
+      // together, then added in order (the loads of a group are all in flight at once)
+      for (int64_t j = 0; j < step; j += 16) {
+        float t[16];
+#pragma unroll
+        for (int u = 0; u < 16; ++u) t[u] = term(((i + j + u) * 4 + kq) * 8 + v);
+#pragma unroll
+        for (int u = 0; u < 16; ++u) acc[0] += t[u];
+      }
       i += step;
       for (int lev = 1; lev < 4; ++lev) {
         acc[lev] += acc[lev - 1];
@@ -360,10 +368,13 @@ extern "C" int hi2x_finish(const uint8_t* codes_ro, const float* comp_ro, const 
   if (n == 0) return HI2X_OK;
   hipStream_t s = as_stream(stream);
   const int64_t total = n * k;
-  hipLaunchKernelGGL(unpermute_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s,
-                     codes_ro, comp_ro, perm, n, k, codes, comp);
-  int rc = launch_status("unpermute_kernel");
-  if (rc) return rc;
+  // without a permutation the outputs may alias the inputs: nothing to move then
+  if (!(perm == nullptr && codes == codes_ro && comp == comp_ro)) {
+    hipLaunchKernelGGL(unpermute_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s,
+                       codes_ro, comp_ro, perm, n, k, codes, comp);
+    const int rc = launch_status("unpermute_kernel");
+    if (rc) return rc;
+  }
   hipLaunchKernelGGL(sse_kernel, dim3((unsigned)((n + 7) / 8)), dim3(256), 0, s, codes, n, k,
                      block, lo_d, step_d, ldd, w, d, sse);
   return launch_status("sse_kernel");

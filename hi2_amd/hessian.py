@@ -381,8 +381,12 @@ def _finish(unit: _Unit, job: GptqJob) -> Encoded:
     perm = None if job.perm is None else job.perm.to(dev, torch.int64).contiguous()
     codes_ro = unit.codes.contiguous()
     comp_ro = None if unit.comp is None else unit.comp.contiguous()
-    codes = torch.empty(n_rows, k, dtype=torch.uint8, device=dev)
-    comp = None if comp_ro is None else torch.empty(n_rows, k, dtype=torch.float32, device=dev)
+    if perm is None:  # rounding order is storage order: the finish writes only sse
+        codes, comp = codes_ro, comp_ro
+    else:
+        codes = torch.empty(n_rows, k, dtype=torch.uint8, device=dev)
+        comp = None if comp_ro is None else torch.empty(n_rows, k, dtype=torch.float32,
+                                                        device=dev)
     sse = torch.empty(n_rows, dtype=torch.float32, device=dev)
     lo_d, st_d = unit.lo_d.contiguous(), unit.step_d.contiguous()
     _lib.call("hi2x_finish", dev, _lib.ptr(codes_ro), _lib.ptr(comp_ro), _lib.ptr(perm), n_rows,

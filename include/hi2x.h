@@ -101,7 +101,8 @@ int hi2x_decode_params(const uint8_t* lo_u8, const uint8_t* step_u8, const uint1
 /* _finish (hi2/hessian.py:318-345): codes_ro/comp_ro [n, k] in rounding order ->
  * codes/comp in column order (perm [k] i64 or NULL), sse [n] = sum_c d_c (rec - w)^2
  * with rec = fp16(lo + code*step) in f32 and the sum in torch's CPU order.
- * lo_d/step_d [n, ldd] f32, w [n, k] f32 original rows, d [k] f32. */
+ * lo_d/step_d [n, ldd] f32, w [n, k] f32 original rows, d [k] f32.  With perm NULL,
+ * codes == codes_ro and comp == comp_ro (aliases) are allowed: then only sse is written. */
 int hi2x_finish(const uint8_t* codes_ro, const float* comp_ro, const int64_t* perm,
                 int64_t n, int64_t k, int64_t block, const float* lo_d, const float* step_d,
                 int64_t ldd, const float* w, const float* d, uint8_t* codes, float* comp,
