@@ -48,11 +48,16 @@ SIGNATURES = {
     "hi2x_chol_lambda": [_P, _I64, _F, _I, _P, _P],
     "hi2x_chol_inv_upper": [_P, _I64, _F, _I, _P, _P, _I64, _P],
     "hi2x_chol_inv_upper_async": [_P, _I64, _F, _I, _P, _P, _P, _I64, _P],
+    "hi2x_refine_run": [_P, _P, _I64, _I64, _P, _P, _I64, _P, _P, _P, _I64, _P, _P, _I64, _P],
+    "hi2x_refine_gradient": [_P, _P, _I64, _I64, _P, _P, _I64, _P, _P, _P, _P, _P],
+    "hi2x_refine_block": [_P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _I64, _P, _P, _P, _P,
+                          _I64, _P, _P],
 }
 # workspace sizes (int64 bytes, -1 for bad arguments): name -> argtypes
 SIZES = {
     "hi2x_hessian_workspace_bytes": [_I, _I64, _I64],
     "hi2x_chol_workspace_bytes": [_I64],
+    "hi2x_refine_workspace_bytes": [_I64, _I64, _I64],
 }
 
 
@@ -109,7 +114,8 @@ def lib():
 
 
 # launch-timing kinds (HI2X_TIME_* in include/hi2x.h)
-TIME_GPTQ_TRAILING, TIME_HESSIAN_SYRK, TIME_CHOL_GEMM, TIME_CHOL_LEAF, TIME_GPTQ_BLOCK = range(5)
+(TIME_GPTQ_TRAILING, TIME_HESSIAN_SYRK, TIME_CHOL_GEMM, TIME_CHOL_LEAF, TIME_GPTQ_BLOCK,
+ TIME_REFINE_GEMM, TIME_REFINE_BLOCK) = range(7)
 
 
 def timing_enable(kinds) -> None:

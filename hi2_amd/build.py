@@ -14,7 +14,8 @@ import sys
 HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libhi2x.so")
-SOURCES = ["api.hip", "gptq.hip", "ladder.hip", "format.hip", "hessian.hip", "chol.hip"]
+SOURCES = ["api.hip", "gptq.hip", "ladder.hip", "format.hip", "hessian.hip", "chol.hip",
+           "refine.hip"]
 ARCH = "gfx950"
 
 FLAGS = [

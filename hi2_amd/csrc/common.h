@@ -16,6 +16,16 @@ int launch_status(const char* what);
 
 inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 
+// The cross-block update of gptq.hip on `s`, for other kernels' schedules:
+//   wc[r, c] -= sum_k err1[r, 128 t + k] * U_g[i1 + 128 t + k, c]   (c in [c0, c1), t < nblk)
+// each block's product a sequential fp32 FMA chain subtracted in block order.  When skip
+// is not null the launch does nothing if *skip reads zero once it runs; its launches are
+// timed under timing_kind.
+int trailing_update(float* wc, int64_t n, int64_t k, int64_t i1, int nblk, const float* err1,
+                    int64_t lde, int64_t c0, int64_t c1, const int32_t* row_grp,
+                    const int64_t* u_ptrs, hipStream_t s, const unsigned long long* skip,
+                    int timing_kind);
+
 // Launch timing (hi2x_timing_enable): while the kind is enabled, a LaunchTimer brackets
 // the launch it scopes with HIP events on the launch's stream and records its algorithmic
 // work.  Construct it right before the launch, let it go out of scope right after.

@@ -247,10 +247,11 @@ __global__ __launch_bounds__(256, 2) void gptq_trailing_kernel(
     float* __restrict__ wc, int64_t N, int64_t K, int64_t i1, int nblk,
     const float* __restrict__ err1, int64_t lde, int64_t c0, int64_t c1,
     const int32_t* __restrict__ row_grp, const int64_t* __restrict__ u_ptrs, int64_t tn,
-    int64_t ntiles) {
+    int64_t ntiles, const unsigned long long* __restrict__ skip) {
   __shared__ MgSmem sm;
   const int64_t tile = xcd_tile(blockIdx.x, ntiles);
   if (tile < 0) return;
+  if (skip != nullptr && *skip == 0ull) return;  // a caller's device-side "nothing to do"
   const int64_t r0 = (tile / tn) * MG_T;
   const int64_t cc0 = c0 + (tile % tn) * MG_T;
   const int64_t rlast = ((r0 + MG_T < N) ? r0 + MG_T : N) - 1;
@@ -344,20 +345,31 @@ int launch_block(const float* wc, int64_t n, int64_t k, int64_t i1, int64_t len,
 
 int launch_trailing(float* wc, int64_t n, int64_t k, int64_t i1, int nblk, const float* err1,
                     int64_t lde, int64_t c0, int64_t c1, const int32_t* row_grp,
-                    const int64_t* u_ptrs, hipStream_t s) {
+                    const int64_t* u_ptrs, hipStream_t s,
+                    const unsigned long long* skip = nullptr,
+                    int timing_kind = HI2X_TIME_GPTQ_TRAILING) {
   if (c1 <= c0 || n == 0) return HI2X_OK;
   const int64_t tn = (c1 - c0 + MG_T - 1) / MG_T, tm = (n + MG_T - 1) / MG_T;
   const int64_t ntiles = tn * tm;
   const dim3 grid((unsigned)((ntiles + 7) / 8 * 8));
   double rank = 0.0;
   for (int t = 0; t < nblk; ++t) rank += (double)std::min<int64_t>(LMAX, k - (i1 + (int64_t)t * LMAX));
-  LaunchTimer timer(HI2X_TIME_GPTQ_TRAILING, 2.0 * n * rank * (c1 - c0), s);
+  LaunchTimer timer(timing_kind, 2.0 * n * rank * (c1 - c0), s);
   hipLaunchKernelGGL(gptq_trailing_kernel, grid, dim3(256), 0, s, wc, n, k, i1, nblk, err1,
-                     lde, c0, c1, row_grp, u_ptrs, tn, ntiles);
+                     lde, c0, c1, row_grp, u_ptrs, tn, ntiles, skip);
   return launch_status("gptq_trailing_kernel");
 }
 
 }  // namespace
+
+int trailing_update(float* wc, int64_t n, int64_t k, int64_t i1, int nblk, const float* err1,
+                    int64_t lde, int64_t c0, int64_t c1, const int32_t* row_grp,
+                    const int64_t* u_ptrs, hipStream_t s, const unsigned long long* skip,
+                    int timing_kind) {
+  return launch_trailing(wc, n, k, i1, nblk, err1, lde, c0, c1, row_grp, u_ptrs, s, skip,
+                         timing_kind);
+}
+
 }  // namespace hi2x
 
 using namespace hi2x;

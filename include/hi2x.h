@@ -220,6 +220,45 @@ int hi2x_chol_inv_upper(const float* hs, int64_t k, float damp, int attempt, flo
 int hi2x_chol_inv_upper_async(const float* hs, int64_t k, float damp, int attempt, float* u,
                               int32_t* status, void* ws, int64_t ws_bytes, void* stream);
 
+/* ---- local code refinement ------------------------------------------------------------ */
+
+/* Workspace of hi2x_refine_run for n rows of width k and `passes` sweeps. */
+int64_t hi2x_refine_workspace_bytes(int64_t n, int64_t k, int64_t passes);
+
+/* Local code refinement after GPTQ (hi2/refine.py:43-106 refine_expanded, called through
+ * refine_groups hi2/refine.py:125-144 from calibrate.encode_many hi2/calibrate.py:374-391):
+ *   w [n, k] f32 rows in the stored basis, codes [n, k] u8 refined in place,
+ *   lo/st [n, ldp] f32 decoded ladders, row r's column j using entry j / block[r]
+ *   (block [n] i32: the row's ladder block, 1 for per-column ladders), top [n] f32 the
+ *   row's highest code, hs [k, k] f32 the Hessian in the stored basis, `passes` sweeps.
+ * The reference stops after a sweep that moves no code; here that check runs on the
+ * device (no host synchronisation).  moved: device u64 [passes] or NULL, receives the
+ * codes moved by each sweep (0 for sweeps that did not run).  Codes are bit-identical
+ * to the reference loop given its products' rounding (each product a sequential fp32
+ * FMA chain, as the reference's CPU BLAS evaluates them at its tests' shapes). */
+int hi2x_refine_run(const float* w, uint8_t* codes, int64_t n, int64_t k, const float* lo,
+                    const float* st, int64_t ldp, const int32_t* block, const float* top,
+                    const float* hs, int64_t passes, unsigned long long* moved, void* ws,
+                    int64_t ws_bytes, void* stream);
+
+/* The start of refine_expanded (hi2/refine.py:72-74) and of objective (hi2/refine.py:33-36):
+ * e [n, k] f32 = fp16(lo + code * st) - w, then (g not NULL) g [n, k] f32 = e @ hs with
+ * each element a sequential fp32 FMA chain over k.  Arguments as hi2x_refine_run. */
+int hi2x_refine_gradient(const float* w, const uint8_t* codes, int64_t n, int64_t k,
+                         const float* lo, const float* st, int64_t ldp, const int32_t* block,
+                         const float* hs, float* e, float* g, void* stream);
+
+/* One block of the sweep (the fused kernel of hi2/refine_kernel.py:52-91, Python entry
+ * hi2/refine_kernel.py:171-176): columns [b0, b0 + len) (len <= 128) of every row, with
+ * g [n, ldg] f32 the block's slice of g = e hs (read only: g + r * ldg + i is column
+ * b0 + i of row r), codes/lo/st/block/top/hs as hi2x_refine_run; dw [n, ldw] f32 out
+ * receives the change of each decoded value (0 where the code did not move); moved
+ * (device u64 or NULL) is incremented by the number of moves. */
+int hi2x_refine_block(const float* g, int64_t ldg, int64_t n, int64_t k, int64_t b0,
+                      int64_t len, uint8_t* codes, const float* lo, const float* st,
+                      int64_t ldp, const int32_t* block, const float* top, const float* hs,
+                      float* dw, int64_t ldw, unsigned long long* moved, void* stream);
+
 /* ---- measurement ------------------------------------------------------------------------ */
 
 /* Launch-timing hook.  No counterpart in the reference (whose profiling is host-side
@@ -234,6 +273,8 @@ int hi2x_chol_inv_upper_async(const float* hs, int64_t k, float damp, int attemp
 #define HI2X_TIME_CHOL_GEMM 2     /* work = flops of the triangular product */
 #define HI2X_TIME_CHOL_LEAF 3     /* work = 2 * n^3 / 3 (factor + inverse of the leaf) */
 #define HI2X_TIME_GPTQ_BLOCK 4    /* work = rows * len * (len - 1) (intra-block flops) */
+#define HI2X_TIME_REFINE_GEMM 5   /* work = 2 * rows * rank * columns (flops) */
+#define HI2X_TIME_REFINE_BLOCK 6  /* work = rows * len (column decisions) */
 int hi2x_timing_enable(unsigned mask);
 
 /* Sum over the recorded launches of `kind`: count, event-timed milliseconds, work. */

@@ -78,6 +78,7 @@ def lib():
             "or_torch_sum_strided": (F, [P, I64, I64]),
             "or_pack_codes": (I64, [P, I64, I64, I, P]),
             "or_assemble_piece": (I64, [P, I64, P, P, P, I64, I, I64, P, P, P, P, P]),
+            "or_refine": (I, [P, P, I64, I64, P, P, I64, P, P, P, I, P]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(_lib, name)
@@ -308,3 +309,20 @@ def assemble(pieces, row_nbits, row_block, k):
             raise ValueError("code outside the ladder")
     return dict(codes=codes, code_off=code_off.astype(np.int32), blk_params=params_,
                 param_off=param_off.astype(np.int32), row_consts=consts)
+
+
+def refine(w, codes, lo, st, block, top, hs, passes):
+    """Local code refinement (``hi2/refine.py:43-106``) of rows ``w [n, k]`` with codes
+    ``[n, k]`` u8, decoded ladders ``lo/st [n, k / block]`` (``block`` and ``top`` scalars
+    or per-row arrays), Hessian ``hs [k, k]``.  Returns (codes, moved per row, sweeps run)."""
+    w = _c(w, np.float32)
+    n, k = w.shape
+    codes = _c(codes, np.uint8).copy()
+    lo = _c(lo, np.float32)
+    st = _c(st, np.float32)
+    block = _c(np.broadcast_to(np.asarray(block), (n,)), np.int32)
+    top = _c(np.broadcast_to(np.asarray(top, np.float32), (n,)), np.float32)
+    moved = np.zeros(n, np.int64)
+    sweeps = lib().or_refine(_p(w), _p(codes), n, k, _p(lo), _p(st), lo.shape[1] if lo.ndim == 2 else 0,
+                             _p(block), _p(top), _p(_c(hs, np.float32)), int(passes), _p(moved))
+    return codes, moved, sweeps

@@ -646,3 +646,102 @@ int64_t or_assemble_piece(const int64_t* rows, int64_t r, const uint8_t* codes,
   }
   return bad;
 }
+
+/* ---- local code refinement (hi2/refine.py:43-106; column-loop op spec
+ * hi2/refine_kernel.py:63-91) ------------------------------------------------------
+ * Rows w [n, k] f32 (stored basis), codes [n, k] u8 (refined in place), decoded ladders
+ * lo/st [n, ldp] f32 where row r's column j uses ladder block j / block[r], top[r] the
+ * row's highest code, hs [k, k] f32.  Per row:
+ *   e = fp16(lo + c*st) - w;  g = e @ hs, each element a sequential fp32 FMA chain over
+ *   k in order (the oracle's fixed order for the reference's rank-k BLAS product);
+ *   per sweep and 128-column block [b0, b1): the reference's column loop, every product
+ *   and sum rounded separately, the candidates +1 then -1 compared as torch's max over
+ *   the stacked pair (a NaN gain propagates and is never taken, ties keep +1); then
+ *   g += (dw @ hs[b0:b1]) with the product a sequential FMA chain over the block's
+ *   columns from zero and one addition (hi2/refine.py:99).
+ * Rows are independent given hs, and a row whose sweep moves no code never moves again
+ * (its g and codes are unchanged, so the next sweep repeats the same decisions): the
+ * reference's stop after a sweep that moves nothing in any row is the same as stopping
+ * each row after its own first such sweep.  moved[r] (optional) receives the number of
+ * codes moved in row r over all sweeps.  Returns the number of sweeps the reference
+ * runs: min(passes, 1 + the largest number of sweeps in which some row moved). */
+int or_refine(const float* w, uint8_t* codes, int64_t n, int64_t k, const float* lo,
+              const float* st, int64_t ldp, const int32_t* block, const float* top,
+              const float* hs, int passes, int64_t* moved) {
+  int most = 0;
+#pragma omp parallel for schedule(dynamic, 1) reduction(max : most)
+  for (int64_t r = 0; r < n; ++r) {
+    float* g = (float*)malloc((size_t)k * sizeof(float));
+    float* e = (float*)malloc((size_t)k * sizeof(float));
+    uint8_t* c = codes + r * k;
+    const float* lr = lo + r * ldp;
+    const float* sr = st + r * ldp;
+    const int64_t B = block[r];
+    const float tp = top[r];
+    for (int64_t j = 0; j < k; ++j)
+      e[j] = f16r(lr[j / B] + (float)c[j] * sr[j / B]) - w[r * k + j];
+    for (int64_t col = 0; col < k; ++col) {
+      float acc = 0.0f;
+      for (int64_t i = 0; i < k; ++i) acc = fmaf(e[i], hs[i * k + col], acc);
+      g[col] = acc;
+    }
+    int64_t mv = 0;
+    int sweeps_moved = 0;
+    for (int p = 0; p < passes; ++p) {
+      int64_t mp = 0;
+      for (int64_t b0 = 0; b0 < k; b0 += 128) {
+        const int L = (int)((k - b0 < 128) ? k - b0 : 128);
+        float gb[128], dwb[128];
+        for (int q = 0; q < L; ++q) gb[q] = g[b0 + q];
+        for (int jj = 0; jj < L; ++jj) {
+          const int64_t j = b0 + jj;
+          const float lo_j = lr[j / B], st_j = sr[j / B];
+          const float cj = (float)c[j];
+          const float cur = f16r(lo_j + cj * st_j);
+          const float hd = hs[j * k + j];
+          const float gj = gb[jj];
+          float gain[2], dw[2], cn[2];
+          for (int t = 0; t < 2; ++t) {
+            cn[t] = cj + (t == 0 ? 1.0f : -1.0f);
+            dw[t] = f16r(lo_j + cn[t] * st_j) - cur;
+            const int ok = (cn[t] >= 0.0f) && (cn[t] <= tp) && (st_j > 0.0f);
+            const float t1 = 2.0f * dw[t];
+            const float t2 = t1 * gj;
+            const float t3 = dw[t] * dw[t];
+            const float t4 = t3 * hd;
+            gain[t] = ok ? -(t2 + t4) : -INFINITY;
+          }
+          /* torch max over [gain+, gain-]: NaN wins (never > 0), else the first largest */
+          int which = 0;
+          float best = gain[0];
+          if (!isnan(gain[0]) && (isnan(gain[1]) || gain[1] > gain[0])) {
+            which = 1;
+            best = gain[1];
+          }
+          const int take = best > 0.0f;
+          const float dwj = take ? dw[which] : 0.0f;
+          if (take) {
+            c[j] = (uint8_t)cn[which];
+            ++mp;
+          }
+          dwb[jj] = dwj;
+          const float* hr = hs + j * k + b0;
+          for (int q = 0; q < L; ++q) gb[q] = gb[q] + dwj * hr[q];
+        }
+        for (int64_t col = 0; col < k; ++col) {
+          float acc = 0.0f;
+          for (int jj = 0; jj < L; ++jj) acc = fmaf(dwb[jj], hs[(b0 + jj) * k + col], acc);
+          g[col] = g[col] + acc;
+        }
+      }
+      mv += mp;
+      if (mp == 0) break;
+      ++sweeps_moved;
+    }
+    if (moved) moved[r] = mv;
+    if (sweeps_moved > most) most = sweeps_moved;
+    free(g);
+    free(e);
+  }
+  return passes < most + 1 ? passes : most + 1;
+}

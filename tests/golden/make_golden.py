@@ -10,12 +10,16 @@ depend on the reference's own torch-CPU arithmetic:
   ``hi2/encode.py:53-92``);
 * ``hi2.hessian.encode_rows_gptq_reference`` (the verbatim column loop with the BLAS
   trailing update, ``hi2/hessian.py:89-175``), on the inputs of the reference's own
-  ``tests/test_gptq_fast.py:19-36`` ``_layer`` recipe.
+  ``tests/test_gptq_fast.py:19-36`` ``_layer`` recipe;
+* ``hi2.refine.refine_groups`` (the local code refinement torch loop with its two BLAS
+  products, ``hi2/refine.py:43-144``), on the inputs of the reference's own
+  ``tests/test_refine_kernel.py:25-32`` ``_rows`` recipe.
 
 The fixtures are plain ``.npz`` data (inputs and expected outputs); nothing of the
 reference is stored.  Run from the repository root:
 
-    python tests/golden/make_golden.py
+    python tests/golden/make_golden.py            # every fixture
+    python tests/golden/make_golden.py refine     # refine_*.npz only
 """
 
 import os
@@ -59,7 +63,76 @@ def _correlated(t, k, seed):
     return x
 
 
+def _refine_rows(nbits, block, n, k, seed, encode_rows_gptq_reference, inverse_factor):
+    # same recipe as the reference's tests/test_refine_kernel.py:25-32
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(500, k, generator=g) * torch.exp(0.5 * torch.randn(k, generator=g))
+    hs = (x.T @ x) / 500
+    w = torch.randn(n, k, generator=g) * 0.3
+    enc = encode_rows_gptq_reference(w, hs.diagonal().clone(), inverse_factor(hs), nbits, block)
+    return w, enc, hs
+
+
+REFINE_CASES = {  # file: [(tag, [(nbits, block, rows)], k, seed, passes)]
+    "refine_1.npz": [
+        ("a", [(2, 32, 64)], 256, 64, 3),
+        ("b", [(4, 64, 100)], 192, 100, 3),
+        ("c", [(2, 16, 37)], 160, 37, 2),
+        ("d", [(4, 16, 1)], 128, 1, 3),
+        ("zero", [(2, 32, 33)], 128, 2, 0),
+    ],
+    "refine_2.npz": [
+        ("e", [(2, 32, 40)], 384, 40, 2),
+        ("mixed", [(2, 32, 70), (4, 64, 45)], 192, 1, 2),
+        ("conv", [(2, 32, 33)], 128, 2, 40),
+    ],
+}
+
+
+def make_refine():
+    sys.path.insert(0, REF)
+    from hi2.format import decode_params
+    from hi2.hessian import encode_rows_gptq_reference, inverse_factor
+    from hi2.refine import refine_groups
+
+    torch.set_num_threads(1)
+    for fname, cases in REFINE_CASES.items():
+        arrs = {}
+        for tag, groups, k, seed, passes in cases:
+            _refine_case(arrs, tag, groups, k, seed, passes, decode_params,
+                         encode_rows_gptq_reference, inverse_factor, refine_groups)
+        np.savez_compressed(os.path.join(OUT, fname), **arrs)
+
+
+def _refine_case(arrs, tag, groups, k, seed, passes, decode_params,
+                 encode_rows_gptq_reference, inverse_factor, refine_groups):
+    grp, hs = [], None
+    for nbits, block, n in groups:
+        w, enc, h = _refine_rows(nbits, block, n, k, seed, encode_rows_gptq_reference,
+                                 inverse_factor)
+        hs = h if hs is None else hs  # mixed: both groups use the first group's Hessian
+        grp.append((w, enc, nbits, block))
+    out = refine_groups(grp, hs, passes)
+    arrs[f"{tag}_hs"] = hs.numpy()
+    arrs[f"{tag}_passes"] = np.array(passes, np.int64)
+    for gi, ((w, enc, nbits, block), codes) in enumerate(zip(grp, out)):
+        lo, step = decode_params(enc.params[..., 0], enc.params[..., 1],
+                                 enc.consts[:, 0:1], enc.consts[:, 1:2], enc.consts[:, 2:3])
+        p = f"{tag}_g{gi}"
+        arrs[f"{p}_spec"] = np.array([nbits, block], np.int64)
+        arrs[f"{p}_w"] = w.numpy()
+        arrs[f"{p}_codes_in"] = enc.codes.numpy()
+        arrs[f"{p}_params"] = enc.params.numpy()
+        arrs[f"{p}_consts"] = enc.consts.view(torch.int16).numpy()
+        arrs[f"{p}_lo"] = lo.float().numpy()
+        arrs[f"{p}_step"] = step.float().numpy()
+        arrs[f"{p}_codes"] = codes.numpy()
+
+
 def main():
+    if sys.argv[1:] == ["refine"]:
+        make_refine()
+        return
     sys.path.insert(0, REF)
     from hi2.encode import EFFORT, fit_ladder
     from hi2.hessian import encode_rows_gptq_reference, inverse_factor
@@ -132,6 +205,8 @@ def main():
         arrs[f"{tag}_step"] = step.numpy()
     arrs["effort_normal_grid"] = np.array(EFFORT["normal"]["grid"], np.float64)
     np.savez_compressed(os.path.join(OUT, "fit_ladder.npz"), **arrs)
+
+    make_refine()
 
     with open(os.path.join(OUT, "golden_meta.txt"), "w") as f:
         for k, v in meta.items():

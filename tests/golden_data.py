@@ -36,3 +36,24 @@ def inverse_cases():
     tags = sorted({k.rsplit("_", 1)[0] for k in g.files})
     for tag in tags:
         yield tag, g[f"{tag}_hs"], g[f"{tag}_u"]
+
+
+def refine_cases():
+    """Yields (tag, hs, passes, groups) for the reference's refine_groups fixtures
+    (tests/golden/refine_*.npz); each group is a dict with nbits, block, w, codes_in,
+    params, consts, lo, step (decoded) and codes (the reference's refined codes)."""
+    for fname in ("refine_1.npz", "refine_2.npz"):
+        g = np.load(os.path.join(GOLDEN, fname))
+        tags = sorted({k.split("_", 1)[0] for k in g.files})
+        for tag in tags:
+            groups = []
+            gi = 0
+            while f"{tag}_g{gi}_spec" in g.files:
+                p = f"{tag}_g{gi}"
+                nbits, block = (int(v) for v in g[f"{p}_spec"])
+                grp = {f: g[f"{p}_{f}"] for f in ("w", "codes_in", "params", "consts", "lo",
+                                                   "step", "codes")}
+                grp.update(nbits=nbits, block=block)
+                groups.append(grp)
+                gi += 1
+            yield tag, g[f"{tag}_hs"], int(g[f"{tag}_passes"]), groups

@@ -51,6 +51,14 @@ def test_argument_errors_come_back_as_status_without_a_gpu():
     assert rc == _lib.EINVAL and "multiple of 16" in _lib.last_error()
     rc = lib.hi2x_pack_codes(None, 1, 30, 4, None, None, None)
     assert rc == _lib.EINVAL
+    rc = lib.hi2x_refine_block(None, 128, 4, 256, 0, 200, None, None, None, 4, None, None,
+                               None, None, 128, None, None)
+    assert rc == _lib.EINVAL and "outside" in _lib.last_error()
+    rc = lib.hi2x_refine_run(None, None, 4, 256, None, None, 0, None, None, None, 2, None, None,
+                             0, None)
+    assert rc == _lib.EINVAL and "bad shape" in _lib.last_error()
+    assert lib.hi2x_refine_workspace_bytes(4, 256, 2) >= 2 * 4 * 256 * 4
+    assert lib.hi2x_refine_workspace_bytes(-1, 256, 2) == -1
     rc = lib.hi2x_timing_query(0, None, None, None)
     assert rc == _lib.EINVAL and "null" in _lib.last_error()
     _lib.timing_enable([])  # nothing recorded yet: no HIP call is made
@@ -83,6 +91,16 @@ def test_python_surface_matches_the_reference_modules():
     for name in ("GROUP", "hadamard16", "fwht_groups", "decode_params", "ladder_dequantize",
                  "pack_codes", "HI2Tensor", "FIELDS", "assemble"):
         assert hasattr(fmt, name), name
+    import hi2_amd.refine as rf
+    import hi2_amd.refine_kernel as rk
+
+    for name in ("BLOCK_COLUMNS", "objective", "_expand", "refine_expanded", "refine_codes",
+                 "refine_groups", "refine_encoded"):
+        assert hasattr(rf, name), name
+    for name in ("BLOCK_COLUMNS", "load", "available", "failure", "refine_block", "supported",
+                 "kernel_dir"):
+        assert hasattr(rk, name), name
+    assert rf.BLOCK_COLUMNS == rk.BLOCK_COLUMNS == 128
     assert hs.BLOCK_COLUMNS == gk.BLOCK_COLUMNS == 128
     assert enc.EFFORT["normal"]["grid"] == (0.0, 0.04, 0.08, 0.12, 0.16, 0.20)
 
@@ -99,6 +117,11 @@ def test_cpu_tensors_are_refused_not_computed():
         hs.encode_rows_gptq(torch.zeros(4, 32), torch.ones(32), torch.eye(32), 2, 16)
     with pytest.raises(ValueError):
         fmt.fwht_groups(torch.zeros(2, 24), torch.ones(1))
+    import hi2_amd.refine as rf
+
+    with pytest.raises(RuntimeError, match="MI355X"):
+        rf.refine_codes(torch.zeros(4, 32), torch.zeros(4, 32, dtype=torch.uint8),
+                        torch.zeros(4, 1), torch.ones(4, 1), torch.eye(32), 2, 32, 1)
 
 
 def test_hadamard16_constant():
