@@ -303,16 +303,19 @@ int launch_block(const float* g, int64_t ldg, int64_t n, int64_t k, int64_t b0, 
   return launch_status("refine_block_kernel");
 }
 
+constexpr int64_t SB = 4;  // blocks per super-block of the sweep's update schedule
+
 // Workspace layout of hi2x_refine_run (each part 256-byte aligned).
 struct RefineWs {
-  size_t e, g, zeros, uptr, moved, total;
+  size_t e, g, dw, zeros, uptr, moved, total;
 };
 RefineWs refine_ws(int64_t n, int64_t k, int64_t passes) {
   auto up = [](size_t x) { return (x + 255) & ~(size_t)255; };
   RefineWs w;
   w.e = 0;
   w.g = up(w.e + (size_t)n * k * 4);
-  w.zeros = up(w.g + (size_t)n * k * 4);
+  w.dw = up(w.g + (size_t)n * k * 4);
+  w.zeros = up(w.dw + (size_t)n * SB * LMAX * 4);
   w.uptr = up(w.zeros + (size_t)n * 4);
   w.moved = up(w.uptr + 8);
   w.total = up(w.moved + (size_t)(passes > 0 ? passes : 1) * 8);
@@ -393,18 +396,46 @@ extern "C" int hi2x_refine_run(const float* w, uint8_t* codes, int64_t n, int64_
   }
   if ((rc = launch_residual(w, codes, n, k, lo, st, ldp, block, e, s))) return rc;
   if ((rc = launch_gradient(e, hs, g, n, k, s))) return rc;
-  float* ndw = e;  // e is dead once g is formed; its first n * 128 floats hold -dw
+  // The sweep in super-blocks of SB blocks.  Every block's product P_b = dw_b Hs[b, :]
+  // must reach every column of g that is read later, added in block order.  After block b
+  // the columns of the super-block's later blocks get P_b at once (near update); the other
+  // columns get the super-block's products at its end, each tile held in registers while
+  // the SB products stream through (far update): the columns ahead before the next
+  // super-block runs, and the columns behind (with the super-block's own, which still lack
+  // the products of their own and later blocks) only when another sweep will read them.
+  float* ndw = reinterpret_cast<float*>(wsp.p + L.dw);  // -dw of the super-block's blocks
+  const int64_t lde = SB * LMAX;
+  const int64_t nblocks = (k + LMAX - 1) / LMAX;
   for (int64_t p = 0; p < passes; ++p) {
     const unsigned long long* prev = p > 0 ? cnt + p - 1 : nullptr;
-    for (int64_t b0 = 0; b0 < k; b0 += LMAX) {
-      const int64_t len = (k - b0 < LMAX) ? k - b0 : LMAX;
-      rc = launch_block(g + b0, k, n, k, b0, len, codes, lo, st, ldp, block, top, hs, ndw, LMAX,
-                        true, cnt + p, prev, s);
+    const bool last = p + 1 == passes;
+    for (int64_t s0 = 0; s0 < nblocks; s0 += SB) {
+      const int64_t s1 = (s0 + SB < nblocks) ? s0 + SB : nblocks;
+      const int64_t cs0 = s0 * LMAX, cs1 = (s1 * LMAX < k) ? s1 * LMAX : k;
+      for (int64_t b = s0; b < s1; ++b) {
+        const int64_t b0 = b * LMAX, len = (k - b0 < LMAX) ? k - b0 : LMAX;
+        float* db = ndw + (b - s0) * LMAX;
+        rc = launch_block(g + b0, k, n, k, b0, len, codes, lo, st, ldp, block, top, hs, db, lde,
+                          true, cnt + p, prev, s);
+        if (rc) return rc;
+        // g - ((-dw) Hs) = g + dw Hs: the near columns of this super-block
+        rc = trailing_update(g, n, k, b0, 1, db, lde, b0 + len, cs1, zeros, uptr, s, cnt + p,
+                             HI2X_TIME_REFINE_GEMM);
+        if (rc) return rc;
+      }
+      rc = trailing_update(g, n, k, cs0, (int)(s1 - s0), ndw, lde, cs1, k, zeros, uptr, s,
+                           cnt + p, HI2X_TIME_REFINE_GEMM);
       if (rc) return rc;
-      // g[:, :] += dw @ Hs[b0:b1, :]  as  g - ((-dw) @ Hs[b0:b1, :])
-      rc = trailing_update(g, n, k, b0, 1, ndw, LMAX, 0, k, zeros, uptr, s, cnt + p,
-                           HI2X_TIME_REFINE_GEMM);
+      if (last) continue;  // columns behind are read only by a later sweep
+      rc = trailing_update(g, n, k, cs0, (int)(s1 - s0), ndw, lde, 0, cs0, zeros, uptr, s,
+                           cnt + p, HI2X_TIME_REFINE_GEMM);
       if (rc) return rc;
+      for (int64_t b = s0; b < s1; ++b) {  // block b's own columns: products of blocks >= b
+        const int64_t b0 = b * LMAX, b1 = (b0 + LMAX < k) ? b0 + LMAX : k;
+        rc = trailing_update(g, n, k, b0, (int)(s1 - b), ndw + (b - s0) * LMAX, lde, b0, b1,
+                             zeros, uptr, s, cnt + p, HI2X_TIME_REFINE_GEMM);
+        if (rc) return rc;
+      }
     }
   }
   return HI2X_OK;
