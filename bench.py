@@ -6,7 +6,7 @@ A step is one full encode of the block with every input resident in HBM:
 weight matrices -> GPTQ of every row (30 % INT2/B32, 70 % INT4/B64, seeded mask) ->
 rdna_hint_flex packing into device buffers.  Prints one JSON line.
 
-    python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu]
+    python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu] [--refine-steps R]
 """
 
 import argparse
@@ -93,11 +93,12 @@ def _chain_stream(dev, i):
     return _CHAIN_STREAMS[key]
 
 
-def encode_block(xs, ws, masks, timer=None, lanes=None):
+def encode_block(xs, ws, masks, timer=None, lanes=None, keep=None):
     """Encode the whole block.  Each calibration input runs its own chain on its own
     stream (Hessian -> transform -> factor -> rotation -> GPTQ -> packing of the linears
     it feeds); the chains are independent, so they overlap on the GPU.  The host waits
-    only after every chain has been enqueued (factor status, packing's range check)."""
+    only after every chain has been enqueued (factor status, packing's range check).
+    keep (a dict) receives each input's (stream, hs, jobs, where, encs)."""
     import torch
 
     from hi2_amd.format import assemble, fwht_groups
@@ -165,6 +166,38 @@ def encode_block(xs, ws, masks, timer=None, lanes=None):
                 out[name] = assemble(pieces, masks[name]["nbits"], masks[name]["block"], had, k,
                                      stager=_DeviceStager)
         main.wait_stream(st)
+        if keep is not None:
+            keep[inp] = (st, hs, jobs, where, encs)
+    return out
+
+
+REFINE_PASSES = 2  # the reference's default for a calibrated GPTQ run without QAD
+
+
+def refine_linears(kept):
+    """Local code refinement of every linear of the block (hi2/calibrate.py:374-391: one
+    sweep per tensor over all its candidate groups, with the input's transformed Hessian),
+    each calibration input's linears on that input's stream.  Returns the refined codes."""
+    import torch
+
+    from hi2_amd.refine import refine_groups
+
+    dev = next(iter(kept.values()))[1].device
+    main = torch.cuda.current_stream(dev)
+    out = {}
+    for inp in ORDER:
+        st, hs, jobs, where, encs = kept[inp]
+        st.wait_stream(main)
+        with torch.cuda.stream(st):
+            for name, n, k, i in LINEARS:
+                if i != inp:
+                    continue
+                xs = [x for x, (nm, _) in enumerate(where) if nm == name]
+                out[name] = refine_groups(
+                    [(jobs[x].w, encs[x], jobs[x].nbits, jobs[x].block) for x in xs], hs,
+                    REFINE_PASSES)
+    for inp in ORDER:
+        main.wait_stream(kept[inp][0])
     return out
 
 
@@ -196,6 +229,9 @@ KERNELS = {  # kind -> (kernel, bound, peak FLOP/s, work unit)
     2: ("tri_gemm_kernel", "mfma", PEAK_F32, "M*N*rank (one triangular operand)"),
     3: ("leaf_kernel", "latency", PEAK_F32, "2*n^3/3"),
     4: ("gptq_block_kernel", "latency", PEAK_F32, "rows*L*(L-1)"),
+    5: ("refine GEMMs (refine_gradient_kernel + gptq_trailing_kernel)", "mfma", PEAK_F32,
+        "2*rows*rank*cols"),
+    6: ("refine_block_kernel", "latency", PEAK_F32, "rows*L (column decisions)"),
 }
 DOMINANT = 0  # the GPTQ trailing-update GEMM: the metric's MFMA kernel with the most time
 
@@ -305,6 +341,8 @@ def main():
     ap.add_argument("--steps", type=int, default=3)
     ap.add_argument("--warmup", type=int, default=1)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--refine-steps", type=int, default=2,
+                    help="timed steps of the separate refinement leg (0: skip it)")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="first run 3 plain device copies of MIB MiB (f32), the known-size "
                          "reference for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE")
@@ -350,6 +388,34 @@ def main():
     kernels = {KERNELS[k][0]: kernel_stats(k) for k in KERNELS}
     roof_iso = roofline(DOMINANT)
     _lib.timing_enable([])
+    refine = None
+    if args.refine_steps:
+        kept = {}
+        encode_block(xs, ws, masks, keep=kept)
+        refine_linears(kept)  # warm-up
+        torch.cuda.synchronize()
+        _lib.timing_enable([5])
+        t0 = time.perf_counter()
+        for _ in range(args.refine_steps):
+            refine_linears(kept)
+        torch.cuda.synchronize()
+        r_ms = (time.perf_counter() - t0) * 1e3 / args.refine_steps
+        r_roof = roofline(5)
+        _lib.timing_enable([5, 6])
+        refine_linears({k: (torch.cuda.current_stream(dev),) + v[1:] for k, v in kept.items()})
+        torch.cuda.synchronize()
+        refine = {
+            "what": f"local code refinement, {REFINE_PASSES} sweeps, of all 7 linears' GPTQ "
+                    "codes (hi2/refine.py; the reference's default after calibrated GPTQ "
+                    "without QAD); not part of value",
+            "steps": args.refine_steps,
+            "ms_per_step": r_ms,
+            "ms_per_linear": r_ms / len(LINEARS),
+            "roofline": r_roof,
+            "kernels_one_step_serial": {KERNELS[k][0]: kernel_stats(k) for k in (5, 6)},
+        }
+        _lib.timing_enable([])
+        del kept
     res = {
         "metric": "encode ms per linear layer (Llama-3-8B-shaped block, 7 linears)",
         "value": ms_step / len(LINEARS),
@@ -372,6 +438,8 @@ def main():
         "roofline_isolated": roof_iso,
         "kernels_one_step": kernels,
     }
+    if refine is not None:
+        res["refine"] = refine
     if not args.no_cpu:
         res["cpu_baseline"] = cpu_baseline()
     print(json.dumps(res), flush=True)

@@ -178,10 +178,11 @@ def _gptq_rows(dev, n, k, t, nbits, block, seed):
     return w, enc, hs, lo.float(), st.float()
 
 
-@pytest.mark.parametrize("k,n,passes", [(4096, 48, 2), (14336, 16, 2)])
+@pytest.mark.parametrize("k,n,passes", [(4096, 48, 2), (14336, 16, 2), (960, 70, 3)])
 def test_refine_at_configuration_widths_equals_the_oracle(k, n, passes, dev):
     """Mixed INT2/B32 and INT4/B64 rows at the q_proj (K=4096) and down_proj (K=14336)
-    widths, two sweeps: codes equal the oracle's bit for bit."""
+    widths and at a width with a partial last block (K=960, three sweeps): codes equal
+    the oracle's bit for bit."""
     from hi2_amd.refine import refine_groups
 
     print(f"refine width k={k} n={n} passes={passes}", flush=True)
