@@ -268,7 +268,8 @@ __global__ __launch_bounds__(256, 2) void gptq_trailing_kernel(
     ColsLoader<NoMask> bl{U + i1 * K, K, c1, R, NoMask{}};
     f32x16 acc[2][2], cv[2][2];
     mg_zero(acc);
-    ct.load(cv);  // the wc tile stays in registers across the blocks
+    // the wc tile stays in registers across the blocks; it is loaded during the first
+    // chunk's MFMAs (first needed at the end of the first block)
     mg_mainloop_seg<2, MG_T, LMAX>(
         acc, sm, al, bl, r0, cc0, 0, R, []() {},
         [&](f32x16(&a)[2][2]) {
@@ -281,7 +282,8 @@ __global__ __launch_bounds__(256, 2) void gptq_trailing_kernel(
                 cv[x][y][j] = cv[x][y][j] - a[x][y][j];
                 a[x][y][j] = 0.0f;
               }
-        });
+        },
+        [&]() { ct.load(cv); });
     ct.store(cv, [](int, int, int) { return true; });
     return;
   }

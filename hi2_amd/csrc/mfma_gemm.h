@@ -240,11 +240,14 @@ __device__ __forceinline__ void mg_mainloop(f32x16 (&acc)[NA][NA], MgSmemT<T>& s
 // are in flight while the MFMAs run).  The next chunk's loads are issued before every
 // chunk's MFMAs, across segment boundaries too, so only the first chunk's load latency
 // is exposed.
-template <int NA, int T, int SEG, class AL, class BL, class Pre, class End>
+// first() runs once, in the first chunk, before the second chunk's loads are issued (the
+// place for loads the first segment's end needs: they are in flight during the first
+// chunk's MFMAs instead of ahead of the first chunk's wait).
+template <int NA, int T, int SEG, class AL, class BL, class Pre, class End, class First>
 __device__ __forceinline__ void mg_mainloop_seg(f32x16 (&acc)[NA][NA], MgSmemT<T>& sm,
                                                 const AL& al, const BL& bl, int64_t r0,
                                                 int64_t c0, int64_t kbeg, int64_t kend,
-                                                Pre pre, End end) {
+                                                Pre pre, End end, First first) {
   static_assert(NA * 64 == T, "accumulators must cover the tile");
   static_assert(SEG % MG_KC == 0, "segments are whole chunks");
   constexpr int CPS = SEG / MG_KC;  // chunks per segment
@@ -265,6 +268,7 @@ __device__ __forceinline__ void mg_mainloop_seg(f32x16 (&acc)[NA][NA], MgSmemT<T
     const int64_t kn = kbeg + (int64_t)(ch + 1) * MG_KC;
     const bool more = ch + 1 < nch;
     const bool seg_last = !more || (ch + 1) % CPS == 0;
+    if (ch == 0) first();
     if (seg_last) pre();
     if (more) {
       al.load(r0, kn, tid, sa);

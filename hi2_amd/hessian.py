@@ -37,7 +37,17 @@ ROW_ELEMS = 1 << 26  # rows per chunk are bounded so the working copies fit
 # chunks of several jobs batched through one kernel launch sequence (weights per batch)
 BATCH_ELEMS = int(os.environ.get("HI2_BATCH_ELEMS", 1 << 27))
 # 128-column blocks whose far-column updates share one pass over the working copy
-SUPER_BLOCKS = int(os.environ.get("HI2_SUPER_BLOCKS", 4))
+SUPER_BLOCKS = int(os.environ.get("HI2_SUPER_BLOCKS", 0))  # 0: by width (_super_blocks)
+
+
+def _super_blocks(k: int) -> int:
+    """Blocks per lazy super-block of the column loop: eight for the widest layers
+    (K >= 8192: half the passes over the trailing columns, measured 8.87 -> 8.41 ms of
+    trailing updates at 4096 x 14336), four below (eight measured slightly slower at
+    14336 x 4096, where the near updates grow)."""
+    if SUPER_BLOCKS > 0:
+        return SUPER_BLOCKS
+    return 8 if k >= 8192 else 4
 
 __all__ = [
     "EFFORT",
@@ -359,7 +369,7 @@ def _round_kernel(
         [2 ** jobs[x.job].nbits - 1 for x in units], dtype=torch.float32), dev)
     codes = torch.zeros(total, k, dtype=torch.uint8, device=dev)
     comp = torch.zeros(total, k, dtype=torch.float32, device=dev) if want_comp else None
-    sb = SUPER_BLOCKS if super_blocks is None else super_blocks
+    sb = _super_blocks(k) if super_blocks is None else super_blocks
     sb = max(1, min(int(sb), (k + BLOCK_COLUMNS - 1) // BLOCK_COLUMNS))
     err_ws = torch.empty(total, BLOCK_COLUMNS * sb, dtype=torch.float32, device=dev)
     _lib.call("hi2x_gptq_run", dev, _lib.ptr(wc), total, k, _lib.ptr(codes), _lib.ptr(lo),
