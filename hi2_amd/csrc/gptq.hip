@@ -243,40 +243,44 @@ struct GroupMask {  // A rows of the current group pass (this thread's staged ro
   __device__ __forceinline__ bool elem(int64_t, int64_t) const { return true; }
 };
 
-__global__ __launch_bounds__(256, 2) void gptq_trailing_kernel(
+// T: workgroup tile edge, 128 (2 x 2 accumulators per wave, two workgroups per CU) or 64
+// (one accumulator per wave, for launches with too few 128-tiles to fill the chip).
+template <int T>
+__global__ __launch_bounds__(256, T == MG_T ? 2 : 4) void gptq_trailing_kernel(
     float* __restrict__ wc, int64_t N, int64_t K, int64_t i1, int nblk,
     const float* __restrict__ err1, int64_t lde, int64_t c0, int64_t c1,
     const int32_t* __restrict__ row_grp, const int64_t* __restrict__ u_ptrs, int64_t tn,
     int64_t ntiles, const unsigned long long* __restrict__ skip) {
-  __shared__ MgSmem sm;
+  constexpr int NA = T / 64;
+  __shared__ MgSmemT<T> sm;
   const int64_t tile = xcd_tile(blockIdx.x, ntiles);
   if (tile < 0) return;
   if (skip != nullptr && *skip == 0ull) return;  // a caller's device-side "nothing to do"
-  const int64_t r0 = (tile / tn) * MG_T;
-  const int64_t cc0 = c0 + (tile % tn) * MG_T;
-  const int64_t rlast = ((r0 + MG_T < N) ? r0 + MG_T : N) - 1;
+  const int64_t r0 = (tile / tn) * T;
+  const int64_t cc0 = c0 + (tile % tn) * T;
+  const int64_t rlast = ((r0 + T < N) ? r0 + T : N) - 1;
   const int g0 = row_grp[r0], g1 = row_grp[rlast];
   const int tid = threadIdx.x;
-  const int64_t my_row = r0 + (tid >> 1);  // row this thread stages for the A operand
+  const int64_t my_row = r0 + tid / (256 / T);  // row this thread stages for the A operand
   const int my_grp = my_row < N ? row_grp[my_row] : -1;
-  const CTile<> ct(wc, K, N, c1, r0, cc0);
+  const CTile<T> ct(wc, K, N, c1, r0, cc0);
 
   if (g0 == g1) {  // one factor for the whole tile: the blocks as one pipelined rank stream
     const float* U = reinterpret_cast<const float*>(u_ptrs[g0]);
     const int64_t R = (K - i1 < (int64_t)nblk * LMAX) ? K - i1 : (int64_t)nblk * LMAX;
-    RowsLoader<GroupMask> al{err1, lde, N, R, GroupMask{my_grp == g0}};
-    ColsLoader<NoMask> bl{U + i1 * K, K, c1, R, NoMask{}};
-    f32x16 acc[2][2], cv[2][2];
+    RowsLoader<GroupMask, T> al{err1, lde, N, R, GroupMask{my_grp == g0}};
+    ColsLoader<NoMask, T> bl{U + i1 * K, K, c1, R, NoMask{}};
+    f32x16 acc[NA][NA], cv[NA][NA];
     mg_zero(acc);
     // the wc tile stays in registers across the blocks; it is loaded during the first
     // chunk's MFMAs (first needed at the end of the first block)
-    mg_mainloop_seg<2, MG_T, LMAX>(
+    mg_mainloop_seg<NA, T, LMAX>(
         acc, sm, al, bl, r0, cc0, 0, R, []() {},
-        [&](f32x16(&a)[2][2]) {
+        [&](f32x16(&a)[NA][NA]) {
 #pragma unroll
-          for (int x = 0; x < 2; ++x)
+          for (int x = 0; x < NA; ++x)
 #pragma unroll
-            for (int y = 0; y < 2; ++y)
+            for (int y = 0; y < NA; ++y)
 #pragma unroll
               for (int j = 0; j < 16; ++j) {
                 cv[x][y][j] = cv[x][y][j] - a[x][y][j];
@@ -292,19 +296,19 @@ __global__ __launch_bounds__(256, 2) void gptq_trailing_kernel(
     for (int t = 0; t < nblk; ++t) {
       const int64_t ib = i1 + (int64_t)t * LMAX;
       const int64_t L = (K - ib < LMAX) ? K - ib : LMAX;
-      f32x16 acc[2][2];
+      f32x16 acc[NA][NA];
       mg_zero(acc);
-      RowsLoader<GroupMask> al{err1 + t * LMAX, lde, N, L, GroupMask{my_grp == g}};
-      ColsLoader<NoMask> bl{U + ib * K, K, c1, L, NoMask{}};
+      RowsLoader<GroupMask, T> al{err1 + t * LMAX, lde, N, L, GroupMask{my_grp == g}};
+      ColsLoader<NoMask, T> bl{U + ib * K, K, c1, L, NoMask{}};
       mg_mainloop(acc, sm, al, bl, r0, cc0, 0, L);
       // wc tile -= this block's product (read-modify-write: the tile is not held in
       // registers across the rank loop, which keeps two workgroups per CU resident)
-      f32x16 cv[2][2];
+      f32x16 cv[NA][NA];
       ct.load(cv);
 #pragma unroll
-      for (int a = 0; a < 2; ++a)
+      for (int a = 0; a < NA; ++a)
 #pragma unroll
-        for (int b = 0; b < 2; ++b)
+        for (int b = 0; b < NA; ++b)
 #pragma unroll
           for (int j = 0; j < 16; ++j) cv[a][b][j] = cv[a][b][j] - acc[a][b][j];
       if (g0 == g1) {
@@ -312,10 +316,10 @@ __global__ __launch_bounds__(256, 2) void gptq_trailing_kernel(
       } else {  // a tile shared by two factors: bit a*16+j = row (a, j) is in group g
         uint32_t in_g = 0;
 #pragma unroll
-        for (int a = 0; a < 2; ++a)
+        for (int a = 0; a < NA; ++a)
 #pragma unroll
           for (int j = 0; j < 16; ++j) {
-            const int64_t rr = r0 + mg_row(a, j);
+            const int64_t rr = r0 + mg_row<T>(a, j);
             in_g |= (uint32_t)(rr < N && row_grp[rr] == g) << (a * 16 + j);
           }
         ct.store(cv, [&](int a, int j, int) { return (in_g >> (a * 16 + j)) & 1u; });
@@ -351,14 +355,23 @@ int launch_trailing(float* wc, int64_t n, int64_t k, int64_t i1, int nblk, const
                     const unsigned long long* skip = nullptr,
                     int timing_kind = HI2X_TIME_GPTQ_TRAILING) {
   if (c1 <= c0 || n == 0) return HI2X_OK;
-  const int64_t tn = (c1 - c0 + MG_T - 1) / MG_T, tm = (n + MG_T - 1) / MG_T;
-  const int64_t ntiles = tn * tm;
-  const dim3 grid((unsigned)((ntiles + 7) / 8 * 8));
   double rank = 0.0;
   for (int t = 0; t < nblk; ++t) rank += (double)std::min<int64_t>(LMAX, k - (i1 + (int64_t)t * LMAX));
   LaunchTimer timer(timing_kind, 2.0 * n * rank * (c1 - c0), s);
-  hipLaunchKernelGGL(gptq_trailing_kernel, grid, dim3(256), 0, s, wc, n, k, i1, nblk, err1,
-                     lde, c0, c1, row_grp, u_ptrs, tn, ntiles, skip);
+  // 128-tiles fill the chip from two rounds of its 512 workgroup slots on; smaller grids
+  // (the near updates of a super-block) run on 64-tiles, four times as many workgroups
+  const int64_t tn128 = (c1 - c0 + MG_T - 1) / MG_T, tm128 = (n + MG_T - 1) / MG_T;
+  if (tn128 * tm128 >= 512) {
+    const int64_t ntiles = tn128 * tm128;
+    hipLaunchKernelGGL(gptq_trailing_kernel<MG_T>, dim3((unsigned)((ntiles + 7) / 8 * 8)),
+                       dim3(256), 0, s, wc, n, k, i1, nblk, err1, lde, c0, c1, row_grp, u_ptrs,
+                       tn128, ntiles, skip);
+  } else {
+    const int64_t tn = (c1 - c0 + 63) / 64, tm = (n + 63) / 64, ntiles = tn * tm;
+    hipLaunchKernelGGL(gptq_trailing_kernel<64>, dim3((unsigned)((ntiles + 7) / 8 * 8)),
+                       dim3(256), 0, s, wc, n, k, i1, nblk, err1, lde, c0, c1, row_grp, u_ptrs,
+                       tn, ntiles, skip);
+  }
   return launch_status("gptq_trailing_kernel");
 }
 
