@@ -7,6 +7,7 @@ weight matrices -> GPTQ of every row (30 % INT2/B32, 70 % INT4/B64, seeded mask)
 rdna_hint_flex packing into device buffers.  Prints one JSON line.
 
     python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu] [--refine-steps R]
+    python bench.py --micro {trailing,syrk,factor,refine} [--steps R]   # one kernel alone
 """
 
 import argparse
@@ -335,6 +336,107 @@ def cpu_baseline(seed=0):
     }
 
 
+# ---- kernel microbenchmarks (for profiling single kernels; not the contract line) --------
+def micro(which, reps=3):
+    """One kernel family at the cfg3 shapes, alone on the GPU, event-timed; prints one
+    JSON line per shape.  trailing: hi2x_gptq_run (column loop + cross-block updates) on
+    4096 x 14336 and 14336 x 4096; syrk: HessianStats.update of 8192 bf16 tokens at
+    K = 4096 and 14336; factor: inverse_factor at K = 14336 and 4096; refine: two
+    refinement sweeps of GPTQ codes at 4096 x 4096, 4096 x 14336 and 14336 x 4096."""
+    import torch
+
+    from hi2_amd import _lib
+    from hi2_amd.hessian import HessianStats, encode_rows_gptq, inverse_factor
+
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+
+    def hessian(k, seed=0):
+        g = torch.Generator(device=dev).manual_seed(seed)
+        x = torch.randn(TOKENS, k, generator=g, device=dev)
+        x[:, torch.randperm(k, generator=g, device=dev)[: (k + 99) // 100]] *= 20.0
+        st = HessianStats(k, dev)
+        st.update(x.to(torch.bfloat16))
+        return st.transformed(None, torch.ones(k // 16, dtype=torch.uint8, device=dev)), x
+
+    def timed(fn, kinds):
+        fn()
+        torch.cuda.synchronize()
+        _lib.timing_enable(kinds)
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            fn()
+        torch.cuda.synchronize()
+        ms = (time.perf_counter() - t0) * 1e3 / reps
+        stats = {}
+        for kd in kinds:
+            n, kms, work = _lib.timing_query(kd)
+            name, bound, peak, unit = KERNELS[kd]
+            stats[name] = {"launches": n // reps, "ms": kms / reps,
+                           "tflops": work / kms / 1e9 if kms > 0 and work > 0 else None,
+                           "frac_of_peak": work / kms / 1e9 / (peak / 1e12)
+                           if kms > 0 and work > 0 else None}
+        _lib.timing_enable([])
+        return ms, stats
+
+    if which == "trailing":
+        for n, k in ((HIDDEN, INTER), (INTER, HIDDEN)):
+            g = torch.Generator(device=dev).manual_seed(0)
+            u = torch.triu(torch.randn(k, k, generator=g, device=dev) * (0.1 / k ** 0.5))
+            u += torch.eye(k, device=dev)
+            w = torch.randn(n, k, generator=g, device=dev) * 0.02
+            lo = torch.full((n, k // 16), -0.05, device=dev)
+            st = torch.full((n, k // 16), 0.1 / 15, device=dev)
+            row_grp = torch.zeros(n, dtype=torch.int32, device=dev)
+            u_ptrs = torch.tensor([u.data_ptr()], dtype=torch.int64, device=dev)
+            blk = (torch.arange(k, device=dev) // 64).to(torch.int32).reshape(1, k)
+            nmax = torch.tensor([15.0], device=dev)
+            codes = torch.zeros(n, k, dtype=torch.uint8, device=dev)
+            from hi2_amd.hessian import _super_blocks
+
+            sb = _super_blocks(k)
+            err = torch.empty(n, 128 * sb, device=dev)
+
+            def run():
+                wc = w.clone()
+                _lib.call("hi2x_gptq_run", dev, _lib.ptr(wc), n, k, _lib.ptr(codes),
+                          _lib.ptr(lo), _lib.ptr(st), k // 16, _lib.ptr(row_grp),
+                          _lib.ptr(u_ptrs), _lib.ptr(blk), _lib.ptr(nmax), None, _lib.ptr(err),
+                          sb)
+
+            ms, stats = timed(run, [0, 4])
+            print(json.dumps({"micro": "trailing", "rows": n, "k": k, "super_blocks": sb,
+                              "ms": ms, "kernels": stats}), flush=True)
+    elif which == "syrk":
+        for k in (HIDDEN, INTER):
+            g = torch.Generator(device=dev).manual_seed(0)
+            x = torch.randn(TOKENS, k, generator=g, device=dev).to(torch.bfloat16)
+            st = HessianStats(k, dev)
+            ms, stats = timed(lambda: st.update(x), [1])
+            print(json.dumps({"micro": "syrk", "tokens": TOKENS, "k": k, "ms": ms,
+                              "kernels": stats}), flush=True)
+    elif which == "factor":
+        for k in (INTER, HIDDEN):
+            hs, _ = hessian(k)
+            ms, stats = timed(lambda: inverse_factor(hs, DAMP), [2, 3])
+            print(json.dumps({"micro": "factor", "k": k, "ms": ms, "kernels": stats}),
+                  flush=True)
+    elif which == "refine":
+        from hi2_amd.refine import refine_groups
+
+        for n, k in ((HIDDEN, HIDDEN), (HIDDEN, INTER), (INTER, HIDDEN)):
+            hs, _ = hessian(k)
+            g = torch.Generator(device=dev).manual_seed(1)
+            w = torch.randn(n, k, generator=g, device=dev) * 0.02
+            enc = encode_rows_gptq(w, hs.diagonal().clone(), inverse_factor(hs, DAMP), 4, 64)
+            ms, stats = timed(lambda: refine_groups([(w, enc, 4, 64)], hs, REFINE_PASSES),
+                              [5, 6])
+            print(json.dumps({"micro": "refine", "rows": n, "k": k, "sweeps": REFINE_PASSES,
+                              "ms": ms, "kernels": stats}), flush=True)
+    else:
+        raise SystemExit(f"unknown --micro {which}")
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -343,6 +445,9 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--refine-steps", type=int, default=2,
                     help="timed steps of the separate refinement leg (0: skip it)")
+    ap.add_argument("--micro", choices=["trailing", "syrk", "factor", "refine"],
+                    help="instead of the block step: one kernel family alone at the cfg3 "
+                         "shapes (for single-kernel profiles; prints one line per shape)")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="first run 3 plain device copies of MIB MiB (f32), the known-size "
                          "reference for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE")
@@ -351,6 +456,9 @@ def main():
         print(json.dumps({"error": "this build measures one GPU only (--gpus 1); the "
                           "multi-GPU design is documented, not run"}))
         sys.exit(2)
+    if args.micro:
+        micro(args.micro, max(1, args.steps))
+        return
     import torch
 
     dev = torch.device("cuda", 0)
