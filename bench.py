@@ -7,7 +7,7 @@ weight matrices -> GPTQ of every row (30 % INT2/B32, 70 % INT4/B64, seeded mask)
 rdna_hint_flex packing into device buffers.  Prints one JSON line.
 
     python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu] [--refine-steps R]
-    python bench.py --micro {trailing,syrk,factor,refine} [--steps R]   # one kernel alone
+    python bench.py --micro {trailing,syrk,factor,refine,stats} [--steps R]   # one kernel alone
 """
 
 import argparse
@@ -342,7 +342,9 @@ def micro(which, reps=3):
     JSON line per shape.  trailing: hi2x_gptq_run (column loop + cross-block updates) on
     4096 x 14336 and 14336 x 4096; syrk: HessianStats.update of 8192 bf16 tokens at
     K = 4096 and 14336; factor: inverse_factor at K = 14336 and 4096; refine: two
-    refinement sweeps of GPTQ codes at 4096 x 4096, 4096 x 14336 and 14336 x 4096."""
+    refinement sweeps of GPTQ codes at 4096 x 4096, 4096 x 14336 and 14336 x 4096;
+    stats: ColumnStats.update of 8192 bf16 tokens and the cached-Sigma payload at
+    K = 4096 and 14336."""
     import torch
 
     from hi2_amd import _lib
@@ -433,6 +435,30 @@ def micro(which, reps=3):
                               [5, 6])
             print(json.dumps({"micro": "refine", "rows": n, "k": k, "sweeps": REFINE_PASSES,
                               "ms": ms, "kernels": stats}), flush=True)
+    elif which == "stats":
+        from hi2_amd.cache import sigma_payload
+        from hi2_amd.stats import ColumnStats
+
+        for k in (HIDDEN, INTER):
+            g = torch.Generator(device=dev).manual_seed(0)
+            x = torch.randn(TOKENS, k, generator=g, device=dev).to(torch.bfloat16)
+            cs = ColumnStats(k, dev)
+            ms, _ = timed(lambda: cs.update(x), [])
+            nsub = (TOKENS + 255) // 256
+            # X read once; the fp32 partials written and read back; S read and written
+            hbm = TOKENS * k * 2 + 2 * nsub * k * 16 * 4 + 2 * k * 16 * 8
+            print(json.dumps({"micro": "colstats_update", "tokens": TOKENS, "k": k, "ms": ms,
+                              "hbm_bytes": hbm, "gb_per_s": hbm / ms / 1e6,
+                              "frac_of_hbm_peak": hbm / ms / 1e6 / (PEAK_HBM / 1e9)}),
+                  flush=True)
+            hs = HessianStats(k, dev)
+            hs.update(x)
+            sig = hs.mean()
+            ms, _ = timed(lambda: sigma_payload(sig, hs.n), [])
+            hbm = k * k * 4 + k * (k + 1) // 2 * 4  # the matrix read, the triangle written
+            print(json.dumps({"micro": "sigma_payload", "k": k, "ms_incl_d2h": ms,
+                              "hbm_bytes": hbm, "d2h_bytes": k * (k + 1) // 2 * 4}),
+                  flush=True)
     else:
         raise SystemExit(f"unknown --micro {which}")
 
@@ -445,7 +471,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--refine-steps", type=int, default=2,
                     help="timed steps of the separate refinement leg (0: skip it)")
-    ap.add_argument("--micro", choices=["trailing", "syrk", "factor", "refine"],
+    ap.add_argument("--micro", choices=["trailing", "syrk", "factor", "refine", "stats"],
                     help="instead of the block step: one kernel family alone at the cfg3 "
                          "shapes (for single-kernel profiles; prints one line per shape)")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",

@@ -52,12 +52,16 @@ SIGNATURES = {
     "hi2x_refine_gradient": [_P, _P, _I64, _I64, _P, _P, _I64, _P, _P, _P, _P, _P],
     "hi2x_refine_block": [_P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _I64, _P, _P, _P, _P,
                           _I64, _P, _P],
+    "hi2x_colstats_update": [_P, _I, _I64, _I64, _P, _P, _I64, _P],
+    "hi2x_colstats_diag": [_P, _I64, _I64, _P, _P, _P, _P],
+    "hi2x_sigma_pack_upper": [_P, _I64, _I, _P, _P, _P],
 }
 # workspace sizes (int64 bytes, -1 for bad arguments): name -> argtypes
 SIZES = {
     "hi2x_hessian_workspace_bytes": [_I, _I64, _I64],
     "hi2x_chol_workspace_bytes": [_I64],
     "hi2x_refine_workspace_bytes": [_I64, _I64, _I64],
+    "hi2x_colstats_workspace_bytes": [_I64, _I64],
 }
 
 

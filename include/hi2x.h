@@ -220,6 +220,32 @@ int hi2x_chol_inv_upper(const float* hs, int64_t k, float damp, int attempt, flo
 int hi2x_chol_inv_upper_async(const float* hs, int64_t k, float damp, int attempt, float* u,
                               int32_t* status, void* ws, int64_t ws_bytes, void* stream);
 
+/* ---- calibration statistics ------------------------------------------------------------ */
+
+/* Workspace of hi2x_colstats_update for t tokens of width k (-1 for bad arguments). */
+int64_t hi2x_colstats_workspace_bytes(int64_t t, int64_t k);
+
+/* ColumnStats.update (hi2/stats.py:26-33): s [k/16, 16, 16] f64 += the 16 x 16 second
+ * moments x_g^T x_g of every column group of x [t, k] (dtype 0 = f32, 2 = bf16), chunk by
+ * chunk of 4096 tokens: each chunk's moments in fp32 (sub-chunks of 256 tokens, each a
+ * sequential FMA chain, summed in order), then added to s in f64, chunks in order. */
+int hi2x_colstats_update(const void* x, int dtype, int64_t t, int64_t k, double* s, void* ws,
+                         int64_t ws_bytes, void* stream);
+
+/* ColumnStats.diag (hi2/stats.py:39-55): out [k] f32 = E[x_j^2] of the activation
+ * x * inv_scale (inv_scale f32 [k] or NULL), in the rotated basis where flags [k/16] u8
+ * (or NULL: none) is set; s as above over n tokens. */
+int hi2x_colstats_diag(const double* s, int64_t k, int64_t n, const uint8_t* flags,
+                       const float* inv_scale, float* out, void* stream);
+
+/* The cached-Sigma payload's triangle (hi2/cache.py:266-277, sigma_payload): tri =
+ * sigma [k, k]'s upper triangle row-major (row i: columns i..k-1; k(k+1)/2 elements),
+ * f32 or, with fp16 != 0, fp16 bits; *asym (device i32, zeroed by the caller) += the
+ * number of pairs with sigma[i][j] != sigma[j][i] (zero: the matrix is exactly
+ * symmetric and the triangle is the payload). */
+int hi2x_sigma_pack_upper(const float* sigma, int64_t k, int fp16, void* tri, int32_t* asym,
+                          void* stream);
+
 /* ---- local code refinement ------------------------------------------------------------ */
 
 /* Workspace of hi2x_refine_run for n rows of width k and `passes` sweeps. */

@@ -79,6 +79,8 @@ def lib():
             "or_pack_codes": (I64, [P, I64, I64, I, P]),
             "or_assemble_piece": (I64, [P, I64, P, P, P, I64, I, I64, P, P, P, P, P]),
             "or_refine": (I, [P, P, I64, I64, P, P, I64, P, P, P, I, P]),
+            "or_colstats_update": (None, [P, I, I64, I64, P]),
+            "or_colstats_diag": (None, [P, I64, I64, P, P, P]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(_lib, name)
@@ -326,3 +328,24 @@ def refine(w, codes, lo, st, block, top, hs, passes):
     sweeps = lib().or_refine(_p(w), _p(codes), n, k, _p(lo), _p(st), lo.shape[1] if lo.ndim == 2 else 0,
                              _p(block), _p(top), _p(_c(hs, np.float32)), int(passes), _p(moved))
     return codes, moved, sweeps
+
+
+def colstats_update(s, x):
+    """ColumnStats.update (``hi2/stats.py:26-33``) into ``s [K/16, 16, 16]`` float64 in
+    place; ``x [t, K]`` float32, or bf16 bits as uint16."""
+    x = np.ascontiguousarray(x)
+    assert s.dtype == np.float64 and s.flags.c_contiguous
+    lib().or_colstats_update(_p(x), 1 if x.dtype == np.uint16 else 0, x.shape[0], x.shape[1],
+                             _p(s))
+    return s
+
+
+def colstats_diag(s, n, flags=None, inv_scale=None):
+    """ColumnStats.diag (``hi2/stats.py:39-55``): float32 ``[K]``."""
+    s = _c(s, np.float64)
+    k = s.shape[0] * 16
+    out = np.zeros(k, np.float32)
+    fl = None if flags is None else _c(flags, np.uint8)
+    inv = None if inv_scale is None else _c(inv_scale, np.float32)
+    lib().or_colstats_diag(_p(s), k, int(n), _p(fl), _p(inv), _p(out))
+    return out

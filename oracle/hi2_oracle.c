@@ -745,3 +745,80 @@ int or_refine(const float* w, uint8_t* codes, int64_t n, int64_t k, const float*
   }
   return passes < most + 1 ? passes : most + 1;
 }
+
+/* ---- ColumnStats (hi2/stats.py:26-33) -----------------------------------------------
+ * s [K/16, 16, 16] f64 += the 16 x 16 second moments of every column group of x [t, K]
+ * (bf16 bits when is_bf16, else f32), chunk by chunk of 4096 tokens as the reference's
+ * update: each chunk's moments in fp32, then added to s in f64.  The reference forms a
+ * chunk's fp32 moments with torch's einsum; the oracle fixes its own order, the one the
+ * GPU kernel uses: sub-chunks of 256 tokens, each a sequential fp32 FMA chain over its
+ * tokens from zero, their results added in order (fp32) into the chunk's moment. */
+void or_colstats_update(const void* x, int is_bf16, int64_t t, int64_t k, double* s) {
+  const int64_t ng = k / 16;
+#pragma omp parallel for schedule(static)
+  for (int64_t g = 0; g < ng; ++g) {
+    for (int i = 0; i < 16; ++i)
+      for (int j = 0; j < 16; ++j) {
+        double acc = s[(g * 16 + i) * 16 + j];
+        for (int64_t c0 = 0; c0 < t; c0 += 4096) {
+          const int64_t c1 = (c0 + 4096 < t) ? c0 + 4096 : t;
+          float chunk = 0.0f;
+          for (int64_t s0 = c0; s0 < c1; s0 += 256) {
+            const int64_t s1 = (s0 + 256 < c1) ? s0 + 256 : c1;
+            float sub = 0.0f;
+            for (int64_t r = s0; r < s1; ++r) {
+              float a, b;
+              if (is_bf16) {
+                a = bf16_to_f32(((const uint16_t*)x)[r * k + g * 16 + i]);
+                b = bf16_to_f32(((const uint16_t*)x)[r * k + g * 16 + j]);
+              } else {
+                a = ((const float*)x)[r * k + g * 16 + i];
+                b = ((const float*)x)[r * k + g * 16 + j];
+              }
+              sub = fmaf(a, b, sub);
+            }
+            chunk = chunk + sub;
+          }
+          acc = acc + (double)chunk;
+        }
+        s[(g * 16 + i) * 16 + j] = acc;
+      }
+  }
+}
+
+/* ColumnStats.diag (hi2/stats.py:39-55): out [K] f32.  s = S / max(n, 1) in f64, times
+ * inv_j inv_k when inv_scale (f32 [K]) is given ((s * inv_j) * inv_k); plain = s_ii; on a
+ * flagged group rot_i = sum_j h_ij (sum_k s_jk h_ik) with h = H16 / 4, each sum
+ * sequential in f64 without fused products (the reference's f64 einsum fixes its own
+ * order; the difference is far below the f32 output's rounding). */
+void or_colstats_diag(const double* S, int64_t k, int64_t n, const uint8_t* flags,
+                      const float* inv_scale, float* out) {
+  const int64_t ng = k / 16;
+  const double nn = (double)(n > 1 ? n : 1);
+  for (int64_t g = 0; g < ng; ++g) {
+    double s[16][16];
+    for (int j = 0; j < 16; ++j)
+      for (int q = 0; q < 16; ++q) {
+        double v = S[(g * 16 + j) * 16 + q] / nn;
+        if (inv_scale) v = (v * (double)inv_scale[g * 16 + j]) * (double)inv_scale[g * 16 + q];
+        s[j][q] = v;
+      }
+    for (int i = 0; i < 16; ++i) {
+      double v = s[i][i];
+      if (flags && flags[g]) {
+        double rot = 0.0;
+        for (int j = 0; j < 16; ++j) {
+          double tj = 0.0;
+          for (int q = 0; q < 16; ++q) {
+            const double hq = (__builtin_popcount(i & q) & 1) ? -0.25 : 0.25;
+            tj = tj + s[j][q] * hq;
+          }
+          const double hj = (__builtin_popcount(i & j) & 1) ? -0.25 : 0.25;
+          rot = rot + hj * tj;
+        }
+        v = rot;
+      }
+      out[g * 16 + i] = (float)v;
+    }
+  }
+}

@@ -13,13 +13,16 @@ depend on the reference's own torch-CPU arithmetic:
   ``tests/test_gptq_fast.py:19-36`` ``_layer`` recipe;
 * ``hi2.refine.refine_groups`` (the local code refinement torch loop with its two BLAS
   products, ``hi2/refine.py:43-144``), on the inputs of the reference's own
-  ``tests/test_refine_kernel.py:25-32`` ``_rows`` recipe.
+  ``tests/test_refine_kernel.py:25-32`` ``_rows`` recipe;
+* ``hi2.stats.ColumnStats`` (``update`` per 4096-token chunk through torch's fp32
+  einsum, ``diag`` with and without rotation flags and smoothing, ``hi2/stats.py:26-55``).
 
 The fixtures are plain ``.npz`` data (inputs and expected outputs); nothing of the
 reference is stored.  Run from the repository root:
 
     python tests/golden/make_golden.py            # every fixture
     python tests/golden/make_golden.py refine     # refine_*.npz only
+    python tests/golden/make_golden.py colstats   # colstats.npz only
 """
 
 import os
@@ -129,9 +132,39 @@ def _refine_case(arrs, tag, groups, k, seed, passes, decode_params,
         arrs[f"{p}_codes"] = codes.numpy()
 
 
+def make_colstats():
+    sys.path.insert(0, REF)
+    from hi2.stats import ColumnStats
+
+    torch.set_num_threads(1)
+    g = torch.Generator().manual_seed(3)
+    k, t1, t2 = 64, 4500, 700  # the first update spans two 4096-token chunks
+    x = (torch.randn(t1 + t2, k, generator=g) * torch.exp(0.7 * torch.randn(k, generator=g)))
+    xb = x.to(torch.bfloat16)
+    arrs = {"x_bf16": xb.view(torch.int16).numpy(), "split": np.array([t1, t2], np.int64)}
+    flags = torch.tensor([1, 0, 1, 1], dtype=torch.uint8)
+    inv = 1.0 / (torch.rand(k, generator=g) + 0.5).half().float()
+    arrs["flags"] = flags.numpy()
+    arrs["inv_scale"] = inv.numpy()
+    for tag, xs in (("bf16", xb), ("f32", xb.float())):
+        st = ColumnStats(k)
+        st.update(xs[:t1])
+        st.update(xs[t1:])
+        arrs[f"{tag}_S"] = st.S.numpy()
+        arrs[f"{tag}_n"] = np.array(st.n, np.int64)
+        arrs[f"{tag}_diag"] = st.diag().numpy()
+        arrs[f"{tag}_diag_rot"] = st.diag(flags).numpy()
+        arrs[f"{tag}_diag_inv"] = st.diag(None, inv).numpy()
+        arrs[f"{tag}_diag_rot_inv"] = st.diag(flags, inv).numpy()
+    np.savez_compressed(os.path.join(OUT, "colstats.npz"), **arrs)
+
+
 def main():
     if sys.argv[1:] == ["refine"]:
         make_refine()
+        return
+    if sys.argv[1:] == ["colstats"]:
+        make_colstats()
         return
     sys.path.insert(0, REF)
     from hi2.encode import EFFORT, fit_ladder
@@ -207,6 +240,7 @@ def main():
     np.savez_compressed(os.path.join(OUT, "fit_ladder.npz"), **arrs)
 
     make_refine()
+    make_colstats()
 
     with open(os.path.join(OUT, "golden_meta.txt"), "w") as f:
         for k, v in meta.items():

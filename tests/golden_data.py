@@ -57,3 +57,11 @@ def refine_cases():
                 groups.append(grp)
                 gi += 1
             yield tag, g[f"{tag}_hs"], int(g[f"{tag}_passes"]), groups
+
+
+def colstats_case():
+    """The reference ColumnStats fixture (tests/golden/colstats.npz): input as bf16 bits
+    [t, 64], the split of the two update calls, flags, inv_scale, and per input dtype
+    ("bf16", "f32": the same values as float32) the reference's S, n and diag variants."""
+    g = np.load(os.path.join(GOLDEN, "colstats.npz"))
+    return {f: g[f] for f in g.files}

@@ -101,6 +101,16 @@ def test_python_surface_matches_the_reference_modules():
                  "kernel_dir"):
         assert hasattr(rk, name), name
     assert rf.BLOCK_COLUMNS == rk.BLOCK_COLUMNS == 128
+    import hi2_amd.cache as ch
+    import hi2_amd.stats as sts
+
+    for name in ("TOKEN_CHUNK", "ColumnStats"):
+        assert hasattr(sts, name), name
+    for name in ("update", "merge", "diag", "state", "from_state"):
+        assert hasattr(sts.ColumnStats, name), name
+    for name in ("_fname", "_upper", "sigma_payload", "load_sigma"):
+        assert hasattr(ch, name), name
+    assert sts.TOKEN_CHUNK == 4096
     assert hs.BLOCK_COLUMNS == gk.BLOCK_COLUMNS == 128
     assert enc.EFFORT["normal"]["grid"] == (0.0, 0.04, 0.08, 0.12, 0.16, 0.20)
 
@@ -119,6 +129,12 @@ def test_cpu_tensors_are_refused_not_computed():
         fmt.fwht_groups(torch.zeros(2, 24), torch.ones(1))
     import hi2_amd.refine as rf
 
+    import hi2_amd.stats as sts
+
+    with pytest.raises(RuntimeError, match="MI355X"):
+        sts.ColumnStats(32, "cpu")
+    with pytest.raises(ValueError):
+        sts.ColumnStats(24, "cuda")
     with pytest.raises(RuntimeError, match="MI355X"):
         rf.refine_codes(torch.zeros(4, 32), torch.zeros(4, 32, dtype=torch.uint8),
                         torch.zeros(4, 1), torch.ones(4, 1), torch.eye(32), 2, 32, 1)
