@@ -7,6 +7,7 @@ weight matrices -> GPTQ of every row (30 % INT2/B32, 70 % INT4/B64, seeded mask)
 rdna_hint_flex packing into device buffers.  Prints one JSON line.
 
     python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu] [--refine-steps R]
+                    [--many-steps M]
     python bench.py --micro {trailing,syrk,factor,refine,stats} [--steps R]   # one kernel alone
 """
 
@@ -200,6 +201,33 @@ def refine_linears(kept):
     for inp in ORDER:
         main.wait_stream(kept[inp][0])
     return out
+
+
+def many_requests(xs, ws, masks):
+    """The block as the reference's pipeline hands it to ``encode_many``
+    (hi2/calibrate.py:297): bf16 weights and the cached fp32 Sigma of each input on the
+    host (pageable, as loaded), picks of the fixed allocation over the candidates
+    (INT2/B32, INT4/B64), two refinement sweeps."""
+    import torch
+
+    from hi2_amd.calibrate import Config, EncodeRequest, TensorTable
+    from hi2_amd.hessian import HessianStats
+
+    dev = next(iter(xs.values())).device
+    sigma = {}
+    for inp, k in INPUTS.items():
+        hst = HessianStats(k, dev)
+        hst.update(xs[inp])
+        sigma[inp] = hst.mean().cpu()
+    cands = [(2, 32), (4, 64)]
+    reqs = []
+    for name, n, k, inp in LINEARS:
+        picks = (masks[name]["nbits"] == 4).to(torch.int64)
+        table = TensorTable(name, (n, k), torch.ones(k // 16, dtype=torch.uint8),
+                            torch.zeros(1), cands, 0.0, TOKENS, None)
+        reqs.append(EncodeRequest(ws[name].cpu(), None, table, picks, sigma[inp], inp))
+    cfg = Config(candidates=cands, refine_passes=REFINE_PASSES, effort=EFFORT, damp=DAMP)
+    return reqs, cfg
 
 
 class StageTimer:
@@ -471,6 +499,9 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--refine-steps", type=int, default=2,
                     help="timed steps of the separate refinement leg (0: skip it)")
+    ap.add_argument("--many-steps", type=int, default=2,
+                    help="timed calls of the drop-in encode_many leg on host inputs "
+                         "(0: skip it)")
     ap.add_argument("--micro", choices=["trailing", "syrk", "factor", "refine", "stats"],
                     help="instead of the block step: one kernel family alone at the cfg3 "
                          "shapes (for single-kernel profiles; prints one line per shape)")
@@ -550,6 +581,42 @@ def main():
         }
         _lib.timing_enable([])
         del kept
+    many = None
+    if args.many_steps:
+        from hi2_amd.calibrate import Executor, encode_many
+
+        reqs, cfg = many_requests(xs, ws, masks)
+        ex = Executor([str(dev)])
+        encode_many(reqs, cfg, ex)  # warm-up
+        t0 = time.perf_counter()
+        for _ in range(args.many_steps):
+            packed = encode_many(reqs, cfg, ex)
+        m_ms = (time.perf_counter() - t0) * 1e3 / args.many_steps
+        srcs = [r.w for r in reqs] + list({id(r.sigma): r.sigma for r in reqs}.values())
+        h2d = sum(t.numel() * t.element_size() for t in srcs)
+        # the staging floor: the same host tensors to the device, nothing else
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        staged = [_lib.h2d(t, dev) for t in srcs]
+        torch.cuda.synchronize()
+        stage_ms = (time.perf_counter() - t0) * 1e3
+        del staged
+        d2h = sum(sum(getattr(p, f).numel() * getattr(p, f).element_size()
+                      for f in ("codes", "blk_params", "row_consts")) for p in packed)
+        many = {
+            "what": "drop-in hi2_amd.calibrate.encode_many on the block's 7 requests with "
+                    "bf16 weights and cached fp32 Sigma on the host: H2D, transform, "
+                    "factor, rotation, GPTQ, 2 refinement sweeps, packing, D2H of the "
+                    "packed buffers (PCIe-inclusive; the Hessian is not in it, the "
+                    "refinement is); not part of value",
+            "steps": args.many_steps,
+            "ms_per_step": m_ms,
+            "ms_per_linear": m_ms / len(LINEARS),
+            "h2d_bytes": h2d,
+            "h2d_staging_ms": stage_ms,
+            "d2h_bytes": d2h,
+        }
+        del reqs, packed
     res = {
         "metric": "encode ms per linear layer (Llama-3-8B-shaped block, 7 linears)",
         "value": ms_step / len(LINEARS),
@@ -574,6 +641,8 @@ def main():
     }
     if refine is not None:
         res["refine"] = refine
+    if many is not None:
+        res["encode_many"] = many
     if not args.no_cpu:
         res["cpu_baseline"] = cpu_baseline()
     print(json.dumps(res), flush=True)

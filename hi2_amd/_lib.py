@@ -204,10 +204,23 @@ def side_stream(dev: torch.device, i: int) -> torch.cuda.Stream:
     return st
 
 
+H2D_CHUNK = 64 << 20  # bytes per pinned staging chunk of a large host tensor
+
+
 def h2d(t: torch.Tensor, dev: torch.device) -> torch.Tensor:
-    """Host tensor to the device without blocking the host: staged through pinned
-    memory (torch's pinned allocator keeps the buffer until the copy has run)."""
-    return t.contiguous().pin_memory().to(dev, non_blocking=True)
+    """Host tensor to the device without waiting for the copy: staged through pinned
+    memory (torch's pinned allocator keeps each buffer until its copy has run).  Large
+    tensors go in chunks of ``H2D_CHUNK`` bytes, so the DMA of one chunk overlaps the
+    host's copy of the next into pinned memory."""
+    t = t.contiguous()
+    nbytes = t.numel() * t.element_size()
+    if t.dim() == 0 or nbytes <= H2D_CHUNK:
+        return t.pin_memory().to(dev, non_blocking=True)
+    out = torch.empty(t.shape, dtype=t.dtype, device=dev)
+    step = max(1, H2D_CHUNK // max(1, t[0].numel() * t.element_size()))
+    for i in range(0, t.shape[0], step):
+        out[i:i + step].copy_(t[i:i + step].pin_memory(), non_blocking=True)
+    return out
 
 
 def workspace(dev: torch.device, size_fn: str, *args) -> torch.Tensor:

@@ -26,6 +26,13 @@ Pinning (what holds each function to the reference):
 * ``inverse_factor``: golden vectors (``tests/golden/inverse_factor.npz``) and
   ``U^T U (Hs + lam I) = I``.
 * ``pack_codes`` / ``assemble_piece``: LSB-first KATs and the mixed-row offsets KAT.
+* ``refine``: golden vectors of ``refine_groups`` (``tests/golden/refine_*.npz``), the
+  reference's sweep invariants and an unblocked float64 column loop.
+* ``colstats_update`` / ``colstats_diag``: golden vectors of ``ColumnStats``
+  (``tests/golden/colstats.npz``) and float64 brute force.
+* ``encode_many`` (a composition of the functions above): the golden output of the
+  reference's ``encode_many`` (``tests/golden/encode_many.npz``), given the factors the
+  reference computed there.
 """
 
 import ctypes
@@ -348,4 +355,77 @@ def colstats_diag(s, n, flags=None, inv_scale=None):
     fl = None if flags is None else _c(flags, np.uint8)
     inv = None if inv_scale is None else _c(inv_scale, np.float32)
     lib().or_colstats_diag(_p(s), k, int(n), _p(fl), _p(inv), _p(out))
+    return out
+
+
+def _f16_bits_to_f32(bits):
+    return np.asarray(bits, np.uint16).view(np.float16).astype(np.float32)
+
+
+def encode_many(tensors, cands, cfg, factors=None):
+    """The orchestration of ``encode_many`` (``hi2/calibrate.py:297-424``) on one device,
+    composed of the functions above.  ``tensors``: dicts with ``w`` f32 [R, K]
+    (original basis), ``had``, ``picks``, ``col_scale`` (fp16 bits) or None, ``sigma``
+    or None, ``sigma_id`` or None, ``stats`` ``(S, n)`` or None, ``comp`` (bool).
+    ``cfg``: dict(rounding, act_order, refine_passes, effort, damp=0.01).  ``factors``:
+    the inverse factors to use, in the order the distinct inputs first appear
+    (default: :func:`inverse_factor`).  Returns per tensor ``(packed dict, comp)``."""
+    fac = None if factors is None else list(factors)
+    damp = cfg.get("damp", 0.01)
+    chains = {}
+    out = []
+    for i, t in enumerate(tensors):
+        w = np.ascontiguousarray(t["w"], np.float32)
+        r, k = w.shape
+        cs = t["col_scale"]
+        s = None if cs is None else _f16_bits_to_f32(cs)
+        ws = w * s if s is not None else w  # one fp32 rounding, as torch's host multiply
+        had = np.asarray(t["had"], np.uint8).reshape(-1)
+        wt = fwht16(ws, had) if had.any() else ws
+        gptq = cfg["rounding"] == "gptq" and t["sigma"] is not None
+        perm = None
+        if gptq:
+            key = (t["sigma_id"] if t["sigma_id"] is not None else f"#{i}",
+                   None if cs is None else np.asarray(cs, np.uint16).tobytes(), had.tobytes())
+            if key not in chains:
+                hs = transform_sigma(t["sigma"], cs, had)
+                d = np.diag(hs).copy()
+                if cfg["act_order"]:
+                    p = np.argsort(-d, kind="stable")
+                    hs = np.ascontiguousarray(hs[p][:, p])
+                else:
+                    p = None
+                u = fac.pop(0) if fac is not None else inverse_factor(hs, damp)[0]
+                chains[key] = (hs, d, u, p)
+            hs, d, u, perm = chains[key]
+        else:
+            if t["stats"] is None:
+                d = np.ones(k, np.float32)
+            else:
+                inv = None if s is None else (np.float32(1.0) / s).astype(np.float32)
+                d = colstats_diag(t["stats"][0], t["stats"][1], had, inv)
+            u = np.eye(k, dtype=np.float32)
+        picks = np.asarray(t["picks"], np.int64)
+        refine_rows = gptq and cfg["refine_passes"] and perm is None and not t["comp"]
+        pieces = []
+        comp = np.zeros((r, k), np.float32) if t["comp"] else None
+        for ci, (nb, b) in enumerate(cands):
+            rows = np.nonzero(picks == ci)[0]
+            if rows.size == 0:
+                continue
+            e = encode_rows_gptq(wt[rows], d, u, nb, b, cfg["effort"], perm,
+                                 comp=bool(gptq and t["comp"]))
+            codes = e["codes"]
+            if refine_rows:
+                codes, _, _ = refine(wt[rows], codes, e["lo_d"], e["step_d"], b, 2 ** nb - 1,
+                                     hs, cfg["refine_passes"])
+            pieces.append((rows, codes, e["params"], e["consts"]))
+            if comp is not None:
+                comp[rows] = e["comp"] if gptq else wt[rows]
+        nbits = np.array([cands[c][0] for c in picks], np.int64)
+        block = np.array([cands[c][1] for c in picks], np.int64)
+        packed = assemble(pieces, nbits, block, k)
+        packed.update(row_nbits=nbits.astype(np.uint8), row_block=block.astype(np.uint8),
+                      had=had)
+        out.append((packed, comp))
     return out

@@ -15,7 +15,10 @@ depend on the reference's own torch-CPU arithmetic:
   products, ``hi2/refine.py:43-144``), on the inputs of the reference's own
   ``tests/test_refine_kernel.py:25-32`` ``_rows`` recipe;
 * ``hi2.stats.ColumnStats`` (``update`` per 4096-token chunk through torch's fp32
-  einsum, ``diag`` with and without rotation flags and smoothing, ``hi2/stats.py:26-55``).
+  einsum, ``diag`` with and without rotation flags and smoothing, ``hi2/stats.py:26-55``);
+* ``hi2.calibrate.encode_many`` (factor sharing, candidate grouping, refinement,
+  ``comp`` and packing of several tensors, ``hi2/calibrate.py:297-424``), with every
+  factor it computed recorded beside the packed output.
 
 The fixtures are plain ``.npz`` data (inputs and expected outputs); nothing of the
 reference is stored.  Run from the repository root:
@@ -23,6 +26,7 @@ reference is stored.  Run from the repository root:
     python tests/golden/make_golden.py            # every fixture
     python tests/golden/make_golden.py refine     # refine_*.npz only
     python tests/golden/make_golden.py colstats   # colstats.npz only
+    python tests/golden/make_golden.py encode_many  # encode_many.npz only
 """
 
 import os
@@ -159,7 +163,115 @@ def make_colstats():
     np.savez_compressed(os.path.join(OUT, "colstats.npz"), **arrs)
 
 
+# encode_many requests: name -> (rows, input, sigma_id, smoothed, flags, weight dtype, comp)
+EM_TENSORS = {
+    "q": (36, "in0", "in0", True, "mixed", torch.bfloat16, False),
+    "k": (20, "in0", "in0", True, "mixed", torch.bfloat16, True),
+    "o": (28, "in1", None, False, "ones", torch.float32, False),
+    "n": (12, "in0", None, True, "mixed", torch.bfloat16, True),  # no sigma: nearest rows
+    "v": (16, "in0", "in0", True, "ones", torch.float32, False),  # same input, other flags
+}
+EM_INPUTS = {"in0": (128, 1200), "in1": (64, 700)}  # K, tokens
+# config tag -> (rounding, act_order, refine_passes, effort)
+EM_CONFIGS = {
+    "g": ("gptq", False, 0, "normal"),
+    "ga": ("gptq", True, 0, "fast"),
+    "gr": ("gptq", False, 2, "normal"),
+    "nr": ("nearest", False, 0, "normal"),
+}
+
+
+def make_encode_many():
+    sys.path.insert(0, REF)
+    import hi2.hessian as H
+    from hi2.calibrate import (ALL_CANDIDATES, INT8_CANDIDATES, Config, EncodeRequest,
+                               TensorTable, encode_many, smoothing_scale)
+    from hi2.executor import Executor
+    from hi2.format import GROUP
+    from hi2.stats import ColumnStats
+
+    torch.set_num_threads(1)
+    g = torch.Generator().manual_seed(29)
+    cands = list(ALL_CANDIDATES) + list(INT8_CANDIDATES)
+    arrs = {"candidates": np.array(cands, np.int64), "names": np.array(list(EM_TENSORS)),
+            "configs": np.array(list(EM_CONFIGS))}
+    for tag, (rounding, ao, passes, effort) in EM_CONFIGS.items():
+        arrs[f"{tag}_cfg"] = np.array([rounding, str(int(ao)), str(passes), effort])
+    stats, sigma = {}, {}
+    for inp, (k, t) in EM_INPUTS.items():
+        x = torch.randn(t, k, generator=g) * torch.exp(0.6 * torch.randn(k, generator=g))
+        x[:, :: 7] *= 5.0
+        x = x.to(torch.bfloat16)
+        st = ColumnStats(k)
+        st.update(x)
+        stats[inp] = st
+        xf = x.float()
+        sigma[inp] = (xf.T @ xf) / t
+        arrs[f"{inp}_S"] = st.S.numpy()
+        arrs[f"{inp}_n"] = np.array(st.n, np.int64)
+        arrs[f"{inp}_sigma"] = sigma[inp].numpy()
+    s16 = smoothing_scale(stats["in0"], 0.5)
+    arrs["in0_col_scale"] = s16.view(torch.int16).numpy()
+    reqs_in = []
+    for name, (rows, inp, sid, smooth, fl, dt, comp) in EM_TENSORS.items():
+        k = EM_INPUTS[inp][0]
+        w = torch.randn(rows, k, generator=g) * torch.exp(0.4 * torch.randn(rows, 1, generator=g))
+        w[:, :: max(1, k // 5)] *= 6
+        w = (w * 0.05).to(dt)
+        if fl == "ones":
+            had = torch.ones(k // GROUP, dtype=torch.uint8)
+        else:
+            had = (torch.arange(k // GROUP) % 3 != 1).to(torch.uint8)
+        picks = torch.randint(0, len(cands), (rows,), generator=g)
+        arrs[f"w_{name}"] = (w.view(torch.int16) if dt == torch.bfloat16 else w).numpy()
+        arrs[f"had_{name}"] = had.numpy()
+        arrs[f"picks_{name}"] = picks.numpy().astype(np.int64)
+        arrs[f"meta_{name}"] = np.array([inp, sid or "", str(int(smooth)), str(int(comp)),
+                                         str(int(name != "n")), str(int(name != "o"))])
+        reqs_in.append((name, w, inp, sid, s16 if smooth else None, had, picks, comp))
+    orig = H.inverse_factor
+    for tag, (rounding, ao, passes, effort) in EM_CONFIGS.items():
+        cfg = Config(candidates=cands, rounding=rounding, act_order=ao, refine_passes=passes,
+                     effort=effort)
+        reqs = []
+        for name, w, inp, sid, cs, had, picks, comp in reqs_in:
+            k = w.shape[1]
+            table = TensorTable(name, (w.shape[0], k), had.clone(),
+                                torch.zeros(len(cands), w.shape[0]), cands, 0.0,
+                                stats[inp].n, None if cs is None else cs.clone())
+            sig = None if name == "n" else sigma[inp]
+            reqs.append(EncodeRequest(w, None if name == "o" else stats[inp], table, picks,
+                                      sig, sid, {} if comp else None))
+        factors = []
+
+        def record(hs, damp=0.01):
+            u = orig(hs, damp)
+            factors.append(u.clone())
+            return u
+
+        H.inverse_factor = record
+        try:
+            out = encode_many(reqs, cfg, Executor(["cpu"]))
+        finally:
+            H.inverse_factor = orig
+        arrs[f"{tag}_nfactors"] = np.array(len(factors), np.int64)
+        for j, u in enumerate(factors):
+            arrs[f"{tag}_u{j}"] = u.numpy()
+        for r, o in zip(reqs, out):
+            nm = r.table.name
+            for f in ("codes", "code_off", "blk_params", "param_off", "row_nbits",
+                      "row_block", "had"):
+                arrs[f"{tag}_{nm}_{f}"] = getattr(o, f).numpy()
+            arrs[f"{tag}_{nm}_row_consts"] = o.row_consts.view(torch.int16).numpy()
+            if r.comp_out is not None:
+                arrs[f"{tag}_{nm}_comp"] = r.comp_out["comp"].numpy()
+    np.savez_compressed(os.path.join(OUT, "encode_many.npz"), **arrs)
+
+
 def main():
+    if sys.argv[1:] == ["encode_many"]:
+        make_encode_many()
+        return
     if sys.argv[1:] == ["refine"]:
         make_refine()
         return
@@ -241,6 +353,7 @@ def main():
 
     make_refine()
     make_colstats()
+    make_encode_many()
 
     with open(os.path.join(OUT, "golden_meta.txt"), "w") as f:
         for k, v in meta.items():

@@ -65,3 +65,46 @@ def colstats_case():
     ("bf16", "f32": the same values as float32) the reference's S, n and diag variants."""
     g = np.load(os.path.join(GOLDEN, "colstats.npz"))
     return {f: g[f] for f in g.files}
+
+
+def encode_many_case():
+    """The reference encode_many fixture (tests/golden/encode_many.npz).  Returns
+    (candidates, tensors, configs): tensors is a list of dicts (name, w float32 [R, K],
+    w_bf16 (bf16 bits) or None, had, picks, col_scale (fp16 bits) or None, sigma or None,
+    sigma_id or None, stats (S, n) or None, comp); configs maps a tag to a dict
+    (rounding, act_order, refine_passes, effort, factors: the reference's factors in
+    call order, out: per tensor name the packed fields and comp)."""
+    g = np.load(os.path.join(GOLDEN, "encode_many.npz"))
+    cands = [tuple(int(v) for v in c) for c in g["candidates"]]
+    cs = g["in0_col_scale"].view(np.uint16)
+    tensors = []
+    for name in g["names"]:
+        name = str(name)
+        inp, sid, smooth, comp, has_sigma, has_stats = (str(v) for v in g[f"meta_{name}"])
+        w = g[f"w_{name}"]
+        wb = None
+        if w.dtype == np.int16:
+            wb = w.view(np.uint16)
+            w = (wb.astype(np.uint32) << 16).view(np.float32)
+        tensors.append(dict(
+            name=name, w=w, w_bf16=wb, had=g[f"had_{name}"], picks=g[f"picks_{name}"],
+            col_scale=cs if smooth == "1" else None,
+            sigma=g[f"{inp}_sigma"] if has_sigma == "1" else None, sigma_id=sid or None,
+            stats=(g[f"{inp}_S"], int(g[f"{inp}_n"])) if has_stats == "1" else None,
+            comp=comp == "1"))
+    configs = {}
+    for tag in g["configs"]:
+        tag = str(tag)
+        rounding, ao, passes, effort = (str(v) for v in g[f"{tag}_cfg"])
+        out = {}
+        for t in tensors:
+            p = f"{tag}_{t['name']}_"
+            o = {f: g[p + f] for f in ("codes", "code_off", "blk_params", "param_off",
+                                       "row_nbits", "row_block", "had")}
+            o["row_consts"] = g[p + "row_consts"].view(np.uint16)
+            o["comp"] = g[p + "comp"] if p + "comp" in g.files else None
+            out[t["name"]] = o
+        configs[tag] = dict(rounding=rounding, act_order=ao == "1", refine_passes=int(passes),
+                            effort=effort, out=out,
+                            factors=[g[f"{tag}_u{j}"] for j in range(int(g[f"{tag}_nfactors"]))])
+    return cands, tensors, configs

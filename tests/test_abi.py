@@ -111,6 +111,19 @@ def test_python_surface_matches_the_reference_modules():
     for name in ("_fname", "_upper", "sigma_payload", "load_sigma"):
         assert hasattr(ch, name), name
     assert sts.TOKEN_CHUNK == 4096
+    import hi2_amd.calibrate as cal
+
+    for name in ("ALL_CANDIDATES", "INT8_CANDIDATES", "SELECTABLE", "Config", "TensorTable",
+                 "EncodeRequest", "Executor", "encode_many", "encode_with_picks",
+                 "encode_with_picks_reference", "_factor_key"):
+        assert hasattr(cal, name), name
+    assert cal.SELECTABLE == [(2, 16), (2, 32), (2, 64), (4, 16), (4, 32), (4, 64), (8, 32),
+                              (8, 64)]
+    c = cal.Config()
+    assert (c.rounding, c.damp, c.act_order, c.refine_passes, c.effort) == \
+        ("gptq", 0.01, False, 0, "normal")
+    assert cal.Executor(["cuda:0", "cuda:1"]).shards(5) == [
+        (torch.device("cuda:0"), 0, 2), (torch.device("cuda:1"), 2, 5)]
     assert hs.BLOCK_COLUMNS == gk.BLOCK_COLUMNS == 128
     assert enc.EFFORT["normal"]["grid"] == (0.0, 0.04, 0.08, 0.12, 0.16, 0.20)
 
@@ -138,6 +151,14 @@ def test_cpu_tensors_are_refused_not_computed():
     with pytest.raises(RuntimeError, match="MI355X"):
         rf.refine_codes(torch.zeros(4, 32), torch.zeros(4, 32, dtype=torch.uint8),
                         torch.zeros(4, 1), torch.ones(4, 1), torch.eye(32), 2, 32, 1)
+    import hi2_amd.calibrate as cal
+
+    table = cal.TensorTable("t", (4, 32), torch.ones(2, dtype=torch.uint8), torch.zeros(1),
+                            [(2, 16)], 0.0, 0)
+    req = cal.EncodeRequest(torch.zeros(4, 32), None, table, torch.zeros(4, dtype=torch.long),
+                            torch.eye(32))
+    with pytest.raises(RuntimeError, match="MI355X"):
+        cal.encode_many([req], cal.Config(candidates=[(2, 16)]), cal.Executor(["cpu"]))
 
 
 def test_hadamard16_constant():
