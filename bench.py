@@ -8,7 +8,7 @@ rdna_hint_flex packing into device buffers.  Prints one JSON line.
 
     python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu] [--refine-steps R]
                     [--many-steps M]
-    python bench.py --micro {trailing,syrk,factor,refine,stats} [--steps R]   # one kernel alone
+    python bench.py --micro {trailing,syrk,factor,refine,stats,qad} [--steps R]  # one kernel alone
 """
 
 import argparse
@@ -372,7 +372,9 @@ def micro(which, reps=3):
     K = 4096 and 14336; factor: inverse_factor at K = 14336 and 4096; refine: two
     refinement sweeps of GPTQ codes at 4096 x 4096, 4096 x 14336 and 14336 x 4096;
     stats: ColumnStats.update of 8192 bf16 tokens and the cached-Sigma payload at
-    K = 4096 and 14336."""
+    K = 4096 and 14336; qad: the QAD decode forward, backward and transform over the
+    latents of q_proj, gate_proj and down_proj (30 % INT2/B32, 70 % INT4/B64 rows, step
+    units)."""
     import torch
 
     from hi2_amd import _lib
@@ -487,6 +489,65 @@ def micro(which, reps=3):
             print(json.dumps({"micro": "sigma_payload", "k": k, "ms_incl_d2h": ms,
                               "hbm_bytes": hbm, "d2h_bytes": k * (k + 1) // 2 * 4}),
                   flush=True)
+    elif which == "qad":
+        from hi2_amd.qad_kernel import load
+
+        mod = load()
+
+        def events(fn, n=20):
+            fn()
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            for _ in range(n):
+                fn()
+            b.record()
+            torch.cuda.synchronize()
+            return a.elapsed_time(b) / n
+
+        for name, r, k, _ in LINEARS:
+            if name not in ("q_proj", "down_proj", "gate_proj"):
+                continue
+            g = torch.Generator(device=dev).manual_seed(1)
+            latent = torch.randn(r, k, generator=g, device=dev)
+            unit = torch.rand(r, k, generator=g, device=dev) * 0.5 + 0.5
+            grad = torch.randn(r, k, generator=g, device=dev)
+            out, g_lat = torch.empty_like(latent), torch.empty_like(latent)
+            perm = torch.randperm(r, generator=g, device=dev)
+            n2 = int(round(INT2_FRAC * r))
+            groups = []
+            for rows, nbits, block in ((perm[:n2].sort().values, 2, 32),
+                                       (perm[n2:].sort().values, 4, 64)):
+                nb = k // block
+                lo_u = torch.rand(rows.numel(), nb, generator=g, device=dev) * 255
+                st_u = torch.rand(rows.numel(), nb, generator=g, device=dev) * 255
+                c = torch.tensor([-3.0, 6.0 / 255, 0.1], device=dev).half().repeat(rows.numel(), 1)
+                groups.append((lo_u, st_u, c.contiguous(), rows.contiguous(), block,
+                               float(2 ** nbits - 1), torch.empty_like(lo_u),
+                               torch.empty_like(lo_u)))
+
+            def fwd():
+                for lo_u, st_u, c, rows, block, nmax, _, _ in groups:
+                    mod.decode_fwd(latent, unit, lo_u, st_u, c, rows, block, nmax, out)
+
+            def bwd():
+                for lo_u, st_u, c, rows, block, nmax, g_lo, g_st in groups:
+                    mod.decode_bwd(grad, latent, unit, lo_u, st_u, c, rows, block, nmax, g_lat,
+                                   g_lo, g_st)
+
+            flags = torch.ones(k // 16, dtype=torch.uint8, device=dev)
+            cs = (torch.rand(k, generator=g, device=dev) + 0.5).half()
+            y = torch.empty_like(latent)
+            elems = r * k
+            # algorithmic HBM bytes: fwd latent + unit in, values out; bwd grad + latent +
+            # unit in, latent gradient out; the transform x in, out (block bytes negligible)
+            for kern, fn, per in (("decode_fwd", fwd, 12), ("decode_bwd", bwd, 16),
+                                  ("wht_scale", lambda: mod.wht_scale(out, flags, cs, False, y),
+                                   8)):
+                ms = events(fn)
+                gbs = elems * per / ms / 1e6
+                print(json.dumps({"micro": f"qad_{kern}", "linear": name, "rows": r, "k": k,
+                                  "ms": ms, "hbm_bytes": elems * per, "gb_per_s": gbs,
+                                  "frac_of_hbm_peak": gbs / (PEAK_HBM / 1e9)}), flush=True)
     else:
         raise SystemExit(f"unknown --micro {which}")
 
@@ -502,7 +563,7 @@ def main():
     ap.add_argument("--many-steps", type=int, default=2,
                     help="timed calls of the drop-in encode_many leg on host inputs "
                          "(0: skip it)")
-    ap.add_argument("--micro", choices=["trailing", "syrk", "factor", "refine", "stats"],
+    ap.add_argument("--micro", choices=["trailing", "syrk", "factor", "refine", "stats", "qad"],
                     help="instead of the block step: one kernel family alone at the cfg3 "
                          "shapes (for single-kernel profiles; prints one line per shape)")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",

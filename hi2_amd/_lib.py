@@ -55,6 +55,10 @@ SIGNATURES = {
     "hi2x_colstats_update": [_P, _I, _I64, _I64, _P, _P, _I64, _P],
     "hi2x_colstats_diag": [_P, _I64, _I64, _P, _P, _P, _P],
     "hi2x_sigma_pack_upper": [_P, _I64, _I, _P, _P, _P],
+    "hi2x_qad_decode_fwd": [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I, _F, _P],
+    "hi2x_qad_decode_bwd": [_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I, _F, _P, _P,
+                            _P],
+    "hi2x_qad_wht_scale": [_P, _I64, _I64, _P, _P, _I, _P],
 }
 # workspace sizes (int64 bytes, -1 for bad arguments): name -> argtypes
 SIZES = {

@@ -15,7 +15,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libhi2x.so")
 SOURCES = ["api.hip", "gptq.hip", "ladder.hip", "format.hip", "hessian.hip", "chol.hip",
-           "refine.hip", "stats.hip"]
+           "refine.hip", "stats.hip", "qad.hip"]
 ARCH = "gfx950"
 
 FLAGS = [

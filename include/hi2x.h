@@ -285,6 +285,40 @@ int hi2x_refine_block(const float* g, int64_t ldg, int64_t n, int64_t k, int64_t
                       int64_t ldp, const int32_t* block, const float* top, const float* hs,
                       float* dw, int64_t ldw, unsigned long long* moved, void* stream);
 
+/* ---- QAD decode (the fake-quantised Linears of quantisation-aware distillation) --------- */
+
+/* decode_fwd (hi2/qad_kernel.py:88-108, Python side hi2/qad_kernel.py:276-293): for the
+ * n_rows rows of one (nbits, block) group, out[rows[r], :] = fp16(lo + q * step) as f32,
+ * with v = latent[rows[r], :] (times unit[rows[r], :] when unit is not NULL), the block's
+ * lo/step decoded from the continuous bytes lo_u/st_u [n_rows, k / block] f32
+ * (clamp(rint(u), 0, 255)) and the row constants consts [n_rows, 3] fp16 bits (lo_min,
+ * lo_scale, step_scale), q = clamp(rint((v - lo) / step), 0, nmax) (0 for a zero step).
+ * latent/unit/out are [r_total, k] f32 row-major, 16-byte aligned; block 16, 32 or 64;
+ * rows int64 on the device: a row outside [0, r_total) is skipped (nothing read or
+ * written for it; the reference does not check). */
+int hi2x_qad_decode_fwd(const float* latent, const float* unit, const float* lo_u,
+                        const float* st_u, const uint16_t* consts, const int64_t* rows,
+                        int64_t n_rows, int64_t r_total, int64_t k, int block, float nmax,
+                        float* out, void* stream);
+
+/* decode_bwd (hi2/qad_kernel.py:110-159, Python side hi2/qad_kernel.py:295-318): the
+ * gradients of the straight-through graph of decode_fwd given grad [R, k] f32 of its
+ * output: g_latent [r_total, k] (rows of the group written), g_lo / g_st
+ * [n_rows, k / block] (the per-block sums as a pairwise tree over the block, times
+ * lo_scale / step_scale; 0 for a skipped row).  Other arguments as hi2x_qad_decode_fwd. */
+int hi2x_qad_decode_bwd(const float* grad, const float* latent, const float* unit,
+                        const float* lo_u, const float* st_u, const uint16_t* consts,
+                        const int64_t* rows, int64_t n_rows, int64_t r_total, int64_t k,
+                        int block, float nmax, float* g_latent, float* g_lo, float* g_st,
+                        void* stream);
+
+/* wht_scale (hi2/qad_kernel.py:165-189, Python side hi2/qad_kernel.py:321-336): out =
+ * H16(x) / scale over the flagged 16-column groups (x / scale elsewhere), or with pre_div
+ * H16(x / scale); H16 the normalised order-16 Walsh-Hadamard butterfly.  x/out [n_rows, k]
+ * f32 row-major, 16-byte aligned; flags [k / 16] u8; scale [k] fp16 bits or NULL. */
+int hi2x_qad_wht_scale(const float* x, int64_t n_rows, int64_t k, const uint8_t* flags,
+                       const uint16_t* scale, int pre_div, float* out, void* stream);
+
 /* ---- measurement ------------------------------------------------------------------------ */
 
 /* Launch-timing hook.  No counterpart in the reference (whose profiling is host-side

@@ -30,6 +30,11 @@ Pinning (what holds each function to the reference):
   reference's sweep invariants and an unblocked float64 column loop.
 * ``colstats_update`` / ``colstats_diag``: golden vectors of ``ColumnStats``
   (``tests/golden/colstats.npz``) and float64 brute force.
+* ``qad_decode_fwd`` / ``qad_decode_bwd`` / ``qad_wht_scale``: the reference's torch
+  graph (``tests/golden/qad.npz``, written from ``hi2.qad.FakeQuantLinear`` on the CPU):
+  stored values and latent gradients bit-exact, block gradients and the transform within
+  float32 summation rounding; exact sums on integer-valued inputs; the transform against
+  the H16 product in float64.
 * ``encode_many`` (a composition of the functions above): the golden output of the
   reference's ``encode_many`` (``tests/golden/encode_many.npz``), given the factors the
   reference computed there.
@@ -88,6 +93,10 @@ def lib():
             "or_refine": (I, [P, P, I64, I64, P, P, I64, P, P, P, I, P]),
             "or_colstats_update": (None, [P, I, I64, I64, P]),
             "or_colstats_diag": (None, [P, I64, I64, P, P, P]),
+            "or_qad_decode_fwd": (None, [P, P, P, P, P, P, I64, I64, I64, ctypes.c_float, P]),
+            "or_qad_decode_bwd": (None, [P, P, P, P, P, P, P, I64, I64, I64, ctypes.c_float,
+                                         P, P, P]),
+            "or_qad_wht_scale": (None, [P, I64, I64, P, P, I, P]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(_lib, name)
@@ -428,4 +437,46 @@ def encode_many(tensors, cands, cfg, factors=None):
         packed.update(row_nbits=nbits.astype(np.uint8), row_block=block.astype(np.uint8),
                       had=had)
         out.append((packed, comp))
+    return out
+
+
+def qad_decode_fwd(latent, unit, lo_u, st_u, consts_bits, rows, block, nbits, out=None):
+    """decode_fwd (``hi2/qad_kernel.py:88-108``) into ``out`` [R, K] (rows of the group)."""
+    latent = _c(latent, np.float32)
+    r_all, k = latent.shape
+    out = np.zeros_like(latent) if out is None else out
+    rows = _c(rows, np.int64)
+    lib().or_qad_decode_fwd(_p(latent), _p(None if unit is None else _c(unit, np.float32)),
+                            _p(_c(lo_u, np.float32)), _p(_c(st_u, np.float32)),
+                            _p(_c(consts_bits, np.uint16)), _p(rows), rows.size, k, int(block),
+                            float(2 ** nbits - 1), _p(out))
+    return out
+
+
+def qad_decode_bwd(grad, latent, unit, lo_u, st_u, consts_bits, rows, block, nbits,
+                   g_latent=None):
+    """decode_bwd (``hi2/qad_kernel.py:110-159``): (g_latent [R, K], g_lo, g_st)."""
+    latent = _c(latent, np.float32)
+    k = latent.shape[1]
+    rows = _c(rows, np.int64)
+    g_latent = np.zeros_like(latent) if g_latent is None else g_latent
+    nb = k // int(block)
+    g_lo = np.zeros((rows.size, nb), np.float32)
+    g_st = np.zeros((rows.size, nb), np.float32)
+    lib().or_qad_decode_bwd(_p(_c(grad, np.float32)), _p(latent),
+                            _p(None if unit is None else _c(unit, np.float32)),
+                            _p(_c(lo_u, np.float32)), _p(_c(st_u, np.float32)),
+                            _p(_c(consts_bits, np.uint16)), _p(rows), rows.size, k, int(block),
+                            float(2 ** nbits - 1), _p(g_latent), _p(g_lo), _p(g_st))
+    return g_latent, g_lo, g_st
+
+
+def qad_wht_scale(x, flags, scale_bits, pre_div):
+    """wht_scale (``hi2/qad_kernel.py:165-189``)."""
+    x = _c(x, np.float32)
+    n, k = x.shape
+    out = np.zeros_like(x)
+    lib().or_qad_wht_scale(_p(x), n, k, _p(_c(flags, np.uint8)),
+                           _p(None if scale_bits is None else _c(scale_bits, np.uint16)),
+                           int(bool(pre_div)), _p(out))
     return out

@@ -822,3 +822,120 @@ void or_colstats_diag(const double* S, int64_t k, int64_t n, const uint8_t* flag
     }
   }
 }
+
+/* ---- QAD decode (hi2/qad_kernel.py:57-189; hi2/qad.py:366-400) -------------------------- */
+
+/* The block's fp16 lo and step from its continuous bytes (hi2/qad_kernel.py:60-69):
+ * byte = clamp(rint(u), 0, 255) (fmin/fmax: a NaN byte reads as 0); lo = fp16(f32(f64(byte)
+ * * f64(lo_scale) + f64(lo_min))), step = fp16(f32(byte) * step_scale). */
+static void qad_ladder(float lo_u, float st_u, const uint16_t* c, float* lo, float* st) {
+  const float lb = fminf(fmaxf(rne(lo_u), 0.0f), 255.0f);
+  const float sb = fminf(fmaxf(rne(st_u), 0.0f), 255.0f);
+  const double v = (double)lb * (double)or_f16_to_f32(c[1]) + (double)or_f16_to_f32(c[0]);
+  *lo = f16r((float)v);
+  *st = f16r(sb * or_f16_to_f32(c[2]));
+}
+
+/* q = clamp(rint(z), 0, nmax) with NaN kept (torch.clamp), 0 for a zero step
+ * (hi2/qad.py:390-392). */
+static float qad_code(float z, float nmax, int zero) {
+  float q = rne(z);
+  q = q < 0.0f ? 0.0f : q;
+  q = q > nmax ? nmax : q;
+  return zero ? 0.0f : q;
+}
+
+/* decode_fwd (hi2/qad_kernel.py:88-108; the value of hi2/qad.py:371-395): out[rows[r], j] =
+ * fp16(f64(lo) + f64(q) * f64(step)), the f64 value converted as torch converts f64 to fp16
+ * (through f32). */
+void or_qad_decode_fwd(const float* latent, const float* unit, const float* lo_u,
+                       const float* st_u, const uint16_t* consts, const int64_t* rows,
+                       int64_t n_rows, int64_t k, int64_t block, float nmax, float* out) {
+  const int64_t nblk = k / block;
+  for (int64_t r = 0; r < n_rows; ++r)
+    for (int64_t b = 0; b < nblk; ++b) {
+      float lo, st;
+      qad_ladder(lo_u[r * nblk + b], st_u[r * nblk + b], consts + r * 3, &lo, &st);
+      const int zero = st == 0.0f;
+      const float safe = zero ? 1.0f : st;
+      for (int64_t j = b * block; j < (b + 1) * block; ++j) {
+        const int64_t off = rows[r] * k + j;
+        float v = latent[off];
+        if (unit) v = v * unit[off];
+        const float q = qad_code((v - lo) / safe, nmax, zero);
+        out[off] = f16r((float)((double)lo + (double)q * (double)st));
+      }
+    }
+}
+
+/* decode_bwd (hi2/qad_kernel.py:110-159): the straight-through gradients of
+ * hi2/qad.py:380-399 in closed form; the per-block sums are the pairwise tree
+ * s[i] += s[i + h] (i < h) for h = block/2, ..., 1, in fp32. */
+void or_qad_decode_bwd(const float* grad, const float* latent, const float* unit,
+                       const float* lo_u, const float* st_u, const uint16_t* consts,
+                       const int64_t* rows, int64_t n_rows, int64_t k, int64_t block,
+                       float nmax, float* g_latent, float* g_lo, float* g_st) {
+  const int64_t nblk = k / block;
+  float* s_lo = (float*)malloc(sizeof(float) * block);
+  float* s_st = (float*)malloc(sizeof(float) * block);
+  for (int64_t r = 0; r < n_rows; ++r)
+    for (int64_t b = 0; b < nblk; ++b) {
+      float lo, st;
+      const uint16_t* c = consts + r * 3;
+      qad_ladder(lo_u[r * nblk + b], st_u[r * nblk + b], c, &lo, &st);
+      const int zero = st == 0.0f;
+      const float safe = zero ? 1.0f : st;
+      for (int64_t t = 0; t < block; ++t) {
+        const int64_t off = rows[r] * k + b * block + t;
+        const float un = unit ? unit[off] : 1.0f;
+        float v = latent[off];
+        if (unit) v = v * un;
+        const float z = (v - lo) / safe;
+        const float q = qad_code(z, nmax, zero);
+        const float G = grad[off];
+        const int inside = z >= 0.0f && z <= nmax;
+        const float gz = inside ? G * st : 0.0f;
+        const float gv = gz / safe;
+        g_latent[off] = unit ? gv * un : gv;
+        s_lo[t] = G - gv;
+        float a = G * q;
+        if (!zero) a = a + (-gz) * (z / safe);
+        s_st[t] = a;
+      }
+      for (int64_t h = block / 2; h > 0; h /= 2)
+        for (int64_t i = 0; i < h; ++i) {
+          s_lo[i] = s_lo[i] + s_lo[i + h];
+          s_st[i] = s_st[i] + s_st[i + h];
+        }
+      g_lo[r * nblk + b] = s_lo[0] * or_f16_to_f32(c[1]);
+      g_st[r * nblk + b] = s_st[0] * or_f16_to_f32(c[2]);
+    }
+  free(s_lo);
+  free(s_st);
+}
+
+/* wht_scale (hi2/qad_kernel.py:165-189): per flagged 16-column group the butterfly
+ * y[t] = (t & h) ? y[t ^ h] - y[t] : y[t] + y[t ^ h] for h = 1, 2, 4, 8, times 0.25; the
+ * division by the fp16 scale after it, or before it with pre_div. */
+void or_qad_wht_scale(const float* x, int64_t n_rows, int64_t k, const uint8_t* flags,
+                      const uint16_t* scale, int pre_div, float* out) {
+  for (int64_t r = 0; r < n_rows; ++r)
+    for (int64_t g = 0; g < k / 16; ++g) {
+      float y[16], orig[16];
+      for (int t = 0; t < 16; ++t) {
+        float v = x[r * k + g * 16 + t];
+        if (pre_div && scale) v = v / or_f16_to_f32(scale[g * 16 + t]);
+        y[t] = orig[t] = v;
+      }
+      for (int h = 1; h < 16; h <<= 1) {
+        float nxt[16];
+        for (int t = 0; t < 16; ++t) nxt[t] = (t & h) ? y[t ^ h] - y[t] : y[t] + y[t ^ h];
+        memcpy(y, nxt, sizeof(y));
+      }
+      for (int t = 0; t < 16; ++t) {
+        float v = flags[g] ? y[t] * 0.25f : orig[t];
+        if (!pre_div && scale) v = v / or_f16_to_f32(scale[g * 16 + t]);
+        out[r * k + g * 16 + t] = v;
+      }
+    }
+}

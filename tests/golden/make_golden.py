@@ -16,6 +16,9 @@ depend on the reference's own torch-CPU arithmetic:
   ``tests/test_refine_kernel.py:25-32`` ``_rows`` recipe;
 * ``hi2.stats.ColumnStats`` (``update`` per 4096-token chunk through torch's fp32
   einsum, ``diag`` with and without rotation flags and smoothing, ``hi2/stats.py:26-55``);
+* ``hi2.qad.FakeQuantLinear`` (the torch graph of the fused QAD decode,
+  ``hi2/qad.py:366-422``: stored values, the original-basis weights, and the autograd
+  gradients of both for the latent weights and both ladder bytes of every block);
 * ``hi2.calibrate.encode_many`` (factor sharing, candidate grouping, refinement,
   ``comp`` and packing of several tensors, ``hi2/calibrate.py:297-424``), with every
   factor it computed recorded beside the packed output.
@@ -27,6 +30,7 @@ reference is stored.  Run from the repository root:
     python tests/golden/make_golden.py refine     # refine_*.npz only
     python tests/golden/make_golden.py colstats   # colstats.npz only
     python tests/golden/make_golden.py encode_many  # encode_many.npz only
+    python tests/golden/make_golden.py qad          # qad.npz only
 """
 
 import os
@@ -268,7 +272,79 @@ def make_encode_many():
     np.savez_compressed(os.path.join(OUT, "encode_many.npz"), **arrs)
 
 
+# QAD cases: tag -> (latent units, zero-step and far-off blocks, clamped first 16 columns)
+QAD_CASES = {"abs": ("abs", False, False), "step": ("step", True, False),
+             "clamp": ("abs", True, True)}
+
+
+def make_qad():
+    sys.path.insert(0, REF)
+    from hi2.calibrate import (ALL_CANDIDATES, INT8_CANDIDATES, Config, EncodeRequest,
+                               TensorTable, encode_many)
+    from hi2.executor import Executor
+    from hi2.format import GROUP
+    from hi2.qad import FakeQuantLinear
+
+    torch.set_num_threads(1)
+    g = torch.Generator().manual_seed(37)
+    cands = list(ALL_CANDIDATES) + list(INT8_CANDIDATES)
+    r, k = 40, 128
+    w = torch.randn(r, k, generator=g) * torch.exp(0.4 * torch.randn(r, 1, generator=g)) * 0.05
+    cs = (torch.rand(k, generator=g) * 1.5 + 0.5).half()
+    had = (torch.arange(k // GROUP) % 3 != 1).to(torch.uint8)
+    picks = torch.randint(0, len(cands), (r,), generator=g)
+    table = TensorTable("t", (r, k), had, torch.zeros(len(cands), r), cands, 0.0, 0, cs)
+    cfg = Config(candidates=cands, rounding="nearest")
+    t0 = encode_many([EncodeRequest(w, None, table, picks)], cfg, Executor(["cpu"]))[0]
+    arrs = {"w": w.numpy(), "had": had.numpy(), "col_scale": cs.view(torch.int16).numpy()}
+    for tag, (units, zero_blocks, clamp) in QAD_CASES.items():
+        fq = FakeQuantLinear(w, t0, None, "weights", units)
+        with torch.no_grad():
+            fq.latent.add_(0.3 * fq.latent.std() * torch.randn(r, k, generator=g))
+            for gr in fq.groups:
+                gr.lo_u.add_(0.7 * torch.randn(gr.lo_u.shape, generator=g))
+                gr.step_u.add_(0.7 * torch.randn(gr.step_u.shape, generator=g))
+                if zero_blocks:
+                    gr.step_u[::3, ::2] = 0.0
+                    gr.lo_u[1::4] += 40.0
+            fq.project()
+            if clamp:
+                fq.latent[:, :16] += 50.0 * fq.latent.abs().max()
+        params = [fq.latent] + [p for gr in fq.groups for p in (gr.lo_u, gr.step_u)]
+        grad = torch.randn(r, k, generator=g)
+        grad2 = torch.randn(r, k, generator=g)
+        stored = fq.stored(False).detach()
+        st_grads = torch.autograd.grad(fq.stored(True), params, grad)
+        orig = fq()
+        or_grads = torch.autograd.grad(orig, params, grad2)
+        p = f"{tag}_"
+        arrs[p + "latent"] = fq.latent.detach().numpy()
+        arrs[p + "unit"] = fq.unit.numpy()
+        arrs[p + "ngroups"] = np.array(len(fq.groups), np.int64)
+        for gi, gr in enumerate(fq.groups):
+            q = f"{p}g{gi}_"
+            arrs[q + "rows"] = gr.rows.numpy()
+            arrs[q + "consts"] = gr.consts.view(torch.int16).numpy()
+            arrs[q + "spec"] = np.array([gr.nbits, gr.block], np.int64)
+            arrs[q + "lo_u"] = gr.lo_u.detach().numpy()
+            arrs[q + "st_u"] = gr.step_u.detach().numpy()
+            arrs[q + "g_lo"] = st_grads[1 + 2 * gi].numpy()
+            arrs[q + "g_st"] = st_grads[2 + 2 * gi].numpy()
+            arrs[q + "og_lo"] = or_grads[1 + 2 * gi].numpy()
+            arrs[q + "og_st"] = or_grads[2 + 2 * gi].numpy()
+        arrs[p + "grad"] = grad.numpy()
+        arrs[p + "grad2"] = grad2.numpy()
+        arrs[p + "stored"] = stored.numpy()
+        arrs[p + "g_latent"] = st_grads[0].numpy()
+        arrs[p + "original"] = orig.detach().numpy()
+        arrs[p + "og_latent"] = or_grads[0].numpy()
+    np.savez_compressed(os.path.join(OUT, "qad.npz"), **arrs)
+
+
 def main():
+    if sys.argv[1:] == ["qad"]:
+        make_qad()
+        return
     if sys.argv[1:] == ["encode_many"]:
         make_encode_many()
         return
@@ -354,6 +430,7 @@ def main():
     make_refine()
     make_colstats()
     make_encode_many()
+    make_qad()
 
     with open(os.path.join(OUT, "golden_meta.txt"), "w") as f:
         for k, v in meta.items():

@@ -108,3 +108,27 @@ def encode_many_case():
                             effort=effort, out=out,
                             factors=[g[f"{tag}_u{j}"] for j in range(int(g[f"{tag}_nfactors"]))])
     return cands, tensors, configs
+
+
+def qad_cases():
+    """The reference QAD fixture (tests/golden/qad.npz, hi2.qad.FakeQuantLinear's torch
+    graph).  Yields (tag, case): latent [R, K], unit [R, K] or None, had, col_scale (fp16
+    bits), groups (rows, consts (fp16 bits), nbits, block, lo_u, st_u and the reference's
+    gradients g_lo/g_st of the stored values and og_lo/og_st of the original-basis
+    weights), grad / grad2 (the output gradients), stored, g_latent, original, og_latent."""
+    g = np.load(os.path.join(GOLDEN, "qad.npz"))
+    for tag in ("abs", "step", "clamp"):
+        p = f"{tag}_"
+        unit = g[p + "unit"]
+        case = dict(latent=g[p + "latent"], unit=unit if unit.size else None, had=g["had"],
+                    col_scale=g["col_scale"].view(np.uint16), w=g["w"], groups=[])
+        for gi in range(int(g[p + "ngroups"])):
+            q = f"{p}g{gi}_"
+            nbits, block = (int(v) for v in g[q + "spec"])
+            grp = {f: g[q + f] for f in ("rows", "lo_u", "st_u", "g_lo", "g_st", "og_lo",
+                                          "og_st")}
+            grp.update(consts=g[q + "consts"].view(np.uint16), nbits=nbits, block=block)
+            case["groups"].append(grp)
+        for f in ("grad", "grad2", "stored", "g_latent", "original", "og_latent"):
+            case[f] = g[p + f]
+        yield tag, case

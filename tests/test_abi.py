@@ -59,6 +59,17 @@ def test_argument_errors_come_back_as_status_without_a_gpu():
     assert rc == _lib.EINVAL and "bad shape" in _lib.last_error()
     assert lib.hi2x_refine_workspace_bytes(4, 256, 2) >= 2 * 4 * 256 * 4
     assert lib.hi2x_refine_workspace_bytes(-1, 256, 2) == -1
+    rc = lib.hi2x_qad_decode_fwd(None, None, None, None, None, None, 4, 4, 128, 24, 3.0, None,
+                                 None)
+    assert rc == _lib.EINVAL and "16, 32 or 64" in _lib.last_error()
+    rc = lib.hi2x_qad_decode_bwd(None, None, None, None, None, None, None, 4, 4, 96, 64, 3.0,
+                                 None, None, None, None)
+    assert rc == _lib.EINVAL and "multiple of the block" in _lib.last_error()
+    rc = lib.hi2x_qad_wht_scale(None, 2, 24, None, None, 0, None, None)
+    assert rc == _lib.EINVAL and "multiple of 16" in _lib.last_error()
+    rc = lib.hi2x_qad_wht_scale(ctypes.c_void_p(8), 2, 32, None, None, 0, ctypes.c_void_p(16),
+                                None)
+    assert rc == _lib.EINVAL and "aligned" in _lib.last_error()
     rc = lib.hi2x_timing_query(0, None, None, None)
     assert rc == _lib.EINVAL and "null" in _lib.last_error()
     _lib.timing_enable([])  # nothing recorded yet: no HIP call is made
@@ -111,6 +122,13 @@ def test_python_surface_matches_the_reference_modules():
     for name in ("_fname", "_upper", "sigma_payload", "load_sigma"):
         assert hasattr(ch, name), name
     assert sts.TOKEN_CHUNK == 4096
+    import hi2_amd.qad_kernel as qk
+
+    for name in ("load", "available", "failure", "original", "stored", "supported",
+                 "kernel_dir", "_StoredDecode", "_Transform"):
+        assert hasattr(qk, name), name
+    for name in ("decode_fwd", "decode_bwd", "wht_scale"):
+        assert hasattr(qk._Kernels, name), name
     import hi2_amd.calibrate as cal
 
     for name in ("ALL_CANDIDATES", "INT8_CANDIDATES", "SELECTABLE", "Config", "TensorTable",
