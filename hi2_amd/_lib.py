@@ -227,6 +227,15 @@ def h2d(t: torch.Tensor, dev: torch.device) -> torch.Tensor:
     return out
 
 
+def to_device(t: torch.Tensor, dev: torch.device, dtype: torch.dtype | None = None
+              ) -> torch.Tensor:
+    """``t.to(dev, dtype)`` without a host wait: a host tensor goes through :func:`h2d`
+    (torch's pageable copy would synchronise the current stream)."""
+    if t.device.type == "cpu":
+        return h2d(t if dtype is None else t.to(dtype), dev)
+    return t.to(dev) if dtype is None else t.to(dev, dtype)
+
+
 def workspace(dev: torch.device, size_fn: str, *args) -> torch.Tensor:
     """A device workspace for an entry point, from torch's caching allocator on the
     current stream (so concurrent streams never share a block): ``size_fn`` is the

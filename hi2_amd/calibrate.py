@@ -194,6 +194,7 @@ class _Chain:
     status: torch.Tensor
     perm: torch.Tensor | None
     jobs: list = field(default_factory=list)  # indices into the device's job list
+    reqs: list = field(default_factory=list)  # the requests that read this input
 
 
 def _rows_of(picks_host: torch.Tensor, lo: int, hi: int, ci: int) -> torch.Tensor:
@@ -229,10 +230,12 @@ def _round_chain(ch, reqs, jobs, job_at, encs, cfg) -> None:
         _refine_chain(ch, reqs, jobs, job_at, encs, cfg.refine_passes)
 
 
-def _on_device(reqs, cfg, ex, i: int, use_gptq, comp_full):
+def _on_device(reqs, cfg, ex, i: int, use_gptq, comp_full, pack=None):
     """Every request's shard ``i``.  Returns ``{request: [(rows, codes, params, consts),
     ...]}`` in candidate order, the stream each request's pieces were made on, the
-    requests in the order their work was enqueued, and the streams to join."""
+    requests in the order their work was enqueued, and the streams to join.  With
+    ``pack`` (one device), ``pack(ri, pieces, stream)`` is called for each request as soon
+    as its chain is finished, while later chains still run."""
     dev = _device(ex.devices[i])
     main = torch.cuda.current_stream(dev)
     lanes = [_lib.side_stream(dev, 64 + j) for j in range(LANES)]
@@ -293,6 +296,7 @@ def _on_device(reqs, cfg, ex, i: int, use_gptq, comp_full):
                     hs = hs[perm][:, perm].contiguous()
                 u, status = _factor(hs, cfg.damp)
             ch = _Chain(st, hs, d, u, status, perm)
+            ch.reqs = groups[fk]
             chains.append(ch)
 
             def emit(ri, r, wt, had, ch=ch):
@@ -329,19 +333,27 @@ def _on_device(reqs, cfg, ex, i: int, use_gptq, comp_full):
         if near_jobs:
             for (ri, rows, slot), e in zip(near_at, encode_jobs_gptq(near_jobs, cfg.effort)):
                 pieces[ri][slot] = (rows, e.codes, e.params, e.consts)
-        # the host waits for each chain's factor status only now; a chain whose first
-        # attempt failed (the reference's damping retries) is rounded and refined again
-        for ch in chains:
+        if pack is not None:
+            for ri in near:
+                pack(ri, pieces[ri], main)
+        # the host waits for each chain's factor status only now, the chain enqueued last
+        # (the first to end) first; a chain whose first attempt failed (the reference's
+        # damping retries) is rounded and refined again; then its tensors are packed
+        for ch in reversed(chains):
             with torch.cuda.stream(ch.stream):
                 retried = finish_factor(ch.hs, ch.u, ch.status, cfg.damp)
             if retried:
                 _round_chain(ch, reqs, jobs, job_at, encs, cfg)
-        for x, (ri, rows, slot) in enumerate(job_at):
-            e = encs[x]
-            pieces[ri][slot] = (rows, e.codes, e.params, e.consts)
-            if reqs[ri].comp_out is not None:
-                with torch.cuda.stream(stream_of[ri]):
-                    comp_full[ri].index_copy_(0, _to_device(rows, dev), e.comp)
+            for x in ch.jobs:
+                ri, rows, slot = job_at[x]
+                e = encs[x]
+                pieces[ri][slot] = (rows, e.codes, e.params, e.consts)
+                if reqs[ri].comp_out is not None:
+                    with torch.cuda.stream(ch.stream):
+                        comp_full[ri].index_copy_(0, _to_device(rows, dev), e.comp)
+            if pack is not None:
+                for ri in ch.reqs:
+                    pack(ri, pieces[ri], ch.stream)
     return pieces, stream_of, enqueued, lanes
 
 
@@ -358,32 +370,35 @@ def encode_many(reqs: list, cfg, ex=None) -> list[HI2Tensor]:
         ri: torch.zeros(tuple(r.table.shape), dtype=torch.float32, device=first)
         for ri, r in enumerate(reqs) if r.comp_out is not None
     }
-    per_dev = [_on_device(reqs, cfg, ex, i, use_gptq, comp_full) for i in range(n_dev)]
-    # a tensor whose pieces all came from one chain is packed on that chain's stream (the
-    # host waits for that chain only); otherwise on the caller's stream after a join
     main = torch.cuda.current_stream(first)
     out: list[HI2Tensor | None] = [None] * len(reqs)
-    # pack in the reverse of the enqueue order: the widest chain, enqueued first, ends last
-    pack = list(dict.fromkeys(ri for _, _, enq, _ in per_dev for ri in reversed(enq)))
-    for ri in pack + [ri for ri in range(len(reqs)) if ri not in pack]:
+
+    def pack(ri, pieces, st):
+        """Packing (range check, D2H) of request ri on stream st: the host waits for st."""
         r = reqs[ri]
         t = r.table
-        pieces = [p for pd, _, _, _ in per_dev for p in pd.get(ri, []) if p is not None]
-        streams = {id(s): s for _, so, _, _ in per_dev for s in [so.get(ri)] if s is not None}
-        st = next(iter(streams.values())) if len(streams) == 1 else main
-        if st is main:
-            for s in streams.values():
-                main.wait_stream(s)
+        pieces = [p for p in pieces if p is not None]
+        if not pieces:
+            raise ValueError(f"{t.name}: no rows to encode")
         picks = r.picks.detach().cpu().tolist()
         nbits = torch.tensor([t.candidates[c][0] for c in picks])
         block = torch.tensor([t.candidates[c][1] for c in picks])
         with torch.cuda.stream(st):
-            if not pieces:
-                raise ValueError(f"{t.name}: no rows to encode")
             out[ri] = assemble(pieces, nbits, block, t.had, t.shape[1], t.col_scale,
                                stager=_Pinned)
             if r.comp_out is not None:
                 r.comp_out["comp"] = _Pinned.to_host(comp_full[ri])
+
+    if n_dev == 1:
+        # one device: every tensor is packed on its chain's stream as soon as the chain ends
+        per_dev = [_on_device(reqs, cfg, ex, 0, use_gptq, comp_full, pack)]
+    else:
+        per_dev = [_on_device(reqs, cfg, ex, i, use_gptq, comp_full) for i in range(n_dev)]
+        for _, _, _, lanes in per_dev:
+            for s in lanes:
+                main.wait_stream(s)
+        for ri in range(len(reqs)):
+            pack(ri, [p for pd, _, _, _ in per_dev for p in pd.get(ri, [])], main)
     for _, _, _, lanes in per_dev:
         for s in lanes:
             main.wait_stream(s)

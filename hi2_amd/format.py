@@ -44,7 +44,7 @@ def fwht_groups(x: torch.Tensor, flags: torch.Tensor) -> torch.Tensor:
     dev = _lib.require_gpu(x)
     work = x.dtype if x.dtype in (torch.float32, torch.float64) else torch.float64
     xi = x.to(work).contiguous()
-    fl = flags.to(dev, torch.uint8).reshape(-1).contiguous()
+    fl = _lib.to_device(flags.reshape(-1), dev, torch.uint8).contiguous()
     out = torch.empty_like(xi)
     rows = xi.numel() // k if k else 0
     _lib.call("hi2x_fwht16", dev, _lib.ptr(xi), _lib.ptr(out), 0 if work == torch.float32 else 1,

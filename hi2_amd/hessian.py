@@ -136,12 +136,12 @@ class HessianStats:
         if s.dtype != torch.float32 or not s.is_contiguous():
             return transform_sigma(self.mean(), col_scale, had)
         dev = s.device
-        fl = had.to(dev, torch.uint8).reshape(-1).contiguous()
+        fl = _lib.to_device(had.reshape(-1), dev, torch.uint8).contiguous()
         if fl.numel() != k // GROUP:
             raise ValueError(f"had has {fl.numel()} entries, expected {k // GROUP}")
         cs = None
         if col_scale is not None:
-            cs = col_scale.to(dev, torch.float16).reshape(-1).contiguous()
+            cs = _lib.to_device(col_scale.reshape(-1), dev, torch.float16).contiguous()
         out = torch.empty_like(s)
         _lib.call("hi2x_sigma_transform_upper", dev, _lib.ptr(s), self.n, _lib.ptr(cs),
                   _lib.ptr(fl), k, _lib.ptr(out))
@@ -158,12 +158,12 @@ def transform_sigma(
         raise ValueError(f"K={k} must be a multiple of {GROUP}")
     dev = _lib.require_gpu(sigma)
     s = sigma.to(torch.float32).contiguous()
-    fl = had.to(dev, torch.uint8).reshape(-1).contiguous()
+    fl = _lib.to_device(had.reshape(-1), dev, torch.uint8).contiguous()
     if fl.numel() != k // GROUP:
         raise ValueError(f"had has {fl.numel()} entries, expected {k // GROUP}")
     cs = None
     if col_scale is not None:
-        cs = col_scale.to(dev, torch.float16).reshape(-1).contiguous()
+        cs = _lib.to_device(col_scale.reshape(-1), dev, torch.float16).contiguous()
     out = torch.empty_like(s)
     _lib.call("hi2x_sigma_transform", dev, _lib.ptr(s), _lib.ptr(cs), _lib.ptr(fl), k,
               _lib.ptr(out))

@@ -63,7 +63,8 @@ def objective(
 ) -> float:
     """Sum over rows of ``e Hs e^T`` for the decoded codes (``hi2/refine.py:23-36``)."""
     n = w.shape[0]
-    e, g = _gradient(w, codes, lo, step, torch.full((n,), int(block), dtype=torch.int32), hs)
+    e, g = _gradient(w, codes, lo, step,
+                     torch.full((n,), int(block), dtype=torch.int32, device=w.device), hs)
     return float((g * e).sum())
 
 
@@ -105,7 +106,7 @@ def refine_expanded(
     cf = codes.float()
     if bool(((cf < 0) | (cf > 255) | (cf != cf.round())).any()):
         raise RuntimeError("codes must be integers in [0, 255]")
-    ones = torch.ones(n, dtype=torch.int32)
+    ones = torch.ones(n, dtype=torch.int32, device=w.device)
     out = _run(w, cf.to(torch.uint8), lo_x, st_x, ones, top.float(), hs, passes)
     return out.float()
 
@@ -124,8 +125,9 @@ def refine_codes(
     ladders ``lo`` and ``step`` ``[N, K / block]``; returns codes of the dtype of ``codes``
     (``hi2/refine.py:109-122``)."""
     n = w.shape[0]
-    out = _run(w, codes.to(torch.uint8), lo, step, torch.full((n,), int(block), dtype=torch.int32),
-               torch.full((n,), float(2**nbits - 1)), hs, passes)
+    out = _run(w, codes.to(torch.uint8), lo, step,
+               torch.full((n,), int(block), dtype=torch.int32, device=w.device),
+               torch.full((n,), float(2**nbits - 1), device=w.device), hs, passes)
     return out.to(codes.dtype)
 
 
@@ -151,8 +153,9 @@ def refine_groups(groups, hs: torch.Tensor, passes: int) -> list[torch.Tensor]:
     for w, enc, nbits, block in groups:
         lo, step = _decoded(enc)
         n = w.shape[0]
-        parts.append((w, enc.codes, lo, step, torch.full((n,), int(block), dtype=torch.int32),
-                      torch.full((n,), float(2**nbits - 1))))
+        parts.append((w, enc.codes, lo, step,
+                      torch.full((n,), int(block), dtype=torch.int32, device=dev),
+                      torch.full((n,), float(2**nbits - 1), device=dev)))
     ldp = max(p[2].shape[1] for p in parts)
     pad = lambda t: torch.nn.functional.pad(t.to(dev), (0, ldp - t.shape[1]))  # noqa: E731
     w = torch.cat([p[0].to(dev, torch.float32) for p in parts])

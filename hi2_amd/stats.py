@@ -60,12 +60,12 @@ class ColumnStats:
         s = self.S.to(torch.float64).contiguous()
         fl = None
         if flags is not None:
-            fl = flags.to(dev, torch.uint8).reshape(-1).contiguous()
+            fl = _lib.to_device(flags.reshape(-1), dev, torch.uint8).contiguous()
             if fl.numel() != self.k // GROUP:
                 raise ValueError(f"flags has {fl.numel()} entries, expected {self.k // GROUP}")
         inv = None
         if inv_scale is not None:
-            inv = inv_scale.to(dev, torch.float32).reshape(-1).contiguous()
+            inv = _lib.to_device(inv_scale.reshape(-1), dev, torch.float32).contiguous()
         out = torch.empty(self.k, dtype=torch.float32, device=dev)
         _lib.call("hi2x_colstats_diag", dev, _lib.ptr(s), self.k, int(self.n), _lib.ptr(fl),
                   _lib.ptr(inv), _lib.ptr(out))
