@@ -229,3 +229,39 @@ def test_encode_many_at_width_1024_equals_the_oracle(dev, monkeypatch):
         if wc is not None:
             assert np.array_equal(r.comp_out["comp"].numpy(), wc)
 
+
+
+def test_encode_many_at_the_configuration_widths_equals_per_tensor_reference(dev):
+    """cfg3 widths: a down_proj-shaped tensor (1024 x 14336 rows of the 4096) and a q/k
+    pair on one K=4096 input (k with comp), INT2/B32 and INT4/B64 rows, smoothing and
+    rotation: encode_many equals the per-tensor reference path bit for bit."""
+    from hi2_amd.calibrate import (Config, EncodeRequest, Executor, TensorTable, encode_many,
+                                   encode_with_picks_reference)
+
+    print("encode_many cfg3 widths", flush=True)
+    g = torch.Generator(device=dev).manual_seed(11)
+    cands = [(2, 32), (4, 64)]
+    reqs = []
+    for inp, k, tensors in (("down", 14336, (("down_proj", 1024, False),)),
+                            ("attn", 4096, (("q_proj", 512, False), ("k_proj", 256, True)))):
+        x = torch.randn(2048, k, generator=g, device=dev)
+        x[:, torch.randperm(k, generator=g, device=dev)[: k // 100]] *= 20.0
+        sigma = (x.T @ x) / 2048
+        sigma = ((sigma + sigma.T) * 0.5).cpu()
+        cs = (torch.rand(k, generator=g, device=dev) + 0.5).half().cpu()
+        had = (torch.arange(k // 16) % 5 != 0).to(torch.uint8)
+        for name, rows, comp in tensors:
+            w = (torch.randn(rows, k, generator=g, device=dev) * 0.02).to(torch.bfloat16).cpu()
+            picks = (torch.rand(rows, generator=g, device=dev) > 0.3).long().cpu()
+            table = TensorTable(name, (rows, k), had, torch.zeros(1), cands, 0.0, 2048, cs)
+            reqs.append(EncodeRequest(w, None, table, picks, sigma, inp, {} if comp else None))
+    cfg = Config(candidates=cands)
+    ex = Executor([str(dev)])
+    got = encode_many(reqs, cfg, ex)
+    for r, o in zip(reqs, got):
+        co = {} if r.comp_out is not None else None
+        ref = encode_with_picks_reference(r.w, r.stats, r.table, r.picks, cfg, ex, r.sigma, co)
+        for f in FIELDS:
+            assert torch.equal(getattr(o, f), getattr(ref, f)), (r.table.name, f)
+        if co is not None:
+            assert torch.equal(r.comp_out["comp"], co["comp"])
