@@ -62,10 +62,13 @@ __global__ __launch_bounds__(QT) void qad_decode_fwd_kernel(
     const float* __restrict__ lo_u, const float* __restrict__ st_u,
     const uint16_t* __restrict__ consts, const int64_t* __restrict__ rows, int64_t n_rows,
     int64_t r_total, int64_t k, int shift, float nmax, float* __restrict__ out) {
-  const int64_t k4 = k >> 2;
-  const int64_t i = (int64_t)blockIdx.x * QT + threadIdx.x;
-  if (i >= n_rows * k4) return;
-  const int64_t r = i / k4, c0 = (i - r * k4) << 2;
+  // thread (row, column quad); the host keeps n_rows * k / 4 below 2^31, so the index
+  // arithmetic is 32-bit (a 64-bit division is a long emulated sequence on the SIMD)
+  const uint32_t k4 = (uint32_t)(k >> 2);
+  const uint32_t i = blockIdx.x * QT + threadIdx.x;
+  if (i >= (uint32_t)n_rows * k4) return;
+  const uint32_t r32 = i / k4;
+  const int64_t r = r32, c0 = (int64_t)(i - r32 * k4) << 2;
   const int64_t row = rows[r];
   if (row < 0 || row >= r_total) return;  // a row outside the latent is skipped
   const int64_t nblk = k >> shift, b = c0 >> shift;
@@ -103,15 +106,16 @@ __global__ __launch_bounds__(QT) void qad_decode_bwd_kernel(
     const int64_t* __restrict__ rows, int64_t n_rows, int64_t r_total, int64_t k, int shift,
     float nmax, float* __restrict__ g_latent, float* __restrict__ g_lo,
     float* __restrict__ g_st) {
-  const int64_t k4 = k >> 2;
-  const int64_t i = (int64_t)blockIdx.x * QT + threadIdx.x;
-  const bool valid = i < n_rows * k4;
+  const uint32_t k4 = (uint32_t)(k >> 2);
+  const uint32_t i = blockIdx.x * QT + threadIdx.x;
+  const bool valid = i < (uint32_t)n_rows * k4;
   float4 a_lo = make_float4(0.f, 0.f, 0.f, 0.f), a_st = a_lo;
   int64_t r = 0, c0 = 0, b = 0;
   const int64_t nblk = k >> shift;
   if (valid) {
-    r = i / k4;
-    c0 = (i - r * k4) << 2;
+    const uint32_t r32 = i / k4;
+    r = r32;
+    c0 = (int64_t)(i - r32 * k4) << 2;
     b = c0 >> shift;
   }
   // a row outside the latent is skipped: no access, its block gradients read 0
@@ -172,14 +176,15 @@ __global__ __launch_bounds__(QT) void qad_decode_bwd_kernel(
 __global__ __launch_bounds__(QT) void qad_wht_scale_kernel(
     const float* __restrict__ x, int64_t n_rows, int64_t k, const uint8_t* __restrict__ flags,
     const uint16_t* __restrict__ scale, int pre_div, float* __restrict__ out) {
-  const int64_t k4 = k >> 2;
-  const int64_t i = (int64_t)blockIdx.x * QT + threadIdx.x;
-  const bool valid = i < n_rows * k4;
+  const uint32_t k4 = (uint32_t)(k >> 2);
+  const uint32_t i = blockIdx.x * QT + threadIdx.x;
+  const bool valid = i < (uint32_t)n_rows * k4;
   float4 v = make_float4(0.f, 0.f, 0.f, 0.f), s = make_float4(1.f, 1.f, 1.f, 1.f);
-  int64_t c0 = 0;
+  int64_t c0 = 0, r = 0;
   if (valid) {
-    const int64_t r = i / k4;
-    c0 = (i - r * k4) << 2;
+    const uint32_t r32 = i / k4;
+    r = r32;
+    c0 = (int64_t)(i - r32 * k4) << 2;
     v = ld4(x + r * k + c0);
     if (scale) {
 #pragma unroll
@@ -212,7 +217,6 @@ __global__ __launch_bounds__(QT) void qad_wht_scale_kernel(
   if (scale && !pre_div) {
     o.x = o.x / s.x; o.y = o.y / s.y; o.z = o.z / s.z; o.w = o.w / s.w;
   }
-  const int64_t r = i / k4;
   st4(out + r * k + c0, o);
 }
 
@@ -238,6 +242,7 @@ extern "C" int hi2x_qad_decode_fwd(const float* latent, const float* unit, const
                "qad_decode_fwd: latent, unit and out must be 16-byte aligned");
   if (n_rows == 0) return HI2X_OK;
   const int64_t total = n_rows * (k / 4);
+  HI2X_REQUIRE(total < (int64_t(1) << 31), "qad_decode_fwd: %lld rows x K too large", (long long)n_rows);
   hipLaunchKernelGGL(qad_decode_fwd_kernel, dim3((unsigned)((total + QT - 1) / QT)), dim3(QT), 0,
                      as_stream(stream), latent, unit, lo_u, st_u, consts, rows, n_rows, r_total, k,
                      shift, nmax, out);
@@ -258,6 +263,7 @@ extern "C" int hi2x_qad_decode_bwd(const float* grad, const float* latent, const
                "qad_decode_bwd: grad, latent, unit and g_latent must be 16-byte aligned");
   if (n_rows == 0) return HI2X_OK;
   const int64_t total = n_rows * (k / 4);
+  HI2X_REQUIRE(total < (int64_t(1) << 31), "qad_decode_bwd: %lld rows x K too large", (long long)n_rows);
   hipLaunchKernelGGL(qad_decode_bwd_kernel, dim3((unsigned)((total + QT - 1) / QT)), dim3(QT), 0,
                      as_stream(stream), grad, latent, unit, lo_u, st_u, consts, rows, n_rows,
                      r_total, k, shift, nmax, g_latent, g_lo, g_st);
@@ -273,6 +279,7 @@ extern "C" int hi2x_qad_wht_scale(const float* x, int64_t n_rows, int64_t k,
   HI2X_REQUIRE(aligned16(x) && aligned16(out), "qad_wht_scale: x and out must be 16-byte aligned");
   if (n_rows == 0) return HI2X_OK;
   const int64_t total = n_rows * (k / 4);
+  HI2X_REQUIRE(total < (int64_t(1) << 31), "qad_wht_scale: %lld rows x K too large", (long long)n_rows);
   hipLaunchKernelGGL(qad_wht_scale_kernel, dim3((unsigned)((total + QT - 1) / QT)), dim3(QT), 0,
                      as_stream(stream), x, n_rows, k, flags, scale, pre_div, out);
   return launch_status("qad_wht_scale_kernel");
