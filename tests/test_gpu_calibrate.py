@@ -265,3 +265,18 @@ def test_encode_many_at_the_configuration_widths_equals_per_tensor_reference(dev
             assert torch.equal(getattr(o, f), getattr(ref, f)), (r.table.name, f)
         if co is not None:
             assert torch.equal(r.comp_out["comp"], co["comp"])
+
+
+def test_act_order_skips_refinement_as_the_reference(dev):
+    """refine_passes under act_order: the reference refines only unpermuted factors
+    (hi2/calibrate.py:339-341), so the buffers equal the unrefined per-tensor path."""
+    from hi2_amd.calibrate import Config, Executor, encode_many, encode_with_picks_reference
+
+    cfg = Config(candidates=list(CANDS), act_order=True, refine_passes=2, effort="fast")
+    ex = Executor([str(dev)])
+    reqs = _requests(dev)
+    got = encode_many(reqs, cfg, ex)
+    for r, o in zip(reqs, got):
+        ref = encode_with_picks_reference(r.w, r.stats, r.table, r.picks, cfg, ex, r.sigma)
+        for f in FIELDS:
+            assert torch.equal(getattr(o, f), getattr(ref, f)), (r.table.name, f)
