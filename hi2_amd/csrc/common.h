@@ -110,19 +110,7 @@ __device__ __forceinline__ float f16_from_bits(uint16_t b) {
   return (float)__builtin_bit_cast(_Float16, b);
 }
 
-// a / b correctly rounded, given y = a correctly rounded 1 / b (Markstein's iteration:
-// q0 = a y is within 2 ulp of a / b, the first fma correction makes it faithful and the
-// second, from a faithful quotient, is the correctly rounded one; the remainders
-// a - b q are exact in an fma).  Five dependent operations instead of the ten of the
-// scaled IEEE division sequence, for operands that are normal with a normal quotient
-// (the rounding chain's values: weights, fp16 steps and factor diagonals).
-__device__ __forceinline__ float div_rcp(float a, float b, float y) {
-  const float q0 = a * y;
-  const float r0 = __builtin_fmaf(-b, q0, a);
-  const float q1 = __builtin_fmaf(r0, y, q0);
-  const float r1 = __builtin_fmaf(-b, q1, a);
-  return __builtin_fmaf(r1, y, q1);
-}
+#include "divrcp.h"
 
 // torch.clamp(q, 0, n - 1): NaN propagates through both compares.
 __device__ __forceinline__ float clamp_code(float q, float nm) {

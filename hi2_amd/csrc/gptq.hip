@@ -26,7 +26,8 @@ namespace {
 // lane_off(q)).  The U row of step i+1 is read during step i.
 //
 // Step i (fully unrolled): every lane runs the rounding chain on its own column m=i/16
-// (the two divisions through div_rcp with the lane's precomputed reciprocals);
+// (the two divisions through the lane's precomputed reciprocals: div_rcp_code for the
+// code, div_rcp for the error, exact in the owner lane);
 // only lane q = i%16 owns column i (its U value of row i is then U[i][i]), so its error e
 // is broadcast to the row with DPP row_newbcast, and the row applies
 // w[c] -= e * U[i][c] to the columns it holds.  Columns <= i of the other lanes are dead
@@ -79,13 +80,13 @@ __device__ __forceinline__ void gptq_step(RowRegs<COMP>& R, int L, int q, float 
   const float col = R.w[m];
   const float lo_j = R.loc[m], st_j = R.stc[m];
   const float safe = (st_j == 0.0f) ? 1.0f : st_j;
-  float qv = clamp_code(__builtin_rintf(div_rcp(col - lo_j, safe, R.ys[m])), nm);
+  float qv = clamp_code(__builtin_rintf(div_rcp_code(col - lo_j, safe, R.ys[m])), nm);
   if (st_j == 0.0f) qv = 0.0f;
   const float wq = f16_round(lo_j + qv * st_j);
   const float ujj = ub[cur][m >> 2][m & 3];  // U[I][I] in the owner lane
-  const float e = div_rcp(col - wq, ujj, R.yu[m]);
-  const float eb = row_bcast<s>(e);
   const bool own = q == s;
+  const float e = div_rcp(col - wq, ujj, R.yu[m], own);  // exact where the error is kept
+  const float eb = row_bcast<s>(e);
   // the selects are pinned here (empty asm): left free, the compiler keeps every step's
   // e and code in its own register until the end of the loop, which costs occupancy
   R.er[m] = own ? e : R.er[m];

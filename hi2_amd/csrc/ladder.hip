@@ -49,13 +49,13 @@ __global__ __launch_bounds__(256) void ladder_fit_kernel(
   }
   const float span = mx - mn;
 
-  // (x - lo) / safe through the correctly rounded reciprocal of safe (div_rcp): the
-  // same quotients as the IEEE division
+  // (x - lo) / safe through the correctly rounded reciprocal of safe (div_rcp_code):
+  // the same codes as the IEEE division
   auto err_of = [&](float lo, float step) {
     const float safe = (step == 0.0f) ? 1.0f : step;
     const float ys = 1.0f / safe;
     return torch_sum_small<B>([&](int t) {
-      const float c = clamp_code(__builtin_rintf(div_rcp(x[t] - lo, safe, ys)), nm);
+      const float c = clamp_code(__builtin_rintf(div_rcp_code(x[t] - lo, safe, ys)), nm);
       const float rec = lo + c * step;
       const float df = rec - x[t];
       return dd[t] * (df * df);
@@ -83,7 +83,7 @@ __global__ __launch_bounds__(256) void ladder_fit_kernel(
     float c[B];
 #pragma unroll
     for (int t = 0; t < B; ++t)
-      c[t] = clamp_code(__builtin_rintf(div_rcp(x[t] - best_lo, safe, ys)), nm);
+      c[t] = clamp_code(__builtin_rintf(div_rcp_code(x[t] - best_lo, safe, ys)), nm);
     const float sd = torch_sum_small<B>([&](int t) { return dd[t]; });
     const float sc = torch_sum_small<B>([&](int t) { return dd[t] * c[t]; });
     const float scc = torch_sum_small<B>([&](int t) { return (dd[t] * c[t]) * c[t]; });

@@ -4,11 +4,13 @@ Mirror of the reference's ``hi2/gptq_kernel.py`` (``BLOCK_COLUMNS`` 33, ``kernel
 135-137, ``supported`` 140-145, ``load`` 148-174, ``available`` 177-180, ``failure``
 183-184, ``gptq_block`` 187-196) backed by ``hi2x_gptq_block`` of ``libhi2x.so``.
 
-The kernel keeps every row of a 64-row tile in registers (a quad of lanes per row, 32
-columns per lane) and the row group's ``U`` block in LDS; each column's error is
-broadcast across the quad with DPP and pushed into the remaining columns with the
-reference's operation order, so codes, errors and ``comp`` are bit-identical to the
-reference's column loop.
+The kernel gives each row 16 lanes (one DPP row of the wavefront), each lane holding 8
+of the block's 128 columns in registers, so a wavefront works on 4 rows and a 256-thread
+workgroup on 16; the row group's 128 x 128 ``U`` block sits in LDS.  Per column the
+owner lane rounds and computes the error, a DPP row broadcast hands it to the row's
+other 15 lanes, and every lane pushes it into its remaining columns with the reference's
+operation order, so codes, errors and ``comp`` are bit-identical to the reference's
+column loop.
 
 The library is built ahead of time (``python -m hi2_amd.build``).  ``load()`` returns
 None and records :func:`failure` when it is missing; ``HI2_GPTQ_BACKEND=kernel``

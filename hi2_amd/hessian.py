@@ -308,9 +308,10 @@ def _prepare(ji: int, job: GptqJob, s: int, step_rows: int, effort: str) -> _Uni
         raise ValueError(f"K={k} is not a multiple of the block {job.block}")
     dev = w.device
     nb = k // job.block
-    wc = w[s : s + step_rows].to(torch.float32).contiguous()
-    if wc.data_ptr() == w.data_ptr() and wc.dtype == w.dtype:
-        wc = wc.clone()
+    # always a fresh copy: the column loop writes its compensated columns into the
+    # working copy, and a row slice of an fp32 job is otherwise a view of the caller's w
+    # (at any chunk offset, not only the first)
+    wc = w[s : s + step_rows].to(torch.float32, copy=True).contiguous()
     cfg = EFFORT[effort]
     lo, step, _ = _fit(wc.reshape(-1, nb, job.block), job.d, 2**job.nbits, cfg["grid"],
                        cfg["ls"], False)

@@ -62,6 +62,8 @@ class _Kernels:
         dev = _lib.require_gpu(latent, lo_u, st_u, consts, rows, out)
         k, n = _group_args(latent, unit, lo_u, st_u, consts, rows, block)
         _check(out, torch.float32, "out")
+        if out.shape != latent.shape:
+            raise RuntimeError("out must have the latent's shape")
         if n:
             _lib.call("hi2x_qad_decode_fwd", dev, _lib.ptr(latent), _opt(unit), _lib.ptr(lo_u),
                       _lib.ptr(st_u), _lib.ptr(consts), _lib.ptr(rows), n, latent.shape[0], k,

@@ -10,8 +10,10 @@
  *   definite), HI2X_ELAUNCH (a HIP call failed), HI2X_ERANGE (a code outside the
  *   ladder).  hi2x_last_error() returns the calling thread's last message.
  *
- * The library keeps no mutable global state (the last-error text is thread-local),
- * so one host thread per device may call it concurrently.
+ * The encode path keeps no mutable global state (the last-error text is
+ * thread-local), so one host thread per device may call it concurrently.  The one
+ * process-wide mutable state is the opt-in launch-timing record of the measurement
+ * section at the end (hi2x_timing_*), which the encode path never reads.
  *
  * Reference interfaces are cited as path:line of BlivionIaG/hi2.
  */

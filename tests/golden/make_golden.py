@@ -21,7 +21,13 @@ depend on the reference's own torch-CPU arithmetic:
   gradients of both for the latent weights and both ladder bytes of every block);
 * ``hi2.calibrate.encode_many`` (factor sharing, candidate grouping, refinement,
   ``comp`` and packing of several tensors, ``hi2/calibrate.py:297-424``), with every
-  factor it computed recorded beside the packed output.
+  factor it computed recorded beside the packed output;
+* the reference's whole encode pipeline on BASELINE configurations (``e2e_*.npz``):
+  ``HessianStats`` over bf16 calibration tokens, ``mean``, ``transform_sigma``,
+  ``inverse_factor``, ``fwht_groups`` and GPTQ with packing through ``encode_many``, on
+  the seeded inputs of ``tests/e2e_recipes.py`` (cfg1 down-scaled to 512 x 512 with 512
+  and 2048 tokens, a cfg2-style mixed INT2/INT4 case, and cfg1 at its full 2048 x 2048
+  as digests and a 64-row slice).
 
 The fixtures are plain ``.npz`` data (inputs and expected outputs); nothing of the
 reference is stored.  Run from the repository root:
@@ -31,6 +37,7 @@ reference is stored.  Run from the repository root:
     python tests/golden/make_golden.py colstats   # colstats.npz only
     python tests/golden/make_golden.py encode_many  # encode_many.npz only
     python tests/golden/make_golden.py qad          # qad.npz only
+    python tests/golden/make_golden.py e2e          # e2e_*.npz only
 """
 
 import os
@@ -341,7 +348,106 @@ def make_qad():
     np.savez_compressed(os.path.join(OUT, "qad.npz"), **arrs)
 
 
+def make_e2e():
+    sys.path.insert(0, REF)
+    sys.path.insert(0, os.path.dirname(OUT))
+    import hi2.hessian as H
+    from e2e_recipes import CANDIDATES, CASES, DAMP, FULL_CASES, SLICE_ROWS, input_digests, \
+        inputs, sha, upper
+    from hi2.calibrate import Config, EncodeRequest, TensorTable, encode_many
+    from hi2.executor import Executor
+    from hi2.format import fwht_groups
+    from hi2.hessian import GptqJob, HessianStats, encode_jobs_gptq, transform_sigma
+
+    torch.set_num_threads(1)
+    orig = H.inverse_factor
+    for case, (_recipe, k, n, t, _seed) in CASES.items():
+        print(case, flush=True)
+        xb, w, picks, had = inputs(case)
+        had_t = torch.from_numpy(had)
+        st = HessianStats(k)
+        st.update(xb)
+        sigma = st.mean()
+        factors = []
+
+        def record(hs, damp=0.01):
+            u = orig(hs, damp)
+            factors.append(u.clone())
+            return u
+
+        table = TensorTable(case, (n, k), had_t.clone(), torch.zeros(len(CANDIDATES), n),
+                            list(CANDIDATES), 0.0, st.n, None)
+        req = EncodeRequest(torch.from_numpy(w), None, table, torch.from_numpy(picks), sigma,
+                            "x", {})
+        cfg = Config(candidates=list(CANDIDATES), rounding="gptq", act_order=False,
+                     refine_passes=0, effort="normal", damp=DAMP)
+        H.inverse_factor = record
+        try:
+            packed = encode_many([req], cfg, Executor(["cpu"]))[0]
+        finally:
+            H.inverse_factor = orig
+        assert len(factors) == 1
+        u = factors[0]
+        # the per-row outputs encode_many does not return (sse, the unpacked codes), from
+        # the reference's GPTQ entry on the same inputs; comp must equal encode_many's
+        hs = transform_sigma(sigma, None, had_t)
+        d = hs.diagonal().clone()
+        wt = fwht_groups(torch.from_numpy(w), had_t)
+        codes = np.zeros((n, k), np.uint8)
+        comp = np.zeros((n, k), np.float32)
+        sse = np.zeros(n, np.float32)
+        groups = []
+        for ci, (nb, b) in enumerate(CANDIDATES):
+            rows = np.nonzero(picks == ci)[0]
+            if rows.size == 0:
+                continue
+            e = encode_jobs_gptq([GptqJob(wt[torch.from_numpy(rows)], d, u, nb, b)],
+                                 "normal", comp=True)[0]
+            codes[rows] = e.codes.numpy()
+            comp[rows] = e.comp.numpy()
+            sse[rows] = e.sse.numpy()
+            groups.append((ci, rows, e.params.numpy(), e.consts.view(torch.int16).numpy()))
+        assert np.array_equal(comp, req.comp_out["comp"].numpy())
+        meta = {"case": np.array(case), "digest_x": np.array(input_digests(case)["x"]),
+                "digest_w": np.array(input_digests(case)["w"]),
+                "digest_picks": np.array(input_digests(case)["picks"]),
+                "sigma_sha": np.array(sha(sigma.numpy())), "hs_sha": np.array(sha(hs.numpy())),
+                "u_sha": np.array(sha(u.numpy())), "codes_sha": np.array(sha(codes)),
+                "comp_sha": np.array(sha(comp)), "sse": sse,
+                "packed_sha": np.array(sha(packed.codes.numpy())),
+                "d": d.numpy(), "sigma_diag": np.diag(sigma.numpy()).copy(),
+                "u_diag": np.diag(u.numpy()).copy()}
+        if case in FULL_CASES:
+            np.savez_compressed(os.path.join(OUT, f"e2e_{case}_factor.npz"), **meta,
+                                sigma_tri=upper(sigma.numpy()), u_tri=upper(u.numpy()))
+            # codes travel packed (the reference's own words); comp in a file of its own
+            np.savez_compressed(os.path.join(OUT, f"e2e_{case}_comp.npz"), comp=comp)
+            out = {}
+            for f in ("codes", "code_off", "blk_params", "param_off", "row_nbits",
+                      "row_block"):
+                out[f"packed_{f}"] = getattr(packed, f).numpy()
+            out["packed_row_consts"] = packed.row_consts.view(torch.int16).numpy()
+            for ci, rows, params, consts in groups:
+                out[f"g{ci}_rows"] = rows
+                out[f"g{ci}_params"] = params
+                out[f"g{ci}_consts"] = consts
+            np.savez_compressed(os.path.join(OUT, f"e2e_{case}_out.npz"), **out)
+        else:
+            r = SLICE_ROWS
+            out = dict(meta, codes_slice=codes[:r], comp_slice=comp[:r],
+                       u_rows=u.numpy()[:16].copy(), sigma_rows=sigma.numpy()[:16].copy())
+            for ci, rows, params, consts in groups:
+                keep = rows < r
+                out[f"g{ci}_rows"] = rows[keep]
+                out[f"g{ci}_params"] = params[keep]
+                out[f"g{ci}_consts"] = consts[keep]
+            np.savez_compressed(os.path.join(OUT, f"e2e_{case}.npz"), **out)
+
+
 def main():
+    if sys.argv[1:] == ["e2e"]:
+        make_e2e()
+        return
     if sys.argv[1:] == ["qad"]:
         make_qad()
         return
@@ -431,6 +537,7 @@ def main():
     make_colstats()
     make_encode_many()
     make_qad()
+    make_e2e()
 
     with open(os.path.join(OUT, "golden_meta.txt"), "w") as f:
         for k, v in meta.items():

@@ -132,3 +132,52 @@ def qad_cases():
         for f in ("grad", "grad2", "stored", "g_latent", "original", "og_latent"):
             case[f] = g[p + f]
         yield tag, case
+
+
+def unpack_rows(words, code_off, row_nbits, k):
+    """Codes [R, K] uint8 of rdna_hint_flex packed words (LSB first, 32 / nbits codes per
+    int32 word, row r's words at code_off[r]:code_off[r + 1])."""
+    words = np.asarray(words).view(np.uint32)
+    out = np.zeros((len(row_nbits), k), np.uint8)
+    for r, nb in enumerate(np.asarray(row_nbits, np.int64)):
+        wr = words[int(code_off[r]):int(code_off[r + 1])]
+        per = 32 // int(nb)
+        sh = (np.arange(per, dtype=np.uint32) * np.uint32(nb))
+        out[r] = ((wr[:, None] >> sh[None, :]) & np.uint32((1 << int(nb)) - 1)).reshape(-1)
+    return out
+
+
+def e2e_case(case):
+    """The reference pipeline's fixture of an end-to-end case (tests/e2e_recipes.py, written
+    by make_golden.py e2e).  Full cases: sigma [K, K], u [K, K] (upper), d, hs_sha, codes
+    [N, K] (unpacked from the reference's packed words), comp, sse, packed fields, per
+    candidate group (rows, params, consts).  cfg1_full: digests, sse, sigma_diag, u_diag,
+    16 rows of sigma and u, and the first 64 rows' codes, comp, params and consts."""
+    from e2e_recipes import CASES, FULL_CASES, from_upper
+
+    _, k, n, _, _ = CASES[case]
+    if case not in FULL_CASES:
+        g = np.load(os.path.join(GOLDEN, f"e2e_{case}.npz"))
+        out = {f: g[f] for f in g.files}
+    else:
+        f1 = np.load(os.path.join(GOLDEN, f"e2e_{case}_factor.npz"))
+        f2 = np.load(os.path.join(GOLDEN, f"e2e_{case}_out.npz"))
+        f3 = np.load(os.path.join(GOLDEN, f"e2e_{case}_comp.npz"))
+        out = {f: f1[f] for f in f1.files}
+        out.update({f: f2[f] for f in f2.files})
+        out["comp"] = f3["comp"]
+        out["sigma"] = from_upper(out.pop("sigma_tri"), k, True)
+        out["u"] = from_upper(out.pop("u_tri"), k, False)
+        out["packed_row_consts"] = out["packed_row_consts"].view(np.uint16)
+        out["codes"] = unpack_rows(out["packed_codes"], out["packed_code_off"],
+                                   out["packed_row_nbits"], k)
+    groups = []
+    gi = 0
+    for gi in range(4):
+        if f"g{gi}_rows" in out:
+            groups.append((gi, out.pop(f"g{gi}_rows"), out.pop(f"g{gi}_params"),
+                           out.pop(f"g{gi}_consts").view(np.uint16)))
+    out["groups"] = groups
+    for f in [f for f in out if isinstance(out[f], np.ndarray) and out[f].dtype.kind == "U"]:
+        out[f] = str(out[f])
+    return out

@@ -280,3 +280,66 @@ def test_act_order_skips_refinement_as_the_reference(dev):
         ref = encode_with_picks_reference(r.w, r.stats, r.table, r.picks, cfg, ex, r.sigma)
         for f in FIELDS:
             assert torch.equal(getattr(o, f), getattr(ref, f)), (r.table.name, f)
+
+
+@pytest.mark.parametrize("passes", [0, 2])
+def test_damping_retry_reencodes_the_chain(passes, dev, monkeypatch):
+    """An indefinite Sigma (smallest eigenvalue -5 % of the mean diagonal): the first,
+    asynchronous factor attempt (damping 1 %) fails, the reference's retry ladder
+    (hi2/hessian.py:76-86) succeeds at 10 %, and encode_many rounds (and refines) the
+    chain again.  Row chunks are cut small, so chunks at an offset run alone in a batch.
+    Without refinement the buffers equal encode_with_picks_reference (synchronous
+    inverse_factor) bit for bit; with two refinement sweeps they equal the oracle's
+    composition given the retried factor."""
+    import hi2_amd.calibrate as C
+    import hi2_amd.hessian as hm
+    from hi2_amd.calibrate import (Config, EncodeRequest, Executor, TensorTable,
+                                   encode_with_picks_reference)
+
+    monkeypatch.setattr(hm, "ROW_ELEMS", 256 * 24)
+    monkeypatch.setattr(hm, "BATCH_ELEMS", 256 * 24)
+    k, t = 256, 2000
+    rng = np.random.default_rng(17)
+    x = rng.standard_normal((t, k)) * np.exp(0.5 * rng.standard_normal(k))
+    sig = x.T @ x / t
+    ev, vec = np.linalg.eigh(sig)
+    m = np.trace(sig) / k
+    sig = sig - (ev[0] + 0.05 * m) * np.outer(vec[:, 0], vec[:, 0])
+    sig = ((sig + sig.T) / 2).astype(np.float32)
+    statuses, factors = [], []
+    orig = C._factor
+
+    def record(hs, damp):
+        u, st = orig(hs, damp)
+        statuses.append(st)
+        factors.append(u)
+        return u, st
+
+    monkeypatch.setattr(C, "_factor", record)
+    cands = [(2, 32), (4, 64)]
+    had = np.ones(k // 16, np.uint8)
+    w = (rng.standard_normal((70, k)) * 0.02).astype(np.float32)
+    picks = (rng.random(70) > 0.3).astype(np.int64)
+    table = TensorTable("t", (70, k), torch.from_numpy(had), torch.zeros(1), cands, 0.0, t,
+                        None)
+    req = EncodeRequest(torch.from_numpy(w), None, table, torch.from_numpy(picks),
+                        torch.from_numpy(sig), "in")
+    cfg = Config(candidates=cands, refine_passes=passes)
+    ex = Executor([str(dev)])
+    got = C.encode_many([req], cfg, ex)[0]
+    assert len(statuses) == 1 and int(statuses[0].item()) != OK, "first attempt succeeded"
+    if passes == 0:
+        ref = encode_with_picks_reference(req.w, None, table, req.picks, cfg, ex, req.sigma)
+        for f in FIELDS:
+            assert torch.equal(getattr(got, f), getattr(ref, f)), f
+    else:
+        tensor = dict(name="t", w=w, had=had, picks=picks, col_scale=None, sigma=sig,
+                      sigma_id="in", stats=None, comp=False)
+        (want, _), = oracle.encode_many([tensor], cands, dict(
+            rounding="gptq", act_order=False, refine_passes=passes, effort="normal"),
+            [factors[0].cpu().numpy()])
+        for f in FIELDS:
+            gv = getattr(got, f)
+            gv = gv.view(torch.int16).numpy().view(np.uint16) if gv.dtype == torch.float16 \
+                else gv.numpy()
+            assert np.array_equal(gv.reshape(-1), np.asarray(want[f]).reshape(-1)), f

@@ -168,6 +168,24 @@ def test_batched_jobs_match_one_call_each(dev, monkeypatch):
         _same(got, ref)
 
 
+def test_lone_chunk_at_an_offset_leaves_the_job_rows_alone(dev, monkeypatch):
+    """An fp32 job cut into row chunks where a chunk at s > 0 runs alone in its batch
+    (K = 256, 40 rows, 16 rows per chunk, one chunk per batch): the chunk's working copy
+    must be a copy (hi2/hessian.py:211 clones), not a view of the job's rows that the
+    column loop would overwrite with compensated values.  Codes, sse and comp equal the
+    oracle bit for bit, and the job's w is unchanged."""
+    import hi2_amd.hessian as hm
+
+    monkeypatch.setattr(hm, "ROW_ELEMS", 256 * 16)
+    monkeypatch.setattr(hm, "BATCH_ELEMS", 256 * 16)
+    w, d, u, _, _ = _layer(40, 256, 9)
+    wt = T(w, dev)
+    before = wt.clone()
+    got = hm.encode_rows_gptq(wt, T(d, dev), T(u, dev), 4, 32, "normal", comp=True)
+    assert torch.equal(wt, before), "the caller's rows were modified"
+    _same(got, oracle.encode_rows_gptq(w, d, u, 4, 32, "normal"))
+
+
 def test_nearest_encode_rows_equals_oracle(dev):
     from hi2_amd.encode import encode_rows
 
