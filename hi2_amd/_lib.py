@@ -31,6 +31,7 @@ SIGNATURES = {
     "hi2x_gptq_block": [_P, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _I64, _P, _P, _P, _P, _P, _P],
     "hi2x_gptq_trailing": [_P, _I64, _I64, _I64, _I64, _P, _I64, _I64, _I64, _P, _P, _P],
     "hi2x_gptq_run": [_P, _I64, _I64, _P, _P, _P, _I64, _P, _P, _P, _P, _P, _P, _I64, _P],
+    "hi2x_gptq_run_noalloc": [_P, _I64, _I64, _P, _P, _P, _I64, _P, _P, _P, _P, _P, _I64, _P],
     "hi2x_ladder_fit": [_P, _P, _I64, _I64, _I64, _I, _P, _I, _I, _P, _P, _P, _P],
     "hi2x_params": [_P, _P, _I64, _I64, _P, _P, _P, _P, _P, _I64, _P],
     "hi2x_decode_params": [_P, _P, _P, _I64, _I64, _P, _P, _P],

@@ -6,6 +6,8 @@
 #include <stdarg.h>
 #include <stdio.h>
 
+#include <atomic>
+#include <mutex>
 #include <utility>
 
 #include <algorithm>
@@ -458,4 +460,67 @@ extern "C" int hi2x_gptq_run(float* wc, int64_t n, int64_t k, uint8_t* codes, co
     if (rc) return rc;
   }
   return HI2X_OK;
+}
+
+// ---- the column loop without allocation -------------------------------------------------
+// hi2x_gptq_run's error workspace taken from a file-scope device array instead of the
+// caller's buffer: for callers that cannot allocate device memory (code under HIP graph
+// capture, tight serving loops, harnesses that forbid hipMalloc).  Each GPU the library
+// runs on holds its own copy of the array until the process ends; its address on a device
+// is looked up once (hipGetSymbolAddress with that device current) and kept.
+namespace {
+constexpr int64_t kScratchBytes = int64_t(64) << 20;  // 64 MiB per device
+static __device__ __align__(256) float scratch[kScratchBytes / sizeof(float)];
+constexpr int kMaxDevices = 64;
+std::atomic<float*> g_scratch[kMaxDevices];
+std::mutex g_scratch_mu;
+
+// The array's device address on the current device (host code never uses the symbol
+// itself: on the host it names a stand-in, not device memory).
+int scratch_on_current_device(float** out) {
+  int dev = -1;
+  HI2X_HIP(hipGetDevice(&dev));
+  HI2X_REQUIRE(dev >= 0 && dev < kMaxDevices, "gptq_run_noalloc: device %d", dev);
+  float* p = g_scratch[dev].load(std::memory_order_acquire);
+  if (!p) {
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    p = g_scratch[dev].load(std::memory_order_relaxed);
+    if (!p) {
+      void* addr = nullptr;
+      const hipError_t e = hipGetSymbolAddress(&addr, HIP_SYMBOL(scratch));
+      if (e != hipSuccess || !addr) {
+        set_error("gptq_run_noalloc: hipGetSymbolAddress failed on device %d: %s", dev,
+                  hipGetErrorString(e));
+        return HI2X_ELAUNCH;
+      }
+      p = static_cast<float*>(addr);
+      g_scratch[dev].store(p, std::memory_order_release);
+    }
+  }
+  *out = p;
+  return HI2X_OK;
+}
+}  // namespace
+
+extern "C" int hi2x_gptq_run_noalloc(float* wc, int64_t n, int64_t k, uint8_t* codes,
+                                     const float* lo, const float* st, int64_t ldp,
+                                     const int32_t* row_grp, const int64_t* u_ptrs,
+                                     const int32_t* blk, const float* nmax, float* comp,
+                                     int64_t super_blocks, void* stream) {
+  clear_error();
+  HI2X_REQUIRE(n >= 0 && n <= (int64_t(1) << 40) && super_blocks >= 1 && super_blocks <= 64,
+               "gptq_run_noalloc: n=%lld super_blocks=%lld", (long long)n,
+               (long long)super_blocks);
+  const int64_t need = n * LMAX * super_blocks * (int64_t)sizeof(float);
+  HI2X_REQUIRE(need <= kScratchBytes,
+               "gptq_run_noalloc: %lld rows x %lld super-blocks need %lld bytes of error "
+               "scratch, more than its %lld (64 MiB); use hi2x_gptq_run with a workspace",
+               (long long)n, (long long)super_blocks, (long long)need,
+               (long long)kScratchBytes);
+  if (n == 0) return HI2X_OK;
+  float* ws = nullptr;
+  const int rc = scratch_on_current_device(&ws);
+  if (rc) return rc;
+  return hi2x_gptq_run(wc, n, k, codes, lo, st, ldp, row_grp, u_ptrs, blk, nmax, comp, ws,
+                       super_blocks, stream);
 }

@@ -75,6 +75,20 @@ int hi2x_gptq_run(float* wc, int64_t n, int64_t k, uint8_t* codes, const float* 
                   const int64_t* u_ptrs, const int32_t* blk, const float* nmax,
                   float* comp, float* err_ws, int64_t super_blocks, void* stream);
 
+/* hi2x_gptq_run without allocation: no counterpart in the reference.  For callers that
+ * cannot allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc): the same computation and results as hi2x_gptq_run,
+ * with its error workspace taken from a 64 MiB array the library holds on each GPU it
+ * runs on until the process ends (n * 128 * super_blocks * 4 bytes must fit: HI2X_EINVAL
+ * otherwise, before anything is launched).  Calls no allocating routine; call it with the
+ * stream's device current.  Every call on one GPU shares that GPU's array: calls that
+ * overlap on one GPU (concurrent streams or host threads) race and must be serialised
+ * by the caller. */
+int hi2x_gptq_run_noalloc(float* wc, int64_t n, int64_t k, uint8_t* codes, const float* lo,
+                          const float* st, int64_t ldp, const int32_t* row_grp,
+                          const int64_t* u_ptrs, const int32_t* blk, const float* nmax,
+                          float* comp, int64_t super_blocks, void* stream);
+
 /* ---- ladder fit and block parameters ---------------------------------------------- */
 
 /* fit_ladder (hi2/encode.py:53-92; grid part = ladder_grid_k, hi2/ladder_kernel.py:44-86):

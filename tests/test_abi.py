@@ -70,6 +70,10 @@ def test_argument_errors_come_back_as_status_without_a_gpu():
     rc = lib.hi2x_qad_wht_scale(ctypes.c_void_p(8), 2, 32, None, None, 0, ctypes.c_void_p(16),
                                 None)
     assert rc == _lib.EINVAL and "aligned" in _lib.last_error()
+    # the allocation-free column loop refuses a batch beyond its 64 MiB scratch first
+    rc = lib.hi2x_gptq_run_noalloc(None, 40000, 4096, None, None, None, 256, None, None, None,
+                                   None, None, 4, None)
+    assert rc == _lib.EINVAL and "64 MiB" in _lib.last_error()
     rc = lib.hi2x_timing_query(0, None, None, None)
     assert rc == _lib.EINVAL and "null" in _lib.last_error()
     _lib.timing_enable([])  # nothing recorded yet: no HIP call is made
