@@ -41,14 +41,19 @@ SIGNATURES = {
     "hi2x_pack_codes": [_P, _I64, _I64, _I, _P, _P, _P],
     "hi2x_assemble_piece": [_P, _I64, _P, _P, _P, _I64, _I, _I64, _P, _P, _P, _P, _P, _P, _P],
     "hi2x_hessian_syrk": [_P, _I, _I64, _I64, _P, _P, _I64, _P],
-    "hi2x_hessian_syrk_varlen": [_P, _I, _P, _I64, _I64, _P, _P, _I64, _P],
+    "hi2x_hessian_syrk_grouped": [_P, _I64, _I, _P, _P, _I64, _I64, _I64, _P, _I64, _I, _P,
+                                  _I64, _P],
     "hi2x_hessian_syrk_upper": [_P, _I, _I64, _I64, _P, _P, _I64, _P],
     "hi2x_hessian_mirror": [_P, _I64, _P],
+    "hi2x_hessian_blend": [_P, _I64, _I64, _I64, _P, _P, _I, _P],
+    "hi2x_sigma_transform_upper_batched": [_P, _I64, _P, _I64, _P, _P, _I64, _P, _I64, _P],
     "hi2x_sigma_transform": [_P, _P, _P, _I64, _P, _P],
     "hi2x_sigma_transform_upper": [_P, _I64, _P, _P, _I64, _P, _P],
     "hi2x_chol_lambda": [_P, _I64, _F, _I, _P, _P],
     "hi2x_chol_inv_upper": [_P, _I64, _F, _I, _P, _P, _I64, _P],
     "hi2x_chol_inv_upper_async": [_P, _I64, _F, _I, _P, _P, _P, _I64, _P],
+    "hi2x_chol_inv_upper_batched_async": [_P, _I64, _I64, _I64, _F, _I, _P, _I64, _P, _P, _I64,
+                                          _P],
     "hi2x_refine_run": [_P, _P, _I64, _I64, _P, _P, _I64, _P, _P, _P, _I64, _P, _P, _I64, _P],
     "hi2x_refine_gradient": [_P, _P, _I64, _I64, _P, _P, _I64, _P, _P, _P, _P, _P],
     "hi2x_refine_block": [_P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _I64, _P, _P, _P, _P,
@@ -64,7 +69,9 @@ SIGNATURES = {
 # workspace sizes (int64 bytes, -1 for bad arguments): name -> argtypes
 SIZES = {
     "hi2x_hessian_workspace_bytes": [_I, _I64, _I64],
+    "hi2x_hessian_grouped_workspace_bytes": [_I64, _I64, _I64],
     "hi2x_chol_workspace_bytes": [_I64],
+    "hi2x_chol_batched_workspace_bytes": [_I64, _I64],
     "hi2x_refine_workspace_bytes": [_I64, _I64, _I64],
     "hi2x_colstats_workspace_bytes": [_I64, _I64],
 }

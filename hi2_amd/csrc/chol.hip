@@ -45,6 +45,7 @@ struct GemmArgs {
   float* C;
   int64_t M, N, Kd, lda, ldb, ldc;
   float alpha, beta;
+  int64_t sA = 0, sB = 0, sC = 0;  // batch strides (elements): operand z at + z * s
 };
 
 struct MaskLower {  // keep (r, k) with k <= r
@@ -76,9 +77,13 @@ __host__ __device__ inline void tri_krange(int64_t r0, int64_t c0, int64_t T, in
 }
 
 template <int AMODE, int BMODE, bool TB, bool CLOW, int T>
-__global__ __launch_bounds__(256) void tri_gemm_kernel(GemmArgs g, int64_t tm, int64_t tn,
+__global__ __launch_bounds__(256) void tri_gemm_kernel(GemmArgs g0, int64_t tm, int64_t tn,
                                                        int super, MgSched sched) {
   constexpr int NA = T / 64;
+  GemmArgs g = g0;
+  g.A += (int64_t)blockIdx.z * g.sA;
+  g.B += (int64_t)blockIdx.z * g.sB;
+  g.C += (int64_t)blockIdx.z * g.sC;
   __shared__ MgSmemT<T> sm;
   int64_t tr, tc;
   if (sched.per_xcd > 0) {
@@ -154,8 +159,11 @@ __global__ __launch_bounds__(256) void tri_gemm_kernel(GemmArgs g, int64_t tm, i
 // consecutive k (one chunk row) each.
 __global__ __launch_bounds__(256) void split3_kernel(const float* __restrict__ X, int64_t ldx,
                                                      int64_t R, int64_t Kk, int trans, int mask,
-                                                     uint16_t* __restrict__ out, int64_t Kp) {
+                                                     uint16_t* __restrict__ out, int64_t Kp,
+                                                     int64_t sx, int64_t sout) {
   __shared__ float t[64][65];
+  X += (int64_t)blockIdx.z * sx;
+  out += (int64_t)blockIdx.z * sout;
   const int64_t r0 = (int64_t)blockIdx.y * 64, k0 = (int64_t)blockIdx.x * 64;
   const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
   // input block: rows of X are contiguous along k (!trans) or along r (trans)
@@ -218,6 +226,7 @@ struct G3Args {
   float* C;
   int64_t M, N, Kd, Kp, ldc;
   float alpha, beta;
+  int64_t sA = 0, sB = 0, sC = 0;  // batch strides (elements): operand z at + z * s
 };
 constexpr int G3_KC = 16;                 // k per stage (one MFMA k-step)
 constexpr int G3_KA = 32;                 // k alignment of the planes (Kp)
@@ -244,8 +253,12 @@ constexpr int g3_waitcnt(int vm, int lgkm) {
 }
 
 template <int AMODE, int BMODE, bool CLOW>
-__global__ __launch_bounds__(256, 2) void gemm3_kernel(G3Args g, int64_t tm, int64_t tn,
+__global__ __launch_bounds__(256, 2) void gemm3_kernel(G3Args g0, int64_t tm, int64_t tn,
                                                        MgSched sched) {
+  G3Args g = g0;
+  g.A += (int64_t)blockIdx.z * g.sA;
+  g.B += (int64_t)blockIdx.z * g.sB;
+  g.C += (int64_t)blockIdx.z * g.sC;
   __shared__ __attribute__((aligned(1024))) uint16_t SA[G3_NB][3][G3_PL];
   __shared__ __attribute__((aligned(1024))) uint16_t SB[G3_NB][3][G3_PL];
   int64_t tr, tc;
@@ -381,17 +394,19 @@ __global__ __launch_bounds__(256, 2) void gemm3_kernel(G3Args g, int64_t tm, int
 }
 
 int split3(const float* X, int64_t ldx, int64_t R, int64_t Kk, int trans, int mask,
-           uint16_t* out, int64_t Kp, hipStream_t s) {
-  const dim3 grid((unsigned)((Kp + 63) / 64), (unsigned)((R + 63) / 64));
-  hipLaunchKernelGGL(split3_kernel, grid, dim3(256), 0, s, X, ldx, R, Kk, trans, mask, out, Kp);
+           uint16_t* out, int64_t Kp, hipStream_t s, int batch = 1, int64_t sx = 0,
+           int64_t sout = 0) {
+  const dim3 grid((unsigned)((Kp + 63) / 64), (unsigned)((R + 63) / 64), (unsigned)batch);
+  hipLaunchKernelGGL(split3_kernel, grid, dim3(256), 0, s, X, ldx, R, Kk, trans, mask, out, Kp,
+                     sx, sout);
   return launch_status("split3_kernel");
 }
 
 template <int AMODE, int BMODE, bool CLOW>
-int gemm3(const G3Args& a, hipStream_t s) {
+int gemm3(const G3Args& a, hipStream_t s, int batch = 1) {
   if (a.M <= 0 || a.N <= 0) return HI2X_OK;
   const int64_t tm = (a.M + MG_T - 1) / MG_T, tn = (a.N + MG_T - 1) / MG_T;
-  LaunchTimer timer(HI2X_TIME_CHOL_GEMM, (double)a.M * a.N * a.Kd, s);
+  LaunchTimer timer(HI2X_TIME_CHOL_GEMM, (double)a.M * a.N * a.Kd * batch, s);
   MgSched sched = mg_balance(tm, tn, [&](int64_t sr, int64_t sc) {
     double w = 0.0;
     for (int64_t i = 0; i < MG_SUP; ++i)
@@ -405,8 +420,8 @@ int gemm3(const G3Args& a, hipStream_t s) {
     return w;
   });
   const int64_t grid = sched.per_xcd > 0 ? mg_sched_grid(sched) : (tm * tn + 7) / 8 * 8;
-  hipLaunchKernelGGL((gemm3_kernel<AMODE, BMODE, CLOW>), dim3((unsigned)grid), dim3(256), 0, s,
-                     a, tm, tn, sched);
+  hipLaunchKernelGGL((gemm3_kernel<AMODE, BMODE, CLOW>), dim3((unsigned)grid, 1, (unsigned)batch),
+                     dim3(256), 0, s, a, tm, tn, sched);
   return launch_status("gemm3_kernel");
 }
 
@@ -421,18 +436,19 @@ static bool chol_split() {
 }
 
 template <int AMODE, int BMODE, bool TB, bool CLOW>
-int tri_gemm(const GemmArgs& a, hipStream_t s) {
+int tri_gemm(const GemmArgs& a, hipStream_t s, int batch = 1) {
   if (a.M <= 0 || a.N <= 0) return HI2X_OK;
   const int64_t tm = (a.M + MG_T - 1) / MG_T, tn = (a.N + MG_T - 1) / MG_T;
   const int64_t ntiles = tm * tn;
   // every product here has one triangular operand or output: M*N*rank useful flops
-  LaunchTimer timer(HI2X_TIME_CHOL_GEMM, (double)a.M * a.N * a.Kd, s);
+  LaunchTimer timer(HI2X_TIME_CHOL_GEMM, (double)a.M * a.N * a.Kd * batch, s);
   if ((CLOW ? ntiles / 2 : ntiles) < 128) {
     // a small grid: 64-tiles, four times the workgroups for a quarter of the work each
     const int64_t tm6 = (a.M + 63) / 64, tn6 = (a.N + 63) / 64;
     const int64_t grid = (tm6 * tn6 + 7) / 8 * 8;
-    hipLaunchKernelGGL((tri_gemm_kernel<AMODE, BMODE, TB, CLOW, 64>), dim3((unsigned)grid),
-                       dim3(256), 0, s, a, tm6, tn6, 0, MgSched{});
+    hipLaunchKernelGGL((tri_gemm_kernel<AMODE, BMODE, TB, CLOW, 64>),
+                       dim3((unsigned)grid, 1, (unsigned)batch), dim3(256), 0, s, a, tm6, tn6, 0,
+                       MgSched{});
     return launch_status("tri_gemm_kernel");
   }
   // big grids (several rounds of the 512 workgroup slots): super-tiles balanced over the
@@ -456,8 +472,9 @@ int tri_gemm(const GemmArgs& a, hipStream_t s) {
   const int64_t grid = sched.per_xcd > 0 ? mg_sched_grid(sched)
                        : super            ? mg_super_grid(tm, tn, CLOW)
                                           : (ntiles + 7) / 8 * 8;
-  hipLaunchKernelGGL((tri_gemm_kernel<AMODE, BMODE, TB, CLOW, MG_T>), dim3((unsigned)grid),
-                     dim3(256), 0, s, a, tm, tn, super, sched);
+  hipLaunchKernelGGL((tri_gemm_kernel<AMODE, BMODE, TB, CLOW, MG_T>),
+                     dim3((unsigned)grid, 1, (unsigned)batch), dim3(256), 0, s, a, tm, tn, super,
+                     sched);
   return launch_status("tri_gemm_kernel");
 }
 
@@ -468,7 +485,10 @@ int tri_gemm(const GemmArgs& a, hipStream_t s) {
 // Thread q < 4 runs accumulator q; the diagonal is staged through LDS in chunks.
 __global__ __launch_bounds__(256) void diag_mean_kernel(const float* __restrict__ hs, int64_t K,
                                                         float damp, float p10,
-                                                        float* __restrict__ lam_out) {
+                                                        float* __restrict__ lam_out,
+                                                        int64_t shs, int64_t slam) {
+  hs += (int64_t)blockIdx.z * shs;
+  lam_out += (int64_t)blockIdx.z * slam;
   // Accumulator q adds element q of every row of 4 in row order; within a step of
   // `step` rows it starts from zero (the cascade moved it up at the previous step end),
   // so the step sums are independent: all threads form them in parallel (each one the
@@ -534,7 +554,11 @@ __global__ __launch_bounds__(256) void diag_mean_kernel(const float* __restrict_
 __global__ __launch_bounds__(256) void reverse_damp_kernel(const float* __restrict__ hs,
                                                            int64_t K,
                                                            const float* __restrict__ lam,
-                                                           float* __restrict__ P) {
+                                                           float* __restrict__ P, int64_t shs,
+                                                           int64_t slam, int64_t sP) {
+  hs += (int64_t)blockIdx.z * shs;
+  lam += (int64_t)blockIdx.z * slam;
+  P += (int64_t)blockIdx.z * sP;
   const int64_t i = (int64_t)blockIdx.y;
   const float l = *lam;
   for (int64_t j = threadIdx.x + (int64_t)blockIdx.x * blockDim.x; j <= i;
@@ -779,8 +803,10 @@ __device__ __forceinline__ void leaf_store(const float* S, int so, float* P, int
 }
 
 __global__ __launch_bounds__(256) void leaf_kernel(float* __restrict__ P, int64_t K, int64_t r0,
-                                                   int n, int* __restrict__ status) {
+                                                   int n, int* __restrict__ status, int64_t sP) {
   __shared__ float S[NB * LP];
+  P += (int64_t)blockIdx.z * sP;
+  status += blockIdx.z;
   float* blk = P + r0 * K + r0;
   leaf_load(S, 0, blk, K, n);
   __syncthreads();
@@ -795,8 +821,10 @@ __global__ __launch_bounds__(256) void leaf_kernel(float* __restrict__ P, int64_
 //   S_A = leaf(A11) -> A11;  S_B = A21;  T1 = S_B S_A^T -> S_B;  T2 = T1 S_A -> S_A;
 //   S_B = A22 - T1 T1^T (lower);  S_B = leaf(S_B) -> A22;  A21 = -S_B T2.
 __global__ __launch_bounds__(256) void node_kernel(float* __restrict__ P, int64_t K, int64_t r0,
-                                                   int m2, int* __restrict__ status) {
+                                                   int m2, int* __restrict__ status, int64_t sP) {
   __shared__ float S[2 * NB * LP];
+  P += (int64_t)blockIdx.z * sP;
+  status += blockIdx.z;
   float* a11 = P + r0 * K + r0;
   float* a21 = P + (r0 + NB) * K + r0;
   float* a22 = P + (r0 + NB) * K + (r0 + NB);
@@ -869,7 +897,9 @@ __global__ __launch_bounds__(256) void node_kernel(float* __restrict__ P, int64_
 
 // U[i][j] = Linv[K-1-i][K-1-j] for j >= i, 0 below: in place over pairs
 // {(i, j), (K-1-i, K-1-j)}, one thread per element of the upper triangle.
-__global__ __launch_bounds__(256) void reverse_out_kernel(float* __restrict__ P, int64_t K) {
+__global__ __launch_bounds__(256) void reverse_out_kernel(float* __restrict__ P, int64_t K,
+                                                          int64_t sP) {
+  P += (int64_t)blockIdx.z * sP;
   const int64_t i = (int64_t)blockIdx.y;
   for (int64_t j = i + threadIdx.x + (int64_t)blockIdx.x * blockDim.x; j < K;
        j += (int64_t)gridDim.x * blockDim.x) {
@@ -887,7 +917,10 @@ __global__ __launch_bounds__(256) void reverse_out_kernel(float* __restrict__ P,
   }
 }
 
-__global__ void status_init_kernel(int* __restrict__ status, int v) { *status = v; }
+__global__ void status_init_kernel(int* __restrict__ status, int v, int n) {
+  const int i = (int)(blockIdx.x * blockDim.x + threadIdx.x);
+  if (i < n) status[i] = v;
+}
 
 // ---- host recursion -------------------------------------------------------------------
 struct Plan {
@@ -914,6 +947,14 @@ struct Ctx {
   const Plan* plan;
   int* status;
   hipStream_t s;
+  int batch = 1;     // factors of one launch sequence (grid z)
+  int64_t sP = 0;    // floats between consecutive factors' matrices
+  int64_t sW = 0;    // floats between consecutive factors' workspaces
+  // batch stride of an operand: the workspace's for pointers into it, else the matrix's
+  int64_t stride(const void* p) const {
+    const float* f = static_cast<const float*>(p);
+    return (f >= ws && f < ws + plan->total + 64) ? sW : sP;
+  }
 };
 
 // op(B) mask of a TB / !TB product in split coordinates (row = output column j, k)
@@ -922,37 +963,46 @@ constexpr int split_mask_b(int bmode) { return bmode == 1 ? 2 : (bmode == 2 ? 1 
 // One product of the recursion: the big grids through the split planes, the small ones
 // on the fp32 MFMA GEMM.
 template <int AMODE, int BMODE, bool TB, bool CLOW>
-int product(const Ctx& c, const GemmArgs& a) {
+int product(const Ctx& c, GemmArgs a) {
   const int64_t tm = (a.M + MG_T - 1) / MG_T, tn = (a.N + MG_T - 1) / MG_T;
   const int64_t ntiles = tm * tn;
+  a.sA = c.stride(a.A);
+  a.sB = c.stride(a.B);
+  a.sC = c.stride(a.C);
   if (!chol_split() || (CLOW ? ntiles / 2 : ntiles) < 128)
-    return tri_gemm<AMODE, BMODE, TB, CLOW>(a, c.s);
+    return tri_gemm<AMODE, BMODE, TB, CLOW>(a, c.s, c.batch);
   const int64_t Kp = (a.Kd + G3_KA - 1) / G3_KA * G3_KA;
   uint16_t* pa = reinterpret_cast<uint16_t*>(c.ws + c.plan->pa_off);
   uint16_t* pb = reinterpret_cast<uint16_t*>(c.ws + c.plan->pb_off);
-  int rc = split3(a.A, a.lda, a.M, a.Kd, 0, AMODE == 1 ? 1 : 0, pa, Kp, c.s);
+  const int64_t sPl = 2 * c.sW;  // planes live in the workspace (bf16 elements)
+  int rc = split3(a.A, a.lda, a.M, a.Kd, 0, AMODE == 1 ? 1 : 0, pa, Kp, c.s, c.batch, a.sA, sPl);
   if (rc) return rc;
   const uint16_t* bp = pa;
   if (!(TB && a.B == a.A && a.ldb == a.lda && a.N == a.M && AMODE == 0 && BMODE == 0)) {
-    rc = split3(a.B, a.ldb, a.N, a.Kd, TB ? 0 : 1, split_mask_b(BMODE), pb, Kp, c.s);
+    rc = split3(a.B, a.ldb, a.N, a.Kd, TB ? 0 : 1, split_mask_b(BMODE), pb, Kp, c.s, c.batch,
+                a.sB, sPl);
     if (rc) return rc;
     bp = pb;
   }
-  return gemm3<AMODE, BMODE, CLOW>(G3Args{pa, bp, a.C, a.M, a.N, a.Kd, Kp, a.ldc, a.alpha, a.beta},
-                                   c.s);
+  G3Args g{pa, bp, a.C, a.M, a.N, a.Kd, Kp, a.ldc, a.alpha, a.beta};
+  g.sA = sPl;
+  g.sB = sPl;
+  g.sC = a.sC;
+  return gemm3<AMODE, BMODE, CLOW>(g, c.s, c.batch);
 }
 
 int inv_chol(const Ctx& c, int64_t r0, int64_t m, int depth) {
   const int64_t K = c.K;
   if (m <= NB) {
-    LaunchTimer timer(HI2X_TIME_CHOL_LEAF, 2.0 * m * m * m / 3.0, c.s);
-    hipLaunchKernelGGL(leaf_kernel, dim3(1), dim3(256), 0, c.s, c.P, K, r0, (int)m, c.status);
+    LaunchTimer timer(HI2X_TIME_CHOL_LEAF, 2.0 * m * m * m / 3.0 * c.batch, c.s);
+    hipLaunchKernelGGL(leaf_kernel, dim3(1, 1, (unsigned)c.batch), dim3(256), 0, c.s, c.P, K, r0,
+                       (int)m, c.status, c.sP);
     return launch_status("leaf_kernel");
   }
   if (m <= 2 * NB) {  // the node's split is 128 + (m - 128): one fused kernel
-    LaunchTimer timer(HI2X_TIME_CHOL_LEAF, 2.0 * m * m * m / 3.0, c.s);
-    hipLaunchKernelGGL(node_kernel, dim3(1), dim3(256), 0, c.s, c.P, K, r0, (int)(m - NB),
-                       c.status);
+    LaunchTimer timer(HI2X_TIME_CHOL_LEAF, 2.0 * m * m * m / 3.0 * c.batch, c.s);
+    hipLaunchKernelGGL(node_kernel, dim3(1, 1, (unsigned)c.batch), dim3(256), 0, c.s, c.P, K, r0,
+                       (int)(m - NB), c.status, c.sP);
     return launch_status("node_kernel");
   }
   const int64_t nbk = (m + NB - 1) / NB;
@@ -1015,29 +1065,36 @@ static Plan make_plan(int64_t k) {
 }
 static int64_t ws_floats(const Plan& p) { return p.total + 64; }
 
+// The whole chain for `batch` matrices of one size: matrix z at hs + z shs, its factor at
+// u + z su, its workspace at ws + z sw (floats), its status word at status_out + z.
 static int chol_launch(const float* hs, int64_t k, float damp, int attempt, float* u,
-                       int* status_out, float* ws, const Plan& plan, hipStream_t s) {
+                       int* status_out, float* ws, const Plan& plan, hipStream_t s,
+                       int batch = 1, int64_t shs = 0, int64_t su = 0, int64_t sw = 0) {
   float* lam = ws + plan.total;
   const int big = 0x7fffffff;
   int rc = HI2X_OK;
-  hipLaunchKernelGGL(status_init_kernel, dim3(1), dim3(1), 0, s, status_out, big);
+  hipLaunchKernelGGL(status_init_kernel, dim3((unsigned)((batch + 255) / 256)), dim3(256), 0, s,
+                     status_out, big, batch);
   rc = launch_status("status_init_kernel");
   float p10 = 1.0f;
   for (int a = 0; a < attempt; ++a) p10 *= 10.0f;
   if (!rc) {
-    hipLaunchKernelGGL(diag_mean_kernel, dim3(1), dim3(256), 0, s, hs, k, damp, p10, lam);
+    hipLaunchKernelGGL(diag_mean_kernel, dim3(1, 1, (unsigned)batch), dim3(256), 0, s, hs, k, damp,
+                       p10, lam, shs, sw);
     rc = launch_status("diag_mean_kernel");
   }
   if (!rc) {
-    const dim3 g((unsigned)((k + 255) / 256 < 16 ? (k + 255) / 256 : 16), (unsigned)k);
-    hipLaunchKernelGGL(reverse_damp_kernel, g, dim3(256), 0, s, hs, k, lam, u);
+    const dim3 g((unsigned)((k + 255) / 256 < 16 ? (k + 255) / 256 : 16), (unsigned)k,
+                 (unsigned)batch);
+    hipLaunchKernelGGL(reverse_damp_kernel, g, dim3(256), 0, s, hs, k, lam, u, shs, sw, su);
     rc = launch_status("reverse_damp_kernel");
   }
-  Ctx c{u, k, ws, &plan, status_out, s};
+  Ctx c{u, k, ws, &plan, status_out, s, batch, su, sw};
   if (!rc) rc = inv_chol(c, 0, k, 0);
   if (!rc) {  // U = J L^-1 J (garbage if the factorisation failed; the status says so)
-    const dim3 g((unsigned)((k + 255) / 256 < 16 ? (k + 255) / 256 : 16), (unsigned)k);
-    hipLaunchKernelGGL(reverse_out_kernel, g, dim3(256), 0, s, u, k);
+    const dim3 g((unsigned)((k + 255) / 256 < 16 ? (k + 255) / 256 : 16), (unsigned)k,
+                 (unsigned)batch);
+    hipLaunchKernelGGL(reverse_out_kernel, g, dim3(256), 0, s, u, k, su);
     rc = launch_status("reverse_out_kernel");
   }
   return rc;
@@ -1051,7 +1108,7 @@ extern "C" int hi2x_chol_lambda(const float* hs, int64_t k, float damp, int atte
   float p10 = 1.0f;
   for (int a = 0; a < attempt; ++a) p10 *= 10.0f;
   hipLaunchKernelGGL(diag_mean_kernel, dim3(1), dim3(256), 0, as_stream(stream), hs, k, damp,
-                     p10, lam);
+                     p10, lam, (int64_t)0, (int64_t)0);
   return launch_status("diag_mean_kernel");
 }
 
@@ -1104,4 +1161,37 @@ extern "C" int hi2x_chol_inv_upper(const float* hs, int64_t k, float damp, int a
     rc = HI2X_ENOTPD;
   }
   return rc;
+}
+
+// Workspace of one factor of a batch, rounded to 256 bytes.
+static int64_t batch_ws_floats(const Plan& p) { return (ws_floats(p) + 63) / 64 * 64; }
+
+extern "C" int64_t hi2x_chol_batched_workspace_bytes(int64_t k, int64_t batch) {
+  if (k <= 0 || batch <= 0 || batch > 65535) return -1;
+  return batch_ws_floats(make_plan(k)) * batch * (int64_t)sizeof(float);
+}
+
+extern "C" int hi2x_chol_inv_upper_batched_async(const float* hs, int64_t hs_stride, int64_t k,
+                                                 int64_t batch, float damp, int attempt,
+                                                 float* u, int64_t u_stride, int32_t* status,
+                                                 void* ws, int64_t ws_bytes, void* stream) {
+  clear_error();
+  HI2X_REQUIRE(k > 0 && hs && u && status && batch > 0 && batch <= 65535,
+               "chol_inv_upper_batched_async: bad arguments");
+  HI2X_REQUIRE(hs_stride >= k * k && u_stride >= k * k,
+               "chol_inv_upper_batched_async: strides %lld / %lld below k * k",
+               (long long)hs_stride, (long long)u_stride);
+  HI2X_REQUIRE(!(u < hs + hs_stride * batch && hs < u + u_stride * batch),
+               "chol_inv_upper_batched_async: hs and u overlap");
+  HI2X_REQUIRE(attempt >= 0 && attempt < 10, "chol_inv_upper_batched_async: attempt %d",
+               attempt);
+  hipStream_t s = as_stream(stream);
+  const Plan plan = make_plan(k);
+  const int64_t sw = batch_ws_floats(plan);
+  Workspace w;
+  const int rc = take_workspace(w, ws, ws_bytes, (size_t)(sw * batch) * sizeof(float), s,
+                                "chol_inv_upper_batched_async");
+  if (rc) return rc;
+  return chol_launch(hs, k, damp, attempt, u, status, reinterpret_cast<float*>(w.p), plan, s,
+                     (int)batch, hs_stride, u_stride, sw);
 }

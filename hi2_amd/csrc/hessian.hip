@@ -190,6 +190,94 @@ __global__ __launch_bounds__(256) void transpose_bf16_kernel(const uint16_t* __r
   }
 }
 
+// ---- routed (grouped) accumulation: one launch for every group of a token batch --------
+// Group e is the tokens j in [offs[e], offs[e+1]) of a routed batch (the rows an MoE
+// router sent to expert e, hi2/moe.py:83-100); token j is row rows[j] of x (rows NULL:
+// row j).  The plan (on the device, so the caller never waits for the counts) gives every
+// group a 64-aligned token window of the shared transposed copy and orders the groups by
+// descending token count (largest first: the longest tiles start first).
+struct SyrkGroups {
+  const int32_t* order;  // [G] groups by descending token count (ties by index)
+  const int64_t* toff;   // [G] first column of the group's window in xt
+  const int64_t* tp;     // [G] window width: the token count rounded up to 64
+  int64_t sstride;       // floats between consecutive groups' S
+  int64_t ntiles;        // upper 256-tiles per group
+};
+
+__global__ __launch_bounds__(256) void grouped_plan_kernel(const int64_t* __restrict__ offs,
+                                                           int G, int64_t t_total, int64_t cap,
+                                                           int32_t* __restrict__ order,
+                                                           int64_t* __restrict__ toff,
+                                                           int64_t* __restrict__ tp) {
+  // counts (a group outside [0, t_total] or descending offsets counts as empty)
+  for (int e = threadIdx.x; e < G; e += blockDim.x) {
+    const int64_t a = offs[e], b = offs[e + 1];
+    const bool ok = a >= 0 && b >= a && b <= t_total;
+    tp[e] = ok ? (b - a + 63) / 64 * 64 : 0;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {  // windows in group order, never past the capacity
+    int64_t o = 0;
+    for (int e = 0; e < G; ++e) {
+      if (o + tp[e] > cap) tp[e] = 0;
+      toff[e] = o;
+      o += tp[e];
+    }
+  }
+  __syncthreads();
+  for (int e = threadIdx.x; e < G; e += blockDim.x) {
+    const int64_t te = tp[e] ? offs[e + 1] - offs[e] : 0;
+    int rank = 0;
+    for (int f = 0; f < G; ++f) {
+      const int64_t tf = tp[f] ? offs[f + 1] - offs[f] : 0;
+      rank += (tf > te || (tf == te && f < e)) ? 1 : 0;
+    }
+    order[rank] = e;
+  }
+}
+
+// xt [K, cap]: column toff[e] + i of group e = token offs[e] + i (zeros past the group's
+// count); the row of token j is rows[j] (rows NULL: j), rows outside [0, x_rows) read zero.
+__global__ __launch_bounds__(256) void grouped_transpose_kernel(
+    const uint16_t* __restrict__ x, int64_t x_rows, const int64_t* __restrict__ rows,
+    const int64_t* __restrict__ offs, int G, const int64_t* __restrict__ toff,
+    const int64_t* __restrict__ tp, int64_t K, int64_t cap, uint16_t* __restrict__ xt) {
+  __shared__ uint16_t tile[64][66];
+  __shared__ int64_t grp[2];  // group of this 64-column block, its first token
+  const int64_t c0 = (int64_t)blockIdx.y * 64, k0 = (int64_t)blockIdx.x * 64;
+  if (threadIdx.x == 0) {
+    int lo = 0, hi = G - 1, e = -1;  // last group whose window starts at or before c0
+    while (lo <= hi) {
+      const int mid = (lo + hi) / 2;
+      if (toff[mid] <= c0) {
+        e = mid;
+        lo = mid + 1;
+      } else {
+        hi = mid - 1;
+      }
+    }
+    // empty windows share their start with the next group: step to the one holding c0
+    while (e >= 0 && e < G && c0 >= toff[e] + tp[e]) e = (e + 1 < G && toff[e + 1] <= c0) ? e + 1 : -1;
+    grp[0] = e;
+  }
+  __syncthreads();
+  const int e = (int)grp[0];
+  if (e < 0) return;
+  const int64_t first = offs[e] + (c0 - toff[e]), end = offs[e + 1];
+  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+  for (int y = ty; y < 64; y += 4) {
+    const int64_t j = first + y, k = k0 + tx;
+    int64_t r = -1;
+    if (j < end) r = rows ? rows[j] : j;
+    tile[y][tx] = (r >= 0 && r < x_rows && k < K) ? x[r * K + k] : (uint16_t)0;
+  }
+  __syncthreads();
+  for (int y = ty; y < 64; y += 4) {
+    const int64_t k = k0 + y, c = c0 + tx;
+    if (k < K && c < cap) xt[k * cap + c] = tile[tx][y];
+  }
+}
+
 // Operands of one k-step (16 tokens) of the current stage: XA / XB point at this lane's
 // operand row (tile t adds 32 rows), so its 16-byte slot.
 __device__ __forceinline__ void syrk_read(bf16x8 (&av)[4], bf16x8 (&bv)[4], const uint16_t* XA,
@@ -233,28 +321,43 @@ constexpr int waitcnt_imm(int vm, int lgkm) {
   return (vm & 15) | ((vm >> 4) << 14) | (7 << 4) | (lgkm << 8);
 }
 
+// T is xt's row stride (its padded token count); with grouped (gr.order not null) item
+// blockIdx.x is tile (id % ntiles) of the group of rank id / ntiles, over its window.
 __global__ __launch_bounds__(256) void syrk2_bf16_kernel(const uint16_t* __restrict__ xt,
                                                          int64_t T, int64_t K, int nT,
                                                          int64_t ntiles, int splits,
                                                          int64_t tchunk, float* __restrict__ out,
-                                                         int64_t out_stride, int super) {
+                                                         int64_t out_stride, int super,
+                                                         SyrkGroups gr) {
   __shared__ __attribute__((aligned(1024))) uint16_t Xa[S2NB][S2T * S2C];
   __shared__ __attribute__((aligned(1024))) uint16_t Xb[S2NB][S2T * S2C];
   const int64_t id = (int64_t)blockIdx.x;
   int ta, tb, sp = 0;
-  if (super) {
-    if (!syrk_super_tile(id, nT, ta, tb)) return;
+  int64_t tbeg, tend;
+  float* s;
+  if (gr.order) {
+    const int e = gr.order[id / gr.ntiles];
+    const int64_t w = gr.tp[e];
+    if (w == 0) return;
+    upper_tile(nT, (int)(id % gr.ntiles), ta, tb);
+    tbeg = gr.toff[e];
+    tend = tbeg + w;
+    s = out + (int64_t)e * gr.sstride;
   } else {
-    sp = (int)(id % splits);
-    const int64_t tile = xcd_tile(id / splits, ntiles);
-    if (tile < 0) return;
-    upper_tile(nT, (int)tile, ta, tb);
+    if (super) {
+      if (!syrk_super_tile(id, nT, ta, tb)) return;
+    } else {
+      sp = (int)(id % splits);
+      const int64_t tile = xcd_tile(id / splits, ntiles);
+      if (tile < 0) return;
+      upper_tile(nT, (int)tile, ta, tb);
+    }
+    tbeg = (int64_t)sp * tchunk;
+    tend = (tbeg + tchunk < T) ? tbeg + tchunk : T;
+    s = out + (int64_t)sp * out_stride;
   }
   const bool diag = ta == tb;
   const int64_t a0 = (int64_t)ta * S2T, b0 = (int64_t)tb * S2T;
-  const int64_t tbeg = (int64_t)sp * tchunk;
-  const int64_t tend = (tbeg + tchunk < T) ? tbeg + tchunk : T;
-  float* s = out + (int64_t)sp * out_stride;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wr = wave >> 1, wcn = wave & 1;
   f32x16 acc[4][4];
@@ -435,8 +538,10 @@ struct TileIO {
 // S[j][i] = S[i][j] for i < j: 64 x 64 tile pairs (ti <= tj) through LDS, rows of 256
 // bytes on both sides; grid (tj, ti), the workgroups below the diagonal exit at once.
 constexpr int MT = 64, MTP = MT + 1;
-__global__ __launch_bounds__(256) void mirror_kernel(float* __restrict__ s, int64_t K) {
+__global__ __launch_bounds__(256) void mirror_kernel(float* __restrict__ s, int64_t K,
+                                                     int64_t sstride) {
   __shared__ float A[MT][MTP];
+  s += (int64_t)blockIdx.z * sstride;
   const int ti = blockIdx.y, tj = blockIdx.x;
   if (ti > tj) return;
   const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
@@ -647,11 +752,21 @@ __device__ __forceinline__ void group_right(float (*B)[FTP], int row, int h, boo
   }
 }
 
+// nf: the token count (as the reference's mean divides by it); batched (ns not null):
+// matrix z = blockIdx.z at s + z * sstride / out + z * ostride over max(ns[z], 1) tokens.
 __global__ __launch_bounds__(256) void st_upper_kernel(const float* __restrict__ s, float nf,
                                                        const uint16_t* __restrict__ col_scale,
                                                        const uint8_t* __restrict__ had,
-                                                       int64_t K, float* __restrict__ out) {
+                                                       int64_t K, float* __restrict__ out,
+                                                       const int64_t* __restrict__ ns,
+                                                       int64_t sstride, int64_t ostride) {
   __shared__ float X[FT][FTP], Y[FT][FTP];
+  if (ns) {
+    const int64_t z = blockIdx.z, n = ns[z];
+    s += z * sstride;
+    out += z * ostride;
+    nf = (float)(n > 1 ? n : 1);
+  }
   const int ti = blockIdx.y, tj = blockIdx.x;
   if (ti > tj) return;
   const bool diag = ti == tj;
@@ -746,7 +861,7 @@ SyrkPlan syrk_plan(int dtype, int64_t t, int64_t k) {
 
 int launch_mirror(float* s, int64_t k, hipStream_t st) {
   const unsigned nM = (unsigned)((k + MT - 1) / MT);
-  hipLaunchKernelGGL(mirror_kernel, dim3(nM, nM), dim3(256), 0, st, s, k);
+  hipLaunchKernelGGL(mirror_kernel, dim3(nM, nM), dim3(256), 0, st, s, k, (int64_t)0);
   return launch_status("mirror_kernel");
 }
 
@@ -777,7 +892,8 @@ int launch_syrk(const void* x, int dtype, int64_t t, int64_t k, float* s, char* 
                                : (p.ntiles + 7) / 8 * 8 * p.splits;
     LaunchTimer timer(HI2X_TIME_HESSIAN_SYRK, (double)t * k * (k + 1), st);  // upper triangle
     hipLaunchKernelGGL(syrk2_bf16_kernel, dim3((unsigned)grid), dim3(256), 0, st, xt, p.tp, k,
-                       p.nT, p.ntiles, p.splits, p.tchunk, parts ? parts : s, k * k, super);
+                       p.nT, p.ntiles, p.splits, p.tchunk, parts ? parts : s, k * k, super,
+                       SyrkGroups{});
     rc = launch_status("syrk2_bf16_kernel");
   }
   if (!rc && parts) {
@@ -787,6 +903,24 @@ int launch_syrk(const void* x, int dtype, int64_t t, int64_t k, float* s, char* 
   }
   if (!rc && mirror) rc = launch_mirror(s, k, st);
   return rc;
+}
+
+// Workspace of the grouped accumulation: xt [k, cap] bf16 (cap = tokens + 64 per group,
+// the windows' worst case) and the plan tables.
+struct GroupedPlan {
+  int64_t cap = 0;
+  size_t xt_bytes = 0, order_off = 0, toff_off = 0, tp_off = 0, total = 0;
+};
+
+GroupedPlan grouped_plan(int64_t t_total, int64_t G, int64_t k) {
+  GroupedPlan p;
+  p.cap = (t_total + 64 * G + 63) / 64 * 64;
+  p.xt_bytes = ((size_t)p.cap * (size_t)k * 2 + 255) / 256 * 256;
+  p.order_off = p.xt_bytes;
+  p.toff_off = p.order_off + ((size_t)G * 4 + 255) / 256 * 256;
+  p.tp_off = p.toff_off + ((size_t)G * 8 + 255) / 256 * 256;
+  p.total = p.tp_off + ((size_t)G * 8 + 255) / 256 * 256;
+  return p;
 }
 
 }  // namespace
@@ -834,34 +968,60 @@ extern "C" int hi2x_hessian_mirror(float* s, int64_t k, void* stream) {
   return launch_mirror(s, k, as_stream(stream));
 }
 
-extern "C" int hi2x_hessian_syrk_varlen(const void* x, int dtype, const int64_t* offs,
-                                        int64_t n_groups, int64_t k, float* const* s_ptrs,
-                                        void* ws, int64_t ws_bytes, void* stream) {
+extern "C" int64_t hi2x_hessian_grouped_workspace_bytes(int64_t t_total, int64_t n_groups,
+                                                       int64_t k) {
+  if (t_total < 0 || n_groups <= 0 || n_groups > 65535 || k <= 0) return -1;
+  return (int64_t)grouped_plan(t_total, n_groups, k).total;
+}
+
+extern "C" int hi2x_hessian_syrk_grouped(const void* x, int64_t x_rows, int dtype,
+                                         const int64_t* rows, const int64_t* offs,
+                                         int64_t n_groups, int64_t t_total, int64_t k, float* s,
+                                         int64_t s_stride, int upper_only, void* ws,
+                                         int64_t ws_bytes, void* stream) {
   clear_error();
-  HI2X_REQUIRE(dtype == 0 || dtype == 2, "hessian_syrk_varlen: dtype %d", dtype);
-  HI2X_REQUIRE(k > 0 && n_groups >= 0 && offs && (n_groups == 0 || s_ptrs),
-               "hessian_syrk_varlen: bad arguments");
-  const size_t esz = dtype == 2 ? 2 : 4;
-  int64_t tmax = 0;
-  for (int64_t e = 0; e < n_groups; ++e) {
-    const int64_t t = offs[e + 1] - offs[e];
-    HI2X_REQUIRE(t >= 0, "hessian_syrk_varlen: offsets not ascending");
-    tmax = t > tmax ? t : tmax;
-  }
-  if (tmax == 0) return HI2X_OK;
+  HI2X_REQUIRE(dtype == 2, "hessian_syrk_grouped: dtype %d (bf16 tokens only: 2)", dtype);
+  HI2X_REQUIRE(x && offs && s && k > 0 && x_rows >= 0 && t_total >= 0 && n_groups > 0 &&
+                   n_groups <= 65535,
+               "hessian_syrk_grouped: bad arguments");
+  HI2X_REQUIRE(s_stride >= k * k, "hessian_syrk_grouped: s_stride %lld below k * k",
+               (long long)s_stride);
+  if (t_total == 0) return HI2X_OK;
   hipStream_t st = as_stream(stream);
-  Workspace w;  // sized for the longest group, reused by every group in stream order
-  int rc = take_workspace(w, ws, ws_bytes, syrk_plan(dtype, tmax, k).total(), st,
-                          "hessian_syrk_varlen");
+  const GroupedPlan p = grouped_plan(t_total, n_groups, k);
+  HI2X_REQUIRE(p.cap <= (int64_t(1) << 22),
+               "hessian_syrk_grouped: %lld tokens (plus 64 per group) exceed 4M per call",
+               (long long)t_total);
+  Workspace w;
+  int rc = take_workspace(w, ws, ws_bytes, p.total, st, "hessian_syrk_grouped");
   if (rc) return rc;
-  for (int64_t e = 0; e < n_groups; ++e) {
-    const int64_t t = offs[e + 1] - offs[e];
-    if (t == 0) continue;
-    const char* xe = static_cast<const char*>(x) + (size_t)offs[e] * (size_t)k * esz;
-    rc = launch_syrk(xe, dtype, t, k, s_ptrs[e], w.p, st);
-    if (rc) return rc;
+  uint16_t* xt = reinterpret_cast<uint16_t*>(w.p);
+  int32_t* order = reinterpret_cast<int32_t*>(w.p + p.order_off);
+  int64_t* toff = reinterpret_cast<int64_t*>(w.p + p.toff_off);
+  int64_t* tp = reinterpret_cast<int64_t*>(w.p + p.tp_off);
+  const int G = (int)n_groups;
+  hipLaunchKernelGGL(grouped_plan_kernel, dim3(1), dim3(256), 0, st, offs, G, t_total, p.cap,
+                     order, toff, tp);
+  rc = launch_status("grouped_plan_kernel");
+  if (rc) return rc;
+  hipLaunchKernelGGL(grouped_transpose_kernel,
+                     dim3((unsigned)((k + 63) / 64), (unsigned)(p.cap / 64)), dim3(256), 0, st,
+                     (const uint16_t*)x, x_rows, rows, offs, G, toff, tp, k, p.cap, xt);
+  rc = launch_status("grouped_transpose_kernel");
+  if (rc) return rc;
+  const int nT = (int)((k + S2T - 1) / S2T);
+  const int64_t ntiles = (int64_t)nT * (nT + 1) / 2;
+  {
+    LaunchTimer timer(HI2X_TIME_HESSIAN_SYRK, (double)t_total * k * (k + 1), st);
+    hipLaunchKernelGGL(syrk2_bf16_kernel, dim3((unsigned)(ntiles * G)), dim3(256), 0, st, xt,
+                       p.cap, k, nT, ntiles, 1, (int64_t)0, s, (int64_t)0, 0,
+                       SyrkGroups{order, toff, tp, s_stride, ntiles});
+    rc = launch_status("syrk2_bf16_kernel");
   }
-  return HI2X_OK;
+  if (rc || upper_only) return rc;
+  const unsigned nM = (unsigned)((k + MT - 1) / MT);
+  hipLaunchKernelGGL(mirror_kernel, dim3(nM, nM, (unsigned)G), dim3(256), 0, st, s, k, s_stride);
+  return launch_status("mirror_kernel");
 }
 
 extern "C" int hi2x_sigma_transform(const float* sigma, const uint16_t* col_scale,
@@ -897,6 +1057,59 @@ extern "C" int hi2x_sigma_transform_upper(const float* s, int64_t n, const uint1
   const unsigned nT = (unsigned)((k + FT - 1) / FT);
   const float nf = (float)(n > 1 ? n : 1);
   hipLaunchKernelGGL(st_upper_kernel, dim3(nT, nT), dim3(256), 0, as_stream(stream), s, nf,
-                     col_scale, had, k, hs);
+                     col_scale, had, k, hs, (const int64_t*)nullptr, (int64_t)0, (int64_t)0);
   return launch_status("st_upper_kernel");
+}
+
+extern "C" int hi2x_sigma_transform_upper_batched(const float* s, int64_t s_stride,
+                                                  const int64_t* n, int64_t batch,
+                                                  const uint16_t* col_scale, const uint8_t* had,
+                                                  int64_t k, float* hs, int64_t hs_stride,
+                                                  void* stream) {
+  clear_error();
+  HI2X_REQUIRE(k > 0 && k % 16 == 0, "sigma_transform_upper_batched: K=%lld not a multiple "
+               "of 16", (long long)k);
+  HI2X_REQUIRE(s && n && had && hs && batch > 0 && batch <= 65535,
+               "sigma_transform_upper_batched: bad arguments");
+  HI2X_REQUIRE(s_stride >= k * k && hs_stride >= k * k,
+               "sigma_transform_upper_batched: strides below k * k");
+  HI2X_REQUIRE(!(hs < s + s_stride * batch && s < hs + hs_stride * batch),
+               "sigma_transform_upper_batched: s and hs overlap");
+  const unsigned nT = (unsigned)((k + FT - 1) / FT);
+  hipLaunchKernelGGL(st_upper_kernel, dim3(nT, nT, (unsigned)batch), dim3(256), 0,
+                     as_stream(stream), s, 1.0f, col_scale, had, k, hs, n, s_stride, hs_stride);
+  return launch_status("st_upper_kernel");
+}
+
+// ---- MoE token floor (hi2/layerwise.py:245-257 with blend, hi2/moe.py:152-156) ----------
+// tot = ((0 + S_0) + S_1) + ... + S_{G-1} elementwise in fp32 (the reference's Python sum
+// over the experts' sums, taken before any is changed), then for every expert with
+// mask[e]: S_e = S_e + fill[e] * tot (fill the fp32 value of (need - n_e) / n_total).
+// Upper triangle only (upper != 0) or every element.
+__global__ __launch_bounds__(256) void blend_kernel(float* __restrict__ s, int64_t sstride,
+                                                    int G, int64_t K,
+                                                    const float* __restrict__ fill,
+                                                    const uint8_t* __restrict__ mask,
+                                                    int upper) {
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= K * K) return;
+  if (upper && idx % K < idx / K) return;
+  float tot = s[idx] + 0.0f;
+  for (int e = 1; e < G; ++e) tot = tot + s[(int64_t)e * sstride + idx];
+  for (int e = 0; e < G; ++e)
+    if (mask[e]) {
+      float* p = s + (int64_t)e * sstride + idx;
+      *p = *p + fill[e] * tot;
+    }
+}
+
+extern "C" int hi2x_hessian_blend(float* s, int64_t s_stride, int64_t n_groups, int64_t k,
+                                  const float* fill, const uint8_t* mask, int upper_only,
+                                  void* stream) {
+  clear_error();
+  HI2X_REQUIRE(s && fill && mask && k > 0 && n_groups > 0 && s_stride >= k * k,
+               "hessian_blend: bad arguments");
+  hipLaunchKernelGGL(blend_kernel, dim3((unsigned)((k * k + 255) / 256)), dim3(256), 0,
+                     as_stream(stream), s, s_stride, (int)n_groups, k, fill, mask, upper_only);
+  return launch_status("blend_kernel");
 }

@@ -60,6 +60,9 @@ __all__ = [
     "inverse_factor",
     "inverse_factor_async",
     "inverse_factors",
+    "inverse_factors_batched",
+    "inverse_factors_batched_async",
+    "finish_factors_batched",
     "transform_sigma",
 ]
 
@@ -270,6 +273,62 @@ def inverse_factors(hss: list[torch.Tensor], damp: float = 0.01) -> list[torch.T
             raise RuntimeError(f"Hessian is not factorisable even with heavy damping: {last}")
         out.append(u)
     return out
+
+
+def inverse_factors_batched_async(hs: torch.Tensor, damp: float = 0.01):
+    """First attempt of :func:`inverse_factor` for a batch of Hessians of one size
+    (``hs [E, K, K]``, e.g. the experts of an MoE projection), enqueued as one launch
+    sequence on the current stream (every kernel of the chain covers the whole batch):
+    returns ``(u [E, K, K], status [E])``; :func:`finish_factors_batched` waits and redoes
+    the reference's damping retries for the experts whose first attempt failed."""
+    dev = _lib.require_gpu(hs)
+    if hs.dim() != 3 or hs.shape[1] != hs.shape[2]:
+        raise ValueError(f"hs must be [E, K, K], got {tuple(hs.shape)}")
+    e, k = hs.shape[0], hs.shape[1]
+    h = hs.to(torch.float32).contiguous()
+    u = torch.empty_like(h)
+    status = torch.empty(max(e, 1), dtype=torch.int32, device=dev)
+    if e:
+        ws = _lib.workspace(dev, "hi2x_chol_batched_workspace_bytes", k, e)
+        _lib.call("hi2x_chol_inv_upper_batched_async", dev, _lib.ptr(h), k * k, k, e,
+                  float(damp), 0, _lib.ptr(u), k * k, _lib.ptr(status), _lib.ptr(ws),
+                  ws.numel())
+    return u, status[:e]
+
+
+def finish_factors_batched(hs: torch.Tensor, u: torch.Tensor, status: torch.Tensor,
+                           damp: float = 0.01) -> list[int]:
+    """Wait for :func:`inverse_factors_batched_async` and retry, as :func:`inverse_factor`
+    does, every expert whose first attempt failed (its factor is rewritten in ``u``).
+    Returns the experts that were retried."""
+    bad = [i for i, v in enumerate(status.cpu().tolist()) if v != _OK]
+    if not bad:
+        return bad
+    dev = u.device
+    k = u.shape[1]
+    ws = _lib.workspace(dev, "hi2x_chol_workspace_bytes", k)
+    for i in bad:
+        h = hs[i].to(torch.float32).contiguous()
+        last = None
+        for attempt in range(1, 6):
+            try:
+                _lib.call("hi2x_chol_inv_upper", dev, _lib.ptr(h), k, float(damp), attempt,
+                          _lib.ptr(u[i]), _lib.ptr(ws), ws.numel())
+                break
+            except _lib.NotPositiveDefinite as e:
+                last = e
+        else:
+            raise RuntimeError(f"Hessian is not factorisable even with heavy damping: {last}")
+    return bad
+
+
+def inverse_factors_batched(hs: torch.Tensor, damp: float = 0.01) -> torch.Tensor:
+    """:func:`inverse_factor` of every matrix of ``hs [E, K, K]``: one batched launch
+    sequence for the first attempts, the reference's retries per failing matrix.  Same
+    results as :func:`inverse_factor` on each."""
+    u, status = inverse_factors_batched_async(hs, damp)
+    finish_factors_batched(hs, u, status, damp)
+    return u
 
 
 @dataclass

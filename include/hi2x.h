@@ -185,13 +185,23 @@ int hi2x_hessian_syrk_upper(const void* x, int dtype, int64_t t, int64_t k, floa
 /* s[j][i] = s[i][j] for i < j: the lower triangle from the upper. */
 int hi2x_hessian_mirror(float* s, int64_t k, void* stream);
 
-/* Variable-length batch of the above (routed MoE tokens, hi2/moe.py:83-100):
- * group e accumulates rows [offs[e], offs[e+1]) of x into s_ptrs[e] ([k, k] f32).
- * offs is a host array of n_groups + 1 row offsets; s_ptrs a host array.  The workspace
- * is sized for the longest group (hi2x_hessian_workspace_bytes with its row count). */
-int hi2x_hessian_syrk_varlen(const void* x, int dtype, const int64_t* offs,
-                             int64_t n_groups, int64_t k, float* const* s_ptrs, void* ws,
-                             int64_t ws_bytes, void* stream);
+/* Workspace of hi2x_hessian_syrk_grouped (-1 for bad arguments). */
+int64_t hi2x_hessian_grouped_workspace_bytes(int64_t t_total, int64_t n_groups, int64_t k);
+
+/* HessianStats.update of every expert of an MoE layer from one routed token batch, in one
+ * launch sequence (the per-expert calls of hi2/moe.py:83-100 -> hi2/hessian.py:35-40):
+ * group e accumulates the tokens j in [offs[e], offs[e+1]) into s + e * s_stride
+ * ([k, k] f32, s_stride >= k * k), token j being row rows[j] of x [x_rows, k] bf16
+ * (dtype 2), or row j when rows is NULL (a batch already sorted by expert).  offs
+ * (n_groups + 1 entries, ascending within [0, t_total]) and rows (t_total entries) are
+ * device arrays: the token counts never travel to the host.  A group outside that
+ * range counts as empty, a row outside [0, x_rows) as zeros.  The groups run largest
+ * first over one transposed, gathered copy of the tokens; upper_only != 0 leaves the
+ * lower triangles stale (as hi2x_hessian_syrk_upper).  At most 4M tokens per call. */
+int hi2x_hessian_syrk_grouped(const void* x, int64_t x_rows, int dtype, const int64_t* rows,
+                              const int64_t* offs, int64_t n_groups, int64_t t_total,
+                              int64_t k, float* s, int64_t s_stride, int upper_only, void* ws,
+                              int64_t ws_bytes, void* stream);
 
 /* transform_sigma (hi2/hessian.py:50-68): hs [k, k] f32 = sym(M diag(1/s) sigma
  * diag(1/s) M^T) with M block-diagonal (H16/4 on flagged groups, I elsewhere).
@@ -206,6 +216,24 @@ int hi2x_sigma_transform(const float* sigma, const uint16_t* col_scale, const ui
  * hi2x_sigma_transform.  The lower triangle of s is not read. */
 int hi2x_sigma_transform_upper(const float* s, int64_t n, const uint16_t* col_scale,
                                const uint8_t* had, int64_t k, float* hs, void* stream);
+
+/* hi2x_sigma_transform_upper for `batch` running sums of one size at once (the experts of
+ * an MoE projection, each factored on its own input by hi2/calibrate.py:332-348): matrix z
+ * at s + z * s_stride over n[z] tokens (device int64 [batch]) into hs + z * hs_stride
+ * (strides in floats, >= k * k), every matrix with the same col_scale and had. */
+int hi2x_sigma_transform_upper_batched(const float* s, int64_t s_stride, const int64_t* n,
+                                       int64_t batch, const uint16_t* col_scale,
+                                       const uint8_t* had, int64_t k, float* hs,
+                                       int64_t hs_stride, void* stream);
+
+/* The MoE token floor on the experts' Hessians (hi2/layerwise.py:245-257 through
+ * hi2/moe.py:152-156 blend): with tot = the fp32 sum of the n_groups sums s + e * s_stride
+ * in expert order (taken before any changes), every expert with mask[e] != 0 (device u8)
+ * becomes s_e + fill[e] * tot (fill: device f32, the fp32 value of (need - n_e) / n_total),
+ * elementwise in fp32 as the reference's torch ops; the upper triangle only when
+ * upper_only != 0.  The caller sets the topped-up experts' counts to `need`. */
+int hi2x_hessian_blend(float* s, int64_t s_stride, int64_t n_groups, int64_t k,
+                       const float* fill, const uint8_t* mask, int upper_only, void* stream);
 
 /* ---- Cholesky chain ------------------------------------------------------------------ */
 
@@ -235,6 +263,21 @@ int hi2x_chol_inv_upper(const float* hs, int64_t k, float damp, int attempt, flo
  * calibration input) run concurrently on separate streams. */
 int hi2x_chol_inv_upper_async(const float* hs, int64_t k, float damp, int attempt, float* u,
                               int32_t* status, void* ws, int64_t ws_bytes, void* stream);
+
+/* Workspace of hi2x_chol_inv_upper_batched_async for `batch` k x k matrices. */
+int64_t hi2x_chol_batched_workspace_bytes(int64_t k, int64_t batch);
+
+/* The first attempt of inverse_factor (hi2/hessian.py:71-86) for `batch` Hessians of one
+ * size at once: the per-expert factors of an MoE projection (hi2/calibrate.py:332-348
+ * factors each expert's input separately; the experts of hi2/moe.py share the size).
+ * Matrix z: hs + z * hs_stride -> u + z * u_stride (strides in floats, >= k * k), status
+ * word status[z] as in hi2x_chol_inv_upper_async.  Every kernel of the chain covers the
+ * whole batch (grid z), so small factors fill the chip.  Nothing is synchronised; the
+ * caller retries a failed z with hi2x_chol_inv_upper at attempt 1.. as the reference. */
+int hi2x_chol_inv_upper_batched_async(const float* hs, int64_t hs_stride, int64_t k,
+                                      int64_t batch, float damp, int attempt, float* u,
+                                      int64_t u_stride, int32_t* status, void* ws,
+                                      int64_t ws_bytes, void* stream);
 
 /* ---- calibration statistics ------------------------------------------------------------ */
 

@@ -480,3 +480,26 @@ def qad_wht_scale(x, flags, scale_bits, pre_div):
                            _p(None if scale_bits is None else _c(scale_bits, np.uint16)),
                            int(bool(pre_div)), _p(out))
     return out
+
+
+def moe_top_up(sums, counts, need):
+    """The MoE token floor (``hi2/layerwise.py:241-257`` with ``blend``,
+    ``hi2/moe.py:152-156``) on the experts' sums ``[E, K, K]`` (float32): with tot the
+    float32 sum of all experts' sums in expert order (Python's ``sum``: ``0 + S_0``, then
+    ``+ S_1`` ...), every expert with ``n_e < need`` (when any expert saw a token)
+    becomes ``S_e + float32((need - n_e) / n_total) * tot`` and ``n_e = need``.  Returns
+    ``(sums, counts)`` (new arrays)."""
+    sums = np.asarray(sums, np.float32)
+    counts = [int(c) for c in counts]
+    tot_n = sum(counts)
+    tot = np.float32(0) + sums[0]
+    for e in range(1, len(sums)):
+        tot = tot + sums[e]
+    out, out_n = sums.copy(), list(counts)
+    for e, n in enumerate(counts):
+        if n >= need or tot_n == 0:
+            continue
+        fill = np.float32((need - n) / max(tot_n, 1))
+        out[e] = sums[e] + fill * tot
+        out_n[e] = need
+    return out, out_n

@@ -27,7 +27,9 @@ depend on the reference's own torch-CPU arithmetic:
   ``inverse_factor``, ``fwht_groups`` and GPTQ with packing through ``encode_many``, on
   the seeded inputs of ``tests/e2e_recipes.py`` (cfg1 down-scaled to 512 x 512 with 512
   and 2048 tokens, a cfg2-style mixed INT2/INT4 case, and cfg1 at its full 2048 x 2048
-  as digests and a 64-row slice).
+  as digests and a 64-row slice);
+* the MoE token floor (``hi2/layerwise.py:241-257`` with ``hi2.moe.blend``) on seven
+  experts' sums (``moe_blend.npz``).
 
 The fixtures are plain ``.npz`` data (inputs and expected outputs); nothing of the
 reference is stored.  Run from the repository root:
@@ -38,6 +40,7 @@ reference is stored.  Run from the repository root:
     python tests/golden/make_golden.py encode_many  # encode_many.npz only
     python tests/golden/make_golden.py qad          # qad.npz only
     python tests/golden/make_golden.py e2e          # e2e_*.npz only
+    python tests/golden/make_golden.py moe          # moe_blend.npz only
 """
 
 import os
@@ -444,7 +447,43 @@ def make_e2e():
             np.savez_compressed(os.path.join(OUT, f"e2e_{case}.npz"), **out)
 
 
+def make_moe():
+    """The MoE token floor: hi2/layerwise.py:241-257 (the experts' sum, need, which experts
+    are short) with the reference's own blend (hi2/moe.py:152-156) on every short expert."""
+    sys.path.insert(0, REF)
+    from hi2.moe import blend
+
+    torch.set_num_threads(1)
+    g = torch.Generator().manual_seed(53)
+    k = 64
+    counts = [5000, 300, 0, 4096, 1200, 70, 9000]
+    sums = []
+    for n in counts:
+        x = torch.randn(max(n, 1), k, generator=g) * torch.exp(0.5 * torch.randn(k, generator=g))
+        s_ = x.T @ x if n else torch.zeros(k, k)
+        sums.append(s_.float())
+    need = int(2.0 * 2048)  # min_tokens x the expert's widest input (cfg5: 2 x 2048)
+    tot_n = sum(counts)
+    tot_s = sum(sums)  # the reference's Python sum over the experts, as layerwise._merge
+    out, out_n = [], []
+    for s_, n in zip(sums, counts):
+        if n >= need or tot_n == 0:
+            out.append(s_)
+            out_n.append(n)
+            continue
+        b, nn_ = blend(s_, n, tot_s, tot_n, need)
+        out.append(b)
+        out_n.append(nn_)
+    np.savez_compressed(os.path.join(OUT, "moe_blend.npz"), counts=np.array(counts, np.int64),
+                        need=np.array(need, np.int64), sums=np.stack([t.numpy() for t in sums]),
+                        out=np.stack([t.numpy() for t in out]),
+                        out_n=np.array(out_n, np.int64))
+
+
 def main():
+    if sys.argv[1:] == ["moe"]:
+        make_moe()
+        return
     if sys.argv[1:] == ["e2e"]:
         make_e2e()
         return
@@ -538,6 +577,7 @@ def main():
     make_encode_many()
     make_qad()
     make_e2e()
+    make_moe()
 
     with open(os.path.join(OUT, "golden_meta.txt"), "w") as f:
         for k, v in meta.items():

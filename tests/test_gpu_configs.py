@@ -3,7 +3,7 @@
 cfg3 is the bench's own workload (bench.py); these cover the shapes of the other
 configurations at sizes the checks finish in seconds:
 
-- cfg5: per-expert Hessians of a routed (variable-length) token batch;
+- cfg5: in tests/test_gpu_moe.py;
 - cfg2 down_proj width (K = 14336): GPTQ rows bit for bit against the oracle given the
   same factor;
 - cfg4 width (K = 28672, fewer tokens than K): the factor through its inversion residual;
@@ -26,42 +26,6 @@ def T(a, dev):
 
 def N(t):
     return t.detach().cpu().numpy()
-
-
-def test_varlen_hessians_equal_per_group_calls(dev):
-    """cfg5 structure (hi2/moe.py:83-100): one routed token batch, groups of 0, 1, 7,
-    300 and 2048 tokens at K = 1024.  hi2x_hessian_syrk_varlen equals one
-    hi2x_hessian_syrk per group bit for bit, and each group's S matches its float64
-    X_e^T X_e."""
-    from hi2_amd import _lib
-
-    k = 1024
-    sizes = [300, 0, 2048, 1, 7]
-    offs = np.concatenate([[0], np.cumsum(sizes)]).astype(np.int64)
-    g = torch.Generator(device=dev).manual_seed(21)
-    x = (torch.randn(int(offs[-1]), k, device=dev, generator=g)
-         * torch.exp(0.5 * torch.randn(1, k, device=dev, generator=g))).to(torch.bfloat16)
-    ss = [torch.zeros(k, k, device=dev) for _ in sizes]
-    ctypes = _lib.ctypes
-    ptr_arr = (ctypes.c_void_p * len(sizes))(*[s.data_ptr() for s in ss])
-    offs_arr = (ctypes.c_int64 * len(offs))(*[int(o) for o in offs])
-    ptrs = ctypes.cast(ptr_arr, ctypes.c_void_p)
-    offs_c = ctypes.cast(offs_arr, ctypes.c_void_p)
-    ws = _lib.workspace(dev, "hi2x_hessian_workspace_bytes", 2, max(sizes), k)
-    _lib.call("hi2x_hessian_syrk_varlen", dev, _lib.ptr(x), 2, offs_c, len(sizes), k, ptrs,
-              _lib.ptr(ws), ws.numel())
-    for e, t in enumerate(sizes):
-        one = torch.zeros(k, k, device=dev)
-        if t:
-            xe = x[offs[e]:offs[e + 1]].contiguous()
-            w1 = _lib.workspace(dev, "hi2x_hessian_workspace_bytes", 2, t, k)
-            _lib.call("hi2x_hessian_syrk", dev, _lib.ptr(xe), 2, t, k, _lib.ptr(one),
-                      _lib.ptr(w1), w1.numel())
-            xd = xe.double()
-            want = xd.T @ xd
-            assert torch.allclose(ss[e].double(), want, rtol=1e-4,
-                                  atol=1e-4 * want.abs().max().item()), e
-        assert torch.equal(ss[e], one), e
 
 
 def _factor(dev, k, t, seed):
