@@ -4,10 +4,19 @@ A step is one full encode of the block with every input resident in HBM:
 4 calibration Hessians (q/k/v share one input, gate/up another; 8192 bf16 tokens)
 -> transform to the rotated basis -> damped factor -> Hadamard rotation of the 7
 weight matrices -> GPTQ of every row (30 % INT2/B32, 70 % INT4/B64, seeded mask) ->
-rdna_hint_flex packing into device buffers.  Prints one JSON line.
+rdna_hint_flex packing into device buffers.  Prints one JSON line, which also carries:
+
+* a per-linear stage breakdown of one serial step (Hessian, transform, factor per
+  input; rotation, ladder fit, column loop, trailing update, finish, packing per linear)
+  and the HBM rates of the rotation and packing kernels;
+* the cfg4 leg (Llama-3-70B-shaped layer, K = 28672, 25/72/3 % INT2/INT4/INT8 rows) and
+  the cfg5 leg (OLMoE-shaped MoE layer: 64 experts, top-8 of 16384 Zipf-routed tokens),
+  each timed whole;
+* the refinement and encode_many legs, and the CPU baseline (the reference's CPU path
+  restated in torch, oracle/torch_cpu.py, on cfg1 and cfg3 in full).
 
     python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu] [--refine-steps R]
-                    [--many-steps M]
+                    [--many-steps M] [--cfg4-steps S] [--cfg5-steps S]
     python bench.py --micro {trailing,syrk,factor,refine,stats,qad} [--steps R]  # one kernel alone
 """
 
@@ -40,6 +49,20 @@ PEAK_BF16 = 2.5e15  # MI355X dense bf16 MFMA, FLOP/s
 PEAK_F32 = 157.3e12  # MI355X dense fp32 MFMA, FLOP/s
 PEAK_HBM = 8.0e12  # B/s
 
+# a configuration: its linears, calibration inputs (width), tokens and the allocation
+# (fraction of rows, bits, ladder block) of every linear
+CFG3 = dict(name="cfg3", linears=LINEARS, inputs=INPUTS, tokens=TOKENS,
+            alloc=[(INT2_FRAC, 2, 32), (1 - INT2_FRAC, 4, 64)],
+            order=["down", "mlp", "attn", "o"])
+H70, I70 = 8192, 28672
+CFG4 = dict(name="cfg4", tokens=8192,
+            linears=[("q_proj", H70, H70, "attn"), ("o_proj", H70, H70, "o"),
+                     ("gate_proj", I70, H70, "mlp"), ("up_proj", I70, H70, "mlp"),
+                     ("down_proj", H70, I70, "down")],
+            inputs={"attn": H70, "o": H70, "mlp": H70, "down": I70},
+            alloc=[(0.25, 2, 32), (0.72, 4, 64), (0.03, 8, 64)],
+            order=["down", "mlp", "attn", "o"])
+
 
 class _DeviceStager:
     """assemble() stager that keeps the packed buffers on the device."""
@@ -49,37 +72,43 @@ class _DeviceStager:
         return t
 
 
-def make_inputs(dev, seed=0):
+def make_inputs(dev, seed=0, cfg=CFG3):
+    """Calibration tokens (bf16, 1 % x20 outlier channels) per input, bf16 weights
+    ~N(0, 0.02^2), and each linear's allocation: a seeded permutation of the rows cut by
+    the configuration's fractions; the row lists are kept on the device (rounding) and
+    the host (packing)."""
     import torch
 
     g = torch.Generator(device=dev).manual_seed(seed)
     xs = {}
-    for name, k in INPUTS.items():
-        x = torch.randn(TOKENS, k, generator=g, device=dev)
+    for name, k in cfg["inputs"].items():
+        x = torch.randn(cfg["tokens"], k, generator=g, device=dev)
         idx = torch.randperm(k, generator=g, device=dev)[: (k + 99) // 100]
         x[:, idx] *= 20.0  # 1 % outlier channels
         xs[name] = x.to(torch.bfloat16)
+        del x
     ws, masks = {}, {}
-    for name, n, k, _ in LINEARS:
+    for name, n, k, _ in cfg["linears"]:
         w = torch.randn(n, k, generator=g, device=dev) * 0.02
         ws[name] = w.to(torch.bfloat16)
+        del w
         perm = torch.randperm(n, generator=g, device=dev)
-        m = torch.zeros(n, dtype=torch.bool, device=dev)
-        m[perm[: int(round(INT2_FRAC * n))]] = True
-        # the allocation (fixed input of the encode): INT2 rows, INT4 rows, per-row tables
-        masks[name] = {
-            "r2": m.nonzero().flatten(),
-            "r4": (~m).nonzero().flatten(),
-            "nbits": torch.where(m, 2, 4).cpu(),
-            "block": torch.where(m, 32, 64).cpu(),
-        }
+        nbits = torch.empty(n, dtype=torch.int64, device=dev)
+        block = torch.empty(n, dtype=torch.int64, device=dev)
+        groups, lo = [], 0
+        for gi, (frac, nb, b) in enumerate(cfg["alloc"]):
+            hi = n if gi == len(cfg["alloc"]) - 1 else lo + int(round(frac * n))
+            rows = perm[lo:hi].sort().values
+            nbits[rows] = nb
+            block[rows] = b
+            groups.append((nb, b, rows, rows.cpu()))
+            lo = hi
+        masks[name] = {"groups": groups, "nbits": nbits.cpu(), "block": block.cpu()}
     return xs, ws, masks
 
 
-ORDER = ["down", "mlp", "attn", "o"]  # calibration inputs, longest chain first
 # streams and the inputs each one encodes in turn (one stream per input measured best:
 # the short chains fill the GPU around the long chain's latency-bound steps)
-LANES = [["down"], ["mlp"], ["attn"], ["o"]]
 _CHAIN_STREAMS = {}
 HEAD_START = os.environ.get("HI2_HEAD_START", "transform")
 
@@ -95,30 +124,33 @@ def _chain_stream(dev, i):
     return _CHAIN_STREAMS[key]
 
 
-def encode_block(xs, ws, masks, timer=None, lanes=None, keep=None):
+def encode_block(xs, ws, masks, timer=None, lanes=None, keep=None, cfg=CFG3):
     """Encode the whole block.  Each calibration input runs its own chain on its own
     stream (Hessian -> transform -> factor -> rotation -> GPTQ -> packing of the linears
     it feeds); the chains are independent, so they overlap on the GPU.  The host waits
-    only after every chain has been enqueued (factor status, packing's range check).
-    keep (a dict) receives each input's (stream, hs, jobs, where, encs)."""
+    only after every chain has been enqueued (factor status, then one read of the
+    packing's range counter).  keep (a dict) receives each input's (stream, hs, jobs,
+    where, encs)."""
     import torch
 
     from hi2_amd.format import assemble, fwht_groups
     from hi2_amd.hessian import GptqJob, HessianStats, encode_jobs_gptq
-    from hi2_amd.hessian import finish_factor, inverse_factor_async, transform_sigma
+    from hi2_amd.hessian import finish_factor, inverse_factor_async
 
     dev = next(iter(xs.values())).device
     main = torch.cuda.current_stream(dev)
-    lanes = LANES if lanes is None else lanes
+    order_in = cfg["order"]
+    lanes = [[inp] for inp in order_in] if lanes is None else lanes
     lane_of = {inp: li for li, lane in enumerate(lanes) for inp in lane}
-    order = [inp for lane in zip(*[l + [None] * (4 - len(l)) for l in lanes]) for inp in lane
+    width = max(len(l) for l in lanes)
+    order = [inp for lane in zip(*[l + [None] * (width - len(l)) for l in lanes]) for inp in lane
              if inp is not None]
     chains = {}
     for li in range(len(lanes)):
         _chain_stream(dev, li).wait_stream(main)
     lead = None  # the first chain's head start: the others wait for its Hessian stages
     for inp in order:
-        k = INPUTS[inp]
+        k = cfg["inputs"][inp]
         st = _chain_stream(dev, lane_of[inp])
         mark = (lambda stage, inp=inp: timer.mark(inp, stage)) if timer else (lambda stage: None)
         with torch.cuda.stream(st):
@@ -133,6 +165,7 @@ def encode_block(xs, ws, masks, timer=None, lanes=None, keep=None):
                 lead.record(st)
             mark("transform")
             hs = hst.transformed(None, had)  # == transform_sigma(hst.mean(), None, had)
+            del hst
             d = hs.diagonal().clone()
             if HEAD_START == "transform" and lane_of[inp] == 0 and lead is None:
                 lead = torch.cuda.Event()
@@ -141,36 +174,338 @@ def encode_block(xs, ws, masks, timer=None, lanes=None, keep=None):
             u, status = inverse_factor_async(hs, DAMP)
             mark("rotate")
             jobs, where = [], []
-            for name, n, kk, i in LINEARS:
+            for name, n, kk, i in cfg["linears"]:
                 if i != inp:
                     continue
                 wt = fwht_groups(ws[name].float(), had)
-                r2, r4 = masks[name]["r2"], masks[name]["r4"]
-                jobs.append(GptqJob(wt.index_select(0, r2), d, u, 2, 32))
-                where.append((name, r2))
-                jobs.append(GptqJob(wt.index_select(0, r4), d, u, 4, 64))
-                where.append((name, r4))
+                for nb, b, rows_d, rows_h in masks[name]["groups"]:
+                    jobs.append(GptqJob(wt.index_select(0, rows_d), d, u, nb, b))
+                    where.append((name, rows_h))
+                del wt
             mark("gptq")
             encs = encode_jobs_gptq(jobs, EFFORT)
             mark("end")
         chains[inp] = (st, hs, u, status, had, jobs, where, encs)
     out = {}
+    bad = torch.zeros(1, dtype=torch.int32, device=dev)
     for inp in reversed(order):  # the long chain last: the others are packed meanwhile
         st, hs, u, status, had, jobs, where, encs = chains[inp]
         with torch.cuda.stream(st):
             if finish_factor(hs, u, status, DAMP):  # more damping was needed: redo the rounding
                 encs = encode_jobs_gptq(jobs, EFFORT)
-            for name, n, k, i in LINEARS:
+            for name, n, k, i in cfg["linears"]:
                 if i != inp:
                     continue
                 pieces = [(rows, e.codes, e.params, e.consts)
                           for (nm, rows), e in zip(where, encs) if nm == name]
                 out[name] = assemble(pieces, masks[name]["nbits"], masks[name]["block"], had, k,
-                                     stager=_DeviceStager)
+                                     stager=_DeviceStager, bad=bad)
         main.wait_stream(st)
         if keep is not None:
             keep[inp] = (st, hs, jobs, where, encs)
+    if int(bad.item()):
+        raise ValueError("code outside the ladder")
     return out
+
+
+def trailing_flops(cfg) -> float:
+    """Algorithmic flops of every cross-block update of a step: per linear,
+    sum over 128-column blocks of 2 N 128 (K - i2) on the real rows (no padding)."""
+    total = 0.0
+    for _, n, k, _ in cfg["linears"]:
+        for i1 in range(0, k, 128):
+            i2 = min(i1 + 128, k)
+            total += 2.0 * n * (i2 - i1) * (k - i2)
+    return total
+
+
+def stage_breakdown(xs, ws, masks, cfg=CFG3):
+    """One step run serially on one stream with every stage timed: per input its Hessian,
+    transform and factor (stream events), per linear its rotation, ladder fit, column
+    loop, trailing update, finish and packing (the library's per-launch events summed by
+    kernel family).  Returns (per_input, per_linear, hbm) in ms and the HBM rates of the
+    rotation and packing kernels."""
+    import torch
+
+    from hi2_amd import _lib
+    from hi2_amd.format import assemble, fwht_groups
+    from hi2_amd.hessian import GptqJob, HessianStats, encode_jobs_gptq, inverse_factor
+
+    dev = next(iter(xs.values())).device
+    per_input, per_linear = {}, {}
+    hbm = {7: [0.0, 0.0], 9: [0.0, 0.0]}  # kind -> [bytes, ms]
+
+    def ev():
+        e = torch.cuda.Event(enable_timing=True)
+        e.record()
+        return e
+
+    for inp in cfg["order"]:
+        k = cfg["inputs"][inp]
+        had = torch.ones(k // 16, dtype=torch.uint8, device=dev)
+        e0 = ev()
+        hst = HessianStats(k, dev)
+        hst.update(xs[inp])
+        e1 = ev()
+        hs = hst.transformed(None, had)
+        del hst
+        e2 = ev()
+        u = inverse_factor(hs, DAMP)
+        e3 = ev()
+        torch.cuda.synchronize()
+        per_input[inp] = {"hessian": e0.elapsed_time(e1), "transform": e1.elapsed_time(e2),
+                          "factor": e2.elapsed_time(e3)}
+        d = hs.diagonal().clone()
+        for name, n, kk, i in cfg["linears"]:
+            if i != inp:
+                continue
+            kinds = [7, 8, 4, 0, 10, 9]
+            _lib.timing_enable(kinds)
+            wt = fwht_groups(ws[name].float(), had)
+            jobs = [GptqJob(wt.index_select(0, rows_d), d, u, nb, b)
+                    for nb, b, rows_d, _ in masks[name]["groups"]]
+            del wt
+            encs = encode_jobs_gptq(jobs, EFFORT)
+            pieces = [(g[3], e.codes, e.params, e.consts)
+                      for g, e in zip(masks[name]["groups"], encs)]
+            assemble(pieces, masks[name]["nbits"], masks[name]["block"], had, kk,
+                     stager=_DeviceStager)
+            torch.cuda.synchronize()
+            row = {}
+            for kind, label in ((7, "rotate"), (8, "ladder_fit"), (4, "column_loop"),
+                                (0, "trailing"), (10, "finish"), (9, "pack")):
+                cnt, ms, work = _lib.timing_query(kind)
+                row[label] = round(ms, 3)
+                if kind in hbm:
+                    hbm[kind][0] += work
+                    hbm[kind][1] += ms
+            per_linear[name] = row
+            _lib.timing_enable([])
+            del jobs, encs
+        del hs, u, d
+    rates = {}
+    for kind, kname in ((7, "fwht16_kernel"), (9, "assemble_kernel")):
+        b, ms = hbm[kind]
+        if ms > 0:
+            gbs = b / ms / 1e6
+            rates[kname] = {"bound": "hbm", "achieved": gbs, "peak": PEAK_HBM / 1e9,
+                            "unit": "GB/s", "frac": gbs / (PEAK_HBM / 1e9),
+                            "bytes_per_step": b, "ms_per_step": ms,
+                            "work": "fwht: 2 x 4 B per weight (f32 in and out)" if kind == 7
+                            else "pack: code bytes read + packed words + params + consts"}
+    return per_input, per_linear, rates
+
+
+def block_leg(cfg, dev, steps, warmup):
+    """A whole configuration (cfg4) timed like the main step, plus its serial stage
+    breakdown and trailing roofline; the inputs are freed afterwards."""
+    import torch
+
+    from hi2_amd import _lib
+
+    xs, ws, masks = make_inputs(dev, 1, cfg)
+    torch.cuda.synchronize()
+    for _ in range(warmup):
+        encode_block(xs, ws, masks, cfg=cfg)
+    torch.cuda.synchronize()
+    _lib.timing_enable([0, 1, 2])
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        encode_block(xs, ws, masks, cfg=cfg)
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / steps
+    tr = _lib.timing_query(0)
+    sy = _lib.timing_query(1)
+    ch = _lib.timing_query(2)
+    _lib.timing_enable([])
+    per_input, per_linear, rates = stage_breakdown(xs, ws, masks, cfg)
+    flops = trailing_flops(cfg)
+    trail_ms = tr[1] / steps
+    res = {
+        "workload": f"{cfg['name']}: " + ", ".join(f"{n} {r}x{k}" for n, r, k, _ in cfg["linears"])
+                    + f"; {cfg['tokens']} tokens; "
+                    + " / ".join(f"{int(round(f * 100))}% INT{nb}/B{b}" for f, nb, b in cfg["alloc"]),
+        "steps": steps,
+        "ms_per_step": ms,
+        "ms_per_linear": ms / len(cfg["linears"]),
+        "trailing_roofline": {"bound": "mfma", "achieved": flops / trail_ms / 1e9,
+                              "peak": PEAK_F32 / 1e12, "unit": "TFLOP/s",
+                              "frac": flops / trail_ms / 1e9 / (PEAK_F32 / 1e12),
+                              "flops_per_step": flops, "launches_per_step": tr[0] // steps,
+                              "timing": "event-timed launches in the timed steps (chains "
+                                        "concurrent)"},
+        "syrk_tflops_executed": sy[2] / sy[1] / 1e9 if sy[1] > 0 else None,
+        "factor_gemm_tflops": ch[2] / ch[1] / 1e9 if ch[1] > 0 else None,
+        "stages_serial_ms": {"per_input": per_input, "per_linear": per_linear},
+        "hbm_kernels": rates,
+    }
+    del xs, ws, masks
+    torch.cuda.empty_cache()
+    return res
+
+
+# ---- cfg5: the OLMoE-shaped MoE layer ------------------------------------------------------
+E5, T5, TOP5, H5, I5 = 64, 16384, 8, 2048, 1024
+ALLOC5 = [(0.30, 2, 32), (0.70, 4, 64)]
+FLOOR5 = 2.0  # expert_min_tokens (hi2/calibrate.py:69) x the widest input
+
+
+def moe_inputs(dev, seed=5):
+    """Router indices [T, 8] (Zipf(1.1), Gumbel-top-8), hidden tokens [T, 2048], the down
+    projection's inputs [8 T, 1024] in expert order (act(gate) * up of the routed slots,
+    synthesised), bf16 weights of gate/up [E, 2 I, H] and down [E, H, I], and per expert
+    tensor its allocation rows (30 % INT2/B32, 70 % INT4/B64)."""
+    import torch
+
+    from hi2_amd.workloads import activations, zipf_topk
+
+    idx = zipf_topk(T5, E5, TOP5, 1.1, seed, dev)
+    x = activations(T5, H5, seed + 1, dev)
+    xd = activations(T5 * TOP5, I5, seed + 2, dev)
+    g = torch.Generator(device=dev).manual_seed(seed + 3)
+    wgu = (torch.randn(E5, 2 * I5, H5, generator=g, device=dev) * 0.02).to(torch.bfloat16)
+    wdn = (torch.randn(E5, H5, I5, generator=g, device=dev) * 0.02).to(torch.bfloat16)
+    masks = {}
+    for e in range(E5):
+        for name, n in (("gate", I5), ("up", I5), ("down", H5)):
+            perm = torch.randperm(n, generator=g, device=dev)
+            n2 = int(round(ALLOC5[0][0] * n))
+            groups = []
+            nbits = torch.full((n,), ALLOC5[1][1], dtype=torch.int64)
+            block = torch.full((n,), ALLOC5[1][2], dtype=torch.int64)
+            for (frac, nb, b), rows in zip(ALLOC5, (perm[:n2].sort().values,
+                                                    perm[n2:].sort().values)):
+                rh = rows.cpu()
+                nbits[rh] = nb
+                block[rh] = b
+                groups.append((nb, b, rows, rh))
+            masks[(e, name)] = {"groups": groups, "nbits": nbits, "block": block}
+    return idx, x, xd, wgu, wdn, masks
+
+
+def encode_moe(idx, x, xd, wgu, wdn, masks, timer=None):
+    """One MoE layer: the routed batch, every expert's gate/up (K = 2048) and down
+    (K = 1024) Hessians in one grouped launch each, the token floor, the batched
+    transforms and factors, the rotation, GPTQ of all experts' rows (one factor per
+    expert), and packing of the 192 expert tensors into device buffers."""
+    import torch
+
+    from hi2_amd.format import assemble, fwht_groups
+    from hi2_amd.hessian import (GptqJob, encode_jobs_gptq, finish_factors_batched,
+                                 inverse_factors_batched_async)
+    from hi2_amd.moe import ExpertHessians, route_order
+
+    dev = x.device
+    mark = timer.mark if timer else (lambda *a: None)
+    mark("moe", "route")
+    rows, offs = route_order(idx, E5)
+    mark("moe", "hessian")
+    gu = ExpertHessians(E5, H5, dev)
+    gu.update_routed(x, offs, rows)
+    dn = ExpertHessians(E5, I5, dev)
+    dn.update_routed(xd, offs)
+    mark("moe", "floor")
+    need = int(FLOOR5 * H5)
+    gu.top_up(need)
+    dn.top_up(need)
+    mark("moe", "transform")
+    had_h = torch.ones(H5 // 16, dtype=torch.uint8, device=dev)
+    had_i = torch.ones(I5 // 16, dtype=torch.uint8, device=dev)
+    hs_g = gu.transformed(None, had_h)
+    hs_d = dn.transformed(None, had_i)
+    del gu, dn
+    mark("moe", "factor")
+    u_g, st_g = inverse_factors_batched_async(hs_g, DAMP)
+    u_d, st_d = inverse_factors_batched_async(hs_d, DAMP)
+    mark("moe", "rotate")
+    wt_g = fwht_groups(wgu.reshape(-1, H5).float(), had_h).reshape(E5, 2 * I5, H5)
+    wt_d = fwht_groups(wdn.reshape(-1, I5).float(), had_i).reshape(E5, H5, I5)
+    d_g = torch.diagonal(hs_g, dim1=1, dim2=2).contiguous()
+    d_d = torch.diagonal(hs_d, dim1=1, dim2=2).contiguous()
+    jobs, where = [], []
+    for e in range(E5):
+        for name, wt, d, u, off in (("gate", wt_g[e], d_g[e], u_g[e], 0),
+                                    ("up", wt_g[e], d_g[e], u_g[e], I5),
+                                    ("down", wt_d[e], d_d[e], u_d[e], 0)):
+            for nb, b, rows_d, rows_h in masks[(e, name)]["groups"]:
+                jobs.append(GptqJob(wt.index_select(0, rows_d + off), d, u, nb, b))
+                where.append(((e, name), rows_h))
+    del wt_g, wt_d
+    mark("moe", "gptq")
+    encs = encode_jobs_gptq(jobs, EFFORT)
+    mark("moe", "pack")
+    redo = finish_factors_batched(hs_g, u_g, st_g, DAMP) + finish_factors_batched(hs_d, u_d, st_d,
+                                                                                   DAMP)
+    if redo:  # an expert needed more damping: its rows again (the reference's retry)
+        encs = encode_jobs_gptq(jobs, EFFORT)
+    bad = torch.zeros(1, dtype=torch.int32, device=dev)
+    out = {}
+    by = {}
+    for (key, rows_h), enc in zip(where, encs):
+        by.setdefault(key, []).append((rows_h, enc.codes, enc.params, enc.consts))
+    for key, pieces in by.items():
+        m = masks[key]
+        k = H5 if key[1] != "down" else I5
+        out[key] = assemble(pieces, m["nbits"], m["block"], had_h if k == H5 else had_i, k,
+                            stager=_DeviceStager, bad=bad)
+    mark("moe", "end")
+    if int(bad.item()):
+        raise ValueError("code outside the ladder")
+    return out
+
+
+def moe_leg(dev, steps, warmup):
+    import torch
+
+    from hi2_amd import _lib
+
+    inp = moe_inputs(dev)
+    torch.cuda.synchronize()
+    for _ in range(warmup):
+        encode_moe(*inp)
+    torch.cuda.synchronize()
+    _lib.timing_enable([0, 1, 2, 3])
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        encode_moe(*inp)
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / steps
+    tr, sy, ch, lf = (_lib.timing_query(k) for k in (0, 1, 2, 3))
+    _lib.timing_enable([])
+    timer = StageTimer(torch)
+    encode_moe(*inp, timer=timer)
+    stages = timer.summary()["moe"]
+    counts = torch.bincount(inp[0].reshape(-1), minlength=E5).cpu().tolist()
+    # trailing flops on the real rows: per expert gate/up 2048 rows at K = 2048, down
+    # 2048 rows at K = 1024
+    flops = 0.0
+    for n, k in ((2 * I5, H5), (H5, I5)):
+        for i1 in range(0, k, 128):
+            i2 = min(i1 + 128, k)
+            flops += E5 * 2.0 * n * (i2 - i1) * (k - i2)
+    trail_ms = tr[1] / steps
+    res = {
+        "workload": "cfg5: OLMoE-shaped MoE layer, 64 experts (gate/up 1024x2048 sharing a "
+                    "Hessian, down 2048x1024), top-8 of 16384 tokens routed by Zipf(1.1) "
+                    "Gumbel-top-k, token floor 2 x 2048, 30% INT2/B32 + 70% INT4/B64 rows",
+        "steps": steps,
+        "ms_per_layer": ms,
+        "ms_per_expert_linear": ms / (3 * E5),
+        "routed_tokens_per_expert": {"min": min(counts), "median": sorted(counts)[E5 // 2],
+                                     "max": max(counts)},
+        "experts_below_floor": sum(c < int(FLOOR5 * H5) for c in counts),
+        "stages_ms": stages,
+        "trailing_roofline": {"bound": "mfma", "achieved": flops / trail_ms / 1e9,
+                              "peak": PEAK_F32 / 1e12, "unit": "TFLOP/s",
+                              "frac": flops / trail_ms / 1e9 / (PEAK_F32 / 1e12),
+                              "flops_per_step": flops, "launches_per_step": tr[0] // steps},
+        "grouped_syrk": {"launches_per_step": sy[0] // steps, "ms_per_step": sy[1] / steps,
+                         "tflops_executed": sy[2] / sy[1] / 1e9 if sy[1] > 0 else None},
+        "factor_ms_per_step_kernels": (ch[1] + lf[1]) / steps,
+    }
+    del inp
+    torch.cuda.empty_cache()
+    return res
 
 
 REFINE_PASSES = 2  # the reference's default for a calibrated GPTQ run without QAD
@@ -187,7 +522,7 @@ def refine_linears(kept):
     dev = next(iter(kept.values()))[1].device
     main = torch.cuda.current_stream(dev)
     out = {}
-    for inp in ORDER:
+    for inp in CFG3["order"]:
         st, hs, jobs, where, encs = kept[inp]
         st.wait_stream(main)
         with torch.cuda.stream(st):
@@ -198,7 +533,7 @@ def refine_linears(kept):
                 out[name] = refine_groups(
                     [(jobs[x].w, encs[x], jobs[x].nbits, jobs[x].block) for x in xs], hs,
                     REFINE_PASSES)
-    for inp in ORDER:
+    for inp in CFG3["order"]:
         main.wait_stream(kept[inp][0])
     return out
 
@@ -265,18 +600,6 @@ KERNELS = {  # kind -> (kernel, bound, peak FLOP/s, work unit)
 DOMINANT = 0  # the GPTQ trailing-update GEMM: the metric's MFMA kernel with the most time
 
 
-def traffic_per_launch(kernel):
-    """HBM bytes per launch of ``kernel`` from the committed PMC summary (FETCH_SIZE +
-    WRITE_SIZE, scaled by the copy-kernel calibration), or None when not measured."""
-    path = os.path.join(ROOT, "profiles", "traffic.json")
-    try:
-        with open(path) as f:
-            rec = json.load(f).get(kernel)
-    except (OSError, ValueError):
-        return None
-    return None if rec is None else rec.get("bytes_per_launch")
-
-
 def kernel_stats(kind):
     """Event-timed launches of one kernel family since hi2x_timing_enable."""
     from hi2_amd import _lib
@@ -291,80 +614,127 @@ def kernel_stats(kind):
             "tflops": rate / 1e12, "frac_of_peak": rate / peak}
 
 
-def roofline(kind):
-    st = kernel_stats(kind)
-    name, bound, peak, unit = KERNELS[kind]
-    return {"bound": bound, "achieved": st["tflops"], "peak": peak / 1e12, "unit": "TFLOP/s",
-            "frac": st["frac_of_peak"], "traffic": traffic_per_launch(name), "kernel": name,
-            "launches": st["launches"], "avg_ms": st["avg_ms"],
-            "flops_per_launch": st["work_per_launch"], "work": unit}
+def trailing_roofline(steps, basis):
+    """The trailing update's roofline over the last timing window: the algorithmic flops
+    of the block's cross-block updates on real rows (trailing_flops) divided by the summed
+    event-timed durations of its launches."""
+    from hi2_amd import _lib
+
+    n, ms, work = _lib.timing_query(DOMINANT)
+    flops = trailing_flops(CFG3) * steps
+    rate = flops / (ms / 1e3)
+    return {"bound": "mfma", "achieved": rate / 1e12, "peak": PEAK_F32 / 1e12,
+            "unit": "TFLOP/s", "frac": rate / PEAK_F32, "traffic": None,
+            "kernel": KERNELS[DOMINANT][0], "launches": n, "avg_ms": ms / n,
+            "flops_per_launch": flops / n,
+            "work": "2*rows*rank*cols summed over the block's cross-block updates, real rows "
+                    "only (the launches also run the zero rows that align row groups to "
+                    "128)", "timing": basis}
 
 
-def cpu_baseline(seed=0):
-    """The oracle (plain-C restatement of the reference path, OpenMP) timed on this host
-    on a bounded sample of cfg3, scaled to ms per linear of the whole block:
-      Hessian: 256 of 8192 tokens of each input (x32); transform: full K=4096 (the
-      K=14336 one scaled by (14336/4096)^2); factor: K=1024 scaled by (K/1024)^3 per
-      input; rotation + GPTQ + pack: 32 rows of every linear (scaled by N/32)."""
-    import numpy as np
+def _cpu_info():
+    import torch
 
-    import oracle
+    model = None
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    par = torch.__config__.parallel_info()
+    return {"nproc": os.cpu_count(), "model": model, "torch_threads": torch.get_num_threads(),
+            "parallel_info": [l.strip() for l in par.splitlines() if l.strip()][:8]}
 
-    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
-    rng = np.random.default_rng(seed)
-    total = 0.0
-    parts = {}
-    t_tok = 256
-    for name, k in INPUTS.items():
-        x = rng.standard_normal((t_tok, k)).astype(np.float32)
-        s = np.zeros((k, k), np.float32)
+
+def _torch_cpu_block(R, cfg, seed):
+    """The reference's CPU path (oracle/torch_cpu.py) on a whole configuration: per input
+    its Hessian (fp32 chunks), transform and factor; per linear rotation, GPTQ of every
+    allocation group and packing.  Returns seconds per stage."""
+    import torch
+
+    g = torch.Generator().manual_seed(seed)
+    parts = {"hessian": 0.0, "transform": 0.0, "factor": 0.0, "rotate": 0.0, "gptq": 0.0,
+             "pack": 0.0}
+    for inp, k in cfg["inputs"].items():
+        x = torch.randn(cfg["tokens"], k, generator=g)
+        x[:, torch.randperm(k, generator=g)[: (k + 99) // 100]] *= 20.0
+        x = x.to(torch.bfloat16)
+        flags = torch.ones(k // 16, dtype=torch.uint8)
         t0 = time.perf_counter()
-        oracle.hessian_update(s, x)
-        dt = (time.perf_counter() - t0) * (TOKENS / t_tok)
-        parts["hessian"] = parts.get("hessian", 0.0) + dt
-    k0 = 4096
-    a = rng.standard_normal((k0, k0)).astype(np.float32)
-    t0 = time.perf_counter()
-    oracle.transform_sigma(a, None, np.ones(k0 // 16, np.uint8))
-    dt = time.perf_counter() - t0
-    parts["transform"] = sum(dt * (k / k0) ** 2 for k in INPUTS.values())
-    kf = 1024
-    xf = rng.standard_normal((2 * kf, kf)).astype(np.float32)
-    hf = (xf.T @ xf / (2 * kf)).astype(np.float32)
-    t0 = time.perf_counter()
-    oracle.inverse_factor(hf, DAMP)
-    dt = time.perf_counter() - t0
-    parts["factor"] = sum(dt * (k / kf) ** 3 for k in INPUTS.values())
-    rows = 32
-    gptq = 0.0
-    for name, n, k, inp in LINEARS:
-        w = (rng.standard_normal((rows, k)) * 0.02).astype(np.float32)
-        d = (rng.random(k) + 0.5).astype(np.float32)
-        xu = rng.standard_normal((k, k)).astype(np.float32) * 0.01
-        u = np.triu(xu) + np.eye(k, dtype=np.float32)  # any upper factor: same op count
+        sigma = R.hessian_sum(x) / x.shape[0]
+        t1 = time.perf_counter()
+        hs = R.transform_sigma(sigma, None, flags)
+        t2 = time.perf_counter()
+        u = R.inverse_factor(hs, DAMP)
+        t3 = time.perf_counter()
+        parts["hessian"] += t1 - t0
+        parts["transform"] += t2 - t1
+        parts["factor"] += t3 - t2
+        d = hs.diagonal().clone()
+        del x, sigma
+        for name, n, kk, i in cfg["linears"]:
+            if i != inp:
+                continue
+            w = (torch.randn(n, kk, generator=g) * 0.02).to(torch.bfloat16)
+            perm = torch.randperm(n, generator=g)
+            t0 = time.perf_counter()
+            wt = R.rotate(w.float(), flags)
+            t1 = time.perf_counter()
+            lo, packed = 0, []
+            tg = tp = 0.0
+            for gi, (frac, nb, b) in enumerate(cfg["alloc"]):
+                hi = n if gi == len(cfg["alloc"]) - 1 else lo + int(round(frac * n))
+                rows = perm[lo:hi].sort().values
+                lo = hi
+                s0 = time.perf_counter()
+                codes = R.gptq(wt[rows], d, u, nb, b, EFFORT)[0]
+                s1 = time.perf_counter()
+                packed.append(R.pack_codes(codes, nb))
+                s2 = time.perf_counter()
+                tg += s1 - s0
+                tp += s2 - s1
+            parts["rotate"] += t1 - t0
+            parts["gptq"] += tg
+            parts["pack"] += tp
+        del hs, u
+    return parts
+
+
+CFG1 = dict(name="cfg1", tokens=512, linears=[("linear", 2048, 2048, "x")],
+            inputs={"x": 2048}, alloc=[(1.0, 4, 64)])
+
+
+def cpu_baseline(seed=0, which=("cfg1", "cfg3")):
+    """The reference's own CPU path (restated in torch: oracle/torch_cpu.py, bit-identical
+    to the reference on its fixtures) timed on this host's cores, on cfg1 and cfg3 in
+    full.  value: cfg3 ms per linear (the metric of the GPU line)."""
+    import torch
+
+    from oracle import torch_cpu as R
+
+    out = {"unit": "ms per linear", "kind": "port", "cores": torch.get_num_threads(),
+           "host": _cpu_info()}
+    for name, cfg in (("cfg1", CFG1), ("cfg3", CFG3)):
+        if name not in which:
+            continue
         t0 = time.perf_counter()
-        wt = oracle.fwht16(w, np.ones(k // 16, np.uint8))
-        n2 = int(rows * INT2_FRAC)
-        o2 = oracle.encode_rows_gptq(wt[:n2], d, u, 2, 32, EFFORT, comp=False)
-        o4 = oracle.encode_rows_gptq(wt[n2:], d, u, 4, 64, EFFORT, comp=False)
-        oracle.pack_codes(o2["codes"], 2)
-        oracle.pack_codes(o4["codes"], 4)
-        gptq += (time.perf_counter() - t0) * (n / rows)
-    parts["gptq"] = gptq
-    total = sum(parts.values())
-    return {
-        "value": total * 1e3 / len(LINEARS),
-        "unit": "ms per linear",
-        "cores": threads,
-        "kind": "port",
-        "sample": "oracle (C, OpenMP) on a cfg3 sample: 256/8192 tokens per Hessian, "
-                  "transform at K=4096, factor at K=1024, 32 rows per linear for "
-                  "rotation+GPTQ+pack, each scaled to the full block",
-        "stages_s": {k: round(v, 2) for k, v in parts.items()},
-    }
+        parts = _torch_cpu_block(R, cfg, seed)
+        wall = time.perf_counter() - t0
+        out[name] = {"s_total": round(wall, 2),
+                     "ms_per_linear": wall * 1e3 / len(cfg["linears"]),
+                     "stages_s": {k: round(v, 2) for k, v in parts.items()}}
+    main = out.get("cfg3") or out.get("cfg1")
+    out["value"] = main["ms_per_linear"]
+    out["sample"] = ("the reference's CPU path (torch ops of hi2/hessian.py, hi2/encode.py, "
+                     "hi2/format.py restated in oracle/torch_cpu.py) on "
+                     + " and ".join(w for w in which) + " in full, no extrapolation; value "
+                     "is " + ("cfg3" if "cfg3" in out else "cfg1") + " ms per linear")
+    return out
 
 
-# ---- kernel microbenchmarks (for profiling single kernels; not the contract line) --------
 def micro(which, reps=3):
     """One kernel family at the cfg3 shapes, alone on the GPU, event-timed; prints one
     JSON line per shape.  trailing: hi2x_gptq_run (column loop + cross-block updates) on
@@ -552,6 +922,8 @@ def micro(which, reps=3):
         raise SystemExit(f"unknown --micro {which}")
 
 
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -563,6 +935,10 @@ def main():
     ap.add_argument("--many-steps", type=int, default=2,
                     help="timed calls of the drop-in encode_many leg on host inputs "
                          "(0: skip it)")
+    ap.add_argument("--cfg4-steps", type=int, default=2,
+                    help="timed steps of the cfg4 (Llama-3-70B-shaped layer) leg (0: skip)")
+    ap.add_argument("--cfg5-steps", type=int, default=2,
+                    help="timed steps of the cfg5 (OLMoE-shaped MoE layer) leg (0: skip)")
     ap.add_argument("--micro", choices=["trailing", "syrk", "factor", "refine", "stats", "qad"],
                     help="instead of the block step: one kernel family alone at the cfg3 "
                          "shapes (for single-kernel profiles; prints one line per shape)")
@@ -605,15 +981,18 @@ def main():
     wall = time.perf_counter() - t0
     ms_step = wall * 1e3 / args.steps
     stages = timer.summary()
-    roof = roofline(DOMINANT)
+    roof = trailing_roofline(args.steps, "contended: event-timed launches in the timed steps, "
+                             "where the four input chains run concurrently")
     # one more, untimed step with every kernel family event-timed and the chains run one
     # after another on one stream: per-kernel rates without other chains sharing the GPU
     _lib.timing_enable(list(KERNELS))
-    encode_block(xs, ws, masks, lanes=[ORDER])
+    encode_block(xs, ws, masks, lanes=[CFG3["order"]])
     torch.cuda.synchronize()
     kernels = {KERNELS[k][0]: kernel_stats(k) for k in KERNELS}
-    roof_iso = roofline(DOMINANT)
+    roof_iso = trailing_roofline(1, "isolated: one step with the chains run one after "
+                                 "another on one stream")
     _lib.timing_enable([])
+    per_input, per_linear, hbm = stage_breakdown(xs, ws, masks)
     refine = None
     if args.refine_steps:
         kept = {}
@@ -626,7 +1005,7 @@ def main():
             refine_linears(kept)
         torch.cuda.synchronize()
         r_ms = (time.perf_counter() - t0) * 1e3 / args.refine_steps
-        r_roof = roofline(5)
+        r_stats = kernel_stats(5)
         _lib.timing_enable([5, 6])
         refine_linears({k: (torch.cuda.current_stream(dev),) + v[1:] for k, v in kept.items()})
         torch.cuda.synchronize()
@@ -637,7 +1016,7 @@ def main():
             "steps": args.refine_steps,
             "ms_per_step": r_ms,
             "ms_per_linear": r_ms / len(LINEARS),
-            "roofline": r_roof,
+            "gemm_contended": r_stats,
             "kernels_one_step_serial": {KERNELS[k][0]: kernel_stats(k) for k in (5, 6)},
         }
         _lib.timing_enable([])
@@ -678,6 +1057,10 @@ def main():
             "d2h_bytes": d2h,
         }
         del reqs, packed
+    del xs, ws, masks
+    torch.cuda.empty_cache()
+    cfg4 = block_leg(CFG4, dev, args.cfg4_steps, 1) if args.cfg4_steps else None
+    cfg5 = moe_leg(dev, args.cfg5_steps, 1) if args.cfg5_steps else None
     res = {
         "metric": "encode ms per linear layer (Llama-3-8B-shaped block, 7 linears)",
         "value": ms_step / len(LINEARS),
@@ -699,11 +1082,17 @@ def main():
         "roofline": roof,
         "roofline_isolated": roof_iso,
         "kernels_one_step": kernels,
+        "stages_serial_ms": {"per_input": per_input, "per_linear": per_linear},
+        "hbm_kernels": hbm,
     }
     if refine is not None:
         res["refine"] = refine
     if many is not None:
         res["encode_many"] = many
+    if cfg4 is not None:
+        res["cfg4"] = cfg4
+    if cfg5 is not None:
+        res["cfg5"] = cfg5
     if not args.no_cpu:
         res["cpu_baseline"] = cpu_baseline()
     print(json.dumps(res), flush=True)

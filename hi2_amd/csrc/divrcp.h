@@ -21,6 +21,16 @@ HI2X_HD inline float div_rcp_fast(float a, float b, float y) {
   return __builtin_fmaf(r1, y, q1);
 }
 
+// Whether div_rcp_fast(a, b, y) is a / b correctly rounded, given q0 = a y: |a| and |q0|
+// in [2^-100, 2^100] (no subnormal numerator, quotient or remainder and no overflow), or
+// a = +0 with a finite reciprocal (the iteration then yields the quotient's signed
+// zero; -0 is left to the IEEE division).  Checked on 10^8 random operand pairs of every exponent.
+HI2X_HD inline bool div_rcp_ok(float a, float q0) {
+  const float aa = __builtin_fabsf(a), aq = __builtin_fabsf(q0);
+  return (aa >= 0x1p-100f && aq >= 0x1p-100f && aq <= 0x1p100f) ||
+         (__builtin_bit_cast(unsigned, a) == 0u && q0 == 0.0f);
+}
+
 // a / b correctly rounded (bit-identical to IEEE division) for every a and every b with
 // y = 1 / b: the iteration where |a| and |a y| lie in [2^-100, 2^100] (no subnormal
 // numerator, quotient or remainder and no overflow; checked on 10^8 random operand pairs

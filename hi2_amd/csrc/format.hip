@@ -123,6 +123,7 @@ extern "C" int hi2x_fwht16(const void* x, void* y, int dtype, int64_t rows, int6
   const int64_t total = rows * (k / 16);
   const dim3 grid((unsigned)((total + 255) / 256));
   hipStream_t s = as_stream(stream);
+  LaunchTimer timer(HI2X_TIME_FWHT, 2.0 * rows * k * (dtype == 0 ? 4 : 8), s);
   if (dtype == 0)
     hipLaunchKernelGGL(fwht16_kernel<float>, grid, dim3(256), 0, s, (const float*)x, (float*)y,
                        rows, k, flags);
@@ -158,6 +159,8 @@ extern "C" int hi2x_assemble_piece(const int64_t* rows, int64_t r, const uint8_t
   const int64_t nw = k / (32 / nbits), nblk = k / block;
   const int64_t span = nw > nblk ? nw : nblk;
   const int64_t total = r * span;
+  LaunchTimer timer(HI2X_TIME_PACK, (double)r * (k + k * nbits / 8 + 4 * nblk + 12),
+                    as_stream(stream));
   hipLaunchKernelGGL(assemble_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0,
                      as_stream(stream), rows, r, codes, params, consts, k, nbits, nblk, code_off,
                      param_off, out_codes, out_params, out_consts, bad);

@@ -29,7 +29,8 @@ namespace {
 //
 // Step i (fully unrolled): every lane runs the rounding chain on its own column m=i/16
 // (the two divisions through the lane's precomputed reciprocals: div_rcp_code for the
-// code, div_rcp for the error, exact in the owner lane);
+// code, the bare iteration for the error, its exactness checked and the block run again
+// with IEEE division in the rare wave where it is not);
 // only lane q = i%16 owns column i (its U value of row i is then U[i][i]), so its error e
 // is broadcast to the row with DPP row_newbcast, and the row applies
 // w[c] -= e * U[i][c] to the columns it holds.  Columns <= i of the other lanes are dead
@@ -64,13 +65,16 @@ template <bool COMP>
 struct RowRegs {
   float w[CPL], loc[CPL], stc[CPL], ys[CPL], yu[CPL], er[CPL], qc[CPL];
   float cm[COMP ? CPL : 1];  // value each owned column was rounded from
+  int inexact;  // error quotients of this lane that fell outside div_rcp_ok's range
 };
 
 // Step I of the column loop, I a compile-time constant so that every register index
 // below is static (no dynamic VGPR indexing).  ub[I & 1] holds this lane's U row I;
 // the step fills ub[(I + 1) & 1] with row I + 1.  With FULL the block has LMAX columns
-// (no length test per step).
-template <int I, bool FULL, bool COMP>
+// (no length test per step).  The error quotient is the bare reciprocal iteration, its
+// range recorded in R.inexact (a branch in the loop would serialise it); EXACT uses the
+// IEEE division instead, for the rare block that has to be run again.
+template <int I, bool FULL, bool COMP, bool EXACT>
 __device__ __forceinline__ void gptq_step(RowRegs<COMP>& R, int L, int q, float nm,
                                           const float* __restrict__ suq, f32x4 (&ub)[2][2]) {
   constexpr int m = I / QL, s = I % QL, cur = I & 1;
@@ -87,7 +91,17 @@ __device__ __forceinline__ void gptq_step(RowRegs<COMP>& R, int L, int q, float 
   const float wq = f16_round(lo_j + qv * st_j);
   const float ujj = ub[cur][m >> 2][m & 3];  // U[I][I] in the owner lane
   const bool own = q == s;
-  const float e = div_rcp(col - wq, ujj, R.yu[m], own);  // exact where the error is kept
+  const float num = col - wq;
+  float e;
+  if constexpr (EXACT) {
+    e = num / ujj;
+  } else {
+    e = div_rcp_fast(num, ujj, R.yu[m]);
+    // counted in every lane, owner or not (a false alarm only costs a rerun; a test on
+    // the owner alone kept a lane mask per step alive and spilled), in a vector register
+    R.inexact += div_rcp_ok(num, num * R.yu[m]) ? 0 : 1;
+    asm volatile("" : "+v"(R.inexact));
+  }
   const float eb = row_bcast<s>(e);
   // the selects are pinned here (empty asm): left free, the compiler keeps every step's
   // e and code in its own register until the end of the loop, which costs occupancy
@@ -102,11 +116,125 @@ __device__ __forceinline__ void gptq_step(RowRegs<COMP>& R, int L, int q, float 
   for (int mm = (I + 1) / QL; mm < CPL; ++mm) R.w[mm] = R.w[mm] - eb * ub[cur][mm >> 2][mm & 3];
 }
 
-template <bool FULL, bool COMP, int... Is>
+template <bool FULL, bool COMP, bool EXACT, int... Is>
 __device__ __forceinline__ void gptq_steps(std::integer_sequence<int, Is...>, RowRegs<COMP>& R,
                                            int L, int q, float nm, const float* __restrict__ suq,
                                            f32x4 (&ub)[2][2]) {
-  (gptq_step<Is, FULL, COMP>(R, L, q, nm, suq, ub), ...);
+  (gptq_step<Is, FULL, COMP, EXACT>(R, L, q, nm, suq, ub), ...);
+}
+
+// The state of this lane's 8 columns of row lr of the workgroup: the working copy,
+// each column's decoded ladder (blk: the group's column -> block map at column i1), the
+// reciprocals of the steps and of the factor diagonal (su: the U block in LDS).
+template <bool COMP>
+__device__ __forceinline__ void load_row(RowRegs<COMP>& R, const float* __restrict__ wc,
+                                         int64_t K, int64_t i1, int L, int64_t rbase,
+                                         int nrows, int lr, const int32_t* __restrict__ blk,
+                                         const float* __restrict__ lo,
+                                         const float* __restrict__ st, int64_t ldp,
+                                         const float* su, int q) {
+      // this row's columns c = 16m + q: the working copy and each column's ladder block
+      const __amdgpu_buffer_rsrc_t wrs =
+          mg_rsrc(wc + rbase * K + i1, (int64_t)(nrows - 1) * K + L);
+      const __amdgpu_buffer_rsrc_t brs = __builtin_amdgcn_make_buffer_rsrc(
+          const_cast<int32_t*>(blk + i1), (short)0, L * 4, 0x00020000);
+      int bix[CPL];
+#pragma unroll
+      for (int m = 0; m < CPL; ++m) {
+        const int c = QL * m + q;
+        const uint32_t wo = c < L ? (uint32_t)(((int64_t)lr * K + c) * 4) : MG_OOB;
+        R.w[m] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(wrs, (int)wo, 0, 0));
+        bix[m] = (int)__builtin_amdgcn_raw_buffer_load_b32(brs, (int)(c < L ? c * 4 : MG_OOB), 0, 0);
+      }
+      // decoded (lo, step) of those blocks (block 0 for the dead columns c >= L)
+      const __amdgpu_buffer_rsrc_t lrs = mg_rsrc(lo + rbase * ldp, (int64_t)nrows * ldp);
+      const __amdgpu_buffer_rsrc_t srs = mg_rsrc(st + rbase * ldp, (int64_t)nrows * ldp);
+#pragma unroll
+      for (int m = 0; m < CPL; ++m) {
+        const uint32_t po = (uint32_t)(((int64_t)lr * ldp + bix[m]) * 4);
+        R.loc[m] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(lrs, (int)po, 0, 0));
+        R.stc[m] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(srs, (int)po, 0, 0));
+        R.er[m] = 0.0f;
+        R.qc[m] = 0.0f;
+        if constexpr (COMP) R.cm[m] = 0.0f;
+      }
+      // IEEE reciprocals (correctly rounded) of each column's step and factor diagonal;
+      // dead columns (c >= L) get 1
+#pragma unroll
+      for (int m = 0; m < CPL; ++m) {
+        const int c = QL * m + q;
+        const float sc = R.stc[m] == 0.0f ? 1.0f : R.stc[m];
+        const float ud = c < L ? su[c * USTR + lane_off(q) + m] : 1.0f;
+        R.ys[m] = 1.0f / sc;
+        R.yu[m] = 1.0f / ud;
+      }
+      R.inexact = 0;
+}
+
+template <bool COMP>
+__device__ __forceinline__ void store_row(const RowRegs<COMP>& R, int64_t K, int64_t i1, int L,
+                                          int64_t r, int q, float* __restrict__ err1,
+                                          int64_t lde, uint8_t* __restrict__ codes,
+                                          float* __restrict__ comp) {
+#pragma unroll
+  for (int m = 0; m < CPL; ++m) {
+    const int c = QL * m + q;
+    if (c < L) {
+      err1[r * lde + c] = R.er[m];
+      codes[r * K + i1 + c] = (uint8_t)R.qc[m];
+      if constexpr (COMP) comp[r * K + i1 + c] = R.cm[m];
+    }
+  }
+}
+
+// The block for this lane's row with IEEE division, as a rolled loop (its arrays live in
+// scratch memory: this path only runs for a wave whose fast pass met an error quotient
+// outside the reciprocal iteration's exact range, so its speed does not matter, and an
+// unrolled second copy of the loop would double the fast path's registers), then the
+// row's outputs.  The same operations in the same order as gptq_step.
+template <bool COMP>
+__device__ void gptq_rows_exact(const float* __restrict__ wc, int64_t K, int64_t i1, int L,
+                                int64_t rbase, int nrows, int lr, int64_t r,
+                                const int32_t* __restrict__ blk, const float* __restrict__ lo,
+                                const float* __restrict__ st, int64_t ldp, const float* su,
+                                int q, float nm, float* __restrict__ err1, int64_t lde,
+                                uint8_t* __restrict__ codes, float* __restrict__ comp) {
+  RowRegs<COMP> R;
+  load_row<COMP>(R, wc, K, i1, L, rbase, nrows, lr, blk, lo, st, ldp, su, q);
+  volatile float w[CPL], er[CPL], qc[CPL], cm[CPL];
+  for (int m = 0; m < CPL; ++m) {
+    w[m] = R.w[m];
+    er[m] = 0.0f;
+    qc[m] = 0.0f;
+    cm[m] = 0.0f;
+  }
+  const int lane = threadIdx.x & 63;
+#pragma unroll 1
+  for (int i = 0; i < L; ++i) {
+    const int m = i / QL, s = i % QL;
+    const float col = w[m];
+    const float lo_j = R.loc[m], st_j = R.stc[m];
+    const float safe = (st_j == 0.0f) ? 1.0f : st_j;
+    float qv = clamp_code(__builtin_rintf((col - lo_j) / safe), nm);
+    if (st_j == 0.0f) qv = 0.0f;
+    const float wq = f16_round(lo_j + qv * st_j);
+    const float ujj = su[i * USTR + lane_off(q) + m];
+    const float e = (col - wq) / ujj;
+    const float eb = __shfl(e, (lane & ~(QL - 1)) + s, 64);
+    if (q == s) {
+      er[m] = e;
+      qc[m] = qv;
+      cm[m] = col;
+    }
+    for (int mm = (i + 1) / QL; mm < CPL; ++mm)
+      w[mm] = w[mm] - eb * su[i * USTR + lane_off(q) + mm];
+  }
+  for (int m = 0; m < CPL; ++m) {
+    R.er[m] = er[m];
+    R.qc[m] = qc[m];
+    if constexpr (COMP) R.cm[m] = cm[m];
+  }
+  store_row<COMP>(R, K, i1, L, r, q, err1, lde, codes, comp);
 }
 
 template <bool FULL, bool COMP>
@@ -165,59 +293,21 @@ __global__ __launch_bounds__(RPG * QL) void gptq_block_kernel(
 
     const float nm = nmax[g];
     RowRegs<COMP> R;
-    {
-      // this row's columns c = 16m + q: the working copy and each column's ladder block
-      const __amdgpu_buffer_rsrc_t wrs =
-          mg_rsrc(wc + rbase * K + i1, (int64_t)(nrows - 1) * K + L);
-      const __amdgpu_buffer_rsrc_t brs = __builtin_amdgcn_make_buffer_rsrc(
-          const_cast<int32_t*>(blk + (int64_t)g * K + i1), (short)0, L * 4, 0x00020000);
-      int bix[CPL];
-#pragma unroll
-      for (int m = 0; m < CPL; ++m) {
-        const int c = QL * m + q;
-        const uint32_t wo = c < L ? (uint32_t)(((int64_t)lr * K + c) * 4) : MG_OOB;
-        R.w[m] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(wrs, (int)wo, 0, 0));
-        bix[m] = (int)__builtin_amdgcn_raw_buffer_load_b32(brs, (int)(c < L ? c * 4 : MG_OOB), 0, 0);
-      }
-      // decoded (lo, step) of those blocks (block 0 for the dead columns c >= L)
-      const __amdgpu_buffer_rsrc_t lrs = mg_rsrc(lo + rbase * ldp, (int64_t)nrows * ldp);
-      const __amdgpu_buffer_rsrc_t srs = mg_rsrc(st + rbase * ldp, (int64_t)nrows * ldp);
-#pragma unroll
-      for (int m = 0; m < CPL; ++m) {
-        const uint32_t po = (uint32_t)(((int64_t)lr * ldp + bix[m]) * 4);
-        R.loc[m] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(lrs, (int)po, 0, 0));
-        R.stc[m] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(srs, (int)po, 0, 0));
-        R.er[m] = 0.0f;
-        R.qc[m] = 0.0f;
-        if constexpr (COMP) R.cm[m] = 0.0f;
-      }
-      // IEEE reciprocals (correctly rounded) of each column's step and factor diagonal;
-      // dead columns (c >= L) get 1
-#pragma unroll
-      for (int m = 0; m < CPL; ++m) {
-        const int c = QL * m + q;
-        const float sc = R.stc[m] == 0.0f ? 1.0f : R.stc[m];
-        const float ud = c < L ? su[c * USTR + lane_off(q) + m] : 1.0f;
-        R.ys[m] = 1.0f / sc;
-        R.yu[m] = 1.0f / ud;
-      }
-    }
-
+    load_row<COMP>(R, wc, K, i1, L, rbase, nrows, lr, blk + (int64_t)g * K, lo, st, ldp, su, q);
     const float* suq = su + lane_off(q);
     f32x4 ub[2][2];
     ub[0][0] = *reinterpret_cast<const f32x4*>(suq);
     ub[0][1] = *reinterpret_cast<const f32x4*>(suq + 4);
-    gptq_steps<FULL, COMP>(std::make_integer_sequence<int, LMAX>{}, R, L, q, nm, suq, ub);
-
-#pragma unroll
-    for (int m = 0; m < CPL; ++m) {
-      const int c = QL * m + q;
-      if (c < L) {
-        err1[r * lde + c] = R.er[m];
-        codes[r * K + i1 + c] = (uint8_t)R.qc[m];
-        if constexpr (COMP) comp[r * K + i1 + c] = R.cm[m];
-      }
+    gptq_steps<FULL, COMP, false>(std::make_integer_sequence<int, LMAX>{}, R, L, q, nm, suq, ub);
+    if (__ballot(R.inexact != 0) != 0) {
+      // some row of this wave met an error quotient outside the iteration's exact range
+      // (subnormal or negative-zero numerators, extreme magnitudes): the wave runs the
+      // block again from the working copy with IEEE division
+      gptq_rows_exact<COMP>(wc, K, i1, L, rbase, nrows, lr, r, blk + (int64_t)g * K, lo, st,
+                            ldp, su, q, nm, err1, lde, codes, comp);
+      continue;
     }
+    store_row<COMP>(R, K, i1, L, r, q, err1, lde, codes, comp);
   }
 }
 

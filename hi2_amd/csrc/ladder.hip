@@ -289,6 +289,7 @@ int launch_fit(const float* w, const float* d, int64_t rows, int64_t k, int nlev
                hipStream_t s) {
   const int64_t total = rows * (k / B);
   const dim3 blocks((unsigned)((total + 255) / 256));
+  LaunchTimer timer(HI2X_TIME_LADDER_FIT, 4.0 * rows * k, s);
   hipLaunchKernelGGL(ladder_fit_kernel<B>, blocks, dim3(256), 0, s, w, d, rows, k, nlev, grid,
                      g, ls, lo, step, err);
   return launch_status("ladder_fit_kernel");
@@ -368,6 +369,9 @@ extern "C" int hi2x_finish(const uint8_t* codes_ro, const float* comp_ro, const 
   if (n == 0) return HI2X_OK;
   hipStream_t s = as_stream(stream);
   const int64_t total = n * k;
+  const bool moves = !(perm == nullptr && codes == codes_ro && comp == comp_ro);
+  LaunchTimer timer(HI2X_TIME_FINISH,
+                    (double)n * k * (5 + (moves ? 2 + (comp ? 8 : 0) : 0)), s);
   // without a permutation the outputs may alias the inputs: nothing to move then
   if (!(perm == nullptr && codes == codes_ro && comp == comp_ro)) {
     hipLaunchKernelGGL(unpermute_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s,

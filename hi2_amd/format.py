@@ -161,11 +161,18 @@ def assemble(
     k: int,
     col_scale: torch.Tensor | None = None,
     stager=None,
+    bad: torch.Tensor | None = None,
 ) -> HI2Tensor:
     """Flat buffers from per-config row groups ``(rows, codes[r, K] uint8,
     params[r, nb, 2] uint8, consts[r, 3] fp16)``: packing and scatters run on the
     device of the first piece's codes, the result is returned on the host (through
-    ``stager.to_host`` when given)."""
+    ``stager.to_host`` when given).
+
+    The host never waits for the device when the pieces' row indices are host tensors
+    and ``bad`` is given: ``bad`` (device int32 [1]) then counts codes outside their
+    ladder for the caller to check later (several tensors can share one counter);
+    without it the count is read here and a nonzero one raises ``ValueError``, as the
+    reference does."""
     if not pieces:
         raise ValueError("assemble needs at least one piece on the device")
     dev = _lib.require_gpu(pieces[0][1])
@@ -177,19 +184,25 @@ def assemble(
     code_off[1:] = torch.cumsum(words, 0)
     param_off = torch.zeros(r + 1, dtype=torch.int64)
     param_off[1:] = torch.cumsum(blocks, 0)
-    code_off_d, param_off_d = code_off.to(dev), param_off.to(dev)
+    code_off_d, param_off_d = _lib.h2d(code_off, dev), _lib.h2d(param_off, dev)
     codes = torch.zeros(int(code_off[-1]), dtype=torch.int32, device=dev)
     params = torch.zeros(int(param_off[-1]) * 2, dtype=torch.uint8, device=dev)
     consts = torch.zeros(r, 3, dtype=torch.float16, device=dev)
-    bad = torch.zeros(1, dtype=torch.int32, device=dev)
+    own_bad = bad is None
+    if own_bad:
+        bad = torch.zeros(1, dtype=torch.int32, device=dev)
     keep = []
     for rows, c, p, rc in pieces:
-        rows_c = rows.cpu()
-        if rows_c.numel() == 0:
+        if rows.device.type == "cpu":
+            rows_c = rows
+            rows_d = _lib.h2d(rows.to(torch.int64), dev)
+        else:
+            rows_c = rows[:1].cpu()
+            rows_d = rows.to(torch.int64).contiguous()
+        if rows.numel() == 0:
             continue
         nbits = int(nb[rows_c[0]])
         blk = k // int(blocks[rows_c[0]])
-        rows_d = rows.to(dev, torch.int64).contiguous()
         c_d = c.to(dev, torch.uint8).contiguous()
         p_d = p.to(dev, torch.uint8).contiguous()
         rc_d = rc.to(dev, torch.float16).contiguous()
@@ -198,7 +211,7 @@ def assemble(
                   _lib.ptr(p_d), _lib.ptr(rc_d), k, nbits, blk, _lib.ptr(code_off_d),
                   _lib.ptr(param_off_d), _lib.ptr(codes), _lib.ptr(params), _lib.ptr(consts),
                   _lib.ptr(bad))
-    if int(bad.item()):
+    if own_bad and int(bad.item()):
         raise ValueError("code outside the ladder")
     to_host = stager.to_host if stager is not None else (lambda t: t.cpu())
     return HI2Tensor(

@@ -394,6 +394,10 @@ int hi2x_qad_wht_scale(const float* x, int64_t n_rows, int64_t k, const uint8_t*
 #define HI2X_TIME_GPTQ_BLOCK 4    /* work = rows * len * (len - 1) (intra-block flops) */
 #define HI2X_TIME_REFINE_GEMM 5   /* work = 2 * rows * rank * columns (flops) */
 #define HI2X_TIME_REFINE_BLOCK 6  /* work = rows * len (column decisions) */
+#define HI2X_TIME_FWHT 7          /* work = bytes read + written (rows * k * 2 * size) */
+#define HI2X_TIME_LADDER_FIT 8    /* work = bytes of w read (rows * k * 4) */
+#define HI2X_TIME_PACK 9          /* work = bytes: codes read, words, params and consts moved */
+#define HI2X_TIME_FINISH 10       /* work = bytes: codes and w read (sse; + the unpermute) */
 int hi2x_timing_enable(unsigned mask);
 
 /* Sum over the recorded launches of `kind`: count, event-timed milliseconds, work. */

@@ -1,6 +1,7 @@
 // Host check of hi2_amd/csrc/divrcp.h (compiled by tests/test_divrcp.py with g++ -mfma
 // -ffp-contract=off, the same fma and rounding semantics as the gfx950 kernels):
 //   div_rcp(a, b, 1/b)      == a / b bit for bit,
+//   div_rcp_fast(a, b, 1/b) == a / b wherever div_rcp_ok(a, a / b's estimate) accepts,
 //   div_rcp_code(a, b, 1/b) rounds and clamps to the same code as a / b (b normal),
 // over random operand pairs of every exponent and the operands the fast iteration alone
 // gets wrong (subnormal and zero numerators, subnormal quotients, overflow, inf, NaN).
@@ -37,7 +38,7 @@ static bool same_code(float q, float r, float nm) {
 
 struct Family {
   const char* name;
-  long n = 0, bad = 0, bad_code = 0;
+  long n = 0, bad = 0, bad_code = 0, bad_ok = 0;
   float ea = 0, eb = 0;
 };
 
@@ -48,6 +49,11 @@ static void check(Family& f, float a, float b) {
   if (!same(div_rcp(a, b, y), q)) {
     if (!f.bad) f.ea = a, f.eb = b;
     ++f.bad;
+  }
+  // where div_rcp_ok accepts the operands, the bare iteration is the IEEE quotient
+  if (div_rcp_ok(a, a * y) && !same(div_rcp_fast(a, b, y), q)) {
+    if (!f.bad && !f.bad_ok) f.ea = a, f.eb = b;
+    ++f.bad_ok;
   }
   // div_rcp_code's divisors are steps and factor diagonals: normal and finite
   const float ab = std::fabs(b);
@@ -92,9 +98,9 @@ int main() {
   }
   int rc = 0;
   for (const Family& f : fam) {
-    std::printf("%-32s %9ld pairs  div_rcp mismatches %ld  code mismatches %ld", f.name, f.n,
-                f.bad, f.bad_code);
-    if (f.bad || f.bad_code) {
+    std::printf("%-32s %9ld pairs  div_rcp mismatches %ld  accepted fast mismatches %ld  code "
+                "mismatches %ld", f.name, f.n, f.bad, f.bad_ok, f.bad_code);
+    if (f.bad || f.bad_code || f.bad_ok) {
       std::printf("  (first: a=%a b=%a)", f.ea, f.eb);
       rc = 1;
     }

@@ -186,6 +186,24 @@ def test_lone_chunk_at_an_offset_leaves_the_job_rows_alone(dev, monkeypatch):
     _same(got, oracle.encode_rows_gptq(w, d, u, 4, 32, "normal"))
 
 
+@pytest.mark.parametrize("scale", [3e-31, 1e-39])
+def test_tiny_rows_take_the_exact_division_path(dev, scale):
+    """Rows whose error quotients fall outside the reciprocal iteration's exact range
+    (numerators below 2^-100: tiny weights, 3e-31 normal and 1e-39 subnormal) next to
+    ordinary rows in the same waves: the column loop's flagged waves run the block again
+    with IEEE division, and codes, sse and comp equal the oracle (IEEE) bit for bit."""
+    w, d, u, _, _ = _layer(48, 256, 31)
+    w[::3] *= np.float32(scale)
+    got = _encode(dev, w, d, u)
+    _same(got, oracle.encode_rows_gptq(w, d, u, 4, 64, "normal"))
+
+
+def _encode(dev, w, d, u):
+    from hi2_amd.hessian import encode_rows_gptq
+
+    return encode_rows_gptq(T(w, dev), T(d, dev), T(u, dev), 4, 64, "normal", comp=True)
+
+
 def test_nearest_encode_rows_equals_oracle(dev):
     from hi2_amd.encode import encode_rows
 
