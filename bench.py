@@ -390,7 +390,7 @@ def encode_moe(idx, x, xd, wgu, wdn, masks, timer=None):
     expert), and packing of the 192 expert tensors into device buffers."""
     import torch
 
-    from hi2_amd.format import assemble, fwht_groups
+    from hi2_amd.format import assemble_many, fwht_groups
     from hi2_amd.hessian import (GptqJob, encode_jobs_gptq, finish_factors_batched,
                                  inverse_factors_batched_async)
     from hi2_amd.moe import ExpertHessians, route_order
@@ -422,14 +422,21 @@ def encode_moe(idx, x, xd, wgu, wdn, masks, timer=None):
     wt_d = fwht_groups(wdn.reshape(-1, I5).float(), had_i).reshape(E5, H5, I5)
     d_g = torch.diagonal(hs_g, dim1=1, dim2=2).contiguous()
     d_d = torch.diagonal(hs_d, dim1=1, dim2=2).contiguous()
+    # one job per expert, projection input and allocation class: gate and up rows of one
+    # class share the expert's Hessian, so they are rounded together (fewer, larger
+    # units); where[j] lists the (tensor, rows, slice of the job) it holds
     jobs, where = [], []
     for e in range(E5):
-        for name, wt, d, u, off in (("gate", wt_g[e], d_g[e], u_g[e], 0),
-                                    ("up", wt_g[e], d_g[e], u_g[e], I5),
-                                    ("down", wt_d[e], d_d[e], u_d[e], 0)):
-            for nb, b, rows_d, rows_h in masks[(e, name)]["groups"]:
-                jobs.append(GptqJob(wt.index_select(0, rows_d + off), d, u, nb, b))
-                where.append(((e, name), rows_h))
+        for ci, (nb, b) in enumerate((g[0], g[1]) for g in masks[(e, "gate")]["groups"]):
+            rg = masks[(e, "gate")]["groups"][ci]
+            ru = masks[(e, "up")]["groups"][ci]
+            rows = torch.cat([rg[2], ru[2] + I5])
+            jobs.append(GptqJob(wt_g[e].index_select(0, rows), d_g[e], u_g[e], nb, b))
+            where.append([((e, "gate"), rg[3], 0, rg[3].numel()),
+                          ((e, "up"), ru[3], rg[3].numel(), rows.numel())])
+        for nb, b, rows_d, rows_h in masks[(e, "down")]["groups"]:
+            jobs.append(GptqJob(wt_d[e].index_select(0, rows_d), d_d[e], u_d[e], nb, b))
+            where.append([((e, "down"), rows_h, 0, rows_h.numel())])
     del wt_g, wt_d
     mark("moe", "gptq")
     encs = encode_jobs_gptq(jobs, EFFORT)
@@ -439,15 +446,18 @@ def encode_moe(idx, x, xd, wgu, wdn, masks, timer=None):
     if redo:  # an expert needed more damping: its rows again (the reference's retry)
         encs = encode_jobs_gptq(jobs, EFFORT)
     bad = torch.zeros(1, dtype=torch.int32, device=dev)
-    out = {}
     by = {}
-    for (key, rows_h), enc in zip(where, encs):
-        by.setdefault(key, []).append((rows_h, enc.codes, enc.params, enc.consts))
-    for key, pieces in by.items():
-        m = masks[key]
-        k = H5 if key[1] != "down" else I5
-        out[key] = assemble(pieces, m["nbits"], m["block"], had_h if k == H5 else had_i, k,
-                            stager=_DeviceStager, bad=bad)
+    for parts, enc in zip(where, encs):
+        for key, rows_h, a, z in parts:
+            by.setdefault(key, []).append((rows_h, enc.codes[a:z], enc.params[a:z],
+                                           enc.consts[a:z]))
+    keys = list(by)
+    packed = assemble_many([dict(pieces=by[key], row_nbits=masks[key]["nbits"],
+                                 row_block=masks[key]["block"],
+                                 had=had_h if key[1] != "down" else had_i,
+                                 k=H5 if key[1] != "down" else I5) for key in keys],
+                           stager=_DeviceStager, bad=bad)
+    out = dict(zip(keys, packed))
     mark("moe", "end")
     if int(bad.item()):
         raise ValueError("code outside the ladder")

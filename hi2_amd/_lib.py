@@ -66,6 +66,17 @@ SIGNATURES = {
                             _P],
     "hi2x_qad_wht_scale": [_P, _I64, _I64, _P, _P, _I, _P],
 }
+class Piece(ctypes.Structure):
+    """hi2x_piece (include/hi2x.h): one piece of hi2x_assemble_batch."""
+
+    _fields_ = [("rows", _P), ("r", _I64), ("codes", _P), ("params", _P), ("consts", _P),
+                ("k", _I64), ("nbits", ctypes.c_int32), ("pad_", ctypes.c_int32),
+                ("block", _I64), ("code_off", _P), ("param_off", _P), ("out_codes", _P),
+                ("out_params", _P), ("out_consts", _P)]
+
+
+SIGNATURES["hi2x_assemble_batch"] = [_P, _I64, _P, _P]
+
 # workspace sizes (int64 bytes, -1 for bad arguments): name -> argtypes
 SIZES = {
     "hi2x_hessian_workspace_bytes": [_I, _I64, _I64],

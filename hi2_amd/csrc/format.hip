@@ -146,6 +146,36 @@ extern "C" int hi2x_pack_codes(const uint8_t* codes, int64_t rows, int64_t k, in
   return launch_status("pack_kernel");
 }
 
+extern "C" int hi2x_assemble_batch(const hi2x_piece* pieces, int64_t n_pieces, int32_t* bad,
+                                   void* stream) {
+  clear_error();
+  HI2X_REQUIRE(n_pieces >= 0 && (n_pieces == 0 || pieces), "assemble_batch: bad arguments");
+  hipStream_t s = as_stream(stream);
+  double bytes = 0.0;
+  for (int64_t i = 0; i < n_pieces; ++i) {
+    const hi2x_piece& p = pieces[i];
+    HI2X_REQUIRE(p.nbits == 2 || p.nbits == 4 || p.nbits == 8, "assemble_batch: piece %lld "
+                 "nbits=%d", (long long)i, p.nbits);
+    HI2X_REQUIRE(p.block > 0 && p.k % p.block == 0 && p.k % (32 / p.nbits) == 0 && p.r >= 0,
+                 "assemble_batch: piece %lld K/block", (long long)i);
+    bytes += (double)p.r * (p.k + p.k * p.nbits / 8 + 4 * (p.k / p.block) + 12);
+  }
+  LaunchTimer timer(HI2X_TIME_PACK, bytes, s);
+  for (int64_t i = 0; i < n_pieces; ++i) {
+    const hi2x_piece& p = pieces[i];
+    if (p.r == 0) continue;
+    const int64_t nw = p.k / (32 / p.nbits), nblk = p.k / p.block;
+    const int64_t span = nw > nblk ? nw : nblk;
+    const int64_t total = p.r * span;
+    hipLaunchKernelGGL(assemble_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s,
+                       p.rows, p.r, p.codes, p.params, p.consts, p.k, p.nbits, nblk, p.code_off,
+                       p.param_off, p.out_codes, p.out_params, p.out_consts, bad);
+    const int rc = launch_status("assemble_kernel");
+    if (rc) return rc;
+  }
+  return HI2X_OK;
+}
+
 extern "C" int hi2x_assemble_piece(const int64_t* rows, int64_t r, const uint8_t* codes,
                                    const uint8_t* params, const uint16_t* consts, int64_t k,
                                    int nbits, int64_t block, const int64_t* code_off,

@@ -9,9 +9,11 @@ buffers on the host, as the reference does).  Decode/verification helpers
 (``dequantize``, accounting) are not part of the encode path and are not provided.
 """
 
+import ctypes
 import math
 from dataclasses import dataclass
 
+import numpy as np
 import torch
 
 from . import _lib
@@ -226,3 +228,94 @@ def assemble(
         shape=(r, k),
         col_scale=col_scale,
     )
+
+
+def assemble_many(tensors: list[dict], stager=None, bad: torch.Tensor | None = None
+                  ) -> list[HI2Tensor]:
+    """:func:`assemble` of several tensors at once (every expert of an MoE layer): each
+    entry of ``tensors`` holds the arguments of one call (``pieces``, ``row_nbits``,
+    ``row_block``, ``had``, ``k``, optionally ``col_scale``).  The tensors' buffers are
+    views of one allocation per field, the offsets and row lists go to the device in one
+    copy, and every piece is packed through one ``hi2x_assemble_batch`` call, so the host
+    cost does not grow with a call per piece.  Results equal :func:`assemble` on each; the
+    pieces' row lists must be host tensors."""
+    if not tensors:
+        return []
+    dev = _lib.require_gpu(tensors[0]["pieces"][0][1])
+    metas, chunks = [], []
+    n_words = n_blocks = n_rows = pos = 0
+    for t in tensors:
+        nb = t["row_nbits"].to(torch.int64).cpu().numpy()
+        blocks = t["k"] // t["row_block"].to(torch.int64).cpu().numpy()
+        r = nb.size
+        code_off = np.zeros(r + 1, np.int64)
+        code_off[1:] = np.cumsum((t["k"] * nb) // 32)
+        param_off = np.zeros(r + 1, np.int64)
+        param_off[1:] = np.cumsum(blocks)
+        metas.append((r, nb, blocks, code_off, param_off, n_words, n_blocks, n_rows, pos))
+        # device copies shifted into the shared buffers
+        chunks += [code_off + n_words, param_off + n_blocks]
+        pos += 2 * (r + 1)
+        n_words += int(code_off[-1])
+        n_blocks += int(param_off[-1])
+        n_rows += r
+    rows_at = []
+    for t in tensors:
+        for rows, *_ in t["pieces"]:
+            if rows.device.type != "cpu":
+                raise RuntimeError("assemble_many takes host row lists")
+            rn = rows.numpy().astype(np.int64, copy=False)
+            rows_at.append((pos, rn.size, int(rn[0]) if rn.size else 0))
+            chunks.append(rn)
+            pos += rn.size
+    flat = _lib.h2d(torch.from_numpy(np.concatenate(chunks)), dev)
+    base = flat.data_ptr()
+    codes = torch.zeros(max(n_words, 1), dtype=torch.int32, device=dev)
+    params = torch.zeros(max(n_blocks, 1) * 2, dtype=torch.uint8, device=dev)
+    consts = torch.zeros(max(n_rows, 1), 3, dtype=torch.float16, device=dev)
+    own_bad = bad is None
+    if own_bad:
+        bad = torch.zeros(1, dtype=torch.int32, device=dev)
+    pieces, keep = [], []
+    pi = 0
+    cbase, pbase, kbase = codes.data_ptr(), params.data_ptr(), consts.data_ptr()
+    for t, (r, nb, blocks, code_off, param_off, w0, b0, r0, at0) in zip(tensors, metas):
+        k = t["k"]
+        co_ptr, po_ptr = base + 8 * at0, base + 8 * (at0 + r + 1)
+        for _, c, p, rc in t["pieces"]:
+            at, n, first = rows_at[pi]
+            pi += 1
+            if n == 0:
+                continue
+            if c.dtype != torch.uint8 or not c.is_contiguous() or c.device != dev:
+                c = c.to(dev, torch.uint8).contiguous()
+            if p.dtype != torch.uint8 or not p.is_contiguous() or p.device != dev:
+                p = p.to(dev, torch.uint8).contiguous()
+            if rc.dtype != torch.float16 or not rc.is_contiguous() or rc.device != dev:
+                rc = rc.to(dev, torch.float16).contiguous()
+            keep += [c, p, rc]
+            pieces.append(_lib.Piece(base + 8 * at, n, c.data_ptr(), p.data_ptr(), rc.data_ptr(),
+                                     k, int(nb[first]), 0, k // int(blocks[first]), co_ptr,
+                                     po_ptr, cbase, pbase, kbase + 6 * r0))
+    arr = (_lib.Piece * max(len(pieces), 1))(*pieces)
+    _lib.call("hi2x_assemble_batch", dev, ctypes.cast(arr, ctypes.c_void_p), len(pieces),
+              _lib.ptr(bad))
+    if own_bad and int(bad.item()):
+        raise ValueError("code outside the ladder")
+    to_host = stager.to_host if stager is not None else (lambda x: x.cpu())
+    out = []
+    for t, (r, nb, blocks, code_off, param_off, w0, b0, r0, at0) in zip(tensors, metas):
+        nw, nbk = int(code_off[-1]), int(param_off[-1])
+        out.append(HI2Tensor(
+            codes=to_host(codes[w0:w0 + nw]),
+            code_off=torch.from_numpy(code_off.astype(np.int32)),
+            blk_params=to_host(params[2 * b0:2 * (b0 + nbk)]),
+            param_off=torch.from_numpy(param_off.astype(np.int32)),
+            row_consts=to_host(consts[r0:r0 + r]),
+            row_nbits=t["row_nbits"].to(torch.uint8).cpu(),
+            row_block=t["row_block"].to(torch.uint8).cpu(),
+            had=t["had"].to(torch.uint8).reshape(-1).cpu(),
+            shape=(r, t["k"]),
+            col_scale=t.get("col_scale"),
+        ))
+    return out

@@ -415,18 +415,26 @@ def _round_kernel(
         st[off : off + n, :nb] = x.step_d
         views.append((off, n))
         off += pn
-    # small index arrays: built on the host, copied without blocking the host (other
-    # streams keep being fed while this batch waits for its inputs)
-    row_grp = _lib.h2d(torch.repeat_interleave(
-        torch.arange(len(units), dtype=torch.int32), torch.tensor(padded)), dev)
+    # the batch's small tables (row counts, factor addresses, highest codes, blocks) in
+    # one copy that does not block the host (other streams keep being fed while this
+    # batch waits for its inputs); the row -> group map is expanded on the device
     uk = [jobs[x.job].u.to(dev, torch.float32).contiguous() for x in units]
     for u in uk:
         if u.shape != (k, k):
             raise ValueError(f"factor has shape {tuple(u.shape)}, expected ({k}, {k})")
-    u_ptrs = _lib.h2d(torch.tensor([u.data_ptr() for u in uk], dtype=torch.int64), dev)
-    blk = torch.stack([x.blk_of.to(dev, torch.int32) for x in units]).contiguous()
-    nmax = _lib.h2d(torch.tensor(
-        [2 ** jobs[x.job].nbits - 1 for x in units], dtype=torch.float32), dev)
+    ng = len(units)
+    meta = _lib.h2d(torch.tensor(
+        padded + [u.data_ptr() for u in uk] + [2 ** jobs[x.job].nbits - 1 for x in units]
+        + [jobs[x.job].block for x in units], dtype=torch.int64), dev)
+    row_grp = torch.repeat_interleave(torch.arange(ng, dtype=torch.int32, device=dev),
+                                      meta[:ng], output_size=total)
+    u_ptrs = meta[ng:2 * ng]
+    nmax = meta[2 * ng:3 * ng].to(torch.float32)
+    if all(jobs[x.job].perm is None for x in units):
+        blk = (torch.arange(k, dtype=torch.int32, device=dev)[None, :]
+               // meta[3 * ng:4 * ng, None].to(torch.int32)).contiguous()
+    else:
+        blk = torch.stack([x.blk_of.to(dev, torch.int32) for x in units]).contiguous()
     codes = torch.zeros(total, k, dtype=torch.uint8, device=dev)
     comp = torch.zeros(total, k, dtype=torch.float32, device=dev) if want_comp else None
     sb = _super_blocks(k) if super_blocks is None else super_blocks

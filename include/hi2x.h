@@ -156,6 +156,30 @@ int hi2x_assemble_piece(const int64_t* rows, int64_t r, const uint8_t* codes,
                         int32_t* out_codes, uint8_t* out_params, uint16_t* out_consts,
                         int32_t* bad, void* stream);
 
+/* One piece of hi2x_assemble_batch: the arguments of hi2x_assemble_piece. */
+typedef struct hi2x_piece {
+  const int64_t* rows;
+  int64_t r;
+  const uint8_t* codes;
+  const uint8_t* params;
+  const uint16_t* consts;
+  int64_t k;
+  int32_t nbits;
+  int32_t pad_;
+  int64_t block;
+  const int64_t* code_off;
+  const int64_t* param_off;
+  int32_t* out_codes;
+  uint8_t* out_params;
+  uint16_t* out_consts;
+} hi2x_piece;
+
+/* hi2x_assemble_piece for n_pieces pieces (pieces: a host array) in one call, in order,
+ * sharing the range counter bad: the packing of many tensors (every expert of an MoE
+ * layer) without a call per piece.  The reference assembles one tensor at a time
+ * (hi2/format.py:127-184); the result is the same. */
+int hi2x_assemble_batch(const hi2x_piece* pieces, int64_t n_pieces, int32_t* bad, void* stream);
+
 /* ---- Hessian ------------------------------------------------------------------------ */
 
 /* Workspaces.  Entry points that need device scratch take (ws, ws_bytes): a 256-byte

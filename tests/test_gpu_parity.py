@@ -329,6 +329,41 @@ def test_pack_and_assemble_equal_oracle(dev, nbits):
     assert np.array_equal(got.param_off.numpy(), want["param_off"])
 
 
+def test_assemble_many_equals_assemble_per_tensor(dev):
+    """The batched packing of several tensors (hi2x_assemble_batch: one call for every
+    piece of every tensor) equals assemble on each tensor, field by field."""
+    from hi2_amd.format import assemble, assemble_many
+
+    rng = np.random.default_rng(2)
+    tensors = []
+    for ti, (r, k) in enumerate(((37, 256), (64, 128), (20, 512))):
+        perm = rng.permutation(r)
+        cuts = [(2, 32, perm[: r // 3]), (4, 64, perm[r // 3: 2 * r // 3]), (8, 64, perm[2 * r // 3:])]
+        nbits = np.zeros(r, np.int64)
+        block = np.zeros(r, np.int64)
+        pieces = []
+        for nb, b, rows in cuts:
+            rows = np.sort(rows)
+            nbits[rows] = nb
+            block[rows] = b
+            codes = rng.integers(0, 2 ** nb, (rows.size, k)).astype(np.uint8)
+            params = rng.integers(0, 256, (rows.size, k // b, 2)).astype(np.uint8)
+            consts = rng.standard_normal((rows.size, 3)).astype(np.float16)
+            pieces.append((torch.from_numpy(rows), T(codes, dev), T(params, dev),
+                           T(consts, dev)))
+        tensors.append(dict(pieces=pieces, row_nbits=torch.from_numpy(nbits),
+                            row_block=torch.from_numpy(block),
+                            had=torch.ones(k // 16, dtype=torch.uint8), k=k))
+    many = assemble_many(tensors)
+    for t, got in zip(tensors, many):
+        want = assemble(t["pieces"], t["row_nbits"], t["row_block"], t["had"], t["k"])
+        for f in ("codes", "code_off", "blk_params", "param_off", "row_nbits", "row_block",
+                  "had"):
+            assert torch.equal(getattr(got, f), getattr(want, f)), f
+        assert torch.equal(got.row_consts.view(torch.int16), want.row_consts.view(torch.int16))
+        assert got.shape == want.shape
+
+
 # ---- Hessian, transform, factor --------------------------------------------------------------
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 @pytest.mark.parametrize("t,k", [(700, 320), (4096, 256)])
