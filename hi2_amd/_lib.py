@@ -35,6 +35,7 @@ SIGNATURES = {
     "hi2x_ladder_fit": [_P, _P, _I64, _I64, _I64, _I, _P, _I, _I, _P, _P, _P, _P],
     "hi2x_params": [_P, _P, _I64, _I64, _P, _P, _P, _P, _P, _I64, _P],
     "hi2x_decode_params": [_P, _P, _P, _I64, _I64, _P, _P, _P],
+    "hi2x_nearest_codes": [_P, _I64, _I64, _I64, _P, _P, _I64, _I, _P, _P],
     "hi2x_finish": [_P, _P, _P, _I64, _I64, _I64, _P, _P, _I64, _P, _P, _P, _P, _P, _P],
     "hi2x_ladder_dequantize": [_P, _P, _P, _I64, _I64, _I64, _I, _P, _P],
     "hi2x_fwht16": [_P, _P, _I, _I64, _I64, _P, _P],

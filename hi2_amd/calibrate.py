@@ -18,8 +18,9 @@ Placement on the device:
 * the host waits only after every chain is enqueued: for each chain's factor status
   (the reference's damping retries, which redo that chain's rounding), then per tensor
   for refinement and for packing, whose range check and D2H copy end the chain;
-* nearest-rounding rows (``cfg.rounding == "nearest"`` or no Sigma) are one batched
-  call with the identity factor on the caller's stream.
+* nearest-rounding rows (``cfg.rounding == "nearest"`` or no Sigma) go through
+  :func:`hi2_amd.encode.encode_rows` (ladder fit, params, codes, sse) on the caller's
+  stream.
 
 Weights and Sigma may come from the host in their stored dtype (staged through pinned
 memory, cast and smoothed on the device, as exact as the reference's host cast and
@@ -33,6 +34,7 @@ from dataclasses import dataclass, field
 import torch
 
 from . import _lib
+from .encode import encode_rows
 from .format import GROUP, HI2Tensor, assemble, fwht_groups
 from .hessian import (
     GptqJob,
@@ -309,30 +311,21 @@ def _on_device(reqs, cfg, ex, i: int, use_gptq, comp_full, pack=None):
             for ri in groups[fk]:
                 stage(ri, st, emit)
             _round_chain(ch, reqs, jobs, job_at, encs, cfg)
-        # nearest rows: one batched call with the identity factor on the caller's stream
-        near_jobs: list[GptqJob] = []
-        near_at: list[tuple[int, torch.Tensor, int]] = []
-        eyes: dict[int, torch.Tensor] = {}
-
+        # nearest rows (hi2/encode.py:133-173: ladder fit, params, codes, sse) on the
+        # caller's stream
         def emit_near(ri, r, wt, had):
             k = r.table.shape[1]
             d = _weights(r.stats, k, had, dev, _inv_scale(r.table.col_scale))
-            eye = eyes.get(k)
-            if eye is None:
-                eye = eyes[k] = torch.eye(k, dtype=torch.float32, device=dev)
 
             def add(sub, rows, nb, b, slot):
-                near_jobs.append(GptqJob(sub, d, eye, nb, b))
-                near_at.append((ri, rows, slot))
+                e = encode_rows(sub, d, nb, b, cfg.effort)
+                pieces[ri][slot] = (rows, e.codes, e.params, e.consts)
                 if r.comp_out is not None:
                     comp_full[ri].index_copy_(0, _to_device(rows, dev), sub)
             return add
 
         for ri in near:
             stage(ri, main, emit_near)
-        if near_jobs:
-            for (ri, rows, slot), e in zip(near_at, encode_jobs_gptq(near_jobs, cfg.effort)):
-                pieces[ri][slot] = (rows, e.codes, e.params, e.consts)
         if pack is not None:
             for ri in near:
                 pack(ri, pieces[ri], main)
@@ -447,7 +440,6 @@ def encode_with_picks_reference(w, stats, table, picks, cfg, ex=None, sigma=None
                 u = inverse_factor(hs, cfg.damp)
             else:
                 d = _weights(stats, k, had, dev, inv)
-                u = torch.eye(k, dtype=torch.float32, device=dev)
             for ci, (nb, b) in enumerate(table.candidates):
                 rows = _rows_of(picks.detach().cpu(), lo, hi, ci)
                 if rows.numel() == 0:
@@ -456,7 +448,7 @@ def encode_with_picks_reference(w, stats, table, picks, cfg, ex=None, sigma=None
                 if use_gptq:
                     e = encode_rows_gptq_reference(sub, d, u, nb, b, cfg.effort, perm)
                 else:
-                    e = encode_jobs_gptq([GptqJob(sub, d, u, nb, b)], cfg.effort)[0]
+                    e = encode_rows(sub, d, nb, b, cfg.effort)
                 pieces.append((rows + lo, e.codes, e.params, e.consts))
                 if comp_out is not None:
                     comps.append((rows + lo, (e.comp if use_gptq else sub).cpu()))

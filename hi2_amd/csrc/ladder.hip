@@ -283,6 +283,35 @@ __global__ __launch_bounds__(256) void sse_kernel(const uint8_t* __restrict__ co
   if (live && hl == 0) sse[r] = out;
 }
 
+// encode_rows' codes (hi2/encode.py:151-155): q = clamp(st == 0 ? 0 : rint((w - lo) /
+// st), 0, nm) with the row's decoded ladder of the element's block, the quotient by IEEE
+// division.  Four consecutive elements per thread (one 16-byte read of w).
+__global__ __launch_bounds__(256) void nearest_codes_kernel(
+    const float* __restrict__ w, int64_t rows, int64_t k, int64_t block,
+    const float* __restrict__ lo_d, const float* __restrict__ st_d, int64_t ldd, float nm,
+    uint8_t* __restrict__ codes) {
+  const int64_t q4 = k / 4;
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= rows * q4) return;
+  const int64_t r = i / q4, c0 = (i % q4) * 4;
+  const float4 v = *reinterpret_cast<const float4*>(w + r * k + c0);
+  const float* lr = lo_d + r * ldd;
+  const float* sr = st_d + r * ldd;
+  const float x[4] = {v.x, v.y, v.z, v.w};
+  uint32_t packed = 0;
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    const int64_t b = (c0 + t) / block;
+    const float lo = lr[b], st = sr[b];
+    const float safe = st == 0.0f ? 1.0f : st;
+    float q = __builtin_rintf((x[t] - lo) / safe);
+    q = st == 0.0f ? 0.0f : q;
+    q = clamp_code(q, nm);
+    packed |= (uint32_t)(uint8_t)q << (8 * t);
+  }
+  *reinterpret_cast<uint32_t*>(codes + r * k + c0) = packed;
+}
+
 template <int B>
 int launch_fit(const float* w, const float* d, int64_t rows, int64_t k, int nlev,
                const Grid& grid, int g, int ls, float* lo, float* step, float* err,
@@ -357,6 +386,24 @@ extern "C" int hi2x_ladder_dequantize(const uint8_t* codes, const float* lo, con
   hipLaunchKernelGGL(dequant_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0,
                      as_stream(stream), codes, lo, step, rows, nb, block, exact, out_h);
   return launch_status("dequant_kernel");
+}
+
+extern "C" int hi2x_nearest_codes(const float* w, int64_t rows, int64_t k, int64_t block,
+                                  const float* lo_d, const float* st_d, int64_t ldd, int nbits,
+                                  uint8_t* codes, void* stream) {
+  clear_error();
+  HI2X_REQUIRE(rows >= 0 && k > 0 && k % 4 == 0 && block > 0 && k % block == 0,
+               "nearest_codes: bad shape");
+  HI2X_REQUIRE(ldd >= k / block, "nearest_codes: ldd < nb");
+  HI2X_REQUIRE(nbits >= 1 && nbits <= 8, "nearest_codes: nbits=%d", nbits);
+  HI2X_REQUIRE(((uintptr_t)w & 15) == 0 && ((uintptr_t)codes & 3) == 0,
+               "nearest_codes: w must be 16-byte and codes 4-byte aligned");
+  if (rows == 0) return HI2X_OK;
+  const int64_t total = rows * (k / 4);
+  hipLaunchKernelGGL(nearest_codes_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0,
+                     as_stream(stream), w, rows, k, block, lo_d, st_d, ldd,
+                     (float)((1 << nbits) - 1), codes);
+  return launch_status("nearest_codes_kernel");
 }
 
 extern "C" int hi2x_finish(const uint8_t* codes_ro, const float* comp_ro, const int64_t* perm,

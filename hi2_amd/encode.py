@@ -124,11 +124,27 @@ def encode_rows(
     """Quantise ``w[N, K]`` (already in the stored basis) at ``(nbits, block)`` with
     nearest rounding onto the fitted ladders; ``d[K]`` weights the error metric.
 
-    Nearest rounding is the GPTQ column loop with an identity factor (no error is
-    propagated), so it runs through the same kernels."""
-    from .hessian import GptqJob, encode_jobs_gptq
-
-    k = w.shape[1]
-    eye = torch.eye(k, dtype=torch.float32, device=w.device)
-    enc = encode_jobs_gptq([GptqJob(w, d, eye, nbits, block)], effort, comp=False)[0]
-    return Encoded(enc.codes, enc.params, enc.consts, enc.sse)
+    Three kernels over the rows (``hi2/encode.py:133-173``): the ladder fit, the 8-bit
+    parameters with their decode, and the codes; the weighted sse is the finish of the
+    GPTQ path (the same sum).  No factor and no error propagation."""
+    dev = _lib.require_gpu(w, d)
+    n_rows, k = w.shape
+    if k % block:
+        raise ValueError(f"K={k} is not a multiple of the block {block}")
+    nb = k // block
+    cfg = EFFORT[effort]
+    wf = w.to(torch.float32).contiguous()
+    if wf.data_ptr() % 16:
+        wf = wf.clone()
+    dv = d.to(dev, torch.float32).reshape(-1).contiguous()
+    lo, st, _ = _fit(wf.reshape(-1, nb, block), dv, 2 ** nbits, cfg["grid"], cfg["ls"], False)
+    lo_u8, st_u8, consts, lo_d, st_d = params_decoded(lo, st)
+    codes = torch.empty(n_rows, k, dtype=torch.uint8, device=dev)
+    sse = torch.empty(n_rows, dtype=torch.float32, device=dev)
+    if n_rows:
+        _lib.call("hi2x_nearest_codes", dev, _lib.ptr(wf), n_rows, k, block, _lib.ptr(lo_d),
+                  _lib.ptr(st_d), nb, int(nbits), _lib.ptr(codes))
+        _lib.call("hi2x_finish", dev, _lib.ptr(codes), None, None, n_rows, k, block,
+                  _lib.ptr(lo_d), _lib.ptr(st_d), nb, _lib.ptr(wf), _lib.ptr(dv),
+                  _lib.ptr(codes), None, _lib.ptr(sse))
+    return Encoded(codes, torch.stack([lo_u8, st_u8], dim=-1), consts, sse)

@@ -124,6 +124,15 @@ int hi2x_finish(const uint8_t* codes_ro, const float* comp_ro, const int64_t* pe
                 int64_t ldd, const float* w, const float* d, uint8_t* codes, float* comp,
                 float* sse, void* stream);
 
+/* The codes of encode_rows (hi2/encode.py:151-155), nearest rounding onto the fitted
+ * ladders: codes [rows, k] u8 = clamp(st == 0 ? 0 : rint((w - lo) / st), 0, 2^nbits - 1)
+ * with w [rows, k] f32 (16-byte aligned), lo_d/st_d [rows, ldd] f32 the decoded ladder of
+ * each block of `block` columns.  With hi2x_ladder_fit, hi2x_params and hi2x_finish (the
+ * sse) it is the whole of encode_rows: no factor, no error propagation. */
+int hi2x_nearest_codes(const float* w, int64_t rows, int64_t k, int64_t block,
+                       const float* lo_d, const float* st_d, int64_t ldd, int nbits,
+                       uint8_t* codes, void* stream);
+
 /* ladder_dequantize (hi2/format.py:63-69): out_h [rows, nb*B] fp16 bits of
  * lo + code*step evaluated in f32 (f64 when exact != 0), one rounding to fp16.
  * lo/step [rows, nb] f32. */

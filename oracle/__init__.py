@@ -231,6 +231,30 @@ def encode_rows_gptq(w, d, u, nbits, block, effort="normal", perm=None, comp=Tru
                 comp=compo, lo_d=lo_d, step_d=st_d)
 
 
+def encode_rows(w, d, nbits, block, effort="normal"):
+    """``hi2/encode.py:133-173`` (nearest rounding): the ladder fit and params as above,
+    then ``codes = clamp(where(step == 0, 0, rint((w - lo) / safe(step))), 0, 2^n - 1)``
+    in float32 (IEEE division, half-to-even) and the weighted sse of the finish.
+    Returns dict(codes, params, consts, sse, lo_d, step_d)."""
+    w = _c(w, np.float32)
+    n, k = w.shape
+    d = _c(d, np.float32).reshape(-1)
+    nb = k // block
+    lo, st = fit_ladder(w.reshape(n, nb, block), d.reshape(1, nb, block), 2 ** nbits, effort)
+    lo_u8, st_u8, consts, lo_d, st_d = params(lo, st)
+    lo_e = np.repeat(lo_d, block, axis=1)
+    st_e = np.repeat(st_d, block, axis=1)
+    safe = np.where(st_e == 0, np.float32(1), st_e).astype(np.float32)
+    with np.errstate(invalid="ignore"):
+        q = np.rint((w - lo_e) / safe).astype(np.float32)
+    q = np.where(st_e == 0, np.float32(0), q)
+    q = np.clip(q, 0, 2 ** nbits - 1)
+    codes = q.astype(np.uint8)
+    codes, _, sse = finish(codes, None, None, block, lo_d, st_d, w, d)
+    return dict(codes=codes, params=np.stack([lo_u8, st_u8], -1), consts=consts, sse=sse,
+                lo_d=lo_d, step_d=st_d)
+
+
 def hessian_update(s, x):
     """S += X^T X; x is float32 or bf16 given as uint16 bits."""
     s = _c(s, np.float32)

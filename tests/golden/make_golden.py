@@ -29,7 +29,9 @@ depend on the reference's own torch-CPU arithmetic:
   and 2048 tokens, a cfg2-style mixed INT2/INT4 case, and cfg1 at its full 2048 x 2048
   as digests and a 64-row slice);
 * the MoE token floor (``hi2/layerwise.py:241-257`` with ``hi2.moe.blend``) on seven
-  experts' sums (``moe_blend.npz``).
+  experts' sums (``moe_blend.npz``);
+* ``hi2.encode.encode_rows`` (nearest rounding, ``hi2/encode.py:133-173``) at INT2/B32,
+  INT4/B64 and INT8/B64 (``nearest.npz``).
 
 The fixtures are plain ``.npz`` data (inputs and expected outputs); nothing of the
 reference is stored.  Run from the repository root:
@@ -41,6 +43,7 @@ reference is stored.  Run from the repository root:
     python tests/golden/make_golden.py qad          # qad.npz only
     python tests/golden/make_golden.py e2e          # e2e_*.npz only
     python tests/golden/make_golden.py moe          # moe_blend.npz only
+    python tests/golden/make_golden.py nearest      # nearest.npz only
 """
 
 import os
@@ -480,7 +483,38 @@ def make_moe():
                         out_n=np.array(out_n, np.int64))
 
 
+def make_nearest():
+    """hi2.encode.encode_rows (nearest rounding, hi2/encode.py:133-173) on the rotated
+    cfg1_k512_t2048 rows with the reference's own diag(Hs) as the weights: INT2/B32 on
+    the first 96 rows, INT4/B64 on the next 96, INT8/B64 on 32."""
+    sys.path.insert(0, REF)
+    sys.path.insert(0, os.path.dirname(OUT))
+    from e2e_recipes import inputs
+    from hi2.encode import encode_rows
+    from hi2.format import fwht_groups
+    from hi2.hessian import HessianStats, transform_sigma
+
+    torch.set_num_threads(1)
+    xb, w, picks, had = inputs("cfg1_k512_t2048")
+    st = HessianStats(w.shape[1])
+    st.update(xb)
+    d = transform_sigma(st.mean(), None, torch.from_numpy(had)).diagonal().clone()
+    wt = fwht_groups(torch.from_numpy(w), torch.from_numpy(had))
+    arrs = {"d": d.numpy(), "wt": wt[:224].numpy()}
+    for tag, (nb, b, a, z) in {"int2": (2, 32, 0, 96), "int4": (4, 64, 96, 192),
+                                "int8": (8, 64, 192, 224)}.items():
+        e = encode_rows(wt[a:z], d, nb, b, "normal")
+        arrs[f"{tag}_codes"] = e.codes.numpy()
+        arrs[f"{tag}_params"] = e.params.numpy()
+        arrs[f"{tag}_consts"] = e.consts.view(torch.int16).numpy()
+        arrs[f"{tag}_sse"] = e.sse.numpy()
+    np.savez_compressed(os.path.join(OUT, "nearest.npz"), **arrs)
+
+
 def main():
+    if sys.argv[1:] == ["nearest"]:
+        make_nearest()
+        return
     if sys.argv[1:] == ["moe"]:
         make_moe()
         return
@@ -578,6 +612,7 @@ def main():
     make_qad()
     make_e2e()
     make_moe()
+    make_nearest()
 
     with open(os.path.join(OUT, "golden_meta.txt"), "w") as f:
         for k, v in meta.items():

@@ -6,7 +6,9 @@ configurations at sizes the checks finish in seconds:
 - cfg5: in tests/test_gpu_moe.py;
 - cfg2 down_proj width (K = 14336): GPTQ rows bit for bit against the oracle given the
   same factor;
-- cfg4 width (K = 28672, fewer tokens than K): the factor through its inversion residual;
+- cfg4 width (K = 28672, fewer tokens than K): the factor through its inversion residual,
+  and a row slice of down_proj with INT2 / INT4 / INT8 rows against the oracle given the
+  GPU's factor;
 - cfg1 (K = 2048, 512 tokens): the whole pipeline against the oracle pipeline, the
   divergence of error feedback on a rank-deficient Hessian located at rounding ties.
 """
@@ -161,3 +163,30 @@ def test_cfg1_pipeline_against_oracle_pipeline(dev):
     print(f"codes equal {match:.5f}  rows diverging {diverged}/{n}  worst first-divergence "
           f"distance {worst:.3g} steps  total sse rel {sse_rel:.3g}")
     assert match >= 0.99 and diverged <= n // 10 and worst < 0.1 and sse_rel < 1e-2
+
+
+def test_gptq_at_cfg4_down_width_with_int8_rows_equals_oracle(dev):
+    """cfg4 down_proj (8192 x 28672, K = 28672 from 8192 rank-deficient tokens; 25 / 72 / 3 %
+    INT2/B32, INT4/B64, INT8/B64 rows): a 24-row slice of each allocation class through
+    one batched run, bit-identical to the oracle given the same factor (codes, params,
+    consts, sse, comp)."""
+    from hi2_amd.hessian import GptqJob, encode_jobs_gptq
+
+    print("cfg4 down_proj width gptq", flush=True)
+    k = 28672
+    hs, u = _factor(dev, k, 8192, 11)
+    d = torch.diagonal(hs).clone()
+    rng = np.random.default_rng(17)
+    w = (0.02 * rng.standard_normal((24, k))).astype(np.float32)
+    specs = [(0, 8, 2, 32), (8, 16, 4, 64), (16, 24, 8, 64)]
+    jobs = [GptqJob(T(w[a:z], dev), d, u, nb, b) for a, z, nb, b in specs]
+    got = encode_jobs_gptq(jobs, "normal", comp=True)
+    u_h, d_h = N(u), N(d)
+    del u, hs
+    for (a, z, nb, b), e in zip(specs, got):
+        want = oracle.encode_rows_gptq(w[a:z], d_h, u_h, nb, b, "normal")
+        assert np.array_equal(N(e.codes), want["codes"]), nb
+        assert np.array_equal(N(e.params), want["params"]), nb
+        assert np.array_equal(N(e.consts).view(np.int16), want["consts"].view(np.int16)), nb
+        assert np.array_equal(N(e.sse), want["sse"]), nb
+        assert np.array_equal(N(e.comp), want["comp"]), nb

@@ -205,15 +205,35 @@ def _encode(dev, w, d, u):
 
 
 def test_nearest_encode_rows_equals_oracle(dev):
+    """encode_rows (ladder fit, params, hi2x_nearest_codes, the finish's sse) against the
+    oracle's nearest rounding, with zero-step blocks (constant rows) among them."""
     from hi2_amd.encode import encode_rows
 
     rng = np.random.default_rng(3)
     w = (rng.standard_normal((40, 256)) * np.exp(rng.standard_normal((1, 256)))).astype(np.float32)
+    w[5] = 0.25
+    w[7, :64] = -1.5
     d = (rng.random(256) + 0.1).astype(np.float32)
-    eye = np.eye(256, dtype=np.float32)
-    want = oracle.encode_rows_gptq(w, d, eye, 2, 32, "fast")
+    want = oracle.encode_rows(w, d, 2, 32, "fast")
     got = encode_rows(T(w, dev), T(d, dev), 2, 32, "fast")
     _same(got, {**want, "comp": None})
+
+
+@pytest.mark.parametrize("tag,spec", [("int2", (2, 32, 0, 96)), ("int4", (4, 64, 96, 192)),
+                                      ("int8", (8, 64, 192, 224))])
+def test_nearest_encode_rows_equals_reference_golden(dev, tag, spec):
+    """encode_rows against hi2.encode.encode_rows itself (tests/golden/nearest.npz)."""
+    import os
+
+    from hi2_amd.encode import encode_rows
+
+    g = np.load(os.path.join(os.path.dirname(__file__), "golden", "nearest.npz"))
+    nb, b, a, z = spec
+    got = encode_rows(T(g["wt"][a:z], dev), T(g["d"], dev), nb, b, "normal")
+    assert np.array_equal(N(got.codes), g[f"{tag}_codes"])
+    assert np.array_equal(N(got.params), g[f"{tag}_params"])
+    assert np.array_equal(N(got.consts).view(np.int16), g[f"{tag}_consts"])
+    assert np.array_equal(N(got.sse), g[f"{tag}_sse"])
 
 
 # ---- ladder, params, finish -------------------------------------------------------------

@@ -352,3 +352,26 @@ def test_assemble_mixed_rows_offsets():
             p0 = t["param_off"][r] * 2
             assert np.array_equal(t["blk_params"][p0:p0 + p[i].size], p[i].reshape(-1))
             assert np.array_equal(t["row_consts"][r], rc[i])
+
+
+NEAREST_SPECS = {"int2": (2, 32, 0, 96), "int4": (4, 64, 96, 192), "int8": (8, 64, 192, 224)}
+
+
+@pytest.mark.parametrize("tag", list(NEAREST_SPECS))
+def test_encode_rows_equals_the_reference_nearest_golden(tag):
+    """oracle.encode_rows against hi2.encode.encode_rows (tests/golden/nearest.npz):
+    codes, params, consts and sse bit for bit; and it equals the GPTQ flow with an
+    identity factor (no error is propagated), the identity the old nearest path used."""
+    import os
+
+    g = np.load(os.path.join(os.path.dirname(__file__), "golden", "nearest.npz"))
+    nb, b, a, z = NEAREST_SPECS[tag]
+    e = oracle.encode_rows(g["wt"][a:z], g["d"], nb, b, "normal")
+    assert np.array_equal(e["codes"], g[f"{tag}_codes"])
+    assert np.array_equal(e["params"], g[f"{tag}_params"])
+    assert np.array_equal(e["consts"].view(np.int16), g[f"{tag}_consts"])
+    assert np.array_equal(e["sse"], g[f"{tag}_sse"])
+    k = g["wt"].shape[1]
+    via = oracle.encode_rows_gptq(g["wt"][a:z], g["d"], np.eye(k, dtype=np.float32), nb, b,
+                                  "normal")
+    assert np.array_equal(via["codes"], e["codes"]) and np.array_equal(via["sse"], e["sse"])
