@@ -111,6 +111,8 @@ def make_inputs(dev, seed=0, cfg=CFG3):
 # the short chains fill the GPU around the long chain's latency-bound steps)
 _CHAIN_STREAMS = {}
 HEAD_START = os.environ.get("HI2_HEAD_START", "transform")
+# the critical chain's rotations and ladder fits on the last chain's stream (0: in place)
+OFFLOAD_PREP = os.environ.get("HI2_OFFLOAD_PREP", "1") != "0"
 
 
 def _chain_stream(dev, i):
@@ -127,15 +129,17 @@ def _chain_stream(dev, i):
 def encode_block(xs, ws, masks, timer=None, lanes=None, keep=None, cfg=CFG3):
     """Encode the whole block.  Each calibration input runs its own chain on its own
     stream (Hessian -> transform -> factor -> rotation -> GPTQ -> packing of the linears
-    it feeds); the chains are independent, so they overlap on the GPU.  The host waits
-    only after every chain has been enqueued (factor status, then one read of the
-    packing's range counter).  keep (a dict) receives each input's (stream, hs, jobs,
-    where, encs)."""
+    it feeds); the chains are independent, so they overlap on the GPU.  The first chain
+    (the widest input: the critical path) hands its rotations and ladder fits, which need
+    only its Hessian's diagonal, to the head of the last chain's stream, where they run
+    while its factor is computed; its rounding waits for them.  The host waits only after every chain has
+    been enqueued (factor status, then one read of the packing's range counter).  keep
+    (a dict) receives each input's (stream, hs, jobs, where, encs)."""
     import torch
 
     from hi2_amd.format import assemble, fwht_groups
-    from hi2_amd.hessian import GptqJob, HessianStats, encode_jobs_gptq
-    from hi2_amd.hessian import finish_factor, inverse_factor_async
+    from hi2_amd.hessian import GptqJob, HessianStats, encode_jobs_gptq, prepare_jobs_gptq
+    from hi2_amd.hessian import finish_factor, inverse_factor_async, round_prepared
 
     dev = next(iter(xs.values())).device
     main = torch.cuda.current_stream(dev)
@@ -145,10 +149,29 @@ def encode_block(xs, ws, masks, timer=None, lanes=None, keep=None, cfg=CFG3):
     width = max(len(l) for l in lanes)
     order = [inp for lane in zip(*[l + [None] * (width - len(l)) for l in lanes]) for inp in lane
              if inp is not None]
+    # the critical chain's preparation moves to the last chain's stream (with one lane
+    # there is nowhere to move it)
+    crit = order[0] if len(lanes) > 1 and OFFLOAD_PREP else None
+    helper = order[-1] if crit is not None else None
     chains = {}
     for li in range(len(lanes)):
         _chain_stream(dev, li).wait_stream(main)
     lead = None  # the first chain's head start: the others wait for its Hessian stages
+
+    def prepare(inp, had, d, u):
+        """Rotation and ladder fits of the linears fed by inp, on the current stream."""
+        jobs, where = [], []
+        for name, n, kk, i in cfg["linears"]:
+            if i != inp:
+                continue
+            wt = fwht_groups(ws[name].float(), had)
+            for nb, b, rows_d, rows_h in masks[name]["groups"]:
+                jobs.append(GptqJob(wt.index_select(0, rows_d), d, u, nb, b))
+                where.append((name, rows_h))
+            del wt
+        return jobs, where, prepare_jobs_gptq(jobs, EFFORT)
+
+    crit_d = None  # (event after the critical chain's d, had, d, u)
     for inp in order:
         k = cfg["inputs"][inp]
         st = _chain_stream(dev, lane_of[inp])
@@ -156,6 +179,19 @@ def encode_block(xs, ws, masks, timer=None, lanes=None, keep=None, cfg=CFG3):
         with torch.cuda.stream(st):
             if lead is not None and lane_of[inp] != 0:
                 st.wait_event(lead)
+            if inp == helper:  # first the critical chain's rotations and fits
+                ev, chad, cd, cu = crit_d
+                st.wait_event(ev)
+                for t in (chad, cd, cu):
+                    t.record_stream(st)
+                cjobs, cwhere, cprep = prepare(crit, chad, cd, cu)
+                cprep.record_stream(_chain_stream(dev, lane_of[crit]))
+                for j in cjobs:
+                    j.w.record_stream(_chain_stream(dev, lane_of[crit]))
+                done = torch.cuda.Event()
+                done.record(st)
+                chains[crit][5:7] = [cjobs, cwhere]
+                crit_prep = (done, cprep)
             had = torch.ones(k // 16, dtype=torch.uint8, device=dev)
             mark("hessian")
             hst = HessianStats(k, dev)
@@ -170,22 +206,31 @@ def encode_block(xs, ws, masks, timer=None, lanes=None, keep=None, cfg=CFG3):
             if HEAD_START == "transform" and lane_of[inp] == 0 and lead is None:
                 lead = torch.cuda.Event()
                 lead.record(st)
+            if inp == crit:  # d is what the ladder fits need
+                ev = torch.cuda.Event()
+                ev.record(st)
             mark("factor")
             u, status = inverse_factor_async(hs, DAMP)
+            if inp == crit:
+                crit_d = (ev, had, d, u)
+                chains[inp] = [st, hs, u, status, had, None, None, None]
+                continue
             mark("rotate")
-            jobs, where = [], []
-            for name, n, kk, i in cfg["linears"]:
-                if i != inp:
-                    continue
-                wt = fwht_groups(ws[name].float(), had)
-                for nb, b, rows_d, rows_h in masks[name]["groups"]:
-                    jobs.append(GptqJob(wt.index_select(0, rows_d), d, u, nb, b))
-                    where.append((name, rows_h))
-                del wt
+            jobs, where, prep = prepare(inp, had, d, u)
             mark("gptq")
-            encs = encode_jobs_gptq(jobs, EFFORT)
+            encs = round_prepared(prep)
             mark("end")
-        chains[inp] = (st, hs, u, status, had, jobs, where, encs)
+        chains[inp] = [st, hs, u, status, had, jobs, where, encs]
+    if crit is not None:
+        st = chains[crit][0]
+        mark = (lambda stage: timer.mark(crit, stage)) if timer else (lambda stage: None)
+        with torch.cuda.stream(st):
+            done, cprep = crit_prep
+            mark("prep_wait")
+            st.wait_event(done)
+            mark("gptq")
+            chains[crit][7] = round_prepared(cprep)
+            mark("end")
     out = {}
     bad = torch.zeros(1, dtype=torch.int32, device=dev)
     for inp in reversed(order):  # the long chain last: the others are packed meanwhile

@@ -4,7 +4,10 @@ Mirror of the reference's ``hi2/hessian.py`` (same names, argument meaning, modu
 globals and errors): ``HessianStats`` (26-47), ``transform_sigma`` (50-68),
 ``inverse_factor`` (71-86), ``encode_rows_gptq_reference`` (89-175), ``GptqJob``
 (178-188), ``_Unit`` / ``_prepare`` / ``_round_kernel`` / ``_finish`` (191-345),
-``encode_jobs_gptq`` (359-416), ``encode_rows_gptq`` (419-443).
+``encode_jobs_gptq`` (359-416), ``encode_rows_gptq`` (419-443).  ``encode_jobs_gptq`` is
+also offered in its two halves, ``prepare_jobs_gptq`` (copies, ladder fits, block
+parameters: nothing that needs the factor) and ``round_prepared``, so that a caller can
+fit a linear's ladders while its input's factor is still being computed.
 
 Every arithmetic step runs in the hi2x HIP kernels (``libhi2x.so``):
 
@@ -53,6 +56,7 @@ __all__ = [
     "EFFORT",
     "GptqJob",
     "HessianStats",
+    "PreparedJobs",
     "encode_jobs_gptq",
     "encode_rows_gptq",
     "encode_rows_gptq_reference",
@@ -63,6 +67,8 @@ __all__ = [
     "inverse_factors_batched",
     "inverse_factors_batched_async",
     "finish_factors_batched",
+    "prepare_jobs_gptq",
+    "round_prepared",
     "transform_sigma",
 ]
 
@@ -494,6 +500,45 @@ def _use_kernel(dev: torch.device, backend: str) -> bool:
     return True
 
 
+@dataclass
+class PreparedJobs:
+    """The factor-independent half of :func:`encode_jobs_gptq`: every job's row chunks
+    copied into working copies, their ladders fitted and their block parameters
+    quantised.  Nothing in it reads a job's ``u``, so it can be made before the factor
+    exists (on any stream; see :meth:`record_stream`) and rounded with
+    :func:`round_prepared` once it does."""
+
+    jobs: list[GptqJob]
+    units: list[_Unit]
+    backend: str
+
+    def record_stream(self, stream: torch.cuda.Stream) -> None:
+        """Mark every tensor made here as used on ``stream`` (for a rounding issued
+        there while these were made on another stream)."""
+        for x in self.units:
+            for t in (x.wc, x.lo_u8, x.step_u8, x.consts, x.lo_d, x.step_d, x.blk_of):
+                if t is not None:
+                    t.record_stream(stream)
+
+
+@torch.no_grad()
+def prepare_jobs_gptq(jobs: list[GptqJob], effort: str = "normal",
+                      backend: str | None = None) -> PreparedJobs:
+    """Cut the jobs into the reference's row chunks (``ROW_ELEMS``) and fit each
+    chunk's ladder (``hi2/hessian.py:89-104``, the part of ``_prepare`` before the
+    factor is used), on the current stream."""
+    backend = backend or os.environ.get("HI2_GPTQ_BACKEND", "auto")
+    for job in jobs:
+        _lib.require_gpu(job.w)
+    units: list[_Unit] = []
+    for ji, job in enumerate(jobs):
+        n_rows, k = job.w.shape
+        step_rows = max(1, ROW_ELEMS // k)
+        for s in range(0, n_rows, step_rows):
+            units.append(_prepare(ji, job, s, step_rows, effort))
+    return PreparedJobs(jobs, units, backend)
+
+
 @torch.no_grad()
 def encode_jobs_gptq(
     jobs: list[GptqJob],
@@ -506,16 +551,20 @@ def encode_jobs_gptq(
     at once, bit-identical to calling it on each.  Jobs are cut into the reference's
     row chunks (``ROW_ELEMS``); chunks with the same K on the same device are batched
     (up to ``BATCH_ELEMS`` weights) through one ``hi2x_gptq_run``.  With ``comp`` every
-    result carries ``Encoded.comp``."""
-    backend = backend or os.environ.get("HI2_GPTQ_BACKEND", "auto")
-    for job in jobs:
-        _lib.require_gpu(job.w)
-    units: list[_Unit] = []
-    for ji, job in enumerate(jobs):
-        n_rows, k = job.w.shape
-        step_rows = max(1, ROW_ELEMS // k)
-        for s in range(0, n_rows, step_rows):
-            units.append(_prepare(ji, job, s, step_rows, effort))
+    result carries ``Encoded.comp``.  Equal to
+    ``round_prepared(prepare_jobs_gptq(jobs, effort, backend), comp, super_blocks)``."""
+    return round_prepared(prepare_jobs_gptq(jobs, effort, backend), comp, super_blocks)
+
+
+@torch.no_grad()
+def round_prepared(prep: PreparedJobs, comp: bool = False,
+                   super_blocks: int | None = None) -> list[Encoded]:
+    """The rounding half of :func:`encode_jobs_gptq` on the current stream: the column
+    loops and cross-block updates of every prepared chunk, then each job's finish.
+    The working copies are consumed (a prepared set is rounded once)."""
+    jobs, units, backend = prep.jobs, prep.units, prep.backend
+    if any(x.wc is None for x in units):
+        raise ValueError("these prepared jobs have already been rounded")
     batches: dict[tuple, list[list[_Unit]]] = {}
     for x in units:
         key = (x.wc.device, x.wc.shape[1])
