@@ -17,7 +17,7 @@ rdna_hint_flex packing into device buffers.  Prints one JSON line, which also ca
 
     python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu] [--refine-steps R]
                     [--many-steps M] [--cfg4-steps S] [--cfg5-steps S]
-    python bench.py --micro {trailing,syrk,factor,refine,stats,qad} [--steps R]  # one kernel alone
+    python bench.py --micro {trailing,syrk,factor,refine,stats,qad,ladder} [--steps R]  # one kernel alone
 """
 
 import argparse
@@ -651,6 +651,7 @@ KERNELS = {  # kind -> (kernel, bound, peak FLOP/s, work unit)
     5: ("refine GEMMs (refine_gradient_kernel + gptq_trailing_kernel)", "mfma", PEAK_F32,
         "2*rows*rank*cols"),
     6: ("refine_block_kernel", "latency", PEAK_F32, "rows*L (column decisions)"),
+    8: ("ladder_fit_kernel", "valu", PEAK_HBM, "bytes of w read (rows*k*4)"),
 }
 DOMINANT = 0  # the GPTQ trailing-update GEMM: the metric's MFMA kernel with the most time
 
@@ -799,7 +800,8 @@ def micro(which, reps=3):
     stats: ColumnStats.update of 8192 bf16 tokens and the cached-Sigma payload at
     K = 4096 and 14336; qad: the QAD decode forward, backward and transform over the
     latents of q_proj, gate_proj and down_proj (30 % INT2/B32, 70 % INT4/B64 rows, step
-    units)."""
+    units); ladder: the ladder fits of down_proj's and q_proj's rows (30 % INT2/B32,
+    70 % INT4/B64, effort "normal")."""
     import torch
 
     from hi2_amd import _lib
@@ -836,7 +838,23 @@ def micro(which, reps=3):
         _lib.timing_enable([])
         return ms, stats
 
-    if which == "trailing":
+    if which == "ladder":
+        from hi2_amd.encode import EFFORT as EFFORTS
+        from hi2_amd.encode import _fit
+
+        cfg = EFFORTS[EFFORT]
+        for n, k in ((HIDDEN, INTER), (HIDDEN, HIDDEN)):
+            g = torch.Generator(device=dev).manual_seed(0)
+            w = torch.randn(n, k, generator=g, device=dev) * 0.02
+            d = torch.rand(k, generator=g, device=dev) + 0.5
+            for frac, nbits, b in CFG3["alloc"]:
+                rows = int(round(frac * n))
+                wb = w[:rows].reshape(rows, k // b, b)
+                ms, stats = timed(lambda: _fit(wb, d, 2 ** nbits, cfg["grid"], cfg["ls"],
+                                               False), [8])
+                print(json.dumps({"micro": "ladder", "rows": rows, "k": k, "nbits": nbits,
+                                  "block": b, "ms": ms, "kernels": stats}), flush=True)
+    elif which == "trailing":
         for n, k in ((HIDDEN, INTER), (INTER, HIDDEN)):
             g = torch.Generator(device=dev).manual_seed(0)
             u = torch.triu(torch.randn(k, k, generator=g, device=dev) * (0.1 / k ** 0.5))
@@ -994,7 +1012,8 @@ def main():
                     help="timed steps of the cfg4 (Llama-3-70B-shaped layer) leg (0: skip)")
     ap.add_argument("--cfg5-steps", type=int, default=2,
                     help="timed steps of the cfg5 (OLMoE-shaped MoE layer) leg (0: skip)")
-    ap.add_argument("--micro", choices=["trailing", "syrk", "factor", "refine", "stats", "qad"],
+    ap.add_argument("--micro", choices=["trailing", "syrk", "factor", "refine", "stats", "qad",
+                                        "ladder"],
                     help="instead of the block step: one kernel family alone at the cfg3 "
                          "shapes (for single-kernel profiles; prints one line per shape)")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",

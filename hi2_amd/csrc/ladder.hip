@@ -107,6 +107,221 @@ __global__ __launch_bounds__(256) void ladder_fit_kernel(
   if (out_err) out_err[i] = best_err;
 }
 
+// The same fit with NL lanes (2 or 4) per (row, block), for B = 32 and 64: the one-lane
+// kernel holds 2B values per lane (x and d) and runs one wave per SIMD at B = 64, too
+// few to hide its dependent chains.  Torch's CPU sum of a block runs over 8-wide vectors
+// (position e % 8); lane h of a group owns the positions [h P, h P + P), P = 8 / NL,
+// B / NL elements, as local slot j = P (e / 8) + e % 8 - h P.  Every sum is torch's order
+// split at the vector position: each lane forms the per-position partials of its
+// positions in that order, lane 0 starts the sum over positions from zero and each lane
+// in turn continues it with its own (one lane-to-lane move per lane), and the last
+// lane's total goes to the whole group, so every decision below is taken identically by
+// all NL lanes and equals the one-lane kernel's.
+template <int NL>
+struct LaneGroup {  // DPP moves within aligned groups of NL lanes (quad_perm patterns)
+  static_assert(NL == 2 || NL == 4, "lanes per group");
+  // from the previous lane of the group (lane 0 reads itself)
+  static constexpr int PREV = NL == 2 ? 0xA0 : 0x90;  // [0,0,2,2] / [0,0,1,2]
+  static constexpr int LAST = NL == 2 ? 0xF5 : 0xFF;  // [1,1,3,3] / [3,3,3,3]
+  static constexpr int X1 = 0xB1, X2 = 0x4E;           // lane ^ 1: [1,0,3,2]; ^ 2: [2,3,0,1]
+  static constexpr int FIRST = NL == 2 ? 0xA0 : 0x00;  // lane 0 of the group
+  template <int CTRL>
+  static __device__ __forceinline__ float mov(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL,
+                                                              0xf, 0xf, false));
+  }
+  template <int CTRL>
+  static __device__ __forceinline__ int movi(int v) {
+    return __builtin_amdgcn_mov_dpp(v, CTRL, 0xf, 0xf, false);
+  }
+};
+
+// torch_sum_small<B> of fn over the group's elements; fn(j) yields the element in local
+// slot j.  B / 32 rows of 4 vectors, no tail vectors for B = 32 and 64.
+template <int B, int NL, class F>
+__device__ __forceinline__ float group_sum(F fn) {
+  static_assert(B % 32 == 0 && B <= 64, "block size");
+  constexpr int SI = B / 32, P = 8 / NL;
+  using LG = LaneGroup<NL>;
+  float Q[P];
+#pragma unroll
+  for (int vv = 0; vv < P; ++vv) {
+    float p[4];
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) p[kk] = 0.0f;
+#pragma unroll
+    for (int i = 0; i < SI; ++i)
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) p[kk] += fn((i * 4 + kk) * P + vv);
+    Q[vv] = ((p[0] + p[1]) + p[2]) + p[3];
+  }
+  float acc = 0.0f;
+#pragma unroll
+  for (int vv = 0; vv < P; ++vv) acc += Q[vv];
+  // after move m, lane m holds the sum over positions [0, (m + 1) P)
+#pragma unroll
+  for (int m = 1; m < NL; ++m) {
+    float t = LG::template mov<LG::PREV>(acc);
+#pragma unroll
+    for (int vv = 0; vv < P; ++vv) t += Q[vv];
+    acc = t;
+  }
+  return LG::template mov<LG::LAST>(acc);
+}
+
+template <int B, int NL>
+__global__ __launch_bounds__(256) void ladder_fit_group_kernel(
+    const float* __restrict__ w, const float* __restrict__ d, int64_t rows, int64_t k,
+    int nlev, Grid grid, int G, int ls, float* __restrict__ out_lo,
+    float* __restrict__ out_st, float* __restrict__ out_err) {
+  constexpr int NE = B / NL, P = 8 / NL;  // elements and positions per lane
+  using LG = LaneGroup<NL>;
+  const int64_t nb = k / B;
+  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t i = gid / NL;
+  const int h = (int)(gid % NL);
+  if (i >= rows * nb) return;  // the lanes of a group leave together
+  const int64_t r = i / nb, b = i % nb;
+  const float* wp = w + r * k + b * B + P * h;
+  const float* dp = d + b * B + P * h;
+  float x[NE], dd[NE];
+#pragma unroll
+  for (int q = 0; q < B / 8; ++q) {  // vector q: elements 8q + P h .. 8q + P h + P - 1
+    if constexpr (P == 4) {
+      const float4 v = *reinterpret_cast<const float4*>(wp + 8 * q);
+      const float4 e = *reinterpret_cast<const float4*>(dp + 8 * q);
+      x[4 * q] = v.x;
+      x[4 * q + 1] = v.y;
+      x[4 * q + 2] = v.z;
+      x[4 * q + 3] = v.w;
+      dd[4 * q] = e.x;
+      dd[4 * q + 1] = e.y;
+      dd[4 * q + 2] = e.z;
+      dd[4 * q + 3] = e.w;
+    } else {
+      const float2 v = *reinterpret_cast<const float2*>(wp + 8 * q);
+      const float2 e = *reinterpret_cast<const float2*>(dp + 8 * q);
+      x[2 * q] = v.x;
+      x[2 * q + 1] = v.y;
+      dd[2 * q] = e.x;
+      dd[2 * q + 1] = e.y;
+    }
+  }
+  const float nm = (float)(nlev - 1);
+  // min / max as the sequential scan from x[0] with strict comparisons: the first
+  // element (in index order) equal to the extreme.  Each lane scans its elements from
+  // x[0]; the group then keeps the smaller (larger) value, on a tie the earlier element.
+  const float x0 = LG::template mov<LG::FIRST>(x[0]);
+  float mn = x0, mx = x0;
+  int imn = 0, imx = 0;
+#pragma unroll
+  for (int j = 0; j < NE; ++j) {
+    const int e = 8 * (j / P) + P * h + (j % P);
+    if (x[j] < mn) {
+      mn = x[j];
+      imn = e;
+    }
+    if (x[j] > mx) {
+      mx = x[j];
+      imx = e;
+    }
+  }
+  auto merge = [&](float omn, int oin, float omx, int oix) {
+    const bool tmn = omn < mn || (omn == mn && oin < imn);
+    const bool tmx = omx > mx || (omx == mx && oix < imx);
+    mn = tmn ? omn : mn;
+    imn = tmn ? oin : imn;
+    mx = tmx ? omx : mx;
+    imx = tmx ? oix : imx;
+  };
+  merge(LG::template mov<LG::X1>(mn), LG::template movi<LG::X1>(imn),
+        LG::template mov<LG::X1>(mx), LG::template movi<LG::X1>(imx));
+  if constexpr (NL == 4)
+    merge(LG::template mov<LG::X2>(mn), LG::template movi<LG::X2>(imn),
+          LG::template mov<LG::X2>(mx), LG::template movi<LG::X2>(imx));
+  const float span = mx - mn;
+
+  // The code of an element is clamp(rint((x - lo) / safe)).  q0 = (x - lo) * (1 / safe)
+  // is within 2 ulp of the quotient, so rint(q0) is the quotient's rint unless q0 lies
+  // within 2 ulp of a half-integer: |q0 - rint(q0)| >= 0.5 - tol, tol = (nm + 1) 2^-22
+  // covering 2 ulp everywhere below nm + 1 (farther out both clamp to the same end).
+  // The error of a candidate is summed from those cheap codes, and the wave sums it
+  // again with the exact quotients (div_rcp_code) when any of its lanes met a near-tie.
+  // A zero code may come out as -0 here and +0 there: it only ever multiplies into a
+  // term that is squared or added to +0 first, so the sums are the same.
+  const float tol = (nm + 1.0f) * 0x1p-22f;
+  auto err_exact = [&](float lo, float step, float safe, float ys) {
+    return group_sum<B, NL>([&](int j) {
+      const float c = clamp_code(__builtin_rintf(div_rcp_code(x[j] - lo, safe, ys)), nm);
+      const float rec = lo + c * step;
+      const float df = rec - x[j];
+      return dd[j] * (df * df);
+    });
+  };
+  auto err_of = [&](float lo, float step) {
+    const float safe = (step == 0.0f) ? 1.0f : step;
+    const float ys = 1.0f / safe;
+    bool near = false;
+    const float e = group_sum<B, NL>([&](int j) {
+      const float q0 = (x[j] - lo) * ys;
+      const float r0 = __builtin_rintf(q0);
+      near = near || __builtin_fabsf(q0 - r0) >= 0.5f - tol;
+      const float c = __builtin_amdgcn_fmed3f(r0, 0.0f, nm);
+      const float rec = lo + c * step;
+      const float df = rec - x[j];
+      return dd[j] * (df * df);
+    });
+    if (__builtin_amdgcn_ballot_w64(near) == 0) return e;
+    return err_exact(lo, step, safe, ys);
+  };
+
+  float best_lo = 0.0f, best_st = 0.0f, best_err = 0.0f;
+  bool first = true;
+  for (int a = 0; a < G; ++a) {
+    const float lo = mn + grid.v[a] * span;
+    for (int bb = 0; bb < G; ++bb) {
+      const float step = ((mx - grid.v[bb] * span) - lo) / nm;
+      const float err = err_of(lo, step);
+      if (first || err < best_err) {
+        best_lo = lo;
+        best_st = step;
+        best_err = err;
+        first = false;
+      }
+    }
+  }
+  for (int it = 0; it < ls; ++it) {
+    const float safe = (best_st == 0.0f) ? 1.0f : best_st;
+    const float ys = 1.0f / safe;
+    float c[NE];
+#pragma unroll
+    for (int j = 0; j < NE; ++j)
+      c[j] = clamp_code(__builtin_rintf(div_rcp_code(x[j] - best_lo, safe, ys)), nm);
+    const float sd = group_sum<B, NL>([&](int j) { return dd[j]; });
+    const float sc = group_sum<B, NL>([&](int j) { return dd[j] * c[j]; });
+    const float scc = group_sum<B, NL>([&](int j) { return (dd[j] * c[j]) * c[j]; });
+    const float sw = group_sum<B, NL>([&](int j) { return dd[j] * x[j]; });
+    const float scw = group_sum<B, NL>([&](int j) { return (dd[j] * c[j]) * x[j]; });
+    const float det = sd * scc - sc * sc;
+    const bool ok = __builtin_fabsf(det) > 1e-20f;
+    const float step = ok ? (sd * scw - sc * sw) / det : 0.0f;
+    const float sdc = (sd < 1e-20f) ? 1e-20f : sd;
+    const float lo =
+        ok ? (sw - step * sc) / sdc : group_sum<B, NL>([&](int j) { return x[j]; }) / (float)B;
+    const float err = err_of(lo, step);
+    if (err < best_err && step > 0.0f) {
+      best_lo = lo;
+      best_st = step;
+      best_err = err;
+    }
+  }
+  if (h == 0) {
+    out_lo[i] = best_lo;
+    out_st[i] = best_st;
+    if (out_err) out_err[i] = best_err;
+  }
+}
+
 // quantize_params + decode_params, one wave per row (max/min reductions are exact).
 __global__ __launch_bounds__(256) void params_kernel(
     const float* __restrict__ lo, const float* __restrict__ step, int64_t rows, int64_t nb,
@@ -312,15 +527,26 @@ __global__ __launch_bounds__(256) void nearest_codes_kernel(
   *reinterpret_cast<uint32_t*>(codes + r * k + c0) = packed;
 }
 
+#ifndef LADDER_LANES
+#define LADDER_LANES 2  // measured: 4 lanes (twice the occupancy) lose more to the moves
+#endif
+
 template <int B>
 int launch_fit(const float* w, const float* d, int64_t rows, int64_t k, int nlev,
                const Grid& grid, int g, int ls, float* lo, float* step, float* err,
                hipStream_t s) {
   const int64_t total = rows * (k / B);
-  const dim3 blocks((unsigned)((total + 255) / 256));
   LaunchTimer timer(HI2X_TIME_LADDER_FIT, 4.0 * rows * k, s);
-  hipLaunchKernelGGL(ladder_fit_kernel<B>, blocks, dim3(256), 0, s, w, d, rows, k, nlev, grid,
-                     g, ls, lo, step, err);
+  if constexpr (B == 32 || B == 64) {  // a group of lanes per (row, block)
+    constexpr int NL = LADDER_LANES;
+    const dim3 blocks((unsigned)((NL * total + 255) / 256));
+    hipLaunchKernelGGL((ladder_fit_group_kernel<B, NL>), blocks, dim3(256), 0, s, w, d, rows, k,
+                       nlev, grid, g, ls, lo, step, err);
+  } else {
+    const dim3 blocks((unsigned)((total + 255) / 256));
+    hipLaunchKernelGGL(ladder_fit_kernel<B>, blocks, dim3(256), 0, s, w, d, rows, k, nlev,
+                       grid, g, ls, lo, step, err);
+  }
   return launch_status("ladder_fit_kernel");
 }
 

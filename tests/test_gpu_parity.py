@@ -273,6 +273,53 @@ def test_fit_ladder_ties_equal_oracle(dev, n, b):
         assert np.array_equal(N(lo), lo_w) and np.array_equal(N(st), st_w), effort
 
 
+@pytest.mark.parametrize("b", [16, 32, 64])
+def test_fit_ladder_extremes_equal_oracle(dev, b):
+    """Blocks whose min / max are repeated, signed zeros or at the block's first element:
+    the fit's span comes from a sequential scan with strict comparisons (the first
+    element equal to the extreme), which the two-lane kernel rebuilds from each lane's
+    scan and the element positions.  Also all-zero, constant and two-valued blocks, where
+    every candidate's step is zero or the refit's determinant vanishes."""
+    from hi2_amd.encode import fit_ladder
+
+    rng = np.random.default_rng(b)
+    rows, nb = 48, 640 // b
+    wb = (rng.standard_normal((rows, nb, b)) * 0.02).astype(np.float32)
+    for r in range(rows):
+        for j in range(nb):
+            kind = (r * nb + j) % 8
+            blk = wb[r, j]
+            if kind == 0:    # +0 and -0 as the minimum at several positions
+                blk[:] = np.abs(blk)
+                blk[rng.choice(b, 3, replace=False)] = np.float32(-0.0)
+                blk[rng.choice(b, 2, replace=False)] = np.float32(0.0)
+            elif kind == 1:  # -0 and +0 as the maximum
+                blk[:] = -np.abs(blk)
+                blk[rng.choice(b, 2, replace=False)] = np.float32(0.0)
+                blk[rng.choice(b, 2, replace=False)] = np.float32(-0.0)
+            elif kind == 2:  # the extremes at element 0 and repeated later
+                blk[0] = blk.min() - np.float32(0.01)
+                blk[rng.choice(np.arange(1, b), 3, replace=False)] = blk[0]
+            elif kind == 3:  # all zeros, mixed signs
+                blk[:] = np.where(rng.random(b) < 0.5, np.float32(0.0), np.float32(-0.0))
+            elif kind == 4:  # constant
+                blk[:] = np.float32(0.013)
+            elif kind == 5:  # two values
+                blk[:] = np.where(rng.random(b) < 0.5, np.float32(-0.01), np.float32(0.02))
+            elif kind == 6:  # the extremes in the last positions of each lane's half
+                blk[b - 1] = np.float32(0.5)
+                blk[3] = np.float32(-0.5)
+                blk[7] = np.float32(-0.5)
+    db = (rng.random((1, nb, b)) + 0.5).astype(np.float32)
+    for n in (4, 16, 256):
+        for effort in ("fast", "normal"):
+            lo_w, st_w = oracle.fit_ladder(wb, db, n, effort)
+            lo, st = fit_ladder(T(wb, dev), T(db, dev), n, effort)
+            lo, st = N(lo), N(st)
+            assert np.array_equal(lo.view(np.uint32), lo_w.view(np.uint32)), (n, effort)
+            assert np.array_equal(st.view(np.uint32), st_w.view(np.uint32)), (n, effort)
+
+
 def test_params_equal_oracle(dev):
     from hi2_amd.encode import params_decoded, quantize_params
     from hi2_amd.format import decode_params
