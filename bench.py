@@ -137,7 +137,7 @@ def encode_block(xs, ws, masks, timer=None, lanes=None, keep=None, cfg=CFG3):
     (a dict) receives each input's (stream, hs, jobs, where, encs)."""
     import torch
 
-    from hi2_amd.format import assemble, fwht_groups
+    from hi2_amd.format import assemble, rotate_rows
     from hi2_amd.hessian import GptqJob, HessianStats, encode_jobs_gptq, prepare_jobs_gptq
     from hi2_amd.hessian import finish_factor, inverse_factor_async, round_prepared
 
@@ -164,11 +164,10 @@ def encode_block(xs, ws, masks, timer=None, lanes=None, keep=None, cfg=CFG3):
         for name, n, kk, i in cfg["linears"]:
             if i != inp:
                 continue
-            wt = fwht_groups(ws[name].float(), had)
             for nb, b, rows_d, rows_h in masks[name]["groups"]:
-                jobs.append(GptqJob(wt.index_select(0, rows_d), d, u, nb, b))
+                # == fwht_groups(ws[name].float(), had).index_select(0, rows_d)
+                jobs.append(GptqJob(rotate_rows(ws[name], had, rows_d), d, u, nb, b))
                 where.append((name, rows_h))
-            del wt
         return jobs, where, prepare_jobs_gptq(jobs, EFFORT)
 
     crit_d = None  # (event after the critical chain's d, had, d, u)
@@ -273,7 +272,7 @@ def stage_breakdown(xs, ws, masks, cfg=CFG3):
     import torch
 
     from hi2_amd import _lib
-    from hi2_amd.format import assemble, fwht_groups
+    from hi2_amd.format import assemble, rotate_rows
     from hi2_amd.hessian import GptqJob, HessianStats, encode_jobs_gptq, inverse_factor
 
     dev = next(iter(xs.values())).device
@@ -306,10 +305,8 @@ def stage_breakdown(xs, ws, masks, cfg=CFG3):
                 continue
             kinds = [7, 8, 4, 0, 10, 9]
             _lib.timing_enable(kinds)
-            wt = fwht_groups(ws[name].float(), had)
-            jobs = [GptqJob(wt.index_select(0, rows_d), d, u, nb, b)
+            jobs = [GptqJob(rotate_rows(ws[name], had, rows_d), d, u, nb, b)
                     for nb, b, rows_d, _ in masks[name]["groups"]]
-            del wt
             encs = encode_jobs_gptq(jobs, EFFORT)
             pieces = [(g[3], e.codes, e.params, e.consts)
                       for g, e in zip(masks[name]["groups"], encs)]
@@ -329,14 +326,15 @@ def stage_breakdown(xs, ws, masks, cfg=CFG3):
             del jobs, encs
         del hs, u, d
     rates = {}
-    for kind, kname in ((7, "fwht16_kernel"), (9, "assemble_kernel")):
+    for kind, kname in ((7, "rotate_rows_kernel"), (9, "assemble_kernel")):
         b, ms = hbm[kind]
         if ms > 0:
             gbs = b / ms / 1e6
             rates[kname] = {"bound": "hbm", "achieved": gbs, "peak": PEAK_HBM / 1e9,
                             "unit": "GB/s", "frac": gbs / (PEAK_HBM / 1e9),
                             "bytes_per_step": b, "ms_per_step": ms,
-                            "work": "fwht: 2 x 4 B per weight (f32 in and out)" if kind == 7
+                            "work": "rotation: 2 B read (bf16) + 4 B written (f32) per weight "
+                            "of the selected rows" if kind == 7
                             else "pack: code bytes read + packed words + params + consts"}
     return per_input, per_linear, rates
 
@@ -435,7 +433,7 @@ def encode_moe(idx, x, xd, wgu, wdn, masks, timer=None):
     expert), and packing of the 192 expert tensors into device buffers."""
     import torch
 
-    from hi2_amd.format import assemble_many, fwht_groups
+    from hi2_amd.format import assemble_many, rotate_rows
     from hi2_amd.hessian import (GptqJob, encode_jobs_gptq, finish_factors_batched,
                                  inverse_factors_batched_async)
     from hi2_amd.moe import ExpertHessians, route_order
@@ -463,8 +461,6 @@ def encode_moe(idx, x, xd, wgu, wdn, masks, timer=None):
     u_g, st_g = inverse_factors_batched_async(hs_g, DAMP)
     u_d, st_d = inverse_factors_batched_async(hs_d, DAMP)
     mark("moe", "rotate")
-    wt_g = fwht_groups(wgu.reshape(-1, H5).float(), had_h).reshape(E5, 2 * I5, H5)
-    wt_d = fwht_groups(wdn.reshape(-1, I5).float(), had_i).reshape(E5, H5, I5)
     d_g = torch.diagonal(hs_g, dim1=1, dim2=2).contiguous()
     d_d = torch.diagonal(hs_d, dim1=1, dim2=2).contiguous()
     # one job per expert, projection input and allocation class: gate and up rows of one
@@ -476,13 +472,12 @@ def encode_moe(idx, x, xd, wgu, wdn, masks, timer=None):
             rg = masks[(e, "gate")]["groups"][ci]
             ru = masks[(e, "up")]["groups"][ci]
             rows = torch.cat([rg[2], ru[2] + I5])
-            jobs.append(GptqJob(wt_g[e].index_select(0, rows), d_g[e], u_g[e], nb, b))
+            jobs.append(GptqJob(rotate_rows(wgu[e], had_h, rows), d_g[e], u_g[e], nb, b))
             where.append([((e, "gate"), rg[3], 0, rg[3].numel()),
                           ((e, "up"), ru[3], rg[3].numel(), rows.numel())])
         for nb, b, rows_d, rows_h in masks[(e, "down")]["groups"]:
-            jobs.append(GptqJob(wt_d[e].index_select(0, rows_d), d_d[e], u_d[e], nb, b))
+            jobs.append(GptqJob(rotate_rows(wdn[e], had_i, rows_d), d_d[e], u_d[e], nb, b))
             where.append([((e, "down"), rows_h, 0, rows_h.numel())])
-    del wt_g, wt_d
     mark("moe", "gptq")
     encs = encode_jobs_gptq(jobs, EFFORT)
     mark("moe", "pack")

@@ -39,6 +39,7 @@ SIGNATURES = {
     "hi2x_finish": [_P, _P, _P, _I64, _I64, _I64, _P, _P, _I64, _P, _P, _P, _P, _P, _P],
     "hi2x_ladder_dequantize": [_P, _P, _P, _I64, _I64, _I64, _I, _P, _P],
     "hi2x_fwht16": [_P, _P, _I, _I64, _I64, _P, _P],
+    "hi2x_rotate_rows": [_P, _I, _I64, _I64, _P, _I64, _I64, _P, _P, _P, _I64, _P],
     "hi2x_pack_codes": [_P, _I64, _I64, _I, _P, _P, _P],
     "hi2x_assemble_piece": [_P, _I64, _P, _P, _P, _I64, _I, _I64, _P, _P, _P, _P, _P, _P, _P],
     "hi2x_hessian_syrk": [_P, _I, _I64, _I64, _P, _P, _I64, _P],

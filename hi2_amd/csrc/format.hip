@@ -41,6 +41,76 @@ __global__ __launch_bounds__(256) void fwht16_kernel(const T* __restrict__ x, T*
   }
 }
 
+// The weight preparation of a GPTQ unit in one pass: out[i] = fwht16 of row rows[i] of
+// (float(w) * col_scale) (rows null: row i; col_scale null: no product).  float(bf16)
+// is exact and the product is one rounding, as the reference's elementwise ops; the
+// transform is fwht16_kernel's.  One thread per 16-column group, consecutive threads
+// on consecutive groups of a row: a bf16 row is read in 32-byte pieces and written as
+// f32 in 64-byte pieces, each once.
+template <typename T>
+__global__ __launch_bounds__(256) void rotate_rows_kernel(
+    const T* __restrict__ w, int64_t ldw, int64_t nw, const int64_t* __restrict__ rows,
+    int64_t n, int64_t k, const float* __restrict__ col_scale,
+    const uint8_t* __restrict__ flags, float* __restrict__ out, int64_t ldo) {
+  const int64_t ng = k / 16;
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= n * ng) return;
+  const int64_t i = t / ng, g = t % ng;
+  const int64_t src = rows ? rows[i] : i;
+  float* yo = out + i * ldo + 16 * g;
+  if (src < 0 || src >= nw) {  // an index out of range: the row reads NaN
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      *reinterpret_cast<float4*>(yo + 4 * q) =
+          make_float4(__builtin_nanf(""), __builtin_nanf(""), __builtin_nanf(""),
+                      __builtin_nanf(""));
+    return;
+  }
+  const T* xi = w + src * ldw + 16 * g;
+  float v[16];
+  if constexpr (sizeof(T) == 2) {
+    const uint4 a = *reinterpret_cast<const uint4*>(xi);
+    const uint4 b = *reinterpret_cast<const uint4*>(xi + 8);
+    const uint32_t u[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      v[2 * e] = __uint_as_float(u[e] << 16);
+      v[2 * e + 1] = __uint_as_float(u[e] & 0xffff0000u);
+    }
+  } else {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const float4 a = *reinterpret_cast<const float4*>(xi + 4 * q);
+      v[4 * q] = a.x;
+      v[4 * q + 1] = a.y;
+      v[4 * q + 2] = a.z;
+      v[4 * q + 3] = a.w;
+    }
+  }
+  if (col_scale) {
+#pragma unroll
+    for (int q = 0; q < 16; ++q) v[q] = v[q] * col_scale[16 * g + q];
+  }
+  float y[16];
+  if (flags && flags[g]) {
+    const float qv = 0.25f;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      float acc = 0.0f;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc = __builtin_fmaf(v[e], hneg(e, j) ? -qv : qv, acc);
+      y[j] = acc;
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < 16; ++j) y[j] = v[j];
+  }
+#pragma unroll
+  for (int q = 0; q < 4; ++q)
+    *reinterpret_cast<float4*>(yo + 4 * q) = make_float4(y[4 * q], y[4 * q + 1], y[4 * q + 2],
+                                                         y[4 * q + 3]);
+}
+
 __device__ __forceinline__ void note_bad(int32_t* bad, int n) {
   if (n && bad) atomicAdd(bad, n);
 }
@@ -113,6 +183,35 @@ __global__ __launch_bounds__(256) void assemble_kernel(
 }  // namespace hi2x
 
 using namespace hi2x;
+
+extern "C" int hi2x_rotate_rows(const void* w, int dtype, int64_t ldw, int64_t nw,
+                                const int64_t* rows, int64_t n, int64_t k,
+                                const float* col_scale, const uint8_t* flags, float* out,
+                                int64_t ldo, void* stream) {
+  clear_error();
+  HI2X_REQUIRE(k > 0 && k % 16 == 0, "rotate_rows: K=%lld must be a multiple of 16",
+               (long long)k);
+  HI2X_REQUIRE(dtype == 0 || dtype == 2, "rotate_rows: dtype %d (0 = f32, 2 = bf16)", dtype);
+  HI2X_REQUIRE(n >= 0 && nw >= 0 && ldw >= k && ldo >= k, "rotate_rows: bad shape or strides");
+  HI2X_REQUIRE(rows || n <= nw, "rotate_rows: %lld rows of a %lld-row matrix", (long long)n,
+               (long long)nw);
+  if (n == 0) return HI2X_OK;
+  HI2X_REQUIRE(w && out, "rotate_rows: null buffer");
+  HI2X_REQUIRE(((uintptr_t)w % 16) == 0 && ((uintptr_t)out % 16) == 0 &&
+                   (ldw * (dtype == 0 ? 4 : 2)) % 16 == 0 && (ldo * 4) % 16 == 0,
+               "rotate_rows: rows must start on 16-byte boundaries");
+  const int64_t total = n * (k / 16);
+  const dim3 grid((unsigned)((total + 255) / 256));
+  hipStream_t s = as_stream(stream);
+  LaunchTimer timer(HI2X_TIME_FWHT, (double)n * k * ((dtype == 0 ? 4 : 2) + 4), s);
+  if (dtype == 0)
+    hipLaunchKernelGGL(rotate_rows_kernel<float>, grid, dim3(256), 0, s, (const float*)w, ldw,
+                       nw, rows, n, k, col_scale, flags, out, ldo);
+  else
+    hipLaunchKernelGGL(rotate_rows_kernel<uint16_t>, grid, dim3(256), 0, s, (const uint16_t*)w,
+                       ldw, nw, rows, n, k, col_scale, flags, out, ldo);
+  return launch_status("rotate_rows_kernel");
+}
 
 extern "C" int hi2x_fwht16(const void* x, void* y, int dtype, int64_t rows, int64_t k,
                            const uint8_t* flags, void* stream) {

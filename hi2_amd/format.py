@@ -3,8 +3,9 @@
 Mirror of the hot-path part of the reference's ``hi2/format.py`` (same names, argument
 meaning and errors): ``GROUP``, ``hadamard16`` (22-27), ``fwht_groups`` (30-41),
 ``decode_params`` (45-60), ``ladder_dequantize`` (63-69), ``pack_codes`` (73-85),
-``HI2Tensor`` / ``FIELDS`` (97-124) and ``assemble`` (127-184).  The arithmetic runs in
-the hi2x HIP kernels; inputs must be device tensors (``assemble`` returns the flat
+``HI2Tensor`` / ``FIELDS`` (97-124) and ``assemble`` (127-184), plus ``rotate_rows`` (the
+smoothing, rotation and row selection a tensor's weights go through before GPTQ, in one
+pass) and ``assemble_many``.  The arithmetic runs in the hi2x HIP kernels; inputs must be device tensors (``assemble`` returns the flat
 buffers on the host, as the reference does).  Decode/verification helpers
 (``dequantize``, accounting) are not part of the encode path and are not provided.
 """
@@ -52,6 +53,46 @@ def fwht_groups(x: torch.Tensor, flags: torch.Tensor) -> torch.Tensor:
     _lib.call("hi2x_fwht16", dev, _lib.ptr(xi), _lib.ptr(out), 0 if work == torch.float32 else 1,
               rows, k, _lib.ptr(fl))
     return out.to(x.dtype)
+
+
+def rotate_rows(w: torch.Tensor, flags: torch.Tensor | None, rows: torch.Tensor | None = None,
+                col_scale: torch.Tensor | None = None) -> torch.Tensor:
+    """``fwht_groups(w.float() * col_scale, flags)[rows]`` as float32 in one pass over the
+    selected rows (``hi2x_rotate_rows``): the reference's smoothing, staging and
+    rotation of a tensor's weights and its row selection per candidate
+    (``hi2/calibrate.py:106-111, 329-330, 353-357``), bit for bit.  ``w`` is float32 or
+    bfloat16 ``[N, K]``; ``rows`` device or host int64 indices (None: every row; host
+    indices are range-checked here, a device index out of range yields a row of NaN)."""
+    if w.dim() != 2 or w.dtype not in (torch.float32, torch.bfloat16):
+        raise ValueError("rotate_rows takes a float32 or bfloat16 [N, K] matrix")
+    n_all, k = w.shape
+    if k % GROUP:
+        raise ValueError(f"K={k} must be a multiple of {GROUP}")
+    dev = _lib.require_gpu(w)
+    if w.stride(1) != 1 or (w.stride(0) * w.element_size()) % 16:
+        w = w.contiguous()
+    if w.data_ptr() % 16:
+        w = w.clone()
+    if rows is not None and rows.device.type == "cpu" and rows.numel():
+        if int(rows.min()) < 0 or int(rows.max()) >= n_all:
+            raise IndexError(f"row index out of range for {n_all} rows")
+    fl = None
+    if flags is not None:
+        if flags.numel() != k // GROUP:
+            raise ValueError(f"flags has {flags.numel()} entries, expected {k // GROUP}")
+        fl = _lib.to_device(flags.reshape(-1), dev, torch.uint8).contiguous()
+    idx = None if rows is None else _lib.to_device(rows.reshape(-1), dev, torch.int64).contiguous()
+    n = n_all if idx is None else idx.numel()
+    cs = None
+    if col_scale is not None:
+        cs = _lib.to_device(col_scale.reshape(-1), dev, torch.float32).contiguous()
+        if cs.numel() != k:
+            raise ValueError(f"col_scale has {cs.numel()} entries, expected {k}")
+    out = torch.empty(n, k, dtype=torch.float32, device=dev)
+    _lib.call("hi2x_rotate_rows", dev, _lib.ptr(w), 0 if w.dtype == torch.float32 else 2,
+              w.stride(0), n_all, _lib.ptr(idx), n, k, _lib.ptr(cs), _lib.ptr(fl),
+              _lib.ptr(out), k)
+    return out
 
 
 # ---- block parameters (spec 2.2) --------------------------------------------------------

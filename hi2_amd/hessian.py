@@ -367,7 +367,10 @@ class _Unit:
     comp: torch.Tensor | None = None  # fp32 [n, K] value each code was rounded from
 
 
-def _prepare(ji: int, job: GptqJob, s: int, step_rows: int, effort: str) -> _Unit:
+def _prepare(ji: int, job: GptqJob, s: int, step_rows: int, effort: str,
+             dest: torch.Tensor | None = None) -> _Unit:
+    """The chunk's working copy (into ``dest``, a view of its batch's padded buffer, when
+    given), its ladder fit and block parameters."""
     w, k = job.w, job.w.shape[1]
     if k % job.block:
         raise ValueError(f"K={k} is not a multiple of the block {job.block}")
@@ -376,7 +379,11 @@ def _prepare(ji: int, job: GptqJob, s: int, step_rows: int, effort: str) -> _Uni
     # always a fresh copy: the column loop writes its compensated columns into the
     # working copy, and a row slice of an fp32 job is otherwise a view of the caller's w
     # (at any chunk offset, not only the first)
-    wc = w[s : s + step_rows].to(torch.float32, copy=True).contiguous()
+    if dest is None:
+        wc = w[s : s + step_rows].to(torch.float32, copy=True).contiguous()
+    else:
+        wc = dest
+        wc.copy_(w[s : s + step_rows])
     cfg = EFFORT[effort]
     lo, step, _ = _fit(wc.reshape(-1, nb, job.block), job.d, 2**job.nbits, cfg["grid"],
                        cfg["ls"], False)
@@ -384,28 +391,40 @@ def _prepare(ji: int, job: GptqJob, s: int, step_rows: int, effort: str) -> _Uni
     cols = torch.arange(k, device=dev)
     if job.perm is not None:
         p = job.perm.to(dev)
-        wc = wc.index_select(1, p)
+        if dest is None:
+            wc = wc.index_select(1, p)
+        else:
+            wc.copy_(wc.index_select(1, p))
         cols = p
     return _Unit(ji, s, wc, lo_u8, step_u8, consts, lo_d, step_d, cols // job.block)
 
 
+def _padded(sizes: list[int]) -> list[int]:
+    """Rows of each unit in a batch's working buffer: every unit of a multi-unit batch
+    starts on a 128-row boundary, so that no workgroup or tile of the kernels holds rows
+    of two factors (it would run once per factor)."""
+    if len(sizes) > 1:
+        return [-(-n // BLOCK_COLUMNS) * BLOCK_COLUMNS for n in sizes]
+    return list(sizes)
+
+
 def _round_kernel(
-    units: list[_Unit], jobs: list[GptqJob], want_comp: bool = False, super_blocks=None
+    units: list[_Unit], jobs: list[GptqJob], want_comp: bool = False, super_blocks=None,
+    buf: torch.Tensor | None = None,
 ) -> None:
     """All ``units`` (same K, same device) through ``hi2x_gptq_run``: one intra-block
     launch per 128 columns for every row, the cross-block updates on MFMA with the
-    reference's rounding."""
+    reference's rounding.  ``buf``: the batch's working buffer when the units' working
+    copies already sit in it (prepared in place)."""
     dev, k = units[0].wc.device, units[0].wc.shape[1]
     sizes = [x.wc.shape[0] for x in units]
-    # Every unit starts on a 128-row boundary: no workgroup or tile of the kernels then
-    # holds rows of two factors (it would run once per factor).  Padding rows have
-    # w = lo = step = 0: they round to code 0 with zero error and change nothing.
-    if len(units) > 1:
-        padded = [-(-n // BLOCK_COLUMNS) * BLOCK_COLUMNS for n in sizes]
-    else:
-        padded = sizes
+    # Padding rows have w = lo = step = 0: they round to code 0 with zero error and
+    # change nothing.
+    padded = _padded(sizes)
     total = sum(padded)
-    if len(units) > 1:
+    if buf is not None:
+        wc = buf
+    elif len(units) > 1:
         wc = torch.zeros(total, k, dtype=torch.float32, device=dev)
     else:
         wc = units[0].wc
@@ -415,7 +434,7 @@ def _round_kernel(
     views, off = [], 0
     for x, n, pn in zip(units, sizes, padded):
         nb = x.lo_d.shape[1]
-        if len(units) > 1:
+        if len(units) > 1 and buf is None:
             wc[off : off + n] = x.wc
         lo[off : off + n, :nb] = x.lo_d
         st[off : off + n, :nb] = x.step_d
@@ -511,6 +530,8 @@ class PreparedJobs:
     jobs: list[GptqJob]
     units: list[_Unit]
     backend: str
+    # the rounding batches: (device, K) -> [(units, working buffer or None)]
+    batches: dict
 
     def record_stream(self, stream: torch.cuda.Stream) -> None:
         """Mark every tensor made here as used on ``stream`` (for a rounding issued
@@ -519,6 +540,10 @@ class PreparedJobs:
             for t in (x.wc, x.lo_u8, x.step_u8, x.consts, x.lo_d, x.step_d, x.blk_of):
                 if t is not None:
                     t.record_stream(stream)
+        for bl in self.batches.values():
+            for _, buf in bl:
+                if buf is not None:
+                    buf.record_stream(stream)
 
 
 @torch.no_grad()
@@ -530,13 +555,45 @@ def prepare_jobs_gptq(jobs: list[GptqJob], effort: str = "normal",
     backend = backend or os.environ.get("HI2_GPTQ_BACKEND", "auto")
     for job in jobs:
         _lib.require_gpu(job.w)
-    units: list[_Unit] = []
+    # the chunks, then their batches (same K and device, up to BATCH_ELEMS weights); a
+    # batch of several chunks gets one working buffer that every chunk is copied into
+    # (its padding rows zeroed), so that the rounding needs no gathering pass
+    specs = []  # (job, row offset, rows, step_rows)
     for ji, job in enumerate(jobs):
         n_rows, k = job.w.shape
         step_rows = max(1, ROW_ELEMS // k)
         for s in range(0, n_rows, step_rows):
-            units.append(_prepare(ji, job, s, step_rows, effort))
-    return PreparedJobs(jobs, units, backend)
+            specs.append((ji, s, min(step_rows, n_rows - s), step_rows))
+    plan: dict[tuple, list[list[int]]] = {}
+    for si, (ji, _s, n, _st) in enumerate(specs):
+        w = jobs[ji].w
+        key = (w.device, w.shape[1])
+        bl = plan.setdefault(key, [[]])
+        if bl[-1] and sum(specs[t][2] for t in bl[-1]) * w.shape[1] + n * w.shape[1] > BATCH_ELEMS:
+            bl.append([])
+        bl[-1].append(si)
+    units: list[_Unit | None] = [None] * len(specs)
+    batches: dict[tuple, list] = {}
+    for (dev, k), bl in plan.items():
+        for members in bl:
+            buf = None
+            if len(members) > 1:
+                sizes = [specs[t][2] for t in members]
+                padded = _padded(sizes)
+                buf = torch.empty(sum(padded), k, dtype=torch.float32, device=dev)
+            off = 0
+            for j, t in enumerate(members):
+                ji, s0, n, st = specs[t]
+                dest = None
+                if buf is not None:
+                    pn = padded[j]
+                    dest = buf[off : off + n]
+                    if pn > n:
+                        buf[off + n : off + pn].zero_()
+                    off += pn
+                units[t] = _prepare(ji, jobs[ji], s0, st, effort, dest)
+            batches.setdefault((dev, k), []).append(([units[t] for t in members], buf))
+    return PreparedJobs(jobs, units, backend, batches)
 
 
 @torch.no_grad()
@@ -565,13 +622,7 @@ def round_prepared(prep: PreparedJobs, comp: bool = False,
     jobs, units, backend = prep.jobs, prep.units, prep.backend
     if any(x.wc is None for x in units):
         raise ValueError("these prepared jobs have already been rounded")
-    batches: dict[tuple, list[list[_Unit]]] = {}
-    for x in units:
-        key = (x.wc.device, x.wc.shape[1])
-        bl = batches.setdefault(key, [[]])
-        if bl[-1] and sum(y.wc.numel() for y in bl[-1]) + x.wc.numel() > BATCH_ELEMS:
-            bl.append([])
-        bl[-1].append(x)
+    batches = prep.batches
     # batches of different K are independent: each runs on its own stream
     side = []
     for bi, ((dev, _k), bl) in enumerate(batches.items()):
@@ -582,18 +633,21 @@ def round_prepared(prep: PreparedJobs, comp: bool = False,
             st.wait_stream(main)
             side.append((main, st))
         with torch.cuda.stream(st):
-            for batch in bl:
+            for batch, buf in bl:
                 if st is not main:
                     for x in batch:
                         for t in (x.wc, x.lo_d, x.step_d, x.blk_of, jobs[x.job].u):
                             t.record_stream(st)
-                _round_kernel(batch, jobs, comp, super_blocks)
+                    if buf is not None:
+                        buf.record_stream(st)
+                _round_kernel(batch, jobs, comp, super_blocks, buf)
                 for x in batch:
                     if st is not main:
                         x.codes.record_stream(main)
                         if x.comp is not None:
                             x.comp.record_stream(main)
                     x.wc = None  # free the working copy early
+            bl[:] = [(batch, None) for batch, _ in bl]
     for main, st in side:
         main.wait_stream(st)
     per_job: list[list[Encoded]] = [[] for _ in jobs]

@@ -148,6 +148,18 @@ int hi2x_ladder_dequantize(const uint8_t* codes, const float* lo, const float* s
 int hi2x_fwht16(const void* x, void* y, int dtype, int64_t rows, int64_t k,
                 const uint8_t* flags, void* stream);
 
+/* fwht_groups(w.float() * col_scale, flags)[rows] in one pass: the reference's smoothing
+ * (hi2/calibrate.py:106-111), staging to fp32 and rotation (hi2/calibrate.py:329-330,
+ * fwht_groups hi2/format.py:30-41) and row selection per candidate
+ * (hi2/calibrate.py:353-357): w [nw, ldw] f32 (dtype 0) or bf16 (dtype 2), rows [n]
+ * i64 device indices (null: rows 0..n-1; an index outside [0, nw) yields a row of NaN),
+ * col_scale [k] f32 (null: none), flags [k/16] u8 (null: no group transformed); out
+ * [n, ldo] f32.  Rows 16-byte aligned.  Bit-identical to the cast, the product and
+ * hi2x_fwht16 in turn. */
+int hi2x_rotate_rows(const void* w, int dtype, int64_t ldw, int64_t nw, const int64_t* rows,
+                     int64_t n, int64_t k, const float* col_scale, const uint8_t* flags,
+                     float* out, int64_t ldo, void* stream);
+
 /* pack_codes (hi2/format.py:73-85): codes [rows, k] u8 -> words [rows, k*nbits/32]
  * i32, LSB first.  bad: device i32 counter incremented per code >= 2^nbits (the
  * caller raises ValueError when nonzero). */

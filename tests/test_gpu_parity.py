@@ -360,6 +360,38 @@ def test_fwht_equals_oracle_and_is_an_involution(dev):
         fwht_groups(T(x[:, :24], dev), T(fl[:1], dev))
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_rotate_rows_equals_cast_scale_fwht_select(dev, dtype):
+    """rotate_rows(w, flags, rows, s) == fwht_groups(w.float() * s, flags)[rows] bit for
+    bit (the product one fp32 rounding), against the oracle's fwht16; rows repeated and
+    out of order, a strided row view, no rows (every row), no flags (no transform)."""
+    from hi2_amd.format import rotate_rows
+
+    rng = np.random.default_rng(5)
+    n, k = 300, 768
+    x = (rng.standard_normal((n, k)) * np.exp(rng.standard_normal((n, 1)))).astype(np.float32)
+    w = T(x, dev).to(dtype)
+    wf = N(w.float())
+    fl = rng.integers(0, 2, k // 16).astype(np.uint8)
+    cs = (rng.random(k) + 0.5).astype(np.float32)
+    rows = rng.integers(0, n, 257).astype(np.int64)
+    rows[:5] = [3, 3, n - 1, 0, 7]
+    got = rotate_rows(w, T(fl, dev), T(rows, dev), T(cs, dev))
+    assert np.array_equal(N(got), oracle.fwht16((wf * cs)[rows], fl))
+    got = rotate_rows(w, T(fl, dev))
+    assert np.array_equal(N(got), oracle.fwht16(wf, fl))
+    got = rotate_rows(w, None, torch.from_numpy(rows))  # host rows: range-checked
+    assert np.array_equal(N(got), wf[rows])
+    wide = torch.zeros(n, k + 64, dtype=dtype, device=dev)
+    wide[:, :k] = w
+    got = rotate_rows(wide[:, :k], T(fl, dev), T(rows, dev))
+    assert np.array_equal(N(got), oracle.fwht16(wf[rows], fl))
+    with pytest.raises(IndexError):
+        rotate_rows(w, T(fl, dev), torch.tensor([0, n]))
+    bad = rotate_rows(w, T(fl, dev), T(np.array([1, n, -1], np.int64), dev))
+    assert np.isnan(N(bad[1:])).all() and np.array_equal(N(bad[:1]), oracle.fwht16(wf[1:2], fl))
+
+
 @pytest.mark.parametrize("nbits", [2, 4, 8])
 def test_pack_and_assemble_equal_oracle(dev, nbits):
     from hi2_amd.format import assemble, pack_codes
