@@ -35,7 +35,7 @@ import torch
 
 from . import _lib
 from .encode import encode_rows
-from .format import GROUP, HI2Tensor, assemble, fwht_groups
+from .format import GROUP, HI2Tensor, assemble, fwht_groups, rotate_rows
 from .hessian import (
     GptqJob,
     encode_jobs_gptq,
@@ -145,6 +145,20 @@ def _inv_scale(col_scale: torch.Tensor | None) -> torch.Tensor | None:
     if col_scale is None:
         return None
     return 1.0 / col_scale.detach().cpu().float()
+
+
+def _row_source(w: torch.Tensor, col_scale, had: torch.Tensor, dev):
+    """``rows -> fwht(W * s)[rows]`` in float32 on ``dev`` (``rows`` host int64).  The
+    stored dtype crosses PCIe once; float32 and bfloat16 weights are then cast, scaled,
+    rotated and gathered per candidate in one pass (``rotate_rows``), other dtypes
+    through ``_stage_rows`` and a row gather."""
+    if w.dtype in (torch.float32, torch.bfloat16):
+        wd = _to_device(w, dev)
+        cs = None if col_scale is None else _to_device(col_scale, dev).float()
+        fl = _to_device(had.to(torch.uint8), dev) if bool(had.any()) else None
+        return lambda rows: rotate_rows(wd, fl, _to_device(rows, dev), cs)
+    wt = _stage_rows(w, col_scale, had, dev)
+    return lambda rows: wt.index_select(0, _to_device(rows, dev))
 
 
 def _stage_rows(w: torch.Tensor, col_scale, had: torch.Tensor, dev) -> torch.Tensor:
@@ -274,13 +288,13 @@ def _on_device(reqs, cfg, ex, i: int, use_gptq, comp_full, pack=None):
         out = pieces.setdefault(ri, [])
         enqueued.append(ri)
         with torch.cuda.stream(st):
-            wt = _stage_rows(r.w[lo:hi], t.col_scale, had, dev)
-            ctx = emit(ri, r, wt, had)
+            src = _row_source(r.w[lo:hi], t.col_scale, had, dev)
+            ctx = emit(ri, r, had)
             for ci, (nb, b) in enumerate(t.candidates):
                 rows = _rows_of(picks, lo, hi, ci)
                 if rows.numel() == 0:
                     continue
-                sub = wt.index_select(0, _to_device(rows, dev))
+                sub = src(rows)
                 out.append(None)  # filled once encoded: keeps the candidate order
                 ctx(sub, rows + lo, nb, b, len(out) - 1)
 
@@ -301,7 +315,7 @@ def _on_device(reqs, cfg, ex, i: int, use_gptq, comp_full, pack=None):
             ch.reqs = groups[fk]
             chains.append(ch)
 
-            def emit(ri, r, wt, had, ch=ch):
+            def emit(ri, r, had, ch=ch):
                 def add(sub, rows, nb, b, slot):
                     ch.jobs.append(len(jobs))
                     jobs.append(GptqJob(sub, ch.d, ch.u, nb, b, ch.perm))
@@ -313,7 +327,7 @@ def _on_device(reqs, cfg, ex, i: int, use_gptq, comp_full, pack=None):
             _round_chain(ch, reqs, jobs, job_at, encs, cfg)
         # nearest rows (hi2/encode.py:133-173: ladder fit, params, codes, sse) on the
         # caller's stream
-        def emit_near(ri, r, wt, had):
+        def emit_near(ri, r, had):
             k = r.table.shape[1]
             d = _weights(r.stats, k, had, dev, _inv_scale(r.table.col_scale))
 
@@ -429,7 +443,7 @@ def encode_with_picks_reference(w, stats, table, picks, cfg, ex=None, sigma=None
     for dev, lo, hi in ex.shards(r):
         dev = _device(dev)
         with torch.cuda.device(dev):
-            wt = _stage_rows(w[lo:hi], table.col_scale, had, dev)
+            src = _row_source(w[lo:hi], table.col_scale, had, dev)
             if use_gptq:
                 hs = transform_sigma(_to_device(sigma, dev), table.col_scale, had)
                 d = hs.diagonal().clone()
@@ -444,7 +458,7 @@ def encode_with_picks_reference(w, stats, table, picks, cfg, ex=None, sigma=None
                 rows = _rows_of(picks.detach().cpu(), lo, hi, ci)
                 if rows.numel() == 0:
                     continue
-                sub = wt.index_select(0, rows.to(dev))
+                sub = src(rows)
                 if use_gptq:
                     e = encode_rows_gptq_reference(sub, d, u, nb, b, cfg.effort, perm)
                 else:
