@@ -852,8 +852,8 @@ __global__ __launch_bounds__(256) void node_kernel(float* __restrict__ P, int64_
   leaf_prod<NB, true, false>(S, NB, 0, 0, 0, NB, 0, 1.0f);   // T1 = A21 A11^T
   leaf_prod<NB, false, false>(S, NB, 0, 0, 0, 0, 0, 1.0f);   // T2 = T1 A11 (over S_A)
   {  // S_B = A22 - T1 T1^T: lower triangle, zeros above, identity beyond m2
-    ProdAcc<NB> Q;
-    leaf_mma<NB, true>(S, NB, 0, NB, 0, Q);
+    // (A22 is requested from memory first, so that its loads are in flight during the
+    // product)
     const __amdgpu_buffer_rsrc_t rs = mg_rsrc(a22, (int64_t)(m2 - 1) * K + m2);
     float g[ProdAcc<NB>::PER][4];
 #pragma unroll
@@ -864,6 +864,8 @@ __global__ __launch_bounds__(256) void node_kernel(float* __restrict__ P, int64_
         const uint32_t off = (r < m2 && c <= r) ? (uint32_t)(((int64_t)r * K + c) * 4) : MG_OOB;
         g[p][j] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, (int)off, 0, 0));
       }
+    ProdAcc<NB> Q;
+    leaf_mma<NB, true>(S, NB, 0, NB, 0, Q);
     __syncthreads();  // T1 has been read
 #pragma unroll
     for (int p = 0; p < ProdAcc<NB>::PER; ++p)
