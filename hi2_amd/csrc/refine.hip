@@ -111,8 +111,34 @@ __global__ __launch_bounds__(256, 2) void refine_gradient_kernel(
 // ---------------------------------------------------------------------------------
 struct RefRegs {
   float g[CPL], cc[CPL], loc[CPL], stc[CPL], hd[CPL], dw[CPL];
+  // per column, from its code before the block's sweep (a column's code changes only at
+  // its own step): the changes of the two moves, their gain terms 2 dw and dw^2 Hs[j][j],
+  // and whether each move stays on the ladder
+  float dwp[CPL], dwm[CPL], ap[CPL], bp[CPL], am[CPL], bm[CPL];
+  bool okp[CPL], okm[CPL];
   int nmv;
 };
+
+// The parts of a column's two candidate moves that do not depend on its gradient, with
+// the step's operations in its order (each product and sum rounded separately).
+__device__ __forceinline__ void refine_prepare(RefRegs& R, float tp) {
+#pragma unroll
+  for (int m = 0; m < CPL; ++m) {
+    const float cj = R.cc[m], lo_j = R.loc[m], st_j = R.stc[m], hd = R.hd[m];
+    const float now = f16_round(lo_j + cj * st_j);
+    const float cp = cj + 1.0f, cm = cj + -1.0f;
+    const float dwp = f16_round(lo_j + cp * st_j) - now;
+    const float dwm = f16_round(lo_j + cm * st_j) - now;
+    R.okp[m] = (cp >= 0.0f) & (cp <= tp) & (st_j > 0.0f);
+    R.okm[m] = (cm >= 0.0f) & (cm <= tp) & (st_j > 0.0f);
+    R.dwp[m] = dwp;
+    R.dwm[m] = dwm;
+    R.ap[m] = 2.0f * dwp;
+    R.bp[m] = (dwp * dwp) * hd;
+    R.am[m] = 2.0f * dwm;
+    R.bm[m] = (dwm * dwm) * hd;
+  }
+}
 
 template <int I, bool FULL>
 __device__ __forceinline__ void refine_step(RefRegs& R, int L, int q, float tp,
@@ -123,20 +149,15 @@ __device__ __forceinline__ void refine_step(RefRegs& R, int L, int q, float tp,
     hb[cur ^ 1][0] = *reinterpret_cast<const f32x4*>(shq + (I + 1) * USTR);
     hb[cur ^ 1][1] = *reinterpret_cast<const f32x4*>(shq + (I + 1) * USTR + 4);
   }
-  const float gj = R.g[m], cj = R.cc[m], lo_j = R.loc[m], st_j = R.stc[m], hd = R.hd[m];
-  const float now = f16_round(lo_j + cj * st_j);
-  const float cp = cj + 1.0f, cm = cj + -1.0f;
-  const float dwp = f16_round(lo_j + cp * st_j) - now;
-  const float dwm = f16_round(lo_j + cm * st_j) - now;
-  const bool okp = (cp >= 0.0f) & (cp <= tp) & (st_j > 0.0f);
-  const bool okm = (cm >= 0.0f) & (cm <= tp) & (st_j > 0.0f);
-  const float gp = okp ? -((2.0f * dwp) * gj + (dwp * dwp) * hd) : -__builtin_inff();
-  const float gm = okm ? -((2.0f * dwm) * gj + (dwm * dwm) * hd) : -__builtin_inff();
+  // gain of a move: -(2 dw g_j + dw^2 Hs[j][j]) (the gradient-free terms prepared)
+  const float gj = R.g[m], cj = R.cc[m];
+  const float gp = R.okp[m] ? -(R.ap[m] * gj + R.bp[m]) : -__builtin_inff();
+  const float gm = R.okm[m] ? -(R.am[m] * gj + R.bm[m]) : -__builtin_inff();
   const bool pick_m = (gp == gp) & ((gm != gm) | (gm > gp));
   const float best = pick_m ? gm : gp;
   const bool take = best > 0.0f;  // false for NaN
-  const float dw = take ? (pick_m ? dwm : dwp) : 0.0f;
-  const float cn = take ? (pick_m ? cm : cp) : cj;
+  const float dw = take ? (pick_m ? R.dwm[m] : R.dwp[m]) : 0.0f;
+  const float cn = take ? (pick_m ? cj + -1.0f : cj + 1.0f) : cj;
   const float db = row_bcast<s>(dw);
   const bool own = q == s;
   R.cc[m] = own ? cn : R.cc[m];
@@ -230,6 +251,7 @@ __global__ __launch_bounds__(RPG * QL) void refine_block_kernel(
 #pragma unroll
   for (int m = 0; m < CPL; ++m) R.hd[m] = sh[(QL * m + q) * USTR + lane_off(q) + m];
 
+  refine_prepare(R, tp);
   const float* shq = sh + lane_off(q);
   f32x4 hb[2][2];
   hb[0][0] = *reinterpret_cast<const f32x4*>(shq);
