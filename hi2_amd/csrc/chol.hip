@@ -588,6 +588,10 @@ __global__ __launch_bounds__(256) void reverse_damp_kernel(const float* __restri
 // in the sweep.  The reciprocal and square root are the hardware approximations (the
 // factor is compared to a tolerance, not bit for bit).
 constexpr int LP = NB + 4;  // LDS pitch of the leaf block (floats)
+#ifndef HI2X_LEAF_SPLIT
+#define HI2X_LEAF_SPLIT 1
+#endif
+constexpr bool LEAF_SPLIT = HI2X_LEAF_SPLIT;
 
 typedef float f32x4v __attribute__((ext_vector_type(4)));
 
@@ -659,12 +663,106 @@ struct ProdAcc {  // this wave's tiles of an H x H product (tile t = wave + 4p, 
   f32x4v acc[PER];
 };
 
+// Three bf16 planes of 8 consecutive k of one lane's fragment, as the split-plane GEMM
+// writes them: x1 = bf16(x), x2 = bf16(x - x1), x3 = bf16(x - x1 - x2) (the differences
+// are exact in fp32).  Pairs go through v_cvt_pk_bf16_f32; a bf16 back to fp32 is its
+// bits in the upper half of the word.
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x2v __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ void split8(const float4 x0, const float4 x1, bf16x8 (&o)[3]) {
+  const float x[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+  uint32_t w[3][4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    float lo = x[2 * e], hi = x[2 * e + 1];
+#pragma unroll
+    for (int pl = 0; pl < 3; ++pl) {
+      const uint32_t u =
+          __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2v){lo, hi}, bf16x2));
+      w[pl][e] = u;
+      if (pl < 2) {
+        lo = lo - __builtin_bit_cast(float, u << 16);
+        hi = hi - __builtin_bit_cast(float, u & 0xffff0000u);
+      }
+    }
+  }
+#pragma unroll
+  for (int pl = 0; pl < 3; ++pl)
+    o[pl] = __builtin_bit_cast(bf16x8, (uint4){w[pl][0], w[pl][1], w[pl][2], w[pl][3]});
+}
+
+// acc = A op(B) for the node's 128 x 128 blocks on bf16 MFMA through the three-way split
+// (the six terms x_i y_j with i + j <= 4 of the split-plane GEMM, small terms first):
+// v_mfma_f32_16x16x32_bf16 (lane l: row or column l % 16, k 8 (l / 16) .. + 7; the
+// accumulator layout of the fp32 16x16x4 MFMA), six 16-cycle MFMAs per 32 k where the
+// fp32 MFMA takes eight of 32 cycles.  The wave's tiles t = wave + 4p are tile row p / 2,
+// column wave + 4 (p % 2): per 32 k its two column fragments are split first, then the
+// eight row fragments two at a time, each pair's 24 MFMAs (four accumulators in turn)
+// covering the split of the next pair.  fp32-level rounding, not bit-identical to the
+// fp32 MFMA.  (Blocks of 64 and below stay on fp32 MFMA: with a row fragment used by
+// one tile, the split costs more VALU time than the MFMA time it saves.)
+template <bool TB>
+__device__ __forceinline__ void node_mma3(const float* S, int ar, int ac, int br, int bc,
+                                          ProdAcc<128>& P) {
+  constexpr int PER = ProdAcc<128>::PER;
+  const int wave = threadIdx.x >> 6, l = threadIdx.x & 63;
+  const int lr = l & 15, lg = l >> 4;
+#pragma unroll
+  for (int p = 0; p < PER; ++p) P.acc[p] = (f32x4v){0.0f, 0.0f, 0.0f, 0.0f};
+  constexpr int PA[6] = {2, 1, 0, 1, 0, 0}, PB[6] = {0, 1, 2, 0, 1, 0};
+#pragma unroll 1
+  for (int kb = 0; kb < 128; kb += 32) {
+    const int k = kb + 8 * lg;
+    bf16x8 b[2][3];
+#pragma unroll
+    for (int ci = 0; ci < 2; ++ci) {
+      const int tc = wave + 4 * ci;
+      float4 x0, x1;
+      if (TB) {
+        const float* bp = &S[(br + tc * 16 + lr) * LP + bc + k];
+        x0 = *reinterpret_cast<const float4*>(bp);
+        x1 = *reinterpret_cast<const float4*>(bp + 4);
+      } else {
+        const float* bp = &S[(br + k) * LP + bc + tc * 16 + lr];
+        x0 = make_float4(bp[0], bp[LP], bp[2 * LP], bp[3 * LP]);
+        x1 = make_float4(bp[4 * LP], bp[5 * LP], bp[6 * LP], bp[7 * LP]);
+      }
+      split8(x0, x1, b[ci]);
+    }
+#pragma unroll
+    for (int rp = 0; rp < 4; ++rp) {
+      bf16x8 a[2][3];
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+        const float* ap = &S[(ar + (2 * rp + q) * 16 + lr) * LP + ac + k];
+        split8(*reinterpret_cast<const float4*>(ap), *reinterpret_cast<const float4*>(ap + 4),
+               a[q]);
+      }
+#pragma unroll
+      for (int pr = 0; pr < 6; ++pr)
+#pragma unroll
+        for (int q = 0; q < 2; ++q)
+#pragma unroll
+          for (int ci = 0; ci < 2; ++ci) {
+            const int p = 2 * (2 * rp + q) + ci;
+            P.acc[p] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[q][PA[pr]], b[ci][PB[pr]],
+                                                                P.acc[p], 0, 0, 0);
+          }
+    }
+  }
+}
+
 // acc = A (at (ar, ac)) * op(B) (at (br, bc)), H x H blocks of the leaf's LDS, op(B) = B^T
-// when TB.  For each 16 k: lane group g = l/16 supplies k = 16 kb + 4 g + s at MFMA step
+// when TB (the 128 blocks take the split product above).  For each 16 k: lane group g = l/16 supplies k = 16 kb + 4 g + s at MFMA step
 // s, so a lane reads its 4 k of A (and of B^T) as one 16-byte vector.
 template <int H, bool TB>
 __device__ __forceinline__ void leaf_mma(const float* S, int ar, int ac, int br, int bc,
                                          ProdAcc<H>& P) {
+  if constexpr (H == 128 && LEAF_SPLIT) {
+    node_mma3<TB>(S, ar, ac, br, bc, P);
+    return;
+  }
   constexpr int NT = ProdAcc<H>::NT, TILES = ProdAcc<H>::TILES, PER = ProdAcc<H>::PER;
   const int wave = threadIdx.x >> 6, l = threadIdx.x & 63;
   const int lr = l & 15, lg = l >> 4;
