@@ -393,6 +393,180 @@ __global__ __launch_bounds__(256, 2) void gemm3_kernel(G3Args g0, int64_t tm, in
   __syncthreads();  // no wave leaves while loads it issued may still write LDS
 }
 
+// The same product on 256 x 256 tiles for the largest grids: one workgroup of 8 waves per
+// CU, each wave 128 x 64 (4 x 2 accumulators), on the planes' three-stage ring of 48 KB
+// stages.  Per 16 k a wave reads 18 fragment planes for 48 MFMAs (gemm3_kernel: 12 for 24)
+// and the CU brings 48 KB into LDS per 16 k of a 256 x 256 tile (gemm3_kernel: 2 x 24 KB
+// per 16 k of two 128 x 128 tiles), half the LDS and L2 traffic per MFMA.  The next
+// stage's planes are read as the current stage's die (the six terms run small first:
+// A's plane 2 is dead after the first term, B's plane 2 after the third, ...), so two
+// waves per SIMD fit.  Each output element accumulates the same terms in the same order
+// as in gemm3_kernel (a 256-tile may run some stages more than a 128-tile of it, whose
+// masked planes add exact zeros).
+constexpr int GX_T = 256;                // tile edge
+constexpr int GX_SUP = 4;                // super-tile edge of the balanced schedule (tiles)
+constexpr int GX_PL = GX_T * G3_KC;      // bf16 per plane per stage
+
+template <int AMODE, int BMODE, bool CLOW>
+__global__ __launch_bounds__(512, 1) void gemm3x_kernel(G3Args g0, int64_t tm, int64_t tn,
+                                                        MgSched sched) {
+  G3Args g = g0;
+  g.A += (int64_t)blockIdx.z * g.sA;
+  g.B += (int64_t)blockIdx.z * g.sB;
+  g.C += (int64_t)blockIdx.z * g.sC;
+  __shared__ __attribute__((aligned(1024))) uint16_t SA[G3_NB][3][GX_PL];
+  __shared__ __attribute__((aligned(1024))) uint16_t SB[G3_NB][3][GX_PL];
+  int64_t tr, tc;
+  if (sched.per_xcd > 0) {
+    if (!mg_sched_tile<CLOW, GX_SUP>(blockIdx.x, sched, tm, tn, tr, tc)) return;
+  } else {
+    const int64_t t = xcd_tile(blockIdx.x, tm * tn);
+    if (t < 0) return;
+    tr = t / tn;
+    tc = t % tn;
+  }
+  const int64_t r0 = tr * GX_T, c0 = tc * GX_T;
+  if (CLOW && c0 > r0 + GX_T - 1) return;
+  int64_t kbeg, kend;
+  tri_krange<AMODE, BMODE>(r0, c0, GX_T, g.Kd, kbeg, kend);
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wr = wave >> 2, wc = wave & 3;
+  const int wv = __builtin_amdgcn_readfirstlane(wave);
+  f32x16 acc[4][2];
+#pragma unroll
+  for (int a = 0; a < 4; ++a)
+#pragma unroll
+    for (int b = 0; b < 2; ++b)
+#pragma unroll
+      for (int j = 0; j < 16; ++j) acc[a][b][j] = 0.0f;
+  const int rowsA = (int)((g.M - r0 < GX_T) ? g.M - r0 : GX_T);
+  const int rowsB = (int)((g.N - c0 < GX_T) ? g.N - c0 : GX_T);
+  const int64_t plA = g.M * g.Kp, plB = g.N * g.Kp;
+  // load j (0..5) of a stage: operand j / 3, plane j % 3, rows 32 wv .. 32 wv + 31 (the
+  // slot swizzle of gemm3_kernel)
+  const int prow = lane >> 1, piece = (lane & 1) ^ ((lane >> 4) & 1);
+  auto dma_one = [&](int j, int64_t k0, int buf, bool live) {
+    const int opd = j / 3, pl = j % 3;
+    const int row = 32 * wv + prow;
+    const uint16_t* base = opd == 0 ? g.A + pl * plA + ((k0 >> 4) * g.M + r0) * G3_KC
+                                    : g.B + pl * plB + ((k0 >> 4) * g.N + c0) * G3_KC;
+    const int rows = opd == 0 ? rowsA : rowsB;
+    const __amdgpu_buffer_rsrc_t rs = rsrc_u16(base, (int64_t)rows * G3_KC);
+    const uint32_t o = (uint32_t)(row * G3_KC * 2 + 16 * piece);
+    uint16_t* dst = opd == 0 ? &SA[buf][pl][wv * 32 * G3_KC] : &SB[buf][pl][wv * 32 * G3_KC];
+    g3_dma16(rs, (live && row < rows) ? o : MG_OOB, dst);
+  };
+  // fragment reads: A rows wr * 128 + 32 ta + lane % 32, B rows (output columns) wc * 64 +
+  // 32 tb + lane % 32, piece lane / 32 in slot h ^ ((row / 8) % 2)
+  const int so = 8 * ((lane >> 5) ^ ((lane >> 3) & 1));
+  const int rA = wr * 128 + (lane & 31), rB = wc * 64 + (lane & 31);
+  typedef mg_bf16x8 V;
+  auto rdA = [&](V (&av)[3][4], int pl, int buf) {
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+      av[pl][t] = __builtin_bit_cast(V, *reinterpret_cast<const mg_u16x8*>(&SA[buf][pl][(rA + 32 * t) * G3_KC + so]));
+  };
+  auto rdB = [&](V (&bv)[3][2], int pl, int buf) {
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+      bv[pl][t] = __builtin_bit_cast(V, *reinterpret_cast<const mg_u16x8*>(&SB[buf][pl][(rB + 32 * t) * G3_KC + so]));
+  };
+  constexpr int PA[6] = {2, 1, 0, 1, 0, 0}, PB[6] = {0, 1, 2, 0, 1, 0};
+  auto term = [&](auto P, const V (&av)[3][4], const V (&bv)[3][2]) {
+    constexpr int pr = decltype(P)::value;
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      acc[i >> 1][i & 1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+          av[PA[pr]][i >> 1], bv[PB[pr]][i & 1], acc[i >> 1][i & 1], 0, 0, 0);
+  };
+  auto sync = [&]() {
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_barrier();
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  };
+  const int nst = kend > kbeg ? (int)((kend - kbeg + G3_KC - 1) / G3_KC) : 0;
+  const int nst2 = (nst + 1) & ~1;
+  V a0[3][4], b0[3][2], a1[3][4], b1[3][2];  // [plane][tile], stage sets 0 and 1
+  if (nst > 0) {
+#pragma unroll
+    for (int p = 0; p < G3_NB; ++p) {
+#pragma unroll
+      for (int j = 0; j < G3_PER_STAGE; ++j) dma_one(j, kbeg + (int64_t)p * G3_KC, p, p < nst);
+    }
+    __builtin_amdgcn_s_waitcnt(g3_waitcnt(2 * G3_PER_STAGE, 15));  // stage 0 landed
+    sync();
+#pragma unroll
+    for (int pl = 0; pl < 3; ++pl) {
+      rdA(a0, pl, 0);
+      rdB(b0, pl, 0);
+    }
+  }
+  // Stage st (planes x): wait until stage st + 1 has landed and every wave's reads of
+  // stage st (made during stage st - 1) are done, then the six terms, each followed by
+  // one DMA of stage st + 3 into buffer st % 3 and the reads of the next stage's planes
+  // that the terms so far have freed (B0 first, then A2, B2 and A0, A1, B1).
+  auto stage = [&](const V (&xa)[3][4], const V (&xb)[3][2], V (&ya)[3][4], V (&yb)[3][2],
+                   int st) {
+    const int cb = st % G3_NB, nb = (st + 1) % G3_NB;
+    __builtin_amdgcn_s_waitcnt(g3_waitcnt(G3_PER_STAGE, 0));
+    sync();
+    rdB(yb, 0, nb);
+    __builtin_amdgcn_sched_barrier(0);
+    const int64_t kn = kbeg + (int64_t)(st + G3_NB) * G3_KC;
+    const bool live = st + G3_NB < nst;
+    term(std::integral_constant<int, 0>{}, xa, xb);
+    dma_one(0, kn, cb, live);
+    rdA(ya, 2, nb);
+    __builtin_amdgcn_sched_barrier(0);
+    term(std::integral_constant<int, 1>{}, xa, xb);
+    dma_one(1, kn, cb, live);
+    __builtin_amdgcn_sched_barrier(0);
+    term(std::integral_constant<int, 2>{}, xa, xb);
+    dma_one(2, kn, cb, live);
+    rdB(yb, 2, nb);
+    rdA(ya, 0, nb);
+    __builtin_amdgcn_sched_barrier(0);
+    term(std::integral_constant<int, 3>{}, xa, xb);
+    dma_one(3, kn, cb, live);
+    rdA(ya, 1, nb);
+    __builtin_amdgcn_sched_barrier(0);
+    term(std::integral_constant<int, 4>{}, xa, xb);
+    dma_one(4, kn, cb, live);
+    rdB(yb, 1, nb);
+    __builtin_amdgcn_sched_barrier(0);
+    term(std::integral_constant<int, 5>{}, xa, xb);
+    dma_one(5, kn, cb, live);
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  for (int st = 0; st < nst2; st += 2) {
+    stage(a0, b0, a1, b1, st);
+    stage(a1, b1, a0, b0, st + 1);
+  }
+  // C = alpha acc (+ C): register j of tile (ta, tb) at row wr * 128 + 32 ta + 8 (j / 4) +
+  // 4 (lane / 32) + j % 4, column wc * 64 + 32 tb + lane % 32; rows and columns outside
+  // C, and with CLOW the elements above the diagonal, are left alone
+  const __amdgpu_buffer_rsrc_t rc = mg_rsrc(g.C + r0 * g.ldc + c0, (int64_t)(rowsA - 1) * g.ldc + rowsB);
+  const int lr0 = wr * 128 + 4 * (lane >> 5), lc0 = wc * 64 + (lane & 31);
+#pragma unroll
+  for (int tb = 0; tb < 2; ++tb) {
+    const int cc = lc0 + 32 * tb;
+#pragma unroll
+    for (int ta = 0; ta < 4; ++ta)
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        const int rr = lr0 + 32 * ta + 8 * (j >> 2) + (j & 3);
+        const bool ok = rr < rowsA && cc < rowsB && (!CLOW || c0 + cc <= r0 + rr);
+        const uint32_t o = ok ? (uint32_t)(((int64_t)rr * g.ldc + cc) * 4) : MG_OOB;
+        const float x = acc[ta][tb][j];
+        float v = g.alpha * x;
+        if (g.beta != 0.0f)
+          v = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rc, (int)o, 0, 0)) + v;
+        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), rc, (int)o, 0, 0);
+      }
+  }
+  __syncthreads();  // no wave leaves while loads it issued may still write LDS
+}
+
 int split3(const float* X, int64_t ldx, int64_t R, int64_t Kk, int trans, int mask,
            uint16_t* out, int64_t Kp, hipStream_t s, int batch = 1, int64_t sx = 0,
            int64_t sout = 0) {
@@ -403,8 +577,17 @@ int split3(const float* X, int64_t ldx, int64_t R, int64_t Kk, int trans, int ma
 }
 
 template <int AMODE, int BMODE, bool CLOW>
+int gemm3x(const G3Args& a, hipStream_t s, int batch);
+static bool chol_tile256();
+
+template <int AMODE, int BMODE, bool CLOW>
 int gemm3(const G3Args& a, hipStream_t s, int batch = 1) {
   if (a.M <= 0 || a.N <= 0) return HI2X_OK;
+  {
+    const int64_t tm2 = (a.M + GX_T - 1) / GX_T, tn2 = (a.N + GX_T - 1) / GX_T;
+    const int64_t live2 = CLOW ? tm2 * (tm2 + 1) / 2 : tm2 * tn2;
+    if (live2 >= 256 && chol_tile256()) return gemm3x<AMODE, BMODE, CLOW>(a, s, batch);
+  }
   const int64_t tm = (a.M + MG_T - 1) / MG_T, tn = (a.N + MG_T - 1) / MG_T;
   LaunchTimer timer(HI2X_TIME_CHOL_GEMM, (double)a.M * a.N * a.Kd * batch, s);
   MgSched sched = mg_balance(tm, tn, [&](int64_t sr, int64_t sc) {
@@ -423,6 +606,35 @@ int gemm3(const G3Args& a, hipStream_t s, int batch = 1) {
   hipLaunchKernelGGL((gemm3_kernel<AMODE, BMODE, CLOW>), dim3((unsigned)grid, 1, (unsigned)batch),
                      dim3(256), 0, s, a, tm, tn, sched);
   return launch_status("gemm3_kernel");
+}
+
+// 256-tiles where they fill the chip (at least one 256-CU round of live tiles);
+// HI2X_CHOL_TILE256=0 keeps the 128-tiles (read at every product, for comparisons)
+static bool chol_tile256() {
+  const char* e = getenv("HI2X_CHOL_TILE256");
+  return !(e && *e && strcmp(e, "0") == 0);
+}
+
+template <int AMODE, int BMODE, bool CLOW>
+int gemm3x(const G3Args& a, hipStream_t s, int batch) {
+  const int64_t tm = (a.M + GX_T - 1) / GX_T, tn = (a.N + GX_T - 1) / GX_T;
+  LaunchTimer timer(HI2X_TIME_CHOL_GEMM, (double)a.M * a.N * a.Kd * batch, s);
+  MgSched sched = mg_balance(tm, tn, [&](int64_t sr, int64_t sc) {
+    double w = 0.0;
+    for (int64_t i = 0; i < GX_SUP; ++i)
+      for (int64_t j = 0; j < GX_SUP; ++j) {
+        const int64_t tr = sr * GX_SUP + i, tc = sc * GX_SUP + j;
+        if (tr >= tm || tc >= tn || (CLOW && tc > tr)) continue;
+        int64_t kb, ke;
+        tri_krange<AMODE, BMODE>(tr * GX_T, tc * GX_T, GX_T, a.Kd, kb, ke);
+        w += (double)std::max<int64_t>(0, ke - kb) + 2.0 * G3_KC;
+      }
+    return w;
+  }, GX_SUP);
+  const int64_t grid = sched.per_xcd > 0 ? mg_sched_grid(sched) : (tm * tn + 7) / 8 * 8;
+  hipLaunchKernelGGL((gemm3x_kernel<AMODE, BMODE, CLOW>), dim3((unsigned)grid, 1, (unsigned)batch),
+                     dim3(512), 0, s, a, tm, tn, sched);
+  return launch_status("gemm3x_kernel");
 }
 
 // Products of the big grids: bf16 MFMA on split planes (default), or the fp32 MFMA GEMM

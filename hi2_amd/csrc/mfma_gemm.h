@@ -404,14 +404,16 @@ constexpr int MG_SCHED_MAX = 448;  // super-tiles a table holds (else round-robi
 struct MgSched {
   int32_t per_xcd = 0;                 // super-tiles of the busiest XCD (0: no table)
   int32_t nsc = 0;                     // super-tile columns
+  int32_t sup = MG_SUP;                // super-tile edge (tiles)
   uint16_t st[MG_SCHED_MAX] = {};      // [x * per_xcd + j]: sr * nsc + sc, 0xffff: none
 };
 
-// weight(sr, sc) -> work of super-tile (sr, sc) (0: empty)
+// weight(sr, sc) -> work of super-tile (sr, sc) (0: empty); super-tiles of sup x sup tiles
 template <class Weight>
-__host__ inline MgSched mg_balance(int64_t tm, int64_t tn, Weight weight) {
+__host__ inline MgSched mg_balance(int64_t tm, int64_t tn, Weight weight, int sup = MG_SUP) {
   MgSched s;
-  const int64_t nsr = (tm + MG_SUP - 1) / MG_SUP, nsc = (tn + MG_SUP - 1) / MG_SUP;
+  s.sup = sup;
+  const int64_t nsr = (tm + sup - 1) / sup, nsc = (tn + sup - 1) / sup;
   std::vector<std::pair<double, int>> items;
   for (int64_t sr = 0; sr < nsr; ++sr)
     for (int64_t sc = 0; sc < nsc; ++sc) {
@@ -444,20 +446,21 @@ __host__ inline MgSched mg_balance(int64_t tm, int64_t tn, Weight weight) {
 }
 
 __host__ inline int64_t mg_sched_grid(const MgSched& s) {
-  return (int64_t)8 * s.per_xcd * MG_SUP * MG_SUP;
+  return (int64_t)8 * s.per_xcd * s.sup * s.sup;
 }
 
-template <bool TRI>
+// SUP: the table's super-tile edge (MgSched::sup)
+template <bool TRI, int SUP = MG_SUP>
 __device__ __forceinline__ bool mg_sched_tile(int64_t bid, const MgSched& s, int64_t tm,
                                               int64_t tn, int64_t& tr, int64_t& tc) {
   const int x = (int)(bid & 7);
   const int64_t slot = bid >> 3;
-  const int j = (int)(slot / (MG_SUP * MG_SUP)), w = (int)(slot % (MG_SUP * MG_SUP));
+  const int j = (int)(slot / (SUP * SUP)), w = (int)(slot % (SUP * SUP));
   if (j >= s.per_xcd) return false;
   const int u = s.st[x * s.per_xcd + j];
   if (u == 0xffff) return false;
-  tr = (int64_t)(u / s.nsc) * MG_SUP + w / MG_SUP;
-  tc = (int64_t)(u % s.nsc) * MG_SUP + w % MG_SUP;
+  tr = (int64_t)(u / s.nsc) * SUP + w / SUP;
+  tc = (int64_t)(u % s.nsc) * SUP + w % SUP;
   if (tr >= tm || tc >= tn) return false;
   if (TRI && tc > tr) return false;
   return true;
