@@ -630,6 +630,25 @@ def test_inverse_factor_inverts_large(dev):
     assert err < 5e-3, err
 
 
+def test_inverse_factor_256_tiles_equal_128_tiles(dev, monkeypatch):
+    """K = 8448: the top level's three rectangular products (17 x 17 tiles of 256, the
+    last row and column of tiles partial) run on the 256-tile kernel; with
+    HI2X_CHOL_TILE256=0 every product runs on the 128-tiles.  Same terms in the same order
+    per element: the factors are equal bit for bit."""
+    from hi2_amd.hessian import inverse_factor
+
+    k = 8448
+    g = torch.Generator(device=dev).manual_seed(12)
+    x = torch.randn(2 * k, k, device=dev, generator=g)
+    x = x * torch.exp(0.5 * torch.randn(1, k, device=dev, generator=g))
+    hs = (x.T @ x / x.shape[0]).contiguous()
+    del x
+    u256 = inverse_factor(hs, 0.01)
+    monkeypatch.setenv("HI2X_CHOL_TILE256", "0")
+    u128 = inverse_factor(hs, 0.01)
+    assert torch.equal(u256, u128)
+
+
 def test_inverse_factor_retries_and_survives_singular(dev):
     from hi2_amd.hessian import inverse_factor
 
