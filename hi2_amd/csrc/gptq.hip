@@ -68,6 +68,33 @@ struct RowRegs {
   int inexact;  // error quotients of this lane that fell outside div_rcp_ok's range
 };
 
+// The live part of this lane's U row at p: columns mm >= M (earlier ones are dead at the
+// step that uses the row), each element loaded once.  A dead element brought in with its
+// 16-byte vector would be reused by the compiler at once, and the load waited for there.
+template <int LO>  // first live element of the 4 at p (4: none)
+__device__ __forceinline__ void load4_live(float* u, const float* p) {
+  if constexpr (LO == 0) {
+    const f32x4 x = *reinterpret_cast<const f32x4*>(p);
+    u[0] = x[0];
+    u[1] = x[1];
+    u[2] = x[2];
+    u[3] = x[3];
+  } else if constexpr (LO == 1 || LO == 2) {
+    if constexpr (LO == 1) u[1] = p[1];
+    const float2 y = *reinterpret_cast<const float2*>(p + 2);
+    u[2] = y.x;
+    u[3] = y.y;
+  } else if constexpr (LO == 3) {
+    u[3] = p[3];
+  }
+}
+template <int M>
+__device__ __forceinline__ void load_urow(float (&u)[CPL], const float* p) {
+  static_assert(CPL == 8, "two 4-vectors per lane");
+  load4_live<(M > 4 ? 4 : M)>(u, p);
+  load4_live<(M < 4 ? 0 : (M > 8 ? 4 : M - 4))>(u + 4, p + 4);
+}
+
 // Step I of the column loop, I a compile-time constant so that every register index
 // below is static (no dynamic VGPR indexing).  ub[I & 1] holds this lane's U row I;
 // the step fills ub[(I + 1) & 1] with row I + 1.  With FULL the block has LMAX columns
@@ -76,20 +103,17 @@ struct RowRegs {
 // IEEE division instead, for the rare block that has to be run again.
 template <int I, bool FULL, bool COMP, bool EXACT>
 __device__ __forceinline__ void gptq_step(RowRegs<COMP>& R, int L, int q, float nm,
-                                          const float* __restrict__ suq, f32x4 (&ub)[2][2]) {
+                                          const float* __restrict__ suq, float (&ub)[2][CPL]) {
   constexpr int m = I / QL, s = I % QL, cur = I & 1;
   if (!FULL && I >= L) return;
-  if (I + 1 < LMAX) {
-    ub[cur ^ 1][0] = *reinterpret_cast<const f32x4*>(suq + (I + 1) * USTR);
-    ub[cur ^ 1][1] = *reinterpret_cast<const f32x4*>(suq + (I + 1) * USTR + 4);
-  }
+  if constexpr (I + 1 < LMAX) load_urow<(I + 1) / QL>(ub[cur ^ 1], suq + (I + 1) * USTR);
   const float col = R.w[m];
   const float lo_j = R.loc[m], st_j = R.stc[m];
   const float safe = (st_j == 0.0f) ? 1.0f : st_j;
   float qv = clamp_code(__builtin_rintf(div_rcp_code(col - lo_j, safe, R.ys[m])), nm);
   if (st_j == 0.0f) qv = 0.0f;
   const float wq = f16_round(lo_j + qv * st_j);
-  const float ujj = ub[cur][m >> 2][m & 3];  // U[I][I] in the owner lane
+  const float ujj = ub[cur][m];  // U[I][I] in the owner lane
   const bool own = q == s;
   const float num = col - wq;
   float e;
@@ -113,19 +137,70 @@ __device__ __forceinline__ void gptq_step(RowRegs<COMP>& R, int L, int q, float 
     asm volatile("" : "+v"(R.cm[m]));
   }
 #pragma unroll
-  for (int mm = (I + 1) / QL; mm < CPL; ++mm) R.w[mm] = R.w[mm] - eb * ub[cur][mm >> 2][mm & 3];
+  for (int mm = (I + 1) / QL; mm < CPL; ++mm) R.w[mm] = R.w[mm] - eb * ub[cur][mm];
 }
 
 template <bool FULL, bool COMP, bool EXACT, int... Is>
 __device__ __forceinline__ void gptq_steps(std::integer_sequence<int, Is...>, RowRegs<COMP>& R,
                                            int L, int q, float nm, const float* __restrict__ suq,
-                                           f32x4 (&ub)[2][2]) {
+                                           float (&ub)[2][CPL]) {
   (gptq_step<Is, FULL, COMP, EXACT>(R, L, q, nm, suq, ub), ...);
 }
 
-// The state of this lane's 8 columns of row lr of the workgroup: the working copy,
-// each column's decoded ladder (blk: the group's column -> block map at column i1), the
+// The state of this lane's 8 columns of row lr of the workgroup, in three parts so that
+// the kernel can overlap their loads with the U block's: (a) the working copy and each
+// column's ladder block index (blk: the group's column -> block map at column i1),
+// (b) the decoded (lo, step) of those blocks (a second, dependent round trip), (c) the
 // reciprocals of the steps and of the factor diagonal (su: the U block in LDS).
+template <bool COMP>
+__device__ __forceinline__ void load_row_a(RowRegs<COMP>& R, int (&bix)[CPL],
+                                           const float* __restrict__ wc, int64_t K,
+                                           int64_t i1, int L, int64_t rbase, int nrows, int lr,
+                                           const int32_t* __restrict__ blk, int q) {
+  // this row's columns c = 16m + q: the working copy and each column's ladder block
+  const __amdgpu_buffer_rsrc_t wrs = mg_rsrc(wc + rbase * K + i1, (int64_t)(nrows - 1) * K + L);
+  const __amdgpu_buffer_rsrc_t brs = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<int32_t*>(blk + i1), (short)0, L * 4, 0x00020000);
+#pragma unroll
+  for (int m = 0; m < CPL; ++m) {
+    const int c = QL * m + q;
+    const uint32_t wo = c < L ? (uint32_t)(((int64_t)lr * K + c) * 4) : MG_OOB;
+    R.w[m] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(wrs, (int)wo, 0, 0));
+    bix[m] = (int)__builtin_amdgcn_raw_buffer_load_b32(brs, (int)(c < L ? c * 4 : MG_OOB), 0, 0);
+  }
+}
+template <bool COMP>
+__device__ __forceinline__ void load_row_b(RowRegs<COMP>& R, const int (&bix)[CPL],
+                                           int64_t rbase, int nrows, int lr,
+                                           const float* __restrict__ lo,
+                                           const float* __restrict__ st, int64_t ldp) {
+  // decoded (lo, step) of those blocks (block 0 for the dead columns c >= L)
+  const __amdgpu_buffer_rsrc_t lrs = mg_rsrc(lo + rbase * ldp, (int64_t)nrows * ldp);
+  const __amdgpu_buffer_rsrc_t srs = mg_rsrc(st + rbase * ldp, (int64_t)nrows * ldp);
+#pragma unroll
+  for (int m = 0; m < CPL; ++m) {
+    const uint32_t po = (uint32_t)(((int64_t)lr * ldp + bix[m]) * 4);
+    R.loc[m] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(lrs, (int)po, 0, 0));
+    R.stc[m] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(srs, (int)po, 0, 0));
+    R.er[m] = 0.0f;
+    R.qc[m] = 0.0f;
+    if constexpr (COMP) R.cm[m] = 0.0f;
+  }
+}
+template <bool COMP>
+__device__ __forceinline__ void load_row_c(RowRegs<COMP>& R, int L, const float* su, int q) {
+  // IEEE reciprocals (correctly rounded) of each column's step and factor diagonal;
+  // dead columns (c >= L) get 1
+#pragma unroll
+  for (int m = 0; m < CPL; ++m) {
+    const int c = QL * m + q;
+    const float sc = R.stc[m] == 0.0f ? 1.0f : R.stc[m];
+    const float ud = c < L ? su[c * USTR + lane_off(q) + m] : 1.0f;
+    R.ys[m] = 1.0f / sc;
+    R.yu[m] = 1.0f / ud;
+  }
+  R.inexact = 0;
+}
 template <bool COMP>
 __device__ __forceinline__ void load_row(RowRegs<COMP>& R, const float* __restrict__ wc,
                                          int64_t K, int64_t i1, int L, int64_t rbase,
@@ -133,42 +208,10 @@ __device__ __forceinline__ void load_row(RowRegs<COMP>& R, const float* __restri
                                          const float* __restrict__ lo,
                                          const float* __restrict__ st, int64_t ldp,
                                          const float* su, int q) {
-      // this row's columns c = 16m + q: the working copy and each column's ladder block
-      const __amdgpu_buffer_rsrc_t wrs =
-          mg_rsrc(wc + rbase * K + i1, (int64_t)(nrows - 1) * K + L);
-      const __amdgpu_buffer_rsrc_t brs = __builtin_amdgcn_make_buffer_rsrc(
-          const_cast<int32_t*>(blk + i1), (short)0, L * 4, 0x00020000);
-      int bix[CPL];
-#pragma unroll
-      for (int m = 0; m < CPL; ++m) {
-        const int c = QL * m + q;
-        const uint32_t wo = c < L ? (uint32_t)(((int64_t)lr * K + c) * 4) : MG_OOB;
-        R.w[m] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(wrs, (int)wo, 0, 0));
-        bix[m] = (int)__builtin_amdgcn_raw_buffer_load_b32(brs, (int)(c < L ? c * 4 : MG_OOB), 0, 0);
-      }
-      // decoded (lo, step) of those blocks (block 0 for the dead columns c >= L)
-      const __amdgpu_buffer_rsrc_t lrs = mg_rsrc(lo + rbase * ldp, (int64_t)nrows * ldp);
-      const __amdgpu_buffer_rsrc_t srs = mg_rsrc(st + rbase * ldp, (int64_t)nrows * ldp);
-#pragma unroll
-      for (int m = 0; m < CPL; ++m) {
-        const uint32_t po = (uint32_t)(((int64_t)lr * ldp + bix[m]) * 4);
-        R.loc[m] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(lrs, (int)po, 0, 0));
-        R.stc[m] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(srs, (int)po, 0, 0));
-        R.er[m] = 0.0f;
-        R.qc[m] = 0.0f;
-        if constexpr (COMP) R.cm[m] = 0.0f;
-      }
-      // IEEE reciprocals (correctly rounded) of each column's step and factor diagonal;
-      // dead columns (c >= L) get 1
-#pragma unroll
-      for (int m = 0; m < CPL; ++m) {
-        const int c = QL * m + q;
-        const float sc = R.stc[m] == 0.0f ? 1.0f : R.stc[m];
-        const float ud = c < L ? su[c * USTR + lane_off(q) + m] : 1.0f;
-        R.ys[m] = 1.0f / sc;
-        R.yu[m] = 1.0f / ud;
-      }
-      R.inexact = 0;
+  int bix[CPL];
+  load_row_a<COMP>(R, bix, wc, K, i1, L, rbase, nrows, lr, blk, q);
+  load_row_b<COMP>(R, bix, rbase, nrows, lr, lo, st, ldp);
+  load_row_c<COMP>(R, L, su, q);
 }
 
 template <bool COMP>
@@ -264,6 +307,11 @@ __global__ __launch_bounds__(RPG * QL) void gptq_block_kernel(
   // they need no branches (a branch around a load makes the compiler wait for each load
   // in turn): all loads of a phase are issued before the first is used.
   for (int g = g0; g <= g1; ++g) {
+    // the row's working copy and ladder indices first, so that the dependent load of its
+    // ladders runs while the U block is in flight
+    RowRegs<COMP> R;
+    int bix[CPL];
+    load_row_a<COMP>(R, bix, wc, K, i1, L, rbase, nrows, lr, blk + (int64_t)g * K, q);
     __syncthreads();  // LDS of the previous group is no longer read
     {
       // U[i1:i1+L, i1:i1+L]: rows >= L read zero, columns >= L are zeroed here
@@ -277,6 +325,7 @@ __global__ __launch_bounds__(RPG * QL) void gptq_block_kernel(
         const uint32_t off = i < L ? (uint32_t)(((int64_t)i * K + c) * 4) : MG_OOB;
         uv[t] = mg_load4(ur, off);
       }
+      load_row_b<COMP>(R, bix, rbase, nrows, lr, lo, st, ldp);
 #pragma unroll
       for (int t = 0; t < NV; ++t) {
         const int idx = tid + RPG * QL * t, i = idx / (LMAX / 4), c = 4 * (idx % (LMAX / 4));
@@ -292,12 +341,10 @@ __global__ __launch_bounds__(RPG * QL) void gptq_block_kernel(
     if (gr != g) continue;  // uniform over the row's 16 lanes
 
     const float nm = nmax[g];
-    RowRegs<COMP> R;
-    load_row<COMP>(R, wc, K, i1, L, rbase, nrows, lr, blk + (int64_t)g * K, lo, st, ldp, su, q);
+    load_row_c<COMP>(R, L, su, q);
     const float* suq = su + lane_off(q);
-    f32x4 ub[2][2];
-    ub[0][0] = *reinterpret_cast<const f32x4*>(suq);
-    ub[0][1] = *reinterpret_cast<const f32x4*>(suq + 4);
+    float ub[2][CPL];
+    load_urow<0>(ub[0], suq);
     gptq_steps<FULL, COMP, false>(std::make_integer_sequence<int, LMAX>{}, R, L, q, nm, suq, ub);
     if (__ballot(R.inexact != 0) != 0) {
       // some row of this wave met an error quotient outside the iteration's exact range
