@@ -780,6 +780,36 @@ __global__ __launch_bounds__(256) void reverse_damp_kernel(const float* __restri
   }
 }
 
+// The same with 16-byte vectors (K a multiple of 4, 16-byte aligned matrices): vector v of
+// row i (columns 4v .. 4v + 3, 4v <= i) is row K-1-i's vector at K-4-4v reversed.  In the
+// vector that holds the diagonal, the columns past i get the reversed values too: that
+// part of P is above the diagonal, which nothing reads before reverse_out4_kernel writes
+// it.
+__global__ __launch_bounds__(256) void reverse_damp4_kernel(const float* __restrict__ hs,
+                                                            int64_t K,
+                                                            const float* __restrict__ lam,
+                                                            float* __restrict__ P, int64_t shs,
+                                                            int64_t slam, int64_t sP) {
+  hs += (int64_t)blockIdx.z * shs;
+  lam += (int64_t)blockIdx.z * slam;
+  P += (int64_t)blockIdx.z * sP;
+  const int64_t i = (int64_t)blockIdx.y;
+  const float l = *lam;
+  const float* src = hs + (K - 1 - i) * K + (K - 4);
+  float* dst = P + i * K;
+  for (int64_t v = threadIdx.x + (int64_t)blockIdx.x * blockDim.x; 4 * v <= i;
+       v += (int64_t)gridDim.x * blockDim.x) {
+    const float4 x = *reinterpret_cast<const float4*>(src - 4 * v);
+    float4 y = make_float4(x.w, x.z, x.y, x.x);
+    const int64_t e = i - 4 * v;  // the diagonal's place in the vector (if < 4)
+    y.x = e == 0 ? y.x + l : y.x;
+    y.y = e == 1 ? y.y + l : y.y;
+    y.z = e == 2 ? y.z + l : y.z;
+    y.w = e == 3 ? y.w + l : y.w;
+    *reinterpret_cast<float4*>(dst + 4 * v) = y;
+  }
+}
+
 // ---- leaf: L^-1 of chol(P[r0:r0+n, r0:r0+n]) in place (lower triangle) ---------------------
 // One workgroup of 4 waves holds the 128 x 128 block in LDS (identity beyond n, zeros
 // above the diagonal) and runs the same recursion as the host on it, down to 16 x 16:
@@ -1070,7 +1100,7 @@ __device__ __forceinline__ bool leaf_rec(float* S, int o) {
 // Rows [0, n) x columns [0, n) of the n x n diagonal block at P (row stride K) into the
 // LDS block at row offset so of S: lower triangle, zeros above, identity beyond n.  The
 // buffer ends at the block's last element: rows past n read zero; n and K are multiples
-// of 16, so every 16-byte vector is all in or all out.
+// of 4 (the entry points require it of K), so every 16-byte vector is all in or all out.
 __device__ __forceinline__ void leaf_load(float* S, int so, const float* P, int64_t K, int n) {
   const __amdgpu_buffer_rsrc_t rs = mg_rsrc(P, (int64_t)(n - 1) * K + n);
   constexpr int V = NB / 4;  // float4 per row
@@ -1225,6 +1255,40 @@ __global__ __launch_bounds__(256) void reverse_out_kernel(float* __restrict__ P,
     } else {
       P[i * K + j] = P[ri * K + rj];
       P[ri * K + rj] = 0.0f;
+    }
+  }
+}
+
+// The same with 16-byte vectors (K a multiple of 4, 16-byte aligned P): vector v of row i
+// (columns 4v .. 4v + 3, 4v + 3 > i) receives row K-1-i's vector at K-4-4v reversed, which
+// is then zeroed; in the vector that holds the diagonal only the columns past i move (one
+// element at a time: the others are row i's lower part, the source of row K-1-i's), and
+// the diagonal is swapped.  Every element moves or is zeroed by exactly one thread.
+__global__ __launch_bounds__(256) void reverse_out4_kernel(float* __restrict__ P, int64_t K,
+                                                           int64_t sP) {
+  P += (int64_t)blockIdx.z * sP;
+  const int64_t i = (int64_t)blockIdx.y, ri = K - 1 - i;
+  float* row = P + i * K;
+  float* mir = P + ri * K + (K - 4);
+  for (int64_t v = i / 4 + threadIdx.x + (int64_t)blockIdx.x * blockDim.x; 4 * v < K;
+       v += (int64_t)gridDim.x * blockDim.x) {
+    if (4 * v > i) {  // every column of the vector is past the diagonal
+      const float4 x = *reinterpret_cast<const float4*>(mir - 4 * v);
+      *reinterpret_cast<float4*>(row + 4 * v) = make_float4(x.w, x.z, x.y, x.x);
+      *reinterpret_cast<float4*>(mir - 4 * v) = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int64_t j = 4 * v + e, rj = K - 1 - j;
+        if (j > i) {
+          row[j] = P[ri * K + rj];
+          P[ri * K + rj] = 0.0f;
+        } else if (j == i && i < ri) {
+          const float a = row[i], b = P[ri * K + ri];
+          row[i] = b;
+          P[ri * K + ri] = a;
+        }
+      }
     }
   }
 }
@@ -1395,7 +1459,16 @@ static int chol_launch(const float* hs, int64_t k, float damp, int attempt, floa
                        p10, lam, shs, sw);
     rc = launch_status("diag_mean_kernel");
   }
-  if (!rc) {
+  // 16-byte vectors where every row and matrix start is 16-byte aligned
+  const bool vec4 = k % 4 == 0 && shs % 4 == 0 && su % 4 == 0 &&
+                    (reinterpret_cast<uintptr_t>(hs) & 15) == 0 &&
+                    (reinterpret_cast<uintptr_t>(u) & 15) == 0;
+  if (!rc && vec4) {
+    const dim3 g((unsigned)((k + 1023) / 1024 < 16 ? (k + 1023) / 1024 : 16), (unsigned)k,
+                 (unsigned)batch);
+    hipLaunchKernelGGL(reverse_damp4_kernel, g, dim3(256), 0, s, hs, k, lam, u, shs, sw, su);
+    rc = launch_status("reverse_damp4_kernel");
+  } else if (!rc) {
     const dim3 g((unsigned)((k + 255) / 256 < 16 ? (k + 255) / 256 : 16), (unsigned)k,
                  (unsigned)batch);
     hipLaunchKernelGGL(reverse_damp_kernel, g, dim3(256), 0, s, hs, k, lam, u, shs, sw, su);
@@ -1403,7 +1476,12 @@ static int chol_launch(const float* hs, int64_t k, float damp, int attempt, floa
   }
   Ctx c{u, k, ws, &plan, status_out, s, batch, su, sw};
   if (!rc) rc = inv_chol(c, 0, k, 0);
-  if (!rc) {  // U = J L^-1 J (garbage if the factorisation failed; the status says so)
+  if (!rc && vec4) {  // U = J L^-1 J (garbage if the factorisation failed; the status says so)
+    const dim3 g((unsigned)((k + 1023) / 1024 < 16 ? (k + 1023) / 1024 : 16), (unsigned)k,
+                 (unsigned)batch);
+    hipLaunchKernelGGL(reverse_out4_kernel, g, dim3(256), 0, s, u, k, su);
+    rc = launch_status("reverse_out4_kernel");
+  } else if (!rc) {
     const dim3 g((unsigned)((k + 255) / 256 < 16 ? (k + 255) / 256 : 16), (unsigned)k,
                  (unsigned)batch);
     hipLaunchKernelGGL(reverse_out_kernel, g, dim3(256), 0, s, u, k, su);
@@ -1434,6 +1512,7 @@ extern "C" int hi2x_chol_inv_upper_async(const float* hs, int64_t k, float damp,
                                          void* stream) {
   clear_error();
   HI2X_REQUIRE(k > 0 && hs && u && hs != u && status, "chol_inv_upper_async: bad arguments");
+  HI2X_REQUIRE(k % 4 == 0, "chol_inv_upper_async: k=%lld is not a multiple of 4", (long long)k);
   HI2X_REQUIRE(attempt >= 0 && attempt < 10, "chol_inv_upper_async: attempt %d", attempt);
   hipStream_t s = as_stream(stream);
   const Plan plan = make_plan(k);
@@ -1448,6 +1527,7 @@ extern "C" int hi2x_chol_inv_upper(const float* hs, int64_t k, float damp, int a
                                    float* u, void* ws, int64_t ws_bytes, void* stream) {
   clear_error();
   HI2X_REQUIRE(k > 0 && hs && u && hs != u, "chol_inv_upper: bad arguments");
+  HI2X_REQUIRE(k % 4 == 0, "chol_inv_upper: k=%lld is not a multiple of 4", (long long)k);
   HI2X_REQUIRE(attempt >= 0 && attempt < 10, "chol_inv_upper: attempt %d", attempt);
   hipStream_t s = as_stream(stream);
   const Plan plan = make_plan(k);
@@ -1490,6 +1570,8 @@ extern "C" int hi2x_chol_inv_upper_batched_async(const float* hs, int64_t hs_str
   clear_error();
   HI2X_REQUIRE(k > 0 && hs && u && status && batch > 0 && batch <= 65535,
                "chol_inv_upper_batched_async: bad arguments");
+  HI2X_REQUIRE(k % 4 == 0, "chol_inv_upper_batched: k=%lld is not a multiple of 4",
+               (long long)k);
   HI2X_REQUIRE(hs_stride >= k * k && u_stride >= k * k,
                "chol_inv_upper_batched_async: strides %lld / %lld below k * k",
                (long long)hs_stride, (long long)u_stride);

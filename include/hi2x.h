@@ -296,8 +296,11 @@ int64_t hi2x_chol_workspace_bytes(int64_t k);
  * (clamped at 1e-12) * 10^attempt, writes u [k, k] f32 = the upper Cholesky factor of
  * (hs + lam I)^-1 (lower triangle zero).  Computed as U = (J chol(J (hs + lam I) J) J)^-1
  * (J = reversal), the same matrix as the reference's chol -> cholesky_inverse ->
- * chol(upper) chain.  Synchronises `stream`; returns HI2X_ENOTPD when the damped matrix
- * is not numerically positive definite (the caller retries with attempt + 1). */
+ * chol(upper) chain.  k is a multiple of 4 (the leaves move 16-byte vectors; the
+ * reference's widths are multiples of 16, its golden factors multiples of 8).
+ * Synchronises `stream`; returns
+ * HI2X_ENOTPD when the damped matrix is not numerically positive definite (the caller
+ * retries with attempt + 1). */
 int hi2x_chol_inv_upper(const float* hs, int64_t k, float damp, int attempt, float* u,
                         void* ws, int64_t ws_bytes, void* stream);
 

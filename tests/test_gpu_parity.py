@@ -649,6 +649,15 @@ def test_inverse_factor_256_tiles_equal_128_tiles(dev, monkeypatch):
     assert torch.equal(u256, u128)
 
 
+def test_inverse_factor_rejects_width_not_multiple_of_4(dev):
+    """The factor's leaves move 16-byte vectors: a width that is not a multiple of 4 (no
+    Hessian of the reference has one) is refused before any launch."""
+    from hi2_amd.hessian import inverse_factor
+
+    with pytest.raises(Exception, match="multiple of 4"):
+        inverse_factor(torch.eye(30, device=dev), 0.01)
+
+
 def test_inverse_factor_retries_and_survives_singular(dev):
     from hi2_amd.hessian import inverse_factor
 
