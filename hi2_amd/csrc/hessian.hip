@@ -190,6 +190,42 @@ __global__ __launch_bounds__(256) void transpose_bf16_kernel(const uint16_t* __r
   }
 }
 
+// The same with 16-byte accesses (K a multiple of 8, x 16-byte aligned): a 64 x 64 tile
+// read as 8-element row vectors and written as 8-token column vectors gathered from LDS
+// (row pitch 66: the 8 rows a gather step reads from lie on distinct banks).
+__global__ __launch_bounds__(256) void transpose8_bf16_kernel(const uint16_t* __restrict__ x,
+                                                              int64_t T, int64_t K, int64_t Tp,
+                                                              uint16_t* __restrict__ xt) {
+  __shared__ uint32_t tile[64][33];  // 64 tokens x 66 features (bf16 pairs)
+  const int64_t t0 = (int64_t)blockIdx.y * 64, k0 = (int64_t)blockIdx.x * 64;
+  const int tid = threadIdx.x, c = tid & 7;
+#pragma unroll
+  for (int p = 0; p < 2; ++p) {
+    const int r = (tid >> 3) + 32 * p;
+    const int64_t t = t0 + r, k = k0 + 8 * c;
+    uint4 v = make_uint4(0u, 0u, 0u, 0u);
+    if (t < T && k < K) v = *reinterpret_cast<const uint4*>(x + t * K + k);
+    tile[r][4 * c] = v.x;
+    tile[r][4 * c + 1] = v.y;
+    tile[r][4 * c + 2] = v.z;
+    tile[r][4 * c + 3] = v.w;
+  }
+  __syncthreads();
+  const uint16_t* t16 = reinterpret_cast<const uint16_t*>(&tile[0][0]);
+#pragma unroll
+  for (int p = 0; p < 2; ++p) {
+    const int kk = (tid >> 3) + 32 * p;
+    const int64_t k = k0 + kk;
+    if (k >= K) continue;
+    uint32_t w[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      w[e] = (uint32_t)t16[(8 * c + 2 * e) * 66 + kk] |
+             ((uint32_t)t16[(8 * c + 2 * e + 1) * 66 + kk] << 16);
+    *reinterpret_cast<uint4*>(xt + k * Tp + t0 + 8 * c) = make_uint4(w[0], w[1], w[2], w[3]);
+  }
+}
+
 // ---- routed (grouped) accumulation: one launch for every group of a token batch --------
 // Group e is the tokens j in [offs[e], offs[e+1]) of a routed batch (the rows an MoE
 // router sent to expert e, hi2/moe.py:83-100); token j is row rows[j] of x (rows NULL:
@@ -882,8 +918,13 @@ int launch_syrk(const void* x, int dtype, int64_t t, int64_t k, float* s, char* 
   const SyrkPlan p = syrk_plan(dtype, t, k);
   uint16_t* xt = reinterpret_cast<uint16_t*>(ws);
   float* parts = p.splits > 1 ? reinterpret_cast<float*>(ws + p.xt_bytes) : nullptr;
-  hipLaunchKernelGGL(transpose_bf16_kernel, dim3((unsigned)((k + 63) / 64), (unsigned)(p.tp / 64)),
-                     dim3(256), 0, st, (const uint16_t*)x, t, k, p.tp, xt);
+  const dim3 tg((unsigned)((k + 63) / 64), (unsigned)(p.tp / 64));
+  if (k % 8 == 0 && (reinterpret_cast<uintptr_t>(x) & 15) == 0)
+    hipLaunchKernelGGL(transpose8_bf16_kernel, tg, dim3(256), 0, st, (const uint16_t*)x, t, k,
+                       p.tp, xt);
+  else
+    hipLaunchKernelGGL(transpose_bf16_kernel, tg, dim3(256), 0, st, (const uint16_t*)x, t, k, p.tp,
+                       xt);
   int rc = launch_status("transpose_bf16_kernel");
   if (!rc) {
     // one workgroup per CU: super-tile rounds once the tiles fill several rounds
