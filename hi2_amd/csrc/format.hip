@@ -44,71 +44,105 @@ __global__ __launch_bounds__(256) void fwht16_kernel(const T* __restrict__ x, T*
 // The weight preparation of a GPTQ unit in one pass: out[i] = fwht16 of row rows[i] of
 // (float(w) * col_scale) (rows null: row i; col_scale null: no product).  float(bf16)
 // is exact and the product is one rounding, as the reference's elementwise ops; the
-// transform is fwht16_kernel's.  One thread per 16-column group, consecutive threads
-// on consecutive groups of a row: a bf16 row is read in 32-byte pieces and written as
-// f32 in 64-byte pieces, each once.
+// transform is fwht16_kernel's.  A workgroup takes 256 consecutive 16-column groups
+// (in row-major order over the selected rows), one per thread for the arithmetic; the
+// groups' inputs come in and their outputs go out through LDS in 16-byte pieces with
+// consecutive lanes on consecutive pieces, so every global access is coalesced.  The
+// LDS slots are 3 (bf16 inputs) or 5 (f32 inputs, outputs) pieces apart: the 16 lanes
+// of a 16-byte LDS access fall on distinct banks.
 template <typename T>
 __global__ __launch_bounds__(256) void rotate_rows_kernel(
     const T* __restrict__ w, int64_t ldw, int64_t nw, const int64_t* __restrict__ rows,
     int64_t n, int64_t k, const float* __restrict__ col_scale,
     const uint8_t* __restrict__ flags, float* __restrict__ out, int64_t ldo) {
-  const int64_t ng = k / 16;
-  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (t >= n * ng) return;
-  const int64_t i = t / ng, g = t % ng;
-  const int64_t src = rows ? rows[i] : i;
-  float* yo = out + i * ldo + 16 * g;
-  if (src < 0 || src >= nw) {  // an index out of range: the row reads NaN
+  constexpr int CH = 16 * (int)sizeof(T) / 16;  // input pieces per group (2 or 4)
+  constexpr int IS = CH + 1;                    // input slot (pieces)
+  constexpr int OS = 5;                         // output slot: 4 pieces + 1
+  __shared__ uint4 pin[256 * IS];
+  __shared__ uint4 pout[256 * OS];
+  // group indices fit 32 bits (the host checks n * k / 16 < 2^31): cheap divisions
+  const uint32_t ng = (uint32_t)(k / 16), total = (uint32_t)(n * (k / 16));
+  const uint32_t base = blockIdx.x * 256u;
+  const int tid = threadIdx.x;
+  // the inputs: piece c = group c / CH, part c % CH
 #pragma unroll
-    for (int q = 0; q < 4; ++q)
-      *reinterpret_cast<float4*>(yo + 4 * q) =
-          make_float4(__builtin_nanf(""), __builtin_nanf(""), __builtin_nanf(""),
-                      __builtin_nanf(""));
-    return;
-  }
-  const T* xi = w + src * ldw + 16 * g;
-  float v[16];
-  if constexpr (sizeof(T) == 2) {
-    const uint4 a = *reinterpret_cast<const uint4*>(xi);
-    const uint4 b = *reinterpret_cast<const uint4*>(xi + 8);
-    const uint32_t u[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      v[2 * e] = __uint_as_float(u[e] << 16);
-      v[2 * e + 1] = __uint_as_float(u[e] & 0xffff0000u);
-    }
-  } else {
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const float4 a = *reinterpret_cast<const float4*>(xi + 4 * q);
-      v[4 * q] = a.x;
-      v[4 * q + 1] = a.y;
-      v[4 * q + 2] = a.z;
-      v[4 * q + 3] = a.w;
+  for (int j = 0; j < CH; ++j) {
+    const int c = tid + 256 * j, gl = c / CH, part = c % CH;
+    const uint32_t t = base + gl;
+    if (t < total) {
+      const uint32_t i = t / ng, g = t % ng;
+      const int64_t src = rows ? rows[i] : (int64_t)i;
+      if (src >= 0 && src < nw)
+        pin[gl * IS + part] =
+            *reinterpret_cast<const uint4*>(w + src * ldw + 16 * g + part * (16 / (int)sizeof(T)));
     }
   }
-  if (col_scale) {
+  __syncthreads();
+  {
+    const uint32_t t = base + tid;
+    if (t < total) {
+      const uint32_t i = t / ng, g = t % ng;
+      const int64_t src = rows ? rows[i] : (int64_t)i;
+      float y[16];
+      if (src < 0 || src >= nw) {  // an index out of range: the row reads NaN
 #pragma unroll
-    for (int q = 0; q < 16; ++q) v[q] = v[q] * col_scale[16 * g + q];
-  }
-  float y[16];
-  if (flags && flags[g]) {
-    const float qv = 0.25f;
+        for (int j = 0; j < 16; ++j) y[j] = __builtin_nanf("");
+      } else {
+        float v[16];
+        if constexpr (sizeof(T) == 2) {
+          const uint4 a = pin[tid * IS], b = pin[tid * IS + 1];
+          const uint32_t u[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
 #pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      float acc = 0.0f;
+          for (int e = 0; e < 8; ++e) {
+            v[2 * e] = __uint_as_float(u[e] << 16);
+            v[2 * e + 1] = __uint_as_float(u[e] & 0xffff0000u);
+          }
+        } else {
 #pragma unroll
-      for (int e = 0; e < 16; ++e) acc = __builtin_fmaf(v[e], hneg(e, j) ? -qv : qv, acc);
-      y[j] = acc;
+          for (int q = 0; q < 4; ++q) {
+            const uint4 a = pin[tid * IS + q];
+            v[4 * q] = __uint_as_float(a.x);
+            v[4 * q + 1] = __uint_as_float(a.y);
+            v[4 * q + 2] = __uint_as_float(a.z);
+            v[4 * q + 3] = __uint_as_float(a.w);
+          }
+        }
+        if (col_scale) {
+#pragma unroll
+          for (int q = 0; q < 16; ++q) v[q] = v[q] * col_scale[16 * g + q];
+        }
+        if (flags && flags[g]) {
+          const float qv = 0.25f;
+#pragma unroll
+          for (int j = 0; j < 16; ++j) {
+            float acc = 0.0f;
+#pragma unroll
+            for (int e = 0; e < 16; ++e) acc = __builtin_fmaf(v[e], hneg(e, j) ? -qv : qv, acc);
+            y[j] = acc;
+          }
+        } else {
+#pragma unroll
+          for (int j = 0; j < 16; ++j) y[j] = v[j];
+        }
+      }
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        pout[tid * OS + q] = make_uint4(__float_as_uint(y[4 * q]), __float_as_uint(y[4 * q + 1]),
+                                        __float_as_uint(y[4 * q + 2]),
+                                        __float_as_uint(y[4 * q + 3]));
     }
-  } else {
-#pragma unroll
-    for (int j = 0; j < 16; ++j) y[j] = v[j];
   }
+  __syncthreads();
+  // the outputs: piece c = group c / 4, part c % 4
 #pragma unroll
-  for (int q = 0; q < 4; ++q)
-    *reinterpret_cast<float4*>(yo + 4 * q) = make_float4(y[4 * q], y[4 * q + 1], y[4 * q + 2],
-                                                         y[4 * q + 3]);
+  for (int j = 0; j < 4; ++j) {
+    const int c = tid + 256 * j, gl = c / 4, part = c % 4;
+    const uint32_t t = base + gl;
+    if (t < total) {
+      const uint32_t i = t / ng, g = t % ng;
+      *reinterpret_cast<uint4*>(out + (int64_t)i * ldo + 16 * g + 4 * part) = pout[gl * OS + part];
+    }
+  }
 }
 
 __device__ __forceinline__ void note_bad(int32_t* bad, int n) {
@@ -200,6 +234,8 @@ extern "C" int hi2x_rotate_rows(const void* w, int dtype, int64_t ldw, int64_t n
   HI2X_REQUIRE(((uintptr_t)w % 16) == 0 && ((uintptr_t)out % 16) == 0 &&
                    (ldw * (dtype == 0 ? 4 : 2)) % 16 == 0 && (ldo * 4) % 16 == 0,
                "rotate_rows: rows must start on 16-byte boundaries");
+  HI2X_REQUIRE(n * (k / 16) < (int64_t)1 << 31, "rotate_rows: %lld groups (at most 2^31 - 1)",
+               (long long)(n * (k / 16)));
   const int64_t total = n * (k / 16);
   const dim3 grid((unsigned)((total + 255) / 256));
   hipStream_t s = as_stream(stream);
