@@ -76,22 +76,23 @@ __host__ __device__ inline void tri_krange(int64_t r0, int64_t c0, int64_t T, in
   if (BMODE == 2) kend = (c0 + T < kend) ? c0 + T : kend;
 }
 
+// One output tile of the product (workgroup bid of the launch's tile mapping).
 template <int AMODE, int BMODE, bool TB, bool CLOW, int T>
-__global__ __launch_bounds__(256) void tri_gemm_kernel(GemmArgs g0, int64_t tm, int64_t tn,
-                                                       int super, MgSched sched) {
+__device__ __forceinline__ void tri_gemm_tile(const GemmArgs& g0, MgSmemT<T>& sm, int64_t tm,
+                                              int64_t tn, int super, const MgSched& sched,
+                                              int64_t bid) {
   constexpr int NA = T / 64;
   GemmArgs g = g0;
   g.A += (int64_t)blockIdx.z * g.sA;
   g.B += (int64_t)blockIdx.z * g.sB;
   g.C += (int64_t)blockIdx.z * g.sC;
-  __shared__ MgSmemT<T> sm;
   int64_t tr, tc;
   if (sched.per_xcd > 0) {
-    if (!mg_sched_tile<CLOW>(blockIdx.x, sched, tm, tn, tr, tc)) return;
+    if (!mg_sched_tile<CLOW>(bid, sched, tm, tn, tr, tc)) return;
   } else if (super) {
-    if (!mg_super_tile<tri_order<AMODE, BMODE>(), CLOW>(blockIdx.x, tm, tn, tr, tc)) return;
+    if (!mg_super_tile<tri_order<AMODE, BMODE>(), CLOW>(bid, tm, tn, tr, tc)) return;
   } else {
-    const int64_t t = xcd_tile(blockIdx.x, tm * tn);
+    const int64_t t = xcd_tile(bid, tm * tn);
     if (t < 0) return;
     tr = t / tn;
     tc = t % tn;
@@ -138,6 +139,29 @@ __global__ __launch_bounds__(256) void tri_gemm_kernel(GemmArgs g0, int64_t tm, 
   ct.store(cv, [&](int a, int j, int b) {
     return !CLOW || c0 + mg_col<T>(b) <= r0 + mg_row<T>(a, j);
   });
+}
+
+template <int AMODE, int BMODE, bool TB, bool CLOW, int T>
+__global__ __launch_bounds__(256) void tri_gemm_kernel(GemmArgs g0, int64_t tm, int64_t tn,
+                                                       int super, MgSched sched) {
+  __shared__ MgSmemT<T> sm;
+  tri_gemm_tile<AMODE, BMODE, TB, CLOW, T>(g0, sm, tm, tn, super, sched, blockIdx.x);
+}
+
+// Two independent small products in one launch (64-tiles, xcd-spread tiles): workgroups
+// [0, grid1) run the first, the rest the second.  The recursion pairs A22 -= T1 T1^T with
+// T2 = T1 A11, which needs the same inputs and none of the other's output.
+template <int A1, int B1, bool TB1, bool C1, int A2, int B2, bool TB2, bool C2>
+__global__ __launch_bounds__(256) void tri_gemm_pair_kernel(GemmArgs g1, int64_t tm1,
+                                                            int64_t tn1, int64_t grid1,
+                                                            GemmArgs g2, int64_t tm2,
+                                                            int64_t tn2) {
+  __shared__ MgSmemT<64> sm;
+  const int64_t bid = blockIdx.x;
+  if (bid < grid1)
+    tri_gemm_tile<A1, B1, TB1, C1, 64>(g1, sm, tm1, tn1, 0, MgSched{}, bid);
+  else
+    tri_gemm_tile<A2, B2, TB2, C2, 64>(g2, sm, tm2, tn2, 0, MgSched{}, bid - grid1);
 }
 
 // ---- products of the big levels on bf16 MFMA through a three-way split ---------------
@@ -635,6 +659,19 @@ int gemm3x(const G3Args& a, hipStream_t s, int batch) {
   hipLaunchKernelGGL((gemm3x_kernel<AMODE, BMODE, CLOW>), dim3((unsigned)grid, 1, (unsigned)batch),
                      dim3(512), 0, s, a, tm, tn, sched);
   return launch_status("gemm3x_kernel");
+}
+
+// A22 -= T1 T1^T (lower) and T2 = T1 A11 in one launch, on 64-tiles (pair_small).
+int tri_gemm_pair(GemmArgs a1, GemmArgs a2, hipStream_t s, int batch) {
+  const int64_t tm1 = (a1.M + 63) / 64, tn1 = (a1.N + 63) / 64;
+  const int64_t tm2 = (a2.M + 63) / 64, tn2 = (a2.N + 63) / 64;
+  const int64_t grid1 = (tm1 * tn1 + 7) / 8 * 8, grid2 = (tm2 * tn2 + 7) / 8 * 8;
+  LaunchTimer timer(HI2X_TIME_CHOL_GEMM,
+                    ((double)a1.M * a1.N * a1.Kd + (double)a2.M * a2.N * a2.Kd) * batch, s);
+  hipLaunchKernelGGL((tri_gemm_pair_kernel<0, 0, true, true, 0, 1, false, false>),
+                     dim3((unsigned)(grid1 + grid2), 1, (unsigned)batch), dim3(256), 0, s, a1,
+                     tm1, tn1, grid1, a2, tm2, tn2);
+  return launch_status("tri_gemm_pair_kernel");
 }
 
 // Products of the big grids: bf16 MFMA on split planes (default), or the fp32 MFMA GEMM
@@ -1301,19 +1338,35 @@ __global__ void status_init_kernel(int* __restrict__ status, int v, int n) {
 // ---- host recursion -------------------------------------------------------------------
 struct Plan {
   std::vector<int64_t> t1_off;  // per depth offset into the workspace
+  std::vector<int64_t> t2d_off; // per depth T2 of the paired small products (-1: none)
   int64_t t2_off = 0, total = 0;
   int64_t pa_off = 0, pb_off = 0;  // the two split-plane buffers (offsets in floats)
 };
 
-void plan_sizes(int64_t m, int depth, std::vector<int64_t>& t1, int64_t& t2) {
-  if (m <= NB) return;
+// Whether a node's A22 update and its T2 = T1 A11 both take the small-grid path (64-tiles,
+// fewer than 128 live tiles of 128): they then run as one launch, before the A22
+// recursion, with T2 in a buffer of the node's depth.
+static bool pair_small(int64_t m1, int64_t m2) {
+  const int64_t a = (m2 + MG_T - 1) / MG_T, b = (m1 + MG_T - 1) / MG_T;
+  return (a * a) / 2 < 128 && a * b < 128;
+}
+
+void plan_sizes(int64_t m, int depth, std::vector<int64_t>& t1, int64_t& t2,
+                std::vector<int64_t>& t2d) {
+  if (m <= 2 * NB) return;  // nodes and leaves work in LDS
   const int64_t nbk = (m + NB - 1) / NB;
   const int64_t m1 = ((nbk + 1) / 2) * NB, m2 = m - m1;
-  if ((int)t1.size() <= depth) t1.resize(depth + 1, 0);
+  if ((int)t1.size() <= depth) {
+    t1.resize(depth + 1, 0);
+    t2d.resize(depth + 1, 0);
+  }
   t1[depth] = std::max(t1[depth], m1 * m2);
-  t2 = std::max(t2, m1 * m2);
-  plan_sizes(m1, depth + 1, t1, t2);
-  plan_sizes(m2, depth + 1, t1, t2);
+  if (pair_small(m1, m2))
+    t2d[depth] = std::max(t2d[depth], m1 * m2);
+  else
+    t2 = std::max(t2, m1 * m2);
+  plan_sizes(m1, depth + 1, t1, t2, t2d);
+  plan_sizes(m2, depth + 1, t1, t2, t2d);
 }
 
 struct Ctx {
@@ -1393,6 +1446,24 @@ int inv_chol(const Ctx& c, int64_t r0, int64_t m, int depth) {
   // T1 = A21 A11^T  (op(B) = A11^T upper)
   rc = product<0, 2, true, false>(c, GemmArgs{A21, A11, T1, m2, m1, m1, K, K, m1, 1.0f, 0.0f});
   if (rc) return rc;
+  if (pair_small(m1, m2)) {
+    // A22 -= T1 T1^T and T2 = T1 A11 at once (T2 in this depth's buffer: the A22
+    // recursion below uses the deeper ones), then the recursion, then A21 = -A22 T2
+    float* T2d = c.ws + c.plan->t2d_off[depth];
+    GemmArgs upd{T1, T1, A22, m2, m2, m1, m1, m1, K, -1.0f, 1.0f};
+    GemmArgs t2{T1, A11, T2d, m2, m1, m1, m1, K, m1, 1.0f, 0.0f};
+    upd.sA = c.stride(upd.A);
+    upd.sB = c.stride(upd.B);
+    upd.sC = c.stride(upd.C);
+    t2.sA = c.stride(t2.A);
+    t2.sB = c.stride(t2.B);
+    t2.sC = c.stride(t2.C);
+    rc = tri_gemm_pair(upd, t2, c.s, c.batch);
+    if (rc) return rc;
+    rc = inv_chol(c, r0 + m1, m2, depth + 1);
+    if (rc) return rc;
+    return product<1, 0, false, false>(c, GemmArgs{A22, T2d, A21, m2, m1, m2, K, m1, K, -1.0f, 0.0f});
+  }
   // A22 -= T1 T1^T  (lower triangle)
   rc = product<0, 0, true, true>(c, GemmArgs{T1, T1, A22, m2, m2, m1, m1, m1, K, -1.0f, 1.0f});
   if (rc) return rc;
@@ -1414,12 +1485,16 @@ using namespace hi2x;
 // status word of the synchronous entry.
 static Plan make_plan(int64_t k) {
   Plan plan;
-  std::vector<int64_t> t1;
+  std::vector<int64_t> t1, t2d;
   int64_t t2 = 0;
-  plan_sizes(k, 0, t1, t2);
+  plan_sizes(k, 0, t1, t2, t2d);
   int64_t off = 0;
   for (int64_t sz : t1) {
     plan.t1_off.push_back(off);
+    off += (sz + 63) / 64 * 64;
+  }
+  for (int64_t sz : t2d) {
+    plan.t2d_off.push_back(sz > 0 ? off : -1);
     off += (sz + 63) / 64 * 64;
   }
   plan.t2_off = off;
