@@ -431,24 +431,16 @@ constexpr int GX_T = 256;                // tile edge
 constexpr int GX_SUP = 4;                // super-tile edge of the balanced schedule (tiles)
 constexpr int GX_PL = GX_T * G3_KC;      // bf16 per plane per stage
 
+typedef uint16_t GxStage[G3_NB][3][GX_PL];
+
+// Output tile (tr, tc) of the product (SA, SB: the workgroup's LDS rings).
 template <int AMODE, int BMODE, bool CLOW>
-__global__ __launch_bounds__(512, 1) void gemm3x_kernel(G3Args g0, int64_t tm, int64_t tn,
-                                                        MgSched sched) {
+__device__ __forceinline__ void gemm3x_tile(const G3Args& g0, GxStage& SA, GxStage& SB,
+                                            int64_t tr, int64_t tc) {
   G3Args g = g0;
   g.A += (int64_t)blockIdx.z * g.sA;
   g.B += (int64_t)blockIdx.z * g.sB;
   g.C += (int64_t)blockIdx.z * g.sC;
-  __shared__ __attribute__((aligned(1024))) uint16_t SA[G3_NB][3][GX_PL];
-  __shared__ __attribute__((aligned(1024))) uint16_t SB[G3_NB][3][GX_PL];
-  int64_t tr, tc;
-  if (sched.per_xcd > 0) {
-    if (!mg_sched_tile<CLOW, GX_SUP>(blockIdx.x, sched, tm, tn, tr, tc)) return;
-  } else {
-    const int64_t t = xcd_tile(blockIdx.x, tm * tn);
-    if (t < 0) return;
-    tr = t / tn;
-    tc = t % tn;
-  }
   const int64_t r0 = tr * GX_T, c0 = tc * GX_T;
   if (CLOW && c0 > r0 + GX_T - 1) return;
   int64_t kbeg, kend;
@@ -591,6 +583,59 @@ __global__ __launch_bounds__(512, 1) void gemm3x_kernel(G3Args g0, int64_t tm, i
   __syncthreads();  // no wave leaves while loads it issued may still write LDS
 }
 
+template <int AMODE, int BMODE, bool CLOW>
+__global__ __launch_bounds__(512, 1) void gemm3x_kernel(G3Args g0, int64_t tm, int64_t tn,
+                                                        MgSched sched) {
+  __shared__ __attribute__((aligned(1024))) GxStage SA;
+  __shared__ __attribute__((aligned(1024))) GxStage SB;
+  int64_t tr, tc;
+  if (sched.per_xcd > 0) {
+    if (!mg_sched_tile<CLOW, GX_SUP>(blockIdx.x, sched, tm, tn, tr, tc)) return;
+  } else {
+    const int64_t t = xcd_tile(blockIdx.x, tm * tn);
+    if (t < 0) return;
+    tr = t / tn;
+    tc = t % tn;
+  }
+  gemm3x_tile<AMODE, BMODE, CLOW>(g0, SA, SB, tr, tc);
+}
+
+// Two products in one launch: the node's A22 -= T1 T1^T (lower) and T2 = T1 A11 share T1's
+// planes and each fills the other's last round of tiles.  The table deals both products'
+// super-tiles to the XCDs by summed rank, longest first; an entry is (product << 15) |
+// super-tile index (row-major over that product's super-tile grid of nsc[product]
+// columns), 0xffff none.
+struct GxPair {
+  int32_t per_xcd = 0;
+  int32_t nsc[2] = {0, 0};
+  uint16_t st[MG_SCHED_MAX] = {};
+};
+
+template <int A1, int B1, bool C1, int A2, int B2, bool C2>
+__global__ __launch_bounds__(512, 1) void gemm3x_pair_kernel(G3Args g1, int64_t tm1,
+                                                             int64_t tn1, G3Args g2,
+                                                             int64_t tm2, int64_t tn2,
+                                                             GxPair sched) {
+  __shared__ __attribute__((aligned(1024))) GxStage SA;
+  __shared__ __attribute__((aligned(1024))) GxStage SB;
+  const int x = (int)(blockIdx.x & 7);
+  const int64_t slot = blockIdx.x >> 3;
+  const int j = (int)(slot / (GX_SUP * GX_SUP)), w = (int)(slot % (GX_SUP * GX_SUP));
+  if (j >= sched.per_xcd) return;
+  const int u = sched.st[x * sched.per_xcd + j];
+  if (u == 0xffff) return;
+  const int p = u >> 15, id = u & 0x7fff, nsc = sched.nsc[p];
+  const int64_t tr = (int64_t)(id / nsc) * GX_SUP + w / GX_SUP;
+  const int64_t tc = (int64_t)(id % nsc) * GX_SUP + w % GX_SUP;
+  if (p == 0) {
+    if (tr >= tm1 || tc >= tn1 || (C1 && tc > tr)) return;
+    gemm3x_tile<A1, B1, C1>(g1, SA, SB, tr, tc);
+  } else {
+    if (tr >= tm2 || tc >= tn2 || (C2 && tc > tr)) return;
+    gemm3x_tile<A2, B2, C2>(g2, SA, SB, tr, tc);
+  }
+}
+
 int split3(const float* X, int64_t ldx, int64_t R, int64_t Kk, int trans, int mask,
            uint16_t* out, int64_t Kp, hipStream_t s, int batch = 1, int64_t sx = 0,
            int64_t sout = 0) {
@@ -672,6 +717,73 @@ int tri_gemm_pair(GemmArgs a1, GemmArgs a2, hipStream_t s, int batch) {
                      dim3((unsigned)(grid1 + grid2), 1, (unsigned)batch), dim3(256), 0, s, a1,
                      tm1, tn1, grid1, a2, tm2, tn2);
   return launch_status("tri_gemm_pair_kernel");
+}
+
+// weight of super-tile (sr, sc) of a product on 256-tiles (0: no live tile)
+template <int AMODE, int BMODE, bool CLOW>
+static double gx_weight(const G3Args& a, int64_t tm, int64_t tn, int64_t sr, int64_t sc) {
+  double w = 0.0;
+  for (int64_t i = 0; i < GX_SUP; ++i)
+    for (int64_t j = 0; j < GX_SUP; ++j) {
+      const int64_t tr = sr * GX_SUP + i, tc = sc * GX_SUP + j;
+      if (tr >= tm || tc >= tn || (CLOW && tc > tr)) continue;
+      int64_t kb, ke;
+      tri_krange<AMODE, BMODE>(tr * GX_T, tc * GX_T, GX_T, a.Kd, kb, ke);
+      w += (double)std::max<int64_t>(0, ke - kb) + 2.0 * G3_KC;
+    }
+  return w;
+}
+
+// Both products on 256-tiles in one launch (gemm3x_pair_kernel); 1 when the table
+// would not hold their super-tiles (nothing launched: the caller runs them apart).
+template <int A1, int B1, bool C1, int A2, int B2, bool C2>
+int gemm3x_pair(const G3Args& a1, const G3Args& a2, hipStream_t s, int batch) {
+  const int64_t tm1 = (a1.M + GX_T - 1) / GX_T, tn1 = (a1.N + GX_T - 1) / GX_T;
+  const int64_t tm2 = (a2.M + GX_T - 1) / GX_T, tn2 = (a2.N + GX_T - 1) / GX_T;
+  GxPair sched;
+  sched.nsc[0] = (int32_t)((tn1 + GX_SUP - 1) / GX_SUP);
+  sched.nsc[1] = (int32_t)((tn2 + GX_SUP - 1) / GX_SUP);
+  std::vector<std::pair<double, int>> items;
+  for (int p = 0; p < 2; ++p) {
+    const int64_t tm = p ? tm2 : tm1, tn = p ? tn2 : tn1, nsc = sched.nsc[p];
+    const int64_t nsr = (tm + GX_SUP - 1) / GX_SUP;
+    if (nsr * nsc >= 0x7fff) return 1;
+    for (int64_t sr = 0; sr < nsr; ++sr)
+      for (int64_t sc = 0; sc < nsc; ++sc) {
+        const double w = p ? gx_weight<A2, B2, C2>(a2, tm, tn, sr, sc)
+                           : gx_weight<A1, B1, C1>(a1, tm, tn, sr, sc);
+        if (w > 0.0) items.push_back({w, (p << 15) | (int)(sr * nsc + sc)});
+      }
+  }
+  if (items.empty() || (int64_t)items.size() > MG_SCHED_MAX) return 1;
+  std::stable_sort(items.begin(), items.end(),
+                   [](const std::pair<double, int>& x, const std::pair<double, int>& y) {
+                     return x.first > y.first;
+                   });
+  double load[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  std::vector<int> lists[8];
+  for (const auto& it : items) {
+    int best = 0;
+    for (int x = 1; x < 8; ++x)
+      if (load[x] < load[best]) best = x;
+    load[best] += it.first;
+    lists[best].push_back(it.second);
+  }
+  int per = 0;
+  for (int x = 0; x < 8; ++x) per = std::max(per, (int)lists[x].size());
+  if ((int64_t)per * 8 > MG_SCHED_MAX) return 1;
+  sched.per_xcd = per;
+  for (int x = 0; x < 8; ++x)
+    for (int j = 0; j < per; ++j)
+      sched.st[x * per + j] = j < (int)lists[x].size() ? (uint16_t)lists[x][j] : (uint16_t)0xffff;
+  LaunchTimer timer(HI2X_TIME_CHOL_GEMM,
+                    ((double)a1.M * a1.N * a1.Kd + (double)a2.M * a2.N * a2.Kd) * batch, s);
+  const int64_t grid = (int64_t)8 * per * GX_SUP * GX_SUP;
+  hipLaunchKernelGGL((gemm3x_pair_kernel<A1, B1, C1, A2, B2, C2>),
+                     dim3((unsigned)grid, 1, (unsigned)batch), dim3(512), 0, s, a1, tm1, tn1, a2,
+                     tm2, tn2, sched);
+  const int rc = launch_status("gemm3x_pair_kernel");
+  return rc ? rc : 0;
 }
 
 // Products of the big grids: bf16 MFMA on split planes (default), or the fp32 MFMA GEMM
@@ -1337,9 +1449,9 @@ __global__ void status_init_kernel(int* __restrict__ status, int v, int n) {
 
 // ---- host recursion -------------------------------------------------------------------
 struct Plan {
-  std::vector<int64_t> t1_off;  // per depth offset into the workspace
-  std::vector<int64_t> t2d_off; // per depth T2 of the paired small products (-1: none)
-  int64_t t2_off = 0, total = 0;
+  std::vector<int64_t> t1_off;  // per depth offsets into the workspace: T1
+  std::vector<int64_t> t2_off;  // and T2 (made before the A22 recursion, used after it)
+  int64_t total = 0;
   int64_t pa_off = 0, pb_off = 0;  // the two split-plane buffers (offsets in floats)
 };
 
@@ -1351,22 +1463,14 @@ static bool pair_small(int64_t m1, int64_t m2) {
   return (a * a) / 2 < 128 && a * b < 128;
 }
 
-void plan_sizes(int64_t m, int depth, std::vector<int64_t>& t1, int64_t& t2,
-                std::vector<int64_t>& t2d) {
+void plan_sizes(int64_t m, int depth, std::vector<int64_t>& t12) {
   if (m <= 2 * NB) return;  // nodes and leaves work in LDS
   const int64_t nbk = (m + NB - 1) / NB;
   const int64_t m1 = ((nbk + 1) / 2) * NB, m2 = m - m1;
-  if ((int)t1.size() <= depth) {
-    t1.resize(depth + 1, 0);
-    t2d.resize(depth + 1, 0);
-  }
-  t1[depth] = std::max(t1[depth], m1 * m2);
-  if (pair_small(m1, m2))
-    t2d[depth] = std::max(t2d[depth], m1 * m2);
-  else
-    t2 = std::max(t2, m1 * m2);
-  plan_sizes(m1, depth + 1, t1, t2, t2d);
-  plan_sizes(m2, depth + 1, t1, t2, t2d);
+  if ((int)t12.size() <= depth) t12.resize(depth + 1, 0);
+  t12[depth] = std::max(t12[depth], m1 * m2);
+  plan_sizes(m1, depth + 1, t12);
+  plan_sizes(m2, depth + 1, t12);
 }
 
 struct Ctx {
@@ -1420,6 +1524,47 @@ int product(const Ctx& c, GemmArgs a) {
   return gemm3<AMODE, BMODE, CLOW>(g, c.s, c.batch);
 }
 
+// Whether a product runs on the 256-tile split-plane kernel (as product() and gemm3()
+// decide).
+static bool on_tile256(const GemmArgs& a, bool clow) {
+  const int64_t tm = (a.M + MG_T - 1) / MG_T, tn = (a.N + MG_T - 1) / MG_T;
+  if (!chol_split() || (clow ? tm * tn / 2 : tm * tn) < 128 || !chol_tile256()) return false;
+  const int64_t tm2 = (a.M + GX_T - 1) / GX_T, tn2 = (a.N + GX_T - 1) / GX_T;
+  return (clow ? tm2 * (tm2 + 1) / 2 : tm2 * tn2) >= 256;
+}
+
+// A22 -= T1 T1^T (lower) and T2 = T1 A11: where both run on 256-tiles, T1 is split once
+// for both and they share one launch; otherwise one product after the other.
+int product_pair(const Ctx& c, GemmArgs upd, GemmArgs t2) {
+  if (on_tile256(upd, true) && on_tile256(t2, false) && (upd.Kd % 16) == 0) {
+    upd.sA = c.stride(upd.A);
+    upd.sC = c.stride(upd.C);
+    t2.sB = c.stride(t2.B);
+    t2.sC = c.stride(t2.C);
+    const int64_t Kp = (upd.Kd + G3_KA - 1) / G3_KA * G3_KA;
+    uint16_t* pa = reinterpret_cast<uint16_t*>(c.ws + c.plan->pa_off);
+    uint16_t* pb = reinterpret_cast<uint16_t*>(c.ws + c.plan->pb_off);
+    const int64_t sPl = 2 * c.sW;
+    int rc = split3(upd.A, upd.lda, upd.M, upd.Kd, 0, 0, pa, Kp, c.s, c.batch, upd.sA, sPl);
+    if (rc) return rc;
+    rc = split3(t2.B, t2.ldb, t2.N, t2.Kd, 1, split_mask_b(1), pb, Kp, c.s, c.batch, t2.sB, sPl);
+    if (rc) return rc;
+    G3Args g1{pa, pa, upd.C, upd.M, upd.N, upd.Kd, Kp, upd.ldc, upd.alpha, upd.beta};
+    G3Args g2{pa, pb, t2.C, t2.M, t2.N, t2.Kd, Kp, t2.ldc, t2.alpha, t2.beta};
+    g1.sA = g1.sB = g2.sA = g2.sB = sPl;
+    g1.sC = upd.sC;
+    g2.sC = t2.sC;
+    rc = gemm3x_pair<0, 0, true, 0, 1, false>(g1, g2, c.s, c.batch);
+    if (rc != 1) return rc;
+    rc = gemm3<0, 0, true>(g1, c.s, c.batch);  // the table was too small: apart
+    if (rc) return rc;
+    return gemm3<0, 1, false>(g2, c.s, c.batch);
+  }
+  int rc = product<0, 0, true, true>(c, upd);
+  if (rc) return rc;
+  return product<0, 1, false, false>(c, t2);
+}
+
 int inv_chol(const Ctx& c, int64_t r0, int64_t m, int depth) {
   const int64_t K = c.K;
   if (m <= NB) {
@@ -1440,18 +1585,18 @@ int inv_chol(const Ctx& c, int64_t r0, int64_t m, int depth) {
   float* A21 = c.P + (r0 + m1) * K + r0;
   float* A22 = c.P + (r0 + m1) * K + (r0 + m1);
   float* T1 = c.ws + c.plan->t1_off[depth];
-  float* T2 = c.ws + c.plan->t2_off;
   int rc = inv_chol(c, r0, m1, depth + 1);
   if (rc) return rc;
   // T1 = A21 A11^T  (op(B) = A11^T upper)
   rc = product<0, 2, true, false>(c, GemmArgs{A21, A11, T1, m2, m1, m1, K, K, m1, 1.0f, 0.0f});
   if (rc) return rc;
+  // A22 -= T1 T1^T (lower) and T2 = T1 A11 (op(B) = A11 lower), both from T1 and A11 alone:
+  // at once, before the A22 recursion (T2 in this depth's buffer, the recursion uses the
+  // deeper ones)
+  float* T2 = c.ws + c.plan->t2_off[depth];
+  GemmArgs upd{T1, T1, A22, m2, m2, m1, m1, m1, K, -1.0f, 1.0f};
+  GemmArgs t2{T1, A11, T2, m2, m1, m1, m1, K, m1, 1.0f, 0.0f};
   if (pair_small(m1, m2)) {
-    // A22 -= T1 T1^T and T2 = T1 A11 at once (T2 in this depth's buffer: the A22
-    // recursion below uses the deeper ones), then the recursion, then A21 = -A22 T2
-    float* T2d = c.ws + c.plan->t2d_off[depth];
-    GemmArgs upd{T1, T1, A22, m2, m2, m1, m1, m1, K, -1.0f, 1.0f};
-    GemmArgs t2{T1, A11, T2d, m2, m1, m1, m1, K, m1, 1.0f, 0.0f};
     upd.sA = c.stride(upd.A);
     upd.sB = c.stride(upd.B);
     upd.sC = c.stride(upd.C);
@@ -1459,18 +1604,11 @@ int inv_chol(const Ctx& c, int64_t r0, int64_t m, int depth) {
     t2.sB = c.stride(t2.B);
     t2.sC = c.stride(t2.C);
     rc = tri_gemm_pair(upd, t2, c.s, c.batch);
-    if (rc) return rc;
-    rc = inv_chol(c, r0 + m1, m2, depth + 1);
-    if (rc) return rc;
-    return product<1, 0, false, false>(c, GemmArgs{A22, T2d, A21, m2, m1, m2, K, m1, K, -1.0f, 0.0f});
+  } else {
+    rc = product_pair(c, upd, t2);
   }
-  // A22 -= T1 T1^T  (lower triangle)
-  rc = product<0, 0, true, true>(c, GemmArgs{T1, T1, A22, m2, m2, m1, m1, m1, K, -1.0f, 1.0f});
   if (rc) return rc;
   rc = inv_chol(c, r0 + m1, m2, depth + 1);
-  if (rc) return rc;
-  // T2 = T1 A11  (op(B) = A11 lower)
-  rc = product<0, 1, false, false>(c, GemmArgs{T1, A11, T2, m2, m1, m1, m1, K, m1, 1.0f, 0.0f});
   if (rc) return rc;
   // A21 = -A22 T2  (A = A22 lower)
   return product<1, 0, false, false>(c, GemmArgs{A22, T2, A21, m2, m1, m2, K, m1, K, -1.0f, 0.0f});
@@ -1485,20 +1623,15 @@ using namespace hi2x;
 // status word of the synchronous entry.
 static Plan make_plan(int64_t k) {
   Plan plan;
-  std::vector<int64_t> t1, t2d;
-  int64_t t2 = 0;
-  plan_sizes(k, 0, t1, t2, t2d);
+  std::vector<int64_t> t12;
+  plan_sizes(k, 0, t12);
   int64_t off = 0;
-  for (int64_t sz : t1) {
+  for (int64_t sz : t12) {
     plan.t1_off.push_back(off);
     off += (sz + 63) / 64 * 64;
-  }
-  for (int64_t sz : t2d) {
-    plan.t2d_off.push_back(sz > 0 ? off : -1);
+    plan.t2_off.push_back(off);
     off += (sz + 63) / 64 * 64;
   }
-  plan.t2_off = off;
-  off += (t2 + 63) / 64 * 64;
   // split planes: 3 x rows x Kp bf16 for the largest operand of the top-level products
   int64_t m1 = 0;
   if (k > NB) {
