@@ -276,24 +276,16 @@ constexpr int g3_waitcnt(int vm, int lgkm) {
   return (vm & 15) | ((vm >> 4) << 14) | (7 << 4) | (lgkm << 8);
 }
 
+typedef uint16_t G3Stage[G3_NB][3][G3_PL];
+
+// Output tile (tr, tc) of the product (SA, SB: the workgroup's LDS rings).
 template <int AMODE, int BMODE, bool CLOW>
-__global__ __launch_bounds__(256, 2) void gemm3_kernel(G3Args g0, int64_t tm, int64_t tn,
-                                                       MgSched sched) {
+__device__ __forceinline__ void gemm3_tile(const G3Args& g0, G3Stage& SA, G3Stage& SB,
+                                           int64_t tr, int64_t tc) {
   G3Args g = g0;
   g.A += (int64_t)blockIdx.z * g.sA;
   g.B += (int64_t)blockIdx.z * g.sB;
   g.C += (int64_t)blockIdx.z * g.sC;
-  __shared__ __attribute__((aligned(1024))) uint16_t SA[G3_NB][3][G3_PL];
-  __shared__ __attribute__((aligned(1024))) uint16_t SB[G3_NB][3][G3_PL];
-  int64_t tr, tc;
-  if (sched.per_xcd > 0) {
-    if (!mg_sched_tile<CLOW>(blockIdx.x, sched, tm, tn, tr, tc)) return;
-  } else {
-    const int64_t t = xcd_tile(blockIdx.x, tm * tn);
-    if (t < 0) return;
-    tr = t / tn;
-    tc = t % tn;
-  }
   const int64_t r0 = tr * MG_T, c0 = tc * MG_T;
   if (CLOW && c0 > r0 + MG_T - 1) return;
   int64_t kbeg, kend;
@@ -415,6 +407,55 @@ __global__ __launch_bounds__(256, 2) void gemm3_kernel(G3Args g0, int64_t tm, in
     return !CLOW || c0 + mg_col<MG_T>(b) <= r0 + mg_row<MG_T>(a, j);
   });
   __syncthreads();  // no wave leaves while loads it issued may still write LDS
+}
+
+template <int AMODE, int BMODE, bool CLOW>
+__global__ __launch_bounds__(256, 2) void gemm3_kernel(G3Args g0, int64_t tm, int64_t tn,
+                                                       MgSched sched) {
+  __shared__ __attribute__((aligned(1024))) G3Stage SA;
+  __shared__ __attribute__((aligned(1024))) G3Stage SB;
+  int64_t tr, tc;
+  if (sched.per_xcd > 0) {
+    if (!mg_sched_tile<CLOW>(blockIdx.x, sched, tm, tn, tr, tc)) return;
+  } else {
+    const int64_t t = xcd_tile(blockIdx.x, tm * tn);
+    if (t < 0) return;
+    tr = t / tn;
+    tc = t % tn;
+  }
+  gemm3_tile<AMODE, BMODE, CLOW>(g0, SA, SB, tr, tc);
+}
+
+// Two products in one launch on 128-tiles: the table as gemm3x_pair_kernel's (GxPair),
+// over super-tiles of MG_SUP x MG_SUP tiles.
+struct GxPair {
+  int32_t per_xcd = 0;
+  int32_t nsc[2] = {0, 0};
+  uint16_t st[MG_SCHED_MAX] = {};
+};
+
+template <int A1, int B1, bool C1, int A2, int B2, bool C2>
+__global__ __launch_bounds__(256, 2) void gemm3_pair_kernel(G3Args g1, int64_t tm1, int64_t tn1,
+                                                            G3Args g2, int64_t tm2, int64_t tn2,
+                                                            GxPair sched) {
+  __shared__ __attribute__((aligned(1024))) G3Stage SA;
+  __shared__ __attribute__((aligned(1024))) G3Stage SB;
+  const int x = (int)(blockIdx.x & 7);
+  const int64_t slot = blockIdx.x >> 3;
+  const int j = (int)(slot / (MG_SUP * MG_SUP)), w = (int)(slot % (MG_SUP * MG_SUP));
+  if (j >= sched.per_xcd) return;
+  const int u = sched.st[x * sched.per_xcd + j];
+  if (u == 0xffff) return;
+  const int p = u >> 15, id = u & 0x7fff, nsc = sched.nsc[p];
+  const int64_t tr = (int64_t)(id / nsc) * MG_SUP + w / MG_SUP;
+  const int64_t tc = (int64_t)(id % nsc) * MG_SUP + w % MG_SUP;
+  if (p == 0) {
+    if (tr >= tm1 || tc >= tn1 || (C1 && tc > tr)) return;
+    gemm3_tile<A1, B1, C1>(g1, SA, SB, tr, tc);
+  } else {
+    if (tr >= tm2 || tc >= tn2 || (C2 && tc > tr)) return;
+    gemm3_tile<A2, B2, C2>(g2, SA, SB, tr, tc);
+  }
 }
 
 // The same product on 256 x 256 tiles for the largest grids: one workgroup of 8 waves per
@@ -601,15 +642,10 @@ __global__ __launch_bounds__(512, 1) void gemm3x_kernel(G3Args g0, int64_t tm, i
 }
 
 // Two products in one launch: the node's A22 -= T1 T1^T (lower) and T2 = T1 A11 share T1's
-// planes and each fills the other's last round of tiles.  The table deals both products'
-// super-tiles to the XCDs by summed rank, longest first; an entry is (product << 15) |
-// super-tile index (row-major over that product's super-tile grid of nsc[product]
-// columns), 0xffff none.
-struct GxPair {
-  int32_t per_xcd = 0;
-  int32_t nsc[2] = {0, 0};
-  uint16_t st[MG_SCHED_MAX] = {};
-};
+// planes and each fills the other's last round of tiles.  The table (GxPair) deals both
+// products' super-tiles to the XCDs by summed rank, longest first; an entry is
+// (product << 15) | super-tile index (row-major over that product's super-tile grid of
+// nsc[product] columns), 0xffff none.
 
 template <int A1, int B1, bool C1, int A2, int B2, bool C2>
 __global__ __launch_bounds__(512, 1) void gemm3x_pair_kernel(G3Args g1, int64_t tm1,
@@ -719,39 +755,41 @@ int tri_gemm_pair(GemmArgs a1, GemmArgs a2, hipStream_t s, int batch) {
   return launch_status("tri_gemm_pair_kernel");
 }
 
-// weight of super-tile (sr, sc) of a product on 256-tiles (0: no live tile)
-template <int AMODE, int BMODE, bool CLOW>
-static double gx_weight(const G3Args& a, int64_t tm, int64_t tn, int64_t sr, int64_t sc) {
+// weight of super-tile (sr, sc) (SUP x SUP tiles of T) of a product (0: no live tile)
+template <int AMODE, int BMODE, bool CLOW, int T, int SUP>
+static double pair_weight(const G3Args& a, int64_t tm, int64_t tn, int64_t sr, int64_t sc) {
   double w = 0.0;
-  for (int64_t i = 0; i < GX_SUP; ++i)
-    for (int64_t j = 0; j < GX_SUP; ++j) {
-      const int64_t tr = sr * GX_SUP + i, tc = sc * GX_SUP + j;
+  for (int64_t i = 0; i < SUP; ++i)
+    for (int64_t j = 0; j < SUP; ++j) {
+      const int64_t tr = sr * SUP + i, tc = sc * SUP + j;
       if (tr >= tm || tc >= tn || (CLOW && tc > tr)) continue;
       int64_t kb, ke;
-      tri_krange<AMODE, BMODE>(tr * GX_T, tc * GX_T, GX_T, a.Kd, kb, ke);
+      tri_krange<AMODE, BMODE>(tr * T, tc * T, T, a.Kd, kb, ke);
       w += (double)std::max<int64_t>(0, ke - kb) + 2.0 * G3_KC;
     }
   return w;
 }
 
-// Both products on 256-tiles in one launch (gemm3x_pair_kernel); 1 when the table
-// would not hold their super-tiles (nothing launched: the caller runs them apart).
-template <int A1, int B1, bool C1, int A2, int B2, bool C2>
-int gemm3x_pair(const G3Args& a1, const G3Args& a2, hipStream_t s, int batch) {
-  const int64_t tm1 = (a1.M + GX_T - 1) / GX_T, tn1 = (a1.N + GX_T - 1) / GX_T;
-  const int64_t tm2 = (a2.M + GX_T - 1) / GX_T, tn2 = (a2.N + GX_T - 1) / GX_T;
+// Both products in one launch on T-tiles (T = GX_T: gemm3x_pair_kernel, MG_T:
+// gemm3_pair_kernel); 1 when the table would not hold their super-tiles (nothing
+// launched: the caller runs them apart).
+template <int T, int A1, int B1, bool C1, int A2, int B2, bool C2>
+int g3_pair(const G3Args& a1, const G3Args& a2, hipStream_t s, int batch) {
+  constexpr int SUP = T == GX_T ? GX_SUP : MG_SUP;
+  const int64_t tm1 = (a1.M + T - 1) / T, tn1 = (a1.N + T - 1) / T;
+  const int64_t tm2 = (a2.M + T - 1) / T, tn2 = (a2.N + T - 1) / T;
   GxPair sched;
-  sched.nsc[0] = (int32_t)((tn1 + GX_SUP - 1) / GX_SUP);
-  sched.nsc[1] = (int32_t)((tn2 + GX_SUP - 1) / GX_SUP);
+  sched.nsc[0] = (int32_t)((tn1 + SUP - 1) / SUP);
+  sched.nsc[1] = (int32_t)((tn2 + SUP - 1) / SUP);
   std::vector<std::pair<double, int>> items;
   for (int p = 0; p < 2; ++p) {
     const int64_t tm = p ? tm2 : tm1, tn = p ? tn2 : tn1, nsc = sched.nsc[p];
-    const int64_t nsr = (tm + GX_SUP - 1) / GX_SUP;
+    const int64_t nsr = (tm + SUP - 1) / SUP;
     if (nsr * nsc >= 0x7fff) return 1;
     for (int64_t sr = 0; sr < nsr; ++sr)
       for (int64_t sc = 0; sc < nsc; ++sc) {
-        const double w = p ? gx_weight<A2, B2, C2>(a2, tm, tn, sr, sc)
-                           : gx_weight<A1, B1, C1>(a1, tm, tn, sr, sc);
+        const double w = p ? pair_weight<A2, B2, C2, T, SUP>(a2, tm, tn, sr, sc)
+                           : pair_weight<A1, B1, C1, T, SUP>(a1, tm, tn, sr, sc);
         if (w > 0.0) items.push_back({w, (p << 15) | (int)(sr * nsc + sc)});
       }
   }
@@ -778,12 +816,18 @@ int gemm3x_pair(const G3Args& a1, const G3Args& a2, hipStream_t s, int batch) {
       sched.st[x * per + j] = j < (int)lists[x].size() ? (uint16_t)lists[x][j] : (uint16_t)0xffff;
   LaunchTimer timer(HI2X_TIME_CHOL_GEMM,
                     ((double)a1.M * a1.N * a1.Kd + (double)a2.M * a2.N * a2.Kd) * batch, s);
-  const int64_t grid = (int64_t)8 * per * GX_SUP * GX_SUP;
-  hipLaunchKernelGGL((gemm3x_pair_kernel<A1, B1, C1, A2, B2, C2>),
-                     dim3((unsigned)grid, 1, (unsigned)batch), dim3(512), 0, s, a1, tm1, tn1, a2,
-                     tm2, tn2, sched);
-  const int rc = launch_status("gemm3x_pair_kernel");
-  return rc ? rc : 0;
+  const int64_t grid = (int64_t)8 * per * SUP * SUP;
+  if constexpr (T == GX_T) {
+    hipLaunchKernelGGL((gemm3x_pair_kernel<A1, B1, C1, A2, B2, C2>),
+                       dim3((unsigned)grid, 1, (unsigned)batch), dim3(512), 0, s, a1, tm1, tn1,
+                       a2, tm2, tn2, sched);
+    return launch_status("gemm3x_pair_kernel");
+  } else {
+    hipLaunchKernelGGL((gemm3_pair_kernel<A1, B1, C1, A2, B2, C2>),
+                       dim3((unsigned)grid, 1, (unsigned)batch), dim3(256), 0, s, a1, tm1, tn1,
+                       a2, tm2, tn2, sched);
+    return launch_status("gemm3_pair_kernel");
+  }
 }
 
 // Products of the big grids: bf16 MFMA on split planes (default), or the fp32 MFMA GEMM
@@ -1524,19 +1568,21 @@ int product(const Ctx& c, GemmArgs a) {
   return gemm3<AMODE, BMODE, CLOW>(g, c.s, c.batch);
 }
 
-// Whether a product runs on the 256-tile split-plane kernel (as product() and gemm3()
-// decide).
-static bool on_tile256(const GemmArgs& a, bool clow) {
+// The split-plane tile edge a product runs on (as product() and gemm3() decide): 256,
+// 128, or 0 when it takes the fp32 path.
+static int split_tile(const GemmArgs& a, bool clow) {
   const int64_t tm = (a.M + MG_T - 1) / MG_T, tn = (a.N + MG_T - 1) / MG_T;
-  if (!chol_split() || (clow ? tm * tn / 2 : tm * tn) < 128 || !chol_tile256()) return false;
+  if (!chol_split() || (clow ? tm * tn / 2 : tm * tn) < 128) return 0;
   const int64_t tm2 = (a.M + GX_T - 1) / GX_T, tn2 = (a.N + GX_T - 1) / GX_T;
-  return (clow ? tm2 * (tm2 + 1) / 2 : tm2 * tn2) >= 256;
+  return ((clow ? tm2 * (tm2 + 1) / 2 : tm2 * tn2) >= 256 && chol_tile256()) ? GX_T : MG_T;
 }
 
-// A22 -= T1 T1^T (lower) and T2 = T1 A11: where both run on 256-tiles, T1 is split once
-// for both and they share one launch; otherwise one product after the other.
+// A22 -= T1 T1^T (lower) and T2 = T1 A11: where both run on split planes with the same
+// tile edge, T1 is split once for both and they share one launch; otherwise one product
+// after the other.
 int product_pair(const Ctx& c, GemmArgs upd, GemmArgs t2) {
-  if (on_tile256(upd, true) && on_tile256(t2, false) && (upd.Kd % 16) == 0) {
+  const int tile = split_tile(upd, true);
+  if (tile != 0 && tile == split_tile(t2, false)) {
     upd.sA = c.stride(upd.A);
     upd.sC = c.stride(upd.C);
     t2.sB = c.stride(t2.B);
@@ -1554,7 +1600,8 @@ int product_pair(const Ctx& c, GemmArgs upd, GemmArgs t2) {
     g1.sA = g1.sB = g2.sA = g2.sB = sPl;
     g1.sC = upd.sC;
     g2.sC = t2.sC;
-    rc = gemm3x_pair<0, 0, true, 0, 1, false>(g1, g2, c.s, c.batch);
+    rc = tile == GX_T ? g3_pair<GX_T, 0, 0, true, 0, 1, false>(g1, g2, c.s, c.batch)
+                      : g3_pair<MG_T, 0, 0, true, 0, 1, false>(g1, g2, c.s, c.batch);
     if (rc != 1) return rc;
     rc = gemm3<0, 0, true>(g1, c.s, c.batch);  // the table was too small: apart
     if (rc) return rc;
