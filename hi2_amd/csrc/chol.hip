@@ -164,31 +164,27 @@ __global__ __launch_bounds__(256) void tri_gemm_pair_kernel(GemmArgs g1, int64_t
     tri_gemm_tile<A2, B2, TB2, C2, 64>(g2, sm, tm2, tn2, 0, MgSched{}, bid - grid1);
 }
 
-// ---- products of the big levels on bf16 MFMA through a three-way split ---------------
-// Every fp32 operand x is written once, before the product, as three bf16 planes
-// x1 = bf16(x), x2 = bf16(x - x1), x3 = bf16(x - x1 - x2) (the differences are exact in
-// fp32; x = x1 + x2 + x3 to within 2^-27 |x|), laid out [row][k] with k contiguous
-// (a transposed copy where the product needs one; stored in chunks of 16 k) and the
-// operand's structural zeros
-// written as zeros.  The product keeps the six terms x_i y_j with i + j <= 4 (the dropped
-// ones are below 2^-26 |x y|); bf16 products are exact and v_mfma_f32_32x32x16_bf16
-// accumulates in fp32: six MFMAs of 32 cycles cover 16 k where the fp32 MFMA needs
-// eight of 64, with the rounding of an fp32 GEMM (not bit-identical to one).
+// ---- products of the big levels on fp16 MFMA through a scaled two-way split ----------
+// Every fp32 operand row is scaled by a power of two, s_r = 2^(14 - e_r) with
+// e_r = floor(log2 max_k |x[r][k]|), which puts the row's largest element in [2^14, 2^15)
+// (inside fp16's range), and written once, before the product, as two fp16 planes
+// x1 = fp16(s_r x), x2 = fp16(s_r x - x1) (the difference is exact in fp32): s_r x =
+// x1 + x2 to within 2^-22 of the row's largest element.  The planes are laid out
+// [row][k] with k contiguous (a transposed copy where the product needs one; stored in
+// chunks of 16 k), the operand's structural zeros written as zeros.  The product keeps
+// the three terms x1 y1 + x1 y2 + x2 y1 (the dropped x2 y2 is below 2^-22 of the largest
+// |x_k y_k|); fp16 products are exact and v_mfma_f32_32x32x16_f16 accumulates in fp32,
+// and the epilogue multiplies by 1 / (s_r s_c) (exact: powers of two).  Three MFMAs of 32
+// cycles cover 16 k where the fp32 MFMA needs eight of 64, with the rounding of an fp32
+// GEMM (not bit-identical to one).
 
-// Planes of R x Kp bf16 from X, each stored in chunks of 16 k: element (r, k) of plane p
-// at out[p][k / 16][r][k % 16] (a chunk of a tile's rows is contiguous, so the product
-// reads whole cache lines).  !trans: x = X[r][k] (X is R x Kk, ld ldx), trans: x = X[k][r]
-// (X is Kk x R).  mask 1 keeps k <= r, 2 keeps k >= r; k >= Kk and masked elements are
-// zero.  A workgroup converts a 64 x 64 block through LDS: 4 threads per output row, 16
-// consecutive k (one chunk row) each.
-__global__ __launch_bounds__(256) void split3_kernel(const float* __restrict__ X, int64_t ldx,
-                                                     int64_t R, int64_t Kk, int trans, int mask,
-                                                     uint16_t* __restrict__ out, int64_t Kp,
-                                                     int64_t sx, int64_t sout) {
-  __shared__ float t[64][65];
-  X += (int64_t)blockIdx.z * sx;
-  out += (int64_t)blockIdx.z * sout;
-  const int64_t r0 = (int64_t)blockIdx.y * 64, k0 = (int64_t)blockIdx.x * 64;
+// Operand row maxima: G2_NS slices of the rank, one partial per (slice, row).
+constexpr int G2_NS = 16;
+constexpr int G3_NP = 2;  // planes per operand
+
+__device__ __forceinline__ int split_load_block(float (&t)[64][65], const float* X, int64_t ldx,
+                                                int64_t R, int64_t Kk, int trans, int64_t r0,
+                                                int64_t k0) {
   const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
   // input block: rows of X are contiguous along k (!trans) or along r (trans)
   const int64_t xr0 = trans ? k0 : r0, xc0 = trans ? r0 : k0;
@@ -203,26 +199,95 @@ __global__ __launch_bounds__(256) void split3_kernel(const float* __restrict__ X
     const uint32_t off = (y < rows && tx < cols) ? (uint32_t)(((int64_t)y * ldx + tx) * 4) : MG_OOB;
     t[y][tx] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, (int)off, 0, 0));
   }
+  return 0;
+}
+
+__device__ __forceinline__ bool split_keep(int mask, int64_t r, int64_t k) {
+  return mask == 1 ? k <= r : (mask == 2 ? k >= r : true);
+}
+
+// Grid (G2_NS, row groups): slice s covers k in [s L, (s + 1) L), L = ceil(Kk / G2_NS).
+// !trans (operand rows contiguous): one wave per row, lanes along k; trans (operand rows
+// are columns of X): 64 rows per workgroup, lanes along the row index, the four waves
+// taking every fourth k, combined through LDS.  mask as in split2_kernel.
+__global__ __launch_bounds__(256) void rowmax_kernel(const float* __restrict__ X, int64_t ldx,
+                                                     int64_t R, int64_t Kk, int trans, int mask,
+                                                     float* __restrict__ pm, int64_t sx,
+                                                     int64_t spm) {
+  X += (int64_t)blockIdx.z * sx;
+  pm += (int64_t)blockIdx.z * spm;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t L = (Kk + G2_NS - 1) / G2_NS;
+  const int64_t ks = (int64_t)blockIdx.x * L;
+  const int64_t ke = (ks + L < Kk) ? ks + L : Kk;
+  float m = 0.0f;  // fmaxf skips NaN elements
+  if (!trans) {
+    const int64_t r = (int64_t)blockIdx.y * 4 + wave;
+    if (r >= R) return;
+    const float* x = X + r * ldx;
+    for (int64_t k = ks + lane; k < ke; k += 64)
+      m = split_keep(mask, r, k) ? fmaxf(m, fabsf(x[k])) : m;
+#pragma unroll
+    for (int sh = 32; sh >= 1; sh >>= 1) m = fmaxf(m, __shfl_xor(m, sh));
+    if (lane == 0) pm[blockIdx.x * R + r] = m;
+    return;
+  }
+  __shared__ float part[4][64];
+  const int64_t r = (int64_t)blockIdx.y * 64 + lane;
+  if (r < R) {
+#pragma unroll 8
+    for (int64_t k = ks + wave; k < ke; k += 4)
+      m = split_keep(mask, r, k) ? fmaxf(m, fabsf(X[k * ldx + r])) : m;
+  }
+  part[wave][lane] = m;
+  __syncthreads();
+  if (wave == 0 && r < R)
+    pm[blockIdx.x * R + r] = fmaxf(fmaxf(part[0][lane], part[1][lane]),
+                                   fmaxf(part[2][lane], part[3][lane]));
+}
+
+// Planes of R x Kp fp16 from X, each stored in chunks of 16 k: element (r, k) of plane p
+// at out[p][k / 16][r][k % 16] (a chunk of a tile's rows is contiguous, so the product
+// reads whole cache lines), followed by the R inverse row scales 1 / s_r (fp32) and the
+// row maxima partials of rowmax_kernel ([slice][R]).  !trans: x = X[r][k] (X is R x Kk,
+// ld ldx), trans: x = X[k][r] (X is Kk x R).  mask 1 keeps k <= r, 2 keeps k >= r; k >= Kk
+// and masked elements are zero.  A workgroup converts a 64 x 64 block through LDS: 4
+// threads per output row, 16 consecutive k (one chunk row) each.
+__global__ __launch_bounds__(256) void split2_kernel(const float* __restrict__ X, int64_t ldx,
+                                                     int64_t R, int64_t Kk, int trans, int mask,
+                                                     uint16_t* __restrict__ out, int64_t Kp,
+                                                     int64_t sx, int64_t sout) {
+  __shared__ float t[64][65];
+  X += (int64_t)blockIdx.z * sx;
+  out += (int64_t)blockIdx.z * sout;
+  const int64_t r0 = (int64_t)blockIdx.y * 64, k0 = (int64_t)blockIdx.x * 64;
+  split_load_block(t, X, ldx, R, Kk, trans, r0, k0);
   __syncthreads();
   const int orow = threadIdx.x >> 2, kq = threadIdx.x & 3;  // output row, 16-k quarter
   const int64_t r = r0 + orow;
   if (r >= R) return;
-  mg_u16x8 p1[2], p2[2], p3[2];
+  float* inv = reinterpret_cast<float*>(out + G3_NP * R * Kp);
+  const float* pm = inv + R;
+  float m = 0.0f;  // the row's maximum: four partials per thread, then over the row's lanes
 #pragma unroll
-  for (int e = 0; e < 16; ++e) {
-    const int kk = 16 * kq + e;
-    const int64_t k = k0 + kk;
+  for (int i = 0; i < G2_NS / 4; ++i) m = fmaxf(m, pm[(G2_NS / 4 * kq + i) * R + r]);
+  m = fmaxf(m, __shfl_xor(m, 1));
+  m = fmaxf(m, __shfl_xor(m, 2));
+  int ex = 0;
+  (void)frexpf(m, &ex);  // m = f 2^ex, f in [0.5, 1): floor(log2 m) = ex - 1
+  const int e = m > 0.0f ? (ex - 1 < -100 ? -100 : (ex - 1 > 100 ? 100 : ex - 1)) : 0;
+  const float sc = ldexpf(1.0f, 14 - e);
+  if (blockIdx.x == 0 && kq == 0) inv[r] = ldexpf(1.0f, e - 14);
+  mg_u16x8 p1[2], p2[2];
+#pragma unroll
+  for (int e2 = 0; e2 < 16; ++e2) {
+    const int kk = 16 * kq + e2;
     float x = trans ? t[kk][orow] : t[orow][kk];
-    const bool keep = mask == 1 ? k <= r : (mask == 2 ? k >= r : true);
-    x = keep ? x : 0.0f;
-    const __bf16 b1 = (__bf16)x;
-    const float e1 = x - (float)b1;
-    const __bf16 b2 = (__bf16)e1;
-    const float e2 = e1 - (float)b2;
-    const __bf16 b3 = (__bf16)e2;
-    p1[e >> 3][e & 7] = __builtin_bit_cast(unsigned short, b1);
-    p2[e >> 3][e & 7] = __builtin_bit_cast(unsigned short, b2);
-    p3[e >> 3][e & 7] = __builtin_bit_cast(unsigned short, b3);
+    x = split_keep(mask, r, k0 + kk) ? x * sc : 0.0f;
+    const _Float16 h1 = (_Float16)x;
+    const _Float16 h2 = (_Float16)(x - (float)h1);
+    p1[e2 >> 3][e2 & 7] = __builtin_bit_cast(unsigned short, h1);
+    p2[e2 >> 3][e2 & 7] = __builtin_bit_cast(unsigned short, h2);
   }
   const int64_t kb = k0 + 16 * kq;
   if (kb >= Kp) return;
@@ -232,13 +297,12 @@ __global__ __launch_bounds__(256) void split3_kernel(const float* __restrict__ X
   for (int g = 0; g < 2; ++g) {
     *reinterpret_cast<mg_u16x8*>(o + 8 * g) = p1[g];
     *reinterpret_cast<mg_u16x8*>(o + plane + 8 * g) = p2[g];
-    *reinterpret_cast<mg_u16x8*>(o + 2 * plane + 8 * g) = p3[g];
   }
 }
 
 // C[M, N] = alpha * A B^T + beta * C over k in [kbeg, kend) of each 128 x 128 output tile
 // (tri_krange), A and B given as split planes (16-k chunks).  Workgroup: 4 waves of
-// 64 x 64 (2 x 2 accumulators), two workgroups per CU (72 KB of LDS each), so each SIMD
+// 64 x 64 (2 x 2 accumulators), two workgroups per CU (48 KB of LDS each), so each SIMD
 // has a second wave to issue MFMAs while one waits at a stage barrier.  Stages of 16 k
 // go from L2 straight into LDS through a ring of three (prefetch distance two): each load
 // instruction of a wave writes 1 KB = 32 rows x 2 16-byte slots of one plane, slot q of
@@ -255,8 +319,20 @@ struct G3Args {
 constexpr int G3_KC = 16;                 // k per stage (one MFMA k-step)
 constexpr int G3_KA = 32;                 // k alignment of the planes (Kp)
 constexpr int G3_NB = 3;                  // stages in the ring
-constexpr int G3_PL = MG_T * G3_KC;       // bf16 per plane per stage
-constexpr int G3_PER_STAGE = 6;           // load instructions per wave and stage (2 x 3 x 4 / 4)
+constexpr int G3_PL = MG_T * G3_KC;       // fp16 per plane per stage
+constexpr int G3_PER_STAGE = 2 * G3_NP;   // load instructions per wave and stage (2 x 2 x 4 / 4)
+
+typedef _Float16 mg_f16x8 __attribute__((ext_vector_type(8)));
+
+// The inverse row scales of an operand's planes (rows x Kp per plane, then the scales)
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t plane_scales(const uint16_t* planes,
+                                                               int64_t rows, int64_t Kp) {
+  return mg_rsrc(reinterpret_cast<const float*>(planes + G3_NP * rows * Kp), rows);
+}
+__device__ __forceinline__ float scale_at(__amdgpu_buffer_rsrc_t rs, int64_t i, bool ok) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                       rs, ok ? (int)(i * 4) : (int)MG_OOB, 0, 0));
+}
 
 __device__ __forceinline__ void g3_dma16(__amdgpu_buffer_rsrc_t rs, uint32_t voff, void* lds) {
   const uint32_t la = __builtin_amdgcn_readfirstlane(
@@ -276,7 +352,7 @@ constexpr int g3_waitcnt(int vm, int lgkm) {
   return (vm & 15) | ((vm >> 4) << 14) | (7 << 4) | (lgkm << 8);
 }
 
-typedef uint16_t G3Stage[G3_NB][3][G3_PL];
+typedef uint16_t G3Stage[G3_NB][G3_NP][G3_PL];
 
 // Output tile (tr, tc) of the product (SA, SB: the workgroup's LDS rings).
 template <int AMODE, int BMODE, bool CLOW>
@@ -299,10 +375,10 @@ __device__ __forceinline__ void gemm3_tile(const G3Args& g0, G3Stage& SA, G3Stag
   const int rowsA = (int)((g.M - r0 < MG_T) ? g.M - r0 : MG_T);
   const int rowsB = (int)((g.N - c0 < MG_T) ? g.N - c0 : MG_T);
   const int64_t plA = g.M * g.Kp, plB = g.N * g.Kp;
-  // load j (0..5) of a stage: operand j / 3, plane j % 3, rows 32 wv .. 32 wv + 31
+  // load j (0..3) of a stage: operand j / 2, plane j % 2, rows 32 wv .. 32 wv + 31
   const int prow = lane >> 1, piece = (lane & 1) ^ ((lane >> 4) & 1);
   auto dma_one = [&](int j, int64_t k0, int buf, bool live) {
-    const int opd = j / 3, pl = j % 3;
+    const int opd = j / G3_NP, pl = j % G3_NP;
     const int row = 32 * wv + prow;
     // chunk k0 / 16 of the tile's rows: rows x 16 contiguous bf16
     const uint16_t* base = opd == 0 ? g.A + pl * plA + ((k0 >> 4) * g.M + r0) * G3_KC
@@ -321,23 +397,22 @@ __device__ __forceinline__ void gemm3_tile(const G3Args& g0, G3Stage& SA, G3Stag
   // lane / 32 (k 8 h .. 8 h + 7 of the stage) in slot h ^ ((row / 8) % 2)
   const int rA = wr * 64 + (lane & 31), rB = wcn * 64 + (lane & 31);
   const int so = 8 * ((lane >> 5) ^ ((lane >> 3) & 1));
-  typedef mg_bf16x8 V;
-  V a0[3][2], b0[3][2], a1[3][2], b1[3][2];  // [plane][tile], stage sets 0 and 1
-  auto read = [&](V (&av)[3][2], V (&bv)[3][2], int buf) {
+  typedef mg_f16x8 V;
+  V a0[G3_NP][2], b0[G3_NP][2], a1[G3_NP][2], b1[G3_NP][2];  // [plane][tile], stage sets
+  auto read = [&](V (&av)[G3_NP][2], V (&bv)[G3_NP][2], int buf) {
 #pragma unroll
-    for (int pl = 0; pl < 3; ++pl)
+    for (int pl = 0; pl < G3_NP; ++pl)
 #pragma unroll
       for (int t = 0; t < 2; ++t) {
         av[pl][t] = __builtin_bit_cast(V, *reinterpret_cast<const mg_u16x8*>(&SA[buf][pl][(rA + 32 * t) * G3_KC + so]));
         bv[pl][t] = __builtin_bit_cast(V, *reinterpret_cast<const mg_u16x8*>(&SB[buf][pl][(rB + 32 * t) * G3_KC + so]));
       }
   };
-  // the six products of a k-step, small terms first (planes (2,0) (1,1) (0,2) (1,0) (0,1)
-  // (0,0)), each over the four tiles in turn so that consecutive MFMAs use different
-  // accumulators
-  constexpr int PA[6] = {2, 1, 0, 1, 0, 0}, PB[6] = {0, 1, 2, 0, 1, 0};
+  // the three products of a k-step, small terms first (planes (1,0) (0,1) (0,0)), each
+  // over the four tiles in turn so that consecutive MFMAs use different accumulators
+  constexpr int PA[3] = {1, 0, 0}, PB[3] = {0, 1, 0};
 #define G3_ONE(AV, BV, n)                                                                    \
-  acc[((n) & 3) >> 1][(n) & 1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(                     \
+  acc[((n) & 3) >> 1][(n) & 1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(                      \
       AV[PA[(n) >> 2]][((n) & 3) >> 1], BV[PB[(n) >> 2]][(n) & 1], acc[((n) & 3) >> 1][(n) & 1], \
       0, 0, 0);
   auto sync = [&]() {
@@ -360,7 +435,7 @@ __device__ __forceinline__ void gemm3_tile(const G3Args& g0, G3Stage& SA, G3Stag
   // so that is "at most stage st + 2's loads outstanding") and this wave's reads of stage
   // st are done; after the barrier no wave reads buffer st % 3 any more.  Then the reads
   // of stage st + 1 are issued, and stage st's MFMAs run with the loads of stage st + 3
-  // into buffer st % 3 in between (one after every fourth MFMA).
+  // into buffer st % 3 in between (one after every third MFMA).
 #define G3_STAGE(XA, XB, YA, YB, ST)                                                       \
   {                                                                                        \
     const int st_ = (ST);                                                                  \
@@ -371,10 +446,10 @@ __device__ __forceinline__ void gemm3_tile(const G3Args& g0, G3Stage& SA, G3Stag
     __builtin_amdgcn_sched_barrier(0);                                                     \
     const int64_t kn = kbeg + (int64_t)(st_ + G3_NB) * G3_KC;                              \
     const bool live = st_ + G3_NB < nst;                                                   \
-    _Pragma("unroll") for (int n = 0; n < 24; ++n) {                                       \
+    _Pragma("unroll") for (int n = 0; n < 12; ++n) {                                       \
       G3_ONE(XA, XB, n)                                                                    \
-      if ((n & 3) == 3) {                                                                  \
-        dma_one(n >> 2, kn, cb, live);                                                     \
+      if (n % 3 == 2) {                                                                    \
+        dma_one(n / 3, kn, cb, live);                                                      \
         __builtin_amdgcn_sched_barrier(0);                                                 \
       }                                                                                    \
     }                                                                                      \
@@ -385,6 +460,23 @@ __device__ __forceinline__ void gemm3_tile(const G3Args& g0, G3Stage& SA, G3Stag
   }
 #undef G3_STAGE
 #undef G3_ONE
+  // undo the row scales: acc (1 / s_r) (1 / s_c), exact (powers of two)
+  {
+    const __amdgpu_buffer_rsrc_t sa = plane_scales(g.A, g.M, g.Kp);
+    const __amdgpu_buffer_rsrc_t sb = plane_scales(g.B, g.N, g.Kp);
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+      const int64_t cc = c0 + mg_col<MG_T>(b);
+      const float vc = scale_at(sb, cc, cc < g.N);
+#pragma unroll
+      for (int a = 0; a < 2; ++a)
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+          const int64_t rr = r0 + mg_row<MG_T>(a, j);
+          acc[a][b][j] = (acc[a][b][j] * scale_at(sa, rr, rr < g.M)) * vc;
+        }
+    }
+  }
   const CTile<MG_T> ct(g.C, g.ldc, g.M, g.N, r0, c0);
   f32x16 cv[2][2];
   if (g.beta != 0.0f) {
@@ -459,20 +551,18 @@ __global__ __launch_bounds__(256, 2) void gemm3_pair_kernel(G3Args g1, int64_t t
 }
 
 // The same product on 256 x 256 tiles for the largest grids: one workgroup of 8 waves per
-// CU, each wave 128 x 64 (4 x 2 accumulators), on the planes' three-stage ring of 48 KB
-// stages.  Per 16 k a wave reads 18 fragment planes for 48 MFMAs (gemm3_kernel: 12 for 24)
-// and the CU brings 48 KB into LDS per 16 k of a 256 x 256 tile (gemm3_kernel: 2 x 24 KB
-// per 16 k of two 128 x 128 tiles), half the LDS and L2 traffic per MFMA.  The next
-// stage's planes are read as the current stage's die (the six terms run small first:
-// A's plane 2 is dead after the first term, B's plane 2 after the third, ...), so two
-// waves per SIMD fit.  Each output element accumulates the same terms in the same order
-// as in gemm3_kernel (a 256-tile may run some stages more than a 128-tile of it, whose
-// masked planes add exact zeros).
+// CU, each wave 128 x 64 (4 x 2 accumulators), on the planes' three-stage ring of 32 KB
+// stages.  Per 16 k a wave reads 12 fragment planes for 24 MFMAs (gemm3_kernel: 8 for 12)
+// and the CU brings 32 KB into LDS per 16 k of a 256 x 256 tile (gemm3_kernel: 2 x 16 KB
+// per 16 k of two 128 x 128 tiles), half the LDS and L2 traffic per MFMA.  Each output
+// element accumulates the same terms in the same order as in gemm3_kernel (a 256-tile may
+// run some stages more than a 128-tile of it, whose masked planes add exact zeros) and
+// is scaled the same way.
 constexpr int GX_T = 256;                // tile edge
 constexpr int GX_SUP = 4;                // super-tile edge of the balanced schedule (tiles)
-constexpr int GX_PL = GX_T * G3_KC;      // bf16 per plane per stage
+constexpr int GX_PL = GX_T * G3_KC;      // fp16 per plane per stage
 
-typedef uint16_t GxStage[G3_NB][3][GX_PL];
+typedef uint16_t GxStage[G3_NB][G3_NP][GX_PL];
 
 // Output tile (tr, tc) of the product (SA, SB: the workgroup's LDS rings).
 template <int AMODE, int BMODE, bool CLOW>
@@ -499,11 +589,11 @@ __device__ __forceinline__ void gemm3x_tile(const G3Args& g0, GxStage& SA, GxSta
   const int rowsA = (int)((g.M - r0 < GX_T) ? g.M - r0 : GX_T);
   const int rowsB = (int)((g.N - c0 < GX_T) ? g.N - c0 : GX_T);
   const int64_t plA = g.M * g.Kp, plB = g.N * g.Kp;
-  // load j (0..5) of a stage: operand j / 3, plane j % 3, rows 32 wv .. 32 wv + 31 (the
+  // load j (0..3) of a stage: operand j / 2, plane j % 2, rows 32 wv .. 32 wv + 31 (the
   // slot swizzle of gemm3_kernel)
   const int prow = lane >> 1, piece = (lane & 1) ^ ((lane >> 4) & 1);
   auto dma_one = [&](int j, int64_t k0, int buf, bool live) {
-    const int opd = j / 3, pl = j % 3;
+    const int opd = j / G3_NP, pl = j % G3_NP;
     const int row = 32 * wv + prow;
     const uint16_t* base = opd == 0 ? g.A + pl * plA + ((k0 >> 4) * g.M + r0) * G3_KC
                                     : g.B + pl * plB + ((k0 >> 4) * g.N + c0) * G3_KC;
@@ -517,23 +607,23 @@ __device__ __forceinline__ void gemm3x_tile(const G3Args& g0, GxStage& SA, GxSta
   // 32 tb + lane % 32, piece lane / 32 in slot h ^ ((row / 8) % 2)
   const int so = 8 * ((lane >> 5) ^ ((lane >> 3) & 1));
   const int rA = wr * 128 + (lane & 31), rB = wc * 64 + (lane & 31);
-  typedef mg_bf16x8 V;
-  auto rdA = [&](V (&av)[3][4], int pl, int buf) {
+  typedef mg_f16x8 V;
+  auto rdA = [&](V (&av)[G3_NP][4], int pl, int buf) {
 #pragma unroll
     for (int t = 0; t < 4; ++t)
       av[pl][t] = __builtin_bit_cast(V, *reinterpret_cast<const mg_u16x8*>(&SA[buf][pl][(rA + 32 * t) * G3_KC + so]));
   };
-  auto rdB = [&](V (&bv)[3][2], int pl, int buf) {
+  auto rdB = [&](V (&bv)[G3_NP][2], int pl, int buf) {
 #pragma unroll
     for (int t = 0; t < 2; ++t)
       bv[pl][t] = __builtin_bit_cast(V, *reinterpret_cast<const mg_u16x8*>(&SB[buf][pl][(rB + 32 * t) * G3_KC + so]));
   };
-  constexpr int PA[6] = {2, 1, 0, 1, 0, 0}, PB[6] = {0, 1, 2, 0, 1, 0};
-  auto term = [&](auto P, const V (&av)[3][4], const V (&bv)[3][2]) {
+  constexpr int PA[3] = {1, 0, 0}, PB[3] = {0, 1, 0};
+  auto term = [&](auto P, const V (&av)[G3_NP][4], const V (&bv)[G3_NP][2]) {
     constexpr int pr = decltype(P)::value;
 #pragma unroll
     for (int i = 0; i < 8; ++i)
-      acc[i >> 1][i & 1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+      acc[i >> 1][i & 1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
           av[PA[pr]][i >> 1], bv[PB[pr]][i & 1], acc[i >> 1][i & 1], 0, 0, 0);
   };
   auto sync = [&]() {
@@ -543,7 +633,7 @@ __device__ __forceinline__ void gemm3x_tile(const G3Args& g0, GxStage& SA, GxSta
   };
   const int nst = kend > kbeg ? (int)((kend - kbeg + G3_KC - 1) / G3_KC) : 0;
   const int nst2 = (nst + 1) & ~1;
-  V a0[3][4], b0[3][2], a1[3][4], b1[3][2];  // [plane][tile], stage sets 0 and 1
+  V a0[G3_NP][4], b0[G3_NP][2], a1[G3_NP][4], b1[G3_NP][2];  // [plane][tile], stage sets
   if (nst > 0) {
 #pragma unroll
     for (int p = 0; p < G3_NB; ++p) {
@@ -553,46 +643,36 @@ __device__ __forceinline__ void gemm3x_tile(const G3Args& g0, GxStage& SA, GxSta
     __builtin_amdgcn_s_waitcnt(g3_waitcnt(2 * G3_PER_STAGE, 15));  // stage 0 landed
     sync();
 #pragma unroll
-    for (int pl = 0; pl < 3; ++pl) {
+    for (int pl = 0; pl < G3_NP; ++pl) {
       rdA(a0, pl, 0);
       rdB(b0, pl, 0);
     }
   }
   // Stage st (planes x): wait until stage st + 1 has landed and every wave's reads of
-  // stage st (made during stage st - 1) are done, then the six terms, each followed by
-  // one DMA of stage st + 3 into buffer st % 3 and the reads of the next stage's planes
-  // that the terms so far have freed (B0 first, then A2, B2 and A0, A1, B1).
-  auto stage = [&](const V (&xa)[3][4], const V (&xb)[3][2], V (&ya)[3][4], V (&yb)[3][2],
-                   int st) {
+  // stage st (made during stage st - 1) are done, then the reads of the next stage and
+  // the three terms, with the four DMAs of stage st + 3 into buffer st % 3 between them.
+  auto stage = [&](const V (&xa)[G3_NP][4], const V (&xb)[G3_NP][2], V (&ya)[G3_NP][4],
+                   V (&yb)[G3_NP][2], int st) {
     const int cb = st % G3_NB, nb = (st + 1) % G3_NB;
     __builtin_amdgcn_s_waitcnt(g3_waitcnt(G3_PER_STAGE, 0));
     sync();
-    rdB(yb, 0, nb);
+#pragma unroll
+    for (int pl = 0; pl < G3_NP; ++pl) {
+      rdB(yb, pl, nb);
+      rdA(ya, pl, nb);
+    }
     __builtin_amdgcn_sched_barrier(0);
     const int64_t kn = kbeg + (int64_t)(st + G3_NB) * G3_KC;
     const bool live = st + G3_NB < nst;
     term(std::integral_constant<int, 0>{}, xa, xb);
     dma_one(0, kn, cb, live);
-    rdA(ya, 2, nb);
     __builtin_amdgcn_sched_barrier(0);
     term(std::integral_constant<int, 1>{}, xa, xb);
     dma_one(1, kn, cb, live);
+    dma_one(2, kn, cb, live);
     __builtin_amdgcn_sched_barrier(0);
     term(std::integral_constant<int, 2>{}, xa, xb);
-    dma_one(2, kn, cb, live);
-    rdB(yb, 2, nb);
-    rdA(ya, 0, nb);
-    __builtin_amdgcn_sched_barrier(0);
-    term(std::integral_constant<int, 3>{}, xa, xb);
     dma_one(3, kn, cb, live);
-    rdA(ya, 1, nb);
-    __builtin_amdgcn_sched_barrier(0);
-    term(std::integral_constant<int, 4>{}, xa, xb);
-    dma_one(4, kn, cb, live);
-    rdB(yb, 1, nb);
-    __builtin_amdgcn_sched_barrier(0);
-    term(std::integral_constant<int, 5>{}, xa, xb);
-    dma_one(5, kn, cb, live);
     __builtin_amdgcn_sched_barrier(0);
   };
   for (int st = 0; st < nst2; st += 2) {
@@ -603,10 +683,13 @@ __device__ __forceinline__ void gemm3x_tile(const G3Args& g0, GxStage& SA, GxSta
   // 4 (lane / 32) + j % 4, column wc * 64 + 32 tb + lane % 32; rows and columns outside
   // C, and with CLOW the elements above the diagonal, are left alone
   const __amdgpu_buffer_rsrc_t rc = mg_rsrc(g.C + r0 * g.ldc + c0, (int64_t)(rowsA - 1) * g.ldc + rowsB);
+  const __amdgpu_buffer_rsrc_t sa = plane_scales(g.A, g.M, g.Kp);
+  const __amdgpu_buffer_rsrc_t sb = plane_scales(g.B, g.N, g.Kp);
   const int lr0 = wr * 128 + 4 * (lane >> 5), lc0 = wc * 64 + (lane & 31);
 #pragma unroll
   for (int tb = 0; tb < 2; ++tb) {
     const int cc = lc0 + 32 * tb;
+    const float vc = scale_at(sb, c0 + cc, cc < rowsB);
 #pragma unroll
     for (int ta = 0; ta < 4; ++ta)
 #pragma unroll
@@ -614,7 +697,8 @@ __device__ __forceinline__ void gemm3x_tile(const G3Args& g0, GxStage& SA, GxSta
         const int rr = lr0 + 32 * ta + 8 * (j >> 2) + (j & 3);
         const bool ok = rr < rowsA && cc < rowsB && (!CLOW || c0 + cc <= r0 + rr);
         const uint32_t o = ok ? (uint32_t)(((int64_t)rr * g.ldc + cc) * 4) : MG_OOB;
-        const float x = acc[ta][tb][j];
+        // undo the row scales: acc (1 / s_r) (1 / s_c), exact (powers of two)
+        const float x = (acc[ta][tb][j] * scale_at(sa, r0 + rr, rr < rowsA)) * vc;
         float v = g.alpha * x;
         if (g.beta != 0.0f)
           v = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rc, (int)o, 0, 0)) + v;
@@ -672,13 +756,29 @@ __global__ __launch_bounds__(512, 1) void gemm3x_pair_kernel(G3Args g1, int64_t 
   }
 }
 
-int split3(const float* X, int64_t ldx, int64_t R, int64_t Kk, int trans, int mask,
+// The planes of an operand (split2_kernel's layout at out, batch stride sout): the row
+// maxima first, then the scaled split.  out holds 2 R Kp fp16 then (1 + G2_NS) R floats,
+// within the 3 R Kp fp16 a plane buffer holds (Kp >= 34).
+int split2(const float* X, int64_t ldx, int64_t R, int64_t Kk, int trans, int mask,
            uint16_t* out, int64_t Kp, hipStream_t s, int batch = 1, int64_t sx = 0,
            int64_t sout = 0) {
+  if (R <= 0) return HI2X_OK;
+  if (Kp < 2 * (1 + G2_NS)) {  // split products have ranks in the hundreds at least
+    set_error("split2: rank %lld too small for the scale partials", (long long)Kp);
+    return HI2X_EINVAL;
+  }
+  float* pm = reinterpret_cast<float*>(out + G3_NP * R * Kp) + R;
+  {
+    const dim3 gm((unsigned)G2_NS, (unsigned)(trans ? (R + 63) / 64 : (R + 3) / 4), (unsigned)batch);
+    hipLaunchKernelGGL(rowmax_kernel, gm, dim3(256), 0, s, X, ldx, R, Kk, trans, mask, pm, sx,
+                       sout / 2);
+    const int rc = launch_status("rowmax_kernel");
+    if (rc) return rc;
+  }
   const dim3 grid((unsigned)((Kp + 63) / 64), (unsigned)((R + 63) / 64), (unsigned)batch);
-  hipLaunchKernelGGL(split3_kernel, grid, dim3(256), 0, s, X, ldx, R, Kk, trans, mask, out, Kp,
+  hipLaunchKernelGGL(split2_kernel, grid, dim3(256), 0, s, X, ldx, R, Kk, trans, mask, out, Kp,
                      sx, sout);
-  return launch_status("split3_kernel");
+  return launch_status("split2_kernel");
 }
 
 template <int AMODE, int BMODE, bool CLOW>
@@ -1552,11 +1652,11 @@ int product(const Ctx& c, GemmArgs a) {
   uint16_t* pa = reinterpret_cast<uint16_t*>(c.ws + c.plan->pa_off);
   uint16_t* pb = reinterpret_cast<uint16_t*>(c.ws + c.plan->pb_off);
   const int64_t sPl = 2 * c.sW;  // planes live in the workspace (bf16 elements)
-  int rc = split3(a.A, a.lda, a.M, a.Kd, 0, AMODE == 1 ? 1 : 0, pa, Kp, c.s, c.batch, a.sA, sPl);
+  int rc = split2(a.A, a.lda, a.M, a.Kd, 0, AMODE == 1 ? 1 : 0, pa, Kp, c.s, c.batch, a.sA, sPl);
   if (rc) return rc;
   const uint16_t* bp = pa;
   if (!(TB && a.B == a.A && a.ldb == a.lda && a.N == a.M && AMODE == 0 && BMODE == 0)) {
-    rc = split3(a.B, a.ldb, a.N, a.Kd, TB ? 0 : 1, split_mask_b(BMODE), pb, Kp, c.s, c.batch,
+    rc = split2(a.B, a.ldb, a.N, a.Kd, TB ? 0 : 1, split_mask_b(BMODE), pb, Kp, c.s, c.batch,
                 a.sB, sPl);
     if (rc) return rc;
     bp = pb;
@@ -1591,9 +1691,9 @@ int product_pair(const Ctx& c, GemmArgs upd, GemmArgs t2) {
     uint16_t* pa = reinterpret_cast<uint16_t*>(c.ws + c.plan->pa_off);
     uint16_t* pb = reinterpret_cast<uint16_t*>(c.ws + c.plan->pb_off);
     const int64_t sPl = 2 * c.sW;
-    int rc = split3(upd.A, upd.lda, upd.M, upd.Kd, 0, 0, pa, Kp, c.s, c.batch, upd.sA, sPl);
+    int rc = split2(upd.A, upd.lda, upd.M, upd.Kd, 0, 0, pa, Kp, c.s, c.batch, upd.sA, sPl);
     if (rc) return rc;
-    rc = split3(t2.B, t2.ldb, t2.N, t2.Kd, 1, split_mask_b(1), pb, Kp, c.s, c.batch, t2.sB, sPl);
+    rc = split2(t2.B, t2.ldb, t2.N, t2.Kd, 1, split_mask_b(1), pb, Kp, c.s, c.batch, t2.sB, sPl);
     if (rc) return rc;
     G3Args g1{pa, pa, upd.C, upd.M, upd.N, upd.Kd, Kp, upd.ldc, upd.alpha, upd.beta};
     G3Args g2{pa, pb, t2.C, t2.M, t2.N, t2.Kd, Kp, t2.ldc, t2.alpha, t2.beta};
