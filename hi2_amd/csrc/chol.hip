@@ -206,10 +206,14 @@ __device__ __forceinline__ bool split_keep(int mask, int64_t r, int64_t k) {
   return mask == 1 ? k <= r : (mask == 2 ? k >= r : true);
 }
 
-// Grid (G2_NS, row groups): slice s covers k in [s L, (s + 1) L), L = ceil(Kk / G2_NS).
-// !trans (operand rows contiguous): one wave per row, lanes along k; trans (operand rows
-// are columns of X): 64 rows per workgroup, lanes along the row index, the four waves
-// taking every fourth k, combined through LDS.  mask as in split2_kernel.
+// Grid (G2_NS, row groups): slice s covers k in [s L, (s + 1) L), L = ceil(Kk / G2_NS)
+// rounded up to a multiple of 256.  !trans (operand rows contiguous): one wave per row,
+// each lane 16-byte pieces along k; trans (operand rows are columns of X): 256 rows per
+// workgroup, each lane a 16-byte piece of 4 rows, the four waves taking every fourth k,
+// combined through LDS.  Loads go through buffer resources that end at the last valid
+// element (past it they read zero).  VEC: X and ldx allow 16-byte pieces (else 4-byte
+// loads).  mask as in split2_kernel.
+template <bool VEC>
 __global__ __launch_bounds__(256) void rowmax_kernel(const float* __restrict__ X, int64_t ldx,
                                                      int64_t R, int64_t Kk, int trans, int mask,
                                                      float* __restrict__ pm, int64_t sx,
@@ -217,33 +221,62 @@ __global__ __launch_bounds__(256) void rowmax_kernel(const float* __restrict__ X
   X += (int64_t)blockIdx.z * sx;
   pm += (int64_t)blockIdx.z * spm;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int64_t L = (Kk + G2_NS - 1) / G2_NS;
+  const int64_t L = ((Kk + G2_NS - 1) / G2_NS + 255) / 256 * 256;
   const int64_t ks = (int64_t)blockIdx.x * L;
   const int64_t ke = (ks + L < Kk) ? ks + L : Kk;
-  float m = 0.0f;  // fmaxf skips NaN elements
+  float m[4] = {0.0f, 0.0f, 0.0f, 0.0f};  // fmaxf skips NaN elements
+  auto take = [&](int i, float x, int64_t r, int64_t k) {
+    m[i] = (k < ke && split_keep(mask, r, k)) ? fmaxf(m[i], fabsf(x)) : m[i];
+  };
   if (!trans) {
     const int64_t r = (int64_t)blockIdx.y * 4 + wave;
     if (r >= R) return;
-    const float* x = X + r * ldx;
-    for (int64_t k = ks + lane; k < ke; k += 64)
-      m = split_keep(mask, r, k) ? fmaxf(m, fabsf(x[k])) : m;
+    if (ks < ke) {
+      const __amdgpu_buffer_rsrc_t rs = mg_rsrc(X + r * ldx + ks, ke - ks);
+      for (int64_t k0 = 0; k0 < ke - ks; k0 += 256) {
+        const int64_t k = k0 + 4 * lane;
+        if (VEC) {
+          const f32x4 v = mg_load4(rs, (uint32_t)(k * 4));
 #pragma unroll
-    for (int sh = 32; sh >= 1; sh >>= 1) m = fmaxf(m, __shfl_xor(m, sh));
-    if (lane == 0) pm[blockIdx.x * R + r] = m;
+          for (int i = 0; i < 4; ++i) take(i, v[i], r, ks + k + i);
+        } else {
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            take(i, __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, (int)((k + i) * 4), 0, 0)), r, ks + k + i);
+        }
+      }
+    }
+    float mm = fmaxf(fmaxf(m[0], m[1]), fmaxf(m[2], m[3]));
+#pragma unroll
+    for (int sh = 32; sh >= 1; sh >>= 1) mm = fmaxf(mm, __shfl_xor(mm, sh));
+    if (lane == 0) pm[blockIdx.x * R + r] = mm;
     return;
   }
-  __shared__ float part[4][64];
-  const int64_t r = (int64_t)blockIdx.y * 64 + lane;
-  if (r < R) {
+  __shared__ float part[4][256];
+  const int64_t rb = (int64_t)blockIdx.y * 256, r = rb + 4 * lane;
+  const int nr = (int)((R - rb < 256) ? R - rb : 256);
+  if (ks < ke) {
+    const __amdgpu_buffer_rsrc_t rs = mg_rsrc(X + ks * ldx + rb, (ke - ks - 1) * ldx + nr);
 #pragma unroll 8
-    for (int64_t k = ks + wave; k < ke; k += 4)
-      m = split_keep(mask, r, k) ? fmaxf(m, fabsf(X[k * ldx + r])) : m;
+    for (int64_t k = wave; k < ke - ks; k += 4) {
+      const uint32_t o = 4 * lane < nr ? (uint32_t)((k * ldx + 4 * lane) * 4) : MG_OOB;
+      if (VEC) {
+        const f32x4 v = mg_load4(rs, o);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) take(i, v[i], r + i, ks + k);
+      } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          take(i, __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, o == MG_OOB ? (int)MG_OOB : (int)(o + 4 * i), 0, 0)), r + i, ks + k);
+      }
+    }
   }
-  part[wave][lane] = m;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) part[wave][4 * lane + i] = m[i];
   __syncthreads();
-  if (wave == 0 && r < R)
-    pm[blockIdx.x * R + r] = fmaxf(fmaxf(part[0][lane], part[1][lane]),
-                                   fmaxf(part[2][lane], part[3][lane]));
+  const int c = threadIdx.x;
+  if (c < nr)
+    pm[blockIdx.x * R + rb + c] = fmaxf(fmaxf(part[0][c], part[1][c]), fmaxf(part[2][c], part[3][c]));
 }
 
 // Planes of R x Kp fp16 from X, each stored in chunks of 16 k: element (r, k) of plane p
@@ -769,9 +802,14 @@ int split2(const float* X, int64_t ldx, int64_t R, int64_t Kk, int trans, int ma
   }
   float* pm = reinterpret_cast<float*>(out + G3_NP * R * Kp) + R;
   {
-    const dim3 gm((unsigned)G2_NS, (unsigned)(trans ? (R + 63) / 64 : (R + 3) / 4), (unsigned)batch);
-    hipLaunchKernelGGL(rowmax_kernel, gm, dim3(256), 0, s, X, ldx, R, Kk, trans, mask, pm, sx,
-                       sout / 2);
+    const dim3 gm((unsigned)G2_NS, (unsigned)(trans ? (R + 255) / 256 : (R + 3) / 4), (unsigned)batch);
+    const bool vec = (reinterpret_cast<uintptr_t>(X) & 15) == 0 && ldx % 4 == 0 && sx % 4 == 0;
+    if (vec)
+      hipLaunchKernelGGL(rowmax_kernel<true>, gm, dim3(256), 0, s, X, ldx, R, Kk, trans, mask, pm,
+                         sx, sout / 2);
+    else
+      hipLaunchKernelGGL(rowmax_kernel<false>, gm, dim3(256), 0, s, X, ldx, R, Kk, trans, mask,
+                         pm, sx, sout / 2);
     const int rc = launch_status("rowmax_kernel");
     if (rc) return rc;
   }
