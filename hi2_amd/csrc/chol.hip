@@ -1675,16 +1675,22 @@ struct Ctx {
 // op(B) mask of a TB / !TB product in split coordinates (row = output column j, k)
 constexpr int split_mask_b(int bmode) { return bmode == 1 ? 2 : (bmode == 2 ? 1 : 0); }
 
+// Whether a product runs through the split planes: grids of at least 128 tiles of 128,
+// a lower-triangular output from 96 (14 x 14 tiles: the fp16 split's three MFMAs per 16 k
+// on 105 tiles beat the fp32 MFMA's 406 tiles of 64).
+static bool split_worth(int64_t tm, int64_t tn, bool clow) {
+  return clow ? tm * (tm + 1) / 2 >= 96 : tm * tn >= 128;
+}
+
 // One product of the recursion: the big grids through the split planes, the small ones
 // on the fp32 MFMA GEMM.
 template <int AMODE, int BMODE, bool TB, bool CLOW>
 int product(const Ctx& c, GemmArgs a) {
   const int64_t tm = (a.M + MG_T - 1) / MG_T, tn = (a.N + MG_T - 1) / MG_T;
-  const int64_t ntiles = tm * tn;
   a.sA = c.stride(a.A);
   a.sB = c.stride(a.B);
   a.sC = c.stride(a.C);
-  if (!chol_split() || (CLOW ? ntiles / 2 : ntiles) < 128)
+  if (!chol_split() || !split_worth(tm, tn, CLOW))
     return tri_gemm<AMODE, BMODE, TB, CLOW>(a, c.s, c.batch);
   const int64_t Kp = (a.Kd + G3_KA - 1) / G3_KA * G3_KA;
   uint16_t* pa = reinterpret_cast<uint16_t*>(c.ws + c.plan->pa_off);
@@ -1710,7 +1716,7 @@ int product(const Ctx& c, GemmArgs a) {
 // 128, or 0 when it takes the fp32 path.
 static int split_tile(const GemmArgs& a, bool clow) {
   const int64_t tm = (a.M + MG_T - 1) / MG_T, tn = (a.N + MG_T - 1) / MG_T;
-  if (!chol_split() || (clow ? tm * tn / 2 : tm * tn) < 128) return 0;
+  if (!chol_split() || !split_worth(tm, tn, clow)) return 0;
   const int64_t tm2 = (a.M + GX_T - 1) / GX_T, tn2 = (a.N + GX_T - 1) / GX_T;
   return ((clow ? tm2 * (tm2 + 1) / 2 : tm2 * tn2) >= 256 && chol_tile256()) ? GX_T : MG_T;
 }
