@@ -630,6 +630,33 @@ def test_inverse_factor_inverts_large(dev):
     assert err < 5e-3, err
 
 
+def test_inverse_factor_wide_channel_scales(dev):
+    """K = 4096 with channel scales 2^u, u uniform in [-40, 40] (Hessian entries over a
+    range of 2^160): the big products' operand rows are split into fp16 planes after a
+    power-of-two row scale, so every row of U keeps fp32-level accuracy relative to its
+    own largest element.  Reference: the float64 inverse Cholesky factor of the same
+    damped matrix (torch.linalg on the device)."""
+    from hi2_amd.hessian import inverse_factor
+
+    k, spread = 4096, 40
+    g = torch.Generator(device=dev).manual_seed(5)
+    x = torch.randn(2 * k, k, device=dev, generator=g, dtype=torch.float64)
+    x = x * torch.exp(0.5 * torch.randn(1, k, device=dev, generator=g, dtype=torch.float64))
+    h0 = x.T @ x / x.shape[0]
+    del x
+    dsc = torch.exp2(torch.randint(-spread, spread + 1, (k,), device=dev, generator=g).double())
+    h = (dsc[:, None] * h0 * dsc[None, :]).float().contiguous()
+    u = inverse_factor(h, 0.01).double()
+    hd = h.double()
+    hd = hd + 0.01 * torch.diagonal(hd).mean() * torch.eye(k, device=dev, dtype=torch.float64)
+    rev = torch.arange(k - 1, -1, -1, device=dev)
+    lo = torch.linalg.cholesky(hd[rev][:, rev])
+    eye = torch.eye(k, device=dev, dtype=torch.float64)
+    u64 = torch.linalg.solve_triangular(lo, eye, upper=False)[rev][:, rev]
+    rel = ((u - u64).abs() / u64.abs().amax(dim=1, keepdim=True)).max().item()
+    assert rel < 1e-5, rel
+
+
 def test_inverse_factor_256_tiles_equal_128_tiles(dev, monkeypatch):
     """K = 8448: the top level's three rectangular products (17 x 17 tiles of 256, the
     last row and column of tiles partial) run on the 256-tile kernel; with
