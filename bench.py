@@ -113,6 +113,8 @@ _CHAIN_STREAMS = {}
 HEAD_START = os.environ.get("HI2_HEAD_START", "transform")
 # the critical chain's rotations and ladder fits on the last chain's stream (0: in place)
 OFFLOAD_PREP = os.environ.get("HI2_OFFLOAD_PREP", "1") != "0"
+# the other chains' streams marked background (hi2x_stream_background; 0: not marked)
+BACKGROUND = os.environ.get("HI2_BACKGROUND", "1") != "0"
 
 
 def _chain_stream(dev, i):
@@ -122,7 +124,12 @@ def _chain_stream(dev, i):
 
     key = (dev.index, i)
     if key not in _CHAIN_STREAMS:
-        _CHAIN_STREAMS[key] = torch.cuda.Stream(device=dev)
+        st = torch.cuda.Stream(device=dev)
+        if i > 0 and BACKGROUND:  # every chain but the first (the critical path)
+            from hi2_amd import _lib
+
+            _lib.stream_background(st)
+        _CHAIN_STREAMS[key] = st
     return _CHAIN_STREAMS[key]
 
 

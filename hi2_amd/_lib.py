@@ -32,6 +32,7 @@ SIGNATURES = {
     "hi2x_gptq_trailing": [_P, _I64, _I64, _I64, _I64, _P, _I64, _I64, _I64, _P, _P, _P],
     "hi2x_gptq_run": [_P, _I64, _I64, _P, _P, _P, _I64, _P, _P, _P, _P, _P, _P, _I64, _P],
     "hi2x_gptq_run_noalloc": [_P, _I64, _I64, _P, _P, _P, _I64, _P, _P, _P, _P, _P, _I64, _P],
+    "hi2x_stream_background": [_P, _I],
     "hi2x_ladder_fit": [_P, _P, _I64, _I64, _I64, _I, _P, _I, _I, _P, _P, _P, _P],
     "hi2x_params": [_P, _P, _I64, _I64, _P, _P, _P, _P, _P, _I64, _P],
     "hi2x_decode_params": [_P, _P, _P, _I64, _I64, _P, _P, _P],
@@ -162,6 +163,14 @@ def timing_query(kind: int) -> tuple[int, float, float]:
     check(lib().hi2x_timing_query(kind, ctypes.byref(n), ctypes.byref(ms), ctypes.byref(work)),
           "hi2x_timing_query")
     return n.value, ms.value, work.value
+
+
+def stream_background(st: torch.cuda.Stream, on: bool = True) -> None:
+    """Mark (or unmark) ``st`` as a background stream: the GPTQ cross-block updates
+    launched on it leave room on each CU for the latency-bound kernels of other streams
+    (``hi2x_stream_background``; results are unchanged)."""
+    check(lib().hi2x_stream_background(ctypes.c_void_p(st.cuda_stream), int(bool(on))),
+          "hi2x_stream_background")
 
 
 def last_error() -> str:

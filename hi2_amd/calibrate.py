@@ -255,8 +255,11 @@ def _on_device(reqs, cfg, ex, i: int, use_gptq, comp_full, pack=None):
     dev = _device(ex.devices[i])
     main = torch.cuda.current_stream(dev)
     lanes = [_lib.side_stream(dev, 64 + j) for j in range(LANES)]
-    for st in lanes:
+    for j, st in enumerate(lanes):
         st.wait_stream(main)
+        # lane 0 takes the widest input (the critical path): the others' GPTQ updates
+        # leave room on the CUs for its latency-bound kernels
+        _lib.stream_background(st, j > 0)
     groups: dict = {}  # factor key -> requests, in order of first appearance
     near: list[int] = []
     for ri, r in enumerate(reqs):

@@ -2,6 +2,7 @@
 #include <stdarg.h>
 #include <stdio.h>
 
+#include <algorithm>
 #include <atomic>
 #include <mutex>
 #include <vector>
@@ -73,9 +74,37 @@ LaunchTimer::~LaunchTimer() {
   g_timed.push_back(Timed{kind_, work_, e0_, e1});
 }
 
+// Streams marked as background (hi2x_stream_background): a short list, read on every
+// launch that consults it, written rarely.
+namespace {
+std::mutex g_bg_mu;
+std::vector<hipStream_t> g_bg;
+}  // namespace
+
+bool stream_background(hipStream_t s) {
+  std::lock_guard<std::mutex> lk(g_bg_mu);
+  for (hipStream_t b : g_bg)
+    if (b == s) return true;
+  return false;
+}
+
 }  // namespace hi2x
 
 using namespace hi2x;
+
+extern "C" int hi2x_stream_background(void* stream, int background) {
+  clear_error();
+  const hipStream_t s = as_stream(stream);
+  std::lock_guard<std::mutex> lk(g_bg_mu);
+  auto it = std::find(g_bg.begin(), g_bg.end(), s);
+  if (background && it == g_bg.end()) {
+    HI2X_REQUIRE(g_bg.size() < 256, "stream_background: more than 256 background streams");
+    g_bg.push_back(s);
+  } else if (!background && it != g_bg.end()) {
+    g_bg.erase(it);
+  }
+  return HI2X_OK;
+}
 
 extern "C" int hi2x_timing_enable(unsigned mask) {
   clear_error();

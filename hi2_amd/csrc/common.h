@@ -14,6 +14,11 @@ void clear_error();
 // Status of the last launch on this thread: HI2X_OK or HI2X_ELAUNCH (message set).
 int launch_status(const char* what);
 
+// Whether the caller marked stream s as background (hi2x_stream_background): kernels of
+// the many-workgroup GEMMs launched there hold more LDS per workgroup than they use, so
+// fewer of them share a CU and latency-bound kernels of other streams find room.
+bool stream_background(hipStream_t s);
+
 inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 
 // The cross-block update of gptq.hip on `s`, for other kernels' schedules:

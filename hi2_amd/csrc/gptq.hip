@@ -500,17 +500,21 @@ int launch_trailing(float* wc, int64_t n, int64_t k, int64_t i1, int nblk, const
   LaunchTimer timer(timing_kind, 2.0 * n * rank * (c1 - c0), s);
   // 128-tiles fill the chip from two rounds of its 512 workgroup slots on; smaller grids
   // (the near updates of a super-block) run on 64-tiles, four times as many workgroups
+  // on a background stream the workgroups hold unused LDS on top of their own (72 + 28 KB
+  // for 128-tiles: one per CU instead of two; 36 + 24 KB for 64-tiles: two instead of
+  // four), which leaves each CU room for another stream's small products or leaves
+  const bool bg = stream_background(s);
   const int64_t tn128 = (c1 - c0 + MG_T - 1) / MG_T, tm128 = (n + MG_T - 1) / MG_T;
   if (tn128 * tm128 >= 512) {
     const int64_t ntiles = tn128 * tm128;
     hipLaunchKernelGGL(gptq_trailing_kernel<MG_T>, dim3((unsigned)((ntiles + 7) / 8 * 8)),
-                       dim3(256), 0, s, wc, n, k, i1, nblk, err1, lde, c0, c1, row_grp, u_ptrs,
-                       tn128, ntiles, skip);
+                       dim3(256), bg ? 28 * 1024 : 0, s, wc, n, k, i1, nblk, err1, lde, c0, c1,
+                       row_grp, u_ptrs, tn128, ntiles, skip);
   } else {
     const int64_t tn = (c1 - c0 + 63) / 64, tm = (n + 63) / 64, ntiles = tn * tm;
     hipLaunchKernelGGL(gptq_trailing_kernel<64>, dim3((unsigned)((ntiles + 7) / 8 * 8)),
-                       dim3(256), 0, s, wc, n, k, i1, nblk, err1, lde, c0, c1, row_grp, u_ptrs,
-                       tn, ntiles, skip);
+                       dim3(256), bg ? 24 * 1024 : 0, s, wc, n, k, i1, nblk, err1, lde, c0, c1,
+                       row_grp, u_ptrs, tn, ntiles, skip);
   }
   return launch_status("gptq_trailing_kernel");
 }

@@ -426,6 +426,19 @@ int hi2x_qad_decode_bwd(const float* grad, const float* latent, const float* uni
 int hi2x_qad_wht_scale(const float* x, int64_t n_rows, int64_t k, const uint8_t* flags,
                        const uint16_t* scale, int pre_div, float* out, void* stream);
 
+/* ---- streams ---------------------------------------------------------------------------- */
+
+/* Background hint for a stream.  No counterpart in the reference (its encode runs one
+ * input at a time on the CPU); it is for callers that run independent encodes on several
+ * streams of one GPU, where one of them is the critical path.  With background != 0 the
+ * GPTQ cross-block updates (hi2x_gptq_run, hi2x_gptq_trailing) launched on `stream`
+ * reserve more LDS per workgroup than they use, so fewer of their workgroups share a CU
+ * and the latency-bound kernels of the other streams (the factor's small products and
+ * leaves) find room; background 0 clears the mark.  Results are unchanged.
+ * Process-wide; marks streams by handle (a destroyed stream's handle may be reused:
+ * clear the mark first). */
+int hi2x_stream_background(void* stream, int background);
+
 /* ---- measurement ------------------------------------------------------------------------ */
 
 /* Launch-timing hook.  No counterpart in the reference (whose profiling is host-side

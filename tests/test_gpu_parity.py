@@ -151,6 +151,36 @@ def test_super_block_schedule_is_bit_identical(dev, sb):
         assert torch.equal(getattr(got, f), getattr(ref, f)), f
 
 
+def test_background_stream_leaves_results_unchanged(dev):
+    """hi2x_stream_background only changes how many of the cross-block update's
+    workgroups share a CU: the same job on a background stream gives the same bits.
+    4096 rows x 4096 columns, so the far updates take the 128-tile path and the near
+    ones the 64-tile path."""
+    from hi2_amd import _lib
+    from hi2_amd.hessian import GptqJob, encode_jobs_gptq, inverse_factor
+
+    k, n = 4096, 4096
+    g = torch.Generator(device=dev).manual_seed(21)
+    x = torch.randn(2 * k, k, device=dev, generator=g)
+    hs = (x.T @ x / x.shape[0]).contiguous()
+    del x
+    u = inverse_factor(hs, 0.01)
+    w = torch.randn(n, k, device=dev, generator=g) * 0.02
+    job = GptqJob(w, torch.diagonal(hs).clone(), u, 4, 64)
+    st = torch.cuda.Stream(device=dev)
+    st.wait_stream(torch.cuda.current_stream(dev))
+    try:
+        with torch.cuda.stream(st):
+            ref = encode_jobs_gptq([job], "normal", comp=True)[0]
+            _lib.stream_background(st)
+            got = encode_jobs_gptq([job], "normal", comp=True)[0]
+    finally:
+        _lib.stream_background(st, False)
+    torch.cuda.current_stream(dev).wait_stream(st)
+    for f in ("codes", "params", "consts", "sse", "comp"):
+        assert torch.equal(getattr(got, f), getattr(ref, f)), f
+
+
 def test_batched_jobs_match_one_call_each(dev, monkeypatch):
     # reference tests/test_gptq_fast.py:58-72: several row chunks and batches, two widths
     import hi2_amd.hessian as hm
