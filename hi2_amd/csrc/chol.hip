@@ -213,13 +213,32 @@ __device__ __forceinline__ bool split_keep(int mask, int64_t r, int64_t k) {
 // combined through LDS.  Loads go through buffer resources that end at the last valid
 // element (past it they read zero).  VEC: X and ldx allow 16-byte pieces (else 4-byte
 // loads).  mask as in split2_kernel.
+// One operand of a split: rows R of X (layouts as in split2_kernel) into the planes at out.
+struct SplitOp {
+  const float* X;
+  int64_t ldx, R, Kk, Kp, sx, sout;  // batch strides sx (floats) and sout (16-bit values)
+  int trans, mask;
+  uint16_t* out;
+};
+
+// The operand of this workgroup: grid rows below y0 belong to o0, the rest to o1 (two
+// operands of a product split by one launch); by is the row group within the operand.
+__device__ __forceinline__ SplitOp split_operand(const SplitOp& o0, const SplitOp& o1, int y0,
+                                                 int64_t& by) {
+  const bool second = (int)blockIdx.y >= y0;
+  by = second ? (int64_t)blockIdx.y - y0 : (int64_t)blockIdx.y;
+  return second ? o1 : o0;
+}
+
 template <bool VEC>
-__global__ __launch_bounds__(256) void rowmax_kernel(const float* __restrict__ X, int64_t ldx,
-                                                     int64_t R, int64_t Kk, int trans, int mask,
-                                                     float* __restrict__ pm, int64_t sx,
-                                                     int64_t spm) {
-  X += (int64_t)blockIdx.z * sx;
-  pm += (int64_t)blockIdx.z * spm;
+__global__ __launch_bounds__(256) void rowmax_kernel(SplitOp o0, SplitOp o1, int y0) {
+  int64_t by;
+  const SplitOp o = split_operand(o0, o1, y0, by);
+  const float* __restrict__ X = o.X + (int64_t)blockIdx.z * o.sx;
+  const int64_t ldx = o.ldx, R = o.R, Kk = o.Kk;
+  const int trans = o.trans, mask = o.mask;
+  float* __restrict__ pm =
+      reinterpret_cast<float*>(o.out + (int64_t)blockIdx.z * o.sout + G3_NP * R * o.Kp) + R;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int64_t L = ((Kk + G2_NS - 1) / G2_NS + 255) / 256 * 256;
   const int64_t ks = (int64_t)blockIdx.x * L;
@@ -229,7 +248,7 @@ __global__ __launch_bounds__(256) void rowmax_kernel(const float* __restrict__ X
     m[i] = (k < ke && split_keep(mask, r, k)) ? fmaxf(m[i], fabsf(x)) : m[i];
   };
   if (!trans) {
-    const int64_t r = (int64_t)blockIdx.y * 4 + wave;
+    const int64_t r = by * 4 + wave;
     if (r >= R) return;
     if (ks < ke) {
       const __amdgpu_buffer_rsrc_t rs = mg_rsrc(X + r * ldx + ks, ke - ks);
@@ -253,7 +272,7 @@ __global__ __launch_bounds__(256) void rowmax_kernel(const float* __restrict__ X
     return;
   }
   __shared__ float part[4][256];
-  const int64_t rb = (int64_t)blockIdx.y * 256, r = rb + 4 * lane;
+  const int64_t rb = by * 256, r = rb + 4 * lane;
   const int nr = (int)((R - rb < 256) ? R - rb : 256);
   if (ks < ke) {
     const __amdgpu_buffer_rsrc_t rs = mg_rsrc(X + ks * ldx + rb, (ke - ks - 1) * ldx + nr);
@@ -286,14 +305,16 @@ __global__ __launch_bounds__(256) void rowmax_kernel(const float* __restrict__ X
 // ld ldx), trans: x = X[k][r] (X is Kk x R).  mask 1 keeps k <= r, 2 keeps k >= r; k >= Kk
 // and masked elements are zero.  A workgroup converts a 64 x 64 block through LDS: 4
 // threads per output row, 16 consecutive k (one chunk row) each.
-__global__ __launch_bounds__(256) void split2_kernel(const float* __restrict__ X, int64_t ldx,
-                                                     int64_t R, int64_t Kk, int trans, int mask,
-                                                     uint16_t* __restrict__ out, int64_t Kp,
-                                                     int64_t sx, int64_t sout) {
+__global__ __launch_bounds__(256) void split2_kernel(SplitOp o0, SplitOp o1, int y0) {
   __shared__ float t[64][65];
-  X += (int64_t)blockIdx.z * sx;
-  out += (int64_t)blockIdx.z * sout;
-  const int64_t r0 = (int64_t)blockIdx.y * 64, k0 = (int64_t)blockIdx.x * 64;
+  int64_t by;
+  const SplitOp o = split_operand(o0, o1, y0, by);
+  const float* __restrict__ X = o.X + (int64_t)blockIdx.z * o.sx;
+  uint16_t* __restrict__ out = o.out + (int64_t)blockIdx.z * o.sout;
+  const int64_t ldx = o.ldx, R = o.R, Kk = o.Kk, Kp = o.Kp;
+  const int trans = o.trans, mask = o.mask;
+  const int64_t r0 = by * 64, k0 = (int64_t)blockIdx.x * 64;
+  if (k0 >= Kp) return;  // the other operand of the launch has more rank
   split_load_block(t, X, ldx, R, Kk, trans, r0, k0);
   __syncthreads();
   const int orow = threadIdx.x >> 2, kq = threadIdx.x & 3;  // output row, 16-k quarter
@@ -325,11 +346,11 @@ __global__ __launch_bounds__(256) void split2_kernel(const float* __restrict__ X
   const int64_t kb = k0 + 16 * kq;
   if (kb >= Kp) return;
   const int64_t plane = R * Kp;
-  uint16_t* o = out + ((kb >> 4) * R + r) * 16;
+  uint16_t* dst = out + ((kb >> 4) * R + r) * 16;
 #pragma unroll
   for (int g = 0; g < 2; ++g) {
-    *reinterpret_cast<mg_u16x8*>(o + 8 * g) = p1[g];
-    *reinterpret_cast<mg_u16x8*>(o + plane + 8 * g) = p2[g];
+    *reinterpret_cast<mg_u16x8*>(dst + 8 * g) = p1[g];
+    *reinterpret_cast<mg_u16x8*>(dst + plane + 8 * g) = p2[g];
   }
 }
 
@@ -789,33 +810,40 @@ __global__ __launch_bounds__(512, 1) void gemm3x_pair_kernel(G3Args g1, int64_t 
   }
 }
 
-// The planes of an operand (split2_kernel's layout at out, batch stride sout): the row
-// maxima first, then the scaled split.  out holds 2 R Kp fp16 then (1 + G2_NS) R floats,
-// within the 3 R Kp fp16 a plane buffer holds (Kp >= 34).
-int split2(const float* X, int64_t ldx, int64_t R, int64_t Kk, int trans, int mask,
-           uint16_t* out, int64_t Kp, hipStream_t s, int batch = 1, int64_t sx = 0,
-           int64_t sout = 0) {
-  if (R <= 0) return HI2X_OK;
-  if (Kp < 2 * (1 + G2_NS)) {  // split products have ranks in the hundreds at least
-    set_error("split2: rank %lld too small for the scale partials", (long long)Kp);
-    return HI2X_EINVAL;
-  }
-  float* pm = reinterpret_cast<float*>(out + G3_NP * R * Kp) + R;
+// The planes of one or two operands of a product (split2_kernel's layout at out, batch
+// stride sout): the row maxima first, then the scaled split, each one launch for both
+// operands.  out holds 2 R Kp fp16 then (1 + G2_NS) R floats, within the 3 R Kp fp16 a
+// plane buffer holds (Kp >= 34).
+int split2(const SplitOp& a, const SplitOp* b, hipStream_t s, int batch = 1) {
+  const SplitOp none{a.X, a.ldx, 0, a.Kk, a.Kp, a.sx, a.sout, a.trans, a.mask, a.out};
+  const SplitOp& o1 = b ? *b : none;
+  for (const SplitOp* o : {&a, &o1})
+    if (o->R > 0 && o->Kp < 2 * (1 + G2_NS)) {  // split products have ranks in the hundreds
+      set_error("split2: rank %lld too small for the scale partials", (long long)o->Kp);
+      return HI2X_EINVAL;
+    }
+  auto groups = [](const SplitOp& o) {  // rowmax_kernel row groups of an operand
+    return (unsigned)(o.trans ? (o.R + 255) / 256 : (o.R + 3) / 4);
+  };
+  auto vec = [](const SplitOp& o) {
+    return o.R <= 0 || ((reinterpret_cast<uintptr_t>(o.X) & 15) == 0 && o.ldx % 4 == 0 &&
+                        o.sx % 4 == 0);
+  };
+  const unsigned ga = groups(a), gb = o1.R > 0 ? groups(o1) : 0;
+  if (ga + gb == 0) return HI2X_OK;
   {
-    const dim3 gm((unsigned)G2_NS, (unsigned)(trans ? (R + 255) / 256 : (R + 3) / 4), (unsigned)batch);
-    const bool vec = (reinterpret_cast<uintptr_t>(X) & 15) == 0 && ldx % 4 == 0 && sx % 4 == 0;
-    if (vec)
-      hipLaunchKernelGGL(rowmax_kernel<true>, gm, dim3(256), 0, s, X, ldx, R, Kk, trans, mask, pm,
-                         sx, sout / 2);
+    const dim3 gm((unsigned)G2_NS, ga + gb, (unsigned)batch);
+    if (vec(a) && vec(o1))
+      hipLaunchKernelGGL(rowmax_kernel<true>, gm, dim3(256), 0, s, a, o1, (int)ga);
     else
-      hipLaunchKernelGGL(rowmax_kernel<false>, gm, dim3(256), 0, s, X, ldx, R, Kk, trans, mask,
-                         pm, sx, sout / 2);
+      hipLaunchKernelGGL(rowmax_kernel<false>, gm, dim3(256), 0, s, a, o1, (int)ga);
     const int rc = launch_status("rowmax_kernel");
     if (rc) return rc;
   }
-  const dim3 grid((unsigned)((Kp + 63) / 64), (unsigned)((R + 63) / 64), (unsigned)batch);
-  hipLaunchKernelGGL(split2_kernel, grid, dim3(256), 0, s, X, ldx, R, Kk, trans, mask, out, Kp,
-                     sx, sout);
+  const unsigned ya = (unsigned)((a.R + 63) / 64), yb = (unsigned)((o1.R + 63) / 64);
+  const int64_t kp = std::max(a.Kp, o1.R > 0 ? o1.Kp : 0);
+  const dim3 grid((unsigned)((kp + 63) / 64), ya + yb, (unsigned)batch);
+  hipLaunchKernelGGL(split2_kernel, grid, dim3(256), 0, s, a, o1, (int)ya);
   return launch_status("split2_kernel");
 }
 
@@ -1696,15 +1724,13 @@ int product(const Ctx& c, GemmArgs a) {
   uint16_t* pa = reinterpret_cast<uint16_t*>(c.ws + c.plan->pa_off);
   uint16_t* pb = reinterpret_cast<uint16_t*>(c.ws + c.plan->pb_off);
   const int64_t sPl = 2 * c.sW;  // planes live in the workspace (bf16 elements)
-  int rc = split2(a.A, a.lda, a.M, a.Kd, 0, AMODE == 1 ? 1 : 0, pa, Kp, c.s, c.batch, a.sA, sPl);
+  const SplitOp oa{a.A, a.lda, a.M, a.Kd, Kp, a.sA, sPl, 0, AMODE == 1 ? 1 : 0, pa};
+  const SplitOp ob{a.B, a.ldb, a.N, a.Kd, Kp, a.sB, sPl, TB ? 0 : 1, split_mask_b(BMODE), pb};
+  // B is A itself in the symmetric update: one operand's planes serve both
+  const bool same = TB && a.B == a.A && a.ldb == a.lda && a.N == a.M && AMODE == 0 && BMODE == 0;
+  const int rc = split2(oa, same ? nullptr : &ob, c.s, c.batch);
   if (rc) return rc;
-  const uint16_t* bp = pa;
-  if (!(TB && a.B == a.A && a.ldb == a.lda && a.N == a.M && AMODE == 0 && BMODE == 0)) {
-    rc = split2(a.B, a.ldb, a.N, a.Kd, TB ? 0 : 1, split_mask_b(BMODE), pb, Kp, c.s, c.batch,
-                a.sB, sPl);
-    if (rc) return rc;
-    bp = pb;
-  }
+  const uint16_t* bp = same ? pa : pb;
   G3Args g{pa, bp, a.C, a.M, a.N, a.Kd, Kp, a.ldc, a.alpha, a.beta};
   g.sA = sPl;
   g.sB = sPl;
@@ -1735,9 +1761,9 @@ int product_pair(const Ctx& c, GemmArgs upd, GemmArgs t2) {
     uint16_t* pa = reinterpret_cast<uint16_t*>(c.ws + c.plan->pa_off);
     uint16_t* pb = reinterpret_cast<uint16_t*>(c.ws + c.plan->pb_off);
     const int64_t sPl = 2 * c.sW;
-    int rc = split2(upd.A, upd.lda, upd.M, upd.Kd, 0, 0, pa, Kp, c.s, c.batch, upd.sA, sPl);
-    if (rc) return rc;
-    rc = split2(t2.B, t2.ldb, t2.N, t2.Kd, 1, split_mask_b(1), pb, Kp, c.s, c.batch, t2.sB, sPl);
+    const SplitOp oa{upd.A, upd.lda, upd.M, upd.Kd, Kp, upd.sA, sPl, 0, 0, pa};
+    const SplitOp ob{t2.B, t2.ldb, t2.N, t2.Kd, Kp, t2.sB, sPl, 1, split_mask_b(1), pb};
+    int rc = split2(oa, &ob, c.s, c.batch);
     if (rc) return rc;
     G3Args g1{pa, pa, upd.C, upd.M, upd.N, upd.Kd, Kp, upd.ldc, upd.alpha, upd.beta};
     G3Args g2{pa, pb, t2.C, t2.M, t2.N, t2.Kd, Kp, t2.ldc, t2.alpha, t2.beta};
