@@ -189,3 +189,15 @@ def test_hadamard16_constant():
     h = fmt.hadamard16()
     assert torch.allclose(h @ h, torch.eye(16, dtype=torch.float64))
     assert torch.equal(h, h.T)
+
+
+def test_stream_background_marks_and_clears_without_a_gpu():
+    # the background mark is a host-side registry keyed by the stream handle: no HIP call
+    from hi2_amd import _lib
+
+    lib = _lib.lib()
+    handle = ctypes.c_void_p(0x1234560)
+    assert lib.hi2x_stream_background(handle, 1) == _lib.OK
+    assert lib.hi2x_stream_background(handle, 1) == _lib.OK  # marking twice is harmless
+    assert lib.hi2x_stream_background(handle, 0) == _lib.OK
+    assert lib.hi2x_stream_background(handle, 0) == _lib.OK  # so is clearing twice
