@@ -329,7 +329,8 @@ __global__ __launch_bounds__(256) void split2_kernel(SplitOp o0, SplitOp o1, int
   m = fmaxf(m, __shfl_xor(m, 2));
   int ex = 0;
   (void)frexpf(m, &ex);  // m = f 2^ex, f in [0.5, 1): floor(log2 m) = ex - 1
-  const int e = m > 0.0f ? (ex - 1 < -100 ? -100 : (ex - 1 > 100 ? 100 : ex - 1)) : 0;
+  // e in [-100, 127]: the scale 2^(14 - e) and its inverse stay normal for every finite m
+  const int e = m > 0.0f ? (ex - 1 < -100 ? -100 : (ex - 1 > 127 ? 127 : ex - 1)) : 0;
   const float sc = ldexpf(1.0f, 14 - e);
   if (blockIdx.x == 0 && kq == 0) inv[r] = ldexpf(1.0f, e - 14);
   mg_u16x8 p1[2], p2[2];

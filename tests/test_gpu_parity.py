@@ -660,21 +660,23 @@ def test_inverse_factor_inverts_large(dev):
     assert err < 5e-3, err
 
 
-def test_inverse_factor_wide_channel_scales(dev):
-    """K = 4096 with channel scales 2^u, u uniform in [-40, 40] (Hessian entries over a
-    range of 2^160): the big products' operand rows are split into fp16 planes after a
-    power-of-two row scale, so every row of U keeps fp32-level accuracy relative to its
-    own largest element.  Reference: the float64 inverse Cholesky factor of the same
-    damped matrix (torch.linalg on the device)."""
+@pytest.mark.parametrize("lo, hi", [(-40, 40), (40, 52)])
+def test_inverse_factor_wide_channel_scales(dev, lo, hi):
+    """K = 4096 with channel scales 2^u, u uniform in [lo, hi]: Hessian entries over a
+    range of 2^160, or all large (up to ~2^107, operand rows whose largest element is above
+    2^100, while the damping's diagonal sum stays finite in fp32).  The big products' operand rows are split into fp16
+    planes after a power-of-two row scale, so every row of U keeps fp32-level accuracy
+    relative to its own largest element.  Reference: the float64 inverse Cholesky factor
+    of the same damped matrix (torch.linalg on the device)."""
     from hi2_amd.hessian import inverse_factor
 
-    k, spread = 4096, 40
+    k = 4096
     g = torch.Generator(device=dev).manual_seed(5)
     x = torch.randn(2 * k, k, device=dev, generator=g, dtype=torch.float64)
     x = x * torch.exp(0.5 * torch.randn(1, k, device=dev, generator=g, dtype=torch.float64))
     h0 = x.T @ x / x.shape[0]
     del x
-    dsc = torch.exp2(torch.randint(-spread, spread + 1, (k,), device=dev, generator=g).double())
+    dsc = torch.exp2(torch.randint(lo, hi + 1, (k,), device=dev, generator=g).double())
     h = (dsc[:, None] * h0 * dsc[None, :]).float().contiguous()
     u = inverse_factor(h, 0.01).double()
     hd = h.double()
