@@ -1265,10 +1265,10 @@ struct ProdAcc {  // this wave's tiles of an H x H product (tile t = wave + 4p, 
   f32x4v acc[PER];
 };
 
-// Three bf16 planes of 8 consecutive k of one lane's fragment, as the split-plane GEMM
-// writes them: x1 = bf16(x), x2 = bf16(x - x1), x3 = bf16(x - x1 - x2) (the differences
-// are exact in fp32).  Pairs go through v_cvt_pk_bf16_f32; a bf16 back to fp32 is its
-// bits in the upper half of the word.
+// Three bf16 planes of 8 consecutive k of one lane's fragment: x1 = bf16(x),
+// x2 = bf16(x - x1), x3 = bf16(x - x1 - x2) (the differences are exact in fp32; bf16 has
+// fp32's exponent range, so no row scale is needed).  Pairs go through
+// v_cvt_pk_bf16_f32; a bf16 back to fp32 is its bits in the upper half of the word.
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x2v __attribute__((ext_vector_type(2)));
@@ -1295,7 +1295,9 @@ __device__ __forceinline__ void split8(const float4 x0, const float4 x1, bf16x8 
 }
 
 // acc = A op(B) for the node's 128 x 128 blocks on bf16 MFMA through the three-way split
-// (the six terms x_i y_j with i + j <= 4 of the split-plane GEMM, small terms first):
+// (the six terms x_i y_j with i + j <= 2, small terms first; the big products' scaled
+// two-plane fp16 split measured slower here, its row maxima and conversions back to
+// fp32 costing the VALU time its halved MFMAs save):
 // v_mfma_f32_16x16x32_bf16 (lane l: row or column l % 16, k 8 (l / 16) .. + 7; the
 // accumulator layout of the fp32 16x16x4 MFMA), six 16-cycle MFMAs per 32 k where the
 // fp32 MFMA takes eight of 32 cycles.  The wave's tiles t = wave + 4p are tile row p / 2,
