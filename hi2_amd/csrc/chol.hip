@@ -1085,9 +1085,20 @@ __global__ __launch_bounds__(256) void diag_mean_kernel(const float* __restrict_
       const int64_t sidx = task >> 2, q = task & 3;
       const int64_t row0 = (s0 + sidx) * step;
       float a = 0.0f;
-      for (int64_t r = 0; r < step; ++r) {
-        const int64_t e = 4 * (row0 + r) + q;
-        a += hs[e * K + e];
+      if (step == 16) {  // every K below 2^22: the 16 loads issued before the first add
+        float v[16];
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int64_t e = 4 * (row0 + r) + q;
+          v[r] = hs[e * K + e];
+        }
+#pragma unroll
+        for (int r = 0; r < 16; ++r) a += v[r];
+      } else {
+        for (int64_t r = 0; r < step; ++r) {
+          const int64_t e = 4 * (row0 + r) + q;
+          a += hs[e * K + e];
+        }
       }
       ssum[sidx][q] = a;
     }
