@@ -260,6 +260,16 @@ def _on_device(reqs, cfg, ex, i: int, use_gptq, comp_full, pack=None):
         # lane 0 takes the widest input (the critical path): the others' GPTQ updates
         # leave room on the CUs for its latency-bound kernels
         _lib.stream_background(st, j > 0)
+    try:
+        return _enqueue(reqs, cfg, ex, i, use_gptq, comp_full, pack, dev, main, lanes)
+    finally:
+        # the marks are read when a launch is enqueued: every chain is enqueued now
+        for st in lanes:
+            _lib.stream_background(st, False)
+
+
+def _enqueue(reqs, cfg, ex, i, use_gptq, comp_full, pack, dev, main, lanes):
+    """The body of :func:`_on_device` once its lane streams are set up."""
     groups: dict = {}  # factor key -> requests, in order of first appearance
     near: list[int] = []
     for ri, r in enumerate(reqs):

@@ -230,53 +230,57 @@ __device__ __forceinline__ void store_row(const RowRegs<COMP>& R, int64_t K, int
   }
 }
 
-// The block for this lane's row with IEEE division, as a rolled loop (its arrays live in
-// scratch memory: this path only runs for a wave whose fast pass met an error quotient
-// outside the reciprocal iteration's exact range, so its speed does not matter, and an
-// unrolled second copy of the loop would double the fast path's registers), then the
-// row's outputs.  The same operations in the same order as gptq_step.
-template <bool COMP>
-__device__ void gptq_rows_exact(const float* __restrict__ wc, int64_t K, int64_t i1, int L,
-                                int64_t rbase, int nrows, int lr, int64_t r,
-                                const int32_t* __restrict__ blk, const float* __restrict__ lo,
-                                const float* __restrict__ st, int64_t ldp, const float* su,
-                                int q, float nm, float* __restrict__ err1, int64_t lde,
-                                uint8_t* __restrict__ codes, float* __restrict__ comp) {
-  RowRegs<COMP> R;
-  load_row<COMP>(R, wc, K, i1, L, rbase, nrows, lr, blk, lo, st, ldp, su, q);
-  volatile float w[CPL], er[CPL], qc[CPL], cm[CPL];
-  for (int m = 0; m < CPL; ++m) {
-    w[m] = R.w[m];
-    er[m] = 0.0f;
-    qc[m] = 0.0f;
-    cm[m] = 0.0f;
-  }
-  const int lane = threadIdx.x & 63;
+// Column group M (columns i = 16M + s, s = 0..15) of the block with IEEE division: the
+// 16 steps as a rolled loop whose register index M is a compile-time constant, so the
+// row state stays in registers (no dynamically indexed array, no scratch memory).  The
+// same operations in the same order as gptq_step; w[M] is also updated at s = 15, where
+// every lane's column of group M is already rounded (a dead value, as in gptq_step).
+template <int M, bool COMP>
+__device__ __forceinline__ void exact_group(RowRegs<COMP>& R, int L, int q, float nm,
+                                            const float* __restrict__ suq, int lane) {
 #pragma unroll 1
-  for (int i = 0; i < L; ++i) {
-    const int m = i / QL, s = i % QL;
-    const float col = w[m];
-    const float lo_j = R.loc[m], st_j = R.stc[m];
+  for (int s = 0; s < QL; ++s) {
+    const int i = QL * M + s;
+    if (i >= L) break;  // L is uniform: the whole wave leaves together
+    const float col = R.w[M];
+    const float lo_j = R.loc[M], st_j = R.stc[M];
     const float safe = (st_j == 0.0f) ? 1.0f : st_j;
     float qv = clamp_code(__builtin_rintf((col - lo_j) / safe), nm);
     if (st_j == 0.0f) qv = 0.0f;
     const float wq = f16_round(lo_j + qv * st_j);
-    const float ujj = su[i * USTR + lane_off(q) + m];
-    const float e = (col - wq) / ujj;
+    const float* ui = suq + i * USTR;
+    const float e = (col - wq) / ui[M];  // U[i][i] in the owner lane
     const float eb = __shfl(e, (lane & ~(QL - 1)) + s, 64);
-    if (q == s) {
-      er[m] = e;
-      qc[m] = qv;
-      cm[m] = col;
-    }
-    for (int mm = (i + 1) / QL; mm < CPL; ++mm)
-      w[mm] = w[mm] - eb * su[i * USTR + lane_off(q) + mm];
+    const bool own = q == s;
+    R.er[M] = own ? e : R.er[M];
+    R.qc[M] = own ? qv : R.qc[M];
+    if constexpr (COMP) R.cm[M] = own ? col : R.cm[M];
+#pragma unroll
+    for (int mm = M; mm < CPL; ++mm) R.w[mm] = R.w[mm] - eb * ui[mm];
   }
-  for (int m = 0; m < CPL; ++m) {
-    R.er[m] = er[m];
-    R.qc[m] = qc[m];
-    if constexpr (COMP) R.cm[m] = cm[m];
-  }
+}
+template <bool COMP, int... Ms>
+__device__ __forceinline__ void exact_groups(std::integer_sequence<int, Ms...>,
+                                             RowRegs<COMP>& R, int L, int q, float nm,
+                                             const float* __restrict__ suq, int lane) {
+  (exact_group<Ms, COMP>(R, L, q, nm, suq, lane), ...);
+}
+
+// The block for this lane's row again, from the working copy, with IEEE division, then
+// the row's outputs.  Runs only for a wave whose fast pass met an error quotient outside
+// the reciprocal iteration's exact range; it reloads the fast pass's register state R
+// (dead once the wave has decided to run again) instead of holding a second copy.
+template <bool COMP>
+__device__ void gptq_rows_exact(RowRegs<COMP>& R, const float* __restrict__ wc, int64_t K,
+                                int64_t i1, int L, int64_t rbase, int nrows, int lr,
+                                int64_t r, const int32_t* __restrict__ blk,
+                                const float* __restrict__ lo, const float* __restrict__ st,
+                                int64_t ldp, const float* su, int q, float nm,
+                                float* __restrict__ err1, int64_t lde,
+                                uint8_t* __restrict__ codes, float* __restrict__ comp) {
+  load_row<COMP>(R, wc, K, i1, L, rbase, nrows, lr, blk, lo, st, ldp, su, q);
+  exact_groups<COMP>(std::make_integer_sequence<int, CPL>{}, R, L, q, nm, su + lane_off(q),
+                     (int)(threadIdx.x & 63));
   store_row<COMP>(R, K, i1, L, r, q, err1, lde, codes, comp);
 }
 
@@ -350,8 +354,8 @@ __global__ __launch_bounds__(RPG * QL) void gptq_block_kernel(
       // some row of this wave met an error quotient outside the iteration's exact range
       // (subnormal or negative-zero numerators, extreme magnitudes): the wave runs the
       // block again from the working copy with IEEE division
-      gptq_rows_exact<COMP>(wc, K, i1, L, rbase, nrows, lr, r, blk + (int64_t)g * K, lo, st,
-                            ldp, su, q, nm, err1, lde, codes, comp);
+      gptq_rows_exact<COMP>(R, wc, K, i1, L, rbase, nrows, lr, r, blk + (int64_t)g * K, lo,
+                            st, ldp, su, q, nm, err1, lde, codes, comp);
       continue;
     }
     store_row<COMP>(R, K, i1, L, r, q, err1, lde, codes, comp);

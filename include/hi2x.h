@@ -10,10 +10,19 @@
  *   definite), HI2X_ELAUNCH (a HIP call failed), HI2X_ERANGE (a code outside the
  *   ladder).  hi2x_last_error() returns the calling thread's last message.
  *
- * The encode path keeps no mutable global state (the last-error text is
- * thread-local), so one host thread per device may call it concurrently.  The one
- * process-wide mutable state is the opt-in launch-timing record of the measurement
- * section at the end (hi2x_timing_*), which the encode path never reads.
+ * The last-error text is thread-local, so one host thread per device may call the
+ * library concurrently.  Process-wide mutable state, each piece guarded by its own lock:
+ *   - the opt-in launch-timing record of the measurement section at the end
+ *     (hi2x_timing_*), which the encode path never reads;
+ *   - the set of streams marked background (hi2x_stream_background), read by every
+ *     GPTQ cross-block update launch to size its LDS reservation (a scheduling hint:
+ *     results are unchanged); callers clear their marks when their chains end;
+ *   - the per-device address of the 64 MiB error array of hi2x_gptq_run_noalloc,
+ *     looked up once per device.  The array itself is part of the library's code
+ *     object, so it is resident on every GPU the library's GPTQ kernels are loaded on,
+ *     whether or not that entry point is called.
+ * No kernel of the library uses a private (scratch) segment, so no launch makes the HIP
+ * runtime allocate device memory.
  *
  * Reference interfaces are cited as path:line of BlivionIaG/hi2.
  */

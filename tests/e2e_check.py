@@ -1,101 +1,5 @@
-"""Agreement of a free-running encode pipeline with the reference's on the end-to-end
-fixtures, and the classification of every row where the two differ.
+"""The tie classification of the end-to-end tests (oracle/parity.py, the checker shared
+with bench.py's parity object)."""
 
-Two fp32 pipelines that sum the Hessian GEMM in different orders and factor it with
-different blockings produce Sigma, Hs and U that differ in the last bits.  From there a
-row of the encoding can only come apart at a discrete decision:
-
-* a **ladder tie**: the ladder fit of some block (argmin over the grid and the LSQ
-  refits on the row's uncompensated weights, weighted by diag(Hs)) picks another
-  (lo, step) because two candidates' weighted errors are equal to fp32 precision, or the
-  8-bit quantisation of the row's ladders lands on other bytes; from that block on the
-  row follows another, equally good, path;
-* a **rounding tie**: with the same ladder, the compensated value of a column lies so
-  close to a rounding boundary that the two runs' accumulated fp32 differences put it on
-  different sides.
-
-``first_divergences`` finds, per row, the first column where the runs differ (a code,
-or the first column of a block whose decoded ladder differs) and measures the tie: for
-a ladder tie the relative gap between the two fits' weighted errors (float64, the
-reference's weights), for a rounding tie the distance, in ladder steps, between the two
-runs' pre-rounding quotients at that column.
-"""
-
-import numpy as np
-
-import oracle
-
-
-def f16_bits_to_f32(bits):
-    return np.asarray(bits, np.uint16).view(np.float16).astype(np.float32)
-
-
-def decode(params, consts_bits):
-    """decode_params (hi2/format.py:45-60): lo = fp16(f32(f64(u) f64(lo_scale) +
-    f64(lo_min))), step = fp16(f32(u) f32(step_scale)); returns f32 [rows, nb] each."""
-    c = f16_bits_to_f32(consts_bits).astype(np.float64)
-    lo_u = params[..., 0].astype(np.float64)
-    st_u = params[..., 1].astype(np.float32)
-    lo = (lo_u * c[:, 1:2] + c[:, 0:1]).astype(np.float32).astype(np.float16)
-    st = (st_u * c[:, 2:3].astype(np.float32)).astype(np.float16)
-    return lo.astype(np.float32), st.astype(np.float32)
-
-
-def _fit_err(wb, db, lo, st, nlev):
-    safe = st if st != 0 else 1.0
-    q = np.clip(np.rint((wb - lo) / safe), 0, nlev - 1)
-    rec = lo + q * st
-    return float((db * (rec - wb) ** 2).sum())
-
-
-def first_divergences(wt, codes_o, codes_r, params_o, params_r, consts_o, consts_r, comp_o,
-                      comp_r, d_o, d_r, nbits, block):
-    """Per diverging row of one candidate group (rows ``wt`` [n, K] in the stored basis,
-    ``*_o`` this build's, ``*_r`` the reference's): dicts with ``row``, ``col``, ``kind``
-    ("ladder" or "rounding") and ``tie`` (the relative fit-error gap of the blocks whose
-    fits differ, or the quotient distance in steps)."""
-    n, k = codes_o.shape
-    nb = k // block
-    lo_o, st_o = decode(params_o, consts_o)
-    lo_r, st_r = decode(params_r, consts_r)
-    lad_diff = (lo_o != lo_r) | (st_o != st_r)
-    out = []
-    for i in range(n):
-        cd = np.nonzero(codes_o[i] != codes_r[i])[0]
-        ld = np.nonzero(lad_diff[i])[0]
-        if cd.size == 0 and ld.size == 0:
-            continue
-        first_code = int(cd[0]) if cd.size else k
-        first_lad = int(ld[0]) * block if ld.size else k
-        if first_lad <= first_code:
-            # the raw fits of both runs: every block whose fit differs must be a tie
-            wb = wt[i].reshape(1, nb, block)
-            fo = oracle.fit_ladder(wb, d_o.reshape(1, nb, block), 2 ** nbits, "normal")
-            fr = oracle.fit_ladder(wb, d_r.reshape(1, nb, block), 2 ** nbits, "normal")
-            gap = 0.0
-            w64 = wt[i].reshape(nb, block).astype(np.float64)
-            d64 = d_r.reshape(nb, block).astype(np.float64)
-            for b in range(nb):
-                if fo[0][0, b] == fr[0][0, b] and fo[1][0, b] == fr[1][0, b]:
-                    continue
-                eo = _fit_err(w64[b], d64[b], float(fo[0][0, b]), float(fo[1][0, b]), 2 ** nbits)
-                er = _fit_err(w64[b], d64[b], float(fr[0][0, b]), float(fr[1][0, b]), 2 ** nbits)
-                gap = max(gap, abs(eo - er) / max(eo, er, 1e-300))
-            out.append(dict(row=i, col=first_lad, kind="ladder", tie=gap))
-        else:
-            j = first_code
-            b = j // block
-            qo = (float(comp_o[i, j]) - float(lo_o[i, b])) / float(st_o[i, b])
-            qr = (float(comp_r[i, j]) - float(lo_r[i, b])) / float(st_r[i, b])
-            out.append(dict(row=i, col=j, kind="rounding", tie=abs(qo - qr),
-                            boundary=min(int(codes_o[i, j]), int(codes_r[i, j])) + 0.5,
-                            q=(qo, qr)))
-    return out
-
-
-def summarise(divs, n_rows):
-    lad = [x["tie"] for x in divs if x["kind"] == "ladder"]
-    rnd = [x["tie"] for x in divs if x["kind"] == "rounding"]
-    return (f"rows diverging {len(divs)}/{n_rows} (ladder ties {len(lad)}, max fit gap "
-            f"{max(lad, default=0):.2g}; rounding ties {len(rnd)}, max quotient distance "
-            f"{max(rnd, default=0):.3g} steps)")
+from oracle.parity import (classify_departures, decode, f16_bits_to_f32,  # noqa: F401
+                           first_divergences, row_digests, summarise)

@@ -27,7 +27,9 @@ depend on the reference's own torch-CPU arithmetic:
   ``inverse_factor``, ``fwht_groups`` and GPTQ with packing through ``encode_many``, on
   the seeded inputs of ``tests/e2e_recipes.py`` (cfg1 down-scaled to 512 x 512 with 512
   and 2048 tokens, a cfg2-style mixed INT2/INT4 case, and cfg1 at its full 2048 x 2048
-  as digests and a 64-row slice);
+  as digests and a 64-row slice), and at the benchmark's widths (cfg3's q_proj at
+  K = 4096 with 8192 tokens, cfg2's down_proj at K = 14336) as digests, every row's sse
+  and per-row digests, and a slice of rows;
 * the MoE token floor (``hi2/layerwise.py:241-257`` with ``hi2.moe.blend``) on seven
   experts' sums (``moe_blend.npz``);
 * ``hi2.encode.encode_rows`` (nearest rounding, ``hi2/encode.py:133-173``) at INT2/B32,
@@ -41,7 +43,8 @@ reference is stored.  Run from the repository root:
     python tests/golden/make_golden.py colstats   # colstats.npz only
     python tests/golden/make_golden.py encode_many  # encode_many.npz only
     python tests/golden/make_golden.py qad          # qad.npz only
-    python tests/golden/make_golden.py e2e          # e2e_*.npz only
+    python tests/golden/make_golden.py e2e          # e2e_*.npz only (small cases)
+    python tests/golden/make_golden.py e2e_wide [case ...]  # the K = 4096 / 14336 cases
     python tests/golden/make_golden.py moe          # moe_blend.npz only
     python tests/golden/make_golden.py nearest      # nearest.npz only
 """
@@ -54,6 +57,8 @@ import torch
 
 REF = os.environ.get("HI2_REFERENCE", "/root/reference")
 OUT = os.path.dirname(os.path.abspath(__file__))
+# the repository root: tests/e2e_recipes.py digests rows with the oracle's helper
+sys.path.insert(0, os.path.dirname(os.path.dirname(OUT)))
 
 CASES = [(2, 16), (2, 32), (2, 64), (4, 16), (4, 32), (4, 64), (8, 32), (8, 64)]
 
@@ -358,8 +363,8 @@ def make_e2e():
     sys.path.insert(0, REF)
     sys.path.insert(0, os.path.dirname(OUT))
     import hi2.hessian as H
-    from e2e_recipes import CANDIDATES, CASES, DAMP, FULL_CASES, SLICE_ROWS, input_digests, \
-        inputs, sha, upper
+    from e2e_recipes import CANDIDATES, CASES, DAMP, FULL_CASES, SLICE_ROWS, WIDE_CASES, \
+        input_digests, inputs, sha, upper
     from hi2.calibrate import Config, EncodeRequest, TensorTable, encode_many
     from hi2.executor import Executor
     from hi2.format import fwht_groups
@@ -368,6 +373,8 @@ def make_e2e():
     torch.set_num_threads(1)
     orig = H.inverse_factor
     for case, (_recipe, k, n, t, _seed) in CASES.items():
+        if case in WIDE_CASES:
+            continue
         print(case, flush=True)
         xb, w, picks, had = inputs(case)
         had_t = torch.from_numpy(had)
@@ -450,6 +457,119 @@ def make_e2e():
             np.savez_compressed(os.path.join(OUT, f"e2e_{case}.npz"), **out)
 
 
+def make_e2e_wide(cases=None):
+    """The reference's pipeline at the benchmark's widths (tests/e2e_recipes.py
+    WIDE_CASES: K = 4096 with 8192 tokens, K = 14336 with 4096 tokens), where this build's
+    factor runs its fp16 split-plane products: HessianStats over the bf16 tokens, mean,
+    transform_sigma, inverse_factor, fwht_groups, GPTQ of every candidate group through
+    encode_jobs_gptq (comp on) and assemble.  Stored per case, in three files near 1 MB:
+    digests of the inputs, of Sigma, Hs, U, the codes, comp, sse and every packed field;
+    every row's sse, consts and 8-byte digests of its codes and ladder bytes, 4-byte
+    digests of its codes per 512 columns; d; the
+    diagonals and a few evenly spread rows of Sigma and U; the first rows' codes, ladder
+    bytes and comp in full.  Beside it, the same digests of the reference against itself
+    with its Hessian accumulated in 2048-token chunks (``HessianStats.update``'s chunk
+    argument), and the share of codes the two reference runs have equal.  Torch runs on 8
+    threads here (recorded as "threads"): the case is too large for one."""
+    sys.path.insert(0, REF)
+    sys.path.insert(0, os.path.dirname(OUT))
+    from e2e_recipes import (CANDIDATES, CASES, DAMP, WIDE_CASES, WIDE_SLICE_ROWS,
+                             factor_rows, input_digests, inputs, row_digests,
+                             segment_digests, sha)
+    from hi2.format import assemble, fwht_groups
+    from hi2.hessian import (GptqJob, HessianStats, encode_jobs_gptq, inverse_factor,
+                             transform_sigma)
+
+    threads = 8
+    torch.set_num_threads(threads)
+    for case in cases or WIDE_CASES:
+        _recipe, k, n, t, _seed = CASES[case]
+        print(case, flush=True)
+        xb, w, picks, had = inputs(case)
+        had_t = torch.from_numpy(had)
+        st = HessianStats(k)
+        st.update(xb)
+        sigma = st.mean()
+        hs = transform_sigma(sigma, None, had_t)
+        d = hs.diagonal().clone()
+        u = inverse_factor(hs, DAMP)
+        wt = fwht_groups(torch.from_numpy(w), had_t)
+        codes = np.zeros((n, k), np.uint8)
+        comp = np.zeros((n, k), np.float32)
+        sse = np.zeros(n, np.float32)
+        consts = np.zeros((n, 3), np.uint16)
+        pdig = np.zeros(n, np.uint64)
+        groups, pieces = [], []
+        for ci, (nb, b) in enumerate(CANDIDATES):
+            rows = np.nonzero(picks == ci)[0]
+            if rows.size == 0:
+                continue
+            print(f"  gptq INT{nb}/B{b}: {rows.size} rows", flush=True)
+            e = encode_jobs_gptq([GptqJob(wt[torch.from_numpy(rows)], d, u, nb, b)],
+                                 "normal", comp=True)[0]
+            codes[rows] = e.codes.numpy()
+            comp[rows] = e.comp.numpy()
+            sse[rows] = e.sse.numpy()
+            cb = e.consts.view(torch.int16).numpy().view(np.uint16)
+            consts[rows] = cb
+            pdig[rows] = row_digests(e.params.numpy())
+            groups.append((ci, rows, e.params.numpy(), cb))
+            pieces.append((torch.from_numpy(rows), e.codes, e.params, e.consts))
+        nbits = torch.tensor([CANDIDATES[c][0] for c in picks])
+        block = torch.tensor([CANDIDATES[c][1] for c in picks])
+        packed = assemble(pieces, nbits, block, had_t, k)
+        dg = input_digests(case)
+        rs = factor_rows(case)
+        sg, un = sigma.numpy(), u.numpy()
+        meta = {"case": np.array(case), "threads": np.array(threads),
+                "digest_x": np.array(dg["x"]), "digest_w": np.array(dg["w"]),
+                "digest_picks": np.array(dg["picks"]), "sigma_sha": np.array(sha(sg)),
+                "hs_sha": np.array(sha(hs.numpy())), "u_sha": np.array(sha(un)),
+                "codes_sha": np.array(sha(codes)), "comp_sha": np.array(sha(comp)),
+                "sse_sha": np.array(sha(sse))}
+        for f in ("codes", "code_off", "blk_params", "param_off", "row_consts"):
+            meta[f"packed_{f}_sha"] = np.array(sha(getattr(packed, f).numpy()))
+        np.savez_compressed(os.path.join(OUT, f"e2e_{case}_factor.npz"), **meta,
+                            factor_rows=rs, sigma_rows=sg[rs].copy(), u_rows=un[rs].copy(),
+                            sigma_diag=np.diag(sg).copy(), u_diag=np.diag(un).copy())
+        r = WIDE_SLICE_ROWS[case]
+        out = dict(d=d.numpy(), sse=sse, consts_all=consts, codes_digest=row_digests(codes),
+                   codes_segments=segment_digests(codes), params_digest=pdig,
+                   codes_slice=codes[:r])
+        for ci, rows, params, cb in groups:
+            keep = rows < r
+            out[f"g{ci}_rows"] = rows[keep]
+            out[f"g{ci}_params"] = params[keep]
+            out[f"g{ci}_consts"] = cb[keep]
+        # the reference against itself: the same pipeline with its Hessian accumulated in
+        # 2048-token chunks (HessianStats.update's own chunk argument) instead of 4096 —
+        # the departures two correct fp32 runs of the reference show between them
+        st2 = HessianStats(k)
+        st2.update(xb, chunk=2048)
+        hs2 = transform_sigma(st2.mean(), None, had_t)
+        d2 = hs2.diagonal().clone()
+        u2 = inverse_factor(hs2, DAMP)
+        codes2 = np.zeros((n, k), np.uint8)
+        pdig2 = np.zeros(n, np.uint64)
+        sse2 = np.zeros(n, np.float32)
+        for ci, (nb, b) in enumerate(CANDIDATES):
+            rows = np.nonzero(picks == ci)[0]
+            if rows.size == 0:
+                continue
+            print(f"  self-check, 2048-token chunks: INT{nb}/B{b}", flush=True)
+            e = encode_jobs_gptq([GptqJob(wt[torch.from_numpy(rows)], d2, u2, nb, b)],
+                                 "normal")[0]
+            codes2[rows] = e.codes.numpy()
+            sse2[rows] = e.sse.numpy()
+            pdig2[rows] = row_digests(e.params.numpy())
+        out.update(self_codes_digest=row_digests(codes2), self_params_digest=pdig2,
+                   self_codes_segments=segment_digests(codes2), self_sse=sse2,
+                   self_codes_equal=np.array((codes2 == codes).mean()))
+        np.savez_compressed(os.path.join(OUT, f"e2e_{case}_out.npz"), **out)
+        np.savez_compressed(os.path.join(OUT, f"e2e_{case}_comp.npz"), comp_slice=comp[:r])
+        del st, sigma, hs, u, wt, codes, comp, st2, hs2, u2, codes2
+
+
 def make_moe():
     """The MoE token floor: hi2/layerwise.py:241-257 (the experts' sum, need, which experts
     are short) with the reference's own blend (hi2/moe.py:152-156) on every short expert."""
@@ -517,6 +637,9 @@ def main():
         return
     if sys.argv[1:] == ["moe"]:
         make_moe()
+        return
+    if sys.argv[1:2] == ["e2e_wide"]:
+        make_e2e_wide(sys.argv[2:] or None)
         return
     if sys.argv[1:] == ["e2e"]:
         make_e2e()

@@ -152,11 +152,21 @@ def e2e_case(case):
     by make_golden.py e2e).  Full cases: sigma [K, K], u [K, K] (upper), d, hs_sha, codes
     [N, K] (unpacked from the reference's packed words), comp, sse, packed fields, per
     candidate group (rows, params, consts).  cfg1_full: digests, sse, sigma_diag, u_diag,
-    16 rows of sigma and u, and the first 64 rows' codes, comp, params and consts."""
-    from e2e_recipes import CASES, FULL_CASES, from_upper
+    16 rows of sigma and u, and the first 64 rows' codes, comp, params and consts.  Wide
+    cases: see below."""
+    from e2e_recipes import CASES, FULL_CASES, WIDE_CASES, from_upper
 
     _, k, n, _, _ = CASES[case]
-    if case not in FULL_CASES:
+    if case in WIDE_CASES:
+        # wide cases (K = 4096, 14336): digests, every row's sse, consts and digests of its
+        # codes and ladder bytes, d, Sigma/U diagonals and factor_rows of each, and the
+        # first rows' codes, comp, params and consts
+        out = {}
+        for part in ("factor", "out", "comp"):
+            with np.load(os.path.join(GOLDEN, f"e2e_{case}_{part}.npz")) as f:
+                out.update({name: f[name] for name in f.files})
+        out["consts_all"] = out["consts_all"].view(np.uint16)
+    elif case not in FULL_CASES:
         g = np.load(os.path.join(GOLDEN, f"e2e_{case}.npz"))
         out = {f: g[f] for f in g.files}
     else:

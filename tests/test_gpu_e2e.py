@@ -28,13 +28,34 @@ import numpy as np
 import pytest
 import torch
 
-from e2e_check import first_divergences, summarise
-from e2e_recipes import CANDIDATES, CASES, FULL_CASES, input_digests, inputs, sha
+from e2e_check import classify_departures, first_divergences, summarise
+from e2e_recipes import (CANDIDATES, CASES, FULL_CASES, WIDE_CASES, input_digests, inputs,
+                         row_digests, segment_digests, sha)
 from golden_data import e2e_case
 
 pytestmark = pytest.mark.gpu
 
 FULL = list(FULL_CASES)
+WIDE = list(WIDE_CASES)
+# every departure at a tie: a ladder tie's two weighted fit errors equal to this relative
+# gap, a rounding tie's two pre-rounding quotients within this many ladder steps
+# (measured on the MI355X: fit gaps <= 6.7e-6, quotient distances <= 3.3e-4 steps)
+LADDER_TIE = 1e-5
+ROUNDING_TIE = 1e-3
+# a ladder departure where only the digests are at hand: the two runs' d (the fit's
+# weights) within this relative difference in the blocks whose fits differ
+D_TIE = 1e-5
+# the wide cases, measured on the MI355X (the GPU path is deterministic):
+#   K = 4096, full rank: U 1.46e-5 rel.; 126 of 4096 rows depart (96 at the ladder, 30 in
+#   their codes alone; the reference against itself with 2048-token chunks: 67), codes
+#   equal >= 0.9832 by 512-column segments; total sse 6.7e-5 rel., the rows that stay
+#   9.3e-7;
+#   K = 14336, rank 4096: U 6.5e-4 rel.; 1572 rows depart (320 / 1252; the reference
+#   against itself: 846), codes equal >= 0.7720 by segments (the slice: 0.9534); total
+#   sse 3.3e-4 rel. (the reference against itself: 1.2e-3), the rows that stay 8.8e-7
+WIDE_BAR = {"cfg3_q_proj": dict(u=3e-5, codes_equal=0.98, rows_departing=0.034, sse_rel=1e-4),
+            "cfg2_down_proj": dict(u=1e-3, codes_equal=0.75, rows_departing=0.42,
+                                   sse_rel=5e-4)}
 # share of equal codes: the north-star 99.9 % on full-rank Hessians; the measured level
 # with margin on the rank-deficient ones (measured on the MI355X: 99.897 % at 512 x 512
 # with 512 tokens, 98.71 % on cfg1's first 64 rows, 7 of them departing at ties; the
@@ -140,11 +161,14 @@ def test_given_the_reference_factor_the_encoding_is_bit_exact(case, dev):
 
 
 def _agreement(case, o, g, rows_of_slice=None):
-    """Codes agreement, tie classification and the reconstruction error of a free run."""
+    """Codes agreement, tie classification and the reconstruction error of a free run:
+    the share of equal codes, the departures, the total sse's relative difference and the
+    largest relative sse difference over the rows that do not depart (all rows of a full
+    case, the slice of a sliced one)."""
     codes_r, comp_r = (g["codes"], g["comp"]) if rows_of_slice is None else \
         (g["codes_slice"], g["comp_slice"])
     keep = np.arange(len(codes_r))
-    divs, equal, total = [], 0, 0
+    divs, equal, total, departed = [], 0, 0, []
     for ci, rows, params, consts in g["groups"]:
         nb, b = CANDIDATES[ci]
         sel = np.isin(np.nonzero(o["picks"] == ci)[0], rows)
@@ -152,12 +176,17 @@ def _agreement(case, o, g, rows_of_slice=None):
         rr = rows[np.isin(rows, keep)]
         equal += int((o["codes"][rr] == codes_r[rr]).sum())
         total += o["codes"][rr].size
-        divs += first_divergences(o["wt"][rr], o["codes"][rr], codes_r[rr], po, params, co,
-                                  consts, o["comp"][rr], comp_r[rr], o["d"], g["d"], nb, b)
-    sse_rel = abs(o["sse"].astype(np.float64).sum() / g["sse"].astype(np.float64).sum() - 1)
+        dv = first_divergences(o["wt"][rr], o["codes"][rr], codes_r[rr], po, params, co,
+                               consts, o["comp"][rr], comp_r[rr], o["d"], g["d"], nb, b)
+        departed += [int(rr[x["row"]]) for x in dv]
+        divs += dv
+    so, sr = o["sse"].astype(np.float64), g["sse"].astype(np.float64)
+    sse_rel = abs(so.sum() / sr.sum() - 1)
+    stay = np.setdiff1d(keep, departed)
+    sse_keep = float(np.max(np.abs(so[stay] - sr[stay]) / np.maximum(sr[stay], 1e-30)))
     msg = (f"{case}: codes equal {equal / total:.6f} of {total}; " + summarise(divs, len(keep))
-           + f"; total sse rel {sse_rel:.3g}")
-    return equal / total, divs, sse_rel, msg
+           + f"; total sse rel {sse_rel:.3g}; sse of the rows that stay {sse_keep:.3g}")
+    return equal / total, divs, sse_rel, sse_keep, msg, sorted(departed)
 
 
 @pytest.mark.parametrize("case", FULL)
@@ -169,12 +198,13 @@ def test_free_running_pipeline_departs_from_the_reference_only_at_ties(case, dev
     sig = N(o["sigma"])
     srel = np.abs(sig - g["sigma"]).max() / np.abs(g["sigma"]).max()
     urel = np.abs(N(o["u"]) - g["u"]).max() / np.abs(g["u"]).max()
-    frac, divs, sse_rel, msg = _agreement(case, o, g)
+    frac, divs, sse_rel, sse_keep, msg, _ = _agreement(case, o, g)
     print(f"sigma rel {srel:.3g}  factor rel {urel:.3g}  " + msg, flush=True)
     assert srel < 1e-5 and urel < 1e-3
     assert frac >= CODES_EQUAL[case], msg
     for x in divs:
-        assert x["tie"] < (1e-5 if x["kind"] == "ladder" else 0.02), (x, msg)
+        assert x["tie"] < (LADDER_TIE if x["kind"] == "ladder" else ROUNDING_TIE), (x, msg)
+    assert sse_keep < 1e-4, msg
     assert sse_rel < SSE_REL[case], msg
 
 
@@ -192,13 +222,98 @@ def test_free_running_pipeline_at_cfg1_full_size(dev):
                np.abs(np.diag(sig) - g["sigma_diag"]).max() / np.abs(g["sigma_diag"]).max())
     u = N(o["u"])
     urel = np.abs(u[:16] - g["u_rows"]).max() / np.abs(g["u_rows"]).max()
-    frac, divs, sse_rel, msg = _agreement(case, o, g, rows_of_slice=True)
+    frac, divs, sse_rel, sse_keep, msg, _ = _agreement(case, o, g, rows_of_slice=True)
     print(f"sigma rel {srel:.3g}  factor rel {urel:.3g}  " + msg, flush=True)
     assert srel < 1e-5 and urel < 3e-3
     assert frac >= CODES_EQUAL[case], msg
     for x in divs:
-        assert x["tie"] < (1e-5 if x["kind"] == "ladder" else 0.05), (x, msg)
+        assert x["tie"] < (LADDER_TIE if x["kind"] == "ladder" else ROUNDING_TIE), (x, msg)
+    assert sse_keep < 1e-4, msg
     assert sse_rel < SSE_REL[case], msg
+
+
+def _params_digests(o, n):
+    """8-byte digests of every row's ladder bytes (rows of each candidate group)."""
+    out = np.zeros(n, np.uint64)
+    for ci in o["per"]:
+        rows = np.nonzero(o["picks"] == ci)[0]
+        out[rows] = row_digests(o["per"][ci][0])
+    return out
+
+
+@pytest.mark.parametrize("case", WIDE)
+def test_free_running_pipeline_at_the_benchmark_widths(case, dev):
+    """(b) at the bench's own widths, where the factor's large products run on the fp16
+    split planes: cfg3's q_proj input (K = 4096, 8192 tokens, full rank) and cfg2's
+    down_proj (K = 14336, 4096 tokens, rank 4096).  Against the reference's pipeline:
+    Sigma and U on the stored rows and diagonals; over every row, which rows depart (their
+    codes, ladder bytes or consts differ from the reference's: per-row digests) and the
+    share of equal codes (bounded below by the 512-column segments whose digests agree);
+    on the slice rows the tie of every departure; the sse of every row that stays within
+    1e-4 of the reference's, and the total sse."""
+    print(f"e2e (b) {case}", flush=True)
+    g = e2e_case(case)
+    assert input_digests(case)["w"] == g["digest_w"]
+    o = _pipeline(case, dev)
+    n, k = o["codes"].shape
+    rs = g["factor_rows"]
+    sig, u = N(o["sigma"]), N(o["u"])
+    srel = max(np.abs(sig[rs] - g["sigma_rows"]).max() / np.abs(g["sigma_rows"]).max(),
+               np.abs(np.diag(sig) - g["sigma_diag"]).max() / np.abs(g["sigma_diag"]).max())
+    urel = max(np.abs(u[rs] - g["u_rows"]).max() / np.abs(g["u_rows"]).max(),
+               np.abs(np.diag(u) - g["u_diag"]).max() / np.abs(g["u_diag"]).max())
+    consts = np.zeros((n, 3), np.uint16)
+    for ci in o["per"]:
+        consts[np.nonzero(o["picks"] == ci)[0]] = o["per"][ci][1]
+    depart = ((row_digests(o["codes"]) != g["codes_digest"])
+              | (_params_digests(o, n) != g["params_digest"])
+              | (consts != g["consts_all"]).any(axis=1))
+    seg_equal = float((segment_digests(o["codes"]) == g["codes_segments"]).mean())
+    # every departing row: a ladder departure (the oracle's fit from the reference's d
+    # reproduces the reference's ladder bytes and differs from this build's at a tie) or
+    # a departure in the codes alone
+    cls = []
+    for ci, (nb, b) in enumerate(CANDIDATES):
+        rows = np.nonzero(o["picks"] == ci)[0]
+        if rows.size == 0:
+            continue
+        dep = np.nonzero(depart[rows])[0]
+        cls += classify_departures(o["wt"][rows], dep, o["d"], g["d"], nb, b,
+                                   g["params_digest"][rows], g["consts_all"][rows],
+                                   o["per"][ci][0], o["per"][ci][1])
+    lad = [x["tie"] for x in cls if x["kind"] == "ladder"]
+    n_rnd = sum(x["kind"] == "rounding" for x in cls)
+    g["codes"], g["comp"] = g["codes_slice"], g["comp_slice"]
+    r = len(g["codes_slice"])
+    frac_s, divs, _, _, msg, departed = _agreement(case, o, g, rows_of_slice=True)
+    so, sr = o["sse"].astype(np.float64), g["sse"].astype(np.float64)
+    sse_rel = abs(so.sum() / sr.sum() - 1)
+    stay = ~depart
+    sse_keep = float(np.max(np.abs(so[stay] - sr[stay]) / np.maximum(sr[stay], 1e-30)))
+    self_dep = ((g["self_codes_digest"] != g["codes_digest"])
+                | (g["self_params_digest"] != g["params_digest"]))
+    self_seg = float((g["self_codes_segments"] == g["codes_segments"]).mean())
+    print(f"{case}: the reference against itself (2048-token chunks): rows departing "
+          f"{int(self_dep.sum())}/{n}, codes equal {float(g['self_codes_equal']):.6f} "
+          f"(>= {self_seg:.6f} by segments)", flush=True)
+    print(f"{case}: sigma rel {srel:.3g}  factor rel {urel:.3g}  rows departing "
+          f"{int(depart.sum())}/{n}  codes equal >= {seg_equal:.6f} (512-column segments)  "
+          f"(ladder {len(lad)}, their d within {max(lad, default=0):.2g} rel., fit gaps "
+          f"<= {max((x['fit_gap'] for x in cls if x['kind'] == 'ladder'), default=0):.2g}; "
+          f"codes alone {n_rnd}; "
+          f"unexplained {sum(not x['explained'] for x in cls)})  "
+          f"total sse rel {sse_rel:.3g}  sse of the rows that stay {sse_keep:.3g}; "
+          f"slice of {r} rows: {msg}", flush=True)
+    assert srel < 1e-5 and urel < WIDE_BAR[case]["u"]
+    assert list(np.nonzero(depart[:r])[0]) == departed  # the digests see what the slice shows
+    for x in divs:
+        assert x["tie"] < (LADDER_TIE if x["kind"] == "ladder" else ROUNDING_TIE), (x, msg)
+    assert all(x["explained"] for x in cls)
+    assert max(lad, default=0) < D_TIE
+    assert seg_equal >= WIDE_BAR[case]["codes_equal"]
+    assert depart.mean() <= WIDE_BAR[case]["rows_departing"]
+    assert sse_keep < 1e-4
+    assert sse_rel < WIDE_BAR[case]["sse_rel"]
 
 
 def test_encode_many_from_the_device_hessian_equals_the_direct_path(dev):
