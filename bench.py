@@ -45,7 +45,7 @@ INPUTS = {"attn": HIDDEN, "o": HIDDEN, "mlp": HIDDEN, "down": INTER}
 INT2_FRAC = 0.30
 DAMP = 0.01
 EFFORT = "normal"
-PEAK_BF16 = 2.5e15  # MI355X dense bf16 MFMA, FLOP/s
+PEAK_BF16 = 2.5e15  # MI355X dense bf16 (and fp16) MFMA, FLOP/s
 PEAK_F32 = 157.3e12  # MI355X dense fp32 MFMA, FLOP/s
 PEAK_HBM = 8.0e12  # B/s
 
@@ -72,38 +72,53 @@ class _DeviceStager:
         return t
 
 
-def make_inputs(dev, seed=0, cfg=CFG3):
+def make_inputs(dev, seed=0, cfg=CFG3, host=False):
     """Calibration tokens (bf16, 1 % x20 outlier channels) per input, bf16 weights
     ~N(0, 0.02^2), and each linear's allocation: a seeded permutation of the rows cut by
     the configuration's fractions; the row lists are kept on the device (rounding) and
-    the host (packing)."""
+    the host (packing).  With ``host`` every tensor is drawn on the host (torch's CPU
+    generator) and copied to the device once, before anything is timed; the host tensors
+    are returned as a fourth value, so that the CPU baseline and the parity check run on
+    exactly the GPU step's inputs."""
     import torch
 
-    g = torch.Generator(device=dev).manual_seed(seed)
-    xs = {}
+    gdev = torch.device("cpu") if host else dev
+    g = torch.Generator(device=gdev).manual_seed(seed)
+    xs, hx, hw = {}, {}, {}
     for name, k in cfg["inputs"].items():
-        x = torch.randn(cfg["tokens"], k, generator=g, device=dev)
-        idx = torch.randperm(k, generator=g, device=dev)[: (k + 99) // 100]
+        x = torch.randn(cfg["tokens"], k, generator=g, device=gdev)
+        idx = torch.randperm(k, generator=g, device=gdev)[: (k + 99) // 100]
         x[:, idx] *= 20.0  # 1 % outlier channels
-        xs[name] = x.to(torch.bfloat16)
+        xb = x.to(torch.bfloat16)
         del x
+        if host:
+            hx[name] = xb
+            xb = xb.to(dev)
+        xs[name] = xb
     ws, masks = {}, {}
     for name, n, k, _ in cfg["linears"]:
-        w = torch.randn(n, k, generator=g, device=dev) * 0.02
-        ws[name] = w.to(torch.bfloat16)
+        w = torch.randn(n, k, generator=g, device=gdev) * 0.02
+        wb = w.to(torch.bfloat16)
         del w
-        perm = torch.randperm(n, generator=g, device=dev)
-        nbits = torch.empty(n, dtype=torch.int64, device=dev)
-        block = torch.empty(n, dtype=torch.int64, device=dev)
+        if host:
+            hw[name] = wb
+            wb = wb.to(dev)
+        ws[name] = wb
+        perm = torch.randperm(n, generator=g, device=gdev)
+        nbits = torch.empty(n, dtype=torch.int64)
+        block = torch.empty(n, dtype=torch.int64)
         groups, lo = [], 0
         for gi, (frac, nb, b) in enumerate(cfg["alloc"]):
             hi = n if gi == len(cfg["alloc"]) - 1 else lo + int(round(frac * n))
             rows = perm[lo:hi].sort().values
-            nbits[rows] = nb
-            block[rows] = b
-            groups.append((nb, b, rows, rows.cpu()))
+            rows_h = rows.cpu()
+            nbits[rows_h] = nb
+            block[rows_h] = b
+            groups.append((nb, b, rows.to(dev), rows_h))
             lo = hi
-        masks[name] = {"groups": groups, "nbits": nbits.cpu(), "block": block.cpu()}
+        masks[name] = {"groups": groups, "nbits": nbits, "block": block}
+    if host:
+        return xs, ws, masks, (hx, hw)
     return xs, ws, masks
 
 
@@ -118,33 +133,55 @@ BACKGROUND = os.environ.get("HI2_BACKGROUND", "1") != "0"
 
 
 def _chain_stream(dev, i):
-    """One persistent stream per chain (reused every step, so each keeps its cached
-    device blocks; the library's own side streams are separate)."""
+    """The stream of chain lane i: lane 0 (the critical chain) runs on the caller's
+    current stream, every other lane on a persistent stream of its own (reused every step,
+    so each keeps its cached device blocks; the library's own side streams are separate).
+    HIP maps streams onto a few hardware queues (four here), and two streams on one queue
+    run in turn: the critical chain measured 24 ms for its factor alone on a queue and
+    29 ms sharing one with another chain, and which pool stream lands on which queue
+    depends on what the process created before.  The current stream's queue held no other
+    stream in every kernel trace, so the critical chain takes it."""
     import torch
 
+    if i == 0:
+        return torch.cuda.current_stream(dev)
     key = (dev.index, i)
     if key not in _CHAIN_STREAMS:
-        st = torch.cuda.Stream(device=dev)
-        if i > 0 and BACKGROUND:  # every chain but the first (the critical path)
-            from hi2_amd import _lib
-
-            _lib.stream_background(st)
-        _CHAIN_STREAMS[key] = st
+        _CHAIN_STREAMS[key] = torch.cuda.Stream(device=dev)
     return _CHAIN_STREAMS[key]
 
 
 def encode_block(xs, ws, masks, timer=None, lanes=None, keep=None, cfg=CFG3):
+    """Encode the whole block (see _encode_block).  Every chain's stream but the first
+    (the critical path) is marked background while the step's work is enqueued, and the
+    marks are cleared once it is (they are read when a launch is enqueued)."""
+    from hi2_amd import _lib
+
+    dev = next(iter(xs.values())).device
+    n_lanes = len(cfg["order"]) if lanes is None else len(lanes)
+    marked = [_chain_stream(dev, i) for i in range(1, n_lanes)] if BACKGROUND else []
+    for st in marked:
+        _lib.stream_background(st, True)
+    try:
+        return _encode_block(xs, ws, masks, timer, lanes, keep, cfg)
+    finally:
+        for st in marked:
+            _lib.stream_background(st, False)
+
+
+def _encode_block(xs, ws, masks, timer=None, lanes=None, keep=None, cfg=CFG3):
     """Encode the whole block.  Each calibration input runs its own chain on its own
     stream (Hessian -> transform -> factor -> rotation -> GPTQ -> packing of the linears
     it feeds); the chains are independent, so they overlap on the GPU.  The first chain
     (the widest input: the critical path) hands its rotations and ladder fits, which need
     only its Hessian's diagonal, to the head of the last chain's stream, where they run
-    while its factor is computed; its rounding waits for them.  The host waits only after every chain has
-    been enqueued (factor status, then one read of the packing's range counter).  keep
-    (a dict) receives each input's (stream, hs, jobs, where, encs)."""
+    while its factor is computed; its rounding waits for them.  Once every chain has ended,
+    one launch packs all linears.  The host waits only after every chain has been enqueued
+    (factor status, then one read of the packing's range counter).  keep (a dict) receives
+    each input's (stream, hs, jobs, where, encs)."""
     import torch
 
-    from hi2_amd.format import assemble, rotate_rows
+    from hi2_amd.format import assemble_many, rotate_rows
     from hi2_amd.hessian import GptqJob, HessianStats, encode_jobs_gptq, prepare_jobs_gptq
     from hi2_amd.hessian import finish_factor, inverse_factor_async, round_prepared
 
@@ -161,7 +198,7 @@ def encode_block(xs, ws, masks, timer=None, lanes=None, keep=None, cfg=CFG3):
     crit = order[0] if len(lanes) > 1 and OFFLOAD_PREP else None
     helper = order[-1] if crit is not None else None
     chains = {}
-    for li in range(len(lanes)):
+    for li in range(1, len(lanes)):  # lane 0 is main itself
         _chain_stream(dev, li).wait_stream(main)
     lead = None  # the first chain's head start: the others wait for its Hessian stages
 
@@ -237,23 +274,28 @@ def encode_block(xs, ws, masks, timer=None, lanes=None, keep=None, cfg=CFG3):
             mark("gptq")
             chains[crit][7] = round_prepared(cprep)
             mark("end")
-    out = {}
     bad = torch.zeros(1, dtype=torch.int32, device=dev)
-    for inp in reversed(order):  # the long chain last: the others are packed meanwhile
+    tensors, names = [], []
+    for inp in reversed(order):  # the long chain last
         st, hs, u, status, had, jobs, where, encs = chains[inp]
         with torch.cuda.stream(st):
             if finish_factor(hs, u, status, DAMP):  # more damping was needed: redo the rounding
                 encs = encode_jobs_gptq(jobs, EFFORT)
-            for name, n, k, i in cfg["linears"]:
-                if i != inp:
-                    continue
-                pieces = [(rows, e.codes, e.params, e.consts)
-                          for (nm, rows), e in zip(where, encs) if nm == name]
-                out[name] = assemble(pieces, masks[name]["nbits"], masks[name]["block"], had, k,
-                                     stager=_DeviceStager, bad=bad)
         main.wait_stream(st)
+        for name, n, k, i in cfg["linears"]:
+            if i != inp:
+                continue
+            pieces = [(rows, e.codes, e.params, e.consts)
+                      for (nm, rows), e in zip(where, encs) if nm == name]
+            tensors.append(dict(pieces=pieces, row_nbits=masks[name]["nbits"],
+                                row_block=masks[name]["block"],
+                                had=torch.ones(k // 16, dtype=torch.uint8), k=k))
+            names.append(name)
         if keep is not None:
             keep[inp] = (st, hs, jobs, where, encs)
+    # every linear of the block packed by one launch, on the main stream once every chain
+    # has ended
+    out = dict(zip(names, assemble_many(tensors, stager=_DeviceStager, bad=bad)))
     if int(bad.item()):
         raise ValueError("code outside the ladder")
     return out
@@ -279,12 +321,13 @@ def stage_breakdown(xs, ws, masks, cfg=CFG3):
     import torch
 
     from hi2_amd import _lib
-    from hi2_amd.format import assemble, rotate_rows
+    from hi2_amd.format import assemble_many, rotate_rows
     from hi2_amd.hessian import GptqJob, HessianStats, encode_jobs_gptq, inverse_factor
 
     dev = next(iter(xs.values())).device
     per_input, per_linear = {}, {}
     hbm = {7: [0.0, 0.0], 9: [0.0, 0.0]}  # kind -> [bytes, ms]
+    tensors = []  # every linear's pieces, packed by one launch at the end (as the step does)
 
     def ev():
         e = torch.cuda.Event(enable_timing=True)
@@ -310,19 +353,19 @@ def stage_breakdown(xs, ws, masks, cfg=CFG3):
         for name, n, kk, i in cfg["linears"]:
             if i != inp:
                 continue
-            kinds = [7, 8, 4, 0, 10, 9]
+            kinds = [7, 8, 4, 0, 10]
             _lib.timing_enable(kinds)
             jobs = [GptqJob(rotate_rows(ws[name], had, rows_d), d, u, nb, b)
                     for nb, b, rows_d, _ in masks[name]["groups"]]
             encs = encode_jobs_gptq(jobs, EFFORT)
-            pieces = [(g[3], e.codes, e.params, e.consts)
-                      for g, e in zip(masks[name]["groups"], encs)]
-            assemble(pieces, masks[name]["nbits"], masks[name]["block"], had, kk,
-                     stager=_DeviceStager)
+            tensors.append(dict(pieces=[(g[3], e.codes, e.params, e.consts)
+                                        for g, e in zip(masks[name]["groups"], encs)],
+                                row_nbits=masks[name]["nbits"], row_block=masks[name]["block"],
+                                had=torch.ones(kk // 16, dtype=torch.uint8), k=kk))
             torch.cuda.synchronize()
             row = {}
             for kind, label in ((7, "rotate"), (8, "ladder_fit"), (4, "column_loop"),
-                                (0, "trailing"), (10, "finish"), (9, "pack")):
+                                (0, "trailing"), (10, "finish")):
                 cnt, ms, work = _lib.timing_query(kind)
                 row[label] = round(ms, 3)
                 if kind in hbm:
@@ -332,6 +375,13 @@ def stage_breakdown(xs, ws, masks, cfg=CFG3):
             _lib.timing_enable([])
             del jobs, encs
         del hs, u, d
+    _lib.timing_enable([9])
+    assemble_many(tensors, stager=_DeviceStager)
+    torch.cuda.synchronize()
+    cnt, ms, work = _lib.timing_query(9)
+    _lib.timing_enable([])
+    hbm[9] = [work, ms]
+    del tensors
     rates = {}
     for kind, kname in ((7, "rotate_rows_kernel"), (9, "assemble_kernel")):
         b, ms = hbm[kind]
@@ -342,7 +392,9 @@ def stage_breakdown(xs, ws, masks, cfg=CFG3):
                             "bytes_per_step": b, "ms_per_step": ms,
                             "work": "rotation: 2 B read (bf16) + 4 B written (f32) per weight "
                             "of the selected rows" if kind == 7
-                            else "pack: code bytes read + packed words + params + consts"}
+                            else "pack (all linears of the step in one launch): code bytes "
+                            "read + packed words written + ladder bytes read and written + "
+                            "consts"}
     return per_input, per_linear, rates
 
 
@@ -358,7 +410,7 @@ def block_leg(cfg, dev, steps, warmup):
     for _ in range(warmup):
         encode_block(xs, ws, masks, cfg=cfg)
     torch.cuda.synchronize()
-    _lib.timing_enable([0, 1, 2])
+    _lib.timing_enable([0, 1, 2, 11])
     t0 = time.perf_counter()
     for _ in range(steps):
         encode_block(xs, ws, masks, cfg=cfg)
@@ -367,6 +419,7 @@ def block_leg(cfg, dev, steps, warmup):
     tr = _lib.timing_query(0)
     sy = _lib.timing_query(1)
     ch = _lib.timing_query(2)
+    sp = _lib.timing_query(11)
     _lib.timing_enable([])
     per_input, per_linear, rates = stage_breakdown(xs, ws, masks, cfg)
     flops = trailing_flops(cfg)
@@ -385,7 +438,8 @@ def block_leg(cfg, dev, steps, warmup):
                               "timing": "event-timed launches in the timed steps (chains "
                                         "concurrent)"},
         "syrk_tflops_executed": sy[2] / sy[1] / 1e9 if sy[1] > 0 else None,
-        "factor_gemm_tflops": ch[2] / ch[1] / 1e9 if ch[1] > 0 else None,
+        "factor_fp32_gemm_tflops": ch[2] / ch[1] / 1e9 if ch[1] > 0 else None,
+        "factor_split_fp16_tflops_executed": sp[2] / sp[1] / 1e9 if sp[1] > 0 else None,
         "stages_serial_ms": {"per_input": per_input, "per_linear": per_linear},
         "hbm_kernels": rates,
     }
@@ -487,25 +541,34 @@ def encode_moe(idx, x, xd, wgu, wdn, masks, timer=None):
             where.append([((e, "down"), rows_h, 0, rows_h.numel())])
     mark("moe", "gptq")
     encs = encode_jobs_gptq(jobs, EFFORT)
+    bad = torch.zeros(1, dtype=torch.int32, device=dev)
+    flags = {H5: torch.ones(H5 // 16, dtype=torch.uint8), I5: torch.ones(I5 // 16, dtype=torch.uint8)}
+
+    def pack(encs):
+        """The 192 expert tensors' packing, enqueued behind the rounding (the host builds
+        its tables while the GPU rounds)."""
+        by = {}
+        for parts, enc in zip(where, encs):
+            for key, rows_h, a, z in parts:
+                by.setdefault(key, []).append((rows_h, enc.codes[a:z], enc.params[a:z],
+                                               enc.consts[a:z]))
+        keys = list(by)
+        packed = assemble_many([dict(pieces=by[key], row_nbits=masks[key]["nbits"],
+                                     row_block=masks[key]["block"],
+                                     had=flags[H5 if key[1] != "down" else I5],
+                                     k=H5 if key[1] != "down" else I5) for key in keys],
+                               stager=_DeviceStager, bad=bad)
+        return dict(zip(keys, packed))
+
     mark("moe", "pack")
+    out = pack(encs)
+    mark("moe", "end")
+    # the factor statuses are read only now (the read waits for the work enqueued so far)
     redo = finish_factors_batched(hs_g, u_g, st_g, DAMP) + finish_factors_batched(hs_d, u_d, st_d,
                                                                                    DAMP)
     if redo:  # an expert needed more damping: its rows again (the reference's retry)
-        encs = encode_jobs_gptq(jobs, EFFORT)
-    bad = torch.zeros(1, dtype=torch.int32, device=dev)
-    by = {}
-    for parts, enc in zip(where, encs):
-        for key, rows_h, a, z in parts:
-            by.setdefault(key, []).append((rows_h, enc.codes[a:z], enc.params[a:z],
-                                           enc.consts[a:z]))
-    keys = list(by)
-    packed = assemble_many([dict(pieces=by[key], row_nbits=masks[key]["nbits"],
-                                 row_block=masks[key]["block"],
-                                 had=had_h if key[1] != "down" else had_i,
-                                 k=H5 if key[1] != "down" else I5) for key in keys],
-                           stager=_DeviceStager, bad=bad)
-    out = dict(zip(keys, packed))
-    mark("moe", "end")
+        bad.zero_()
+        out = pack(encode_jobs_gptq(jobs, EFFORT))
     if int(bad.item()):
         raise ValueError("code outside the ladder")
     return out
@@ -521,13 +584,13 @@ def moe_leg(dev, steps, warmup):
     for _ in range(warmup):
         encode_moe(*inp)
     torch.cuda.synchronize()
-    _lib.timing_enable([0, 1, 2, 3])
+    _lib.timing_enable([0, 1, 2, 3, 11])
     t0 = time.perf_counter()
     for _ in range(steps):
         encode_moe(*inp)
     torch.cuda.synchronize()
     ms = (time.perf_counter() - t0) * 1e3 / steps
-    tr, sy, ch, lf = (_lib.timing_query(k) for k in (0, 1, 2, 3))
+    tr, sy, ch, lf, sp = (_lib.timing_query(k) for k in (0, 1, 2, 3, 11))
     _lib.timing_enable([])
     timer = StageTimer(torch)
     encode_moe(*inp, timer=timer)
@@ -558,7 +621,7 @@ def moe_leg(dev, steps, warmup):
                               "flops_per_step": flops, "launches_per_step": tr[0] // steps},
         "grouped_syrk": {"launches_per_step": sy[0] // steps, "ms_per_step": sy[1] / steps,
                          "tflops_executed": sy[2] / sy[1] / 1e9 if sy[1] > 0 else None},
-        "factor_ms_per_step_kernels": (ch[1] + lf[1]) / steps,
+        "factor_ms_per_step_kernels": (ch[1] + lf[1] + sp[1]) / steps,
     }
     del inp
     torch.cuda.empty_cache()
@@ -581,7 +644,8 @@ def refine_linears(kept):
     out = {}
     for inp in CFG3["order"]:
         st, hs, jobs, where, encs = kept[inp]
-        st.wait_stream(main)
+        if st != main:
+            st.wait_stream(main)
         with torch.cuda.stream(st):
             for name, n, k, i in LINEARS:
                 if i != inp:
@@ -591,7 +655,8 @@ def refine_linears(kept):
                     [(jobs[x].w, encs[x], jobs[x].nbits, jobs[x].block) for x in xs], hs,
                     REFINE_PASSES)
     for inp in CFG3["order"]:
-        main.wait_stream(kept[inp][0])
+        if kept[inp][0] != main:
+            main.wait_stream(kept[inp][0])
     return out
 
 
@@ -647,7 +712,11 @@ class StageTimer:
 KERNELS = {  # kind -> (kernel, bound, peak FLOP/s, work unit)
     0: ("gptq_trailing_kernel", "mfma", PEAK_F32, "2*rows*rank*cols"),
     1: ("syrk2_bf16_kernel", "mfma", PEAK_BF16, "T*K*(K+1) (upper triangle, 2 flops per product)"),
-    2: ("tri_gemm_kernel", "mfma", PEAK_F32, "M*N*rank (one triangular operand)"),
+    2: ("tri_gemm_kernel", "mfma", PEAK_F32, "M*N*rank (one triangular operand; the "
+        "factor's fp32 MFMA products)"),
+    11: ("gemm3_kernel/gemm3x_kernel (split planes)", "mfma", PEAK_BF16,
+         "3*M*N*rank fp16 MFMA flops executed (three fp16 products per fp32-equivalent "
+         "product of one triangular operand)"),
     3: ("leaf_kernel", "latency", PEAK_F32, "2*n^3/3"),
     4: ("gptq_block_kernel", "latency", PEAK_F32, "rows*L*(L-1)"),
     5: ("refine GEMMs (refine_gradient_kernel + gptq_trailing_kernel)", "mfma", PEAK_F32,
@@ -707,19 +776,26 @@ def _cpu_info():
             "parallel_info": [l.strip() for l in par.splitlines() if l.strip()][:8]}
 
 
-def _torch_cpu_block(R, cfg, seed):
+def _torch_cpu_block(R, cfg, seed, host=None, keep=None):
     """The reference's CPU path (oracle/torch_cpu.py) on a whole configuration: per input
     its Hessian (fp32 chunks), transform and factor; per linear rotation, GPTQ of every
-    allocation group and packing.  Returns seconds per stage."""
+    allocation group and packing.  Returns seconds per stage.  ``host`` = (calibration
+    tokens, weights, allocation) runs it on given host tensors (the GPU step's own
+    inputs); otherwise it draws its own from ``seed``.  ``keep`` (a dict) receives, per
+    input, Sigma, Hs and U, and per linear and allocation group its rotated rows, codes,
+    ladder bytes, consts, sse and comp (numpy), for the parity check."""
     import torch
 
     g = torch.Generator().manual_seed(seed)
     parts = {"hessian": 0.0, "transform": 0.0, "factor": 0.0, "rotate": 0.0, "gptq": 0.0,
              "pack": 0.0}
     for inp, k in cfg["inputs"].items():
-        x = torch.randn(cfg["tokens"], k, generator=g)
-        x[:, torch.randperm(k, generator=g)[: (k + 99) // 100]] *= 20.0
-        x = x.to(torch.bfloat16)
+        if host is None:
+            x = torch.randn(cfg["tokens"], k, generator=g)
+            x[:, torch.randperm(k, generator=g)[: (k + 99) // 100]] *= 20.0
+            x = x.to(torch.bfloat16)
+        else:
+            x = host[0][inp]
         flags = torch.ones(k // 16, dtype=torch.uint8)
         t0 = time.perf_counter()
         sigma = R.hessian_sum(x) / x.shape[0]
@@ -732,28 +808,42 @@ def _torch_cpu_block(R, cfg, seed):
         parts["transform"] += t2 - t1
         parts["factor"] += t3 - t2
         d = hs.diagonal().clone()
+        if keep is not None:
+            keep.setdefault("inputs", {})[inp] = {"sigma": sigma.numpy(), "hs": hs.numpy(),
+                                                  "u": u.numpy()}
         del x, sigma
         for name, n, kk, i in cfg["linears"]:
             if i != inp:
                 continue
-            w = (torch.randn(n, kk, generator=g) * 0.02).to(torch.bfloat16)
-            perm = torch.randperm(n, generator=g)
+            if host is None:
+                w = (torch.randn(n, kk, generator=g) * 0.02).to(torch.bfloat16)
+                perm = torch.randperm(n, generator=g)
+                rows_of, lo = [], 0
+                for gi, (frac, nb, b) in enumerate(cfg["alloc"]):
+                    hi = n if gi == len(cfg["alloc"]) - 1 else lo + int(round(frac * n))
+                    rows_of.append((nb, b, perm[lo:hi].sort().values))
+                    lo = hi
+            else:
+                w = host[1][name]
+                rows_of = [(nb, b, rows_h) for nb, b, _, rows_h in host[2][name]["groups"]]
             t0 = time.perf_counter()
             wt = R.rotate(w.float(), flags)
             t1 = time.perf_counter()
-            lo, packed = 0, []
             tg = tp = 0.0
-            for gi, (frac, nb, b) in enumerate(cfg["alloc"]):
-                hi = n if gi == len(cfg["alloc"]) - 1 else lo + int(round(frac * n))
-                rows = perm[lo:hi].sort().values
-                lo = hi
+            for nb, b, rows in rows_of:
                 s0 = time.perf_counter()
-                codes = R.gptq(wt[rows], d, u, nb, b, EFFORT)[0]
+                codes, prm, cst, sse, comp = R.gptq(wt[rows], d, u, nb, b, EFFORT)
                 s1 = time.perf_counter()
-                packed.append(R.pack_codes(codes, nb))
+                R.pack_codes(codes, nb)
                 s2 = time.perf_counter()
                 tg += s1 - s0
                 tp += s2 - s1
+                if keep is not None:
+                    keep.setdefault("linears", {}).setdefault(name, []).append({
+                        "nb": nb, "b": b, "rows": rows.numpy(), "wt": wt[rows].numpy(),
+                        "codes": codes.numpy(), "params": prm.numpy(),
+                        "consts": cst.view(torch.int16).numpy().view("uint16"),
+                        "sse": sse.numpy(), "comp": comp.numpy()})
             parts["rotate"] += t1 - t0
             parts["gptq"] += tg
             parts["pack"] += tp
@@ -765,10 +855,12 @@ CFG1 = dict(name="cfg1", tokens=512, linears=[("linear", 2048, 2048, "x")],
             inputs={"x": 2048}, alloc=[(1.0, 4, 64)])
 
 
-def cpu_baseline(seed=0, which=("cfg1", "cfg3")):
+def cpu_baseline(seed=0, which=("cfg1", "cfg3"), host=None, keep=None):
     """The reference's own CPU path (restated in torch: oracle/torch_cpu.py, bit-identical
     to the reference on its fixtures) timed on this host's cores, on cfg1 and cfg3 in
-    full.  value: cfg3 ms per linear (the metric of the GPU line)."""
+    full.  value: cfg3 ms per linear (the metric of the GPU line).  ``host``: cfg3's
+    inputs as the GPU step drew them (see make_inputs); ``keep`` receives cfg3's outputs
+    (see _torch_cpu_block)."""
     import torch
 
     from oracle import torch_cpu as R
@@ -779,7 +871,8 @@ def cpu_baseline(seed=0, which=("cfg1", "cfg3")):
         if name not in which:
             continue
         t0 = time.perf_counter()
-        parts = _torch_cpu_block(R, cfg, seed)
+        parts = _torch_cpu_block(R, cfg, seed, host if name == "cfg3" else None,
+                                 keep if name == "cfg3" else None)
         wall = time.perf_counter() - t0
         out[name] = {"s_total": round(wall, 2),
                      "ms_per_linear": wall * 1e3 / len(cfg["linears"]),
@@ -788,9 +881,104 @@ def cpu_baseline(seed=0, which=("cfg1", "cfg3")):
     out["value"] = main["ms_per_linear"]
     out["sample"] = ("the reference's CPU path (torch ops of hi2/hessian.py, hi2/encode.py, "
                      "hi2/format.py restated in oracle/torch_cpu.py) on "
-                     + " and ".join(w for w in which) + " in full, no extrapolation; value "
-                     "is " + ("cfg3" if "cfg3" in out else "cfg1") + " ms per linear")
+                     + " and ".join(w for w in which) + " in full, no extrapolation"
+                     + ("; cfg3 on the GPU step's own inputs (drawn on the host, copied to "
+                        "the device before the timed region)" if host is not None else "")
+                     + "; value is " + ("cfg3" if "cfg3" in out else "cfg1")
+                     + " ms per linear")
     return out
+
+
+def gpu_outputs(xs, ws, masks, cfg=CFG3):
+    """The step's outputs for the parity check, on the host: one more (untimed) step with
+    every chain's Hs, factor and encodings kept, the rounding run again with comp on (the
+    same codes: comp only records the values the codes were rounded from), and each
+    input's Sigma."""
+    import torch
+
+    from hi2_amd.hessian import HessianStats, encode_jobs_gptq
+
+    dev = next(iter(xs.values())).device
+    kept = {}
+    encode_block(xs, ws, masks, keep=kept, cfg=cfg)
+    out = {"inputs": {}, "linears": {}}
+    for inp, k in cfg["inputs"].items():
+        _, hs, jobs, where, encs = kept.pop(inp)
+        hst = HessianStats(k, dev)
+        hst.update(xs[inp])
+        out["inputs"][inp] = {"sigma": hst.mean().cpu().numpy(), "hs": hs.cpu().numpy(),
+                              "u": jobs[0].u.cpu().numpy()}
+        del hst
+        with_comp = encode_jobs_gptq(jobs, EFFORT, comp=True)
+        for (name, rows_h), job, e, ec in zip(where, jobs, encs, with_comp):
+            if not torch.equal(e.codes, ec.codes):
+                raise RuntimeError(f"{name}: codes changed with comp on")
+            out["linears"].setdefault(name, []).append({
+                "nb": job.nbits, "b": job.block, "rows": rows_h.numpy(),
+                "codes": e.codes.cpu().numpy(), "params": e.params.cpu().numpy(),
+                "consts": e.consts.view(torch.int16).cpu().numpy().view("uint16"),
+                "sse": e.sse.cpu().numpy(), "comp": ec.comp.cpu().numpy()})
+        del hs, jobs, encs, with_comp
+    torch.cuda.synchronize()
+    return out
+
+
+def parity(gpu, cpu, cfg=CFG3):
+    """The GPU step's cfg3 encoding against the reference's CPU path on the same inputs:
+    Sigma, Hs and U relative to the largest entry, and per linear the share of equal
+    codes, every departing row classified as a ladder or a rounding tie with its distance,
+    and the sse (oracle/parity.py: compare_groups)."""
+    import numpy as np
+
+    from oracle.parity import compare_groups
+
+    res = {"against": "the reference's CPU path (oracle/torch_cpu.py; bit-identical to the "
+                      "reference on its fixtures at their thread count) on the same "
+                      "host-drawn inputs, with this host's torch threads",
+           "inputs": {}, "linears": {}}
+    for inp in cfg["inputs"]:
+        o, r = gpu["inputs"][inp], cpu["inputs"][inp]
+        res["inputs"][inp] = {
+            f"{m}_rel": float(np.abs(o[m] - r[m]).max() / np.abs(r[m]).max())
+            for m in ("sigma", "hs", "u")}
+    equal = total = dep = nl = nr = 0
+    tie_q = tie_d = 0.0
+    stay = 0.0
+    sse_o = sse_r = 0.0
+    for name, n, k, inp in cfg["linears"]:
+        d_o = np.diag(gpu["inputs"][inp]["hs"]).copy()
+        d_r = np.diag(cpu["inputs"][inp]["hs"]).copy()
+        groups = []
+        for go, gr in zip(gpu["linears"][name], cpu["linears"][name]):
+            if (go["nb"], go["b"]) != (gr["nb"], gr["b"]) or not np.array_equal(go["rows"],
+                                                                               gr["rows"]):
+                raise RuntimeError(f"{name}: allocation groups differ")
+            groups.append({"wt": gr["wt"], "o": go, "r": gr, "d_o": d_o, "d_r": d_r,
+                           "nbits": go["nb"], "block": go["b"]})
+        c = compare_groups(groups)
+        res["linears"][name] = c
+        equal += c["codes_equal"] * c["codes"]
+        total += c["codes"]
+        dep += c["rows_departing"]
+        nl += c["ladder"]["rows"]
+        nr += c["rounding"]["rows"]
+        tie_q = max(tie_q, c["rounding"]["max_quotient_distance_steps"])
+        tie_d = max(tie_d, c["ladder"]["max_d_rel"])
+        stay = max(stay, c["sse_rel_max_rows_that_stay"])
+        so = sum(float(x["sse"].astype(np.float64).sum()) for x in gpu["linears"][name])
+        sr = sum(float(x["sse"].astype(np.float64).sum()) for x in cpu["linears"][name])
+        sse_o += so
+        sse_r += sr
+    res["codes_equal"] = equal / total
+    res["rows"] = sum(n for _, n, _, _ in cfg["linears"])
+    res["rows_departing"] = dep
+    res["ladder_rows"] = nl
+    res["rounding_rows"] = nr
+    res["max_rounding_tie_steps"] = tie_q
+    res["max_ladder_d_rel"] = tie_d
+    res["sse_rel_total"] = abs(sse_o / sse_r - 1)
+    res["sse_rel_max_rows_that_stay"] = stay
+    return res
 
 
 def micro(which, reps=3):
@@ -895,7 +1083,7 @@ def micro(which, reps=3):
     elif which == "factor":
         for k in (INTER, HIDDEN):
             hs, _ = hessian(k)
-            ms, stats = timed(lambda: inverse_factor(hs, DAMP), [2, 3])
+            ms, stats = timed(lambda: inverse_factor(hs, DAMP), [2, 3, 11])
             print(json.dumps({"micro": "factor", "k": k, "ms": ms, "kernels": stats}),
                   flush=True)
     elif which == "refine":
@@ -1040,7 +1228,9 @@ def main():
             dst.copy_(src)
         torch.cuda.synchronize()
         del src, dst
-    xs, ws, masks = make_inputs(dev)
+    # cfg3's inputs drawn once on the host and copied to the device before anything is
+    # timed: the CPU baseline and the parity check run on these same tensors
+    xs, ws, masks, host = make_inputs(dev, host=True)
     torch.cuda.synchronize()
     for _ in range(args.warmup):
         encode_block(xs, ws, masks)
@@ -1069,6 +1259,7 @@ def main():
                                  "another on one stream")
     _lib.timing_enable([])
     per_input, per_linear, hbm = stage_breakdown(xs, ws, masks)
+    gpu_out = None if args.no_cpu else gpu_outputs(xs, ws, masks)
     refine = None
     if args.refine_steps:
         kept = {}
@@ -1133,7 +1324,7 @@ def main():
             "d2h_bytes": d2h,
         }
         del reqs, packed
-    del xs, ws, masks
+    del xs, ws
     torch.cuda.empty_cache()
     cfg4 = block_leg(CFG4, dev, args.cfg4_steps, 1) if args.cfg4_steps else None
     cfg5 = moe_leg(dev, args.cfg5_steps, 1) if args.cfg5_steps else None
@@ -1149,7 +1340,8 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f32",
-        "data": "synthetic (seeded normal X with 1% x20 outlier channels, W ~ N(0, 0.02^2))",
+        "data": "synthetic (seeded normal X with 1% x20 outlier channels, W ~ N(0, 0.02^2), "
+                "drawn on the host and resident in HBM before the timed region)",
         "config": {"workload": "cfg3: Llama-3-8B-shaped decoder block, 8192 calibration "
                                "tokens, 30% INT2/B32 + 70% INT4/B64 rows, order-16 Hadamard, "
                                "damp 0.01, effort normal", "linears": len(LINEARS),
@@ -1170,7 +1362,10 @@ def main():
     if cfg5 is not None:
         res["cfg5"] = cfg5
     if not args.no_cpu:
-        res["cpu_baseline"] = cpu_baseline()
+        cpu_out = {}
+        res["cpu_baseline"] = cpu_baseline(host=(host[0], host[1], masks), keep=cpu_out)
+        res["parity"] = parity(gpu_out, cpu_out)
+        del cpu_out, gpu_out
     print(json.dumps(res), flush=True)
 
 

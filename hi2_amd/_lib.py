@@ -146,7 +146,7 @@ def lib():
 # launch-timing kinds (HI2X_TIME_* in include/hi2x.h)
 (TIME_GPTQ_TRAILING, TIME_HESSIAN_SYRK, TIME_CHOL_GEMM, TIME_CHOL_LEAF, TIME_GPTQ_BLOCK,
  TIME_REFINE_GEMM, TIME_REFINE_BLOCK, TIME_FWHT, TIME_LADDER_FIT, TIME_PACK,
- TIME_FINISH) = range(11)
+ TIME_FINISH, TIME_CHOL_SPLIT) = range(12)
 
 
 def timing_enable(kinds) -> None:

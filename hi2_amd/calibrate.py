@@ -254,17 +254,22 @@ def _on_device(reqs, cfg, ex, i: int, use_gptq, comp_full, pack=None):
     as its chain is finished, while later chains still run."""
     dev = _device(ex.devices[i])
     main = torch.cuda.current_stream(dev)
-    lanes = [_lib.side_stream(dev, 64 + j) for j in range(LANES)]
-    for j, st in enumerate(lanes):
+    # lane 0 takes the widest input (the critical path) on the caller's stream, the others
+    # persistent side streams.  HIP maps streams onto a few hardware queues and two streams
+    # on one queue run in turn; the caller's stream had its queue to itself in every kernel
+    # trace, while which queue a side stream lands on depends on what the process created
+    # before it (the critical chain sharing one cost 20 % of the block's encode).  The
+    # other lanes are marked background: their GPTQ updates leave room on the CUs for the
+    # critical chain's latency-bound kernels.
+    lanes = [main] + [_lib.side_stream(dev, 64 + j) for j in range(1, LANES)]
+    for st in lanes[1:]:
         st.wait_stream(main)
-        # lane 0 takes the widest input (the critical path): the others' GPTQ updates
-        # leave room on the CUs for its latency-bound kernels
-        _lib.stream_background(st, j > 0)
+        _lib.stream_background(st, True)
     try:
         return _enqueue(reqs, cfg, ex, i, use_gptq, comp_full, pack, dev, main, lanes)
     finally:
         # the marks are read when a launch is enqueued: every chain is enqueued now
-        for st in lanes:
+        for st in lanes[1:LANES]:
             _lib.stream_background(st, False)
 
 
@@ -338,8 +343,12 @@ def _enqueue(reqs, cfg, ex, i, use_gptq, comp_full, pack, dev, main, lanes):
             for ri in groups[fk]:
                 stage(ri, st, emit)
             _round_chain(ch, reqs, jobs, job_at, encs, cfg)
-        # nearest rows (hi2/encode.py:133-173: ladder fit, params, codes, sse) on the
-        # caller's stream
+        # nearest rows (hi2/encode.py:133-173: ladder fit, params, codes, sse) on a side
+        # stream of their own (the caller's carries the critical chain)
+        near_st = _lib.side_stream(dev, 64 + LANES)
+        near_st.wait_stream(main)
+        lanes.append(near_st)
+
         def emit_near(ri, r, had):
             k = r.table.shape[1]
             d = _weights(r.stats, k, had, dev, _inv_scale(r.table.col_scale))
@@ -352,10 +361,10 @@ def _enqueue(reqs, cfg, ex, i, use_gptq, comp_full, pack, dev, main, lanes):
             return add
 
         for ri in near:
-            stage(ri, main, emit_near)
+            stage(ri, near_st, emit_near)
         if pack is not None:
             for ri in near:
-                pack(ri, pieces[ri], main)
+                pack(ri, pieces[ri], near_st)
         # the host waits for each chain's factor status only now, the chain enqueued last
         # (the first to end) first; a chain whose first attempt failed (the reference's
         # damping retries) is rounded and refined again; then its tensors are packed

@@ -435,7 +435,7 @@ __device__ __forceinline__ void gemm3_tile(const G3Args& g0, G3Stage& SA, G3Stag
   auto dma_one = [&](int j, int64_t k0, int buf, bool live) {
     const int opd = j / G3_NP, pl = j % G3_NP;
     const int row = 32 * wv + prow;
-    // chunk k0 / 16 of the tile's rows: rows x 16 contiguous bf16
+    // chunk k0 / 16 of the tile's rows: rows x 16 contiguous fp16
     const uint16_t* base = opd == 0 ? g.A + pl * plA + ((k0 >> 4) * g.M + r0) * G3_KC
                                     : g.B + pl * plB + ((k0 >> 4) * g.N + c0) * G3_KC;
     const int rows = opd == 0 ? rowsA : rowsB;
@@ -861,7 +861,7 @@ int gemm3(const G3Args& a, hipStream_t s, int batch = 1) {
     if (live2 >= 256 && chol_tile256()) return gemm3x<AMODE, BMODE, CLOW>(a, s, batch);
   }
   const int64_t tm = (a.M + MG_T - 1) / MG_T, tn = (a.N + MG_T - 1) / MG_T;
-  LaunchTimer timer(HI2X_TIME_CHOL_GEMM, (double)a.M * a.N * a.Kd * batch, s);
+  LaunchTimer timer(HI2X_TIME_CHOL_SPLIT, 3.0 * a.M * a.N * a.Kd * batch, s);
   MgSched sched = mg_balance(tm, tn, [&](int64_t sr, int64_t sc) {
     double w = 0.0;
     for (int64_t i = 0; i < MG_SUP; ++i)
@@ -890,7 +890,7 @@ static bool chol_tile256() {
 template <int AMODE, int BMODE, bool CLOW>
 int gemm3x(const G3Args& a, hipStream_t s, int batch) {
   const int64_t tm = (a.M + GX_T - 1) / GX_T, tn = (a.N + GX_T - 1) / GX_T;
-  LaunchTimer timer(HI2X_TIME_CHOL_GEMM, (double)a.M * a.N * a.Kd * batch, s);
+  LaunchTimer timer(HI2X_TIME_CHOL_SPLIT, 3.0 * a.M * a.N * a.Kd * batch, s);
   MgSched sched = mg_balance(tm, tn, [&](int64_t sr, int64_t sc) {
     double w = 0.0;
     for (int64_t i = 0; i < GX_SUP; ++i)
@@ -981,8 +981,8 @@ int g3_pair(const G3Args& a1, const G3Args& a2, hipStream_t s, int batch) {
   for (int x = 0; x < 8; ++x)
     for (int j = 0; j < per; ++j)
       sched.st[x * per + j] = j < (int)lists[x].size() ? (uint16_t)lists[x][j] : (uint16_t)0xffff;
-  LaunchTimer timer(HI2X_TIME_CHOL_GEMM,
-                    ((double)a1.M * a1.N * a1.Kd + (double)a2.M * a2.N * a2.Kd) * batch, s);
+  LaunchTimer timer(HI2X_TIME_CHOL_SPLIT,
+                    3.0 * ((double)a1.M * a1.N * a1.Kd + (double)a2.M * a2.N * a2.Kd) * batch, s);
   const int64_t grid = (int64_t)8 * per * SUP * SUP;
   if constexpr (T == GX_T) {
     hipLaunchKernelGGL((gemm3x_pair_kernel<A1, B1, C1, A2, B2, C2>),
@@ -997,8 +997,8 @@ int g3_pair(const G3Args& a1, const G3Args& a2, hipStream_t s, int batch) {
   }
 }
 
-// Products of the big grids: bf16 MFMA on split planes (default), or the fp32 MFMA GEMM
-// when HI2X_CHOL_FP32 is set to a nonzero value (read once per process).
+// Products of the big grids: fp16 MFMA on the two scaled split planes (default), or the
+// fp32 MFMA GEMM when HI2X_CHOL_FP32 is set to a nonzero value (read once per process).
 static bool chol_split() {
   static const bool split = [] {
     const char* e = getenv("HI2X_CHOL_FP32");
@@ -1737,7 +1737,7 @@ int product(const Ctx& c, GemmArgs a) {
   const int64_t Kp = (a.Kd + G3_KA - 1) / G3_KA * G3_KA;
   uint16_t* pa = reinterpret_cast<uint16_t*>(c.ws + c.plan->pa_off);
   uint16_t* pb = reinterpret_cast<uint16_t*>(c.ws + c.plan->pb_off);
-  const int64_t sPl = 2 * c.sW;  // planes live in the workspace (bf16 elements)
+  const int64_t sPl = 2 * c.sW;  // planes live in the workspace (16-bit elements)
   const SplitOp oa{a.A, a.lda, a.M, a.Kd, Kp, a.sA, sPl, 0, AMODE == 1 ? 1 : 0, pa};
   const SplitOp ob{a.B, a.ldb, a.N, a.Kd, Kp, a.sB, sPl, TB ? 0 : 1, split_mask_b(BMODE), pb};
   // B is A itself in the symmetric update: one operand's planes serve both
@@ -1863,7 +1863,9 @@ static Plan make_plan(int64_t k) {
     plan.t2_off.push_back(off);
     off += (sz + 63) / 64 * 64;
   }
-  // split planes: 3 x rows x Kp bf16 for the largest operand of the top-level products
+  // split planes: 3 x rows x Kp 16-bit values for the largest operand of the top-level
+  // products (split2_kernel's layout: two fp16 planes, then the inverse row scales and
+  // the row-maximum partials in fp32)
   int64_t m1 = 0;
   if (k > NB) {
     const int64_t nbk = (k + NB - 1) / NB;

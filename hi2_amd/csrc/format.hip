@@ -171,46 +171,109 @@ __global__ __launch_bounds__(256) void pack_kernel(const uint8_t* __restrict__ c
   note_bad(bad, nbad);
 }
 
-// assemble, one piece: thread (i, wi) packs word wi of piece row i into the flat
-// buffer at code_off[rows[i]] + wi; threads (i, b) with b < nblk copy the two bytes
-// of block b to param_off[rows[i]] + b; thread (i, 0) copies the row constants.
-__global__ __launch_bounds__(256) void assemble_kernel(
-    const int64_t* __restrict__ rows, int64_t r, const uint8_t* __restrict__ codes,
-    const uint8_t* __restrict__ params, const uint16_t* __restrict__ consts, int64_t k,
-    int nbits, int64_t nblk, const int64_t* __restrict__ code_off,
-    const int64_t* __restrict__ param_off, int32_t* __restrict__ out_codes,
-    uint8_t* __restrict__ out_params, uint16_t* __restrict__ out_consts,
-    int32_t* __restrict__ bad) {
-  const int per = 32 / nbits;
-  const int64_t nw = k / per;
-  const int64_t span = nw > nblk ? nw : nblk;
-  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (t >= r * span) return;
-  const int64_t i = t / span, j = t % span;
-  const int64_t row = rows[i];
-  if (j < nw) {
-    const uint8_t* c = codes + i * k + j * per;
-    const uint32_t lim = 1u << nbits;
-    uint32_t v = 0;
-    int nbad = 0;
-    for (int q = 0; q < per; ++q) {
-      const uint32_t cv = c[q];
-      nbad += cv >= lim;
-      v |= (cv & (lim - 1u)) << (nbits * q);
+// assemble (hi2/format.py:155-171): the pieces of one or more tensors in one launch.
+// Each piece is a group of rows sharing (nbits, B); its descriptor travels in the kernel
+// arguments (up to kPackPieces per launch) with the first workgroup of every piece.  A
+// workgroup covers 256 consecutive items of one row of one piece: item j packs word j
+// of the row (32/nbits codes, LSB first, from one 4-, 8- or 16-byte load) into the flat
+// buffer at code_off[rows[i]] + j, moves the row's ladder bytes of block j (one 16-bit
+// pair) to param_off[rows[i]] + j, and items 0..2 of the row's first workgroup move its
+// three constants.  Codes at or above 2^nbits are counted in bad (packed masked).
+constexpr int kPackPieces = 24;
+struct PackPiece {
+  const int64_t* rows;
+  const uint8_t* codes;
+  const uint8_t* params;
+  const uint16_t* consts;
+  const int64_t* code_off;
+  const int64_t* param_off;
+  int32_t* out_codes;
+  uint8_t* out_params;
+  uint16_t* out_consts;
+  int32_t k, nbits, nblk, nw, chunks;  // chunks: workgroups per row
+  int32_t vec;                         // bit 0: 16-byte code rows, bit 1: 2-byte params
+};
+struct PackBatch {
+  PackPiece p[kPackPieces];
+  int32_t wg_start[kPackPieces + 1];
+  int32_t n;
+};
+
+template <int PER>
+__device__ __forceinline__ uint32_t pack_word(const uint32_t (&x)[PER / 4], int nbits,
+                                              int& nbad) {
+  const uint32_t lim = 1u << nbits;
+  uint32_t v = 0;
+#pragma unroll
+  for (int q = 0; q < PER; ++q) {
+    const uint32_t cv = (x[q / 4] >> (8 * (q % 4))) & 0xffu;
+    nbad += cv >= lim;
+    v |= (cv & (lim - 1u)) << (nbits * q);
+  }
+  return v;
+}
+
+__global__ __launch_bounds__(256) void assemble_batch_kernel(const PackBatch b,
+                                                             int32_t* __restrict__ bad) {
+  const int wg = blockIdx.x;
+  int pi = 0;
+  while (pi + 1 < b.n && wg >= b.wg_start[pi + 1]) ++pi;  // uniform: scalar registers
+  const PackPiece& p = b.p[pi];
+  const int local = wg - b.wg_start[pi];
+  const int i = local / p.chunks, part = local - i * p.chunks;
+  const int j = part * 256 + (int)threadIdx.x;
+  const int64_t row = p.rows[i];
+  int nbad = 0;
+  if (j < p.nw) {
+    const uint8_t* c = p.codes + (int64_t)i * p.k;
+    uint32_t v;
+    if (p.nbits == 2) {
+      uint32_t x[4];
+      if (p.vec & 1) {
+        const uint4 y = reinterpret_cast<const uint4*>(c)[j];
+        x[0] = y.x, x[1] = y.y, x[2] = y.z, x[3] = y.w;
+      } else {
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          x[q] = c[16 * j + 4 * q] | (c[16 * j + 4 * q + 1] << 8) |
+                 (c[16 * j + 4 * q + 2] << 16) | ((uint32_t)c[16 * j + 4 * q + 3] << 24);
+      }
+      v = pack_word<16>(x, 2, nbad);
+    } else if (p.nbits == 4) {
+      uint32_t x[2];
+      if (p.vec & 1) {
+        const uint2 y = reinterpret_cast<const uint2*>(c)[j];
+        x[0] = y.x, x[1] = y.y;
+      } else {
+#pragma unroll
+        for (int q = 0; q < 2; ++q)
+          x[q] = c[8 * j + 4 * q] | (c[8 * j + 4 * q + 1] << 8) |
+                 (c[8 * j + 4 * q + 2] << 16) | ((uint32_t)c[8 * j + 4 * q + 3] << 24);
+      }
+      v = pack_word<8>(x, 4, nbad);
+    } else {
+      uint32_t x[1];
+      if (p.vec & 1)
+        x[0] = reinterpret_cast<const uint32_t*>(c)[j];
+      else
+        x[0] = c[4 * j] | (c[4 * j + 1] << 8) | (c[4 * j + 2] << 16) |
+               ((uint32_t)c[4 * j + 3] << 24);
+      v = pack_word<4>(x, 8, nbad);
     }
-    out_codes[code_off[row] + j] = (int32_t)v;
-    note_bad(bad, nbad);
+    p.out_codes[p.code_off[row] + j] = (int32_t)v;
   }
-  if (j < nblk) {
-    const int64_t dst = (param_off[row] + j) * 2;
-    out_params[dst] = params[(i * nblk + j) * 2];
-    out_params[dst + 1] = params[(i * nblk + j) * 2 + 1];
+  if (j < p.nblk) {
+    const int64_t src = (int64_t)i * p.nblk + j, dst = p.param_off[row] + j;
+    if (p.vec & 2) {
+      reinterpret_cast<uint16_t*>(p.out_params)[dst] =
+          reinterpret_cast<const uint16_t*>(p.params)[src];
+    } else {
+      p.out_params[2 * dst] = p.params[2 * src];
+      p.out_params[2 * dst + 1] = p.params[2 * src + 1];
+    }
   }
-  if (j == 0) {
-    out_consts[row * 3 + 0] = consts[i * 3 + 0];
-    out_consts[row * 3 + 1] = consts[i * 3 + 1];
-    out_consts[row * 3 + 2] = consts[i * 3 + 2];
-  }
+  if (part == 0 && threadIdx.x < 3) p.out_consts[row * 3 + threadIdx.x] = p.consts[i * 3 + threadIdx.x];
+  note_bad(bad, nbad);
 }
 
 }  // namespace
@@ -281,34 +344,72 @@ extern "C" int hi2x_pack_codes(const uint8_t* codes, int64_t rows, int64_t k, in
   return launch_status("pack_kernel");
 }
 
+// One launch per kPackPieces pieces (the pieces' checks come first, before anything is
+// launched).
+static int assemble_launch(const hi2x_piece* pieces, int64_t n_pieces, int32_t* bad,
+                           hipStream_t s) {
+  double bytes = 0.0;
+  for (int64_t i = 0; i < n_pieces; ++i) {
+    const hi2x_piece& p = pieces[i];
+    HI2X_REQUIRE(p.nbits == 2 || p.nbits == 4 || p.nbits == 8, "assemble: piece %lld "
+                 "nbits=%d", (long long)i, p.nbits);
+    HI2X_REQUIRE(p.block > 0 && p.k > 0 && p.k % p.block == 0 && p.k % (32 / p.nbits) == 0 &&
+                     p.r >= 0 && p.k < (int64_t(1) << 30),
+                 "assemble: piece %lld K/block", (long long)i);
+    HI2X_REQUIRE(p.r == 0 || (p.rows && p.codes && p.params && p.consts && p.code_off &&
+                              p.param_off && p.out_codes && p.out_params && p.out_consts),
+                 "assemble: piece %lld has a null buffer", (long long)i);
+    bytes += (double)p.r * (p.k + p.k * p.nbits / 8 + 4 * (p.k / p.block) + 12);
+  }
+  LaunchTimer timer(HI2X_TIME_PACK, bytes, s);
+  PackBatch b;
+  int64_t i = 0;
+  while (i < n_pieces) {
+    b.n = 0;
+    int64_t wgs = 0;
+    for (; i < n_pieces && b.n < kPackPieces; ++i) {
+      const hi2x_piece& q = pieces[i];
+      if (q.r == 0) continue;
+      const int64_t nw = q.k / (32 / q.nbits), nblk = q.k / q.block;
+      const int64_t span = nw > nblk ? nw : nblk;
+      const int64_t chunks = (span + 255) / 256;
+      HI2X_REQUIRE(wgs + q.r * chunks < (int64_t(1) << 31), "assemble: too many rows");
+      PackPiece& p = b.p[b.n];
+      p.rows = q.rows;
+      p.codes = q.codes;
+      p.params = q.params;
+      p.consts = q.consts;
+      p.code_off = q.code_off;
+      p.param_off = q.param_off;
+      p.out_codes = q.out_codes;
+      p.out_params = q.out_params;
+      p.out_consts = q.out_consts;
+      p.k = (int32_t)q.k;
+      p.nbits = q.nbits;
+      p.nblk = (int32_t)nblk;
+      p.nw = (int32_t)nw;
+      p.chunks = (int32_t)chunks;
+      p.vec = ((reinterpret_cast<uintptr_t>(q.codes) % 16 == 0 && q.k % 16 == 0) ? 1 : 0) |
+              ((reinterpret_cast<uintptr_t>(q.params) % 2 == 0 &&
+                reinterpret_cast<uintptr_t>(q.out_params) % 2 == 0) ? 2 : 0);
+      b.wg_start[b.n] = (int32_t)wgs;
+      wgs += q.r * chunks;
+      ++b.n;
+    }
+    if (b.n == 0) break;
+    b.wg_start[b.n] = (int32_t)wgs;
+    hipLaunchKernelGGL(assemble_batch_kernel, dim3((unsigned)wgs), dim3(256), 0, s, b, bad);
+    const int rc = launch_status("assemble_batch_kernel");
+    if (rc) return rc;
+  }
+  return HI2X_OK;
+}
+
 extern "C" int hi2x_assemble_batch(const hi2x_piece* pieces, int64_t n_pieces, int32_t* bad,
                                    void* stream) {
   clear_error();
   HI2X_REQUIRE(n_pieces >= 0 && (n_pieces == 0 || pieces), "assemble_batch: bad arguments");
-  hipStream_t s = as_stream(stream);
-  double bytes = 0.0;
-  for (int64_t i = 0; i < n_pieces; ++i) {
-    const hi2x_piece& p = pieces[i];
-    HI2X_REQUIRE(p.nbits == 2 || p.nbits == 4 || p.nbits == 8, "assemble_batch: piece %lld "
-                 "nbits=%d", (long long)i, p.nbits);
-    HI2X_REQUIRE(p.block > 0 && p.k % p.block == 0 && p.k % (32 / p.nbits) == 0 && p.r >= 0,
-                 "assemble_batch: piece %lld K/block", (long long)i);
-    bytes += (double)p.r * (p.k + p.k * p.nbits / 8 + 4 * (p.k / p.block) + 12);
-  }
-  LaunchTimer timer(HI2X_TIME_PACK, bytes, s);
-  for (int64_t i = 0; i < n_pieces; ++i) {
-    const hi2x_piece& p = pieces[i];
-    if (p.r == 0) continue;
-    const int64_t nw = p.k / (32 / p.nbits), nblk = p.k / p.block;
-    const int64_t span = nw > nblk ? nw : nblk;
-    const int64_t total = p.r * span;
-    hipLaunchKernelGGL(assemble_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s,
-                       p.rows, p.r, p.codes, p.params, p.consts, p.k, p.nbits, nblk, p.code_off,
-                       p.param_off, p.out_codes, p.out_params, p.out_consts, bad);
-    const int rc = launch_status("assemble_kernel");
-    if (rc) return rc;
-  }
-  return HI2X_OK;
+  return assemble_launch(pieces, n_pieces, bad, as_stream(stream));
 }
 
 extern "C" int hi2x_assemble_piece(const int64_t* rows, int64_t r, const uint8_t* codes,
@@ -318,16 +419,7 @@ extern "C" int hi2x_assemble_piece(const int64_t* rows, int64_t r, const uint8_t
                                    uint8_t* out_params, uint16_t* out_consts, int32_t* bad,
                                    void* stream) {
   clear_error();
-  HI2X_REQUIRE(nbits == 2 || nbits == 4 || nbits == 8, "assemble: nbits=%d", nbits);
-  HI2X_REQUIRE(block > 0 && k % block == 0 && k % (32 / nbits) == 0, "assemble: K/block");
-  if (r == 0) return HI2X_OK;
-  const int64_t nw = k / (32 / nbits), nblk = k / block;
-  const int64_t span = nw > nblk ? nw : nblk;
-  const int64_t total = r * span;
-  LaunchTimer timer(HI2X_TIME_PACK, (double)r * (k + k * nbits / 8 + 4 * nblk + 12),
-                    as_stream(stream));
-  hipLaunchKernelGGL(assemble_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0,
-                     as_stream(stream), rows, r, codes, params, consts, k, nbits, nblk, code_off,
-                     param_off, out_codes, out_params, out_consts, bad);
-  return launch_status("assemble_kernel");
+  const hi2x_piece p{rows, r, codes, params, consts, k, nbits, 0, block, code_off, param_off,
+                     out_codes, out_params, out_consts};
+  return assemble_launch(&p, 1, bad, as_stream(stream));
 }

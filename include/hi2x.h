@@ -459,7 +459,7 @@ int hi2x_stream_background(void* stream, int background);
  * switched while other threads launch. */
 #define HI2X_TIME_GPTQ_TRAILING 0 /* work = 2 * rows * rank * columns (flops) */
 #define HI2X_TIME_HESSIAN_SYRK 1  /* work = tokens * k * (k + 1) (flops, upper triangle) */
-#define HI2X_TIME_CHOL_GEMM 2     /* work = flops of the triangular product */
+#define HI2X_TIME_CHOL_GEMM 2     /* work = flops of the triangular product (fp32 MFMA) */
 #define HI2X_TIME_CHOL_LEAF 3     /* work = 2 * n^3 / 3 (factor + inverse of the leaf) */
 #define HI2X_TIME_GPTQ_BLOCK 4    /* work = rows * len * (len - 1) (intra-block flops) */
 #define HI2X_TIME_REFINE_GEMM 5   /* work = 2 * rows * rank * columns (flops) */
@@ -468,6 +468,9 @@ int hi2x_stream_background(void* stream, int background);
 #define HI2X_TIME_LADDER_FIT 8    /* work = bytes of w read (rows * k * 4) */
 #define HI2X_TIME_PACK 9          /* work = bytes: codes read, words, params and consts moved */
 #define HI2X_TIME_FINISH 10       /* work = bytes: codes and w read (sse; + the unpermute) */
+#define HI2X_TIME_CHOL_SPLIT 11   /* work = fp16 MFMA flops executed by the factor's split-plane
+                                     products: 3 products per fp32-equivalent product of the
+                                     triangular shape (M * N * rank each) */
 int hi2x_timing_enable(unsigned mask);
 
 /* Sum over the recorded launches of `kind`: count, event-timed milliseconds, work. */

@@ -66,7 +66,8 @@ def first_divergences(wt, codes_o, codes_r, params_o, params_r, consts_o, consts
     """Per diverging row of one candidate group (rows ``wt`` [n, K] in the stored basis,
     ``*_o`` this build's, ``*_r`` the reference's): dicts with ``row``, ``col``, ``kind``
     ("ladder" or "rounding") and ``tie`` (the relative fit-error gap of the blocks whose
-    fits differ, or the quotient distance in steps)."""
+    fits differ, or the quotient distance in steps); a ladder tie also carries ``d_rel``,
+    the largest relative difference of the two runs' d over those blocks."""
     n, k = codes_o.shape
     nb = k // block
     lo_o, st_o = decode(params_o, consts_o)
@@ -85,7 +86,7 @@ def first_divergences(wt, codes_o, codes_r, params_o, params_r, consts_o, consts
             wb = wt[i].reshape(1, nb, block)
             fo = fit_ladder(wb, d_o.reshape(1, nb, block), 2 ** nbits, "normal")
             fr = fit_ladder(wb, d_r.reshape(1, nb, block), 2 ** nbits, "normal")
-            gap = 0.0
+            gap = d_rel = 0.0
             w64 = wt[i].reshape(nb, block).astype(np.float64)
             d64 = d_r.reshape(nb, block).astype(np.float64)
             for b in range(nb):
@@ -94,7 +95,10 @@ def first_divergences(wt, codes_o, codes_r, params_o, params_r, consts_o, consts
                 eo = _fit_err(w64[b], d64[b], float(fo[0][0, b]), float(fo[1][0, b]), 2 ** nbits)
                 er = _fit_err(w64[b], d64[b], float(fr[0][0, b]), float(fr[1][0, b]), 2 ** nbits)
                 gap = max(gap, abs(eo - er) / max(eo, er, 1e-300))
-            out.append(dict(row=i, col=first_lad, kind="ladder", tie=gap))
+                do = d_o[b * block:(b + 1) * block].astype(np.float64)
+                d_rel = max(d_rel, float(np.max(np.abs(do - d64[b])
+                                                / np.maximum(np.abs(d64[b]), 1e-300))))
+            out.append(dict(row=i, col=first_lad, kind="ladder", tie=gap, d_rel=d_rel))
         else:
             j = first_code
             b = j // block
@@ -159,3 +163,52 @@ def classify_departures(wt, rows, d_o, d_r, nbits, block, params_digest_r, const
                                                                           1e-300))))
         out.append(dict(row=int(i), kind="ladder", tie=tie, fit_gap=gap, explained=explained))
     return out
+
+
+def compare_groups(groups):
+    """Agreement of two encodings of one tensor, group by group.  ``groups`` holds, per
+    candidate group, dicts ``wt`` (the rotated rows [n, K], identical for both runs),
+    ``o`` and ``r`` (this build's and the reference's: ``codes`` u8 [n, K], ``params``
+    u8 [n, nb, 2], ``consts`` u16 [n, 3], ``sse`` f32 [n], ``comp`` f32 [n, K]), ``d_o``,
+    ``d_r`` (each run's ladder weights diag(Hs)), ``nbits`` and ``block``.  Returns the
+    share of equal codes, the departing rows by kind with their largest tie (ladder: the
+    fit-error gap and the d difference; rounding: the quotient distance in steps), the
+    total sse's relative difference and the largest relative sse difference over the rows
+    that do not depart."""
+    equal = total = rows = 0
+    lad, rnd = [], []
+    sse_o, sse_r, stay_rel = [], [], 0.0
+    for g in groups:
+        o, r = g["o"], g["r"]
+        n = o["codes"].shape[0]
+        dep = ((o["codes"] != r["codes"]).any(1)
+               | (o["params"].reshape(n, -1) != r["params"].reshape(n, -1)).any(1)
+               | (o["consts"] != r["consts"]).any(1))
+        idx = np.nonzero(dep)[0]
+        equal += int((o["codes"] == r["codes"]).sum())
+        total += o["codes"].size
+        rows += n
+        if idx.size:
+            divs = first_divergences(g["wt"][idx], o["codes"][idx], r["codes"][idx],
+                                     o["params"][idx], r["params"][idx], o["consts"][idx],
+                                     r["consts"][idx], o["comp"][idx], r["comp"][idx],
+                                     g["d_o"], g["d_r"], g["nbits"], g["block"])
+            lad += [x for x in divs if x["kind"] == "ladder"]
+            rnd += [x for x in divs if x["kind"] == "rounding"]
+        so, sr = o["sse"].astype(np.float64), r["sse"].astype(np.float64)
+        sse_o.append(so.sum())
+        sse_r.append(sr.sum())
+        keep = ~dep
+        if keep.any():
+            stay_rel = max(stay_rel, float(np.max(np.abs(so[keep] - sr[keep])
+                                                  / np.maximum(sr[keep], 1e-30))))
+    return {"codes_equal": equal / max(total, 1), "codes": total, "rows": rows,
+            "rows_departing": len(lad) + len(rnd),
+            "ladder": {"rows": len(lad),
+                       "max_fit_gap": max((x["tie"] for x in lad), default=0.0),
+                       "max_d_rel": max((x["d_rel"] for x in lad), default=0.0)},
+            "rounding": {"rows": len(rnd),
+                         "max_quotient_distance_steps": max((x["tie"] for x in rnd),
+                                                            default=0.0)},
+            "sse_rel_total": abs(sum(sse_o) / max(sum(sse_r), 1e-300) - 1),
+            "sse_rel_max_rows_that_stay": stay_rel}

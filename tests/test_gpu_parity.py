@@ -493,6 +493,54 @@ def test_assemble_many_equals_assemble_per_tensor(dev):
         assert got.shape == want.shape
 
 
+def _offset_copy(a: np.ndarray, dev, shift: int):
+    """A device copy of a that starts `shift` bytes into its allocation (misaligned for
+    shift % 16 != 0)."""
+    flat = torch.zeros(a.nbytes + shift, dtype=torch.uint8, device=dev)
+    flat[shift:] = T(np.ascontiguousarray(a).view(np.uint8).reshape(-1), dev)
+    return flat[shift:].view(getattr(torch, a.dtype.name)).view(a.shape)
+
+
+def test_assemble_batch_over_many_launches_and_misaligned_pieces(dev):
+    """hi2x_assemble_batch with more pieces than one launch carries (40 pieces of three
+    tensors, K up to 14336: several workgroups per row), some pieces' codes and ladder
+    bytes starting off their vector boundaries (the byte-load path), against the oracle's
+    assemble of each tensor."""
+    from hi2_amd.format import assemble_many
+
+    rng = np.random.default_rng(7)
+    tensors, want = [], []
+    for ti, (r, k) in enumerate(((48, 4096), (40, 960), (32, 14336))):
+        nbits = np.zeros(r, np.int64)
+        block = np.zeros(r, np.int64)
+        pieces, pieces_np = [], []
+        order = rng.permutation(r)
+        for pi, rows in enumerate(np.array_split(order, 14 if ti == 0 else 13)):
+            rows = np.sort(rows)
+            nb = int(rng.choice([2, 4, 8]))
+            b = int(rng.choice([16, 32, 64]))
+            nbits[rows] = nb
+            block[rows] = b
+            c = rng.integers(0, 2 ** nb, (rows.size, k)).astype(np.uint8)
+            p = rng.integers(0, 256, (rows.size, k // b, 2)).astype(np.uint8)
+            rc = rng.standard_normal((rows.size, 3)).astype(np.float16)
+            pieces_np.append((rows, c, p, rc.view(np.uint16)))
+            shift = (pi % 3) * 5  # 0: aligned; 5, 10: off the 16-byte and 2-byte grids
+            pieces.append((torch.from_numpy(rows), _offset_copy(c, dev, shift),
+                           _offset_copy(p, dev, shift), T(rc, dev)))
+        tensors.append(dict(pieces=pieces, row_nbits=torch.from_numpy(nbits),
+                            row_block=torch.from_numpy(block),
+                            had=torch.ones(k // 16, dtype=torch.uint8), k=k))
+        want.append(oracle.assemble(pieces_np, nbits, block, k))
+    assert sum(len(t["pieces"]) for t in tensors) == 40
+    for got, w in zip(assemble_many(tensors), want):
+        assert np.array_equal(got.codes.numpy(), w["codes"])
+        assert np.array_equal(got.blk_params.numpy(), w["blk_params"])
+        assert np.array_equal(got.row_consts.numpy().view(np.uint16), w["row_consts"])
+        assert np.array_equal(got.code_off.numpy(), w["code_off"])
+        assert np.array_equal(got.param_off.numpy(), w["param_off"])
+
+
 # ---- Hessian, transform, factor --------------------------------------------------------------
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 @pytest.mark.parametrize("t,k", [(700, 320), (4096, 256)])

@@ -56,3 +56,29 @@ def test_timing_records_hessian_syrk(dev):
         _lib.timing_enable([])
     assert launches == 1 and ms > 0.0 and work == float(t * k * (k + 1))
     assert _lib.timing_query(_lib.TIME_HESSIAN_SYRK) == (0, 0.0, 0.0)
+
+
+def test_timing_separates_the_factor_fp32_and_split_products(dev):
+    """At K = 4096 the factor's top products run on the fp16 split planes (their own
+    family, counting the three fp16 products) and the smaller ones on the fp32 MFMA GEMM:
+    each family records its launches, and neither reports more than its peak."""
+    from hi2_amd import _lib
+    from hi2_amd.hessian import inverse_factor
+
+    k = 4096
+    g = torch.Generator(device=dev).manual_seed(3)
+    x = torch.randn(2 * k, k, generator=g, device=dev)
+    hs = (x.T @ x) / (2 * k)
+    inverse_factor(hs, 0.01)
+    torch.cuda.synchronize()
+    _lib.timing_enable([_lib.TIME_CHOL_GEMM, _lib.TIME_CHOL_SPLIT])
+    try:
+        inverse_factor(hs, 0.01)
+        torch.cuda.synchronize()
+        f32 = _lib.timing_query(_lib.TIME_CHOL_GEMM)
+        f16 = _lib.timing_query(_lib.TIME_CHOL_SPLIT)
+    finally:
+        _lib.timing_enable([])
+    assert f32[0] > 0 and f16[0] > 0
+    assert f32[2] / (f32[1] / 1e3) < 157.3e12
+    assert f16[2] / (f16[1] / 1e3) < 2.5e15
