@@ -728,7 +728,9 @@ DOMINANT = 0  # the GPTQ trailing-update GEMM: the metric's MFMA kernel with the
 
 
 def kernel_stats(kind):
-    """Event-timed launches of one kernel family since hi2x_timing_enable."""
+    """Event-timed launches of one kernel family since hi2x_timing_enable.  The SYRK also
+    carries the algorithmic rate: the reference's Hessian is a full fp32 GEMM, 2 T K^2
+    flops per input (its executed work here is the upper triangle, T K (K + 1))."""
     from hi2_amd import _lib
 
     name, bound, peak, unit = KERNELS[kind]
@@ -736,9 +738,15 @@ def kernel_stats(kind):
     if n == 0 or ms <= 0.0:
         return None
     rate = work / (ms / 1e3)
-    return {"kernel": name, "bound": bound, "launches": n, "avg_ms": ms / n,
-            "total_ms": ms, "work_per_launch": work / n, "work_unit": unit,
-            "tflops": rate / 1e12, "frac_of_peak": rate / peak}
+    out = {"kernel": name, "bound": bound, "launches": n, "avg_ms": ms / n,
+           "total_ms": ms, "work_per_launch": work / n, "work_unit": unit,
+           "tflops": rate / 1e12, "frac_of_peak": rate / peak}
+    if kind == 1:  # T K (K + 1) executed -> 2 T K^2 algorithmic: a factor 2 K / (K + 1)
+        k = max(CFG3["inputs"].values())
+        alg = rate * 2.0 * k / (k + 1)
+        out["algorithmic"] = {"work_unit": "2*T*K^2 (the reference's full GEMM)",
+                              "tflops": alg / 1e12, "frac_of_peak": alg / peak}
+    return out
 
 
 def trailing_roofline(steps, basis):

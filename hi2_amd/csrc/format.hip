@@ -174,12 +174,13 @@ __global__ __launch_bounds__(256) void pack_kernel(const uint8_t* __restrict__ c
 // assemble (hi2/format.py:155-171): the pieces of one or more tensors in one launch.
 // Each piece is a group of rows sharing (nbits, B); its descriptor travels in the kernel
 // arguments (up to kPackPieces per launch) with the first workgroup of every piece.  A
-// workgroup covers 256 consecutive items of one row of one piece: item j packs word j
-// of the row (32/nbits codes, LSB first, from one 4-, 8- or 16-byte load) into the flat
-// buffer at code_off[rows[i]] + j, moves the row's ladder bytes of block j (one 16-bit
-// pair) to param_off[rows[i]] + j, and items 0..2 of the row's first workgroup move its
-// three constants.  Codes at or above 2^nbits are counted in bad (packed masked).
+// wave packs one row: lane l takes words l, l + 64, ... of the row (32/nbits codes, LSB
+// first, each from one 4-, 8- or 16-byte load, four loads in flight per round) into the
+// flat buffer at code_off[rows[i]] + j, moves the ladder bytes of blocks l, l + 64, ...
+// (16-bit pairs) to param_off[rows[i]] + b, and lanes 0..2 move the row's three
+// constants.  Codes at or above 2^nbits are counted in bad (packed masked).
 constexpr int kPackPieces = 24;
+constexpr int kPackRows = 4;  // rows (waves) per workgroup
 struct PackPiece {
   const int64_t* rows;
   const uint8_t* codes;
@@ -190,8 +191,8 @@ struct PackPiece {
   int32_t* out_codes;
   uint8_t* out_params;
   uint16_t* out_consts;
-  int32_t k, nbits, nblk, nw, chunks;  // chunks: workgroups per row
-  int32_t vec;                         // bit 0: 16-byte code rows, bit 1: 2-byte params
+  int32_t k, nbits, nblk, nw, r;
+  int32_t vec;  // bit 0: 16-byte code rows, bit 1: 2-byte params
 };
 struct PackBatch {
   PackPiece p[kPackPieces];
@@ -200,79 +201,95 @@ struct PackBatch {
 };
 
 template <int PER>
-__device__ __forceinline__ uint32_t pack_word(const uint32_t (&x)[PER / 4], int nbits,
-                                              int& nbad) {
-  const uint32_t lim = 1u << nbits;
+__device__ __forceinline__ uint32_t pack_word(const uint32_t (&x)[PER / 4], int& nbad) {
+  constexpr int NB = 32 / PER;
+  constexpr uint32_t LIM = 1u << NB;
   uint32_t v = 0;
 #pragma unroll
   for (int q = 0; q < PER; ++q) {
     const uint32_t cv = (x[q / 4] >> (8 * (q % 4))) & 0xffu;
-    nbad += cv >= lim;
-    v |= (cv & (lim - 1u)) << (nbits * q);
+    nbad += cv >= LIM;
+    v |= (cv & (LIM - 1u)) << (NB * q);
   }
   return v;
 }
 
-__global__ __launch_bounds__(256) void assemble_batch_kernel(const PackBatch b,
-                                                             int32_t* __restrict__ bad) {
+// Word j of a code row c (PER codes), as PER / 4 dwords.
+template <int PER>
+__device__ __forceinline__ void load_word(uint32_t (&x)[PER / 4], const uint8_t* c, int j,
+                                          bool vec) {
+  if (vec) {
+    if constexpr (PER == 16) {
+      const uint4 y = reinterpret_cast<const uint4*>(c)[j];
+      x[0] = y.x, x[1] = y.y, x[2] = y.z, x[3] = y.w;
+    } else if constexpr (PER == 8) {
+      const uint2 y = reinterpret_cast<const uint2*>(c)[j];
+      x[0] = y.x, x[1] = y.y;
+    } else {
+      x[0] = reinterpret_cast<const uint32_t*>(c)[j];
+    }
+  } else {
+#pragma unroll
+    for (int q = 0; q < PER / 4; ++q) {
+      const uint8_t* b = c + PER * j + 4 * q;
+      x[q] = b[0] | (b[1] << 8) | (b[2] << 16) | ((uint32_t)b[3] << 24);
+    }
+  }
+}
+
+template <int PER>
+__device__ __forceinline__ int pack_row(const uint8_t* __restrict__ c, int nw, bool vec,
+                                        int32_t* __restrict__ out, int lane) {
+  constexpr int U = 4;  // loads in flight per lane
+  int nbad = 0;
+  for (int j0 = lane; j0 < nw; j0 += 64 * U) {
+    uint32_t x[U][PER / 4];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int j = j0 + 64 * u;
+      if (j < nw) load_word<PER>(x[u], c, j, vec);
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int j = j0 + 64 * u;
+      if (j < nw) out[j] = (int32_t)pack_word<PER>(x[u], nbad);
+    }
+  }
+  return nbad;
+}
+
+__global__ __launch_bounds__(64 * kPackRows) void assemble_batch_kernel(
+    const PackBatch b, int32_t* __restrict__ bad) {
   const int wg = blockIdx.x;
   int pi = 0;
   while (pi + 1 < b.n && wg >= b.wg_start[pi + 1]) ++pi;  // uniform: scalar registers
   const PackPiece& p = b.p[pi];
-  const int local = wg - b.wg_start[pi];
-  const int i = local / p.chunks, part = local - i * p.chunks;
-  const int j = part * 256 + (int)threadIdx.x;
+  const int lane = threadIdx.x & 63;
+  const int i = (wg - b.wg_start[pi]) * kPackRows + (int)(threadIdx.x >> 6);
+  if (i >= p.r) return;
   const int64_t row = p.rows[i];
-  int nbad = 0;
-  if (j < p.nw) {
-    const uint8_t* c = p.codes + (int64_t)i * p.k;
-    uint32_t v;
-    if (p.nbits == 2) {
-      uint32_t x[4];
-      if (p.vec & 1) {
-        const uint4 y = reinterpret_cast<const uint4*>(c)[j];
-        x[0] = y.x, x[1] = y.y, x[2] = y.z, x[3] = y.w;
-      } else {
-#pragma unroll
-        for (int q = 0; q < 4; ++q)
-          x[q] = c[16 * j + 4 * q] | (c[16 * j + 4 * q + 1] << 8) |
-                 (c[16 * j + 4 * q + 2] << 16) | ((uint32_t)c[16 * j + 4 * q + 3] << 24);
-      }
-      v = pack_word<16>(x, 2, nbad);
-    } else if (p.nbits == 4) {
-      uint32_t x[2];
-      if (p.vec & 1) {
-        const uint2 y = reinterpret_cast<const uint2*>(c)[j];
-        x[0] = y.x, x[1] = y.y;
-      } else {
-#pragma unroll
-        for (int q = 0; q < 2; ++q)
-          x[q] = c[8 * j + 4 * q] | (c[8 * j + 4 * q + 1] << 8) |
-                 (c[8 * j + 4 * q + 2] << 16) | ((uint32_t)c[8 * j + 4 * q + 3] << 24);
-      }
-      v = pack_word<8>(x, 4, nbad);
-    } else {
-      uint32_t x[1];
-      if (p.vec & 1)
-        x[0] = reinterpret_cast<const uint32_t*>(c)[j];
-      else
-        x[0] = c[4 * j] | (c[4 * j + 1] << 8) | (c[4 * j + 2] << 16) |
-               ((uint32_t)c[4 * j + 3] << 24);
-      v = pack_word<4>(x, 8, nbad);
-    }
-    p.out_codes[p.code_off[row] + j] = (int32_t)v;
-  }
-  if (j < p.nblk) {
-    const int64_t src = (int64_t)i * p.nblk + j, dst = p.param_off[row] + j;
-    if (p.vec & 2) {
-      reinterpret_cast<uint16_t*>(p.out_params)[dst] =
-          reinterpret_cast<const uint16_t*>(p.params)[src];
-    } else {
-      p.out_params[2 * dst] = p.params[2 * src];
-      p.out_params[2 * dst + 1] = p.params[2 * src + 1];
+  const uint8_t* c = p.codes + (int64_t)i * p.k;
+  int32_t* out = p.out_codes + p.code_off[row];
+  const bool vec = (p.vec & 1) != 0;
+  int nbad;
+  if (p.nbits == 2)
+    nbad = pack_row<16>(c, p.nw, vec, out, lane);
+  else if (p.nbits == 4)
+    nbad = pack_row<8>(c, p.nw, vec, out, lane);
+  else
+    nbad = pack_row<4>(c, p.nw, vec, out, lane);
+  const int64_t src = (int64_t)i * p.nblk, dst = p.param_off[row];
+  if (p.vec & 2) {
+    const uint16_t* ps = reinterpret_cast<const uint16_t*>(p.params) + src;
+    uint16_t* pd = reinterpret_cast<uint16_t*>(p.out_params) + dst;
+    for (int j = lane; j < p.nblk; j += 64) pd[j] = ps[j];
+  } else {
+    for (int j = lane; j < p.nblk; j += 64) {
+      p.out_params[2 * (dst + j)] = p.params[2 * (src + j)];
+      p.out_params[2 * (dst + j) + 1] = p.params[2 * (src + j) + 1];
     }
   }
-  if (part == 0 && threadIdx.x < 3) p.out_consts[row * 3 + threadIdx.x] = p.consts[i * 3 + threadIdx.x];
+  if (lane < 3) p.out_consts[row * 3 + lane] = p.consts[(int64_t)i * 3 + lane];
   note_bad(bad, nbad);
 }
 
@@ -371,9 +388,9 @@ static int assemble_launch(const hi2x_piece* pieces, int64_t n_pieces, int32_t* 
       const hi2x_piece& q = pieces[i];
       if (q.r == 0) continue;
       const int64_t nw = q.k / (32 / q.nbits), nblk = q.k / q.block;
-      const int64_t span = nw > nblk ? nw : nblk;
-      const int64_t chunks = (span + 255) / 256;
-      HI2X_REQUIRE(wgs + q.r * chunks < (int64_t(1) << 31), "assemble: too many rows");
+      const int64_t nwg = (q.r + kPackRows - 1) / kPackRows;
+      HI2X_REQUIRE(q.r < (int64_t(1) << 31) && wgs + nwg < (int64_t(1) << 31),
+                   "assemble: too many rows");
       PackPiece& p = b.p[b.n];
       p.rows = q.rows;
       p.codes = q.codes;
@@ -388,17 +405,18 @@ static int assemble_launch(const hi2x_piece* pieces, int64_t n_pieces, int32_t* 
       p.nbits = q.nbits;
       p.nblk = (int32_t)nblk;
       p.nw = (int32_t)nw;
-      p.chunks = (int32_t)chunks;
+      p.r = (int32_t)q.r;
       p.vec = ((reinterpret_cast<uintptr_t>(q.codes) % 16 == 0 && q.k % 16 == 0) ? 1 : 0) |
               ((reinterpret_cast<uintptr_t>(q.params) % 2 == 0 &&
                 reinterpret_cast<uintptr_t>(q.out_params) % 2 == 0) ? 2 : 0);
       b.wg_start[b.n] = (int32_t)wgs;
-      wgs += q.r * chunks;
+      wgs += nwg;
       ++b.n;
     }
     if (b.n == 0) break;
     b.wg_start[b.n] = (int32_t)wgs;
-    hipLaunchKernelGGL(assemble_batch_kernel, dim3((unsigned)wgs), dim3(256), 0, s, b, bad);
+    hipLaunchKernelGGL(assemble_batch_kernel, dim3((unsigned)wgs), dim3(64 * kPackRows), 0, s,
+                       b, bad);
     const int rc = launch_status("assemble_batch_kernel");
     if (rc) return rc;
   }

