@@ -34,6 +34,8 @@ SIGNATURES = {
     "hi2x_gptq_run_noalloc": [_P, _I64, _I64, _P, _P, _P, _I64, _P, _P, _P, _P, _P, _I64, _P],
     "hi2x_stream_background": [_P, _I],
     "hi2x_ladder_fit": [_P, _P, _I64, _I64, _I64, _I, _P, _I, _I, _P, _P, _P, _P],
+    "hi2x_ladder_fit_rows": [_P, _P, _P, _I64, _I64, _I64, _I, _P, _I, _I, _P, _P, _P, _P],
+    "hi2x_finish_rows": [_P, _I64, _I64, _P, _P, _I64, _P, _P, _P, _P],
     "hi2x_params": [_P, _P, _I64, _I64, _P, _P, _P, _P, _P, _I64, _P],
     "hi2x_decode_params": [_P, _P, _P, _I64, _I64, _P, _P, _P],
     "hi2x_nearest_codes": [_P, _I64, _I64, _I64, _P, _P, _I64, _I, _P, _P],

@@ -19,13 +19,14 @@ template <int B>
 __global__ __launch_bounds__(256) void ladder_fit_kernel(
     const float* __restrict__ w, const float* __restrict__ d, int64_t rows, int64_t k,
     int nlev, Grid grid, int G, int ls, float* __restrict__ out_lo,
-    float* __restrict__ out_st, float* __restrict__ out_err) {
+    float* __restrict__ out_st, float* __restrict__ out_err,
+    const int32_t* __restrict__ d_row) {
   const int64_t nb = k / B;
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= rows * nb) return;
   const int64_t r = i / nb, b = i % nb;
   const float* wp = w + r * k + b * B;
-  const float* dp = d + b * B;
+  const float* dp = d + (d_row ? (int64_t)d_row[r] * k : 0) + b * B;
   float x[B], dd[B];
 #pragma unroll
   for (int t = 0; t < B; t += 4) {
@@ -173,7 +174,8 @@ template <int B, int NL>
 __global__ __launch_bounds__(256) void ladder_fit_group_kernel(
     const float* __restrict__ w, const float* __restrict__ d, int64_t rows, int64_t k,
     int nlev, Grid grid, int G, int ls, float* __restrict__ out_lo,
-    float* __restrict__ out_st, float* __restrict__ out_err) {
+    float* __restrict__ out_st, float* __restrict__ out_err,
+    const int32_t* __restrict__ d_row) {
   constexpr int NE = B / NL, P = 8 / NL;  // elements and positions per lane
   using LG = LaneGroup<NL>;
   const int64_t nb = k / B;
@@ -183,7 +185,7 @@ __global__ __launch_bounds__(256) void ladder_fit_group_kernel(
   if (i >= rows * nb) return;  // the lanes of a group leave together
   const int64_t r = i / nb, b = i % nb;
   const float* wp = w + r * k + b * B + P * h;
-  const float* dp = d + b * B + P * h;
+  const float* dp = d + (d_row ? (int64_t)d_row[r] * k : 0) + b * B + P * h;
   float x[NE], dd[NE];
 #pragma unroll
   for (int q = 0; q < B / 8; ++q) {  // vector q: elements 8q + P h .. 8q + P h + P - 1
@@ -435,23 +437,37 @@ __device__ __forceinline__ int64_t ceil_log2_dev(int64_t x) {
   return 64 - __builtin_clzll((unsigned long long)(x - 1));
 }
 
+// With groups (not null), row r of the batch belongs to group row_grp[r]: its
+// uncompensated row is row r - row0 of the group's w, its weights the group's d and its
+// ladder block the group's; rows past the group's own (padding) are skipped.
 __global__ __launch_bounds__(256) void sse_kernel(const uint8_t* __restrict__ codes,
                                                   int64_t n, int64_t k, int64_t B,
                                                   const float* __restrict__ lo_d,
                                                   const float* __restrict__ st_d, int64_t ldd,
                                                   const float* __restrict__ w,
                                                   const float* __restrict__ d,
-                                                  float* __restrict__ sse) {
+                                                  float* __restrict__ sse,
+                                                  const int32_t* __restrict__ row_grp,
+                                                  const hi2x_rows_group* __restrict__ groups) {
   const int lane = threadIdx.x & 63;
   const int half = lane >> 5, hl = lane & 31;
   const int kq = hl >> 3, v = hl & 7;
   const int64_t r = ((int64_t)blockIdx.x * (blockDim.x / 64) + (threadIdx.x >> 6)) * 2 + half;
-  const bool live = r < n;
+  bool live = r < n;
   const int64_t rr = live ? r : 0;
+  const float* wr = w + rr * k;
+  if (groups) {
+    const hi2x_rows_group& gp = groups[row_grp[rr]];
+    const int64_t lr = rr - gp.row0;
+    live = live && lr < gp.rows;
+    wr = gp.w + (live ? lr : 0) * k;
+    d = gp.d;
+    B = gp.block;
+  }
   auto term = [&](int64_t c) -> float {
     const int64_t b = c / B;
     const float rec = f16_round(lo_d[rr * ldd + b] + (float)codes[rr * k + c] * st_d[rr * ldd + b]);
-    const float df = rec - w[rr * k + c];
+    const float df = rec - wr[c];
     return d[c] * (df * df);
   };
   const int64_t vec_size = k / 8;
@@ -534,18 +550,18 @@ __global__ __launch_bounds__(256) void nearest_codes_kernel(
 template <int B>
 int launch_fit(const float* w, const float* d, int64_t rows, int64_t k, int nlev,
                const Grid& grid, int g, int ls, float* lo, float* step, float* err,
-               hipStream_t s) {
+               hipStream_t s, const int32_t* d_row = nullptr) {
   const int64_t total = rows * (k / B);
   LaunchTimer timer(HI2X_TIME_LADDER_FIT, 4.0 * rows * k, s);
   if constexpr (B == 32 || B == 64) {  // a group of lanes per (row, block)
     constexpr int NL = LADDER_LANES;
     const dim3 blocks((unsigned)((NL * total + 255) / 256));
     hipLaunchKernelGGL((ladder_fit_group_kernel<B, NL>), blocks, dim3(256), 0, s, w, d, rows, k,
-                       nlev, grid, g, ls, lo, step, err);
+                       nlev, grid, g, ls, lo, step, err, d_row);
   } else {
     const dim3 blocks((unsigned)((total + 255) / 256));
     hipLaunchKernelGGL(ladder_fit_kernel<B>, blocks, dim3(256), 0, s, w, d, rows, k, nlev,
-                       grid, g, ls, lo, step, err);
+                       grid, g, ls, lo, step, err, d_row);
   }
   return launch_status("ladder_fit_kernel");
 }
@@ -573,6 +589,29 @@ extern "C" int hi2x_ladder_fit(const float* w, const float* d, int64_t rows, int
     case 16: return launch_fit<16>(w, d, rows, k, nlev, gr, g, ls, lo, step, err, s);
     case 32: return launch_fit<32>(w, d, rows, k, nlev, gr, g, ls, lo, step, err, s);
     default: return launch_fit<64>(w, d, rows, k, nlev, gr, g, ls, lo, step, err, s);
+  }
+}
+
+extern "C" int hi2x_ladder_fit_rows(const float* w, const float* d, const int32_t* d_row,
+                                    int64_t rows, int64_t k, int64_t block, int nlev,
+                                    const float* grid, int g, int ls, float* lo, float* step,
+                                    float* err, void* stream) {
+  clear_error();
+  HI2X_REQUIRE(block == 16 || block == 32 || block == 64, "ladder_fit_rows: block %lld",
+               (long long)block);
+  HI2X_REQUIRE(k > 0 && k % block == 0, "ladder_fit_rows: K=%lld not a multiple of %lld",
+               (long long)k, (long long)block);
+  HI2X_REQUIRE(g >= 1 && g <= 8 && grid, "ladder_fit_rows: grid of %d points", g);
+  HI2X_REQUIRE(nlev >= 2 && nlev <= 256 && ls >= 0, "ladder_fit_rows: nlev=%d ls=%d", nlev, ls);
+  if (rows == 0) return HI2X_OK;
+  HI2X_REQUIRE(w && d && d_row && lo && step, "ladder_fit_rows: null buffer");
+  Grid gr{};
+  for (int i = 0; i < g; ++i) gr.v[i] = grid[i];
+  hipStream_t s = as_stream(stream);
+  switch (block) {
+    case 16: return launch_fit<16>(w, d, rows, k, nlev, gr, g, ls, lo, step, err, s, d_row);
+    case 32: return launch_fit<32>(w, d, rows, k, nlev, gr, g, ls, lo, step, err, s, d_row);
+    default: return launch_fit<64>(w, d, rows, k, nlev, gr, g, ls, lo, step, err, s, d_row);
   }
 }
 
@@ -653,6 +692,22 @@ extern "C" int hi2x_finish(const uint8_t* codes_ro, const float* comp_ro, const 
     if (rc) return rc;
   }
   hipLaunchKernelGGL(sse_kernel, dim3((unsigned)((n + 7) / 8)), dim3(256), 0, s, codes, n, k,
-                     block, lo_d, step_d, ldd, w, d, sse);
+                     block, lo_d, step_d, ldd, w, d, sse, (const int32_t*)nullptr,
+                     (const hi2x_rows_group*)nullptr);
+  return launch_status("sse_kernel");
+}
+
+extern "C" int hi2x_finish_rows(const uint8_t* codes, int64_t n, int64_t k, const float* lo_d,
+                                const float* step_d, int64_t ldd, const int32_t* row_grp,
+                                const hi2x_rows_group* groups, float* sse, void* stream) {
+  clear_error();
+  HI2X_REQUIRE(n >= 0 && k > 0 && k % 16 == 0 && ldd >= k / 16, "finish_rows: bad shape");
+  if (n == 0) return HI2X_OK;
+  HI2X_REQUIRE(codes && lo_d && step_d && row_grp && groups && sse, "finish_rows: null buffer");
+  hipStream_t s = as_stream(stream);
+  LaunchTimer timer(HI2X_TIME_FINISH, (double)n * k * 5, s);
+  hipLaunchKernelGGL(sse_kernel, dim3((unsigned)((n + 7) / 8)), dim3(256), 0, s, codes, n, k,
+                     (int64_t)64, lo_d, step_d, ldd, (const float*)nullptr, (const float*)nullptr,
+                     sse, row_grp, groups);
   return launch_status("sse_kernel");
 }

@@ -365,6 +365,8 @@ class _Unit:
     blk_of: torch.Tensor  # [K] block of each column in rounding order
     codes: torch.Tensor | None = None  # uint8 [n, K] in rounding order
     comp: torch.Tensor | None = None  # fp32 [n, K] value each code was rounded from
+    params: torch.Tensor | None = None  # uint8 [n, nb, 2] (prepared with its batch)
+    sse: torch.Tensor | None = None  # fp32 [n] (finished with its batch)
 
 
 def _prepare(ji: int, job: GptqJob, s: int, step_rows: int, effort: str,
@@ -399,6 +401,123 @@ def _prepare(ji: int, job: GptqJob, s: int, step_rows: int, effort: str,
     return _Unit(ji, s, wc, lo_u8, step_u8, consts, lo_d, step_d, cols // job.block)
 
 
+# Batches of at least this many chunks (all without a column permutation, rows fp32 and
+# contiguous) are prepared and finished as a whole: one ladder fit and one params launch
+# per (block, bits) class and one sse launch per batch, instead of several launches and
+# allocations per chunk (the many small jobs of an MoE layer's experts).  Results are
+# the same: every row sees the same operations in the same order.
+GROUPED_MIN = 4
+
+
+def _groupable(jobs: list, specs: list, members: list[int]) -> bool:
+    for t in members:
+        job = jobs[specs[t][0]]
+        if (job.perm is not None or job.w.dtype != torch.float32 or not job.w.is_contiguous()
+                or job.w.shape[1] % job.block):
+            return False
+    return True
+
+
+def _prepare_grouped(jobs: list, specs: list, members: list[int], effort: str,
+                     dev: torch.device, k: int):
+    """The chunks ``members`` of one batch (see GROUPED_MIN), ordered by (block, bits) so
+    that each class's rows are contiguous: the padded working buffer, every row's ladder
+    fit with its own job's d (``hi2x_ladder_fit_rows``) and params (``hi2x_params``) per
+    class, the decoded ladders written straight into the batch's ``lo``/``st``
+    (``ldp = K / 16``).  Padding rows are zero rows: they fit to lo = step = 0 and
+    quantise to zero bytes, the zeros the per-chunk path leaves them.  Returns the units
+    (in batch order), the buffer and (lo, st)."""
+    order = sorted(members, key=lambda t: (jobs[specs[t][0]].block, jobs[specs[t][0]].nbits))
+    sizes = [specs[t][2] for t in order]
+    padded = _padded(sizes)
+    total = sum(padded)
+    offs = [0]
+    for pn in padded:
+        offs.append(offs[-1] + pn)
+    buf = torch.zeros(total, k, dtype=torch.float32, device=dev)
+    d_at: dict[int, int] = {}
+    dl, urow = [], []
+    for t, o in zip(order, offs):
+        ji, s0, n, _ = specs[t]
+        job = jobs[ji]
+        buf[o:o + n].copy_(job.w[s0:s0 + n])
+        key = id(job.d)
+        if key not in d_at:
+            d_at[key] = len(dl)
+            dl.append(job.d.to(dev, torch.float32).reshape(-1))
+        urow.append(d_at[key])
+    dtab = torch.stack(dl).contiguous()
+    meta = _lib.h2d(torch.tensor(urow + padded, dtype=torch.int64), dev)
+    d_row = torch.repeat_interleave(meta[:len(order)].to(torch.int32), meta[len(order):],
+                                    output_size=total)
+    ldp = k // 16
+    lo = torch.zeros(total, ldp, dtype=torch.float32, device=dev)
+    st = torch.zeros(total, ldp, dtype=torch.float32, device=dev)
+    cfg = EFFORT[effort]
+    from .encode import _grid_array
+
+    units, i = [], 0
+    while i < len(order):
+        job0 = jobs[specs[order[i]][0]]
+        j = i
+        while j < len(order) and (jobs[specs[order[j]][0]].block,
+                                  jobs[specs[order[j]][0]].nbits) == (job0.block, job0.nbits):
+            j += 1
+        r0, r1 = offs[i], offs[j]
+        rows, b = r1 - r0, job0.block
+        nb = k // b
+        lo_c = torch.empty(rows, nb, dtype=torch.float32, device=dev)
+        st_c = torch.empty(rows, nb, dtype=torch.float32, device=dev)
+        _lib.call("hi2x_ladder_fit_rows", dev, _lib.ptr(buf[r0:r1]), _lib.ptr(dtab),
+                  _lib.ptr(d_row[r0:r1]), rows, k, b, 2 ** job0.nbits,
+                  _grid_array(cfg["grid"]), len(cfg["grid"]), int(cfg["ls"]), _lib.ptr(lo_c),
+                  _lib.ptr(st_c), None)
+        lo_u8 = torch.empty(rows, nb, dtype=torch.uint8, device=dev)
+        st_u8 = torch.empty(rows, nb, dtype=torch.uint8, device=dev)
+        consts = torch.empty(rows, 3, dtype=torch.float16, device=dev)
+        _lib.call("hi2x_params", dev, _lib.ptr(lo_c), _lib.ptr(st_c), rows, nb, _lib.ptr(lo_u8),
+                  _lib.ptr(st_u8), _lib.ptr(consts), _lib.ptr(lo[r0:r1]), _lib.ptr(st[r0:r1]),
+                  ldp)
+        params = torch.stack([lo_u8, st_u8], dim=-1)
+        blk_of = torch.arange(k, device=dev) // b
+        for q in range(i, j):
+            ji, s0, n, _ = specs[order[q]]
+            o = offs[q] - r0
+            units.append(_Unit(ji, s0, buf[offs[q]:offs[q] + n], lo_u8[o:o + n], st_u8[o:o + n],
+                               consts[o:o + n], lo[offs[q]:offs[q] + n, :nb],
+                               st[offs[q]:offs[q] + n, :nb], blk_of,
+                               params=params[o:o + n]))
+        i = j
+    return order, units, buf, (lo, st)
+
+
+def _finish_grouped(units: list[_Unit], jobs: list, total: int, k: int, row_grp: torch.Tensor,
+                    codes: torch.Tensor, tabs, dev: torch.device) -> None:
+    """Every unit's sse of a batch prepared by _prepare_grouped in one launch
+    (``hi2x_finish_rows``); the units' rows are in batch order at 128-row boundaries."""
+    sizes = [x.codes.shape[0] for x in units]
+    padded = _padded(sizes)
+    tab, off = [], 0
+    for x, n, pn in zip(units, sizes, padded):
+        job = jobs[x.job]
+        w = job.w[x.s:x.s + n]
+        d = job.d.to(dev, torch.float32).reshape(-1)
+        if not d.is_contiguous():
+            d = d.contiguous()
+        x._keep = (w, d)  # alive until the launch has run (the caller's stream holds it)
+        tab += [w.data_ptr(), d.data_ptr(), off, n, job.block]
+        off += pn
+    groups = _lib.h2d(torch.tensor(tab, dtype=torch.int64), dev)
+    sse = torch.empty(total, dtype=torch.float32, device=dev)
+    lo, st = tabs
+    _lib.call("hi2x_finish_rows", dev, _lib.ptr(codes), total, k, _lib.ptr(lo), _lib.ptr(st),
+              lo.shape[1], _lib.ptr(row_grp), _lib.ptr(groups), _lib.ptr(sse))
+    off = 0
+    for x, n, pn in zip(units, sizes, padded):
+        x.sse = sse[off:off + n]
+        off += pn
+
+
 def _padded(sizes: list[int]) -> list[int]:
     """Rows of each unit in a batch's working buffer: every unit of a multi-unit batch
     starts on a 128-row boundary, so that no workgroup or tile of the kernels holds rows
@@ -410,12 +529,14 @@ def _padded(sizes: list[int]) -> list[int]:
 
 def _round_kernel(
     units: list[_Unit], jobs: list[GptqJob], want_comp: bool = False, super_blocks=None,
-    buf: torch.Tensor | None = None,
-) -> None:
+    buf: torch.Tensor | None = None, tabs=None,
+):
     """All ``units`` (same K, same device) through ``hi2x_gptq_run``: one intra-block
     launch per 128 columns for every row, the cross-block updates on MFMA with the
     reference's rounding.  ``buf``: the batch's working buffer when the units' working
-    copies already sit in it (prepared in place)."""
+    copies already sit in it (prepared in place); ``tabs``: the batch's decoded ladders
+    (lo, st) when they are written there already (``_prepare_grouped``).  Returns
+    (total rows, row -> unit map, codes)."""
     dev, k = units[0].wc.device, units[0].wc.shape[1]
     sizes = [x.wc.shape[0] for x in units]
     # Padding rows have w = lo = step = 0: they round to code 0 with zero error and
@@ -429,15 +550,19 @@ def _round_kernel(
     else:
         wc = units[0].wc
     ldp = k // 16
-    lo = torch.zeros(total, ldp, dtype=torch.float32, device=dev)
-    st = torch.zeros(total, ldp, dtype=torch.float32, device=dev)
+    if tabs is not None:
+        lo, st = tabs
+    else:
+        lo = torch.zeros(total, ldp, dtype=torch.float32, device=dev)
+        st = torch.zeros(total, ldp, dtype=torch.float32, device=dev)
     views, off = [], 0
     for x, n, pn in zip(units, sizes, padded):
         nb = x.lo_d.shape[1]
         if len(units) > 1 and buf is None:
             wc[off : off + n] = x.wc
-        lo[off : off + n, :nb] = x.lo_d
-        st[off : off + n, :nb] = x.step_d
+        if tabs is None:
+            lo[off : off + n, :nb] = x.lo_d
+            st[off : off + n, :nb] = x.step_d
         views.append((off, n))
         off += pn
     # the batch's small tables (row counts, factor addresses, highest codes, blocks) in
@@ -473,6 +598,7 @@ def _round_kernel(
         x.comp = None if comp is None else comp[o : o + n]
     # Temporaries freed here (factor copies, index tensors, workspace) return to
     # torch's caching allocator, which reuses them only in order on this stream.
+    return total, row_grp, codes
 
 
 def _finish(unit: _Unit, job: GptqJob) -> Encoded:
@@ -530,7 +656,8 @@ class PreparedJobs:
     jobs: list[GptqJob]
     units: list[_Unit]
     backend: str
-    # the rounding batches: (device, K) -> [(units, working buffer or None)]
+    # the rounding batches: (device, K) -> [(units, working buffer or None, the batch's
+    # decoded ladders (lo, st) when prepared as a whole, else None)]
     batches: dict
 
     def record_stream(self, stream: torch.cuda.Stream) -> None:
@@ -541,9 +668,13 @@ class PreparedJobs:
                 if t is not None:
                     t.record_stream(stream)
         for bl in self.batches.values():
-            for _, buf in bl:
-                if buf is not None:
-                    buf.record_stream(stream)
+            for _, buf, tabs in bl:
+                for t in (buf,) + (tabs or ()):
+                    if t is not None:
+                        t.record_stream(stream)
+            for x in self.units:
+                if x.params is not None:
+                    x.params.record_stream(stream)
 
 
 @torch.no_grad()
@@ -576,6 +707,12 @@ def prepare_jobs_gptq(jobs: list[GptqJob], effort: str = "normal",
     batches: dict[tuple, list] = {}
     for (dev, k), bl in plan.items():
         for members in bl:
+            if len(members) >= GROUPED_MIN and _groupable(jobs, specs, members):
+                order, us, buf, tabs = _prepare_grouped(jobs, specs, members, effort, dev, k)
+                for t, u in zip(order, us):
+                    units[t] = u
+                batches.setdefault((dev, k), []).append((us, buf, tabs))
+                continue
             buf = None
             if len(members) > 1:
                 sizes = [specs[t][2] for t in members]
@@ -592,7 +729,7 @@ def prepare_jobs_gptq(jobs: list[GptqJob], effort: str = "normal",
                         buf[off + n : off + pn].zero_()
                     off += pn
                 units[t] = _prepare(ji, jobs[ji], s0, st, effort, dest)
-            batches.setdefault((dev, k), []).append(([units[t] for t in members], buf))
+            batches.setdefault((dev, k), []).append(([units[t] for t in members], buf, None))
     return PreparedJobs(jobs, units, backend, batches)
 
 
@@ -625,7 +762,7 @@ def round_prepared(prep: PreparedJobs, comp: bool = False,
     batches = prep.batches
     # batches of different K are independent: each runs on its own stream
     side = []
-    for bi, ((dev, _k), bl) in enumerate(batches.items()):
+    for bi, ((dev, k), bl) in enumerate(batches.items()):
         _use_kernel(dev, backend)
         main = torch.cuda.current_stream(dev)
         st = _lib.side_stream(dev, bi) if len(batches) > 1 else main
@@ -633,26 +770,35 @@ def round_prepared(prep: PreparedJobs, comp: bool = False,
             st.wait_stream(main)
             side.append((main, st))
         with torch.cuda.stream(st):
-            for batch, buf in bl:
+            for batch, buf, tabs in bl:
                 if st is not main:
                     for x in batch:
                         for t in (x.wc, x.lo_d, x.step_d, x.blk_of, jobs[x.job].u):
                             t.record_stream(st)
-                    if buf is not None:
-                        buf.record_stream(st)
-                _round_kernel(batch, jobs, comp, super_blocks, buf)
+                    for t in (buf,) + (tabs or ()):
+                        if t is not None:
+                            t.record_stream(st)
+                total, row_grp, codes = _round_kernel(batch, jobs, comp, super_blocks, buf,
+                                                      tabs)
+                if tabs is not None:
+                    _finish_grouped(batch, jobs, total, k, row_grp, codes, tabs, dev)
                 for x in batch:
                     if st is not main:
                         x.codes.record_stream(main)
                         if x.comp is not None:
                             x.comp.record_stream(main)
+                        if x.sse is not None:
+                            x.sse.record_stream(main)
                     x.wc = None  # free the working copy early
-            bl[:] = [(batch, None) for batch, _ in bl]
+            bl[:] = [(batch, None, None) for batch, _, _ in bl]
     for main, st in side:
         main.wait_stream(st)
     per_job: list[list[Encoded]] = [[] for _ in jobs]
     for x in units:
-        per_job[x.job].append(_finish(x, jobs[x.job]))
+        if x.sse is not None:  # finished with its batch
+            per_job[x.job].append(Encoded(x.codes, x.params, x.consts, x.sse, x.comp))
+        else:
+            per_job[x.job].append(_finish(x, jobs[x.job]))
     out = []
     for encs in per_job:
         if len(encs) == 1:

@@ -109,6 +109,14 @@ int hi2x_ladder_fit(const float* w, const float* d, int64_t rows, int64_t k, int
                     int nlev, const float* grid, int g, int ls, float* lo, float* step,
                     float* err, void* stream);
 
+/* hi2x_ladder_fit for rows of several jobs at once (the per-chunk fits of _prepare,
+ * hi2/hessian.py:208-232, each chunk with its own job's d): row r is fitted with the
+ * weights d + d_row[r] * k (d is [G, k] f32, d_row [rows] i32 device arrays).  Results
+ * equal hi2x_ladder_fit on each row with its own d. */
+int hi2x_ladder_fit_rows(const float* w, const float* d, const int32_t* d_row, int64_t rows,
+                         int64_t k, int64_t block, int nlev, const float* grid, int g,
+                         int ls, float* lo, float* step, float* err, void* stream);
+
 /* quantize_params + decode_params (hi2/encode.py:95-119, hi2/format.py:45-60):
  * lo, step [rows, nb] -> lo_u8, step_u8 [rows, nb], consts [rows, 3] fp16 bits
  * (lo_min, lo_scale, step_scale), lo_d, step_d [rows, ldd] f32 decoded values
@@ -132,6 +140,26 @@ int hi2x_finish(const uint8_t* codes_ro, const float* comp_ro, const int64_t* pe
                 int64_t n, int64_t k, int64_t block, const float* lo_d, const float* step_d,
                 int64_t ldd, const float* w, const float* d, uint8_t* codes, float* comp,
                 float* sse, void* stream);
+
+/* One group of rows of a batch for hi2x_finish_rows: rows [row0, row0 + rows) of the
+ * batch are the uncompensated rows w [rows, k] f32 (stored basis, rounding order =
+ * storage order), weighted by d [k] f32, on ladders of `block` columns. */
+typedef struct hi2x_rows_group {
+  const float* w;
+  const float* d;
+  int64_t row0;
+  int64_t rows;
+  int64_t block;
+} hi2x_rows_group;
+
+/* The sse of _finish (hi2/hessian.py:318-345, without a column permutation) for every
+ * row of a batch of several jobs at once: row r belongs to groups[row_grp[r]] (a device
+ * array of G groups; row_grp [n] i32 on the device); codes [n, k] u8, lo_d/step_d
+ * [n, ldd] f32 (ldd >= k / 16) in batch layout.  sse [n] f32 equals hi2x_finish's on each
+ * group; rows outside their group's range (padding) are left unwritten. */
+int hi2x_finish_rows(const uint8_t* codes, int64_t n, int64_t k, const float* lo_d,
+                     const float* step_d, int64_t ldd, const int32_t* row_grp,
+                     const hi2x_rows_group* groups, float* sse, void* stream);
 
 /* The codes of encode_rows (hi2/encode.py:151-155), nearest rounding onto the fitted
  * ladders: codes [rows, k] u8 = clamp(st == 0 ? 0 : rint((w - lo) / st), 0, 2^nbits - 1)

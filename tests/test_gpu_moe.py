@@ -212,3 +212,35 @@ def test_cfg5_layer_hessians_floor_factors_and_gptq(dev):
     for j, (g, w) in enumerate(zip(got, want)):
         assert np.array_equal(N(g.codes), w["codes"]), j
         assert np.array_equal(N(g.comp), w["comp"]), j
+
+
+def test_grouped_preparation_equals_per_chunk_preparation(dev, monkeypatch):
+    """A batch of many small jobs (an MoE layer's experts: each job its own d and factor,
+    INT2/B32 and INT4/B64 rows, K = 512 and 256) prepared and finished as a whole (one
+    ladder fit and params launch per class, one sse launch per batch) equals the
+    per-chunk path (GROUPED_MIN above the chunk count) in every output, bit for bit, with
+    and without comp."""
+    import hi2_amd.hessian as H
+
+    rng = np.random.default_rng(11)
+    jobs = []
+    for e in range(10):
+        for k in (512, 256):
+            x = rng.standard_normal((2 * k, k)) * np.exp(0.4 * rng.standard_normal(k))
+            hs = (x.T @ x / (2 * k)).astype(np.float32)
+            u = torch.from_numpy(oracle.inverse_factor(hs, 0.01)[0]).to(dev)
+            d = torch.from_numpy(np.diag(hs).copy()).to(dev)
+            for nb, b in ((2, 32), (4, 64)):
+                n = int(rng.integers(20, 150))
+                w = torch.from_numpy((rng.standard_normal((n, k)) * 0.02).astype(np.float32))
+                jobs.append(H.GptqJob(w.to(dev), d, u, nb, b))
+    for comp in (False, True):
+        print(f"grouped vs per-chunk, comp={comp}", flush=True)
+        got = H.encode_jobs_gptq(jobs, "normal", comp=comp)
+        monkeypatch.setattr(H, "GROUPED_MIN", 10 ** 9)
+        want = H.encode_jobs_gptq(jobs, "normal", comp=comp)
+        monkeypatch.setattr(H, "GROUPED_MIN", 4)
+        for j, (g, w) in enumerate(zip(got, want)):
+            for f in ("codes", "params", "sse") + (("comp",) if comp else ()):
+                assert torch.equal(getattr(g, f), getattr(w, f)), (j, f)
+            assert torch.equal(g.consts.view(torch.int16), w.consts.view(torch.int16)), j
