@@ -196,7 +196,7 @@ def _encode_block(xs, ws, masks, timer=None, lanes=None, keep=None, cfg=CFG3):
     # the critical chain's preparation moves to the last chain's stream (with one lane
     # there is nowhere to move it)
     crit = order[0] if len(lanes) > 1 and OFFLOAD_PREP else None
-    helper = order[-1] if crit is not None else None
+    helper = lanes[-1][0] if crit is not None else None  # first chain of the last lane
     chains = {}
     for li in range(1, len(lanes)):  # lane 0 is main itself
         _chain_stream(dev, li).wait_stream(main)

@@ -434,13 +434,18 @@ def _prepare_grouped(jobs: list, specs: list, members: list[int], effort: str,
     offs = [0]
     for pn in padded:
         offs.append(offs[-1] + pn)
-    buf = torch.zeros(total, k, dtype=torch.float32, device=dev)
+    # padding rows must read zero: a whole-buffer fill for many units (one launch), the
+    # padding slices alone for a few (no second pass over the rows)
+    few = len(order) <= 16
+    buf = (torch.empty if few else torch.zeros)(total, k, dtype=torch.float32, device=dev)
     d_at: dict[int, int] = {}
     dl, urow = [], []
-    for t, o in zip(order, offs):
+    for t, o, pn in zip(order, offs, padded):
         ji, s0, n, _ = specs[t]
         job = jobs[ji]
         buf[o:o + n].copy_(job.w[s0:s0 + n])
+        if few and pn > n:
+            buf[o + n:o + pn].zero_()
         key = id(job.d)
         if key not in d_at:
             d_at[key] = len(dl)
