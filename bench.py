@@ -176,9 +176,11 @@ def _encode_block(xs, ws, masks, timer=None, lanes=None, keep=None, cfg=CFG3):
     (the widest input: the critical path) hands its rotations and ladder fits, which need
     only its Hessian's diagonal, to the head of the last chain's stream, where they run
     while its factor is computed; its rounding waits for them.  Once every chain has ended,
-    one launch packs all linears.  The host waits only after every chain has been enqueued
-    (factor status, then one read of the packing's range counter).  keep (a dict) receives
-    each input's (stream, hs, jobs, where, encs)."""
+    one launch packs all linears; the host builds its tables while the chains run.  The
+    host waits once, for the packing's range counter, and then reads the factor statuses:
+    an input whose first factor attempt failed gets the damping retries, its rounding is
+    redone and the block is packed again.  keep (a dict) receives each input's (stream, hs,
+    jobs, where, encs)."""
     import torch
 
     from hi2_amd.format import assemble_many, rotate_rows
@@ -198,6 +200,8 @@ def _encode_block(xs, ws, masks, timer=None, lanes=None, keep=None, cfg=CFG3):
     crit = order[0] if len(lanes) > 1 and OFFLOAD_PREP else None
     helper = lanes[-1][0] if crit is not None else None  # first chain of the last lane
     chains = {}
+    point = timer.point if timer else (lambda name: None)
+    point("start")
     for li in range(1, len(lanes)):  # lane 0 is main itself
         _chain_stream(dev, li).wait_stream(main)
     lead = None  # the first chain's head start: the others wait for its Hessian stages
@@ -274,30 +278,50 @@ def _encode_block(xs, ws, masks, timer=None, lanes=None, keep=None, cfg=CFG3):
             mark("gptq")
             chains[crit][7] = round_prepared(cprep)
             mark("end")
-    bad = torch.zeros(1, dtype=torch.int32, device=dev)
-    tensors, names = [], []
-    for inp in reversed(order):  # the long chain last
+    point("enqueued")
+
+    def pack():
+        """Every linear of the block packed by one launch, on the main stream once every
+        chain has ended (the host builds the launch's tables while the chains run)."""
+        bad = torch.zeros(1, dtype=torch.int32, device=dev)
+        tensors, names = [], []
+        for inp in order:
+            st, hs, u, status, had, jobs, where, encs = chains[inp]
+            if st != main:
+                main.wait_stream(st)
+            for name, n, k, i in cfg["linears"]:
+                if i != inp:
+                    continue
+                pieces = [(rows, e.codes, e.params, e.consts)
+                          for (nm, rows), e in zip(where, encs) if nm == name]
+                tensors.append(dict(pieces=pieces, row_nbits=masks[name]["nbits"],
+                                    row_block=masks[name]["block"],
+                                    had=torch.ones(k // 16, dtype=torch.uint8), k=k))
+                names.append(name)
+        return dict(zip(names, assemble_many(tensors, stager=_DeviceStager, bad=bad))), bad
+
+    out, bad = pack()
+    point("packed")
+    if int(bad.item()):  # waits for every chain and the packing
+        raise ValueError("code outside the ladder")
+    point("end")
+    # the factor statuses are final now: an input whose first attempt failed gets the
+    # reference's damping retries, its rounding redone, and the block is packed again
+    redo = False
+    for inp in order:
         st, hs, u, status, had, jobs, where, encs = chains[inp]
         with torch.cuda.stream(st):
-            if finish_factor(hs, u, status, DAMP):  # more damping was needed: redo the rounding
-                encs = encode_jobs_gptq(jobs, EFFORT)
-        main.wait_stream(st)
-        for name, n, k, i in cfg["linears"]:
-            if i != inp:
-                continue
-            pieces = [(rows, e.codes, e.params, e.consts)
-                      for (nm, rows), e in zip(where, encs) if nm == name]
-            tensors.append(dict(pieces=pieces, row_nbits=masks[name]["nbits"],
-                                row_block=masks[name]["block"],
-                                had=torch.ones(k // 16, dtype=torch.uint8), k=k))
-            names.append(name)
-        if keep is not None:
+            if finish_factor(hs, u, status, DAMP):
+                chains[inp][7] = encode_jobs_gptq(jobs, EFFORT)
+                redo = True
+    if redo:
+        out, bad = pack()
+        if int(bad.item()):
+            raise ValueError("code outside the ladder")
+    if keep is not None:
+        for inp in order:
+            st, hs, u, status, had, jobs, where, encs = chains[inp]
             keep[inp] = (st, hs, jobs, where, encs)
-    # every linear of the block packed by one launch, on the main stream once every chain
-    # has ended
-    out = dict(zip(names, assemble_many(tensors, stager=_DeviceStager, bad=bad)))
-    if int(bad.item()):
-        raise ValueError("code outside the ladder")
     return out
 
 
@@ -634,29 +658,39 @@ REFINE_PASSES = 2  # the reference's default for a calibrated GPTQ run without Q
 def refine_linears(kept):
     """Local code refinement of every linear of the block (hi2/calibrate.py:374-391: one
     sweep per tensor over all its candidate groups, with the input's transformed Hessian),
-    each calibration input's linears on that input's stream.  Returns the refined codes."""
+    each calibration input's linears on that input's stream.  The streams other than the
+    caller's (the down_proj input's, the longest chain) are marked background while the
+    work is enqueued, as in the encode step.  Returns the refined codes."""
     import torch
 
+    from hi2_amd import _lib
     from hi2_amd.refine import refine_groups
 
     dev = next(iter(kept.values()))[1].device
     main = torch.cuda.current_stream(dev)
+    side = [kept[inp][0] for inp in CFG3["order"] if kept[inp][0] != main]
+    marked = side if BACKGROUND else []
+    for st in marked:
+        _lib.stream_background(st, True)
     out = {}
-    for inp in CFG3["order"]:
-        st, hs, jobs, where, encs = kept[inp]
-        if st != main:
-            st.wait_stream(main)
-        with torch.cuda.stream(st):
-            for name, n, k, i in LINEARS:
-                if i != inp:
-                    continue
-                xs = [x for x, (nm, _) in enumerate(where) if nm == name]
-                out[name] = refine_groups(
-                    [(jobs[x].w, encs[x], jobs[x].nbits, jobs[x].block) for x in xs], hs,
-                    REFINE_PASSES)
-    for inp in CFG3["order"]:
-        if kept[inp][0] != main:
-            main.wait_stream(kept[inp][0])
+    try:
+        for inp in CFG3["order"]:
+            st, hs, jobs, where, encs = kept[inp]
+            if st != main:
+                st.wait_stream(main)
+            with torch.cuda.stream(st):
+                for name, n, k, i in LINEARS:
+                    if i != inp:
+                        continue
+                    xs = [x for x, (nm, _) in enumerate(where) if nm == name]
+                    out[name] = refine_groups(
+                        [(jobs[x].w, encs[x], jobs[x].nbits, jobs[x].block) for x in xs],
+                        hs, REFINE_PASSES)
+    finally:
+        for st in marked:
+            _lib.stream_background(st, False)
+    for st in side:
+        main.wait_stream(st)
     return out
 
 
@@ -688,16 +722,24 @@ def many_requests(xs, ws, masks):
 
 
 class StageTimer:
-    """Events on each chain's stream at its stage boundaries."""
+    """Events on each chain's stream at its stage boundaries, and host points of the
+    step: each a host clock reading and an event on the caller's stream, so the report
+    shows how far the host's enqueueing ran ahead of the GPU."""
 
     def __init__(self, torch):
         self.torch = torch
         self.events = {}
+        self.points = []
 
     def mark(self, chain, stage):
         e = self.torch.cuda.Event(enable_timing=True)
         e.record()
         self.events.setdefault(chain, []).append((stage, e))
+
+    def point(self, name):
+        e = self.torch.cuda.Event(enable_timing=True)
+        e.record()
+        self.points.append((name, time.perf_counter(), e))
 
     def summary(self):
         self.torch.cuda.synchronize()
@@ -706,6 +748,17 @@ class StageTimer:
             out[chain] = {n0: round(e0.elapsed_time(e1), 3)
                           for (n0, e0), (_, e1) in zip(evs, evs[1:])}
         return out
+
+    def host_points(self):
+        """{point: (host ms, GPU ms)} since the step's first point: the host clock when
+        the point was reached, and the time its event ran on the caller's stream (behind
+        all work enqueued there before it)."""
+        self.torch.cuda.synchronize()
+        if not self.points:
+            return {}
+        _, h0, e0 = self.points[0]
+        return {n: [round((h - h0) * 1e3, 3), round(e0.elapsed_time(e), 3)]
+                for n, h, e in self.points}
 
 
 # kernel families timed by the library (hi2x_timing_*), with the peak that bounds each
@@ -1255,6 +1308,7 @@ def main():
     wall = time.perf_counter() - t0
     ms_step = wall * 1e3 / args.steps
     stages = timer.summary()
+    host_points = timer.host_points()
     roof = trailing_roofline(args.steps, "contended: event-timed launches in the timed steps, "
                              "where the four input chains run concurrently")
     # one more, untimed step with every kernel family event-timed and the chains run one
@@ -1355,6 +1409,9 @@ def main():
                                "damp 0.01, effort normal", "linears": len(LINEARS),
                    "hessian_input_dtype": "bf16 (f32 accumulation)"},
         "chain_stages_ms": stages,
+        "step_points_ms": {"what": "the last timed step: [host clock, GPU time of an event "
+                           "on the caller's stream] at each point, ms since its start",
+                           **host_points},
         "roofline": roof,
         "roofline_isolated": roof_iso,
         "kernels_one_step": kernels,
