@@ -434,9 +434,10 @@ def block_leg(cfg, dev, steps, warmup):
     for _ in range(warmup):
         encode_block(xs, ws, masks, cfg=cfg)
     torch.cuda.synchronize()
-    _lib.timing_enable([0, 1, 2, 11])
     t0 = time.perf_counter()
-    for _ in range(steps):
+    for i in range(steps):
+        if i == steps - 1:  # launch events in the last timed step only
+            _lib.timing_enable([0, 1, 2, 11])
         encode_block(xs, ws, masks, cfg=cfg)
     torch.cuda.synchronize()
     ms = (time.perf_counter() - t0) * 1e3 / steps
@@ -447,7 +448,7 @@ def block_leg(cfg, dev, steps, warmup):
     _lib.timing_enable([])
     per_input, per_linear, rates = stage_breakdown(xs, ws, masks, cfg)
     flops = trailing_flops(cfg)
-    trail_ms = tr[1] / steps
+    trail_ms = tr[1]  # one step's launches
     res = {
         "workload": f"{cfg['name']}: " + ", ".join(f"{n} {r}x{k}" for n, r, k, _ in cfg["linears"])
                     + f"; {cfg['tokens']} tokens; "
@@ -458,8 +459,8 @@ def block_leg(cfg, dev, steps, warmup):
         "trailing_roofline": {"bound": "mfma", "achieved": flops / trail_ms / 1e9,
                               "peak": PEAK_F32 / 1e12, "unit": "TFLOP/s",
                               "frac": flops / trail_ms / 1e9 / (PEAK_F32 / 1e12),
-                              "flops_per_step": flops, "launches_per_step": tr[0] // steps,
-                              "timing": "event-timed launches in the timed steps (chains "
+                              "flops_per_step": flops, "launches_per_step": tr[0],
+                              "timing": "event-timed launches in the last timed step (chains "
                                         "concurrent)"},
         "syrk_tflops_executed": sy[2] / sy[1] / 1e9 if sy[1] > 0 else None,
         "factor_fp32_gemm_tflops": ch[2] / ch[1] / 1e9 if ch[1] > 0 else None,
@@ -608,9 +609,10 @@ def moe_leg(dev, steps, warmup):
     for _ in range(warmup):
         encode_moe(*inp)
     torch.cuda.synchronize()
-    _lib.timing_enable([0, 1, 2, 3, 11])
     t0 = time.perf_counter()
-    for _ in range(steps):
+    for i in range(steps):
+        if i == steps - 1:  # launch events in the last timed step only
+            _lib.timing_enable([0, 1, 2, 3, 11])
         encode_moe(*inp)
     torch.cuda.synchronize()
     ms = (time.perf_counter() - t0) * 1e3 / steps
@@ -627,7 +629,7 @@ def moe_leg(dev, steps, warmup):
         for i1 in range(0, k, 128):
             i2 = min(i1 + 128, k)
             flops += E5 * 2.0 * n * (i2 - i1) * (k - i2)
-    trail_ms = tr[1] / steps
+    trail_ms = tr[1]  # one step's launches
     res = {
         "workload": "cfg5: OLMoE-shaped MoE layer, 64 experts (gate/up 1024x2048 sharing a "
                     "Hessian, down 2048x1024), top-8 of 16384 tokens routed by Zipf(1.1) "
@@ -642,10 +644,10 @@ def moe_leg(dev, steps, warmup):
         "trailing_roofline": {"bound": "mfma", "achieved": flops / trail_ms / 1e9,
                               "peak": PEAK_F32 / 1e12, "unit": "TFLOP/s",
                               "frac": flops / trail_ms / 1e9 / (PEAK_F32 / 1e12),
-                              "flops_per_step": flops, "launches_per_step": tr[0] // steps},
-        "grouped_syrk": {"launches_per_step": sy[0] // steps, "ms_per_step": sy[1] / steps,
+                              "flops_per_step": flops, "launches_per_step": tr[0]},
+        "grouped_syrk": {"launches_per_step": sy[0], "ms_per_step": sy[1],
                          "tflops_executed": sy[2] / sy[1] / 1e9 if sy[1] > 0 else None},
-        "factor_ms_per_step_kernels": (ch[1] + lf[1] + sp[1]) / steps,
+        "factor_ms_per_step_kernels": ch[1] + lf[1] + sp[1],
     }
     del inp
     torch.cuda.empty_cache()
@@ -655,41 +657,46 @@ def moe_leg(dev, steps, warmup):
 REFINE_PASSES = 2  # the reference's default for a calibrated GPTQ run without QAD
 
 
-def refine_linears(kept):
+_REFINE_STREAMS = {}
+
+
+def refine_linears(kept, serial=False):
     """Local code refinement of every linear of the block (hi2/calibrate.py:374-391: one
     sweep per tensor over all its candidate groups, with the input's transformed Hessian),
-    each calibration input's linears on that input's stream.  The streams other than the
-    caller's (the down_proj input's, the longest chain) are marked background while the
-    work is enqueued, as in the encode step.  Returns the refined codes."""
+    each calibration input's linears on a refinement stream of that input's own.  Own
+    streams, not the encode chains' (the down_proj input's is the caller's), and none
+    marked background: 78 against 86 ms per block measured in one process (the
+    refinement is GEMM-bound throughout, so the background reservation only costs).
+    With ``serial`` everything runs on the caller's stream, one linear after another.
+    Returns the refined codes."""
     import torch
 
-    from hi2_amd import _lib
     from hi2_amd.refine import refine_groups
 
     dev = next(iter(kept.values()))[1].device
     main = torch.cuda.current_stream(dev)
-    side = [kept[inp][0] for inp in CFG3["order"] if kept[inp][0] != main]
-    marked = side if BACKGROUND else []
-    for st in marked:
-        _lib.stream_background(st, True)
     out = {}
-    try:
-        for inp in CFG3["order"]:
-            st, hs, jobs, where, encs = kept[inp]
-            if st != main:
-                st.wait_stream(main)
-            with torch.cuda.stream(st):
-                for name, n, k, i in LINEARS:
-                    if i != inp:
-                        continue
-                    xs = [x for x, (nm, _) in enumerate(where) if nm == name]
-                    out[name] = refine_groups(
-                        [(jobs[x].w, encs[x], jobs[x].nbits, jobs[x].block) for x in xs],
-                        hs, REFINE_PASSES)
-    finally:
-        for st in marked:
-            _lib.stream_background(st, False)
-    for st in side:
+    streams = []
+    for li, inp in enumerate(CFG3["order"]):
+        _, hs, jobs, where, encs = kept[inp]
+        key = (dev.index, li)
+        if key not in _REFINE_STREAMS:
+            _REFINE_STREAMS[key] = torch.cuda.Stream(device=dev)
+        st = main if serial else _REFINE_STREAMS[key]
+        if st != main:
+            streams.append(st)
+            st.wait_stream(main)
+        if kept[inp][0] != st:
+            st.wait_stream(kept[inp][0])
+        with torch.cuda.stream(st):
+            for name, n, k, i in LINEARS:
+                if i != inp:
+                    continue
+                xs = [x for x, (nm, _) in enumerate(where) if nm == name]
+                out[name] = refine_groups(
+                    [(jobs[x].w, encs[x], jobs[x].nbits, jobs[x].block) for x in xs], hs,
+                    REFINE_PASSES)
+    for st in streams:
         main.wait_stream(st)
     return out
 
@@ -1299,17 +1306,19 @@ def main():
     from hi2_amd import _lib
 
     timer = StageTimer(torch)
-    _lib.timing_enable([DOMINANT])  # HIP events around each launch of the dominant kernel
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for i in range(args.steps):
-        encode_block(xs, ws, masks, timer if i == args.steps - 1 else None)
+        last = i == args.steps - 1
+        if last:  # HIP events around each launch of the dominant kernel (~1 ms per step)
+            _lib.timing_enable([DOMINANT])
+        encode_block(xs, ws, masks, timer if last else None)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     ms_step = wall * 1e3 / args.steps
     stages = timer.summary()
     host_points = timer.host_points()
-    roof = trailing_roofline(args.steps, "contended: event-timed launches in the timed steps, "
+    roof = trailing_roofline(1, "contended: event-timed launches of the last timed step, "
                              "where the four input chains run concurrently")
     # one more, untimed step with every kernel family event-timed and the chains run one
     # after another on one stream: per-kernel rates without other chains sharing the GPU
@@ -1328,15 +1337,16 @@ def main():
         encode_block(xs, ws, masks, keep=kept)
         refine_linears(kept)  # warm-up
         torch.cuda.synchronize()
-        _lib.timing_enable([5])
         t0 = time.perf_counter()
-        for _ in range(args.refine_steps):
+        for i in range(args.refine_steps):
+            if i == args.refine_steps - 1:  # launch events in the last timed step only
+                _lib.timing_enable([5])
             refine_linears(kept)
         torch.cuda.synchronize()
         r_ms = (time.perf_counter() - t0) * 1e3 / args.refine_steps
         r_stats = kernel_stats(5)
         _lib.timing_enable([5, 6])
-        refine_linears({k: (torch.cuda.current_stream(dev),) + v[1:] for k, v in kept.items()})
+        refine_linears(kept, serial=True)
         torch.cuda.synchronize()
         refine = {
             "what": f"local code refinement, {REFINE_PASSES} sweeps, of all 7 linears' GPTQ "
