@@ -72,3 +72,18 @@ HI2X_HD inline float div_rcp_code(float a, float b, float y) {
   const float q = __builtin_fmaf(r1, y, q1);
   return (__builtin_fabsf(q0) <= 0x1p100f) ? q : q0;
 }
+
+// Whether div_rcp_code(., b, 1 / b) gives the IEEE quotient's code: b normal and finite.
+// A subnormal b (a ladder fit's candidate step over a block whose span is below about
+// 2^-120) has a reciprocal that overflows or is too large for the iteration's remainders.
+HI2X_HD inline bool div_code_ok(float b) {
+  const float ab = __builtin_fabsf(b);
+  return ab >= 0x1p-126f && ab <= 0x1.fffffep127f;
+}
+
+// div_rcp_code for every finite nonzero b: the IEEE quotient where b is subnormal (a
+// branch taken only by such lanes).
+HI2X_HD inline float div_code(float a, float b, float y) {
+  if (__builtin_expect(!div_code_ok(b), 0)) return a / b;
+  return div_rcp_code(a, b, y);
+}

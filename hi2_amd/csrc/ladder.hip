@@ -51,16 +51,25 @@ __global__ __launch_bounds__(256) void ladder_fit_kernel(
   const float span = mx - mn;
 
   // (x - lo) / safe through the correctly rounded reciprocal of safe (div_rcp_code):
-  // the same codes as the IEEE division
-  auto err_of = [&](float lo, float step) {
-    const float safe = (step == 0.0f) ? 1.0f : step;
-    const float ys = 1.0f / safe;
+  // the same codes as the IEEE division.  A subnormal candidate step (spans below about
+  // 2^-120) takes the IEEE division instead, in a branch the wave takes only when one of
+  // its lanes has such a step.
+  auto err_with = [&](float lo, float step, float safe, float ys, auto div) {
     return torch_sum_small<B>([&](int t) {
-      const float c = clamp_code(__builtin_rintf(div_rcp_code(x[t] - lo, safe, ys)), nm);
+      const float c = clamp_code(__builtin_rintf(div(x[t] - lo, safe, ys)), nm);
       const float rec = lo + c * step;
       const float df = rec - x[t];
       return dd[t] * (df * df);
     });
+  };
+  auto err_of = [&](float lo, float step) {
+    const float safe = (step == 0.0f) ? 1.0f : step;
+    const float ys = 1.0f / safe;
+    if (__builtin_amdgcn_ballot_w64(!div_code_ok(safe)) == 0)
+      return err_with(lo, step, safe, ys,
+                      [](float a, float b, float y) { return div_rcp_code(a, b, y); });
+    return err_with(lo, step, safe, ys,
+                    [](float a, float b, float y) { return div_code(a, b, y); });
   };
 
   float best_lo = 0.0f, best_st = 0.0f, best_err = 0.0f;
@@ -82,9 +91,15 @@ __global__ __launch_bounds__(256) void ladder_fit_kernel(
     const float safe = (best_st == 0.0f) ? 1.0f : best_st;
     const float ys = 1.0f / safe;
     float c[B];
+    if (__builtin_amdgcn_ballot_w64(!div_code_ok(safe)) == 0) {
 #pragma unroll
-    for (int t = 0; t < B; ++t)
-      c[t] = clamp_code(__builtin_rintf(div_rcp_code(x[t] - best_lo, safe, ys)), nm);
+      for (int t = 0; t < B; ++t)
+        c[t] = clamp_code(__builtin_rintf(div_rcp_code(x[t] - best_lo, safe, ys)), nm);
+    } else {
+#pragma unroll
+      for (int t = 0; t < B; ++t)
+        c[t] = clamp_code(__builtin_rintf(div_code(x[t] - best_lo, safe, ys)), nm);
+    }
     const float sd = torch_sum_small<B>([&](int t) { return dd[t]; });
     const float sc = torch_sum_small<B>([&](int t) { return dd[t] * c[t]; });
     const float scc = torch_sum_small<B>([&](int t) { return (dd[t] * c[t]) * c[t]; });
@@ -248,13 +263,15 @@ __global__ __launch_bounds__(256) void ladder_fit_group_kernel(
   // within 2 ulp of a half-integer: |q0 - rint(q0)| >= 0.5 - tol, tol = (nm + 1) 2^-22
   // covering 2 ulp everywhere below nm + 1 (farther out both clamp to the same end).
   // The error of a candidate is summed from those cheap codes, and the wave sums it
-  // again with the exact quotients (div_rcp_code) when any of its lanes met a near-tie.
-  // A zero code may come out as -0 here and +0 there: it only ever multiplies into a
-  // term that is squared or added to +0 first, so the sums are the same.
+  // again with the exact quotients (div_code) when any of its lanes met a near-tie or
+  // has a subnormal candidate step (spans below about 2^-120, where the reciprocal
+  // overflows and the IEEE division gives the codes).  A zero code may come out as -0
+  // here and +0 there: it only ever multiplies into a term that is squared or added to +0
+  // first, so the sums are the same.
   const float tol = (nm + 1.0f) * 0x1p-22f;
   auto err_exact = [&](float lo, float step, float safe, float ys) {
     return group_sum<B, NL>([&](int j) {
-      const float c = clamp_code(__builtin_rintf(div_rcp_code(x[j] - lo, safe, ys)), nm);
+      const float c = clamp_code(__builtin_rintf(div_code(x[j] - lo, safe, ys)), nm);
       const float rec = lo + c * step;
       const float df = rec - x[j];
       return dd[j] * (df * df);
@@ -263,7 +280,7 @@ __global__ __launch_bounds__(256) void ladder_fit_group_kernel(
   auto err_of = [&](float lo, float step) {
     const float safe = (step == 0.0f) ? 1.0f : step;
     const float ys = 1.0f / safe;
-    bool near = false;
+    bool near = !div_code_ok(safe);
     const float e = group_sum<B, NL>([&](int j) {
       const float q0 = (x[j] - lo) * ys;
       const float r0 = __builtin_rintf(q0);
@@ -296,9 +313,15 @@ __global__ __launch_bounds__(256) void ladder_fit_group_kernel(
     const float safe = (best_st == 0.0f) ? 1.0f : best_st;
     const float ys = 1.0f / safe;
     float c[NE];
+    if (__builtin_amdgcn_ballot_w64(!div_code_ok(safe)) == 0) {
 #pragma unroll
-    for (int j = 0; j < NE; ++j)
-      c[j] = clamp_code(__builtin_rintf(div_rcp_code(x[j] - best_lo, safe, ys)), nm);
+      for (int j = 0; j < NE; ++j)
+        c[j] = clamp_code(__builtin_rintf(div_rcp_code(x[j] - best_lo, safe, ys)), nm);
+    } else {
+#pragma unroll
+      for (int j = 0; j < NE; ++j)
+        c[j] = clamp_code(__builtin_rintf(div_code(x[j] - best_lo, safe, ys)), nm);
+    }
     const float sd = group_sum<B, NL>([&](int j) { return dd[j]; });
     const float sc = group_sum<B, NL>([&](int j) { return dd[j] * c[j]; });
     const float scc = group_sum<B, NL>([&](int j) { return (dd[j] * c[j]) * c[j]; });

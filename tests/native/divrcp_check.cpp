@@ -3,6 +3,7 @@
 //   div_rcp(a, b, 1/b)      == a / b bit for bit,
 //   div_rcp_fast(a, b, 1/b) == a / b wherever div_rcp_ok(a, a / b's estimate) accepts,
 //   div_rcp_code(a, b, 1/b) rounds and clamps to the same code as a / b (b normal),
+//   div_code(a, b, 1/b)     the same for every finite nonzero b (subnormal b included),
 // over random operand pairs of every exponent and the operands the fast iteration alone
 // gets wrong (subnormal and zero numerators, subnormal quotients, overflow, inf, NaN).
 // Prints one line per family and exits nonzero on the first family with a mismatch.
@@ -38,7 +39,7 @@ static bool same_code(float q, float r, float nm) {
 
 struct Family {
   const char* name;
-  long n = 0, bad = 0, bad_code = 0, bad_ok = 0;
+  long n = 0, bad = 0, bad_code = 0, bad_ok = 0, bad_any = 0;
   float ea = 0, eb = 0;
 };
 
@@ -55,9 +56,21 @@ static void check(Family& f, float a, float b) {
     if (!f.bad && !f.bad_ok) f.ea = a, f.eb = b;
     ++f.bad_ok;
   }
-  // div_rcp_code's divisors are steps and factor diagonals: normal and finite
+  // div_code: any finite divisor (the ladder fit's candidate steps can be subnormal)
+  if (std::isfinite(b))
+    for (float nm : {3.0f, 15.0f, 255.0f})
+      if (!same_code(div_code(a, b, y), q, nm)) {
+        if (!f.bad && !f.bad_any) f.ea = a, f.eb = b;
+        ++f.bad_any;
+        break;
+      }
+  // div_rcp_code's divisors are normal and finite (div_code_ok), else div_code branches
   const float ab = std::fabs(b);
-  if (!(ab >= 0x1p-126f && ab <= 0x1.fffffep127f)) return;
+  if (div_code_ok(b) != (ab >= 0x1p-126f && ab <= 0x1.fffffep127f)) {
+    ++f.bad_any;
+    return;
+  }
+  if (!div_code_ok(b)) return;
   for (float nm : {3.0f, 15.0f, 255.0f})
     if (!same_code(div_rcp_code(a, b, y), q, nm)) {
       if (!f.bad && !f.bad_code) f.ea = a, f.eb = b;
@@ -73,9 +86,10 @@ int main() {
     float v = from_bits((e << 23) | (uint32_t)(g() & 0x7fffff));
     return (g() & 1) ? -v : v;
   };
-  Family fam[6] = {{"random pairs, every exponent"}, {"subnormal numerators"},
+  Family fam[7] = {{"random pairs, every exponent"}, {"subnormal numerators"},
                    {"subnormal / tiny quotients"}, {"zero numerators"},
-                   {"overflowing quotients"}, {"inf / nan operands"}};
+                   {"overflowing quotients"}, {"inf / nan operands"},
+                   {"subnormal divisors (fit steps)"}};
   for (long i = 0; i < 4000000; ++i) check(fam[0], rnd_float(0, 254), rnd_float(0, 254));
   for (long i = 0; i < 2000000; ++i) check(fam[1], rnd_float(0, 0), rnd_float(1, 254));
   for (long i = 0; i < 2000000; ++i) {
@@ -96,11 +110,19 @@ int main() {
     check(fam[5], nan, v);
     check(fam[5], v, inf);
   }
+  // the ladder fit over a block whose span is tiny: numerators x - lo of the span's
+  // size and below, steps span / nm subnormal
+  for (long i = 0; i < 2000000; ++i) {
+    const float b = rnd_float(0, 0);
+    check(fam[6], rnd_float(0, 8), b);
+    check(fam[6], rnd_float(0, 254), b);
+  }
   int rc = 0;
   for (const Family& f : fam) {
     std::printf("%-32s %9ld pairs  div_rcp mismatches %ld  accepted fast mismatches %ld  code "
-                "mismatches %ld", f.name, f.n, f.bad, f.bad_ok, f.bad_code);
-    if (f.bad || f.bad_code || f.bad_ok) {
+                "mismatches %ld  any-divisor code mismatches %ld", f.name, f.n, f.bad, f.bad_ok,
+                f.bad_code, f.bad_any);
+    if (f.bad || f.bad_code || f.bad_ok || f.bad_any) {
       std::printf("  (first: a=%a b=%a)", f.ea, f.eb);
       rc = 1;
     }

@@ -350,6 +350,32 @@ def test_fit_ladder_extremes_equal_oracle(dev, b):
             assert np.array_equal(st.view(np.uint32), st_w.view(np.uint32)), (n, effort)
 
 
+@pytest.mark.parametrize("b", [16, 32, 64])
+def test_fit_ladder_subnormal_steps_equal_oracle(dev, b):
+    """Blocks whose spans are so small that the candidate steps span / nm are subnormal
+    (their reciprocals overflow): the kernels take the IEEE division for those codes.  The
+    fit's outputs equal the oracle's bit for bit (its errors underflow to zero there, so
+    the first candidate wins; the host check of divrcp.h covers the codes themselves)."""
+    from hi2_amd.encode import fit_ladder
+
+    rng = np.random.default_rng(1000 + b)
+    rows, nb = 32, 640 // b
+    tiny = np.float32(2.0) ** -140  # subnormal unit
+    base = np.where(rng.random((rows, nb, 1)) < 0.5, np.float32(0.0),
+                    np.float32(2.0) ** rng.integers(-135, -117, (rows, nb, 1)).astype(np.float32))
+    wb = (base + rng.integers(0, 1 << 12, (rows, nb, b)).astype(np.float32) * tiny)
+    wb = (wb * np.where(rng.random((rows, nb, 1)) < 0.5, 1, -1)).astype(np.float32)
+    db = (rng.random((1, nb, b)) + 0.5).astype(np.float32)
+    for n in (4, 16, 256):
+        for effort in ("fast", "normal"):
+            lo_w, st_w = oracle.fit_ladder(wb, db, n, effort)
+            lo, st = fit_ladder(T(wb, dev), T(db, dev), n, effort)
+            lo, st = N(lo), N(st)
+            assert np.array_equal(lo.view(np.uint32), lo_w.view(np.uint32)), (n, effort)
+            assert np.array_equal(st.view(np.uint32), st_w.view(np.uint32)), (n, effort)
+            assert np.isfinite(lo).all() and np.isfinite(st).all()
+
+
 def test_params_equal_oracle(dev):
     from hi2_amd.encode import params_decoded, quantize_params
     from hi2_amd.format import decode_params
@@ -739,6 +765,73 @@ def test_inverse_factor_wide_channel_scales(dev, lo, hi):
     u64 = torch.linalg.solve_triangular(lo, eye, upper=False)[rev][:, rev]
     rel = ((u - u64).abs() / u64.abs().amax(dim=1, keepdim=True)).max().item()
     assert rel < 1e-5, rel
+
+
+_FP32_FACTOR = r"""
+import sys
+import numpy as np
+import torch
+sys.path.insert(0, sys.argv[1])
+from hi2_amd.hessian import inverse_factor
+h = torch.from_numpy(np.load(sys.argv[2])).cuda()
+np.save(sys.argv[3], inverse_factor(h, 0.01).cpu().numpy())
+"""
+
+
+def test_inverse_factor_elementwise_on_decaying_rows(dev, tmp_path):
+    """K = 4096 with channel scales rising smoothly over 2^16 across the columns, so each
+    row of U = U_A D^-1 decays by up to 2^16 from its largest element.  The big products'
+    fp16 split bounds their error by the operand rows' largest elements, not element by
+    element: the entries of U above 2^-20 of their row's largest are compared one by one
+    with the float64 factor, for the default (split) factor and for the fp32 MFMA one
+    (HI2X_CHOL_FP32=1, read once per process, so in a child process).  Measured: both
+    0.0032 at most and 4.6e-5 / 5.1e-5 at the 99.9th percentile over entries down to 2^-20
+    of their row's largest: the split factor is as accurate element by element."""
+    import os
+    import subprocess
+    import sys
+
+    from hi2_amd.hessian import inverse_factor
+
+    k = 4096
+    g = torch.Generator(device=dev).manual_seed(8)
+    x = torch.randn(2 * k, k, device=dev, generator=g, dtype=torch.float64)
+    h0 = x.T @ x / x.shape[0]
+    del x
+    dsc = torch.exp2(torch.linspace(0.0, 16.0, k, device=dev, dtype=torch.float64))
+    h = (dsc[:, None] * h0 * dsc[None, :]).float().contiguous()
+    del h0
+    u = inverse_factor(h, 0.01).double()
+    hd = h.double()
+    hd = hd + 0.01 * torch.diagonal(hd).mean() * torch.eye(k, device=dev, dtype=torch.float64)
+    rev = torch.arange(k - 1, -1, -1, device=dev)
+    lo = torch.linalg.cholesky(hd[rev][:, rev])
+    eye = torch.eye(k, device=dev, dtype=torch.float64)
+    u64 = torch.linalg.solve_triangular(lo, eye, upper=False)[rev][:, rev]
+    del lo, eye, hd
+    hp, up = tmp_path / "h.npy", tmp_path / "u32.npy"
+    np.save(hp, h.cpu().numpy())
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    env = dict(os.environ, HI2X_CHOL_FP32="1")
+    r = subprocess.run([sys.executable, "-c", _FP32_FACTOR, root, str(hp), str(up)], env=env,
+                       capture_output=True, text=True, timeout=300)
+    assert r.returncode == 0, r.stderr[-2000:]
+    u32 = torch.from_numpy(np.load(up)).to(dev).double()
+    rowmax = u64.abs().amax(dim=1, keepdim=True)
+    live = u64.abs() >= rowmax * 2.0 ** -20
+    decay = (rowmax / u64.abs().clamp_min(1e-300))[live].max().item()
+
+    def elementwise(v):
+        rel = ((v - u64).abs() / u64.abs().clamp_min(1e-300))[live]
+        return rel.max().item(), torch.quantile(rel[:1 << 24].float(), 0.999).item()
+
+    e_split, q_split = elementwise(u)
+    e_fp32, q_fp32 = elementwise(u32)
+    print(f"decay {decay:.3g}; elementwise rel. error max / 99.9 %: split {e_split:.3g} / "
+          f"{q_split:.3g}, fp32 {e_fp32:.3g} / {q_fp32:.3g}")
+    assert decay > 2.0 ** 12  # the rows do decay
+    assert e_split < 2 * e_fp32 + 1e-6, (e_split, e_fp32)
+    assert q_split < 2 * q_fp32 + 1e-7, (q_split, q_fp32)
 
 
 def test_inverse_factor_256_tiles_equal_128_tiles(dev, monkeypatch):
