@@ -211,6 +211,7 @@ class _Chain:
     perm: torch.Tensor | None
     jobs: list = field(default_factory=list)  # indices into the device's job list
     reqs: list = field(default_factory=list)  # the requests that read this input
+    refine_stream: torch.cuda.Stream | None = None  # its refinement's (None: its own)
 
 
 def _rows_of(picks_host: torch.Tensor, lo: int, hi: int, ci: int) -> torch.Tensor:
@@ -218,20 +219,33 @@ def _rows_of(picks_host: torch.Tensor, lo: int, hi: int, ci: int) -> torch.Tenso
 
 
 def _refine_chain(ch, reqs, jobs, job_at, encs, passes: int) -> None:
-    """Enqueue the refinement of a chain's tensors on its stream: one column loop per
-    tensor over all its candidate groups, with the unpermuted Hessian; never for a QAD
-    start (comp_out)."""
+    """Enqueue the refinement of a chain's tensors: one column loop per tensor over all
+    its candidate groups, with the unpermuted Hessian; never for a QAD start (comp_out).
+    It runs on the chain's refinement stream, behind the chain's GPTQ, and the chain's
+    stream waits for it: that stream is never marked background (the refinement is GEMM
+    work throughout, which the background reservation only slows)."""
     by_tensor: dict[int, list[int]] = {}
     for x in ch.jobs:
         if reqs[job_at[x][0]].comp_out is None:
             by_tensor.setdefault(job_at[x][0], []).append(x)
-    with torch.cuda.stream(ch.stream):
+    rst = ch.refine_stream or ch.stream
+    if rst is not ch.stream:
+        rst.wait_stream(ch.stream)
+        ch.hs.record_stream(rst)
+    with torch.cuda.stream(rst):
         for xs in by_tensor.values():
+            if rst is not ch.stream:
+                for x in xs:  # made on the chain's stream, read here
+                    jobs[x].w.record_stream(rst)
+                    for t in (encs[x].codes, encs[x].params, encs[x].consts):
+                        t.record_stream(rst)
             new = refine_groups(
                 [(jobs[x].w, encs[x], jobs[x].nbits, jobs[x].block) for x in xs], ch.hs, passes)
             for x, codes in zip(xs, new):
                 e = encs[x]
                 encs[x] = type(e)(codes, e.params, e.consts, e.sse, e.comp)
+    if rst is not ch.stream:
+        ch.stream.wait_stream(rst)
 
 
 def _round_chain(ch, reqs, jobs, job_at, encs, cfg) -> None:
@@ -331,6 +345,7 @@ def _enqueue(reqs, cfg, ex, i, use_gptq, comp_full, pack, dev, main, lanes):
                 u, status = _factor(hs, cfg.damp)
             ch = _Chain(st, hs, d, u, status, perm)
             ch.reqs = groups[fk]
+            ch.refine_stream = _lib.side_stream(dev, 96 + j % LANES)
             chains.append(ch)
 
             def emit(ri, r, had, ch=ch):
