@@ -13,14 +13,15 @@ Placement on the device:
   rotation flags) is one *chain* on its own stream: Sigma H2D -> ``transform_sigma``
   -> act-order permutation -> damped inverse factor (enqueued without a host wait) ->
   staging, smoothing and rotation of the rows of every tensor that reads that input ->
-  one batched GPTQ call over all their candidate groups.  Chains run on a pool of
-  ``LANES`` streams, so independent inputs overlap on the GPU;
+  one batched GPTQ call over all their candidate groups -> (when configured) the
+  refinement, on a stream of the chain's own that is never marked background.  Chains
+  run on a pool of ``LANES`` streams, so independent inputs overlap on the GPU;
 * the host waits only after every chain is enqueued: for each chain's factor status
-  (the reference's damping retries, which redo that chain's rounding), then per tensor
-  for refinement and for packing, whose range check and D2H copy end the chain;
+  (the reference's damping retries, which redo that chain's rounding and refinement),
+  then per tensor for packing, whose range check and D2H copy end the chain;
 * nearest-rounding rows (``cfg.rounding == "nearest"`` or no Sigma) go through
-  :func:`hi2_amd.encode.encode_rows` (ladder fit, params, codes, sse) on the caller's
-  stream.
+  :func:`hi2_amd.encode.encode_rows` (ladder fit, params, codes, sse) on a side stream
+  of their own.
 
 Weights and Sigma may come from the host in their stored dtype (staged through pinned
 memory, cast and smoothed on the device, as exact as the reference's host cast and
