@@ -65,7 +65,9 @@ template <bool COMP>
 struct RowRegs {
   float w[CPL], loc[CPL], stc[CPL], ys[CPL], yu[CPL], er[CPL], qc[CPL];
   float cm[COMP ? CPL : 1];  // value each owned column was rounded from
-  int inexact;  // error quotients of this lane that fell outside div_rcp_ok's range
+  // lanes of the wave whose error quotient may fall outside the iteration's exact range
+  // (wave-uniform: scalar registers)
+  uint64_t inexact;
 };
 
 // The live part of this lane's U row at p: columns mm >= M (earlier ones are dead at the
@@ -110,7 +112,18 @@ __device__ __forceinline__ void gptq_step(RowRegs<COMP>& R, int L, int q, float 
   const float col = R.w[m];
   const float lo_j = R.loc[m], st_j = R.stc[m];
   const float safe = (st_j == 0.0f) ? 1.0f : st_j;
-  float qv = clamp_code(__builtin_rintf(div_rcp_code(col - lo_j, safe, R.ys[m])), nm);
+  const float dq = col - lo_j;
+  float qv;
+  if constexpr (EXACT) {
+    qv = clamp_code(__builtin_rintf(div_rcp_code(dq, safe, R.ys[m])), nm);
+  } else {
+    // div_rcp_code without its select: the iteration's quotient, whose code is the IEEE
+    // quotient's while |q0| <= 2^100; lanes past that (or NaN) send the wave to the rerun.
+    // Every lane kept has a finite quotient, so the clamp is one median (clamp_code's NaN
+    // propagation only matters in the lanes the rerun redoes)
+    qv = __builtin_amdgcn_fmed3f(__builtin_rintf(div_rcp_fast(dq, safe, R.ys[m])), 0.0f, nm);
+    R.inexact |= __builtin_amdgcn_ballot_w64(!(__builtin_fabsf(dq * R.ys[m]) <= 0x1p100f));
+  }
   if (st_j == 0.0f) qv = 0.0f;
   const float wq = f16_round(lo_j + qv * st_j);
   const float ujj = ub[cur][m];  // U[I][I] in the owner lane
@@ -121,10 +134,16 @@ __device__ __forceinline__ void gptq_step(RowRegs<COMP>& R, int L, int q, float 
     e = num / ujj;
   } else {
     e = div_rcp_fast(num, ujj, R.yu[m]);
-    // counted in every lane, owner or not (a false alarm only costs a rerun; a test on
-    // the owner alone kept a lane mask per step alive and spilled), in a vector register
-    R.inexact += div_rcp_ok(num, num * R.yu[m]) ? 0 : 1;
-    asm volatile("" : "+v"(R.inexact));
+    // div_rcp_ok(num, num yu) holds when |num| is in [2^-50, 2^50] (every column's yu is
+    // in [2^-50, 2^50], checked once per block) or num is +0: tested in every lane, owner
+    // or not (a false alarm only costs a rerun), the lanes that fail OR-ed into a wave
+    // mask in scalar registers
+    // (one ballot per comparison, each the comparison's own lane mask: no vector select)
+    const float an = __builtin_fabsf(num);
+    const uint64_t small = __builtin_amdgcn_ballot_w64(!(an >= 0x1p-50f));  // NaN too
+    const uint64_t large = __builtin_amdgcn_ballot_w64(!(an <= 0x1p50f));
+    const uint64_t nonzero = __builtin_amdgcn_ballot_w64(__builtin_bit_cast(uint32_t, num) != 0u);
+    R.inexact |= (small | large) & nonzero;
   }
   const float eb = row_bcast<s>(e);
   // the selects are pinned here (empty asm): left free, the compiler keeps every step's
@@ -190,7 +209,9 @@ __device__ __forceinline__ void load_row_b(RowRegs<COMP>& R, const int (&bix)[CP
 template <bool COMP>
 __device__ __forceinline__ void load_row_c(RowRegs<COMP>& R, int L, const float* su, int q) {
   // IEEE reciprocals (correctly rounded) of each column's step and factor diagonal;
-  // dead columns (c >= L) get 1
+  // dead columns (c >= L) get 1.  A reciprocal of the diagonal outside [2^-50, 2^50]
+  // (or not finite) marks the wave for the exact rerun: the per-step test relies on it.
+  bool yok = true;
 #pragma unroll
   for (int m = 0; m < CPL; ++m) {
     const int c = QL * m + q;
@@ -198,8 +219,10 @@ __device__ __forceinline__ void load_row_c(RowRegs<COMP>& R, int L, const float*
     const float ud = c < L ? su[c * USTR + lane_off(q) + m] : 1.0f;
     R.ys[m] = 1.0f / sc;
     R.yu[m] = 1.0f / ud;
+    const float ay = __builtin_fabsf(R.yu[m]);
+    yok = yok && ay >= 0x1p-50f && ay <= 0x1p50f;
   }
-  R.inexact = 0;
+  R.inexact = __builtin_amdgcn_ballot_w64(!yok);
 }
 template <bool COMP>
 __device__ __forceinline__ void load_row(RowRegs<COMP>& R, const float* __restrict__ wc,
@@ -350,7 +373,7 @@ __global__ __launch_bounds__(RPG * QL) void gptq_block_kernel(
     float ub[2][CPL];
     load_urow<0>(ub[0], suq);
     gptq_steps<FULL, COMP, false>(std::make_integer_sequence<int, LMAX>{}, R, L, q, nm, suq, ub);
-    if (__ballot(R.inexact != 0) != 0) {
+    if (R.inexact != 0) {
       // some row of this wave met an error quotient outside the iteration's exact range
       // (subnormal or negative-zero numerators, extreme magnitudes): the wave runs the
       // block again from the working copy with IEEE division
