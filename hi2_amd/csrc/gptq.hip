@@ -28,9 +28,10 @@ namespace {
 // lane_off(q)).  The U row of step i+1 is read during step i.
 //
 // Step i (fully unrolled): every lane runs the rounding chain on its own column m=i/16
-// (the two divisions through the lane's precomputed reciprocals: div_rcp_code for the
-// code, the bare iteration for the error, its exactness checked and the block run again
-// with IEEE division in the rare wave where it is not);
+// (the two divisions are the bare reciprocal iteration on the lane's precomputed
+// reciprocals; the lanes whose operands leave the range where the iteration is exact are
+// collected in a wave mask, and the rare wave with any runs the block again with
+// div_rcp_code for the code and IEEE division for the error);
 // only lane q = i%16 owns column i (its U value of row i is then U[i][i]), so its error e
 // is broadcast to the row with DPP row_newbcast, and the row applies
 // w[c] -= e * U[i][c] to the columns it holds.  Columns <= i of the other lanes are dead
@@ -100,9 +101,10 @@ __device__ __forceinline__ void load_urow(float (&u)[CPL], const float* p) {
 // Step I of the column loop, I a compile-time constant so that every register index
 // below is static (no dynamic VGPR indexing).  ub[I & 1] holds this lane's U row I;
 // the step fills ub[(I + 1) & 1] with row I + 1.  With FULL the block has LMAX columns
-// (no length test per step).  The error quotient is the bare reciprocal iteration, its
-// range recorded in R.inexact (a branch in the loop would serialise it); EXACT uses the
-// IEEE division instead, for the rare block that has to be run again.
+// (no length test per step).  Both quotients are the bare reciprocal iteration, their
+// operand ranges recorded in the scalar mask R.inexact (a branch in the loop would
+// serialise it); EXACT uses div_rcp_code for the code and the IEEE division for the
+// error instead, for the rare block that has to be run again.
 template <int I, bool FULL, bool COMP, bool EXACT>
 __device__ __forceinline__ void gptq_step(RowRegs<COMP>& R, int L, int q, float nm,
                                           const float* __restrict__ suq, float (&ub)[2][CPL]) {
