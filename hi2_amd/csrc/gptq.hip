@@ -123,10 +123,14 @@ __device__ __forceinline__ void gptq_step(RowRegs<COMP>& R, int L, int q, float 
     // quotient's while |q0| <= 2^100; lanes past that (or NaN) send the wave to the rerun.
     // Every lane kept has a finite quotient, so the clamp is one median (clamp_code's NaN
     // propagation only matters in the lanes the rerun redoes)
+    // A zero step's column has ys = 0 (load_row_c): its quotient is +0 for every finite
+    // dq, the code 0 the reference gives it, without a select in the chain
     qv = __builtin_amdgcn_fmed3f(__builtin_rintf(div_rcp_fast(dq, safe, R.ys[m])), 0.0f, nm);
     R.inexact |= __builtin_amdgcn_ballot_w64(!(__builtin_fabsf(dq * R.ys[m]) <= 0x1p100f));
   }
-  if (st_j == 0.0f) qv = 0.0f;
+  if constexpr (EXACT) {
+    if (st_j == 0.0f) qv = 0.0f;
+  }
   const float wq = f16_round(lo_j + qv * st_j);
   const float ujj = ub[cur][m];  // U[I][I] in the owner lane
   const bool own = q == s;
@@ -144,8 +148,10 @@ __device__ __forceinline__ void gptq_step(RowRegs<COMP>& R, int L, int q, float 
     const float an = __builtin_fabsf(num);
     const uint64_t small = __builtin_amdgcn_ballot_w64(!(an >= 0x1p-50f));  // NaN too
     const uint64_t large = __builtin_amdgcn_ballot_w64(!(an <= 0x1p50f));
-    const uint64_t nonzero = __builtin_amdgcn_ballot_w64(__builtin_bit_cast(uint32_t, num) != 0u);
-    R.inexact |= (small | large) & nonzero;
+    // +0 passes (the iteration gives +0 there); -0 does not (it would give +0)
+    const uint64_t zero = __builtin_amdgcn_ballot_w64(num == 0.0f);
+    const uint64_t neg = __builtin_amdgcn_ballot_w64(__builtin_bit_cast(int32_t, num) < 0);
+    R.inexact |= (small | large) & ~(zero & ~neg);
   }
   const float eb = row_bcast<s>(e);
   // the selects are pinned here (empty asm): left free, the compiler keeps every step's
@@ -217,9 +223,8 @@ __device__ __forceinline__ void load_row_c(RowRegs<COMP>& R, int L, const float*
 #pragma unroll
   for (int m = 0; m < CPL; ++m) {
     const int c = QL * m + q;
-    const float sc = R.stc[m] == 0.0f ? 1.0f : R.stc[m];
     const float ud = c < L ? su[c * USTR + lane_off(q) + m] : 1.0f;
-    R.ys[m] = 1.0f / sc;
+    R.ys[m] = R.stc[m] == 0.0f ? 0.0f : 1.0f / R.stc[m];  // 0: a zero step (code 0)
     R.yu[m] = 1.0f / ud;
     const float ay = __builtin_fabsf(R.yu[m]);
     yok = yok && ay >= 0x1p-50f && ay <= 0x1p50f;
