@@ -120,13 +120,15 @@ __device__ __forceinline__ void gptq_step(RowRegs<COMP>& R, int L, int q, float 
     qv = clamp_code(__builtin_rintf(div_rcp_code(dq, safe, R.ys[m])), nm);
   } else {
     // div_rcp_code without its select: the iteration's quotient, whose code is the IEEE
-    // quotient's while |q0| <= 2^100; lanes past that (or NaN) send the wave to the rerun.
-    // Every lane kept has a finite quotient, so the clamp is one median (clamp_code's NaN
-    // propagation only matters in the lanes the rerun redoes)
-    // A zero step's column has ys = 0 (load_row_c): its quotient is +0 for every finite
-    // dq, the code 0 the reference gives it, without a select in the chain
+    // quotient's while |q0| = |dq ys| <= 2^100.  That holds in every lane the wave keeps:
+    // load_row_c marks the wave unless |ys| <= 2^40, |lo| <= 2^40 and |step| <= 2^32, and
+    // the error test below marks it unless |num| <= 2^50 with wq finite in fp16, so that
+    // |dq| <= |num| + |wq| + |lo| < 2^51 (NaN and infinities fail those tests).  Every
+    // lane kept has a finite quotient, so the clamp is one median (clamp_code's NaN
+    // propagation only matters in the waves the rerun redoes).  A zero step's column has
+    // ys = 0 (load_row_c): its quotient is +0 for every finite dq, the code 0 the
+    // reference gives it, without a select in the chain.
     qv = __builtin_amdgcn_fmed3f(__builtin_rintf(div_rcp_fast(dq, safe, R.ys[m])), 0.0f, nm);
-    R.inexact |= __builtin_amdgcn_ballot_w64(!(__builtin_fabsf(dq * R.ys[m]) <= 0x1p100f));
   }
   if constexpr (EXACT) {
     if (st_j == 0.0f) qv = 0.0f;
@@ -217,8 +219,10 @@ __device__ __forceinline__ void load_row_b(RowRegs<COMP>& R, const int (&bix)[CP
 template <bool COMP>
 __device__ __forceinline__ void load_row_c(RowRegs<COMP>& R, int L, const float* su, int q) {
   // IEEE reciprocals (correctly rounded) of each column's step and factor diagonal;
-  // dead columns (c >= L) get 1.  A reciprocal of the diagonal outside [2^-50, 2^50]
-  // (or not finite) marks the wave for the exact rerun: the per-step test relies on it.
+  // dead columns (c >= L) get 1.  A reciprocal of the diagonal outside [2^-50, 2^50], of
+  // the step above 2^40, a ladder origin above 2^40 or a step above 2^32 in magnitude (or
+  // any of them not finite) marks the wave for the exact rerun: the per-step tests of
+  // gptq_step rely on these bounds.
   bool yok = true;
 #pragma unroll
   for (int m = 0; m < CPL; ++m) {
@@ -227,7 +231,8 @@ __device__ __forceinline__ void load_row_c(RowRegs<COMP>& R, int L, const float*
     R.ys[m] = R.stc[m] == 0.0f ? 0.0f : 1.0f / R.stc[m];  // 0: a zero step (code 0)
     R.yu[m] = 1.0f / ud;
     const float ay = __builtin_fabsf(R.yu[m]);
-    yok = yok && ay >= 0x1p-50f && ay <= 0x1p50f;
+    yok = yok && ay >= 0x1p-50f && ay <= 0x1p50f && __builtin_fabsf(R.ys[m]) <= 0x1p40f &&
+          __builtin_fabsf(R.loc[m]) <= 0x1p40f && __builtin_fabsf(R.stc[m]) <= 0x1p32f;
   }
   R.inexact = __builtin_amdgcn_ballot_w64(!yok);
 }

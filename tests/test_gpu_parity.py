@@ -228,6 +228,39 @@ def test_tiny_rows_take_the_exact_division_path(dev, scale):
     _same(got, oracle.encode_rows_gptq(w, d, u, 4, 64, "normal"))
 
 
+@pytest.mark.parametrize("kind", ["huge", "tiny_step", "huge_step", "zero_rows"])
+def test_rows_outside_the_column_loops_bounds_take_the_rerun(dev, kind):
+    """The column loop keeps a wave on the reciprocal iteration only while its per-block
+    bounds hold (|1 / step| <= 2^40, |lo| <= 2^40, |step| <= 2^32, 1 / U[c][c] in
+    [2^-50, 2^50]) and its per-step ones (|num| in [2^-50, 2^50] or num = +0).  Rows that
+    break them, next to ordinary rows in the same waves, and rows of exact zeros (num = +0
+    at every step, which must not need the rerun): codes, params, sse and comp equal the
+    oracle (IEEE division) bit for bit.  Rows beyond fp16's range overflow the rounded
+    value wq to infinity, in the oracle as here: their sse and comp are NaN in the same
+    places (compared with NaN equal to NaN)."""
+    w, d, u, _, _ = _layer(48, 256, 37)
+    rng = np.random.default_rng(41)
+    if kind == "huge":  # ladder origins and steps beyond 2^40
+        w[::3] *= np.float32(2.0 ** 45)
+    elif kind == "tiny_step":  # near-constant blocks: steps below 2^-40 (1 / step above)
+        w[1::3] = np.float32(0.75) + rng.standard_normal(w[1::3].shape).astype(np.float32) * np.float32(2.0 ** -46)
+    elif kind == "huge_step":  # steps beyond 2^32 with origins below 2^40
+        w[2::3] = (rng.standard_normal(w[2::3].shape) * 2.0 ** 36).astype(np.float32)
+    else:
+        w[::4] = 0.0
+    got = _encode(dev, w, d, u)
+    want = oracle.encode_rows_gptq(w, d, u, 4, 64, "normal")
+    if kind in ("huge", "huge_step"):
+        assert np.array_equal(N(got.codes), want["codes"])
+        assert np.array_equal(N(got.params), want["params"])
+        assert np.array_equal(N(got.consts).view(np.int16), want["consts"].view(np.int16))
+        assert np.array_equal(N(got.sse), want["sse"], equal_nan=True)
+        assert np.array_equal(N(got.comp), want["comp"], equal_nan=True)
+        assert np.isnan(want["sse"]).any()  # the overflow does happen
+    else:
+        _same(got, want)
+
+
 def _encode(dev, w, d, u):
     from hi2_amd.hessian import encode_rows_gptq
 
