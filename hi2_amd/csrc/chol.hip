@@ -1190,14 +1190,18 @@ __global__ __launch_bounds__(256) void reverse_damp4_kernel(const float* __restr
 // then written back in place after a barrier).
 //
 // The 16 x 16 base is one wave's fused factor-and-invert sweep, lane i (< 16) holding row
-// i in 16 registers.  For c = 0..15:
-//   piv = sqrt(T[c][c]), rp = 1/piv; l_i = T[i][c] rp; the multiplier of column j is
-//   l_j = T[j][c] rp for j > c, rp for j = c, x_j = B[c][j] rp for j < c (row c of L^-1).
-//   Rows i > c, j <= i:  T[i][j] -= l_i m_j  (j > c: Cholesky update; j = c: starts
-//   column c of L^-1 as -l_i rp; j < c: forward substitution)
-//   Row c is final: X[c][j] = B[c][j] rp, X[c][c] = rp.
-// The pivot, column c (T[j][c] of every row j) and row c (B[c][j]) are read into scalar
-// registers with readlane, l_i is the lane's own register: no barrier and no LDS traffic
+// i of the symmetric block in 16 registers (the upper triangle mirrored from the lower one
+// on load).  For c = 0..15, with d = M[c][c], r = 1/sqrt(d) and g_i = -M[i][c] r^2 on
+// the rows i > c (0 on the others):
+//   every j != c:  M[i][j] += g_i M[c][j]
+//     (j > c: the Schur update T[i][j] -= l_i l_j, l_k = T[k][c] r, with T[j][c] = T[c][j]
+//      by symmetry; j < c: the forward substitution B[i][j] -= l_i X[c][j], where row c of
+//      L^-1 is X[c][j] = B[c][j] r)
+//   rows i > c:    M[i][c] = g_i   (= -l_i r, column c of L^-1 before row i's scaling).
+// Row c is then final up to its scale, which is applied once after the sweep:
+// X[c][j] = M[c][j] r_c (j < c), X[c][c] = r_c.  Every multiplier is one of lane c's own
+// registers, broadcast to each row of 16 lanes by DPP (row_newbcast) inside
+// v_fmac_f32_dpp: one instruction per register and column, no barrier and no LDS traffic
 // in the sweep.  The reciprocal and square root are the hardware approximations (the
 // factor is compared to a tolerance, not bit for bit).
 constexpr int LP = NB + 4;  // LDS pitch of the leaf block (floats)
@@ -1208,44 +1212,79 @@ constexpr bool LEAF_SPLIT = HI2X_LEAF_SPLIT;
 
 typedef float f32x4v __attribute__((ext_vector_type(4)));
 
-template <int C, int J>
-__device__ __forceinline__ float lane_read(const float (&v)[16]) {  // v[J] of lane C (uniform)
-  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v[J]), C));
+// v[j] += bcast_C(v[j]) * g for the 15 registers j != C, bcast_C = lane C of each row of 16
+// lanes.  The compiler does not fold a DPP move into an FMA (v_fma_f32 has no DPP form on
+// this target), so the fused instructions are written out.  The leading s_nop 4 gives the
+// five wait states a DPP instruction needs after a VALU write of its source VGPR (two) or
+// of EXEC (five); inside the block no instruction reads a register another one writes.
+#define HI2X_FMAC_DPP(k, C) \
+  "v_fmac_f32_dpp %" #k ", %" #k ", %15 row_newbcast:" #C " row_mask:0xf bank_mask:0xf\n\t"
+#define HI2X_FMAC15(C)                                                                     \
+  "s_nop 4\n\t" HI2X_FMAC_DPP(0, C) HI2X_FMAC_DPP(1, C) HI2X_FMAC_DPP(2, C)              \
+      HI2X_FMAC_DPP(3, C) HI2X_FMAC_DPP(4, C) HI2X_FMAC_DPP(5, C) HI2X_FMAC_DPP(6, C)     \
+          HI2X_FMAC_DPP(7, C) HI2X_FMAC_DPP(8, C) HI2X_FMAC_DPP(9, C) HI2X_FMAC_DPP(10, C) \
+              HI2X_FMAC_DPP(11, C) HI2X_FMAC_DPP(12, C) HI2X_FMAC_DPP(13, C)               \
+                  HI2X_FMAC_DPP(14, C)
+#define HI2X_J(k) ((k) < C ? (k) : (k) + 1)
+#define HI2X_ROW_OPS                                                                   \
+  "+v"(v[HI2X_J(0)]), "+v"(v[HI2X_J(1)]), "+v"(v[HI2X_J(2)]), "+v"(v[HI2X_J(3)]),     \
+      "+v"(v[HI2X_J(4)]), "+v"(v[HI2X_J(5)]), "+v"(v[HI2X_J(6)]), "+v"(v[HI2X_J(7)]), \
+      "+v"(v[HI2X_J(8)]), "+v"(v[HI2X_J(9)]), "+v"(v[HI2X_J(10)]),                    \
+      "+v"(v[HI2X_J(11)]), "+v"(v[HI2X_J(12)]), "+v"(v[HI2X_J(13)]),                  \
+      "+v"(v[HI2X_J(14)])
+template <int C>
+__device__ __forceinline__ void fmac_row(float (&v)[16], float g) {
+  static_assert(C >= 0 && C < 16, "column of the 16 x 16 base");
+  if constexpr (C == 0) asm(HI2X_FMAC15(0) : HI2X_ROW_OPS : "v"(g));
+  else if constexpr (C == 1) asm(HI2X_FMAC15(1) : HI2X_ROW_OPS : "v"(g));
+  else if constexpr (C == 2) asm(HI2X_FMAC15(2) : HI2X_ROW_OPS : "v"(g));
+  else if constexpr (C == 3) asm(HI2X_FMAC15(3) : HI2X_ROW_OPS : "v"(g));
+  else if constexpr (C == 4) asm(HI2X_FMAC15(4) : HI2X_ROW_OPS : "v"(g));
+  else if constexpr (C == 5) asm(HI2X_FMAC15(5) : HI2X_ROW_OPS : "v"(g));
+  else if constexpr (C == 6) asm(HI2X_FMAC15(6) : HI2X_ROW_OPS : "v"(g));
+  else if constexpr (C == 7) asm(HI2X_FMAC15(7) : HI2X_ROW_OPS : "v"(g));
+  else if constexpr (C == 8) asm(HI2X_FMAC15(8) : HI2X_ROW_OPS : "v"(g));
+  else if constexpr (C == 9) asm(HI2X_FMAC15(9) : HI2X_ROW_OPS : "v"(g));
+  else if constexpr (C == 10) asm(HI2X_FMAC15(10) : HI2X_ROW_OPS : "v"(g));
+  else if constexpr (C == 11) asm(HI2X_FMAC15(11) : HI2X_ROW_OPS : "v"(g));
+  else if constexpr (C == 12) asm(HI2X_FMAC15(12) : HI2X_ROW_OPS : "v"(g));
+  else if constexpr (C == 13) asm(HI2X_FMAC15(13) : HI2X_ROW_OPS : "v"(g));
+  else if constexpr (C == 14) asm(HI2X_FMAC15(14) : HI2X_ROW_OPS : "v"(g));
+  else asm(HI2X_FMAC15(15) : HI2X_ROW_OPS : "v"(g));
 }
+#undef HI2X_ROW_OPS
+#undef HI2X_J
+#undef HI2X_FMAC15
+#undef HI2X_FMAC_DPP
 
-template <int C, int... Js>
-__device__ __forceinline__ void base_step(float (&v)[16], int i, bool& bad,
-                                          std::integer_sequence<int, Js...>) {
-  const float d = lane_read<C, C>(v);  // pivot T[c][c]
-  bad = bad || !(d > 0.0f);
+// Column C of the sweep.  Lane i keeps its own pivot in pv (rows below C take theirs at
+// their own column, so i >= C is the previous column's i > C).  M[i][C] becomes g on every
+// row: the rows below need it, and lane C's and the finished rows' registers C are not
+// read again before the final scaling overwrites them.
+template <int C>
+__device__ __forceinline__ void base_step(float (&v)[16], int i, float& pv) {
+  const float d = __builtin_bit_cast(
+      float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v[C]), C));  // pivot M[c][c]
   const float rp = __builtin_amdgcn_rcpf(__builtin_amdgcn_sqrtf(d));
-  const bool below = i > C, at = i == C;
-  const float li = v[C] * rp;  // l_i = T[i][c] rp (rows below c)
-  // row c is final first: X[c][j] = B[c][j] rp (j < c), X[c][c] = rp
-  const float sc = at ? rp : 1.0f;
-  ((v[Js] = Js < C ? v[Js] * sc : v[Js]), ...);
-  v[C] = at ? rp : v[C];
-  // multipliers, uniform over the wave: l_j from row j (j > c), row c's finals (j <= c)
-  const float m[16] = {(Js > C ? __builtin_bit_cast(float, __builtin_amdgcn_readlane(
-                                     __builtin_bit_cast(int, li), (Js > C ? Js : 0)))
-                               : lane_read<C, (Js <= C ? Js : 0)>(v))...};
-  // rows below c: T[i][j] -= l_i m_j (j > c), column c starts as -l_i rp, B[i][j] -= l_i x_j
-  const float lb = below ? li : 0.0f;
-  ((v[Js] = Js == C ? (below ? -lb * m[Js] : v[Js]) : __builtin_fmaf(-lb, m[Js], v[Js])), ...);
+  const float gv = v[C] * -(rp * rp);
+  fmac_row<C>(v, i > C ? gv : 0.0f);
+  v[C] = gv;
+  pv = i >= C ? d : pv;
 }
 
 template <int... Cs>
-__device__ __forceinline__ void base_steps(float (&v)[16], int i, bool& bad,
+__device__ __forceinline__ void base_steps(float (&v)[16], int i, float& pv,
                                            std::integer_sequence<int, Cs...>) {
-  (base_step<Cs>(v, i, bad, std::make_integer_sequence<int, 16>{}), ...);
+  (base_step<Cs>(v, i, pv), ...);
 }
 
 // 16 x 16 block at (o, o): one wave (the caller's wave 0), lane i holds row i % 16 (lanes
-// 16..63 repeat rows 0..15 and do not write back)
+// 16..63 repeat rows 0..15 and do not write back).  Only the block's lower triangle is
+// read: row i below the diagonal, column i (M[j][i] for j > i) as the upper half.
 __device__ __forceinline__ void leaf_base16(float* S, int o, bool& bad) {
   const int l = threadIdx.x & 63, i = l & 15;
   float* row = &S[(o + i) * LP + o];
-  float v[16];
+  float v[16], t[16];
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
     const float4 x = *reinterpret_cast<const float4*>(row + 4 * q);
@@ -1254,9 +1293,18 @@ __device__ __forceinline__ void leaf_base16(float* S, int o, bool& bad) {
     v[4 * q + 2] = x.z;
     v[4 * q + 3] = x.w;
   }
-  base_steps(v, i, bad, std::make_integer_sequence<int, 16>{});
 #pragma unroll
-  for (int j = 0; j < 16; ++j) v[j] = j <= i ? v[j] : 0.0f;  // the block stays lower
+  for (int j = 0; j < 16; ++j) t[j] = S[(o + j) * LP + o + i];
+#pragma unroll
+  for (int j = 0; j < 16; ++j) v[j] = j > i ? t[j] : v[j];
+  float pv = 0.0f;
+  base_steps(v, i, pv, std::make_integer_sequence<int, 16>{});
+  // a pivot not positive (or NaN) anywhere in the block; the same r_i as in the sweep
+  bad = bad || __builtin_amdgcn_ballot_w64(!(pv > 0.0f)) != 0;
+  const float r = __builtin_amdgcn_rcpf(__builtin_amdgcn_sqrtf(pv));
+  // row i of L^-1: X[i][j] = M[i][j] r_i (j < i), X[i][i] = r_i; the block stays lower
+#pragma unroll
+  for (int j = 0; j < 16; ++j) v[j] = j < i ? v[j] * r : (j == i ? r : 0.0f);
   if (l < 16) {
 #pragma unroll
     for (int q = 0; q < 4; ++q)

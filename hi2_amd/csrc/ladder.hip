@@ -143,12 +143,12 @@ struct LaneGroup {  // DPP moves within aligned groups of NL lanes (quad_perm pa
   static constexpr int FIRST = NL == 2 ? 0xA0 : 0x00;  // lane 0 of the group
   template <int CTRL>
   static __device__ __forceinline__ float mov(float v) {
-    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL,
-                                                              0xf, 0xf, false));
+    return __builtin_bit_cast(
+        float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xf, 0xf, true));
   }
   template <int CTRL>
   static __device__ __forceinline__ int movi(int v) {
-    return __builtin_amdgcn_mov_dpp(v, CTRL, 0xf, 0xf, false);
+    return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xf, 0xf, true);
   }
 };
 

@@ -38,9 +38,12 @@ constexpr int USTR = QL * CPL + 4;    // LDS row stride of the Hessian block (fl
 __device__ __forceinline__ int lane_off(int q) { return q * CPL + ((q >> 3) << 2); }
 
 template <int S>
-__device__ __forceinline__ float row_bcast(float v) {  // lane S of each 16-lane row
-  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v),
-                                                            0x150 + S, 0xf, 0xf, false));
+// Lane S of each 16-lane row.  Every source lane is valid, so the old value and bound_ctrl
+// never apply; written as update_dpp with bound_ctrl so that the compiler folds the
+// broadcast into the instruction that uses it (it does not fold a plain DPP move).
+__device__ __forceinline__ float row_bcast(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v),
+                                                               0x150 + S, 0xf, 0xf, true));
 }
 
 // ---------------------------------------------------------------------------------
