@@ -355,6 +355,74 @@ __global__ __launch_bounds__(256) void split2_kernel(SplitOp o0, SplitOp o1, int
   }
 }
 
+// The planes and inverse row scales of split2_kernel, for a row-major operand (!trans),
+// in one pass over it (rowmax_kernel and split2_kernel read the operand twice): one wave
+// per row, the row in registers (lane l holds k = 4 (l + 64 q) .. + 3 for q < NV, so each
+// load instruction reads 1 KB of the row), its maximum by a wave reduction, then both
+// planes.  The same elements, maxima and conversions as the pair, so the same bits.  No
+// LDS, so the workgroups share CUs with whatever else runs.  Grid (1, groups of 4 rows of
+// o0 then of o1, batch); X and ldx allow 16-byte loads (the host checks).
+constexpr int SR_NV_MAX = 28;  // rank up to 7168 (28 x 256)
+
+template <int NV>
+__global__ __launch_bounds__(256) void split_rows_kernel(SplitOp o0, SplitOp o1, int y0) {
+  int64_t by;
+  const SplitOp o = split_operand(o0, o1, y0, by);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t R = o.R, r = by * 4 + wave;
+  if (r >= R) return;
+  const float* __restrict__ X = o.X + (int64_t)blockIdx.z * o.sx;
+  uint16_t* __restrict__ out = o.out + (int64_t)blockIdx.z * o.sout;
+  const int64_t Kp = o.Kp;
+  const int mask = o.mask;
+  const __amdgpu_buffer_rsrc_t rs = mg_rsrc(X + r * o.ldx, o.Kk);  // k >= Kk reads zero
+  f32x4 v[NV];
+#pragma unroll
+  for (int q = 0; q < NV; ++q) v[q] = mg_load4(rs, (uint32_t)(16 * (lane + 64 * q)));
+  float m = 0.0f;  // fmaxf skips NaN elements
+  const int r32 = (int)r;  // rows and ranks stay below 2^31
+#pragma unroll
+  for (int q = 0; q < NV; ++q)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int k = 4 * lane + 256 * q + e;
+      const bool keep = mask == 1 ? k <= r32 : (mask == 2 ? k >= r32 : true);
+      v[q][e] = keep ? v[q][e] : 0.0f;
+      m = fmaxf(m, fabsf(v[q][e]));
+    }
+#pragma unroll
+  for (int sh = 32; sh >= 1; sh >>= 1) m = fmaxf(m, __shfl_xor(m, sh));
+  int ex = 0;  // the row scale as split2_kernel forms it
+  (void)frexpf(m, &ex);
+  const int e = m > 0.0f ? (ex - 1 < -100 ? -100 : (ex - 1 > 127 ? 127 : ex - 1)) : 0;
+  const float sc = ldexpf(1.0f, 14 - e);
+  if (lane == 0) reinterpret_cast<float*>(out + G3_NP * R * Kp)[r] = ldexpf(1.0f, e - 14);
+  const int64_t plane = R * Kp;
+#pragma unroll
+  for (int q = 0; q < NV; ++q) {
+    const int k0 = 4 * lane + 256 * q;
+    if (k0 >= Kp) continue;
+    uint32_t p1[2], p2[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      uint32_t w1 = 0, w2 = 0;
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        const float x = v[q][2 * h + t] * sc;
+        const _Float16 a = (_Float16)x;
+        const _Float16 b = (_Float16)(x - (float)a);
+        w1 |= (uint32_t)__builtin_bit_cast(unsigned short, a) << (16 * t);
+        w2 |= (uint32_t)__builtin_bit_cast(unsigned short, b) << (16 * t);
+      }
+      p1[h] = w1;
+      p2[h] = w2;
+    }
+    uint16_t* dst = out + ((int64_t)(k0 >> 4) * R + r) * 16 + (k0 & 15);
+    *reinterpret_cast<uint2*>(dst) = make_uint2(p1[0], p1[1]);
+    *reinterpret_cast<uint2*>(dst + plane) = make_uint2(p2[0], p2[1]);
+  }
+}
+
 // C[M, N] = alpha * A B^T + beta * C over k in [kbeg, kend) of each 128 x 128 output tile
 // (tri_krange), A and B given as split planes (16-k chunks).  Workgroup: 4 waves of
 // 64 x 64 (2 x 2 accumulators), two workgroups per CU (48 KB of LDS each), so each SIMD
@@ -815,6 +883,17 @@ __global__ __launch_bounds__(512, 1) void gemm3x_pair_kernel(G3Args g1, int64_t 
 // stride sout): the row maxima first, then the scaled split, each one launch for both
 // operands.  out holds 2 R Kp fp16 then (1 + G2_NS) R floats, within the 3 R Kp fp16 a
 // plane buffer holds (Kp >= 34).
+// One-pass splits of row-major operands (split_rows_kernel); HI2X_CHOL_SPLIT_ROWS=0 keeps
+// the rowmax_kernel + split2_kernel pair for every operand (read once per process; the
+// two give the same planes, which the tests compare).
+static bool chol_split_rows() {
+  static const bool on = [] {
+    const char* e = getenv("HI2X_CHOL_SPLIT_ROWS");
+    return !(e && *e && strcmp(e, "0") == 0);
+  }();
+  return on;
+}
+
 int split2(const SplitOp& a, const SplitOp* b, hipStream_t s, int batch = 1) {
   const SplitOp none{a.X, a.ldx, 0, a.Kk, a.Kp, a.sx, a.sout, a.trans, a.mask, a.out};
   const SplitOp& o1 = b ? *b : none;
@@ -830,6 +909,34 @@ int split2(const SplitOp& a, const SplitOp* b, hipStream_t s, int batch = 1) {
     return o.R <= 0 || ((reinterpret_cast<uintptr_t>(o.X) & 15) == 0 && o.ldx % 4 == 0 &&
                         o.sx % 4 == 0);
   };
+  // a row-major operand of rank up to SR_NV_MAX x 256 in one pass
+  auto one_pass = [&](const SplitOp& o) {
+    return chol_split_rows() && o.R > 0 && !o.trans && vec(o) && o.Kp <= 256 * SR_NV_MAX;
+  };
+  if (one_pass(a)) {
+    const bool both = o1.R > 0 && one_pass(o1);  // then one launch (they share Kp)
+    const unsigned ya = (unsigned)((a.R + 3) / 4), yb = both ? (unsigned)((o1.R + 3) / 4) : 0;
+    const dim3 grid(1, ya + yb, (unsigned)batch);
+    const SplitOp& ob = both ? o1 : none;
+    const int nv = (int)((a.Kp + 255) / 256);
+    if (nv <= 4)
+      hipLaunchKernelGGL(split_rows_kernel<4>, grid, dim3(256), 0, s, a, ob, (int)ya);
+    else if (nv <= 8)
+      hipLaunchKernelGGL(split_rows_kernel<8>, grid, dim3(256), 0, s, a, ob, (int)ya);
+    else if (nv <= 12)
+      hipLaunchKernelGGL(split_rows_kernel<12>, grid, dim3(256), 0, s, a, ob, (int)ya);
+    else if (nv <= 16)
+      hipLaunchKernelGGL(split_rows_kernel<16>, grid, dim3(256), 0, s, a, ob, (int)ya);
+    else if (nv <= 20)
+      hipLaunchKernelGGL(split_rows_kernel<20>, grid, dim3(256), 0, s, a, ob, (int)ya);
+    else if (nv <= 24)
+      hipLaunchKernelGGL(split_rows_kernel<24>, grid, dim3(256), 0, s, a, ob, (int)ya);
+    else
+      hipLaunchKernelGGL(split_rows_kernel<SR_NV_MAX>, grid, dim3(256), 0, s, a, ob, (int)ya);
+    const int rc = launch_status("split_rows_kernel");
+    if (rc || both || o1.R <= 0) return rc;
+    return split2(o1, nullptr, s, batch);  // the transposed operand: the pair
+  }
   const unsigned ga = groups(a), gb = o1.R > 0 ? groups(o1) : 0;
   if (ga + gb == 0) return HI2X_OK;
   {

@@ -886,6 +886,57 @@ def test_inverse_factor_256_tiles_equal_128_tiles(dev, monkeypatch):
     assert torch.equal(u256, u128)
 
 
+_SPLIT_CASES = r"""
+import hashlib
+import sys
+import torch
+sys.path.insert(0, sys.argv[1])
+from hi2_amd.hessian import inverse_factor, inverse_factors_batched
+
+
+def hessian(k, seed, batch=0):
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    x = torch.randn(max(batch, 1), 2 * k, k, device="cuda", generator=g)
+    x = x * torch.exp(0.5 * torch.randn(max(batch, 1), 1, k, device="cuda", generator=g))
+    hs = (torch.matmul(x.transpose(1, 2).contiguous(), x) / x.shape[1]).contiguous()
+    return hs if batch else hs[0]
+
+
+for k, seed, batch in ((8448, 21, 0), (6148, 22, 0), (4096, 23, 2)):
+    hs = hessian(k, seed, batch)
+    u = inverse_factors_batched(hs, 0.01) if batch else inverse_factor(hs, 0.01)
+    torch.cuda.synchronize()
+    print(k, batch, hashlib.sha256(u.cpu().numpy().tobytes()).hexdigest(), flush=True)
+"""
+
+
+def test_inverse_factor_one_pass_splits_equal_the_pair(tmp_path):
+    """The split-plane products' row-major operands go through split_rows_kernel (rb rows
+    per workgroup staged in LDS, maxima and planes in one pass), the transposed ones
+    through rowmax_kernel + split2_kernel; HI2X_CHOL_SPLIT_ROWS=0 (read once per process,
+    so in a child process each) sends every operand through the pair.  Same elements,
+    maxima and conversions: the factors are equal bit for bit.  K = 8448 (the top level's
+    operands 4 rows per workgroup, the next level's 8), K = 6148 (the top level's 2948-row
+    operands at 8 rows per workgroup: the last row block partial) and a batch of two
+    K = 4096 factors (8 rows per workgroup, two batch entries per launch)."""
+    import os
+    import subprocess
+    import sys
+
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    out = {}
+    for flag in ("1", "0"):
+        env = dict(os.environ, HI2X_CHOL_SPLIT_ROWS=flag)
+        print(f"factor digests, HI2X_CHOL_SPLIT_ROWS={flag}", flush=True)
+        r = subprocess.run([sys.executable, "-c", _SPLIT_CASES, root], env=env,
+                           capture_output=True, text=True, timeout=300)
+        assert r.returncode == 0, r.stderr[-2000:]
+        out[flag] = [line for line in r.stdout.splitlines() if line.strip()]
+        print("\n".join(out[flag]), flush=True)
+    assert len(out["1"]) == 3
+    assert out["1"] == out["0"]
+
+
 def test_inverse_factor_rejects_width_not_multiple_of_4(dev):
     """The factor's leaves move 16-byte vectors: a width that is not a multiple of 4 (no
     Hessian of the reference has one) is refused before any launch."""
