@@ -108,7 +108,11 @@ __global__ __launch_bounds__(256, 2) void refine_gradient_kernel(
 // (0 when no move is taken) goes to the row's other lanes by DPP row_newbcast, and the
 // row applies g[c] += dw * Hs[i][c] to the columns it holds (columns <= i are dead).
 // Gains are compared as torch's max over the stacked pair (+1, -1): a NaN propagates and
-// is never taken, and ties keep +1.  The owner's new code and dw stay in registers
+// is never taken, and ties keep +1.  A wave whose rows keep every gain finite over the
+// block (refine_bounded and the workgroup's test of the Hessian block) runs the loop with
+// the plain max of the pair and the off-ladder moves folded into their terms (gain
+// -inf), four operations fewer on each step's dependent chain; any other wave runs it
+// with the NaN-aware comparison.  The owner's new code and dw stay in registers
 // (pinned selects, no branch) and are written after the loop: the code in place, dw (or
 // -dw with NEG) to dw[r, i].  Moves are counted into *moved (when not null).
 // ---------------------------------------------------------------------------------
@@ -143,7 +147,7 @@ __device__ __forceinline__ void refine_prepare(RefRegs& R, float tp) {
   }
 }
 
-template <int I, bool FULL>
+template <int I, bool FULL, bool EXACT>
 __device__ __forceinline__ void refine_step(RefRegs& R, int L, int q, float tp,
                                             const float* __restrict__ shq, f32x4 (&hb)[2][2]) {
   constexpr int m = I / QL, s = I % QL, cur = I & 1;
@@ -154,11 +158,21 @@ __device__ __forceinline__ void refine_step(RefRegs& R, int L, int q, float tp,
   }
   // gain of a move: -(2 dw g_j + dw^2 Hs[j][j]) (the gradient-free terms prepared)
   const float gj = R.g[m], cj = R.cc[m];
-  const float gp = R.okp[m] ? -(R.ap[m] * gj + R.bp[m]) : -__builtin_inff();
-  const float gm = R.okm[m] ? -(R.am[m] * gj + R.bm[m]) : -__builtin_inff();
-  const bool pick_m = (gp == gp) & ((gm != gm) | (gm > gp));
-  const float best = pick_m ? gm : gp;
-  const bool take = best > 0.0f;  // false for NaN
+  bool pick_m, take;
+  if constexpr (EXACT) {
+    const float gp = R.okp[m] ? -(R.ap[m] * gj + R.bp[m]) : -__builtin_inff();
+    const float gm = R.okm[m] ? -(R.am[m] * gj + R.bm[m]) : -__builtin_inff();
+    pick_m = (gp == gp) & ((gm != gm) | (gm > gp));
+    const float best = pick_m ? gm : gp;
+    take = best > 0.0f;  // false for NaN
+  } else {
+    // every gain is finite, or -inf for a move off the ladder (its terms were set to 0
+    // and +inf), so torch's max of the pair is the plain one (ties keep +1)
+    const float gp = -(R.ap[m] * gj + R.bp[m]);
+    const float gm = -(R.am[m] * gj + R.bm[m]);
+    pick_m = gm > gp;
+    take = __builtin_fmaxf(gp, gm) > 0.0f;
+  }
   const float dw = take ? (pick_m ? R.dwm[m] : R.dwp[m]) : 0.0f;
   const float cn = take ? (pick_m ? cj + -1.0f : cj + 1.0f) : cj;
   const float db = row_bcast<s>(dw);
@@ -171,11 +185,25 @@ __device__ __forceinline__ void refine_step(RefRegs& R, int L, int q, float tp,
   for (int mm = (I + 1) / QL; mm < CPL; ++mm) R.g[mm] = R.g[mm] + db * hb[cur][mm >> 2][mm & 3];
 }
 
-template <bool FULL, int... Is>
+template <bool FULL, bool EXACT, int... Is>
 __device__ __forceinline__ void refine_steps(std::integer_sequence<int, Is...>, RefRegs& R,
                                              int L, int q, float tp,
                                              const float* __restrict__ shq, f32x4 (&hb)[2][2]) {
-  (refine_step<Is, FULL>(R, L, q, tp, shq, hb), ...);
+  (refine_step<Is, FULL, EXACT>(R, L, q, tp, shq, hb), ...);
+}
+
+// Whether this lane's columns keep every gain of the block finite: with |g| <= 2^60,
+// |dw| <= 2^30 for both moves and every element of the block's Hessian within 2^30 (the
+// workgroup's test), a step changes g by at most 2^60, so |g| stays below 2^68 over the
+// block's 128 steps, |2 dw g| below 2^99 and dw^2 Hs[j][j] below 2^90: no overflow, no
+// NaN.  NaN and infinities fail the comparisons.
+__device__ __forceinline__ bool refine_bounded(const RefRegs& R) {
+  bool ok = true;
+#pragma unroll
+  for (int m = 0; m < CPL; ++m)
+    ok = ok && __builtin_fabsf(R.g[m]) <= 0x1p60f && __builtin_fabsf(R.dwp[m]) <= 0x1p30f &&
+         __builtin_fabsf(R.dwm[m]) <= 0x1p30f;
+  return ok;
 }
 
 template <bool FULL, bool NEG>
@@ -197,6 +225,7 @@ __global__ __launch_bounds__(RPG * QL) void refine_block_kernel(
   const bool live = r < N;
   const int nrows = (int)(((rbase + RPG < N) ? rbase + RPG : N) - rbase);
 
+  bool hwide = false;  // an element of the Hessian block beyond 2^30 (or not finite)
   {
     // Hs[b0:b0+L, b0:b0+L]: rows >= L read zero, columns >= L are zeroed here
     const __amdgpu_buffer_rsrc_t hr = mg_rsrc(hs + b0 * K + b0, (int64_t)(L - 1) * K + L);
@@ -214,7 +243,9 @@ __global__ __launch_bounds__(RPG * QL) void refine_block_kernel(
 #pragma unroll
       for (int x = 0; x < 4; ++x) {
         const int cc = c + x;
-        sh[i * USTR + lane_off(cc % QL) + cc / QL] = (cc < L) ? hv[t][x] : 0.0f;
+        const float h = (cc < L) ? hv[t][x] : 0.0f;
+        sh[i * USTR + lane_off(cc % QL) + cc / QL] = h;
+        hwide = hwide || !(__builtin_fabsf(h) <= 0x1p30f);
       }
     }
   }
@@ -228,7 +259,7 @@ __global__ __launch_bounds__(RPG * QL) void refine_block_kernel(
     const __amdgpu_buffer_rsrc_t grs = mg_rsrc(g + rbase * ldg, (int64_t)(nrows - 1) * ldg + L);
     const __amdgpu_buffer_rsrc_t crs = __builtin_amdgcn_make_buffer_rsrc(
         codes + rbase * K + b0, (short)0, (int)((int64_t)(nrows - 1) * K + L), 0x00020000);
-    const int64_t B = live ? (block[r] > 0 ? block[r] : 1) : 1;
+    const int B = live ? (block[r] > 0 ? block[r] : 1) : 1;
     int bix[CPL];
 #pragma unroll
     for (int m = 0; m < CPL; ++m) {
@@ -237,8 +268,8 @@ __global__ __launch_bounds__(RPG * QL) void refine_block_kernel(
       const uint32_t co = c < L ? (uint32_t)((int64_t)lr * K + c) : MG_OOB;
       R.g[m] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(grs, (int)go, 0, 0));
       R.cc[m] = (float)__builtin_amdgcn_raw_buffer_load_b8(crs, (int)co, 0, 0);
-      int64_t b = (b0 + c) / B;
-      bix[m] = (int)(b < ldp ? b : ldp - 1);
+      const uint32_t b = (uint32_t)(b0 + c) / (uint32_t)B;  // columns stay below 2^31
+      bix[m] = (int)((int64_t)b < ldp ? (int64_t)b : ldp - 1);
     }
     const __amdgpu_buffer_rsrc_t lrs = mg_rsrc(lo + rbase * ldp, (int64_t)nrows * ldp);
     const __amdgpu_buffer_rsrc_t srs = mg_rsrc(st + rbase * ldp, (int64_t)nrows * ldp);
@@ -250,7 +281,7 @@ __global__ __launch_bounds__(RPG * QL) void refine_block_kernel(
       R.dw[m] = 0.0f;
     }
   }
-  __syncthreads();  // the Hessian block is in LDS
+  hwide = __syncthreads_or(hwide);  // the Hessian block is in LDS
 #pragma unroll
   for (int m = 0; m < CPL; ++m) R.hd[m] = sh[(QL * m + q) * USTR + lane_off(q) + m];
 
@@ -259,7 +290,19 @@ __global__ __launch_bounds__(RPG * QL) void refine_block_kernel(
   f32x4 hb[2][2];
   hb[0][0] = *reinterpret_cast<const f32x4*>(shq);
   hb[0][1] = *reinterpret_cast<const f32x4*>(shq + 4);
-  refine_steps<FULL>(std::make_integer_sequence<int, LMAX>{}, R, L, q, tp, shq, hb);
+  if (!hwide && __builtin_amdgcn_ballot_w64(!refine_bounded(R)) == 0) {
+    // a move off the ladder gets the terms 0 and +inf: its gain is -inf for finite g
+#pragma unroll
+    for (int m = 0; m < CPL; ++m) {
+      R.ap[m] = R.okp[m] ? R.ap[m] : 0.0f;
+      R.bp[m] = R.okp[m] ? R.bp[m] : __builtin_inff();
+      R.am[m] = R.okm[m] ? R.am[m] : 0.0f;
+      R.bm[m] = R.okm[m] ? R.bm[m] : __builtin_inff();
+    }
+    refine_steps<FULL, false>(std::make_integer_sequence<int, LMAX>{}, R, L, q, tp, shq, hb);
+  } else {
+    refine_steps<FULL, true>(std::make_integer_sequence<int, LMAX>{}, R, L, q, tp, shq, hb);
+  }
 
   if (live) {
 #pragma unroll

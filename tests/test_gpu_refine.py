@@ -203,3 +203,31 @@ def test_refine_at_configuration_widths_equals_the_oracle(k, n, passes, dev):
                                        hs_h, passes)
         assert moved.sum() > 0
         assert np.array_equal(N(c), want)
+
+
+@pytest.mark.parametrize("scaling", ["all_blocks", "one_block"])
+def test_refine_blocks_outside_the_bounds_take_the_nan_aware_loop(scaling, dev):
+    """The column loop runs the plain max of each move pair only when every gain of the
+    block stays finite (|g| <= 2^60, |dw| <= 2^30, the block's Hessian within 2^30);
+    otherwise the NaN-aware loop.  The Hessian scaled by 2^31 (every block outside) or
+    one 128-column block's rows and columns by 2^16 (its diagonal block by 2^32, the
+    others inside): codes equal the oracle's on the same inputs, bit for bit."""
+    from hi2_amd.format import decode_params
+    from hi2_amd.refine import refine_groups
+
+    k, n, passes = 960, 40, 2
+    w, enc, hs, lo, st = _gptq_rows(dev, n, k, 2048, 4, 64, seed=31)
+    if scaling == "all_blocks":
+        hs = hs * 2.0 ** 31
+    else:
+        sc = torch.ones(k, device=dev)
+        sc[128:256] = 2.0 ** 16
+        hs = sc[:, None] * hs * sc[None, :]
+    assert hs[128:256, 128:256].abs().max() > 2.0 ** 30
+    got = refine_groups([(w, enc, 4, 64)], hs, passes)[0]
+    lo, st = decode_params(enc.params[..., 0], enc.params[..., 1], enc.consts[:, 0:1],
+                           enc.consts[:, 1:2], enc.consts[:, 2:3])
+    want, moved, _ = oracle.refine(N(w), N(enc.codes), N(lo.float()), N(st.float()), 64, 15,
+                                   N(hs), passes)
+    assert moved.sum() > 0
+    assert np.array_equal(N(got), want)
