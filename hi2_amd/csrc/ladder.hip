@@ -460,39 +460,11 @@ __device__ __forceinline__ int64_t ceil_log2_dev(int64_t x) {
   return 64 - __builtin_clzll((unsigned long long)(x - 1));
 }
 
-// With groups (not null), row r of the batch belongs to group row_grp[r]: its
-// uncompensated row is row r - row0 of the group's w, its weights the group's d and its
-// ladder block the group's; rows past the group's own (padding) are skipped.
-__global__ __launch_bounds__(256) void sse_kernel(const uint8_t* __restrict__ codes,
-                                                  int64_t n, int64_t k, int64_t B,
-                                                  const float* __restrict__ lo_d,
-                                                  const float* __restrict__ st_d, int64_t ldd,
-                                                  const float* __restrict__ w,
-                                                  const float* __restrict__ d,
-                                                  float* __restrict__ sse,
-                                                  const int32_t* __restrict__ row_grp,
-                                                  const hi2x_rows_group* __restrict__ groups) {
-  const int lane = threadIdx.x & 63;
-  const int half = lane >> 5, hl = lane & 31;
-  const int kq = hl >> 3, v = hl & 7;
-  const int64_t r = ((int64_t)blockIdx.x * (blockDim.x / 64) + (threadIdx.x >> 6)) * 2 + half;
-  bool live = r < n;
-  const int64_t rr = live ? r : 0;
-  const float* wr = w + rr * k;
-  if (groups) {
-    const hi2x_rows_group& gp = groups[row_grp[rr]];
-    const int64_t lr = rr - gp.row0;
-    live = live && lr < gp.rows;
-    wr = gp.w + (live ? lr : 0) * k;
-    d = gp.d;
-    B = gp.block;
-  }
-  auto term = [&](int64_t c) -> float {
-    const int64_t b = c / B;
-    const float rec = f16_round(lo_d[rr * ldd + b] + (float)codes[rr * k + c] * st_d[rr * ldd + b]);
-    const float df = rec - wr[c];
-    return d[c] * (df * df);
-  };
+// The torch CPU order above for one row, term(c) giving element c's term: returns the
+// row's sum on lane hl == 0 of the half-wave (every lane of the wave takes part in the
+// shuffles).
+template <class F>
+__device__ __forceinline__ float sse_row_sum(int64_t k, int kq, int v, int base, F term) {
   const int64_t vec_size = k / 8;
   const int64_t size_ilp = vec_size / 4;
   float p = 0.0f;
@@ -525,7 +497,6 @@ __global__ __launch_bounds__(256) void sse_kernel(const uint8_t* __restrict__ co
   if (kq == 0)
     for (int64_t i = size_ilp * 4; i < vec_size; ++i) p += term(i * 8 + v);
   // fold the 4 accumulators of lane v: ((p0 + p1) + p2) + p3
-  const int base = half * 32;
   const float p1 = __shfl(p, base + 8 + v);
   const float p2 = __shfl(p, base + 16 + v);
   const float p3 = __shfl(p, base + 24 + v);
@@ -534,6 +505,55 @@ __global__ __launch_bounds__(256) void sse_kernel(const uint8_t* __restrict__ co
   for (int64_t i = vec_size * 8; i < k; ++i) out += term(i);
 #pragma unroll
   for (int vv = 0; vv < 8; ++vv) out += __shfl(p0, base + vv);
+  return out;
+}
+
+// With groups (not null), row r of the batch belongs to group row_grp[r]: its
+// uncompensated row is row r - row0 of the group's w, its weights the group's d and its
+// ladder block the group's; rows past the group's own (padding) are skipped.
+__global__ __launch_bounds__(256) void sse_kernel(const uint8_t* __restrict__ codes,
+                                                  int64_t n, int64_t k, int64_t B,
+                                                  const float* __restrict__ lo_d,
+                                                  const float* __restrict__ st_d, int64_t ldd,
+                                                  const float* __restrict__ w,
+                                                  const float* __restrict__ d,
+                                                  float* __restrict__ sse,
+                                                  const int32_t* __restrict__ row_grp,
+                                                  const hi2x_rows_group* __restrict__ groups) {
+  const int lane = threadIdx.x & 63;
+  const int half = lane >> 5, hl = lane & 31;
+  const int kq = hl >> 3, v = hl & 7;
+  const int64_t r = ((int64_t)blockIdx.x * (blockDim.x / 64) + (threadIdx.x >> 6)) * 2 + half;
+  bool live = r < n;
+  const int64_t rr = live ? r : 0;
+  const float* wr = w + rr * k;
+  if (groups) {
+    const hi2x_rows_group& gp = groups[row_grp[rr]];
+    const int64_t lr = rr - gp.row0;
+    live = live && lr < gp.rows;
+    wr = gp.w + (live ? lr : 0) * k;
+    d = gp.d;
+    B = gp.block;
+  }
+  auto row_sum = [&](auto blk) {
+    return sse_row_sum(k, kq, v, half * 32, [&](int64_t c) -> float {
+      const int64_t b = blk(c);
+      const float rec =
+          f16_round(lo_d[rr * ldd + b] + (float)codes[rr * k + c] * st_d[rr * ldd + b]);
+      const float df = rec - wr[c];
+      return d[c] * (df * df);
+    });
+  };
+  // the element's ladder block c / B (c < k): for k B < 2^32, floor(c M / 2^32) with
+  // M = ceil(2^32 / B) is floor(c / B) exactly (c M / 2^32 exceeds c / B by
+  // c (M B - 2^32) / (B 2^32) < c / 2^32 < 1 / B), one multiply-high; the 64-bit division
+  // otherwise (the wave decides together, so its loop has one form)
+  const uint32_t Bu = (uint32_t)B;
+  const bool by_mul = B >= 2 && B < (1ll << 32) && (uint64_t)k * Bu < (1ull << 32);
+  const uint32_t M = by_mul ? (uint32_t)(((1ull << 32) + Bu - 1) / Bu) : 0u;
+  const float out = __builtin_amdgcn_ballot_w64(!by_mul) == 0
+                        ? row_sum([&](int64_t c) { return (int64_t)__umulhi((uint32_t)c, M); })
+                        : row_sum([&](int64_t c) { return c / B; });
   if (live && hl == 0) sse[r] = out;
 }
 
