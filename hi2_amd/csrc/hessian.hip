@@ -583,17 +583,35 @@ __global__ __launch_bounds__(256) void syrk2_bf16_kernel(const uint16_t* __restr
     }
 }
 
-// S (upper triangle) += partial_0 + partial_1 + ... in split order.
+// S (upper triangle) += partial_0 + partial_1 + ... in split order.  Grid (row i, pieces of
+// the row): VEC (K a multiple of 4, 16-byte aligned buffers) gives each thread 4
+// consecutive columns, the elements below the diagonal written back as read; a piece
+// wholly below the diagonal returns at once.
+template <bool VEC>
 __global__ __launch_bounds__(256) void split_sum_kernel(float* __restrict__ s,
                                                         const float* __restrict__ parts,
                                                         int splits, int64_t K) {
-  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (idx >= K * K) return;
-  const int64_t i = idx / K, j = idx % K;
-  if (j < i) return;
-  float v = s[idx];
-  for (int p = 0; p < splits; ++p) v = v + parts[(int64_t)p * K * K + idx];
-  s[idx] = v;
+  const int64_t i = blockIdx.x;
+  constexpr int W = VEC ? 4 : 1;
+  const int64_t j = ((int64_t)blockIdx.y * 256 + threadIdx.x) * W;
+  if (j >= K || j + W - 1 < i) return;
+  const int64_t idx = i * K + j;
+  if constexpr (VEC) {
+    f32x4 v = *reinterpret_cast<const f32x4*>(s + idx);
+    const f32x4 v0 = v;
+    for (int p = 0; p < splits; ++p) {
+      const f32x4 q = *reinterpret_cast<const f32x4*>(parts + (int64_t)p * K * K + idx);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[e] = v[e] + q[e];
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[e] = j + e < i ? v0[e] : v[e];
+    *reinterpret_cast<f32x4*>(s + idx) = v;
+  } else {
+    float v = s[idx];
+    for (int p = 0; p < splits; ++p) v = v + parts[(int64_t)p * K * K + idx];
+    s[idx] = v;
+  }
 }
 
 // The tail tiles' partials (compact blocks, split s of tail tile t at parts + (t * splits
@@ -1118,8 +1136,14 @@ int launch_syrk(const void* x, int dtype, int64_t t, int64_t k, float* s, char* 
     }
   }
   if (!rc && parts && !p.super) {
-    hipLaunchKernelGGL(split_sum_kernel, dim3((unsigned)((k * k + 255) / 256)), dim3(256), 0, st,
-                       s, parts, p.splits, k);
+    const bool vec = k % 4 == 0 && (reinterpret_cast<uintptr_t>(s) & 15) == 0 &&
+                     (reinterpret_cast<uintptr_t>(parts) & 15) == 0;
+    const int64_t w = vec ? 4 : 1;
+    const dim3 grid((unsigned)k, (unsigned)((k + 256 * w - 1) / (256 * w)));
+    if (vec)
+      hipLaunchKernelGGL(split_sum_kernel<true>, grid, dim3(256), 0, st, s, parts, p.splits, k);
+    else
+      hipLaunchKernelGGL(split_sum_kernel<false>, grid, dim3(256), 0, st, s, parts, p.splits, k);
     rc = launch_status("split_sum_kernel");
   }
   if (!rc && mirror) rc = launch_mirror(s, k, st);
@@ -1307,14 +1331,16 @@ extern "C" int hi2x_sigma_transform_upper_batched(const float* s, int64_t s_stri
 // over the experts' sums, taken before any is changed), then for every expert with
 // mask[e]: S_e = S_e + fill[e] * tot (fill the fp32 value of (need - n_e) / n_total).
 // Upper triangle only (upper != 0) or every element.
+// Grid (row i, pieces of 256 columns): no index division per element, and a piece wholly
+// below the diagonal returns at once when only the upper triangle is blended.
 __global__ __launch_bounds__(256) void blend_kernel(float* __restrict__ s, int64_t sstride,
                                                     int G, int64_t K,
                                                     const float* __restrict__ fill,
                                                     const uint8_t* __restrict__ mask,
                                                     int upper) {
-  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (idx >= K * K) return;
-  if (upper && idx % K < idx / K) return;
+  const int64_t i = blockIdx.x, j = (int64_t)blockIdx.y * 256 + threadIdx.x;
+  if (j >= K || (upper && j < i)) return;
+  const int64_t idx = i * K + j;
   float tot = s[idx] + 0.0f;
   for (int e = 1; e < G; ++e) tot = tot + s[(int64_t)e * sstride + idx];
   for (int e = 0; e < G; ++e)
@@ -1330,7 +1356,7 @@ extern "C" int hi2x_hessian_blend(float* s, int64_t s_stride, int64_t n_groups, 
   clear_error();
   HI2X_REQUIRE(s && fill && mask && k > 0 && n_groups > 0 && s_stride >= k * k,
                "hessian_blend: bad arguments");
-  hipLaunchKernelGGL(blend_kernel, dim3((unsigned)((k * k + 255) / 256)), dim3(256), 0,
+  hipLaunchKernelGGL(blend_kernel, dim3((unsigned)k, (unsigned)((k + 255) / 256)), dim3(256), 0,
                      as_stream(stream), s, s_stride, (int)n_groups, k, fill, mask, upper_only);
   return launch_status("blend_kernel");
 }
