@@ -8,8 +8,9 @@
 // is needed, never L: 2K^3/3 flops.
 //
 // L^-1 is built recursively on P = J H J, in place in its lower triangle:
-//   leaf (n <= 128): one workgroup factors the block and inverts the factor in
-//     registers (fused right-looking sweeps, one barrier per column);
+//   leaf (n <= 128): one workgroup runs the same recursion on the block in LDS down to
+//     16 x 16 bases, each one wave's fused factor-and-invert sweep in registers; a node
+//     of up to 256 columns (two leaves and its four products) is one workgroup too;
 //   node [A11 0; A21 A22], n1 + n2 = n, after inv_chol(A11) left A11 = L11^-1:
 //     T1  = A21 A11^T               (= L21)
 //     A22 = A22 - T1 T1^T           (lower triangle)
