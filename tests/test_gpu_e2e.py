@@ -12,7 +12,7 @@ inverse_factor, fwht_groups, GPTQ and encode_many; inputs tests/e2e_recipes.py):
   packing): Sigma within 1e-5, U within 1e-3 of the reference's (LAPACK) factor, every
   row that departs from the reference doing so at a ladder tie (the two fits' weighted
   errors equal to 1e-5) or a rounding tie (the two runs' pre-rounding quotients within
-  0.02 steps), codes equal on >= 99.9 % of entries where the Hessian has full rank, and
+  1e-3 steps), codes equal on >= 99.9 % of entries where the Hessian has full rank, and
   the total reconstruction error (sum of the rows' sse) within the stated bound of the
   reference's.
 
