@@ -57,11 +57,15 @@ __device__ __forceinline__ float at(const float4& v, int i) {
 
 // out[rows[r], :] = fp16(lo + q * step) (the sum in f64), for the group's
 // rows r; v = latent (times unit when given).
+// The block's divisions by safe (the fp32 divisions of the torch graph) as div_rcp
+// through one reciprocal per thread: bit-identical to IEEE division for every numerator.
+template <int SHIFT>
 __global__ __launch_bounds__(QT) void qad_decode_fwd_kernel(
     const float* __restrict__ latent, const float* __restrict__ unit,
     const float* __restrict__ lo_u, const float* __restrict__ st_u,
     const uint16_t* __restrict__ consts, const int64_t* __restrict__ rows, int64_t n_rows,
-    int64_t r_total, int64_t k, int shift, float nmax, float* __restrict__ out) {
+    int64_t r_total, int64_t k, float nmax, float* __restrict__ out) {
+  constexpr int shift = SHIFT;
   // thread (row, column quad); the host keeps n_rows * k / 4 below 2^31, so the index
   // arithmetic is 32-bit (a 64-bit division is a long emulated sequence on the SIMD)
   const uint32_t k4 = (uint32_t)(k >> 2);
@@ -75,6 +79,7 @@ __global__ __launch_bounds__(QT) void qad_decode_fwd_kernel(
   const Ladder l = block_ladder(lo_u[r * nblk + b], st_u[r * nblk + b], consts + r * 3);
   const bool zero = l.st == 0.0f;
   const float safe = zero ? 1.0f : l.st;
+  const float ys = 1.0f / safe;
   const int64_t off = row * k + c0;
   float4 v = ld4(latent + off);
   if (unit) {
@@ -84,7 +89,7 @@ __global__ __launch_bounds__(QT) void qad_decode_fwd_kernel(
   float4 o;
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
-    const float z = (at(v, e) - l.lo) / safe;
+    const float z = div_rcp(at(v, e) - l.lo, safe, ys);
     const float q = code_of(z, nmax, zero);
     // lo + q * step in f64 (exact), then torch's f64 -> fp16 conversion (through f32)
     const double val = (double)l.lo + (double)q * (double)l.st;
@@ -99,13 +104,38 @@ __global__ __launch_bounds__(QT) void qad_decode_fwd_kernel(
 //   d step_byte = step_scale * sum_block(G * q - [step != 0] gz * (z / safe)).
 // The block sums are the pairwise tree s[i] += s[i + h] for h = B/2 .. 1: the levels
 // h >= 4 are shuffles between the block's lanes, h = 2 and 1 inside the lane.
+// Lane j + D of this lane's row of 16 (DPP row_shl; past the row's end 0: such lanes'
+// sums are never read).  Written as update_dpp so that the add folds it in.
+template <int D>
+__device__ __forceinline__ float from_lane_plus(float v) {
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x100 + D, 0xf, 0xf, true));
+}
+
+// The tree levels h = H .. 4 of the block sums across the block's lanes (lane j += lane
+// j + h/4, within the block's aligned run of B/4 <= 16 lanes, one DPP row).
+template <int H>
+__device__ __forceinline__ void block_tree(float4& a_lo, float4& a_st) {
+  if constexpr (H >= 4) {
+    constexpr int D = H >> 2;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      at(a_lo, e) = at(a_lo, e) + from_lane_plus<D>(at(a_lo, e));
+      at(a_st, e) = at(a_st, e) + from_lane_plus<D>(at(a_st, e));
+    }
+    block_tree<H / 2>(a_lo, a_st);
+  }
+}
+
+template <int SHIFT>
 __global__ __launch_bounds__(QT) void qad_decode_bwd_kernel(
     const float* __restrict__ grad, const float* __restrict__ latent,
     const float* __restrict__ unit, const float* __restrict__ lo_u,
     const float* __restrict__ st_u, const uint16_t* __restrict__ consts,
-    const int64_t* __restrict__ rows, int64_t n_rows, int64_t r_total, int64_t k, int shift,
+    const int64_t* __restrict__ rows, int64_t n_rows, int64_t r_total, int64_t k,
     float nmax, float* __restrict__ g_latent, float* __restrict__ g_lo,
     float* __restrict__ g_st) {
+  constexpr int shift = SHIFT;
   const uint32_t k4 = (uint32_t)(k >> 2);
   const uint32_t i = blockIdx.x * QT + threadIdx.x;
   const bool valid = i < (uint32_t)n_rows * k4;
@@ -124,6 +154,7 @@ __global__ __launch_bounds__(QT) void qad_decode_bwd_kernel(
     const Ladder l = block_ladder(lo_u[r * nblk + b], st_u[r * nblk + b], consts + r * 3);
     const bool zero = l.st == 0.0f;
     const float safe = zero ? 1.0f : l.st;
+    const float ys = 1.0f / safe;
     const int64_t off = row * k + c0;
     float4 v = ld4(latent + off);
     float4 u = make_float4(1.f, 1.f, 1.f, 1.f);
@@ -135,31 +166,24 @@ __global__ __launch_bounds__(QT) void qad_decode_bwd_kernel(
     float4 gl;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      const float z = (at(v, e) - l.lo) / safe;
+      const float z = div_rcp(at(v, e) - l.lo, safe, ys);
       const float q = code_of(z, nmax, zero);
       const float G = at(g, e);
       const bool inside = z >= 0.0f && z <= nmax;
       const float gz = inside ? G * l.st : 0.0f;
-      const float gv = gz / safe;
+      const float gv = div_rcp(gz, safe, ys);
       at(gl, e) = unit ? gv * at(u, e) : gv;
       at(a_lo, e) = G - gv;
       float s = G * q;
-      if (!zero) s = s + (-gz) * (z / safe);
+      if (!zero) s = s + (-gz) * div_rcp(z, safe, ys);
       at(a_st, e) = s;
     }
     st4(g_latent + off, gl);
   }
   // tree levels h = B/2 .. 4 across the block's lanes (lane j += lane j + h/4); the
   // lanes that are not read again compute values nobody uses
-  const int block = 1 << shift;
-  for (int h = block >> 1; h >= 4; h >>= 1) {
-    const int d = h >> 2;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      at(a_lo, e) = at(a_lo, e) + __shfl_down(at(a_lo, e), d);
-      at(a_st, e) = at(a_st, e) + __shfl_down(at(a_st, e), d);
-    }
-  }
+  constexpr int block = 1 << shift;
+  block_tree<block / 2>(a_lo, a_st);
   if (valid && (c0 & (block - 1)) == 0) {
     const float slo = (a_lo.x + a_lo.z) + (a_lo.y + a_lo.w);
     const float sst = (a_st.x + a_st.z) + (a_st.y + a_st.w);
@@ -173,6 +197,21 @@ __global__ __launch_bounds__(QT) void qad_decode_bwd_kernel(
 // pre_div the division first: H16(x / scale).  H16 is the butterfly
 // y[t] = (t & h) ? y[t ^ h] - y[t] : y[t] + y[t ^ h] for h = 1, 2, 4, 8, then * 0.25.
 // h = 1, 2 act inside a lane's 4 columns, h = 4, 8 between the group's 4 lanes.
+// One cross-lane level of the butterfly: partner lane ^ M of the 4-lane group (CTRL its
+// DPP quad_perm), the upper lane keeping the difference.
+template <int M, int CTRL>
+__device__ __forceinline__ void butterfly_step(float4& v, int lane) {
+  const bool upper = (lane & M) != 0;
+  float4 p;
+#pragma unroll
+  for (int e = 0; e < 4; ++e)
+    at(p, e) = __builtin_bit_cast(
+        float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, at(v, e)), CTRL, 0xf, 0xf,
+                                           true));
+#pragma unroll
+  for (int e = 0; e < 4; ++e) at(v, e) = upper ? at(p, e) - at(v, e) : at(v, e) + at(p, e);
+}
+
 __global__ __launch_bounds__(QT) void qad_wht_scale_kernel(
     const float* __restrict__ x, int64_t n_rows, int64_t k, const uint8_t* __restrict__ flags,
     const uint16_t* __restrict__ scale, int pre_div, float* __restrict__ out) {
@@ -202,15 +241,8 @@ __global__ __launch_bounds__(QT) void qad_wht_scale_kernel(
   v.x = y.x + y.z; v.z = y.x - y.z; v.y = y.y + y.w; v.w = y.y - y.w;
   // h = 4, 8: partner lane j ^ 1, j ^ 2 of the group (lanes 4-aligned in the wave)
   const int lane = threadIdx.x & 63;
-#pragma unroll
-  for (int m = 1; m <= 2; m <<= 1) {
-    const bool upper = (lane & m) != 0;
-    float4 p;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) at(p, e) = __shfl_xor(at(v, e), m);
-#pragma unroll
-    for (int e = 0; e < 4; ++e) at(v, e) = upper ? at(p, e) - at(v, e) : at(v, e) + at(p, e);
-  }
+  butterfly_step<1, 0xB1>(v, lane);  // DPP quad_perm [1,0,3,2]: lane ^ 1
+  butterfly_step<2, 0x4E>(v, lane);  // [2,3,0,1]: lane ^ 2
   if (!valid) return;
   const bool flagged = flags[c0 >> 4] != 0;
   float4 o = flagged ? make_float4(v.x * 0.25f, v.y * 0.25f, v.z * 0.25f, v.w * 0.25f) : orig;
@@ -243,9 +275,14 @@ extern "C" int hi2x_qad_decode_fwd(const float* latent, const float* unit, const
   if (n_rows == 0) return HI2X_OK;
   const int64_t total = n_rows * (k / 4);
   HI2X_REQUIRE(total < (int64_t(1) << 31), "qad_decode_fwd: %lld rows x K too large", (long long)n_rows);
-  hipLaunchKernelGGL(qad_decode_fwd_kernel, dim3((unsigned)((total + QT - 1) / QT)), dim3(QT), 0,
-                     as_stream(stream), latent, unit, lo_u, st_u, consts, rows, n_rows, r_total, k,
-                     shift, nmax, out);
+  const dim3 grid((unsigned)((total + QT - 1) / QT));
+#define HI2X_QAD_FWD(S)                                                                     \
+  hipLaunchKernelGGL(qad_decode_fwd_kernel<S>, grid, dim3(QT), 0, as_stream(stream), latent, \
+                     unit, lo_u, st_u, consts, rows, n_rows, r_total, k, nmax, out)
+  if (shift == 4) HI2X_QAD_FWD(4);
+  else if (shift == 5) HI2X_QAD_FWD(5);
+  else HI2X_QAD_FWD(6);
+#undef HI2X_QAD_FWD
   return launch_status("qad_decode_fwd_kernel");
 }
 
@@ -264,9 +301,15 @@ extern "C" int hi2x_qad_decode_bwd(const float* grad, const float* latent, const
   if (n_rows == 0) return HI2X_OK;
   const int64_t total = n_rows * (k / 4);
   HI2X_REQUIRE(total < (int64_t(1) << 31), "qad_decode_bwd: %lld rows x K too large", (long long)n_rows);
-  hipLaunchKernelGGL(qad_decode_bwd_kernel, dim3((unsigned)((total + QT - 1) / QT)), dim3(QT), 0,
-                     as_stream(stream), grad, latent, unit, lo_u, st_u, consts, rows, n_rows,
-                     r_total, k, shift, nmax, g_latent, g_lo, g_st);
+  const dim3 grid((unsigned)((total + QT - 1) / QT));
+#define HI2X_QAD_BWD(S)                                                                    \
+  hipLaunchKernelGGL(qad_decode_bwd_kernel<S>, grid, dim3(QT), 0, as_stream(stream), grad, \
+                     latent, unit, lo_u, st_u, consts, rows, n_rows, r_total, k, nmax,     \
+                     g_latent, g_lo, g_st)
+  if (shift == 4) HI2X_QAD_BWD(4);
+  else if (shift == 5) HI2X_QAD_BWD(5);
+  else HI2X_QAD_BWD(6);
+#undef HI2X_QAD_BWD
   return launch_status("qad_decode_bwd_kernel");
 }
 
