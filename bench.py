@@ -325,54 +325,14 @@ def _encode_block(xs, ws, masks, timer=None, lanes=None, keep=None, cfg=CFG3):
     return out
 
 
-def group_rows(n, alloc):
-    """Rows of each allocation group of an n-row linear (make_inputs' cut)."""
-    sizes, lo = [], 0
-    for gi, (frac, _, _) in enumerate(alloc):
-        hi = n if gi == len(alloc) - 1 else lo + int(round(frac * n))
-        sizes.append(hi - lo)
-        lo = hi
-    return sizes
-
-
-def step_fused_rows(cfg) -> int:
-    """``fused_rows`` of the step's column loops: 0 while encode_block marks its other
-    chains' streams background (the library then keeps every near update a separate
-    launch), else the library's ``hi2x_gptq_fused_rows()``."""
-    from hi2_amd import _lib
-
-    return 0 if BACKGROUND and len(cfg["order"]) > 1 else _lib.gptq_fused_rows()
-
-
-def trailing_flops(cfg, fused_rows=None) -> float:
-    """Algorithmic flops, on real rows (no padding), of the cross-block updates a step
-    launches as gptq_trailing_kernel.  Per batch of the column loop (the jobs of one input,
-    cut and batched as ``prepare_jobs_gptq`` does): for a batch of more than ``fused_rows``
-    rows (padding included: what ``hi2x_gptq_run`` receives) every update, the sum over
-    128-column blocks of 2 R 128 (K - i2); for a smaller batch the far updates only,
-    2 R (c_end - c_start) (K - c_end) per super-block [c_start, c_end), since its near
-    updates run inside gptq_super_kernel.  ``fused_rows`` defaults to the step's
-    (step_fused_rows)."""
-    from hi2_amd.hessian import BLOCK_COLUMNS as L, _super_blocks, batch_rows
-
-    if fused_rows is None:
-        fused_rows = step_fused_rows(cfg)
+def trailing_flops(cfg) -> float:
+    """Algorithmic flops of every cross-block update of a step: per linear,
+    sum over 128-column blocks of 2 N 128 (K - i2) on the real rows (no padding)."""
     total = 0.0
-    for inp in cfg["order"]:
-        shapes = [(g, k, 0) for _, n, k, i in cfg["linears"] if i == inp
-                  for g in group_rows(n, cfg["alloc"])]
-        for k, sizes, padded in batch_rows(shapes):
-            r = sum(sizes)
-            if padded > fused_rows:
-                for i1 in range(0, k, L):
-                    i2 = min(i1 + L, k)
-                    total += 2.0 * r * (i2 - i1) * (k - i2)
-                continue
-            nblk = -(-k // L)
-            sb = max(1, min(_super_blocks(k), nblk))
-            for b in range(0, nblk, sb):
-                c0, c1 = b * L, min((b + sb) * L, k)
-                total += 2.0 * r * (c1 - c0) * (k - c1)
+    for _, n, k, _ in cfg["linears"]:
+        for i1 in range(0, k, 128):
+            i2 = min(i1 + 128, k)
+            total += 2.0 * n * (i2 - i1) * (k - i2)
     return total
 
 
@@ -851,8 +811,8 @@ def kernel_stats(kind):
 
 def trailing_roofline(steps, basis):
     """The trailing update's roofline over the last timing window: the algorithmic flops
-    of the cross-block updates launched as gptq_trailing_kernel, on real rows
-    (trailing_flops), divided by the summed event-timed durations of its launches."""
+    of the block's cross-block updates on real rows (trailing_flops) divided by the summed
+    event-timed durations of its launches."""
     from hi2_amd import _lib
 
     n, ms, work = _lib.timing_query(DOMINANT)
@@ -862,11 +822,9 @@ def trailing_roofline(steps, basis):
             "unit": "TFLOP/s", "frac": rate / PEAK_F32, "traffic": None,
             "kernel": KERNELS[DOMINANT][0], "launches": n, "avg_ms": ms / n,
             "flops_per_launch": flops / n,
-            "work": "2*rows*rank*cols summed over the cross-block updates launched as this "
-                    "kernel, real rows only (the launches also run the zero rows that align "
-                    "row groups to 128): every update of a batch above "
-                    "hi2x_gptq_fused_rows() rows, the far updates only of a smaller one (its "
-                    "near updates run inside gptq_super_kernel)", "timing": basis}
+            "work": "2*rows*rank*cols summed over the block's cross-block updates, real rows "
+                    "only (the launches also run the zero rows that align row groups to "
+                    "128)", "timing": basis}
 
 
 def _cpu_info():

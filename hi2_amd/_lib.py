@@ -103,8 +103,6 @@ def _bind(lib):
                                       ctypes.POINTER(ctypes.c_double)]
     lib.hi2x_last_error.restype = ctypes.c_char_p
     lib.hi2x_last_error.argtypes = []
-    lib.hi2x_gptq_fused_rows.restype = ctypes.c_int64
-    lib.hi2x_gptq_fused_rows.argtypes = []
     for name, args in SIGNATURES.items():
         fn = getattr(lib, name)
         fn.restype = ctypes.c_int
@@ -167,13 +165,6 @@ def timing_query(kind: int) -> tuple[int, float, float]:
     check(lib().hi2x_timing_query(kind, ctypes.byref(n), ctypes.byref(ms), ctypes.byref(work)),
           "hi2x_timing_query")
     return n.value, ms.value, work.value
-
-
-def gptq_fused_rows() -> int:
-    """Largest batch (rows, padding included) whose super-blocks ``hi2x_gptq_run`` runs
-    as one fused launch each while no stream is marked background
-    (``hi2x_gptq_fused_rows``; 0 when switched off)."""
-    return int(lib().hi2x_gptq_fused_rows())
 
 
 def stream_background(st: torch.cuda.Stream, on: bool = True) -> None:

@@ -88,11 +88,6 @@ bool stream_background(hipStream_t s) {
   return false;
 }
 
-bool any_stream_background() {
-  std::lock_guard<std::mutex> lk(g_bg_mu);
-  return !g_bg.empty();
-}
-
 }  // namespace hi2x
 
 using namespace hi2x;

@@ -19,9 +19,6 @@ int launch_status(const char* what);
 // fewer of them share a CU and latency-bound kernels of other streams find room.
 bool stream_background(hipStream_t s);
 
-// Whether any stream is marked background: the caller runs concurrent chains of work.
-bool any_stream_background();
-
 inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 
 // The cross-block update of gptq.hip on `s`, for other kernels' schedules:

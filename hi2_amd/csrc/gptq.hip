@@ -5,8 +5,6 @@
 // rounding spec of hi2/gptq_kernel.py:82-100.
 #include <stdarg.h>
 #include <stdio.h>
-#include <stdlib.h>
-#include <string.h>
 
 #include <atomic>
 #include <mutex>
@@ -324,16 +322,15 @@ __device__ void gptq_rows_exact(RowRegs<COMP>& R, const float* __restrict__ wc, 
   store_row<COMP>(R, K, i1, L, r, q, err1, lde, codes, comp);
 }
 
-// The column loop of block [i1, i1 + L) for this workgroup's rows, every factor group among
-// them in turn (su: the workgroup's LDS block of U).  Reads wc, writes err1, codes, comp.
 template <bool FULL, bool COMP>
-__device__ __forceinline__ void block_rows(
-    float* su, const float* wc, int64_t N, int64_t K, int64_t i1, int L,
+__global__ __launch_bounds__(RPG * QL) void gptq_block_kernel(
+    const float* __restrict__ wc, int64_t N, int64_t K, int64_t i1, int L,
     float* __restrict__ err1, int64_t lde, uint8_t* __restrict__ codes,
     const float* __restrict__ lo, const float* __restrict__ st, int64_t ldp,
     const int32_t* __restrict__ row_grp, const int64_t* __restrict__ u_ptrs,
     const int32_t* __restrict__ blk, const float* __restrict__ nmax,
     float* __restrict__ comp) {
+  __shared__ float su[LMAX * USTR];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
@@ -400,133 +397,6 @@ __device__ __forceinline__ void block_rows(
       continue;
     }
     store_row<COMP>(R, K, i1, L, r, q, err1, lde, codes, comp);
-  }
-}
-
-template <bool FULL, bool COMP>
-__global__ __launch_bounds__(RPG * QL) void gptq_block_kernel(
-    const float* __restrict__ wc, int64_t N, int64_t K, int64_t i1, int L,
-    float* __restrict__ err1, int64_t lde, uint8_t* __restrict__ codes,
-    const float* __restrict__ lo, const float* __restrict__ st, int64_t ldp,
-    const int32_t* __restrict__ row_grp, const int64_t* __restrict__ u_ptrs,
-    const int32_t* __restrict__ blk, const float* __restrict__ nmax,
-    float* __restrict__ comp) {
-  __shared__ float su[LMAX * USTR];
-  block_rows<FULL, COMP>(su, wc, N, K, i1, L, err1, lde, codes, lo, st, ldp, row_grp, u_ptrs,
-                         blk, nmax, comp);
-}
-
-// ---------------------------------------------------------------------------------
-// The near update of a super-block for one workgroup's rows:
-//
-//   wc[r, c] -= sum_k err1[r, k] U_g[i1 + k, c]      c in [i1 + 128, c1), k = 0..127
-//
-// The workgroup's 16 rows are one MFMA tile row; the columns are 16-column tiles dealt to
-// the 4 waves.  v_mfma_f32_16x16x4_f32 evaluates its 4 k as the sequential fma chain in k
-// order (lane group l / 16 supplies k = 4s + l / 16 at step s), so its 32 steps from zero
-// are the sequential fp32 FMA chain over the block's 128 k, and the product is subtracted
-// once: the separate near update of gptq_trailing_kernel, bit for bit.  A (the errors) goes
-// through LDS into the lane order, lane l holding err1[l % 16][4s + l / 16] for s = 0..31;
-// B (U) comes from L2 straight into registers, lane l reading U[i1 + 4s + l / 16][c + l % 16],
-// the next tile's 32 values loaded while the current tile's MFMAs run.  Rows of another
-// factor group are zero in A and left unwritten (one pass per group of the rows).
-// se: RPG x 128 floats of LDS.
-__device__ __forceinline__ void near_rows(float* se, float* wc, int64_t N, int64_t K,
-                                          int64_t i1, const float* err1, int64_t lde,
-                                          int64_t c1, const int32_t* __restrict__ row_grp,
-                                          const int64_t* __restrict__ u_ptrs) {
-  constexpr int NS = LMAX / 4;  // MFMA steps of the block's rank
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int64_t rbase = (int64_t)blockIdx.x * RPG;
-  const int64_t rend = ((rbase + RPG < N) ? rbase + RPG : N) - 1;
-  const int nrows = (int)(rend - rbase + 1);
-  __syncthreads();  // err1 of every row of the workgroup is written
-  for (int idx = tid; idx < RPG * LMAX; idx += RPG * QL) {  // se[k % 4][row][k / 4]
-    const int row = idx / LMAX, k = idx % LMAX;
-    se[((k & 3) * RPG + row) * NS + (k >> 2)] =
-        row < nrows ? err1[(rbase + row) * lde + k] : 0.0f;
-  }
-  __syncthreads();
-  const int ar = lane & 15, ak = lane >> 4;  // this lane's A row (B column) and k group
-  const int g0 = row_grp[rbase], g1 = row_grp[rend];
-  const int64_t cb = i1 + LMAX;
-  const int ntile = (int)((c1 - cb) / 16);
-  for (int g = g0; g <= g1; ++g) {
-    const bool mine_a = ar < nrows && row_grp[rbase + ar] == g;
-    f32x4 ag[NS / 4];
-#pragma unroll
-    for (int v = 0; v < NS / 4; ++v) {
-      const f32x4 x = *reinterpret_cast<const f32x4*>(&se[(ak * RPG + ar) * NS + 4 * v]);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) ag[v][e] = mine_a ? x[e] : 0.0f;
-    }
-    bool mine_o[4];  // output rows 4 ak + j of this lane
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int rr = 4 * ak + j;
-      mine_o[j] = rr < nrows && row_grp[rbase + rr] == g;
-    }
-    const float* U = reinterpret_cast<const float*>(u_ptrs[g]);
-    const __amdgpu_buffer_rsrc_t ur = mg_rsrc(U + i1 * K, (int64_t)(LMAX - 1) * K + c1);
-    // U rows 4 st + ak: one per-lane offset, the step's 4 rows a uniform offset (the
-    // buffer's scalar offset); the resource spans 128 rows, so everything is below 2^31
-    const uint32_t ustep = (uint32_t)(16 * K);
-    auto load_b = [&](int t, float (&b)[NS]) {
-      const uint32_t vo = (uint32_t)(((int64_t)ak * K + cb + 16 * (int64_t)t + ar) * 4);
-#pragma unroll
-      for (int st = 0; st < NS; ++st)
-        b[st] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
-                                              ur, (int)vo, (int)(st * ustep), 0));
-    };
-    auto tile = [&](int t, const float (&b)[NS]) {
-      f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-      for (int st = 0; st < NS; ++st)
-        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(ag[st >> 2][st & 3], b[st], acc, 0, 0, 0);
-      const int64_t c = cb + 16 * (int64_t)t + ar;
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-        if (mine_o[j]) {
-          float* p = wc + (rbase + 4 * ak + j) * K + c;
-          *p = *p - acc[j];
-        }
-    };
-    // tiles wave, wave + 4, ... in pairs, so both buffers are named registers
-    float b0[NS], b1[NS];
-    int t = wave;
-    if (t < ntile) load_b(t, b0);
-    while (t < ntile) {
-      if (t + WPG < ntile) load_b(t + WPG, b1);
-      tile(t, b0);
-      t += WPG;
-      if (t >= ntile) break;
-      if (t + WPG < ntile) load_b(t + WPG, b0);
-      tile(t, b1);
-      t += WPG;
-    }
-  }
-  __syncthreads();  // written before the next block's loads of these rows
-}
-
-// A super-block's nb full blocks for one workgroup's rows in one launch: per block the
-// column loop, then the near update of these rows over the super-block's later columns
-// [i1 + 128, c1).  Inside a super-block a row depends only on its own earlier blocks, so
-// no workgroup waits for another; the far update stays a launch of its own.
-template <bool COMP>
-__global__ __launch_bounds__(RPG * QL, 2) void gptq_super_kernel(
-    float* wc, int64_t N, int64_t K, int64_t b0, int nb, int64_t c1, float* __restrict__ err_ws,
-    int64_t lde, uint8_t* __restrict__ codes, const float* __restrict__ lo,
-    const float* __restrict__ st, int64_t ldp, const int32_t* __restrict__ row_grp,
-    const int64_t* __restrict__ u_ptrs, const int32_t* __restrict__ blk,
-    const float* __restrict__ nmax, float* __restrict__ comp) {
-  __shared__ float su[LMAX * USTR];
-  __shared__ float se[RPG * LMAX];
-  for (int t = 0; t < nb; ++t) {
-    const int64_t i1 = (b0 + t) * LMAX;
-    float* err1 = err_ws + (int64_t)t * LMAX;
-    block_rows<true, COMP>(su, wc, N, K, i1, LMAX, err1, lde, codes, lo, st, ldp, row_grp,
-                           u_ptrs, blk, nmax, comp);
-    if (i1 + LMAX < c1) near_rows(se, wc, N, K, i1, err1, lde, c1, row_grp, u_ptrs);
   }
 }
 
@@ -661,38 +531,6 @@ int launch_block(const float* wc, int64_t n, int64_t k, int64_t i1, int64_t len,
   return launch_status("gptq_block_kernel");
 }
 
-// Batches of at most this many rows run each super-block's full blocks as one
-// gptq_super_kernel launch (column loops and near updates together); larger ones, whose
-// workgroups take several rounds of the chip, keep the near updates as GEMM launches, which
-// read each U tile once per 64 rows instead of once per 16.  The fused launch is taken only
-// while no stream is marked background: on an otherwise idle chip it measured 10.1 ms
-// against 11.3 ms for the column loop of 4096 x 14336, but beside other chains' products
-// (the marked streams) it lost 0.3 to 0.5 ms, its four times larger reads of U competing
-// with theirs for L2 and HBM.  HI2X_GPTQ_FUSED=0 (read at every call) keeps the separate
-// launches for every batch.
-constexpr int64_t kFusedRows = 8192;
-int64_t fused_rows() {
-  const char* e = getenv("HI2X_GPTQ_FUSED");
-  return (e && *e && strcmp(e, "0") == 0) ? 0 : kFusedRows;
-}
-
-int launch_super(float* wc, int64_t n, int64_t k, int64_t b0, int64_t nb, int64_t c1,
-                 float* err_ws, int64_t lde, uint8_t* codes, const float* lo, const float* st,
-                 int64_t ldp, const int32_t* row_grp, const int64_t* u_ptrs, const int32_t* blk,
-                 const float* nmax, float* comp, hipStream_t s) {
-  const dim3 grid((unsigned)((n + RPG - 1) / RPG));
-  LaunchTimer timer(HI2X_TIME_GPTQ_BLOCK, (double)n * LMAX * (LMAX - 1) * nb, s);
-  if (comp)
-    hipLaunchKernelGGL(gptq_super_kernel<true>, grid, dim3(RPG * QL), 0, s, wc, n, k, b0,
-                       (int)nb, c1, err_ws, lde, codes, lo, st, ldp, row_grp, u_ptrs, blk, nmax,
-                       comp);
-  else
-    hipLaunchKernelGGL(gptq_super_kernel<false>, grid, dim3(RPG * QL), 0, s, wc, n, k, b0,
-                       (int)nb, c1, err_ws, lde, codes, lo, st, ldp, row_grp, u_ptrs, blk, nmax,
-                       comp);
-  return launch_status("gptq_super_kernel");
-}
-
 int launch_trailing(float* wc, int64_t n, int64_t k, int64_t i1, int nblk, const float* err1,
                     int64_t lde, int64_t c0, int64_t c1, const int32_t* row_grp,
                     const int64_t* u_ptrs, hipStream_t s,
@@ -772,8 +610,6 @@ extern "C" int hi2x_gptq_trailing(float* wc, int64_t n, int64_t k, int64_t i1, i
                          as_stream(stream));
 }
 
-extern "C" int64_t hi2x_gptq_fused_rows(void) { return fused_rows(); }
-
 extern "C" int hi2x_gptq_run(float* wc, int64_t n, int64_t k, uint8_t* codes, const float* lo,
                              const float* st, int64_t ldp, const int32_t* row_grp,
                              const int64_t* u_ptrs, const int32_t* blk, const float* nmax,
@@ -789,21 +625,10 @@ extern "C" int hi2x_gptq_run(float* wc, int64_t n, int64_t k, uint8_t* codes, co
   hipStream_t s = as_stream(stream);
   const int64_t nblocks = (k + LMAX - 1) / LMAX;
   const int64_t lde = super_blocks * LMAX;
-  const bool fused = n <= fused_rows() && !any_stream_background();
   for (int64_t sb = 0; sb < nblocks; sb += super_blocks) {
     const int64_t sb_end = (sb + super_blocks < nblocks) ? sb + super_blocks : nblocks;
     const int64_t cs_end = (sb_end * LMAX < k) ? sb_end * LMAX : k;
-    int64_t b = sb;
-    if (fused) {  // the super-block's full blocks in one launch (a short last block apart)
-      const int64_t nfull = (sb_end * LMAX <= k) ? sb_end - sb : sb_end - 1 - sb;
-      if (nfull > 0) {
-        const int rc = launch_super(wc, n, k, sb, nfull, cs_end, err_ws, lde, codes, lo, st,
-                                    ldp, row_grp, u_ptrs, blk, nmax, comp, s);
-        if (rc) return rc;
-        b = sb + nfull;
-      }
-    }
-    for (; b < sb_end; ++b) {
+    for (int64_t b = sb; b < sb_end; ++b) {
       const int64_t i1 = b * LMAX;
       const int64_t len = (k - i1 < LMAX) ? k - i1 : LMAX;
       float* eb = err_ws + (b - sb) * LMAX;

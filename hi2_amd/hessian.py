@@ -523,41 +523,6 @@ def _finish_grouped(units: list[_Unit], jobs: list, total: int, k: int, row_grp:
         off += pn
 
 
-def _plan(shapes: list[tuple]) -> tuple[list[tuple], dict[tuple, list[list[int]]]]:
-    """The chunks of jobs of the given (rows, K, device) and their batches: each job is cut
-    into chunks of ``ROW_ELEMS // K`` rows (``hi2/hessian.py:111-116``), and consecutive
-    chunks with the same (device, K) share a batch up to ``BATCH_ELEMS`` weights
-    (``hi2/hessian.py:376-387``).  Returns
-    the chunks (job, row offset, rows, step_rows) and, per (device, K), the batches as
-    lists of chunk indices."""
-    specs = []
-    for ji, (n_rows, k, _) in enumerate(shapes):
-        step_rows = max(1, ROW_ELEMS // k)
-        for s in range(0, n_rows, step_rows):
-            specs.append((ji, s, min(step_rows, n_rows - s), step_rows))
-    plan: dict[tuple, list[list[int]]] = {}
-    for si, (ji, _s, n, _st) in enumerate(specs):
-        k = shapes[ji][1]
-        bl = plan.setdefault((shapes[ji][2], k), [[]])
-        if bl[-1] and (sum(specs[t][2] for t in bl[-1]) + n) * k > BATCH_ELEMS:
-            bl.append([])
-        bl[-1].append(si)
-    return specs, plan
-
-
-def batch_rows(shapes: list[tuple]) -> list[tuple[int, list[int], int]]:
-    """Per batch that jobs of the given (rows, K, device) form: (K, real rows of each of
-    its chunks, rows of its working buffer with the padding of ``_padded``), the row count
-    ``hi2x_gptq_run`` receives."""
-    specs, plan = _plan(shapes)
-    out = []
-    for (_, k), bl in plan.items():
-        for members in bl:
-            sizes = [specs[t][2] for t in members]
-            out.append((k, sizes, sum(_padded(sizes))))
-    return out
-
-
 def _padded(sizes: list[int]) -> list[int]:
     """Rows of each unit in a batch's working buffer: every unit of a multi-unit batch
     starts on a 128-row boundary, so that no workgroup or tile of the kernels holds rows
@@ -726,9 +691,23 @@ def prepare_jobs_gptq(jobs: list[GptqJob], effort: str = "normal",
     backend = backend or os.environ.get("HI2_GPTQ_BACKEND", "auto")
     for job in jobs:
         _lib.require_gpu(job.w)
-    # a batch of several chunks gets one working buffer that every chunk is copied into
+    # the chunks, then their batches (same K and device, up to BATCH_ELEMS weights); a
+    # batch of several chunks gets one working buffer that every chunk is copied into
     # (its padding rows zeroed), so that the rounding needs no gathering pass
-    specs, plan = _plan([(j.w.shape[0], j.w.shape[1], j.w.device) for j in jobs])
+    specs = []  # (job, row offset, rows, step_rows)
+    for ji, job in enumerate(jobs):
+        n_rows, k = job.w.shape
+        step_rows = max(1, ROW_ELEMS // k)
+        for s in range(0, n_rows, step_rows):
+            specs.append((ji, s, min(step_rows, n_rows - s), step_rows))
+    plan: dict[tuple, list[list[int]]] = {}
+    for si, (ji, _s, n, _st) in enumerate(specs):
+        w = jobs[ji].w
+        key = (w.device, w.shape[1])
+        bl = plan.setdefault(key, [[]])
+        if bl[-1] and sum(specs[t][2] for t in bl[-1]) * w.shape[1] + n * w.shape[1] > BATCH_ELEMS:
+            bl.append([])
+        bl[-1].append(si)
     units: list[_Unit | None] = [None] * len(specs)
     batches: dict[tuple, list] = {}
     for (dev, k), bl in plan.items():

@@ -78,19 +78,11 @@ int hi2x_gptq_trailing(float* wc, int64_t n, int64_t k, int64_t i1, int64_t len,
  * of `super_blocks` consecutive blocks applied to the far columns in one pass
  * (each block's product still subtracted separately, in block order, so the result
  * is bit-identical to the per-block schedule).  wc is modified in place.
- * err_ws: device workspace of n * 128 * super_blocks floats.  While no stream is
- * marked background (hi2x_stream_background), batches of at most
- * hi2x_gptq_fused_rows() rows run each super-block's full blocks as one launch, every
- * workgroup applying the near updates of its own rows between its blocks (the same bits). */
+ * err_ws: device workspace of n * 128 * super_blocks floats. */
 int hi2x_gptq_run(float* wc, int64_t n, int64_t k, uint8_t* codes, const float* lo,
                   const float* st, int64_t ldp, const int32_t* row_grp,
                   const int64_t* u_ptrs, const int32_t* blk, const float* nmax,
                   float* comp, float* err_ws, int64_t super_blocks, void* stream);
-
-/* The largest batch (rows) whose near updates hi2x_gptq_run folds into its column-loop
- * launches while no stream is marked background, 0 when HI2X_GPTQ_FUSED=0 is set: no
- * counterpart in the reference; for measurement (which launches carry which flops). */
-int64_t hi2x_gptq_fused_rows(void);
 
 /* hi2x_gptq_run without allocation: no counterpart in the reference.  For callers that
  * cannot allocate device memory (code under HIP graph capture, tight serving loops,

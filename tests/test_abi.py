@@ -27,20 +27,8 @@ def test_library_exports_every_declared_symbol():
         assert hasattr(lib, name), name
     assert lib.hi2x_version() >= 100
     assert set(_lib.SIGNATURES) | set(_lib.SIZES) | {
-        "hi2x_version", "hi2x_last_error", "hi2x_timing_enable", "hi2x_timing_query",
-        "hi2x_gptq_fused_rows"
+        "hi2x_version", "hi2x_last_error", "hi2x_timing_enable", "hi2x_timing_query"
     } == set(names)
-
-
-def test_fused_rows_query_follows_the_environment(monkeypatch):
-    # read at every call; no HIP call
-    from hi2_amd import _lib
-
-    lib = _lib.lib()
-    monkeypatch.delenv("HI2X_GPTQ_FUSED", raising=False)
-    assert lib.hi2x_gptq_fused_rows() == 8192
-    monkeypatch.setenv("HI2X_GPTQ_FUSED", "0")
-    assert lib.hi2x_gptq_fused_rows() == 0
 
 
 def test_raw_symbols_resolve_without_ctypes_wrappers():

@@ -151,54 +151,6 @@ def test_super_block_schedule_is_bit_identical(dev, sb):
         assert torch.equal(getattr(got, f), getattr(ref, f)), f
 
 
-@pytest.mark.parametrize("k,sb", [(1024, 8), (1088, 4), (1088, 1), (4096, 8)])
-def test_fused_super_blocks_equal_separate_launches(dev, monkeypatch, k, sb):
-    """Batches of at most hi2x_gptq_fused_rows() rows run each super-block's full blocks as
-    one launch (every workgroup's column loops with the near updates of its own rows in
-    between, on v_mfma_f32_16x16x4f32); HI2X_GPTQ_FUSED=0 (read at every call) keeps the
-    separate column-loop and near-update launches, and so does any stream marked
-    background.  Three row groups with their own factors (one in act order; 37, 150 and 70
-    rows, so workgroups straddle groups), K with a short last block (1088: 64 columns),
-    super-blocks of 1, 4 and 8 blocks: the same codes, params, consts, sse and comp; the
-    fused call launches fewer separate near updates (none with one block per super-block)."""
-    from hi2_amd import _lib
-    from hi2_amd.hessian import GptqJob, encode_jobs_gptq
-
-    assert _lib.lib().hi2x_gptq_fused_rows() >= 8192
-    jobs = []
-    for seed, (rows, nbits, block, ao) in enumerate(((37, 2, 32, False), (150, 4, 64, True),
-                                                     (70, 8, 64, False))):
-        w, d, u, perm, _ = _layer(rows, k, 40 + seed + k, act_order=ao)
-        jobs.append(GptqJob(T(w, dev), T(d, dev), T(u, dev), nbits, block,
-                            None if perm is None else T(perm, dev)))
-
-    def run():
-        _lib.timing_enable([_lib.TIME_GPTQ_TRAILING])
-        try:
-            out = encode_jobs_gptq(jobs, "normal", comp=True, super_blocks=sb)
-            torch.cuda.synchronize()
-            return out, _lib.timing_query(_lib.TIME_GPTQ_TRAILING)[0]
-        finally:
-            _lib.timing_enable([])
-
-    fused, n_fused = run()
-    side = torch.cuda.Stream(device=dev)
-    _lib.stream_background(side, True)
-    try:
-        marked, n_marked = run()
-    finally:
-        _lib.stream_background(side, False)
-    monkeypatch.setenv("HI2X_GPTQ_FUSED", "0")
-    assert _lib.lib().hi2x_gptq_fused_rows() == 0
-    apart, n_apart = run()
-    assert n_marked == n_apart
-    assert n_fused < n_apart if sb > 1 else n_fused == n_apart
-    for a, b, c in zip(fused, apart, marked):
-        for f in ("codes", "params", "consts", "sse", "comp"):
-            assert torch.equal(getattr(a, f), getattr(b, f)), f
-            assert torch.equal(getattr(c, f), getattr(b, f)), f
-
-
 def test_background_stream_leaves_results_unchanged(dev):
     """hi2x_stream_background only changes how many of the cross-block update's
     workgroups share a CU: the same job on a background stream gives the same bits.
