@@ -188,17 +188,22 @@ template <bool COMP>
 __device__ __forceinline__ void load_row_a(RowRegs<COMP>& R, int (&bix)[CPL],
                                            const float* __restrict__ wc, int64_t K,
                                            int64_t i1, int L, int64_t rbase, int nrows, int lr,
-                                           const int32_t* __restrict__ blk, int q) {
-  // this row's columns c = 16m + q: the working copy and each column's ladder block
+                                           const int32_t* __restrict__ blk, int gspan, int gsel,
+                                           int q) {
+  // this row's columns c = 16m + q: the working copy and each column's ladder block, the
+  // latter from map gsel of the gspan + 1 block maps at blk (a run of groups sharing one
+  // factor, factor_run_end: gspan * K + L < 2^29, so the byte offsets fit in 32 bits)
   const __amdgpu_buffer_rsrc_t wrs = mg_rsrc(wc + rbase * K + i1, (int64_t)(nrows - 1) * K + L);
   const __amdgpu_buffer_rsrc_t brs = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<int32_t*>(blk + i1), (short)0, L * 4, 0x00020000);
+      const_cast<int32_t*>(blk + i1), (short)0, (int)(((int64_t)gspan * K + L) * 4), 0x00020000);
+  const uint32_t boff = (uint32_t)gsel * (uint32_t)K;
 #pragma unroll
   for (int m = 0; m < CPL; ++m) {
     const int c = QL * m + q;
     const uint32_t wo = c < L ? (uint32_t)(((int64_t)lr * K + c) * 4) : MG_OOB;
     R.w[m] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(wrs, (int)wo, 0, 0));
-    bix[m] = (int)__builtin_amdgcn_raw_buffer_load_b32(brs, (int)(c < L ? c * 4 : MG_OOB), 0, 0);
+    bix[m] = (int)__builtin_amdgcn_raw_buffer_load_b32(
+        brs, (int)(c < L ? (boff + (uint32_t)c) * 4u : MG_OOB), 0, 0);
   }
 }
 template <bool COMP>
@@ -243,11 +248,11 @@ template <bool COMP>
 __device__ __forceinline__ void load_row(RowRegs<COMP>& R, const float* __restrict__ wc,
                                          int64_t K, int64_t i1, int L, int64_t rbase,
                                          int nrows, int lr, const int32_t* __restrict__ blk,
-                                         const float* __restrict__ lo,
+                                         int gspan, int gsel, const float* __restrict__ lo,
                                          const float* __restrict__ st, int64_t ldp,
                                          const float* su, int q) {
   int bix[CPL];
-  load_row_a<COMP>(R, bix, wc, K, i1, L, rbase, nrows, lr, blk, q);
+  load_row_a<COMP>(R, bix, wc, K, i1, L, rbase, nrows, lr, blk, gspan, gsel, q);
   load_row_b<COMP>(R, bix, rbase, nrows, lr, lo, st, ldp);
   load_row_c<COMP>(R, L, su, q);
 }
@@ -311,17 +316,33 @@ __device__ __forceinline__ void exact_groups(std::integer_sequence<int, Ms...>,
 template <bool COMP>
 __device__ void gptq_rows_exact(RowRegs<COMP>& R, const float* __restrict__ wc, int64_t K,
                                 int64_t i1, int L, int64_t rbase, int nrows, int lr,
-                                int64_t r, const int32_t* __restrict__ blk,
+                                int64_t r, const int32_t* __restrict__ blk, int gspan, int gsel,
                                 const float* __restrict__ lo, const float* __restrict__ st,
                                 int64_t ldp, const float* su, int q, float nm,
                                 float* __restrict__ err1, int64_t lde,
                                 uint8_t* __restrict__ codes, float* __restrict__ comp) {
-  load_row<COMP>(R, wc, K, i1, L, rbase, nrows, lr, blk, lo, st, ldp, su, q);
+  load_row<COMP>(R, wc, K, i1, L, rbase, nrows, lr, blk, gspan, gsel, lo, st, ldp, su, q);
   exact_groups<COMP>(std::make_integer_sequence<int, CPL>{}, R, L, q, nm, su + lane_off(q),
                      (int)(threadIdx.x & 63));
   store_row<COMP>(R, K, i1, L, r, q, err1, lde, codes, comp);
 }
 
+// Last group of the run that starts at group g (groups up to g1): the following groups
+// whose factor is the same matrix (equal u_ptrs; the row classes of one input), at most
+// as many as keep (ge - g) * K + 128 < 2^29 for the block-map offsets of load_row_a.
+// Rows of one run share one pass of the column loop and one tile pass of the cross-block
+// update, so a batch needs no padding between them.
+__device__ __forceinline__ int factor_run_end(const int64_t* __restrict__ u_ptrs, int g, int g1,
+                                              int64_t K) {
+  const int64_t ug = u_ptrs[g];
+  int ge = g;
+  while (ge < g1 && u_ptrs[ge + 1] == ug && (int64_t)(ge + 1 - g) * K + LMAX < (1 << 29)) ++ge;
+  return ge;
+}
+
+// The column loop of block [i1, i1 + L) for this workgroup's rows, one run of groups
+// (factor_run_end) after the other, each row with its own group's block map and highest
+// code (su: the workgroup's LDS block of U).  Reads wc, writes err1, codes, comp.
 template <bool FULL, bool COMP>
 __global__ __launch_bounds__(RPG * QL) void gptq_block_kernel(
     const float* __restrict__ wc, int64_t N, int64_t K, int64_t i1, int L,
@@ -348,12 +369,16 @@ __global__ __launch_bounds__(RPG * QL) void gptq_block_kernel(
   // Global reads go through buffer resources that end at the last valid element, so
   // they need no branches (a branch around a load makes the compiler wait for each load
   // in turn): all loads of a phase are issued before the first is used.
-  for (int g = g0; g <= g1; ++g) {
+  for (int g = g0, ge = g0; g <= g1; g = ge + 1) {
+    ge = factor_run_end(u_ptrs, g, g1, K);
+    const bool mine = gr >= g && gr <= ge;  // uniform over the row's 16 lanes
+    const int gsel = mine ? gr - g : 0;
     // the row's working copy and ladder indices first, so that the dependent load of its
     // ladders runs while the U block is in flight
     RowRegs<COMP> R;
     int bix[CPL];
-    load_row_a<COMP>(R, bix, wc, K, i1, L, rbase, nrows, lr, blk + (int64_t)g * K, q);
+    load_row_a<COMP>(R, bix, wc, K, i1, L, rbase, nrows, lr, blk + (int64_t)g * K, ge - g, gsel,
+                     q);
     __syncthreads();  // LDS of the previous group is no longer read
     {
       // U[i1:i1+L, i1:i1+L]: rows >= L read zero, columns >= L are zeroed here
@@ -380,9 +405,9 @@ __global__ __launch_bounds__(RPG * QL) void gptq_block_kernel(
       }
     }
     __syncthreads();
-    if (gr != g) continue;  // uniform over the row's 16 lanes
+    if (!mine) continue;
 
-    const float nm = nmax[g];
+    const float nm = nmax[gr];
     load_row_c<COMP>(R, L, su, q);
     const float* suq = su + lane_off(q);
     float ub[2][CPL];
@@ -392,8 +417,8 @@ __global__ __launch_bounds__(RPG * QL) void gptq_block_kernel(
       // some row of this wave met an error quotient outside the iteration's exact range
       // (subnormal or negative-zero numerators, extreme magnitudes): the wave runs the
       // block again from the working copy with IEEE division
-      gptq_rows_exact<COMP>(R, wc, K, i1, L, rbase, nrows, lr, r, blk + (int64_t)g * K, lo,
-                            st, ldp, su, q, nm, err1, lde, codes, comp);
+      gptq_rows_exact<COMP>(R, wc, K, i1, L, rbase, nrows, lr, r, blk + (int64_t)g * K, ge - g,
+                            gsel, lo, st, ldp, su, q, nm, err1, lde, codes, comp);
       continue;
     }
     store_row<COMP>(R, K, i1, L, r, q, err1, lde, codes, comp);
@@ -446,11 +471,13 @@ __global__ __launch_bounds__(256, T == MG_T ? 2 : 4) void gptq_trailing_kernel(
   const int64_t my_row = r0 + tid / (256 / T);  // row this thread stages for the A operand
   const int my_grp = my_row < N ? row_grp[my_row] : -1;
   const CTile<T> ct(wc, K, N, c1, r0, cc0);
+  bool one = true;  // every group of the tile has the same factor (the row classes of one input)
+  for (int g = g0 + 1; g <= g1; ++g) one = one && u_ptrs[g] == u_ptrs[g0];
 
-  if (g0 == g1) {  // one factor for the whole tile: the blocks as one pipelined rank stream
+  if (one) {  // one factor for the whole tile: the blocks as one pipelined rank stream
     const float* U = reinterpret_cast<const float*>(u_ptrs[g0]);
     const int64_t R = (K - i1 < (int64_t)nblk * LMAX) ? K - i1 : (int64_t)nblk * LMAX;
-    RowsLoader<GroupMask, T> al{err1, lde, N, R, GroupMask{my_grp == g0}};
+    RowsLoader<GroupMask, T> al{err1, lde, N, R, GroupMask{my_grp >= 0}};
     ColsLoader<NoMask, T> bl{U + i1 * K, K, c1, R, NoMask{}};
     f32x16 acc[NA][NA], cv[NA][NA];
     mg_zero(acc);
@@ -473,14 +500,17 @@ __global__ __launch_bounds__(256, T == MG_T ? 2 : 4) void gptq_trailing_kernel(
     ct.store(cv, [](int, int, int) { return true; });
     return;
   }
-  for (int g = g0; g <= g1; ++g) {
+  // a tile shared by several factors: one masked pass per run of groups with one factor
+  for (int g = g0, ge = g0; g <= g1; g = ge + 1) {
+    for (ge = g; ge < g1 && u_ptrs[ge + 1] == u_ptrs[g];) ++ge;
     const float* U = reinterpret_cast<const float*>(u_ptrs[g]);
     for (int t = 0; t < nblk; ++t) {
       const int64_t ib = i1 + (int64_t)t * LMAX;
       const int64_t L = (K - ib < LMAX) ? K - ib : LMAX;
       f32x16 acc[NA][NA];
       mg_zero(acc);
-      RowsLoader<GroupMask, T> al{err1 + t * LMAX, lde, N, L, GroupMask{my_grp == g}};
+      RowsLoader<GroupMask, T> al{err1 + t * LMAX, lde, N, L,
+                                  GroupMask{my_grp >= g && my_grp <= ge}};
       ColsLoader<NoMask, T> bl{U + ib * K, K, c1, L, NoMask{}};
       mg_mainloop(acc, sm, al, bl, r0, cc0, 0, L);
       // wc tile -= this block's product (read-modify-write: the tile is not held in
@@ -493,19 +523,17 @@ __global__ __launch_bounds__(256, T == MG_T ? 2 : 4) void gptq_trailing_kernel(
         for (int b = 0; b < NA; ++b)
 #pragma unroll
           for (int j = 0; j < 16; ++j) cv[a][b][j] = cv[a][b][j] - acc[a][b][j];
-      if (g0 == g1) {
-        ct.store(cv, [](int, int, int) { return true; });
-      } else {  // a tile shared by two factors: bit a*16+j = row (a, j) is in group g
-        uint32_t in_g = 0;
+      // bit a*16+j: row (a, j) is in the run [g, ge]
+      uint32_t in_g = 0;
 #pragma unroll
-        for (int a = 0; a < NA; ++a)
+      for (int a = 0; a < NA; ++a)
 #pragma unroll
-          for (int j = 0; j < 16; ++j) {
-            const int64_t rr = r0 + mg_row<T>(a, j);
-            in_g |= (uint32_t)(rr < N && row_grp[rr] == g) << (a * 16 + j);
-          }
-        ct.store(cv, [&](int a, int j, int) { return (in_g >> (a * 16 + j)) & 1u; });
-      }
+        for (int j = 0; j < 16; ++j) {
+          const int64_t rr = r0 + mg_row<T>(a, j);
+          const int gg = rr < N ? row_grp[rr] : -1;
+          in_g |= (uint32_t)(gg >= g && gg <= ge) << (a * 16 + j);
+        }
+      ct.store(cv, [&](int a, int j, int) { return (in_g >> (a * 16 + j)) & 1u; });
     }
   }
 }

@@ -429,7 +429,7 @@ def _prepare_grouped(jobs: list, specs: list, members: list[int], effort: str,
     (in batch order), the buffer and (lo, st)."""
     order = sorted(members, key=lambda t: (jobs[specs[t][0]].block, jobs[specs[t][0]].nbits))
     sizes = [specs[t][2] for t in order]
-    padded = _padded(sizes)
+    padded = _padded(sizes, _factor_keys(jobs, [specs[t][0] for t in order]))
     total = sum(padded)
     offs = [0]
     for pn in padded:
@@ -501,7 +501,7 @@ def _finish_grouped(units: list[_Unit], jobs: list, total: int, k: int, row_grp:
     """Every unit's sse of a batch prepared by _prepare_grouped in one launch
     (``hi2x_finish_rows``); the units' rows are in batch order at 128-row boundaries."""
     sizes = [x.codes.shape[0] for x in units]
-    padded = _padded(sizes)
+    padded = _padded(sizes, _factor_keys(jobs, [x.job for x in units]))
     tab, off = [], 0
     for x, n, pn in zip(units, sizes, padded):
         job = jobs[x.job]
@@ -523,13 +523,30 @@ def _finish_grouped(units: list[_Unit], jobs: list, total: int, k: int, row_grp:
         off += pn
 
 
-def _padded(sizes: list[int]) -> list[int]:
-    """Rows of each unit in a batch's working buffer: every unit of a multi-unit batch
-    starts on a 128-row boundary, so that no workgroup or tile of the kernels holds rows
-    of two factors (it would run once per factor)."""
-    if len(sizes) > 1:
-        return [-(-n // BLOCK_COLUMNS) * BLOCK_COLUMNS for n in sizes]
-    return list(sizes)
+def _padded(sizes: list[int], keys: list | None = None) -> list[int]:
+    """Rows of each unit in a batch's working buffer.  In a multi-unit batch every run of
+    consecutive units with one factor (equal ``keys``, the identity of each unit's job's
+    ``u``; all different when None) starts on a 128-row boundary, so that no workgroup or
+    tile of the kernels holds rows of two factors (it would run once per factor); the
+    units inside a run follow each other without padding, since the kernels give a run's
+    rows one pass (the row classes of one input: down_proj's 1229 + 2867 rows fill 4096,
+    256 column-loop workgroups, instead of 4224)."""
+    if len(sizes) <= 1:
+        return list(sizes)
+    keys = list(range(len(sizes))) if keys is None else keys
+    out, off = [], 0
+    for i, n in enumerate(sizes):
+        end = off + n
+        if i + 1 < len(sizes) and keys[i + 1] != keys[i]:
+            end = -(-end // BLOCK_COLUMNS) * BLOCK_COLUMNS
+        out.append(end - off)
+        off = end
+    return out
+
+
+def _factor_keys(jobs: list, job_ids: list[int]) -> list[int]:
+    """The factor identity of each unit (by its job index) for :func:`_padded`."""
+    return [id(jobs[j].u) for j in job_ids]
 
 
 def _round_kernel(
@@ -546,7 +563,7 @@ def _round_kernel(
     sizes = [x.wc.shape[0] for x in units]
     # Padding rows have w = lo = step = 0: they round to code 0 with zero error and
     # change nothing.
-    padded = _padded(sizes)
+    padded = _padded(sizes, _factor_keys(jobs, [x.job for x in units]))
     total = sum(padded)
     if buf is not None:
         wc = buf
@@ -573,8 +590,15 @@ def _round_kernel(
     # the batch's small tables (row counts, factor addresses, highest codes, blocks) in
     # one copy that does not block the host (other streams keep being fed while this
     # batch waits for its inputs); the row -> group map is expanded on the device
-    uk = [jobs[x.job].u.to(dev, torch.float32).contiguous() for x in units]
-    for u in uk:
+    # one device copy per distinct factor, so that units sharing a factor pass one address
+    # (the kernels give such rows one pass)
+    u_of: dict[int, torch.Tensor] = {}
+    for x in units:
+        u = jobs[x.job].u
+        if id(u) not in u_of:
+            u_of[id(u)] = u.to(dev, torch.float32).contiguous()
+    uk = [u_of[id(jobs[x.job].u)] for x in units]
+    for u in u_of.values():
         if u.shape != (k, k):
             raise ValueError(f"factor has shape {tuple(u.shape)}, expected ({k}, {k})")
     ng = len(units)
@@ -721,7 +745,7 @@ def prepare_jobs_gptq(jobs: list[GptqJob], effort: str = "normal",
             buf = None
             if len(members) > 1:
                 sizes = [specs[t][2] for t in members]
-                padded = _padded(sizes)
+                padded = _padded(sizes, _factor_keys(jobs, [specs[t][0] for t in members]))
                 buf = torch.empty(sum(padded), k, dtype=torch.float32, device=dev)
             off = 0
             for j, t in enumerate(members):

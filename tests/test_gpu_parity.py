@@ -181,6 +181,86 @@ def test_background_stream_leaves_results_unchanged(dev):
         assert torch.equal(getattr(got, f), getattr(ref, f)), f
 
 
+def _shared_factor_batch(k, seed):
+    """Five row groups over two factors in the order A A B A A (A in storage order, B in
+    act order), 71 rows unpadded (sizes 5, 20, 9, 30, 7): workgroups of 16 rows and
+    64-row tiles straddle groups of one factor and of two."""
+    rng = np.random.default_rng(seed)
+    sizes = [5, 20, 9, 30, 7]
+    _, _, ua, _, _ = _layer(4, k, seed + 1)
+    _, _, ub, perm_b, _ = _layer(4, k, seed + 2, act_order=True)
+    which = [0, 0, 1, 0, 0]
+    us = [(ua, ub)[w] for w in which]
+    blks = [np.arange(k) // 32, np.arange(k) // 64, perm_b // 32, np.arange(k) // 16,
+            np.arange(k) // 64]
+    nmax = np.array([3, 15, 255, 15, 3], np.float32)
+    n = sum(sizes)
+    wc = (rng.standard_normal((n, k)) * 0.3).astype(np.float32)
+    ldp = k // 16
+    lo = (rng.standard_normal((n, ldp)) * 0.2 - 0.5).astype(np.float32)
+    st = (rng.random((n, ldp)) * 0.1 + 0.01).astype(np.float32)
+    row_grp = np.repeat(np.arange(5), sizes).astype(np.int32)
+    return sizes, which, (ua, ub), us, np.stack(blks).astype(np.int32), nmax, wc, lo, st, row_grp
+
+
+def test_groups_sharing_a_factor_share_passes(dev):
+    """Consecutive row groups whose factor is one matrix (one address in u_ptrs: the row
+    classes of one input) run as one pass of the column loop and of the cross-block tile
+    update, each row with its own group's block map and highest code; a group of another
+    factor in between splits the run.  hi2x_gptq_block against the oracle, and
+    hi2x_gptq_run over the whole unpadded batch (K = 448: a short last block, two-block
+    super-blocks) against one call per group, bit for bit."""
+    from hi2_amd import _lib, gptq_kernel
+
+    k, i1, length = 224, 128, 96
+    sizes, which, (ua, ub), us, blk, nm, wc, lo, st, row_grp = _shared_factor_batch(k, 30)
+    n = sum(sizes)
+    err_w, codes_w, comp_w = oracle.gptq_block(wc, i1, length, lo, st, row_grp, us, blk, nm)
+    uf = [T(ua, dev), T(ub, dev)]
+    u_ptrs = torch.tensor([uf[w].data_ptr() for w in which], dtype=torch.int64, device=dev)
+    err1 = torch.empty(n, length, dtype=torch.float32, device=dev)
+    codes = torch.zeros(n, k, dtype=torch.uint8, device=dev)
+    comp = torch.zeros(n, k, dtype=torch.float32, device=dev)
+    gptq_kernel.gptq_block(T(wc, dev), i1, length, err1, codes, T(lo, dev), T(st, dev),
+                           T(row_grp, dev), u_ptrs, T(blk, dev), T(nm, dev), comp)
+    assert np.array_equal(N(err1), err_w)
+    assert np.array_equal(N(codes), codes_w)
+    assert np.array_equal(N(comp), comp_w)
+
+    k, sb = 448, 2
+    sizes, which, (ua, ub), us, blk, nm, wc, lo, st, row_grp = _shared_factor_batch(k, 40)
+    n = sum(sizes)
+    uf = [T(ua, dev), T(ub, dev)]
+
+    def run(rows, grp, ptrs, blk_t, nm_t):
+        m = rows.shape[0]
+        # every device buffer is bound to a name until the launches have run (a temporary
+        # would be freed once its address is taken, and its block handed to the next one)
+        w, lo_t, st_t = T(wc[rows], dev), T(lo[rows], dev), T(st[rows], dev)
+        grp_t, blk_d, nm_d = T(grp, dev), T(blk_t, dev), T(nm_t, dev)
+        assert grp_t.shape == (m,) and int(grp_t.max()) < ptrs.numel() == blk_d.shape[0]
+        out = torch.zeros(m, k, dtype=torch.uint8, device=dev)
+        cmp = torch.zeros(m, k, dtype=torch.float32, device=dev)
+        ws = torch.empty(m, 128 * sb, dtype=torch.float32, device=dev)
+        _lib.call("hi2x_gptq_run", dev, _lib.ptr(w), m, k, _lib.ptr(out), _lib.ptr(lo_t),
+                  _lib.ptr(st_t), k // 16, _lib.ptr(grp_t), _lib.ptr(ptrs), _lib.ptr(blk_d),
+                  _lib.ptr(nm_d), _lib.ptr(cmp), _lib.ptr(ws), sb)
+        torch.cuda.synchronize()
+        return N(w), N(out), N(cmp)
+
+    ptrs = torch.tensor([uf[w].data_ptr() for w in which], dtype=torch.int64, device=dev)
+    whole = run(np.arange(n), row_grp, ptrs, blk, nm)
+    off = 0
+    for g, m in enumerate(sizes):
+        rows = np.arange(off, off + m)
+        one = run(rows, np.zeros(m, np.int32),
+                  torch.tensor([uf[which[g]].data_ptr()], dtype=torch.int64, device=dev),
+                  blk[g:g + 1], nm[g:g + 1])
+        for a, b in zip(whole, one):
+            assert np.array_equal(a[off:off + m], b), g
+        off += m
+
+
 def test_batched_jobs_match_one_call_each(dev, monkeypatch):
     # reference tests/test_gptq_fast.py:58-72: several row chunks and batches, two widths
     import hi2_amd.hessian as hm

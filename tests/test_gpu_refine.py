@@ -140,8 +140,9 @@ def test_refine_block_mirror_is_the_first_block_of_a_sweep(dev):
         blk = torch.full((n,), gg["block"], dtype=torch.int32, device=dev)
         e = torch.empty(n, k, device=dev)
         gr = torch.empty(n, k, device=dev)
+        ht = T(h, dev)  # held until the launch has run
         _lib.call("hi2x_refine_gradient", dev, _lib.ptr(w), _lib.ptr(codes), n, k, _lib.ptr(lo),
-                  _lib.ptr(st), lo.shape[1], _lib.ptr(blk), _lib.ptr(T(h, dev)), _lib.ptr(e),
+                  _lib.ptr(st), lo.shape[1], _lib.ptr(blk), _lib.ptr(ht), _lib.ptr(e),
                   _lib.ptr(gr))
         lo_x, st_x = _expand(lo, st, gg["block"])
         top = torch.full((n,), float(2 ** gg["nbits"] - 1), device=dev)
