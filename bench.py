@@ -809,21 +809,42 @@ def kernel_stats(kind):
     return out
 
 
+def pmc_traffic(kernel):
+    """HBM bytes per launch of ``kernel`` (read + write) from the committed counter
+    summary (profiles/traffic.json: rocprofv3 FETCH_SIZE and WRITE_SIZE passes over this
+    bench's step, each scaled by what the counter reads for a 1 GiB device copy), with the
+    split; None when the summary or the kernel is absent."""
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "traffic.json")
+    try:
+        with open(path) as f:
+            e = json.load(f).get(kernel)
+    except (OSError, ValueError):
+        return None, None
+    if not e:
+        return None, None
+    rd, wr = e["fetch_bytes_per_launch"], e["write_bytes_per_launch"]
+    return rd + wr, {"read_bytes": rd, "write_bytes": wr, "dispatches": e["dispatches"],
+                     "source": "profiles/traffic.json (rocprofv3 --pmc FETCH_SIZE, then "
+                               "WRITE_SIZE, averaged over the step's launches)"}
+
+
 def trailing_roofline(steps, basis):
     """The trailing update's roofline over the last timing window: the algorithmic flops
     of the block's cross-block updates on real rows (trailing_flops) divided by the summed
-    event-timed durations of its launches."""
+    event-timed durations of its launches; ``traffic`` from the committed PMC summary."""
     from hi2_amd import _lib
 
     n, ms, work = _lib.timing_query(DOMINANT)
     flops = trailing_flops(CFG3) * steps
     rate = flops / (ms / 1e3)
+    traffic, split = pmc_traffic(KERNELS[DOMINANT][0])
     return {"bound": "mfma", "achieved": rate / 1e12, "peak": PEAK_F32 / 1e12,
-            "unit": "TFLOP/s", "frac": rate / PEAK_F32, "traffic": None,
+            "unit": "TFLOP/s", "frac": rate / PEAK_F32, "traffic": traffic,
+            "traffic_split": split,
             "kernel": KERNELS[DOMINANT][0], "launches": n, "avg_ms": ms / n,
             "flops_per_launch": flops / n,
             "work": "2*rows*rank*cols summed over the block's cross-block updates, real rows "
-                    "only (the launches also run the zero rows that align row groups to "
+                    "only (the launches also run the zero rows that align factor runs to "
                     "128)", "timing": basis}
 
 
@@ -1077,14 +1098,20 @@ def micro(which, reps=3):
         return st.transformed(None, torch.ones(k // 16, dtype=torch.uint8, device=dev)), x
 
     def timed(fn, kinds):
+        """Wall milliseconds per call with no timing events (events around every launch
+        add gaps that fall hardest on many-launch schedules), then the kernels' event
+        statistics over the same number of calls in a second pass."""
         fn()
         torch.cuda.synchronize()
-        _lib.timing_enable(kinds)
         t0 = time.perf_counter()
         for _ in range(reps):
             fn()
         torch.cuda.synchronize()
         ms = (time.perf_counter() - t0) * 1e3 / reps
+        _lib.timing_enable(kinds)
+        for _ in range(reps):
+            fn()
+        torch.cuda.synchronize()
         stats = {}
         for kd in kinds:
             n, kms, work = _lib.timing_query(kd)

@@ -342,9 +342,12 @@ __device__ __forceinline__ int factor_run_end(const int64_t* __restrict__ u_ptrs
 
 // The column loop of block [i1, i1 + L) for this workgroup's rows, one run of groups
 // (factor_run_end) after the other, each row with its own group's block map and highest
-// code (su: the workgroup's LDS block of U).  Reads wc, writes err1, codes, comp.
+// code (su: the workgroup's LDS block of U).  Reads wc, writes err1, codes, comp.  Two
+// workgroups per CU: without the bound the per-row highest code took the full blocks'
+// variants to 256 VGPRs + AGPRs, one wave per SIMD, and the big batches' column loops
+// (gate/up, MoE experts) ran at half rate; with it they fit in 256 VGPRs, no scratch.
 template <bool FULL, bool COMP>
-__global__ __launch_bounds__(RPG * QL) void gptq_block_kernel(
+__global__ __launch_bounds__(RPG * QL, 2) void gptq_block_kernel(
     const float* __restrict__ wc, int64_t N, int64_t K, int64_t i1, int L,
     float* __restrict__ err1, int64_t lde, uint8_t* __restrict__ codes,
     const float* __restrict__ lo, const float* __restrict__ st, int64_t ldp,
