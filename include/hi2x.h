@@ -58,7 +58,10 @@ const char* hi2x_last_error(void);
  *   codes [n, k] u8 out (rounding-order positions i1..i1+len), lo/st [n, ldp] f32
  *   decoded block params, row_grp [n] i32 (sorted ascending), u_ptrs [G] i64 device
  *   addresses of contiguous [k, k] f32 factors, blk [G, k] i32 block of each column,
- *   nmax [G] f32 (codes - 1), comp [n, k] f32 out or NULL.
+ *   nmax [G] f32 (codes - 1), comp [n, k] f32 out or NULL.  Consecutive groups with
+ *   the same u_ptrs address form one run: their rows share one pass (each row with its
+ *   own group's blk and nmax), so they need no padding between them; a workgroup of 16
+ *   rows holding rows of two factors runs once per factor (same results, slower).
  * Bit-exact to the reference column loop (hi2/hessian.py:248-261). */
 int hi2x_gptq_block(const float* wc, int64_t n, int64_t k, int64_t i1, int64_t len,
                     float* err1, uint8_t* codes, const float* lo, const float* st,
@@ -68,7 +71,9 @@ int hi2x_gptq_block(const float* wc, int64_t n, int64_t k, int64_t i1, int64_t l
 /* Cross-block update of hi2/hessian.py:310-312 for every row r (group g):
  *   wc[r, c] -= err1[r, :len] @ U_g[i1:i1+len, c]   for c in [c0, c1)
  * err1 [n, lde] f32.  Each product is a sequential fp32 FMA chain over the rank in
- * order, then one subtraction: the rounding of the reference's BLAS call. */
+ * order, then one subtraction: the rounding of the reference's BLAS call.  A tile whose
+ * rows all have one factor address (any number of groups) is one pass; a tile of several
+ * factors runs one masked pass per run of equal addresses. */
 int hi2x_gptq_trailing(float* wc, int64_t n, int64_t k, int64_t i1, int64_t len,
                        const float* err1, int64_t lde, int64_t c0, int64_t c1,
                        const int32_t* row_grp, const int64_t* u_ptrs, void* stream);
