@@ -499,7 +499,7 @@ def _prepare_grouped(jobs: list, specs: list, members: list[int], effort: str,
 def _finish_grouped(units: list[_Unit], jobs: list, total: int, k: int, row_grp: torch.Tensor,
                     codes: torch.Tensor, tabs, dev: torch.device) -> None:
     """Every unit's sse of a batch prepared by _prepare_grouped in one launch
-    (``hi2x_finish_rows``); the units' rows are in batch order at 128-row boundaries."""
+    (``hi2x_finish_rows``); the units' rows are in batch order, laid out by ``_padded``."""
     sizes = [x.codes.shape[0] for x in units]
     padded = _padded(sizes, _factor_keys(jobs, [x.job for x in units]))
     tab, off = [], 0
