@@ -79,9 +79,9 @@ class _DeviceStager:
 def quiet_host():
     """Python's cyclic garbage collector off for a timed GPU loop (collected once before).
     The step is enqueued from Python with host synchronisations inside it, so a full
-    collection falling inside a step stalls the GPU: in one process, 40 consecutive steps
-    measured 35.9 ms at the median with single steps of 48.5 and 58.5 ms when the
-    collector ran, and at most 38.8 ms with it off."""
+    collection falling inside a step stalls the GPU: runs of 20-40 steps measured 35.9 ms
+    at the median, two of four processes with the collector on a single step of 48.5 or
+    58.5 ms, the two with it off none above 38.8 ms."""
     gc.collect()
     was = gc.isenabled()
     gc.disable()
