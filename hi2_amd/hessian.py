@@ -37,8 +37,14 @@ from .format import GROUP
 
 BLOCK_COLUMNS = 128  # lazy-update block of GPTQ
 ROW_ELEMS = 1 << 26  # rows per chunk are bounded so the working copies fit
-# chunks of several jobs batched through one kernel launch sequence (weights per batch)
-BATCH_ELEMS = int(os.environ.get("HI2_BATCH_ELEMS", 1 << 27))
+# chunks of several jobs batched through one kernel launch sequence (weights per batch).
+# 2^28 (a working copy of at most 1 GiB f32, so that every byte offset into a batch
+# buffer stays below 2^30) where the reference takes 2^27: batching never changes a
+# result, and bigger batches fill the chip in fewer sequential launch chains (the 70B
+# layer's down_proj, 8192 rows at K = 28672, in one batch of 512 column-loop workgroups
+# instead of two of 275 and 238: that layer 207.8-208.7 -> 202.4-203.5 ms; the 8B block
+# and the MoE layer unchanged).
+BATCH_ELEMS = int(os.environ.get("HI2_BATCH_ELEMS", 1 << 28))
 # 128-column blocks whose far-column updates share one pass over the working copy
 SUPER_BLOCKS = int(os.environ.get("HI2_SUPER_BLOCKS", 0))  # 0: by width (_super_blocks)
 
